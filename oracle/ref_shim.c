@@ -1,0 +1,19 @@
+/* ref_shim.c -- exports the reference's own CPU routines for the oracle checks.
+ *
+ * TEST INFRASTRUCTURE ONLY. oracle/build.py compiles this file against the
+ * reference sources where they lie (their paths come in as REF_Q8_CPU and
+ * REF_PQ2_HOST); nothing of the reference is copied into this repository.
+ * The output goes to oracle/_ref/ and is used only to pin the oracle:
+ *   ref_q8_gemv   -> gemv_q8   (.auto/lfm3/q8_gemv_cpu.c:29-58)
+ *   ref_q8_quant  -> quant_row (.auto/lfm3/q8_gemv_cpu.c:63-81)
+ *   pq2_gemv_cpu / pq2_h2f are exported by pulsar_arm/bonsai2/pq2_host.c itself.
+ */
+#define main q8_gemv_cpu_reference_main
+#include REF_Q8_CPU
+#undef main
+
+void ref_q8_gemv(const signed char *q, const float *s, const float *x, float *y, int N, int K) {
+  gemv_q8(q, s, x, y, N, K);
+}
+
+void ref_q8_quant(const float *w, int K, signed char *q, float *s) { quant_row(w, K, q, s); }

@@ -1,0 +1,71 @@
+// pq_device.h -- device-side scalar helpers shared by every gfx950 kernel.
+//
+// All HIP sources are compiled with -ffp-contract=off: a fused multiply-add is
+// written as __builtin_fmaf, every other a*b+c rounds twice. Division and
+// sqrtf are the correctly rounded forms (hipcc's default for HIP), so host and
+// device agree on them bit for bit.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pq {
+
+// bf16 <-> f32. bf16 is raw 16-bit storage; f32 -> bf16 is round-to-nearest-
+// even with inf/nan passed through (lfm3_nanode.cu:114-121).
+__device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float v) {
+  const uint32_t u = __float_as_uint(v);
+  if (((u >> 23) & 0xffu) == 0xffu) return (uint16_t)(u >> 16);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// binary16 <-> f32 through the hardware converts (v_cvt_f32_f16 is exact;
+// v_cvt_f16_f32 rounds to nearest even and keeps subnormals).
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return __builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// e^x with the build's one definition: Cody & Waite reduction
+// n = rint(x*log2 e), r = (x - n*ln2_hi) - n*ln2_lo, degree-7 Taylor
+// polynomial in Horner form, then two exact power-of-two factors so only the
+// last multiply rounds. Identical operation sequence on the host side.
+__device__ __forceinline__ float expf_pq(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  if (x < -104.0f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(n, -0.693145751953125f, x);
+  r = __builtin_fmaf(n, -1.428606765330187045e-06f, r);
+  float p = 1.98412698412698412e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const int a = ni / 2, b = ni - a;
+  const float fa = __uint_as_float((uint32_t)(a + 127) << 23);
+  const float fb = __uint_as_float((uint32_t)(b + 127) << 23);
+  return (p * fa) * fb;
+}
+
+// Wave64 xor-butterfly sum: after it every lane holds the pairwise (balanced
+// binary) sum of the 64 lanes' values in lane order -- the order the host
+// side writes as a recursive halving sum.
+__device__ __forceinline__ float wave_pairwise_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace pq

@@ -1,0 +1,33 @@
+// pq_host.h -- host-side helpers of the C ABI: error state and argument checks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/pulsar_amd.h"
+
+namespace pq {
+
+// Records the message of the calling thread's last failure and returns code.
+int fail(int code, const char *fmt, ...);
+
+inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Checks the launch that was just queued; a failed launch returns
+// PQ_ERR_LAUNCH and produces no output (the reference's rule: no number from
+// a kernel that did not run, lfm3_nanode.cu:4957-4961).
+inline int check_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PQ_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return PQ_OK;
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace pq
+
+#define PQ_REQUIRE(cond, code, ...) \
+  do {                              \
+    if (!(cond)) return ::pq::fail((code), __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,413 @@
+// q8.hip -- Q8_0 activation quantizer, weight packing, the T=1 decode GEMV and
+// the T-wide prefill GEMM for gfx950.
+//
+// Packed weight layout (64-row tiles, nb = K/32 blocks, nch = ceil(nb/8)):
+//   codes  [tile][b][h][r][16 B] = codes[64*tile + r][32*b + 16*h .. +16]
+//   scales [tile][c][r][8] fp16  = scale[64*tile + r][8*c + i]
+// One (tile, b, h) slab is 1 KB: a wave64 load of 16 B per lane. The decode
+// GEMV gives each lane one row (thread-per-row, the reference's TL kernels'
+// mapping, lfm3_nanode.cu:4051-4123); the MFMA GEMM reads the same slabs as
+// the 32x32x32 B operand (lane = row % 32, k-half = lane / 32).
+//
+// Numerics (R1), per output (row, position):
+//   isum_b = sum_j w[32b+j] * qx[32b+j]          int32, exact (v_dot4)
+//   s_b    = fl(f16(scale_b) * dx_b)
+//   a_c    = fmaf(s_b, (float)isum_b, a_c)       blocks of chunk c ascending, from 0
+//   y      = fl(y + a_c)                          chunks ascending, from 0
+#include "pq_device.h"
+#include "pq_host.h"
+
+namespace pq {
+
+constexpr int kQ = PQ_QBLK;             // 32 codes per block
+constexpr int kCB = PQ_CHUNK_BLOCKS;    // 8 blocks per R1 chunk
+constexpr int kTR = PQ_TILE_ROWS;       // 64 rows per tile
+constexpr int kSlab = 2 * kTR * 16;     // bytes per (tile, block): 2 halves x 64 rows x 16 B
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__host__ __device__ inline int nchunks(int K) { return (K / kQ + kCB - 1) / kCB; }
+__host__ __device__ inline int ntiles(int N) { return (N + kTR - 1) / kTR; }
+
+// ------------------------------------------------------------------ quantizer
+// One 32-lane half wave per block: lane j holds x_j, amax by an xor-butterfly
+// max (order-free), d = amax/127, q = rne(x/d) clamped.
+template <typename TX>
+__device__ __forceinline__ float load_act(const TX *p);
+template <>
+__device__ __forceinline__ float load_act<float>(const float *p) { return *p; }
+template <>
+__device__ __forceinline__ float load_act<uint16_t>(const uint16_t *p) { return bf2f(*p); }
+
+template <typename TX>
+__global__ __launch_bounds__(256) void q8_quant_kernel(const TX *__restrict__ x, int8_t *__restrict__ qx,
+                                                        float *__restrict__ dx, long long nblk) {
+  const long long gt = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long blk = gt >> 5;
+  const int j = (int)(gt & 31);
+  const bool valid = blk < nblk;
+  const float v = valid ? load_act<TX>(x + blk * kQ + j) : 0.0f;
+  float a = fabsf(v);
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+  const float d = a / 127.0f;
+  int q = 0;
+  if (d != 0.0f) {
+    q = (int)__builtin_rintf(v / d);
+    q = q > 127 ? 127 : (q < -127 ? -127 : q);
+  }
+  if (valid) {
+    qx[blk * kQ + j] = (int8_t)q;
+    if (j == 0) dx[blk] = d;
+  }
+}
+
+// -------------------------------------------------------------------- packing
+// One thread per 16-byte slab piece (tile, b, h, r).
+__global__ __launch_bounds__(256) void q8_pack_codes_kernel(const int8_t *__restrict__ codes, int8_t *__restrict__ pc,
+                                                             int N, int K, long long npieces) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= npieces) return;
+  const int nb = K / kQ;
+  const int r = (int)(i % kTR);
+  const int h = (int)((i / kTR) % 2);
+  const long long tb = i / (2 * kTR);
+  const int b = (int)(tb % nb);
+  const long long tile = tb / nb;
+  const long long row = tile * kTR + r;
+  int4 v = make_int4(0, 0, 0, 0);
+  if (row < N) v = *reinterpret_cast<const int4 *>(codes + row * K + (long long)b * kQ + 16 * h);
+  *reinterpret_cast<int4 *>(pc + i * 16) = v;
+}
+
+// One thread per (tile, chunk, row): its 8 scales.
+__global__ __launch_bounds__(256) void q8_pack_scales_kernel(const uint16_t *__restrict__ sc, uint16_t *__restrict__ ps,
+                                                              int N, int K, long long nitems) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nitems) return;
+  const int nb = K / kQ, nch = nchunks(K);
+  const int r = (int)(i % kTR);
+  const long long tc = i / kTR;
+  const int c = (int)(tc % nch);
+  const long long tile = tc / nch;
+  const long long row = tile * kTR + r;
+  uint16_t v[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int b = c * kCB + k;
+    v[k] = (row < N && b < nb) ? sc[row * nb + b] : (uint16_t)0;
+  }
+  uint4 o;
+  o.x = v[0] | ((uint32_t)v[1] << 16);
+  o.y = v[2] | ((uint32_t)v[3] << 16);
+  o.z = v[4] | ((uint32_t)v[5] << 16);
+  o.w = v[6] | ((uint32_t)v[7] << 16);
+  *reinterpret_cast<uint4 *>(ps + i * 8) = o;
+}
+
+// ------------------------------------------------------------- decode GEMV
+// Block b of one row against x: 8 v_dot4 over the lane's two 16-byte halves;
+// x comes through wave-uniform (scalar) loads.
+__device__ __forceinline__ int blk_isum(const int8_t *__restrict__ slab, int lane, const int8_t *__restrict__ xb) {
+  const int4 w0 = *reinterpret_cast<const int4 *>(slab + lane * 16);
+  const int4 w1 = *reinterpret_cast<const int4 *>(slab + kTR * 16 + lane * 16);
+  const int *x4 = reinterpret_cast<const int *>(xb);
+  int s = 0;
+  s = __builtin_amdgcn_sdot4(w0.x, x4[0], s, false);
+  s = __builtin_amdgcn_sdot4(w0.y, x4[1], s, false);
+  s = __builtin_amdgcn_sdot4(w0.z, x4[2], s, false);
+  s = __builtin_amdgcn_sdot4(w0.w, x4[3], s, false);
+  s = __builtin_amdgcn_sdot4(w1.x, x4[4], s, false);
+  s = __builtin_amdgcn_sdot4(w1.y, x4[5], s, false);
+  s = __builtin_amdgcn_sdot4(w1.z, x4[6], s, false);
+  s = __builtin_amdgcn_sdot4(w1.w, x4[7], s, false);
+  return s;
+}
+
+__device__ __forceinline__ float half_of(uint32_t w, int hi) { return h2f((uint16_t)(hi ? (w >> 16) : (w & 0xffffu))); }
+
+// Grid: ntile * nsplit workgroups of W waves; workgroup (tile, split) owns
+// chunks [split*W, split*W + W), one chunk per wave. Each wave produces the
+// chunk partial a_c of its 64 rows. With nsplit == 1 the workgroup folds the
+// partials from LDS; otherwise every workgroup stores its partials and the
+// last to arrive at the tile's counter folds all of them in chunk order and
+// returns the counter to zero.
+__global__ __launch_bounds__(512) void q8_gemv_kernel(const int8_t *__restrict__ pc, const uint16_t *__restrict__ ps,
+                                                        const int8_t *__restrict__ qx, const float *__restrict__ dx,
+                                                        void *__restrict__ y, int y_bf16, int N, int K, int nsplit,
+                                                        float *__restrict__ part, unsigned *__restrict__ cnt) {
+  __shared__ float sp[8][kTR];
+  __shared__ int s_last;
+  const int nb = K / kQ, nch = nchunks(K);
+  const int W = blockDim.x >> 6;
+  const int tile = blockIdx.x / nsplit;
+  const int split = blockIdx.x - tile * nsplit;
+  // readfirstlane: the wave index is wave-uniform, so x and dx below come
+  // through scalar loads into SGPRs.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int c = split * W + wave;
+  float a = 0.0f;
+  if (c < nch) {
+    const int b0 = c * kCB;
+    const int8_t *slab0 = pc + ((size_t)tile * nb + b0) * kSlab;
+    const uint4 sv = *reinterpret_cast<const uint4 *>(ps + (((size_t)tile * nch + c) * kTR + lane) * 8);
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    if (b0 + kCB <= nb) {
+      // All 16 loads of the chunk are issued before the first dot product.
+      v4i w[2 * kCB];
+#pragma unroll
+      for (int i = 0; i < kCB; i++) {
+        w[2 * i] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + lane * 16));
+        w[2 * i + 1] =
+            __builtin_nontemporal_load(reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + kTR * 16 + lane * 16));
+      }
+      int is[kCB];
+#pragma unroll
+      for (int i = 0; i < kCB; i++) {
+        const int *x4 = reinterpret_cast<const int *>(qx + (size_t)(b0 + i) * kQ);
+        int s = 0;
+        s = __builtin_amdgcn_sdot4(w[2 * i].x, x4[0], s, false);
+        s = __builtin_amdgcn_sdot4(w[2 * i].y, x4[1], s, false);
+        s = __builtin_amdgcn_sdot4(w[2 * i].z, x4[2], s, false);
+        s = __builtin_amdgcn_sdot4(w[2 * i].w, x4[3], s, false);
+        s = __builtin_amdgcn_sdot4(w[2 * i + 1].x, x4[4], s, false);
+        s = __builtin_amdgcn_sdot4(w[2 * i + 1].y, x4[5], s, false);
+        s = __builtin_amdgcn_sdot4(w[2 * i + 1].z, x4[6], s, false);
+        s = __builtin_amdgcn_sdot4(w[2 * i + 1].w, x4[7], s, false);
+        is[i] = s;
+      }
+#pragma unroll
+      for (int i = 0; i < kCB; i++) {
+        const float s = half_of(sw[i >> 1], i & 1) * dx[b0 + i];
+        a = __builtin_fmaf(s, (float)is[i], a);
+      }
+    } else {
+      for (int i = 0; b0 + i < nb; i++) {
+        const int is = blk_isum(slab0 + (size_t)i * kSlab, lane, qx + (size_t)(b0 + i) * kQ);
+        const uint32_t w = (i >> 1) == 0 ? sw[0] : (i >> 1) == 1 ? sw[1] : (i >> 1) == 2 ? sw[2] : sw[3];
+        const float s = half_of(w, i & 1) * dx[b0 + i];
+        a = __builtin_fmaf(s, (float)is, a);
+      }
+    }
+  }
+  const int row = tile * kTR + lane;
+  if (nsplit == 1) {
+    sp[wave][lane] = a;
+    __syncthreads();
+    if (wave == 0 && row < N) {
+      float acc = 0.0f;
+      for (int cc = 0; cc < nch; cc++) acc = acc + sp[cc][lane];
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(acc);
+      else reinterpret_cast<float *>(y)[row] = acc;
+    }
+    return;
+  }
+  if (c < nch) part[((size_t)tile * nch + c) * kTR + lane] = a;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = (atomicAdd(&cnt[tile], 1u) == (unsigned)(nsplit - 1));
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  if (wave == 0 && row < N) {
+    float acc = 0.0f;
+    for (int cc = 0; cc < nch; cc++)
+      acc = acc + __hip_atomic_load(&part[((size_t)tile * nch + cc) * kTR + lane], __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(acc);
+    else reinterpret_cast<float *>(y)[row] = acc;
+  }
+  if (threadIdx.x == 0) atomicExch(&cnt[tile], 0u);
+}
+
+// ------------------------------------------------------------ prefill GEMM
+// Workgroup = 4 waves = one 64-row tile x 64 positions; wave w owns row
+// half (w & 1) and position tile (w >> 1), a 32x32 accumulator. Per block one
+// v_mfma_i32_32x32x32_i8: A = activations (i = position), B = weights (j =
+// row); lane l then holds D[i][j] for j = l % 32 and i = 8(r/4) + 4(l/32) + r%4
+// (r = 0..15), and applies the R1 epilogue to its 16 outputs. dx of the
+// workgroup's 64 positions is staged per chunk in LDS as [block][position].
+
+__global__ __launch_bounds__(256) void q8_gemm_kernel(const int8_t *__restrict__ pc, const uint16_t *__restrict__ ps,
+                                                       const int8_t *__restrict__ qx, const float *__restrict__ dx,
+                                                       void *__restrict__ y, int y_bf16, int N, int K, int T) {
+  __shared__ __align__(16) float dxs[kCB][64];
+  const int nb = K / kQ, nch = nchunks(K);
+  const int tile = blockIdx.x;
+  const int p0 = blockIdx.y * 64;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = wave & 1, pt = wave >> 1;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int jrow = sub * 32 + l32;                 // row within the tile
+  const int apos = p0 + pt * 32 + l32;             // A-operand position of this lane
+  const bool aval = apos < T;
+  const int8_t *arow = qx + (size_t)(aval ? apos : 0) * K + 16 * h;
+  float yacc[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) yacc[r] = 0.0f;
+  for (int c = 0; c < nch; c++) {
+    const int b0 = c * kCB;
+    const int nbc = (b0 + kCB <= nb) ? kCB : nb - b0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < kCB * 64; i += 256) {
+      const int bi = i >> 6, p = i & 63;
+      const int pos = p0 + p;
+      dxs[bi][p] = (bi < nbc && pos < T) ? dx[(size_t)pos * nb + b0 + bi] : 0.0f;
+    }
+    __syncthreads();
+    const uint4 sv = *reinterpret_cast<const uint4 *>(ps + (((size_t)tile * nch + c) * kTR + jrow) * 8);
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    float a[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) a[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCB; i++) {
+      if (i < nbc) {
+        const int b = b0 + i;
+        const v4i bw = *reinterpret_cast<const v4i *>(pc + ((size_t)tile * nb + b) * kSlab + (h * kTR + jrow) * 16);
+        v4i av = {0, 0, 0, 0};
+        if (aval) av = *reinterpret_cast<const v4i *>(arow + (size_t)b * kQ);
+        v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw, acc, 0, 0, 0);
+        const float dw = half_of(sw[i >> 1], i & 1);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[i][pt * 32 + 8 * g + 4 * h]);
+          const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            const int r = 4 * g + k;
+            const float s = dw * dv[k];
+            a[r] = __builtin_fmaf(s, (float)acc[r], a[r]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) yacc[r] = yacc[r] + a[r];
+  }
+  const int row = tile * kTR + jrow;
+  if (row >= N) return;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int pos = p0 + pt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+    if (pos < T) {
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)pos * N + row] = f2bf(yacc[r]);
+      else reinterpret_cast<float *>(y)[(size_t)pos * N + row] = yacc[r];
+    }
+  }
+}
+
+// Waves per workgroup for the decode GEMV: the largest W in {8,4,2,1} (and
+// <= the chunk count) whose grid still gives every CU a workgroup.
+static int gemv_waves(int N, int K) {
+  static int forced = -1;
+  if (forced < 0) {
+    const char *e = getenv("PQ_GEMV_WAVES");
+    forced = e ? atoi(e) : 0;
+  }
+  const int nch = nchunks(K), nt = ntiles(N);
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced < nch ? forced : nch;
+  int W = nch < 8 ? nch : 8;
+  while (W > 1 && (long long)nt * ((nch + W - 1) / W) < 256) W >>= 1;
+  return W;
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" size_t pq_q8_packed_codes_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % kQ) return 0;
+  return (size_t)ntiles(N) * (K / kQ) * kSlab;
+}
+
+extern "C" size_t pq_q8_packed_scales_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % kQ) return 0;
+  return (size_t)ntiles(N) * nchunks(K) * kTR * 8 * sizeof(uint16_t);
+}
+
+// Workspace layout: [PQ_WS_COUNTERS arrival counters][fp32 partials]. The
+// counter region holds nothing else, so it is all zero between calls whatever
+// shapes came before; the partials are rewritten before every read.
+extern "C" size_t pq_q8_gemv_workspace_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % kQ) return 0;
+  const size_t nt = ntiles(N);
+  return (size_t)PQ_WS_COUNTERS * sizeof(unsigned) + nt * nchunks(K) * kTR * sizeof(float);
+}
+
+extern "C" int pq_q8_quant_f32(const float *x, int8_t *qx, float *dx, int K, int T, void *stream) {
+  PQ_REQUIRE(x && qx && dx, PQ_ERR_ARG, "pq_q8_quant_f32: null pointer");
+  PQ_REQUIRE(K > 0 && K % kQ == 0 && T > 0, PQ_ERR_ARG, "pq_q8_quant_f32: K=%d T=%d (K must be a multiple of 32)", K, T);
+  const long long nblk = (long long)T * (K / kQ);
+  const long long threads = nblk * 32;
+  hipLaunchKernelGGL(q8_quant_kernel<float>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, as_stream(stream),
+                     x, qx, dx, nblk);
+  return check_launch("pq_q8_quant_f32");
+}
+
+extern "C" int pq_q8_quant_bf16(const uint16_t *x, int8_t *qx, float *dx, int K, int T, void *stream) {
+  PQ_REQUIRE(x && qx && dx, PQ_ERR_ARG, "pq_q8_quant_bf16: null pointer");
+  PQ_REQUIRE(K > 0 && K % kQ == 0 && T > 0, PQ_ERR_ARG, "pq_q8_quant_bf16: K=%d T=%d (K must be a multiple of 32)", K, T);
+  const long long nblk = (long long)T * (K / kQ);
+  const long long threads = nblk * 32;
+  hipLaunchKernelGGL(q8_quant_kernel<uint16_t>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     as_stream(stream), x, qx, dx, nblk);
+  return check_launch("pq_q8_quant_bf16");
+}
+
+extern "C" int pq_q8_pack(const int8_t *codes, const uint16_t *scales, int N, int K, int8_t *pcodes,
+                          uint16_t *pscales, void *stream) {
+  PQ_REQUIRE(codes && scales && pcodes && pscales, PQ_ERR_ARG, "pq_q8_pack: null pointer");
+  PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0, PQ_ERR_ARG, "pq_q8_pack: N=%d K=%d", N, K);
+  PQ_REQUIRE(aligned(codes, 16) && aligned(pcodes, 16) && aligned(pscales, 16), PQ_ERR_ALIGN,
+             "pq_q8_pack: codes and packed buffers must be 16-byte aligned");
+  const long long npieces = (long long)ntiles(N) * (K / kQ) * 2 * kTR;
+  hipLaunchKernelGGL(q8_pack_codes_kernel, dim3((unsigned)((npieces + 255) / 256)), dim3(256), 0, as_stream(stream),
+                     codes, pcodes, N, K, npieces);
+  int rc = check_launch("pq_q8_pack codes");
+  if (rc) return rc;
+  const long long nitems = (long long)ntiles(N) * nchunks(K) * kTR;
+  hipLaunchKernelGGL(q8_pack_scales_kernel, dim3((unsigned)((nitems + 255) / 256)), dim3(256), 0, as_stream(stream),
+                     scales, pscales, N, K, nitems);
+  return check_launch("pq_q8_pack scales");
+}
+
+extern "C" int pq_q8_gemv(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,
+                          int y_dtype, int N, int K, void *ws, size_t ws_bytes, void *stream) {
+  PQ_REQUIRE(pcodes && pscales && qx && dx && y, PQ_ERR_ARG, "pq_q8_gemv: null pointer");
+  PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0, PQ_ERR_ARG, "pq_q8_gemv: N=%d K=%d (K must be a multiple of 32)", N, K);
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemv: y_dtype %d", y_dtype);
+  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16) && aligned(qx, 16) && aligned(dx, 4), PQ_ERR_ALIGN,
+             "pq_q8_gemv: packed weights and qx must be 16-byte aligned");
+  const int nch = nchunks(K), nt = ntiles(N);
+  const int W = gemv_waves(N, K);
+  const int nsplit = (nch + W - 1) / W;
+  float *part = nullptr;
+  unsigned *cnt = nullptr;
+  if (nsplit > 1) {
+    const size_t need = pq_q8_gemv_workspace_bytes(N, K);
+    PQ_REQUIRE(ws != nullptr && ws_bytes >= need, PQ_ERR_WORKSPACE,
+               "pq_q8_gemv: workspace of %zu bytes needed (got %zu)", need, ws_bytes);
+    PQ_REQUIRE(aligned(ws, 256), PQ_ERR_ALIGN, "pq_q8_gemv: workspace must be 256-byte aligned");
+    PQ_REQUIRE(nt <= PQ_WS_COUNTERS, PQ_ERR_ARG, "pq_q8_gemv: N=%d exceeds %d tiles", N, PQ_WS_COUNTERS);
+    cnt = reinterpret_cast<unsigned *>(ws);
+    part = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + (size_t)PQ_WS_COUNTERS * sizeof(unsigned));
+  }
+  hipLaunchKernelGGL(q8_gemv_kernel, dim3((unsigned)(nt * nsplit)), dim3(64 * W), 0, as_stream(stream), pcodes,
+                     pscales, qx, dx, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, nsplit, part, cnt);
+  return check_launch("pq_q8_gemv");
+}
+
+extern "C" int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,
+                          int y_dtype, int N, int K, int T, void *stream) {
+  PQ_REQUIRE(pcodes && pscales && qx && dx && y, PQ_ERR_ARG, "pq_q8_gemm: null pointer");
+  PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0 && T > 0, PQ_ERR_ARG, "pq_q8_gemm: N=%d K=%d T=%d", N, K, T);
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemm: y_dtype %d", y_dtype);
+  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16) && aligned(qx, 16) && aligned(dx, 4), PQ_ERR_ALIGN,
+             "pq_q8_gemm: packed weights and qx must be 16-byte aligned");
+  hipLaunchKernelGGL(q8_gemm_kernel, dim3((unsigned)ntiles(N), (unsigned)((T + 63) / 64)), dim3(256), 0,
+                     as_stream(stream), pcodes, pscales, qx, dx, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, T);
+  return check_launch("pq_q8_gemm");
+}
