@@ -1,0 +1,189 @@
+"""Benchmark: Q8_0 GEMV HBM throughput on one MI355X (one LFM-style layer's GEMVs + LM head).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one pass of the decode hot path over one synthetic layer at T=1:
+quantize x (K=2048 and K=8192) to Q8_0, then the GEMVs fused q|k|v 3072x2048,
+o_proj 2048x2048, gate+up 16384x2048, down 2048x8192 and the LM head
+65536x2048 (fp32 logits), all from packed Q8_0 weights resident in HBM. The
+weights rotate over enough copies (>= 600 MB) that no step reads another
+step's weights out of the 256 MB Infinity Cache.
+
+Prints ONE JSON line. value = algorithmic bytes per step / time per step (GB/s);
+roofline = the GEMV kernel's algorithmic bytes / its HIP-event-timed launch
+durations on the launch stream, against 8 TB/s; cpu_baseline = the reference's
+own CPU GEMV (.auto/lfm3/q8_gemv_cpu.c gemv_q8, compiled into oracle/_ref) on
+the host cores over a bounded sample of the same shapes.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pulsar-asm_amd"))
+
+HBM_PEAK_GBS = 8000.0
+SHAPES = [  # name, N, K, output dtype
+    ("qkv", 3072, 2048, "bf16"),
+    ("o_proj", 2048, 2048, "bf16"),
+    ("gate_up", 16384, 2048, "bf16"),
+    ("down", 2048, 8192, "bf16"),
+    ("lm_head", 65536, 2048, "f32"),
+]
+
+
+def gemv_bytes(N, K, out):
+    return N * K + N * (K // 32) * 2 + K + (K // 32) * 4 + N * (4 if out == "f32" else 2)
+
+
+def cpu_baseline(seconds=10.0):
+    """The reference's gemv_q8 (fp32 x, fp32 scales) over the same shapes, on all host cores."""
+    import ctypes as C
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    ref = pyoracle.ref()
+    kind = "reference"
+    if ref is None:
+        kind = "port"
+    data = []
+    for i, (name, N, K, _) in enumerate(SHAPES):
+        W = pyoracle.gen_codes(20261201 + 4 * i, N * K).reshape(N, K)
+        S = pyoracle.gen_scales(20261201 + 4 * i + 1, N * (K // 32)).view(np.float16).astype(np.float32)
+        x = pyoracle.gen_normal(20261201 + 4 * i + 2, K)
+        y = np.empty(N, np.float32)
+        data.append((N, K, W, S.reshape(N, K // 32), x, y))
+
+    def run_step():
+        for (N, K, W, S, x, y) in data:
+            if ref is not None:
+                ref.ref_q8_gemv(W.ctypes.data_as(C.c_void_p), S.ctypes.data_as(C.c_void_p),
+                                x.ctypes.data_as(C.c_void_p), y.ctypes.data_as(C.c_void_p), C.c_int(N), C.c_int(K))
+            else:
+                y[:] = pyoracle.q8_gemv_a11(W, S, x)
+
+    run_step()
+    nbytes = sum(N * K + N * (K // 32) * 4 + K * 4 + N * 4 for (N, K, *_r) in data)
+    steps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        run_step()
+        steps += 1
+    dt = (time.perf_counter() - t0) / steps
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+            "ms_per_step": round(dt * 1e3, 3),
+            "sample": f"{steps} passes of the 5 layer+LM-head GEMV shapes through gemv_q8 "
+                      f"(q8_gemv_cpu.c:29-58, OpenMP over rows; fp32 x and fp32 scales, {nbytes / 1e6:.1f} MB/pass)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--rotate-mb", type=int, default=600)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMV would shard by rows; "
+              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import pulsar_amd as pq
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(20261201)
+    g = torch.Generator(device=dev)
+    g.manual_seed(20261201)
+    set_bytes = sum(pq.lib().pq_q8_packed_codes_bytes(N, K) + pq.lib().pq_q8_packed_scales_bytes(N, K)
+                    for (_, N, K, _) in SHAPES)
+    ncopy = max(2, math.ceil(args.rotate_mb * 1e6 / set_bytes))
+    copies = []
+    for c in range(ncopy):
+        ws = {}
+        for (name, N, K, _) in SHAPES:
+            codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+            scales = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().view(torch.int16)
+            ws[name] = pq.Q8Weight(codes, scales)
+            del codes, scales
+        copies.append(ws)
+    x2 = torch.randn(2048, device=dev, generator=g)
+    x8 = torch.randn(8192, device=dev, generator=g)
+    outs = {name: torch.empty(N, dtype=torch.float32 if o == "f32" else torch.bfloat16, device=dev)
+            for (name, N, K, o) in SHAPES}
+    torch.cuda.synchronize()
+
+    from pulsar_amd.hiptime import Event
+    stream = pq.stream_ptr()
+
+    def step(i, ev=None):
+        ws = copies[i % ncopy]
+        q2, d2 = pq.q8_quant(x2)
+        q8, d8 = pq.q8_quant(x8)
+        for j, (name, N, K, o) in enumerate(SHAPES):
+            q, d = (q8, d8) if K == 8192 else (q2, d2)
+            if ev is not None:
+                pq.lib().pq_time_next_launch(ev[j][0].h, ev[j][1].h)
+            pq.q8_gemv(ws[name], q, d, out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, stop = Event(), Event()
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_ms(stop) / args.steps
+
+    # per-launch durations of the GEMV kernel: events attached to its own dispatch packets
+    per = {name: 0.0 for (name, *_r) in SHAPES}
+    ev = [(Event(), Event()) for _ in SHAPES]
+    for i in range(args.steps):
+        step(i, ev)
+        torch.cuda.synchronize()
+        for j, (name, *_r) in enumerate(SHAPES):
+            per[name] += ev[j][0].elapsed_ms(ev[j][1])
+    per = {k: v / args.steps for k, v in per.items()}
+
+    step_bytes = sum(gemv_bytes(N, K, o) for (_, N, K, o) in SHAPES)
+    gemv_ms = sum(per.values())
+    achieved = step_bytes / (gemv_ms * 1e-3) / 1e9
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    per_shape = {name: {"us": round(per[name] * 1e3, 2),
+                        "GB/s": round(gemv_bytes(N, K, o) / (per[name] * 1e-3) / 1e9, 1)}
+                 for (name, N, K, o) in SHAPES}
+
+    line = {
+        "metric": "Q8 GEMV HBM GB/s (% of peak); backbone decode tok/s on 1 MI355X",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xint8->int32, fp32 scales",
+        "data": "synthetic (seeded uniform int8 codes, |N(0,1)|*0.01 fp16 scales, N(0,1) x)",
+        "config": {"workload": "one LFM-style layer's T=1 Q8_0 GEMVs + LM head (hidden 2048)",
+                   "gemvs": [f"{n}:{N}x{K}" for (n, N, K, _) in SHAPES],
+                   "bytes_per_step": step_bytes, "weight_copies_rotated": ncopy,
+                   "rotated_MB": round(ncopy * set_bytes / 1e6, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "q8_gemv_kernel", "per_shape": per_shape},
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

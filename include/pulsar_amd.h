@@ -8,7 +8,7 @@
  *     prints (pq_last_error() gives the message of the calling thread's last
  *     failure) -- the reference prints and exit(2)s (lfm3_nanode.cu:1927-1929)
  *     or returns 1 (lfm3_nanode.cu:4956-4967);
- *   - allocates nothing: scratch comes in as a workspace argument.
+ *   - allocates nothing (buffers are the caller's).
  * Paths in comments are relative to the PULSAR-ASM tree.
  */
 #ifndef PULSAR_AMD_H
@@ -30,7 +30,6 @@ extern "C" {
 #define PQ_QBLK 32             /* Q8_0 block: 32 codes, one fp16 scale           */
 #define PQ_CHUNK_BLOCKS 8      /* R1 chunk: the fp32 partial covers 8 blocks     */
 #define PQ_TILE_ROWS 64        /* rows per tile of the packed weight layout      */
-#define PQ_WS_COUNTERS 16384   /* arrival counters at the head of a workspace    */
 
 #define PQ_DTYPE_F32 0
 #define PQ_DTYPE_BF16 1
@@ -39,14 +38,11 @@ extern "C" {
 const char *pq_version(void);
 const char *pq_last_error(void);
 
-/* ---------------------------------------------------------------- workspace
- * Scratch for split-K partials and arrival counters: the first
- * PQ_WS_COUNTERS * 4 bytes are counters, the rest partials. The counters must
- * start at zero: call pq_workspace_init once after allocating (every kernel
- * that uses a counter returns it to zero). One workspace per stream: two
- * launches that overlap on different streams must not share one. */
-size_t pq_q8_gemv_workspace_bytes(int N, int K);
-int pq_workspace_init(void *ws, size_t ws_bytes, void *stream);
+/* Profiling hook: the calling thread's next kernel launch records the two
+ * hipEvent_t on its own dispatch (hipExtLaunchKernel), so their elapsed time
+ * is that kernel's duration. NULL, NULL disarms. The counterpart of the
+ * reference's LFM_KTIME per-statement event brackets (lfm3_nanode.cu:1030-1051). */
+int pq_time_next_launch(void *start_event, void *stop_event);
 
 /* --------------------------------------------------------- Q8_0 activations
  * x [T][K] -> qx [T][K] int8, dx [T][K/32] fp32. Per 32-block:
@@ -76,10 +72,11 @@ int pq_q8_pack(const int8_t *codes, const uint16_t *scales, int N, int K,
  * Order per output (R1): isum_b exact int32; s_b = fl(f16(W.s_b) * dx_b);
  * per 8-block chunk a = fmaf(s_b, (float)isum_b, a) from 0; y = y + a_c over
  * chunks ascending from 0. y may alias the buffer qx was quantized from.
+ * Each workgroup owns whole rows (no cross-workgroup reduction, no scratch).
  * Replaces gemv / gemv_f / tlb_decode (lfm3_nanode.cu:1916-1966, 3634-3663,
  * 4524-4530) and their kernels q8_partial + k_combine_* (222-374). */
 int pq_q8_gemv(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
-               void *y, int y_dtype, int N, int K, void *ws, size_t ws_bytes, void *stream);
+               void *y, int y_dtype, int N, int K, void *stream);
 
 /* ------------------------------------------------------- Q8_0 GEMM, T wide
  * y[T][N] for T positions (qx [T][K], dx [T][K/32], position-first), each

@@ -1,5 +1,6 @@
 // pq_host.h -- host-side helpers of the C ABI: error state and argument checks.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -24,6 +25,27 @@ inline int check_launch(const char *what) {
 }
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Timing hook (pq_time_next_launch): events that the next kernel launch of the
+// calling thread carries on its own dispatch packet.
+struct TimedLaunch {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+TimedLaunch &timed_launch();
+
+// Launches a kernel; if pq_time_next_launch armed a pair of events, they are
+// attached to this dispatch (hipExtLaunchKernelGGL) and the pair is consumed.
+template <typename... Args, typename F>
+inline void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+  TimedLaunch &t = timed_launch();
+  if (t.start != nullptr) {
+    hipEvent_t a = t.start, b = t.stop;
+    t.start = t.stop = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, st, a, b, 0, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+  }
+}
 
 }  // namespace pq
 

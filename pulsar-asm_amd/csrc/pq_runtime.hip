@@ -1,4 +1,4 @@
-// pq_runtime.cpp -- error state, version and workspace initialisation.
+// pq_runtime.hip -- error state and version of the C ABI.
 #include <string.h>
 
 #include "pq_host.h"
@@ -15,11 +15,9 @@ int fail(int code, const char *fmt, ...) {
   return code;
 }
 
-// Zero fill as a kernel: a hipMemsetAsync node misbehaves on replay when a
-// caller captures this stream into a HIP graph.
-__global__ void fill_u32_kernel(uint32_t *p, size_t n, uint32_t v) {
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-    p[i] = v;
+TimedLaunch &timed_launch() {
+  static thread_local TimedLaunch t;
+  return t;
 }
 
 }  // namespace pq
@@ -28,12 +26,11 @@ extern "C" const char *pq_version(void) { return "pulsar-amd 0.1 gfx950"; }
 
 extern "C" const char *pq_last_error(void) { return pq::g_err; }
 
-extern "C" int pq_workspace_init(void *ws, size_t ws_bytes, void *stream) {
-  PQ_REQUIRE(ws != nullptr && ws_bytes >= 4, PQ_ERR_WORKSPACE, "pq_workspace_init: null or empty workspace");
-  PQ_REQUIRE(pq::aligned(ws, 4), PQ_ERR_ALIGN, "pq_workspace_init: workspace must be 4-byte aligned");
-  const size_t n = ws_bytes / 4;
-  const unsigned grid = (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
-  hipLaunchKernelGGL(pq::fill_u32_kernel, dim3(grid), dim3(256), 0, pq::as_stream(stream),
-                     (uint32_t *)ws, n, 0u);
-  return pq::check_launch("pq_workspace_init");
+extern "C" int pq_time_next_launch(void *start_event, void *stop_event) {
+  PQ_REQUIRE((start_event == nullptr) == (stop_event == nullptr), PQ_ERR_ARG,
+             "pq_time_next_launch: pass both events or neither");
+  pq::TimedLaunch &t = pq::timed_launch();
+  t.start = reinterpret_cast<hipEvent_t>(start_event);
+  t.stop = reinterpret_cast<hipEvent_t>(stop_event);
+  return PQ_OK;
 }

@@ -107,118 +107,154 @@ __global__ __launch_bounds__(256) void q8_pack_scales_kernel(const uint16_t *__r
 }
 
 // ------------------------------------------------------------- decode GEMV
-// Block b of one row against x: 8 v_dot4 over the lane's two 16-byte halves;
-// x comes through wave-uniform (scalar) loads.
-__device__ __forceinline__ int blk_isum(const int8_t *__restrict__ slab, int lane, const int8_t *__restrict__ xb) {
-  const int4 w0 = *reinterpret_cast<const int4 *>(slab + lane * 16);
-  const int4 w1 = *reinterpret_cast<const int4 *>(slab + kTR * 16 + lane * 16);
-  const int *x4 = reinterpret_cast<const int *>(xb);
-  int s = 0;
-  s = __builtin_amdgcn_sdot4(w0.x, x4[0], s, false);
-  s = __builtin_amdgcn_sdot4(w0.y, x4[1], s, false);
-  s = __builtin_amdgcn_sdot4(w0.z, x4[2], s, false);
-  s = __builtin_amdgcn_sdot4(w0.w, x4[3], s, false);
-  s = __builtin_amdgcn_sdot4(w1.x, x4[4], s, false);
-  s = __builtin_amdgcn_sdot4(w1.y, x4[5], s, false);
-  s = __builtin_amdgcn_sdot4(w1.z, x4[6], s, false);
-  s = __builtin_amdgcn_sdot4(w1.w, x4[7], s, false);
-  return s;
-}
-
 __device__ __forceinline__ float half_of(uint32_t w, int hi) { return h2f((uint16_t)(hi ? (w >> 16) : (w & 0xffffu))); }
 
-// Grid: ntile * nsplit workgroups of W waves; workgroup (tile, split) owns
-// chunks [split*W, split*W + W), one chunk per wave. Each wave produces the
-// chunk partial a_c of its 64 rows. With nsplit == 1 the workgroup folds the
-// partials from LDS; otherwise every workgroup stores its partials and the
-// last to arrive at the tile's counter folds all of them in chunk order and
-// returns the counter to zero.
+// One row's chunk partial a_c, in two phases so a workgroup can issue its
+// weight loads before it waits on anything else: load_chunk issues the 16
+// 16-byte code loads (and the 8 scales) of a full chunk; dot_chunk folds the
+// blocks ascending, each an exact int32 dot (8 v_dot4 over the lane's two
+// halves) folded into a = fmaf(fl(dw*dx), (float)isum, a). XS(i, x) yields the
+// 8 x dwords of block b0+i and DX(i) its scale (scalar registers when the
+// chunk is wave-uniform, LDS otherwise).
+struct ChunkRegs {
+  v4i w[2 * kCB];
+  uint32_t sw[4];
+};
+
+__device__ __forceinline__ void load_chunk(ChunkRegs &R, const int8_t *__restrict__ slab0,
+                                           const uint16_t *__restrict__ sp8, int trow) {
+#pragma unroll
+  for (int i = 0; i < kCB; i++) {
+    R.w[2 * i] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + trow * 16));
+    R.w[2 * i + 1] =
+        __builtin_nontemporal_load(reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + kTR * 16 + trow * 16));
+  }
+  const uint4 sv = *reinterpret_cast<const uint4 *>(sp8);
+  R.sw[0] = sv.x; R.sw[1] = sv.y; R.sw[2] = sv.z; R.sw[3] = sv.w;
+}
+
+__device__ __forceinline__ int dot8(v4i w0, v4i w1, const int *x) {
+  int t = 0;
+  t = __builtin_amdgcn_sdot4(w0.x, x[0], t, false);
+  t = __builtin_amdgcn_sdot4(w0.y, x[1], t, false);
+  t = __builtin_amdgcn_sdot4(w0.z, x[2], t, false);
+  t = __builtin_amdgcn_sdot4(w0.w, x[3], t, false);
+  t = __builtin_amdgcn_sdot4(w1.x, x[4], t, false);
+  t = __builtin_amdgcn_sdot4(w1.y, x[5], t, false);
+  t = __builtin_amdgcn_sdot4(w1.z, x[6], t, false);
+  t = __builtin_amdgcn_sdot4(w1.w, x[7], t, false);
+  return t;
+}
+
+template <typename XF, typename DF>
+__device__ __forceinline__ float dot_chunk(const ChunkRegs &R, XF XS, DF DX) {
+  int is[kCB];
+#pragma unroll
+  for (int i = 0; i < kCB; i++) {
+    int x[8];
+    XS(i, x);
+    is[i] = dot8(R.w[2 * i], R.w[2 * i + 1], x);
+  }
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kCB; i++) a = __builtin_fmaf(half_of(R.sw[i >> 1], i & 1) * DX(i), (float)is[i], a);
+  return a;
+}
+
+// The last chunk of a K that is not a multiple of 256: blocks b0 .. nb-1.
+template <typename XF, typename DF>
+__device__ __forceinline__ float tail_chunk(const int8_t *__restrict__ slab0, const uint16_t *__restrict__ sp8, int nbc,
+                                            int trow, XF XS, DF DX) {
+  float a = 0.0f;
+  for (int i = 0; i < nbc; i++) {
+    const v4i w0 = *reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + trow * 16);
+    const v4i w1 = *reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + kTR * 16 + trow * 16);
+    int x[8];
+    XS(i, x);
+    const int t = dot8(w0, w1, x);
+    a = __builtin_fmaf(h2f(sp8[i]) * DX(i), (float)t, a);
+  }
+  return a;
+}
+
+constexpr int kXStride = 256 + 16;
+constexpr int kMaxStagedK = 32768;  // x staged in LDS only up to this K (35 KB)  // LDS bytes per staged x chunk (the pad spreads chunks over banks)
+
+// Workgroup = R rows (a slice of one 64-row tile) x every chunk of K, so each
+// workgroup writes finished outputs and no reduction crosses workgroups. Lane
+// l handles row r = l % R of the slice and chunk slot cs = l / R (C = 64/R
+// slots per wave); in round rd, wave w's lanes take chunks
+// (rd*W + w)*C + cs. Each lane computes its chunk partial a_c; the round's
+// partials go to LDS in chunk order and lanes 0..R-1 of wave 0 fold them into
+// y = y + a_c. With R = 64 a wave's chunk is wave-uniform and x / dx come in
+// through scalar loads; with R < 64 the workgroup stages x and dx in LDS.
+template <int R>
 __global__ __launch_bounds__(512) void q8_gemv_kernel(const int8_t *__restrict__ pc, const uint16_t *__restrict__ ps,
-                                                        const int8_t *__restrict__ qx, const float *__restrict__ dx,
-                                                        void *__restrict__ y, int y_bf16, int N, int K, int nsplit,
-                                                        float *__restrict__ part, unsigned *__restrict__ cnt) {
-  __shared__ float sp[8][kTR];
-  __shared__ int s_last;
+                                                       const int8_t *__restrict__ qx, const float *__restrict__ dx,
+                                                       void *__restrict__ y, int y_bf16, int N, int K) {
+  constexpr int C = 64 / R;
+  extern __shared__ __align__(16) unsigned char smem[];
   const int nb = K / kQ, nch = nchunks(K);
   const int W = blockDim.x >> 6;
-  const int tile = blockIdx.x / nsplit;
-  const int split = blockIdx.x - tile * nsplit;
-  // readfirstlane: the wave index is wave-uniform, so x and dx below come
-  // through scalar loads into SGPRs.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int c = split * W + wave;
-  float a = 0.0f;
-  if (c < nch) {
+  const int cs = lane / R, r = lane % R;
+  const int tile = blockIdx.x / C, trow = (blockIdx.x % C) * R + r;
+  const int row = tile * kTR + trow;
+  float *sp = reinterpret_cast<float *>(smem);                   // [W*C][R] partials of one round
+  int8_t *xs = reinterpret_cast<int8_t *>(smem + (size_t)W * 64 * 4);
+  float *dxs = reinterpret_cast<float *>(xs + (size_t)nch * kXStride);
+  const int per_round = W * C;
+  const int nrounds = (nch + per_round - 1) / per_round;
+  const int slot = wave * C + cs;
+  float yv = 0.0f;
+  for (int rd = 0; rd < nrounds; rd++) {
+    const int c = rd * per_round + slot;
     const int b0 = c * kCB;
+    const bool full = c < nch && b0 + kCB <= nb;
     const int8_t *slab0 = pc + ((size_t)tile * nb + b0) * kSlab;
-    const uint4 sv = *reinterpret_cast<const uint4 *>(ps + (((size_t)tile * nch + c) * kTR + lane) * 8);
-    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
-    if (b0 + kCB <= nb) {
-      // All 16 loads of the chunk are issued before the first dot product.
-      v4i w[2 * kCB];
+    const uint16_t *sp8 = ps + (((size_t)tile * nch + c) * kTR + trow) * 8;
+    ChunkRegs regs;
+    if (full) load_chunk(regs, slab0, sp8, trow);   // in flight while x is staged
+    if (C > 1 && rd == 0) {
+      for (int i = threadIdx.x; i < nb * 2; i += blockDim.x)
+        *reinterpret_cast<v4i *>(xs + (i >> 4) * kXStride + (i & 15) * 16) = *reinterpret_cast<const v4i *>(qx + i * 16);
+      for (int i = threadIdx.x; i < nb; i += blockDim.x) dxs[i] = dx[i];
+      __syncthreads();
+    }
+    float a = 0.0f;
+    if (c < nch) {
+      if (C == 1) {
+        const int *xg = reinterpret_cast<const int *>(qx + (size_t)b0 * kQ);
+        auto XS = [&](int i, int *x) {
 #pragma unroll
-      for (int i = 0; i < kCB; i++) {
-        w[2 * i] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + lane * 16));
-        w[2 * i + 1] =
-            __builtin_nontemporal_load(reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + kTR * 16 + lane * 16));
-      }
-      int is[kCB];
-#pragma unroll
-      for (int i = 0; i < kCB; i++) {
-        const int *x4 = reinterpret_cast<const int *>(qx + (size_t)(b0 + i) * kQ);
-        int s = 0;
-        s = __builtin_amdgcn_sdot4(w[2 * i].x, x4[0], s, false);
-        s = __builtin_amdgcn_sdot4(w[2 * i].y, x4[1], s, false);
-        s = __builtin_amdgcn_sdot4(w[2 * i].z, x4[2], s, false);
-        s = __builtin_amdgcn_sdot4(w[2 * i].w, x4[3], s, false);
-        s = __builtin_amdgcn_sdot4(w[2 * i + 1].x, x4[4], s, false);
-        s = __builtin_amdgcn_sdot4(w[2 * i + 1].y, x4[5], s, false);
-        s = __builtin_amdgcn_sdot4(w[2 * i + 1].z, x4[6], s, false);
-        s = __builtin_amdgcn_sdot4(w[2 * i + 1].w, x4[7], s, false);
-        is[i] = s;
-      }
-#pragma unroll
-      for (int i = 0; i < kCB; i++) {
-        const float s = half_of(sw[i >> 1], i & 1) * dx[b0 + i];
-        a = __builtin_fmaf(s, (float)is[i], a);
-      }
-    } else {
-      for (int i = 0; b0 + i < nb; i++) {
-        const int is = blk_isum(slab0 + (size_t)i * kSlab, lane, qx + (size_t)(b0 + i) * kQ);
-        const uint32_t w = (i >> 1) == 0 ? sw[0] : (i >> 1) == 1 ? sw[1] : (i >> 1) == 2 ? sw[2] : sw[3];
-        const float s = half_of(w, i & 1) * dx[b0 + i];
-        a = __builtin_fmaf(s, (float)is, a);
+          for (int k = 0; k < 8; k++) x[k] = xg[i * 8 + k];
+        };
+        auto DX = [&](int i) { return dx[b0 + i]; };
+        a = full ? dot_chunk(regs, XS, DX) : tail_chunk(slab0, sp8, nb - b0, trow, XS, DX);
+      } else {
+        const int8_t *xc = xs + (size_t)c * kXStride;
+        auto XS = [&](int i, int *x) {
+          const v4i lo = *reinterpret_cast<const v4i *>(xc + i * 32);
+          const v4i hi = *reinterpret_cast<const v4i *>(xc + i * 32 + 16);
+          x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+          x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+        };
+        auto DX = [&](int i) { return dxs[b0 + i]; };
+        a = full ? dot_chunk(regs, XS, DX) : tail_chunk(slab0, sp8, nb - b0, trow, XS, DX);
       }
     }
-  }
-  const int row = tile * kTR + lane;
-  if (nsplit == 1) {
-    sp[wave][lane] = a;
+    sp[slot * R + r] = a;
     __syncthreads();
-    if (wave == 0 && row < N) {
-      float acc = 0.0f;
-      for (int cc = 0; cc < nch; cc++) acc = acc + sp[cc][lane];
-      if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(acc);
-      else reinterpret_cast<float *>(y)[row] = acc;
+    if (wave == 0 && lane < R) {
+      const int n = nch - rd * per_round < per_round ? nch - rd * per_round : per_round;
+      for (int k = 0; k < n; k++) yv = yv + sp[k * R + lane];
     }
-    return;
+    __syncthreads();
   }
-  if (c < nch) part[((size_t)tile * nch + c) * kTR + lane] = a;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = (atomicAdd(&cnt[tile], 1u) == (unsigned)(nsplit - 1));
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (wave == 0 && row < N) {
-    float acc = 0.0f;
-    for (int cc = 0; cc < nch; cc++)
-      acc = acc + __hip_atomic_load(&part[((size_t)tile * nch + cc) * kTR + lane], __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-    if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(acc);
-    else reinterpret_cast<float *>(y)[row] = acc;
+  if (wave == 0 && lane < R && row < N) {
+    if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yv);
+    else reinterpret_cast<float *>(y)[row] = yv;
   }
-  if (threadIdx.x == 0) atomicExch(&cnt[tile], 0u);
 }
 
 // ------------------------------------------------------------ prefill GEMM
@@ -299,19 +335,28 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const int8_t *__restrict__
   }
 }
 
-// Waves per workgroup for the decode GEMV: the largest W in {8,4,2,1} (and
-// <= the chunk count) whose grid still gives every CU a workgroup.
-static int gemv_waves(int N, int K) {
-  static int forced = -1;
-  if (forced < 0) {
-    const char *e = getenv("PQ_GEMV_WAVES");
-    forced = e ? atoi(e) : 0;
+// Decode GEMV launch shape: R rows per workgroup (64, or narrower slices when
+// there are too few 64-row tiles to give each of the 256 CUs a workgroup) and
+// W waves, enough to give every chunk of K a lane.
+struct GemvShape { int R, W; };
+static GemvShape gemv_shape(int N, int K) {
+  static int fR = -1, fW = -1;
+  if (fR < 0) {
+    const char *e = getenv("PQ_GEMV_R");
+    const char *f = getenv("PQ_GEMV_W");
+    fR = e ? atoi(e) : 0;
+    fW = f ? atoi(f) : 0;
   }
-  const int nch = nchunks(K), nt = ntiles(N);
-  if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced < nch ? forced : nch;
-  int W = nch < 8 ? nch : 8;
-  while (W > 1 && (long long)nt * ((nch + W - 1) / W) < 256) W >>= 1;
-  return W;
+  const int nt = ntiles(N), nch = nchunks(K);
+  int R = 64;
+  while (R > 8 && (long long)nt * (64 / R) < 256) R >>= 1;
+  if (fR == 8 || fR == 16 || fR == 32 || fR == 64) R = fR;
+  if (K > kMaxStagedK) R = 64;
+  const int C = 64 / R;
+  int W = (nch + C - 1) / C;
+  W = W < 1 ? 1 : (W > 8 ? 8 : W);
+  if (fW >= 1 && fW <= 8) W = fW;
+  return {R, W};
 }
 
 }  // namespace pq
@@ -328,21 +373,12 @@ extern "C" size_t pq_q8_packed_scales_bytes(int N, int K) {
   return (size_t)ntiles(N) * nchunks(K) * kTR * 8 * sizeof(uint16_t);
 }
 
-// Workspace layout: [PQ_WS_COUNTERS arrival counters][fp32 partials]. The
-// counter region holds nothing else, so it is all zero between calls whatever
-// shapes came before; the partials are rewritten before every read.
-extern "C" size_t pq_q8_gemv_workspace_bytes(int N, int K) {
-  if (N <= 0 || K <= 0 || K % kQ) return 0;
-  const size_t nt = ntiles(N);
-  return (size_t)PQ_WS_COUNTERS * sizeof(unsigned) + nt * nchunks(K) * kTR * sizeof(float);
-}
-
 extern "C" int pq_q8_quant_f32(const float *x, int8_t *qx, float *dx, int K, int T, void *stream) {
   PQ_REQUIRE(x && qx && dx, PQ_ERR_ARG, "pq_q8_quant_f32: null pointer");
   PQ_REQUIRE(K > 0 && K % kQ == 0 && T > 0, PQ_ERR_ARG, "pq_q8_quant_f32: K=%d T=%d (K must be a multiple of 32)", K, T);
   const long long nblk = (long long)T * (K / kQ);
   const long long threads = nblk * 32;
-  hipLaunchKernelGGL(q8_quant_kernel<float>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, as_stream(stream),
+  launch(q8_quant_kernel<float>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, as_stream(stream),
                      x, qx, dx, nblk);
   return check_launch("pq_q8_quant_f32");
 }
@@ -352,7 +388,7 @@ extern "C" int pq_q8_quant_bf16(const uint16_t *x, int8_t *qx, float *dx, int K,
   PQ_REQUIRE(K > 0 && K % kQ == 0 && T > 0, PQ_ERR_ARG, "pq_q8_quant_bf16: K=%d T=%d (K must be a multiple of 32)", K, T);
   const long long nblk = (long long)T * (K / kQ);
   const long long threads = nblk * 32;
-  hipLaunchKernelGGL(q8_quant_kernel<uint16_t>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+  launch(q8_quant_kernel<uint16_t>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                      as_stream(stream), x, qx, dx, nblk);
   return check_launch("pq_q8_quant_bf16");
 }
@@ -364,39 +400,35 @@ extern "C" int pq_q8_pack(const int8_t *codes, const uint16_t *scales, int N, in
   PQ_REQUIRE(aligned(codes, 16) && aligned(pcodes, 16) && aligned(pscales, 16), PQ_ERR_ALIGN,
              "pq_q8_pack: codes and packed buffers must be 16-byte aligned");
   const long long npieces = (long long)ntiles(N) * (K / kQ) * 2 * kTR;
-  hipLaunchKernelGGL(q8_pack_codes_kernel, dim3((unsigned)((npieces + 255) / 256)), dim3(256), 0, as_stream(stream),
+  launch(q8_pack_codes_kernel, dim3((unsigned)((npieces + 255) / 256)), dim3(256), 0, as_stream(stream),
                      codes, pcodes, N, K, npieces);
   int rc = check_launch("pq_q8_pack codes");
   if (rc) return rc;
   const long long nitems = (long long)ntiles(N) * nchunks(K) * kTR;
-  hipLaunchKernelGGL(q8_pack_scales_kernel, dim3((unsigned)((nitems + 255) / 256)), dim3(256), 0, as_stream(stream),
+  launch(q8_pack_scales_kernel, dim3((unsigned)((nitems + 255) / 256)), dim3(256), 0, as_stream(stream),
                      scales, pscales, N, K, nitems);
   return check_launch("pq_q8_pack scales");
 }
 
 extern "C" int pq_q8_gemv(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,
-                          int y_dtype, int N, int K, void *ws, size_t ws_bytes, void *stream) {
+                          int y_dtype, int N, int K, void *stream) {
   PQ_REQUIRE(pcodes && pscales && qx && dx && y, PQ_ERR_ARG, "pq_q8_gemv: null pointer");
   PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0, PQ_ERR_ARG, "pq_q8_gemv: N=%d K=%d (K must be a multiple of 32)", N, K);
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemv: y_dtype %d", y_dtype);
   PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16) && aligned(qx, 16) && aligned(dx, 4), PQ_ERR_ALIGN,
              "pq_q8_gemv: packed weights and qx must be 16-byte aligned");
-  const int nch = nchunks(K), nt = ntiles(N);
-  const int W = gemv_waves(N, K);
-  const int nsplit = (nch + W - 1) / W;
-  float *part = nullptr;
-  unsigned *cnt = nullptr;
-  if (nsplit > 1) {
-    const size_t need = pq_q8_gemv_workspace_bytes(N, K);
-    PQ_REQUIRE(ws != nullptr && ws_bytes >= need, PQ_ERR_WORKSPACE,
-               "pq_q8_gemv: workspace of %zu bytes needed (got %zu)", need, ws_bytes);
-    PQ_REQUIRE(aligned(ws, 256), PQ_ERR_ALIGN, "pq_q8_gemv: workspace must be 256-byte aligned");
-    PQ_REQUIRE(nt <= PQ_WS_COUNTERS, PQ_ERR_ARG, "pq_q8_gemv: N=%d exceeds %d tiles", N, PQ_WS_COUNTERS);
-    cnt = reinterpret_cast<unsigned *>(ws);
-    part = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + (size_t)PQ_WS_COUNTERS * sizeof(unsigned));
+  const GemvShape g = gemv_shape(N, K);
+  const int C = 64 / g.R;
+  const size_t lds = (size_t)g.W * 64 * 4 + (C > 1 ? (size_t)nchunks(K) * kXStride + (size_t)(K / kQ) * 4 : 0);
+  const dim3 grid((unsigned)(ntiles(N) * C)), block(64 * g.W);
+  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  hipStream_t st = as_stream(stream);
+  switch (g.R) {
+    case 64: launch(q8_gemv_kernel<64>, grid, block, lds, st, pcodes, pscales, qx, dx, y, yb, N, K); break;
+    case 32: launch(q8_gemv_kernel<32>, grid, block, lds, st, pcodes, pscales, qx, dx, y, yb, N, K); break;
+    case 16: launch(q8_gemv_kernel<16>, grid, block, lds, st, pcodes, pscales, qx, dx, y, yb, N, K); break;
+    default: launch(q8_gemv_kernel<8>, grid, block, lds, st, pcodes, pscales, qx, dx, y, yb, N, K); break;
   }
-  hipLaunchKernelGGL(q8_gemv_kernel, dim3((unsigned)(nt * nsplit)), dim3(64 * W), 0, as_stream(stream), pcodes,
-                     pscales, qx, dx, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, nsplit, part, cnt);
   return check_launch("pq_q8_gemv");
 }
 
@@ -407,7 +439,7 @@ extern "C" int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const i
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemm: y_dtype %d", y_dtype);
   PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16) && aligned(qx, 16) && aligned(dx, 4), PQ_ERR_ALIGN,
              "pq_q8_gemm: packed weights and qx must be 16-byte aligned");
-  hipLaunchKernelGGL(q8_gemm_kernel, dim3((unsigned)ntiles(N), (unsigned)((T + 63) / 64)), dim3(256), 0,
+  launch(q8_gemm_kernel, dim3((unsigned)ntiles(N), (unsigned)((T + 63) / 64)), dim3(256), 0,
                      as_stream(stream), pcodes, pscales, qx, dx, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, T);
   return check_launch("pq_q8_gemm");
 }

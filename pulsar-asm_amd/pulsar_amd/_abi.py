@@ -9,14 +9,13 @@ F = C.c_float
 SIGNATURES = {
     "pq_version": (C.c_char_p, []),
     "pq_last_error": (C.c_char_p, []),
-    "pq_q8_gemv_workspace_bytes": (Z, [I, I]),
-    "pq_workspace_init": (I, [P, Z, P]),
+    "pq_time_next_launch": (I, [P, P]),
     "pq_q8_quant_f32": (I, [P, P, P, I, I, P]),
     "pq_q8_quant_bf16": (I, [P, P, P, I, I, P]),
     "pq_q8_packed_codes_bytes": (Z, [I, I]),
     "pq_q8_packed_scales_bytes": (Z, [I, I]),
     "pq_q8_pack": (I, [P, P, I, I, P, P, P]),
-    "pq_q8_gemv": (I, [P, P, P, P, P, I, I, I, P, Z, P]),
+    "pq_q8_gemv": (I, [P, P, P, P, P, I, I, I, P]),
     "pq_q8_gemm": (I, [P, P, P, P, P, I, I, I, I, P]),
 }
 

@@ -8,7 +8,7 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Workspace", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16"]
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16"]
 
 DT_F32 = 0
 DT_BF16 = 1
@@ -20,31 +20,6 @@ def stream_ptr():
 
 def _ptr(t):
     return t.data_ptr() if t is not None else None
-
-
-class Workspace:
-    """Device scratch for split-K partials and counters (zeroed once)."""
-
-    def __init__(self, nbytes, device="cuda"):
-        nbytes = max(256, (nbytes + 255) // 256 * 256)
-        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        self.nbytes = nbytes
-        check(lib().pq_workspace_init(self.buf.data_ptr(), nbytes, stream_ptr()), "pq_workspace_init")
-
-    def ptr(self):
-        return self.buf.data_ptr()
-
-
-_WS = {}
-
-
-def default_workspace(nbytes, device):
-    key = (str(device), torch.cuda.current_stream().cuda_stream)
-    ws = _WS.get(key)
-    if ws is None or ws.nbytes < nbytes:
-        ws = Workspace(max(nbytes, 1 << 20), device)
-        _WS[key] = ws
-    return ws
 
 
 class Q8Weight:
@@ -92,18 +67,14 @@ def q8_quant(x):
     return (qx[0], dx[0]) if squeeze else (qx, dx)
 
 
-def q8_gemv(w, qx, dx, out_dtype=DT_F32, out=None, ws=None):
+def q8_gemv(w, qx, dx, out_dtype=DT_F32, out=None):
     """y [N] = W . x for one position."""
     if qx.numel() != w.K or dx.numel() != w.K // 32:
         raise ValueError("x does not match K")
     if out is None:
         out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=qx.device)
-    L = lib()
-    need = L.pq_q8_gemv_workspace_bytes(w.N, w.K)
-    if ws is None:
-        ws = default_workspace(need, qx.device)
-    check(L.pq_q8_gemv(w.pcodes.data_ptr(), w.pscales.data_ptr(), qx.data_ptr(), dx.data_ptr(), out.data_ptr(),
-                       out_dtype, w.N, w.K, ws.ptr(), ws.nbytes, stream_ptr()), "pq_q8_gemv")
+    check(lib().pq_q8_gemv(w.pcodes.data_ptr(), w.pscales.data_ptr(), qx.data_ptr(), dx.data_ptr(), out.data_ptr(),
+                           out_dtype, w.N, w.K, stream_ptr()), "pq_q8_gemv")
     return out
 
 

@@ -1,0 +1,361 @@
+"""Pins the CPU oracle (test infrastructure) independently of its own formulas.
+
+Each check is chosen so that a plausible mistake -- a dropped term, a wrong
+index or sign, a transposed operand, a wrong rounding -- fails it: known-answer
+vectors, the reference's own CPU routines (oracle/_ref, compiled from the
+PULSAR-ASM sources), exact recomputation, library conversions and closed
+forms. Runs on the CPU only.
+"""
+import math
+
+import numpy as np
+import pytest
+
+
+def f32bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+# ------------------------------------------------------------------ scalars
+def test_splitmix64_known_answer(orc):
+    # splitmix64 seeded with 0: first output 0xe220a8397b1dcdaf, second 0x6e789e6aa1b965f4
+    # (Steele/Lea/Flood; the values every splitmix64 implementation reproduces)
+    assert orc.lib().orc_sm64_at(0, 0) == 0xE220A8397B1DCDAF
+    assert orc.lib().orc_sm64_at(0, 1) == 0x6E789E6AA1B965F4
+
+
+def test_h2f_all_patterns(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    got = np.array([orc.lib().orc_h2f(int(v)) for v in h], np.float32)
+    want = h.view(np.float16).astype(np.float32)
+    same = (f32bits(got) == f32bits(want)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+    ref = orc.ref()
+    if ref is not None:   # the reference's own pq2_h2f (pq2_host.c:9-20)
+        got_ref = np.array([ref.pq2_h2f(int(v)) for v in h[::7]], np.float32)
+        same = (f32bits(got_ref) == f32bits(got[::7])) | (np.isnan(got_ref) & np.isnan(got[::7]))
+        assert same.all()
+
+
+def test_f2h_matches_ieee_casts(orc):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(30000) * 10.0 ** rng.integers(-9, 6, 30000)).astype(np.float32)
+    edges = np.array([65504, 65519.996, 65520, 65536, 2 ** -24, 2 ** -25, 1.5 * 2 ** -25, 2 ** -14,
+                      6.1e-5, 5.9604645e-08, -0.0, 0.0, np.inf, -np.inf, 1.0009765625, 1.00048828125], np.float32)
+    x = np.concatenate([x, edges, -edges])
+    got = np.array([orc.lib().orc_f2h(float(v)) for v in x], np.uint16)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f2h_matches_reference_quantizer(orc):
+    """quant_row (q8_gemv_cpu.c:63-81) stores (float)(_Float16)(max/127): the
+    reference compiler's own f32->f16 conversion."""
+    ref = orc.ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    import ctypes as C
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal(32 * 500) * 10.0 ** rng.integers(-6, 3, 32 * 500).repeat(1)).astype(np.float32)
+    q = np.empty(w.size, np.int8)
+    s = np.empty(w.size // 32, np.float32)
+    ref.ref_q8_quant(w.ctypes.data_as(C.c_void_p), C.c_int(w.size), q.ctypes.data_as(C.c_void_p),
+                     s.ctypes.data_as(C.c_void_p))
+    amax = np.abs(w.reshape(-1, 32)).max(1).astype(np.float32)
+    mine = np.array([orc.lib().orc_h2f(orc.lib().orc_f2h(float(np.float32(a) / np.float32(127.0)))) for a in amax],
+                    np.float32)
+    assert np.array_equal(f32bits(mine), f32bits(s))
+
+
+def test_f2bf_rne(orc):
+    import torch
+    f = orc.lib().orc_f2bf
+    # closed forms: exact, tie to even (down and up), carry into the exponent, inf/nan passthrough
+    assert f(1.0) == 0x3F80
+    assert f(float(np.uint32(0x3F808000).view(np.float32))) == 0x3F80      # tie, even stays
+    assert f(float(np.uint32(0x3F818000).view(np.float32))) == 0x3F82      # tie, odd rounds up
+    assert f(float(np.uint32(0x3F808001).view(np.float32))) == 0x3F81
+    assert f(float(np.uint32(0x3FFFFFFF).view(np.float32))) == 0x4000      # carry
+    assert f(float("inf")) == 0x7F80 and f(float("-inf")) == 0xFF80
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(20000) * 10.0 ** rng.integers(-30, 30, 20000)).astype(np.float32)
+    got = orc.f2bf(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_expf_accuracy(orc):
+    x = np.concatenate([np.linspace(-103.9, 88.72, 150001), np.linspace(-1, 1, 20001)]).astype(np.float32)
+    got = orc.expf(x).astype(np.float64)
+    true = np.exp(x.astype(np.float64))
+    ulp = np.spacing(true.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - true) / ulp).max() <= 2.0
+    assert orc.lib().orc_expf(0.0) == 1.0
+    assert orc.lib().orc_expf(89.0) == math.inf and orc.lib().orc_expf(-200.0) == 0.0
+    assert math.isnan(orc.lib().orc_expf(float("nan")))
+
+
+def test_pairwise_is_butterfly(orc):
+    rng = np.random.default_rng(11)
+    for n in (1, 2, 64, 2048):
+        v = rng.standard_normal(n).astype(np.float32) * 1e3
+        b = v.copy()
+        while b.size > 1:
+            b = (b[0::2] + b[1::2]).astype(np.float32)
+        got = orc.lib().orc_pairwise(v.ctypes.data_as(__import__("ctypes").c_void_p), n)
+        assert np.float32(got) == b[0]
+
+
+# --------------------------------------------------------------- generators
+def test_generators(orc):
+    c = orc.gen_codes(1, 400000)
+    assert c.min() == -127 and c.max() == 127 and abs(c.mean()) < 0.5
+    z = orc.gen_normal(2, 400000)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
+    s = orc.gen_scales(3, 100000)
+    sv = s.view(np.float16).astype(np.float32)
+    assert (sv >= 0).all() and abs(sv.mean() - 0.01 * math.sqrt(2 / math.pi)) < 2e-4
+    t = orc.gen_ternary(4, 100000)
+    codes = np.stack([(t >> (2 * k)) & 3 for k in range(4)])
+    assert codes.max() == 2 and abs(codes.mean() - 1.0) < 0.01
+    # counter-based: a prefix of a longer stream is the shorter stream
+    assert np.array_equal(orc.gen_codes(9, 1000), orc.gen_codes(9, 5000)[:1000])
+
+
+# --------------------------------------------------------------- quantizers
+def test_q8_quant_properties(orc):
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal(64 * 32) * 10.0 ** rng.integers(-3, 3, 64 * 32)).astype(np.float32)
+    x[:32] = 0.0
+    qx, dx = orc.q8_quant(x)
+    xb, qb = x.reshape(-1, 32), qx.reshape(-1, 32).astype(np.int32)
+    assert dx[0] == 0 and not qb[0].any()
+    amax = np.abs(xb).max(1)
+    assert np.array_equal(f32bits(dx), f32bits((amax / np.float32(127)).astype(np.float32)))
+    assert np.abs(qb).max() <= 127
+    i = np.abs(xb[1:]).argmax(1)
+    assert (np.abs(qb[1:][np.arange(63), i]) == 127).all()
+    err = np.abs(qb[1:] * dx[1:, None].astype(np.float64) - xb[1:])
+    assert (err <= dx[1:, None] * 0.5000001 + 1e-30).all()
+
+
+def test_q8k_quant_properties(orc):
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal(4 * 256).astype(np.float32)
+    x[256:512] = 0.0
+    out = orc.q8k_quant(x)
+    for b in range(4):
+        blk = out[b * 292:(b + 1) * 292]
+        d = blk[:4].view(np.float32)[0]
+        qs = blk[4:260].view(np.int8).astype(np.int32)
+        bs = blk[260:292].view(np.int16)
+        xb = x[b * 256:(b + 1) * 256]
+        if b == 1:
+            assert d == 0 and not qs.any()
+            continue
+        j = int(np.argmax(np.abs(xb)))
+        assert qs[j] == -127                            # iscale = -127/max maps max to -127
+        assert np.array_equal(bs, qs.reshape(16, 16).sum(1))
+        assert np.abs(qs * np.float64(d) - xb).max() <= abs(d) * 0.5000001
+
+
+# ------------------------------------------------------------------- GEMVs
+def _q8_case(orc, seed, N, K):
+    W, S = orc.q8_weights(seed, N, K)
+    x = orc.gen_normal(seed + 2, K)
+    qx, dx = orc.q8_quant(x)
+    return W, S, qx, dx
+
+
+def test_r1_gemv_vs_exact(orc):
+    for N, K in [(97, 2048), (33, 8192), (5, 96), (3, 288)]:
+        W, S, qx, dx = _q8_case(orc, 100 + K, N, K)
+        y = orc.q8_gemv(W, S, qx, dx)
+        ye = orc.q8_gemv_exact(W, S, qx, dx)
+        isum = (W.reshape(N, -1, 32).astype(np.int64) * qx.reshape(-1, 32)).sum(-1)
+        den = (np.abs(isum) * S.view(np.float16).astype(np.float64) * dx).sum(-1)
+        assert (np.abs(y - ye) / den).max() <= 1e-5
+
+
+def test_r1_gemv_closed_forms(orc):
+    """One block: y = fl(fl(dw*dx) * isum). Two 8-block chunks: y = fl(a0 + a1)."""
+    W, S, qx, dx = _q8_case(orc, 7, 4, 32)
+    y = orc.q8_gemv(W, S, qx, dx)
+    isum = (W.astype(np.int64) * qx).sum(1)
+    s = (S[:, 0].view(np.float16).astype(np.float32) * dx[0]).astype(np.float32)
+    assert np.array_equal(f32bits(y), f32bits((s * isum.astype(np.float32)).astype(np.float32)))
+    # a one-block-per-chunk layout: blocks 0 and 8 nonzero, the rest zero
+    W, S, qx, dx = _q8_case(orc, 8, 4, 512)
+    W = W.copy()
+    keep = np.zeros(16, bool)
+    keep[[0, 8]] = True
+    W.reshape(4, 16, 32)[:, ~keep] = 0
+    y = orc.q8_gemv(W, S, qx, dx)
+    parts = []
+    for b in (0, 8):
+        isum = (W[:, 32 * b:32 * b + 32].astype(np.int64) * qx[32 * b:32 * b + 32]).sum(1).astype(np.float32)
+        s = (S[:, b].view(np.float16).astype(np.float32) * dx[b]).astype(np.float32)
+        parts.append((s * isum).astype(np.float32))
+    assert np.array_equal(f32bits(y), f32bits((parts[0] + parts[1]).astype(np.float32)))
+
+
+def test_a11_is_reference_code(orc):
+    """orc_q8_gemv_a11 restates gemv_q8 (q8_gemv_cpu.c:29-58): bit-equal to it."""
+    ref = orc.ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    import ctypes as C
+    for N, K in [(97, 2048), (64, 7680), (13, 64)]:
+        W, S, qx, dx = _q8_case(orc, 200 + K, N, K)
+        S32 = S.view(np.float16).astype(np.float32)
+        x = (qx.astype(np.float32).reshape(-1, 32) * dx[:, None]).reshape(-1).astype(np.float32)
+        ya = orc.q8_gemv_a11(W, S32, x)
+        yr = np.empty(N, np.float32)
+        ref.ref_q8_gemv(W.ctypes.data_as(C.c_void_p), S32.ctypes.data_as(C.c_void_p),
+                        x.ctypes.data_as(C.c_void_p), yr.ctypes.data_as(C.c_void_p), C.c_int(N), C.c_int(K))
+        assert np.array_equal(f32bits(ya), f32bits(yr))
+        # and R1 agrees with the reference's own order within 1e-5 of sum |terms|
+        y = orc.q8_gemv(W, S, qx, dx)
+        isum = (W.reshape(N, -1, 32).astype(np.int64) * qx.reshape(-1, 32)).sum(-1)
+        den = (np.abs(isum) * S32.astype(np.float64) * dx).sum(-1)
+        assert (np.abs(y.astype(np.float64) - yr) / den).max() <= 1e-5
+
+
+def test_gemm_is_per_position_gemv(orc):
+    W, S = orc.q8_weights(31, 70, 288)
+    x = orc.gen_normal(32, 5 * 288).reshape(5, 288)
+    qx, dx = orc.q8_quant(x)
+    Y = orc.q8_gemm(W, S, qx, dx)
+    for t in range(5):
+        assert np.array_equal(f32bits(Y[t]), f32bits(orc.q8_gemv(W, S, qx[t], dx[t])))
+
+
+@pytest.mark.parametrize("N,K", [(37, 9728), (61, 2560), (8, 4096), (3, 256)])
+def test_tq2_is_reference_code(orc, N, K):
+    """orc_tq2_gemv restates pq2_gemv_cpu (pq2_host.c:82-104): bit-equal to it
+    (the shapes are the reference's pq1t_parity.c row widths, fewer rows)."""
+    ref = orc.ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    import ctypes as C
+    codes = orc.gen_ternary(K + N, N * K // 4)
+    S = orc.gen_scales(K + N + 1, N * K // 128)
+    xq = orc.q8k_quant(orc.gen_normal(K + N + 2, K))
+    y = orc.tq2_gemv(codes, S, xq, N, K)
+    yr = np.empty(N, np.float32)
+    ref.pq2_gemv_cpu(C.c_int(N), C.c_int(K), codes.ctypes.data_as(C.c_void_p), S.ctypes.data_as(C.c_void_p),
+                     xq.ctypes.data_as(C.c_void_p), yr.ctypes.data_as(C.c_void_p))
+    assert np.array_equal(f32bits(y), f32bits(yr))
+
+
+def test_tq2_exact_int(orc):
+    """The ternary int32 group dots, recomputed in int64 with the code-1 mapping."""
+    N, K = 5, 512
+    codes = orc.gen_ternary(41, N * K // 4)
+    S = np.full(N * K // 128, 0x3C00, np.uint16)       # scale 1.0
+    x = orc.gen_normal(42, K)
+    xq = orc.q8k_quant(x)
+    y = orc.tq2_gemv(codes, S, xq, N, K)
+    vals = np.stack([(codes >> (2 * k)) & 3 for k in range(4)], 1).reshape(N, K).astype(np.int64) - 1
+    qs = np.concatenate([xq[b * 292 + 4:b * 292 + 260].view(np.int8) for b in range(K // 256)]).astype(np.int64)
+    d = np.array([xq[b * 292:b * 292 + 4].view(np.float32)[0] for b in range(K // 256)], np.float64)
+    want = (vals.reshape(N, -1, 256) * qs.reshape(-1, 256)).sum(-1) @ d
+    assert np.allclose(y, want, rtol=1e-6, atol=1e-6)
+
+
+# -------------------------------------------------------- layer primitives
+def test_rmsnorm_vs_double(orc):
+    rng = np.random.default_rng(19)
+    x = orc.f2bf(rng.standard_normal(2048).astype(np.float32) * 3)
+    w = (1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)
+    y = orc.bf2f(orc.rmsnorm(x, w))
+    xf = orc.bf2f(x).astype(np.float64)
+    want = w * (xf / np.sqrt((xf ** 2).mean() + 1e-5))
+    assert np.abs(y - want).max() <= np.abs(want).max() * 2 ** -7
+
+
+def test_attention_vs_two_pass(orc):
+    nh, nkv, hd = 8, 2, 64
+    for npos in (1, 5, 64, 65, 300):
+        q = orc.f2bf(orc.gen_normal(50 + npos, nh * hd))
+        Kc = orc.gen_normal(51 + npos, npos * nkv * hd).astype(np.float16).view(np.uint16)
+        Vc = orc.gen_normal(52 + npos, npos * nkv * hd).astype(np.float16).view(np.uint16)
+        a = orc.bf2f(orc.attn(q, Kc, Vc, npos, nh, nkv, hd, 0.125))
+        b = orc.attn_twopass(q, Kc, Vc, npos, nh, nkv, hd, 0.125)
+        assert np.abs(a - b).max() <= np.abs(b).max() * 2 ** -7
+        if npos == 1:   # one key: the output is v_0 of the head's kv group, rounded to bf16
+            v0 = Vc.view(np.float16).astype(np.float32).reshape(nkv, hd)
+            want = orc.f2bf(np.repeat(v0, nh // nkv, axis=0).reshape(-1))
+            assert np.array_equal(orc.attn(q, Kc, Vc, 1, nh, nkv, hd, 0.125), want)
+
+
+def test_conv_impulse_response(orc):
+    H, nt = 64, 3
+    taps = orc.gen_normal(60, H * nt)
+    one = orc.f2bf(np.ones(H, np.float32))
+    zero = np.zeros(H, np.uint16)
+    ring = np.zeros(nt * H, np.uint16)
+    outs = []
+    for step in range(nt + 1):
+        x = one if step == 0 else zero
+        bcx = np.concatenate([one, one, x])        # B = 1, C = 1, x = impulse
+        o, ring = orc.conv_step(ring, taps, bcx, H, nt)
+        outs.append(o)
+    for k in range(nt):   # step k sees the impulse in ring slot nt-1-k
+        assert np.array_equal(outs[k], orc.f2bf(taps.reshape(H, nt)[:, nt - 1 - k]))
+    assert not outs[nt].any()
+
+
+def test_silu_and_gate(orc):
+    rng = np.random.default_rng(23)
+    a = orc.f2bf(rng.standard_normal(4096).astype(np.float32) * 8)
+    b = orc.f2bf(rng.standard_normal(4096).astype(np.float32))
+    y = orc.bf2f(orc.silu_mul(a, b))
+    af, bf = orc.bf2f(a).astype(np.float64), orc.bf2f(b).astype(np.float64)
+    want = af / (1 + np.exp(-af)) * bf
+    assert (np.abs(y - want) <= np.abs(want) * 2 ** -7 + 1e-30).all()
+    g = orc.f2bf(np.array([0.0, 100.0, -100.0, 1.5], np.float32))
+    at = orc.f2bf(np.ones(4 * 8, np.float32))
+    out = orc.bf2f(orc.sigmoid_gate(g, at, 4, 8)).reshape(4, 8)
+    assert (out[0] == 0.5).all() and (out[1] == 1.0).all() and (out[2] == 0.0).all()
+
+
+def test_argmax_lowest_index(orc):
+    v = np.array([1.0, 3.0, -2.0, 3.0, 3.0], np.float32)
+    assert orc.argmax(v) == 1
+
+
+# ----------------------------------------------------------------- backbone
+TINY = dict(hidden=256, ffn=512, vocab=1000, nlayers=4, nh=4, nkv=2, hd=64, rot=32, ntaps=3, ctx=256,
+            eps=1e-5, theta=1e6, seed=20261201, attn_mask=0b1010)
+
+
+def test_model_batched_equals_sequential(orc):
+    m = orc.Model(**TINY)
+    prompt = orc.gen_tokens(5, 40, TINY["vocab"])
+    r1, lg1 = m.feed(prompt, True)
+    h1 = m.hidden()
+    m.reset()
+    for t in prompt[:-1]:
+        m.feed(np.array([t], np.int32))
+    r2, lg2 = m.feed(prompt[-1:], True)
+    assert r1 == r2 and np.array_equal(f32bits(lg1), f32bits(lg2)) and np.array_equal(h1, m.hidden())
+    m.close()
+
+
+def test_model_head_composition(orc):
+    """Logits are the tied Q8 head applied to the final-normed residual, and the
+    greedy stream does not collapse onto one token."""
+    m = orc.Model(**TINY)
+    prompt = orc.gen_tokens(6, 17, TINY["vocab"])
+    r, lg = m.feed(prompt, True)
+    W, S = m.tensor(-1, 0)
+    fn = m.tensor(-1, 1)
+    h = orc.rmsnorm(m.hidden(), fn, 1e-5)
+    qx, dx = orc.q8_quant_bf16(h)
+    assert np.array_equal(f32bits(orc.q8_gemv(W, S, qx, dx)), f32bits(lg))
+    assert r == orc.argmax(lg)
+    ids = m.greedy(prompt, 16)
+    assert len(set(ids.tolist())) >= 6
+    m.close()
