@@ -86,6 +86,120 @@ int pq_q8_gemv(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, 
 int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
                void *y, int y_dtype, int N, int K, int T, void *stream);
 
+/* ======================================================= layer operations
+ * bf16 activations are raw uint16 bits. T positions are rows of the given
+ * stride (position-first). Each op rounds once to bf16 where the reference's
+ * kernel does (lfm3_nanode.cu:383-498, 811-941). */
+
+/* RMSNorm of T rows of H (a power of two, 64..8192), sum of squares as a
+ * pairwise tree, rs = 1/sqrtf(ss/H + eps), y = bf16(w * bf16(x * rs)).
+ * Residual form (h != NULL): h3 = rmsnorm(h, w0); x = bf16(x + h3) (x is
+ * updated in place); out = rmsnorm(x, w1) -- one call for layer_body's
+ * "rms1(post_norm) -> eadd -> rms1(next_norm)" triple (3819-3851). The
+ * output goes to y (bf16) and/or to (qx, dx) as Q8_0 for the next GEMV.
+ * Replaces k_rmsnorm / k_rmsnorm_T / rmsnorm_body (383-456) and k_add_bf(4). */
+int pq_rmsnorm(uint16_t *x, const uint16_t *h, const float *w0, const float *w1, uint16_t *y,
+               int8_t *qx, float *dx, int H, int T, float eps, void *stream);
+
+/* Per-head q/k RMSNorm, zero-tail partial RoPE from a [pos][rot/2][cos,sin]
+ * table, and the fp16 KV-cache write of k and v at positions pos0..pos0+T-1.
+ * qkv rows hold [q (nh*hd) | k (nkv*hd) | v (nkv*hd) | ...] with row_stride
+ * elements; q is updated in place. head_dim 64. Replaces k_headnorm,
+ * k_rope and the KV write (460-498, 157-162, 3749-3778). */
+int pq_qk_prep(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm,
+               const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv,
+               int hd, int rot, int T, float eps, void *stream);
+
+/* Split-K flash-decode attention over the fp16 cache [ctx][nkv][hd]: query t
+ * (row t of q, stride q_stride) at position pos0+t attends keys 0..pos0+t.
+ * Splits of 64 positions, merged in ascending order; then the per-head
+ * sigmoid gate (gate row t, stride gate_stride; NULL for none). Output to
+ * out (bf16, stride out_stride) and/or (qx, dx) as Q8_0 for o_proj. ws holds
+ * the split partials (pq_attn_workspace_bytes). Replaces k_attn_head(G) and
+ * k_sigmoid_gate(4) (503-809, 852-888). */
+size_t pq_attn_workspace_bytes(int nh, int max_pos, int T);
+int pq_attn_decode(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                   const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int8_t *qx,
+                   float *dx, int pos0, int nh, int nkv, int hd, int T, float scale, void *ws,
+                   size_t ws_bytes, void *stream);
+
+/* Gated short conv over T positions: bcx rows [B | C | x] (3H), ring
+ * [ntaps][H] bf16 (newest last, updated), out [T][H] bf16 = bf16(C * conv(B*x)).
+ * ntaps 2, 3, 4 or 7. Replaces k_shift_in + k_conv7 / k_conv_chunk (892-941). */
+int pq_conv(uint16_t *ring, const float *taps, const uint16_t *bcx, uint16_t *out, int H, int T,
+            int ntaps, void *stream);
+
+/* silu(gate) * up over rows [gate (F) | up (F)]; output bf16 and/or Q8_0.
+ * Replaces k_silu_mul_bf(v) (821-847). */
+int pq_silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T, void *stream);
+
+/* Greedy id: the lowest index among the maxima of v[n]. Replaces k_argmax
+ * (942-964; the reference breaks ties by thread slot). */
+int pq_argmax(const float *v, int n, int32_t *out, void *stream);
+
+/* Embedding rows of T token ids (device) from the packed tied Q8_0 table:
+ * bf16(code * scale); ids outside [0, vocab) give zero rows. Replaces
+ * k_dequant_row (138-142). */
+int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *tokens, uint16_t *out,
+             int H, int vocab, int T, void *stream);
+
+/* ==================================================== synthetic generator
+ * Host-side fill of a synthetic tensor (there is no checkpoint offline):
+ * splitmix64 output n = mix(seed + (n+1)*0x9e3779b97f4a7c15), used as
+ *   CODES   int8 in [-127,127]   SCALES fp16 bits of |N(0,1)| * a
+ *   NORMAL  float N(0,1)         AFFINE float a + b * N(0,1)
+ *   TERNARY PQ2_0 code bytes, codes in {0,1,2}   TOKENS int32 in [0, a) */
+#define PQ_SYNTH_CODES 0
+#define PQ_SYNTH_NORMAL 1
+#define PQ_SYNTH_SCALES 2
+#define PQ_SYNTH_AFFINE 3
+#define PQ_SYNTH_TERNARY 4
+#define PQ_SYNTH_TOKENS 5
+int pq_synth_fill(int kind, uint64_t seed, void *out_host, size_t n, float a, float b);
+
+/* ================================================================ engine
+ * The backbone on one GPU: weights resident in HBM (packed Q8_0), fp16 KV
+ * cache, conv rings, a prefill path in chunks of prefill_chunk positions (the
+ * batched MFMA GEMM) and a T=1 decode path (the GEMV), all on the engine's own
+ * stream. Layer kinds come from attn_mask (bit L set = attention layer).
+ * Host pointers: tokens, ids, logits, tensors passed to pq_engine_set_*.
+ * The call sequence restates lfm3_nanode.cu main()/layer_body (3739-3856,
+ * 5828-6340) with the reference's host contract: arenas allocated once at
+ * create, errors returned instead of exit(2). */
+typedef struct pq_model_cfg {
+  int hidden, ffn, vocab, nlayers;
+  int nh, nkv, hd, rot;      /* rot = rotated dims (partial rotary factor * hd) */
+  int ntaps, ctx;            /* conv kernel size; KV capacity                   */
+  float eps, theta;
+  uint64_t seed;             /* synthetic weights                              */
+  uint32_t attn_mask;
+  int prefill_chunk;         /* positions per prefill launch (32)               */
+} pq_model_cfg;
+
+void *pq_engine_create(const pq_model_cfg *cfg);             /* NULL on failure */
+int pq_engine_destroy(void *engine);
+int pq_engine_load_synthetic(void *engine);
+/* Load one tensor from host memory (the blob loader's boundary, lfm3_nanode.cu:
+ * 1294-1402): Q8 slots 0 mixer in, 1 mixer out, 2 gate/up, 3 down (layer -1
+ * slot 0 = tied embedding); fp32 slots 4..7 norms, 8/9 q/k norm, 10 conv taps
+ * (layer -1 slot 1 = final norm). Call pq_engine_mark_loaded when done. */
+int pq_engine_set_q8(void *engine, int layer, int slot, const int8_t *codes, const uint16_t *scales);
+int pq_engine_set_f32(void *engine, int layer, int slot, const float *v, size_t n);
+int pq_engine_mark_loaded(void *engine);
+int pq_engine_reset(void *engine);
+/* Feed n tokens (prefill chunks); the greedy id after the last one and its
+ * fp32 logits (either may be NULL) come back to the host. */
+int pq_engine_feed(void *engine, const int32_t *tokens, int n, int32_t *next_id, float *logits);
+/* reset, prompt, then n_steps greedy ids (ids[0] from the prompt's last position). */
+int pq_engine_greedy(void *engine, const int32_t *prompt, int n_prompt, int n_steps, int32_t *ids);
+/* n_steps T=1 decode steps from the current device-side token; ids may be NULL. */
+int pq_engine_decode(void *engine, int n_steps, int32_t *ids);
+int pq_engine_sync(void *engine);
+void *pq_engine_stream(void *engine);
+int pq_engine_position(void *engine);
+int pq_engine_hidden(void *engine, uint16_t *out_host);
+size_t pq_engine_weight_bytes(void *engine);
+
 #ifdef __cplusplus
 }
 #endif

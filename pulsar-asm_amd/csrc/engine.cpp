@@ -1,0 +1,492 @@
+// engine.cpp -- the C++ host side of the LFM3-style backbone on one MI355X.
+//
+// Keeps the reference's host contract (lfm3_nanode.cu): arenas allocated once
+// and never resized (5431), one launch stream, a per-layer call sequence that
+// restates layer_body (3739-3856) for T=1 and layer_chunk_T (4997-5131) for a
+// prefill chunk, the embedding_norm + tied LM head + argmax after the last layer
+// (6183, 5171-5179, 6229). Every device step is a C-ABI entry point of this
+// library; the engine owns buffers and ordering only.
+//
+// Layer (attention):  rmsnorm(op_norm) -> Q8 -> [q|k|v|gate] GEMV -> q/k norm +
+//   RoPE + fp16 KV write -> split-K attention + sigmoid gate -> Q8 -> o_proj
+// Layer (conv):       rmsnorm(op_norm) -> Q8 -> [B|C|x] GEMV -> gated conv -> Q8
+//   -> out_proj
+// then:  post_operator_norm + residual + ffn_norm -> Q8 -> gate/up GEMV ->
+//   silu(gate)*up -> Q8 -> down GEMV -> post_ffn_norm + residual + next norm -> Q8.
+// The residual adds are fused into the following norm (one kernel per
+// "rms1 -> eadd -> rms1" triple of layer_body, same values and roundings).
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <memory>
+#include <vector>
+
+#include "pq_host.h"
+
+namespace pq {
+
+struct Q8Dev {
+  int8_t *pc = nullptr;
+  uint16_t *ps = nullptr;
+  int N = 0, K = 0;
+};
+
+struct LayerDev {
+  int attn = 0;
+  Q8Dev in, out, ug, down;
+  float *op_norm = nullptr, *post_op_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
+  float *q_norm = nullptr, *k_norm = nullptr, *taps = nullptr;
+  uint16_t *kc = nullptr, *vc = nullptr, *ring = nullptr;
+};
+
+struct Engine {
+  pq_model_cfg c{};
+  hipStream_t st = nullptr;
+  std::vector<LayerDev> L;
+  Q8Dev emb;
+  float *final_norm = nullptr, *rope = nullptr;
+  int pos = 0, tmax = 0, qd = 0, kvd = 0, nin = 0, last_t = 1;
+  // activations, sized for tmax positions
+  uint16_t *X = nullptr, *Hb = nullptr, *Wd = nullptr, *A = nullptr;
+  int8_t *qx = nullptr;
+  float *dx = nullptr, *logits = nullptr;
+  int32_t *tok = nullptr, *ids = nullptr;
+  int max_ids = 0;
+  void *attn_ws = nullptr;
+  size_t attn_ws_bytes = 0;
+  std::vector<void *> allocs;
+  bool loaded = false;
+
+  ~Engine() {
+    if (st) hipStreamSynchronize(st);
+    for (void *p : allocs) hipFree(p);
+    if (st) hipStreamDestroy(st);
+  }
+
+  template <typename T>
+  int dalloc(T **p, size_t count) {
+    void *q = nullptr;
+    const size_t bytes = count * sizeof(T) ? count * sizeof(T) : 16;
+    const hipError_t e = hipMalloc(&q, bytes);
+    if (e != hipSuccess) return fail(PQ_ERR_LAUNCH, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    allocs.push_back(q);
+    *p = static_cast<T *>(q);
+    return PQ_OK;
+  }
+};
+
+#define PQ_TRY(expr)             \
+  do {                           \
+    const int _rc = (expr);      \
+    if (_rc != PQ_OK) return _rc; \
+  } while (0)
+
+static int alloc_q8(Engine &E, Q8Dev &q, int N, int K) {
+  q.N = N;
+  q.K = K;
+  PQ_TRY(E.dalloc(&q.pc, pq_q8_packed_codes_bytes(N, K)));
+  PQ_TRY(E.dalloc(&q.ps, pq_q8_packed_scales_bytes(N, K) / 2));
+  return PQ_OK;
+}
+
+static int create(Engine &E, const pq_model_cfg &c) {
+  E.c = c;
+  const int H = c.hidden, F = c.ffn;
+  E.qd = c.nh * c.hd;
+  E.kvd = c.nkv * c.hd;
+  E.nin = E.qd + 2 * E.kvd + c.nh;
+  E.tmax = c.prefill_chunk;
+  if (hipStreamCreateWithFlags(&E.st, hipStreamNonBlocking) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "hipStreamCreate failed");
+  E.L.resize(c.nlayers);
+  for (int l = 0; l < c.nlayers; l++) {
+    LayerDev &D = E.L[l];
+    D.attn = (int)((c.attn_mask >> l) & 1u);
+    if (D.attn) {
+      PQ_TRY(alloc_q8(E, D.in, E.nin, H));
+      PQ_TRY(alloc_q8(E, D.out, H, E.qd));
+      PQ_TRY(E.dalloc(&D.q_norm, c.hd));
+      PQ_TRY(E.dalloc(&D.k_norm, c.hd));
+      PQ_TRY(E.dalloc(&D.kc, (size_t)c.ctx * E.kvd));
+      PQ_TRY(E.dalloc(&D.vc, (size_t)c.ctx * E.kvd));
+    } else {
+      PQ_TRY(alloc_q8(E, D.in, 3 * H, H));
+      PQ_TRY(alloc_q8(E, D.out, H, H));
+      PQ_TRY(E.dalloc(&D.taps, (size_t)H * c.ntaps));
+      PQ_TRY(E.dalloc(&D.ring, (size_t)H * c.ntaps));
+    }
+    PQ_TRY(alloc_q8(E, D.ug, 2 * F, H));
+    PQ_TRY(alloc_q8(E, D.down, H, F));
+    PQ_TRY(E.dalloc(&D.op_norm, H));
+    PQ_TRY(E.dalloc(&D.post_op_norm, H));
+    PQ_TRY(E.dalloc(&D.ffn_norm, H));
+    PQ_TRY(E.dalloc(&D.post_ffn_norm, H));
+  }
+  PQ_TRY(alloc_q8(E, E.emb, c.vocab, H));
+  PQ_TRY(E.dalloc(&E.final_norm, H));
+  PQ_TRY(E.dalloc(&E.rope, (size_t)c.ctx * (c.rot / 2) * 2 + 2));
+  const int T = E.tmax;
+  const int wide = std::max(std::max(3 * H, 2 * F), E.nin);
+  const int kmax = std::max(std::max(H, F), E.qd);
+  PQ_TRY(E.dalloc(&E.X, (size_t)T * H));
+  PQ_TRY(E.dalloc(&E.Hb, (size_t)T * H));
+  PQ_TRY(E.dalloc(&E.Wd, (size_t)T * wide));
+  PQ_TRY(E.dalloc(&E.A, (size_t)T * kmax));
+  PQ_TRY(E.dalloc(&E.qx, (size_t)T * kmax));
+  PQ_TRY(E.dalloc(&E.dx, (size_t)T * kmax / 32));
+  PQ_TRY(E.dalloc(&E.logits, (size_t)c.vocab));
+  PQ_TRY(E.dalloc(&E.tok, (size_t)T));
+  E.max_ids = c.ctx + 1;
+  PQ_TRY(E.dalloc(&E.ids, (size_t)E.max_ids));
+  E.attn_ws_bytes = pq_attn_workspace_bytes(c.nh, c.ctx, T);
+  PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.attn_ws), E.attn_ws_bytes));
+  return PQ_OK;
+}
+
+// ------------------------------------------------------------ weight upload
+static int upload_q8(Engine &E, Q8Dev &q, const int8_t *codes, const uint16_t *scales) {
+  int8_t *dc = nullptr;
+  uint16_t *ds = nullptr;
+  const size_t nc = (size_t)q.N * q.K, ns = (size_t)q.N * (q.K / 32);
+  if (hipMalloc(&dc, nc) != hipSuccess) return fail(PQ_ERR_LAUNCH, "hipMalloc staging failed");
+  if (hipMalloc(&ds, ns * 2) != hipSuccess) {
+    hipFree(dc);
+    return fail(PQ_ERR_LAUNCH, "hipMalloc staging failed");
+  }
+  int rc = PQ_OK;
+  if (hipMemcpyAsync(dc, codes, nc, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+      hipMemcpyAsync(ds, scales, ns * 2, hipMemcpyHostToDevice, E.st) != hipSuccess)
+    rc = fail(PQ_ERR_LAUNCH, "weight upload failed");
+  if (rc == PQ_OK) rc = pq_q8_pack(dc, ds, q.N, q.K, q.pc, q.ps, E.st);
+  if (hipStreamSynchronize(E.st) != hipSuccess && rc == PQ_OK) rc = fail(PQ_ERR_LAUNCH, "weight pack failed");
+  hipFree(dc);
+  hipFree(ds);
+  return rc;
+}
+
+static int upload_f32(Engine &E, float *dst, const float *src, size_t n) {
+  if (hipMemcpyAsync(dst, src, n * 4, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+      hipStreamSynchronize(E.st) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "upload failed");
+  return PQ_OK;
+}
+
+static Q8Dev *q8_slot(Engine &E, int layer, int slot) {
+  if (layer == -1) return slot == 0 ? &E.emb : nullptr;
+  if (layer < 0 || layer >= (int)E.L.size()) return nullptr;
+  LayerDev &D = E.L[layer];
+  switch (slot) {
+    case 0: return &D.in;
+    case 1: return &D.out;
+    case 2: return &D.ug;
+    case 3: return &D.down;
+    default: return nullptr;
+  }
+}
+
+static float *vec_slot(Engine &E, int layer, int slot, size_t *n) {
+  const int H = E.c.hidden;
+  if (layer == -1) {
+    if (slot == 1) { *n = H; return E.final_norm; }
+    return nullptr;
+  }
+  if (layer < 0 || layer >= (int)E.L.size()) return nullptr;
+  LayerDev &D = E.L[layer];
+  *n = H;
+  switch (slot) {
+    case 4: return D.op_norm;
+    case 5: return D.post_op_norm;
+    case 6: return D.ffn_norm;
+    case 7: return D.post_ffn_norm;
+    case 8: *n = E.c.hd; return D.q_norm;
+    case 9: *n = E.c.hd; return D.k_norm;
+    case 10: *n = (size_t)H * E.c.ntaps; return D.taps;
+    default: return nullptr;
+  }
+}
+
+static void rope_table(std::vector<float> &cs, int ctx, int hd, int rot, float theta) {
+  const int half = rot / 2;
+  cs.assign((size_t)ctx * half * 2 + 2, 0.0f);
+  for (int p = 0; p < ctx; p++)
+    for (int i = 0; i < half; i++) {
+      const float invf = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)hd));
+      const float ang = (float)p * invf;
+      cs[((size_t)p * half + i) * 2] = (float)cos((double)ang);
+      cs[((size_t)p * half + i) * 2 + 1] = (float)sin((double)ang);
+    }
+}
+
+// Synthetic weights: tensor t draws from seed + 4t + part (0 codes, 1 scales,
+// 2 fp32 parameters); t = 16*layer + slot, embedding 4000, final norm 4001.
+static int load_synthetic(Engine &E) {
+  const pq_model_cfg &c = E.c;
+  auto seed = [&](int t, int part) { return c.seed + 4ull * (uint64_t)t + (uint64_t)part; };
+  std::vector<int8_t> codes;
+  std::vector<uint16_t> scales;
+  std::vector<float> vec;
+  auto q8 = [&](Q8Dev &q, int t) -> int {
+    codes.resize((size_t)q.N * q.K);
+    scales.resize((size_t)q.N * (q.K / 32));
+    pq_synth_fill(PQ_SYNTH_CODES, seed(t, 0), codes.data(), codes.size(), 0, 0);
+    pq_synth_fill(PQ_SYNTH_SCALES, seed(t, 1), scales.data(), scales.size(), 0.01f, 0);
+    return upload_q8(E, q, codes.data(), scales.data());
+  };
+  auto fv = [&](float *dst, int t, size_t n, float a, float b) -> int {
+    vec.resize(n);
+    pq_synth_fill(PQ_SYNTH_AFFINE, seed(t, 2), vec.data(), n, a, b);
+    return upload_f32(E, dst, vec.data(), n);
+  };
+  const int H = c.hidden;
+  for (int l = 0; l < c.nlayers; l++) {
+    LayerDev &D = E.L[l];
+    const int t0 = 16 * l;
+    PQ_TRY(q8(D.in, t0 + 0));
+    PQ_TRY(q8(D.out, t0 + 1));
+    PQ_TRY(q8(D.ug, t0 + 2));
+    PQ_TRY(q8(D.down, t0 + 3));
+    PQ_TRY(fv(D.op_norm, t0 + 4, H, 1.0f, 0.1f));
+    PQ_TRY(fv(D.post_op_norm, t0 + 5, H, 4.0f, 0.4f));
+    PQ_TRY(fv(D.ffn_norm, t0 + 6, H, 1.0f, 0.1f));
+    PQ_TRY(fv(D.post_ffn_norm, t0 + 7, H, 4.0f, 0.4f));
+    if (D.attn) {
+      PQ_TRY(fv(D.q_norm, t0 + 8, c.hd, 1.0f, 0.1f));
+      PQ_TRY(fv(D.k_norm, t0 + 9, c.hd, 1.0f, 0.1f));
+    } else {
+      PQ_TRY(fv(D.taps, t0 + 10, (size_t)H * c.ntaps, 0.0f, 0.5f));
+    }
+  }
+  PQ_TRY(q8(E.emb, 4000));
+  PQ_TRY(fv(E.final_norm, 4001, H, 1.0f, 0.1f));
+  return PQ_OK;
+}
+
+static int upload_rope(Engine &E) {
+  std::vector<float> cs;
+  rope_table(cs, E.c.ctx, E.c.hd, E.c.rot, E.c.theta);
+  return upload_f32(E, E.rope, cs.data(), cs.size());
+}
+
+// Zero KV caches and conv rings with a kernel-free copy of a zero host buffer
+// (allocated once per reset; reset is not on the decode path).
+static int reset(Engine &E) {
+  std::vector<uint16_t> z;
+  for (LayerDev &D : E.L) {
+    const size_t n = D.attn ? (size_t)E.c.ctx * E.kvd : (size_t)E.c.hidden * E.c.ntaps;
+    z.assign(n, 0);
+    if (D.attn) {
+      if (hipMemcpyAsync(D.kc, z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+          hipMemcpyAsync(D.vc, z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess)
+        return fail(PQ_ERR_LAUNCH, "reset copy failed");
+    } else if (hipMemcpyAsync(D.ring, z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess) {
+      return fail(PQ_ERR_LAUNCH, "reset copy failed");
+    }
+    if (hipStreamSynchronize(E.st) != hipSuccess) return fail(PQ_ERR_LAUNCH, "reset sync failed");
+  }
+  E.pos = 0;
+  return PQ_OK;
+}
+
+// ---------------------------------------------------------------- forward
+static int gemv_or_gemm(Engine &E, const Q8Dev &w, void *y, int T) {
+  if (T == 1) return pq_q8_gemv(w.pc, w.ps, E.qx, E.dx, y, PQ_DTYPE_BF16, w.N, w.K, E.st);
+  return pq_q8_gemm(w.pc, w.ps, E.qx, E.dx, y, PQ_DTYPE_BF16, w.N, w.K, T, E.st);
+}
+
+// Runs T <= tmax positions whose token ids are in E.tok (device) through all
+// layers; leaves the greedy id of the last position in *next (device).
+static int forward(Engine &E, int T, int32_t *next) {
+  const pq_model_cfg &c = E.c;
+  const int H = c.hidden, F = c.ffn;
+  if (E.pos + T > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + %d > %d", E.pos, T, c.ctx);
+  PQ_TRY(pq_embed(E.emb.pc, E.emb.ps, E.tok, E.X, H, c.vocab, T, E.st));
+  PQ_TRY(pq_rmsnorm(E.X, nullptr, E.L[0].op_norm, nullptr, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
+  const float scale = 1.0f / sqrtf((float)c.hd);
+  for (int l = 0; l < c.nlayers; l++) {
+    LayerDev &D = E.L[l];
+    if (D.attn) {
+      PQ_TRY(gemv_or_gemm(E, D.in, E.Wd, T));
+      PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd, c.rot, T,
+                        c.eps, E.st));
+      PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, nullptr, 0, E.qx, E.dx, E.pos,
+                            c.nh, c.nkv, c.hd, T, scale, E.attn_ws, E.attn_ws_bytes, E.st));
+      PQ_TRY(gemv_or_gemm(E, D.out, E.Hb, T));
+    } else {
+      PQ_TRY(gemv_or_gemm(E, D.in, E.Wd, T));
+      PQ_TRY(pq_conv(D.ring, D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
+      PQ_TRY(pq_q8_quant_bf16(E.A, E.qx, E.dx, H, T, E.st));
+      PQ_TRY(gemv_or_gemm(E, D.out, E.Hb, T));
+    }
+    PQ_TRY(pq_rmsnorm(E.X, E.Hb, D.post_op_norm, D.ffn_norm, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
+    PQ_TRY(gemv_or_gemm(E, D.ug, E.Wd, T));
+    PQ_TRY(pq_silu_mul(E.Wd, nullptr, E.qx, E.dx, F, T, E.st));
+    PQ_TRY(gemv_or_gemm(E, D.down, E.Hb, T));
+    const float *next_norm = l + 1 < c.nlayers ? E.L[l + 1].op_norm : E.final_norm;
+    PQ_TRY(pq_rmsnorm(E.X, E.Hb, D.post_ffn_norm, next_norm, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
+  }
+  // tied LM head on the last position's final-normed row
+  PQ_TRY(pq_q8_gemv(E.emb.pc, E.emb.ps, E.qx + (size_t)(T - 1) * H, E.dx + (size_t)(T - 1) * (H / 32), E.logits,
+                    PQ_DTYPE_F32, c.vocab, H, E.st));
+  PQ_TRY(pq_argmax(E.logits, c.vocab, next, E.st));
+  E.pos += T;
+  E.last_t = T;
+  return PQ_OK;
+}
+
+// Prompt in chunks of tmax positions; the greedy id after the last one goes to *next.
+static int prefill(Engine &E, const int32_t *prompt, int n, int32_t *next) {
+  for (int i = 0; i < n; i += E.tmax) {
+    const int T = std::min(E.tmax, n - i);
+    if (hipMemcpyAsync(E.tok, prompt + i, (size_t)T * 4, hipMemcpyHostToDevice, E.st) != hipSuccess)
+      return fail(PQ_ERR_LAUNCH, "token upload failed");
+    PQ_TRY(forward(E, T, next));
+    if (hipStreamSynchronize(E.st) != hipSuccess) return fail(PQ_ERR_LAUNCH, "prefill sync failed");
+  }
+  return PQ_OK;
+}
+
+// n decode steps from the device-resident token *E.tok: step s feeds the id
+// of step s-1 and writes its own into ids[s] and E.tok (no host round trip).
+static int decode(Engine &E, int n, int first_slot) {
+  for (int s = 0; s < n; s++) {
+    PQ_TRY(forward(E, 1, E.tok));
+    if (hipMemcpyAsync(E.ids + first_slot + s, E.tok, 4, hipMemcpyDeviceToDevice, E.st) != hipSuccess)
+      return fail(PQ_ERR_LAUNCH, "id copy failed");
+  }
+  return PQ_OK;
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" void *pq_engine_create(const pq_model_cfg *cfg) {
+  if (!cfg) { fail(PQ_ERR_ARG, "pq_engine_create: null config"); return nullptr; }
+  const pq_model_cfg &c = *cfg;
+  const bool ok = c.hidden >= 256 && (c.hidden & (c.hidden - 1)) == 0 && c.hidden <= 8192 && c.ffn % 256 == 0 &&
+                  c.ffn > 0 && c.vocab > 0 && c.nlayers > 0 && c.nlayers <= 32 && c.hd == 64 && c.nkv > 0 &&
+                  c.nh % c.nkv == 0 && c.nh * c.hd % 64 == 0 && c.rot >= 0 && c.rot <= c.hd && c.rot % 2 == 0 &&
+                  (c.ntaps == 2 || c.ntaps == 3 || c.ntaps == 4 || c.ntaps == 7) && c.ctx > 0 &&
+                  c.prefill_chunk > 0 && c.prefill_chunk <= 512;
+  if (!ok) { fail(PQ_ERR_ARG, "pq_engine_create: unsupported configuration"); return nullptr; }
+  auto E = std::make_unique<Engine>();
+  if (create(*E, c) != PQ_OK) return nullptr;
+  if (upload_rope(*E) != PQ_OK || reset(*E) != PQ_OK) return nullptr;
+  return E.release();
+}
+
+extern "C" int pq_engine_destroy(void *h) {
+  delete static_cast<Engine *>(h);
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_load_synthetic(void *h) {
+  PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
+  Engine &E = *static_cast<Engine *>(h);
+  PQ_TRY(load_synthetic(E));
+  E.loaded = true;
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_set_q8(void *h, int layer, int slot, const int8_t *codes, const uint16_t *scales) {
+  PQ_REQUIRE(h && codes && scales, PQ_ERR_ARG, "pq_engine_set_q8: null pointer");
+  Engine &E = *static_cast<Engine *>(h);
+  Q8Dev *q = q8_slot(E, layer, slot);
+  PQ_REQUIRE(q, PQ_ERR_ARG, "pq_engine_set_q8: no Q8 tensor at layer %d slot %d", layer, slot);
+  return upload_q8(E, *q, codes, scales);
+}
+
+extern "C" int pq_engine_set_f32(void *h, int layer, int slot, const float *v, size_t n) {
+  PQ_REQUIRE(h && v, PQ_ERR_ARG, "pq_engine_set_f32: null pointer");
+  Engine &E = *static_cast<Engine *>(h);
+  size_t want = 0;
+  float *dst = vec_slot(E, layer, slot, &want);
+  PQ_REQUIRE(dst && n == want, PQ_ERR_ARG, "pq_engine_set_f32: layer %d slot %d expects %zu values", layer, slot, want);
+  return upload_f32(E, dst, v, n);
+}
+
+extern "C" int pq_engine_mark_loaded(void *h) {
+  PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
+  static_cast<Engine *>(h)->loaded = true;
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_reset(void *h) {
+  PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
+  return reset(*static_cast<Engine *>(h));
+}
+
+extern "C" int pq_engine_feed(void *h, const int32_t *tokens, int n, int32_t *next_id, float *logits) {
+  PQ_REQUIRE(h && tokens && n > 0, PQ_ERR_ARG, "pq_engine_feed: bad arguments");
+  Engine &E = *static_cast<Engine *>(h);
+  PQ_REQUIRE(E.loaded, PQ_ERR_STATE, "pq_engine_feed: weights not loaded");
+  PQ_TRY(prefill(E, tokens, n, E.tok));
+  if (next_id && hipMemcpy(next_id, E.tok, 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "id copy failed");
+  if (logits && hipMemcpy(logits, E.logits, (size_t)E.c.vocab * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "logits copy failed");
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_greedy(void *h, const int32_t *prompt, int n_prompt, int n_steps, int32_t *ids) {
+  PQ_REQUIRE(h && prompt && ids && n_prompt > 0 && n_steps > 0, PQ_ERR_ARG, "pq_engine_greedy: bad arguments");
+  Engine &E = *static_cast<Engine *>(h);
+  PQ_REQUIRE(E.loaded, PQ_ERR_STATE, "pq_engine_greedy: weights not loaded");
+  PQ_REQUIRE(n_steps <= E.max_ids && n_prompt + n_steps - 1 <= E.c.ctx, PQ_ERR_STATE,
+             "pq_engine_greedy: %d + %d positions exceed the context %d", n_prompt, n_steps, E.c.ctx);
+  PQ_TRY(reset(E));
+  PQ_TRY(prefill(E, prompt, n_prompt, E.tok));
+  if (hipMemcpyAsync(E.ids, E.tok, 4, hipMemcpyDeviceToDevice, E.st) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "id copy failed");
+  PQ_TRY(decode(E, n_steps - 1, 1));
+  if (hipMemcpyAsync(ids, E.ids, (size_t)n_steps * 4, hipMemcpyDeviceToHost, E.st) != hipSuccess ||
+      hipStreamSynchronize(E.st) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "ids copy failed");
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_decode(void *h, int n_steps, int32_t *ids) {
+  PQ_REQUIRE(h && n_steps > 0, PQ_ERR_ARG, "pq_engine_decode: bad arguments");
+  Engine &E = *static_cast<Engine *>(h);
+  PQ_REQUIRE(E.loaded, PQ_ERR_STATE, "pq_engine_decode: weights not loaded");
+  PQ_REQUIRE(n_steps <= E.max_ids && E.pos + n_steps <= E.c.ctx, PQ_ERR_STATE, "pq_engine_decode: context full");
+  PQ_TRY(decode(E, n_steps, 0));
+  if (ids && (hipMemcpyAsync(ids, E.ids, (size_t)n_steps * 4, hipMemcpyDeviceToHost, E.st) != hipSuccess ||
+              hipStreamSynchronize(E.st) != hipSuccess))
+    return fail(PQ_ERR_LAUNCH, "ids copy failed");
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_sync(void *h) {
+  PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
+  return hipStreamSynchronize(static_cast<Engine *>(h)->st) == hipSuccess ? PQ_OK
+                                                                          : fail(PQ_ERR_LAUNCH, "stream sync failed");
+}
+
+extern "C" void *pq_engine_stream(void *h) { return h ? static_cast<Engine *>(h)->st : nullptr; }
+
+extern "C" int pq_engine_position(void *h) { return h ? static_cast<Engine *>(h)->pos : -1; }
+
+extern "C" int pq_engine_hidden(void *h, uint16_t *out) {
+  PQ_REQUIRE(h && out, PQ_ERR_ARG, "pq_engine_hidden: null pointer");
+  Engine &E = *static_cast<Engine *>(h);
+  // The residual stream of the last position fed.
+  return hipMemcpy(out, E.X + (size_t)(E.last_t - 1) * E.c.hidden, (size_t)E.c.hidden * 2, hipMemcpyDeviceToHost) ==
+                 hipSuccess
+             ? PQ_OK
+             : fail(PQ_ERR_LAUNCH, "hidden copy failed");
+}
+
+extern "C" size_t pq_engine_weight_bytes(void *h) {
+  if (!h) return 0;
+  Engine &E = *static_cast<Engine *>(h);
+  size_t b = 0;
+  auto q8 = [&](const Q8Dev &q) { b += (size_t)q.N * q.K + (size_t)q.N * (q.K / 32) * 2; };
+  for (const LayerDev &D : E.L) {
+    q8(D.in); q8(D.out); q8(D.ug); q8(D.down);
+  }
+  q8(E.emb);
+  return b;
+}

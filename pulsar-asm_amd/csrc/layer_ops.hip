@@ -1,0 +1,349 @@
+// layer_ops.hip -- the non-GEMV steps of one LFM3-style decoder layer on gfx950:
+// RMSNorm (optionally fused with the residual add and with the Q8_0
+// quantization of its output), per-head q/k norm + RoPE + fp16 KV write, the
+// gated short conv, silu(gate)*up, argmax and the embedding row lookup.
+//
+// Every op keeps the reference's rounding points (one bf16 round per op,
+// RMSNorm rounding before the weight multiply) and the build's fixed orders:
+// sums of squares are pairwise trees (the wave64 xor butterfly), e^x is
+// pq::expf_pq, 1/sqrt is the correctly rounded 1.0f / sqrtf.
+#include "pq_device.h"
+#include "pq_host.h"
+
+namespace pq {
+
+// ------------------------------------------------------------------ helpers
+// Pairwise sum over the workgroup: each thread passes the pairwise sum of its
+// E consecutive elements; wave butterfly; then a pairwise tree over the waves
+// (W a power of two). Every thread receives the total.
+__device__ __forceinline__ float block_pairwise(float v, float *red) {
+  v = wave_pairwise_sum(v);
+  const int W = blockDim.x >> 6, wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  for (int n = W; n > 1; n >>= 1) {
+    if ((int)threadIdx.x < n / 2) red[threadIdx.x] = red[2 * threadIdx.x] + red[2 * threadIdx.x + 1];
+    __syncthreads();
+  }
+  const float t = red[0];
+  __syncthreads();
+  return t;
+}
+
+template <int E>
+__device__ __forceinline__ float local_pairwise_sq(const float *v) {
+  float s[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) s[i] = v[i] * v[i];
+#pragma unroll
+  for (int n = E; n > 1; n >>= 1)
+#pragma unroll
+    for (int i = 0; i < n / 2; i++) s[i] = s[2 * i] + s[2 * i + 1];
+  return s[0];
+}
+
+// Q8_0 quantization of a thread's E consecutive bf16 outputs (E <= 32, 32/E
+// threads per block): amax over the block's threads (xor butterfly of max),
+// d = amax/127, q = rne(v/d) clamped -- the same rule as q8_quant_kernel.
+template <int E>
+__device__ __forceinline__ void quant_store(const float *v, int8_t *qx, float *dx, int e0) {
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < E; i++) a = fmaxf(a, fabsf(v[i]));
+#pragma unroll
+  for (int o = 1; o < 32 / E; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  const float d = a / 127.0f;
+  int8_t q[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    int t = 0;
+    if (d != 0.0f) {
+      t = (int)__builtin_rintf(v[i] / d);
+      t = t > 127 ? 127 : (t < -127 ? -127 : t);
+    }
+    q[i] = (int8_t)t;
+  }
+#pragma unroll
+  for (int i = 0; i < E; i++) qx[e0 + i] = q[i];
+  if ((e0 & 31) == 0) dx[e0 >> 5] = d;
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// One workgroup per row of H = 256*E... (blockDim * E == H). Optional
+// residual form: h3 = rmsnorm(h, w0); x = bf16(x + h3) (written back);
+// out = rmsnorm(x, w1). The output goes to y (bf16) and/or (qx, dx).
+template <int E, bool RESID>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ x, const uint16_t *__restrict__ h,
+                                                       const float *__restrict__ w0, const float *__restrict__ w1,
+                                                       uint16_t *__restrict__ y, int8_t *__restrict__ qx,
+                                                       float *__restrict__ dx, int H, float eps) {
+  __shared__ float red[8];
+  const size_t row = blockIdx.x;
+  const int e0 = threadIdx.x * E;
+  float v[E];
+  const float inv_n = 1.0f / (float)H;  // exact: H is a power of two
+  if (RESID) {
+    float hv[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) hv[i] = bf2f(h[row * H + e0 + i]);
+    const float ss = block_pairwise(local_pairwise_sq<E>(hv), red);
+    const float rs = 1.0f / sqrtf(ss * inv_n + eps);
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const float h3 = bf2f(f2bf(w0[e0 + i] * bf2f(f2bf(hv[i] * rs))));
+      const uint16_t xn = f2bf(bf2f(x[row * H + e0 + i]) + h3);
+      v[i] = bf2f(xn);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < E; i++) x[row * H + e0 + i] = f2bf(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; i++) v[i] = bf2f(x[row * H + e0 + i]);
+  }
+  const float *w = RESID ? w1 : w0;
+  const float ss = block_pairwise(local_pairwise_sq<E>(v), red);
+  const float rs = 1.0f / sqrtf(ss * inv_n + eps);
+  float o[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) o[i] = bf2f(f2bf(w[e0 + i] * bf2f(f2bf(v[i] * rs))));
+  if (y != nullptr) {
+#pragma unroll
+    for (int i = 0; i < E; i++) y[row * H + e0 + i] = f2bf(o[i]);
+  }
+  if (qx != nullptr) quant_store<E>(o, qx + row * H, dx + row * (H / 32), e0);
+}
+
+// ------------------------------------------------- q/k norm, RoPE, KV write
+// One wave per (head, position); lane d holds dimension d (hd == 64). Heads
+// [0, nh) are q (norm + rope, in place), [nh, nh+nkv) k (norm + rope, then
+// written to the fp16 cache), [nh+nkv, nh+2nkv) v (written to the cache).
+__global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv, int row_stride,
+                                                      const float *__restrict__ qn, const float *__restrict__ kn,
+                                                      const float *__restrict__ cs, uint16_t *__restrict__ kc,
+                                                      uint16_t *__restrict__ vc, int pos0, int nh, int nkv, int rot,
+                                                      float eps) {
+  constexpr int hd = 64;
+  const int head = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  const int pos = pos0 + t;
+  uint16_t *row = qkv + (size_t)t * row_stride;
+  const int kvd = nkv * hd;
+  if (head >= nh + nkv) {  // v: straight to the cache
+    const int g = head - nh - nkv;
+    vc[(size_t)pos * kvd + g * hd + d] = f2h(bf2f(row[nh * hd + kvd + g * hd + d]));
+    return;
+  }
+  const bool isq = head < nh;
+  uint16_t *xr = isq ? row + head * hd : row + nh * hd + (head - nh) * hd;
+  const float *w = isq ? qn : kn;
+  const float x = bf2f(xr[d]);
+  const float ss = wave_pairwise_sum(x * x);
+  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)hd) + eps);
+  float v = bf2f(f2bf(w[d] * bf2f(f2bf(x * rs))));
+  const int half = rot / 2;
+  const float up = __shfl_down(v, hd / 2, 64);     // partner for d < hd/2
+  const float dn = __shfl_up(v, hd / 2, 64);       // partner for d >= hd/2
+  if (d < hd / 2 && d < half) {
+    const float c = cs[((size_t)pos * half + d) * 2], s = cs[((size_t)pos * half + d) * 2 + 1];
+    v = v * c - up * s;
+  } else if (d >= hd / 2 && d - hd / 2 < half) {
+    const int i = d - hd / 2;
+    const float c = cs[((size_t)pos * half + i) * 2], s = cs[((size_t)pos * half + i) * 2 + 1];
+    v = v * c + dn * s;
+  }
+  const uint16_t vb = f2bf(v);
+  if (isq) xr[d] = vb;
+  else kc[(size_t)pos * kvd + (head - nh) * hd + d] = f2h(bf2f(vb));
+}
+
+// ------------------------------------------------------------ short conv
+// One thread per channel walks the T positions with the ring in registers:
+// bx = bf16(B*x), shift, acc = sum_k fl(tap_k * ring_k) ascending, cy = bf16,
+// out = bf16(C*cy) (k_conv_chunk, lfm3_nanode.cu:917-941). Optional Q8_0
+// output of out for the next GEMV.
+template <int NT>
+__global__ __launch_bounds__(256) void conv_kernel(uint16_t *__restrict__ ring, const float *__restrict__ taps,
+                                                    const uint16_t *__restrict__ bcx, uint16_t *__restrict__ out,
+                                                    int H, int T) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= H) return;
+  uint16_t r[NT];
+  float tp[NT];
+#pragma unroll
+  for (int k = 0; k < NT; k++) {
+    r[k] = ring[(size_t)k * H + i];
+    tp[k] = taps[(size_t)i * NT + k];
+  }
+  for (int t = 0; t < T; t++) {
+    const uint16_t *row = bcx + (size_t)t * 3 * H;
+    const uint16_t bx = f2bf(bf2f(row[i]) * bf2f(row[2 * H + i]));
+#pragma unroll
+    for (int k = 0; k < NT - 1; k++) r[k] = r[k + 1];
+    r[NT - 1] = bx;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NT; k++) acc = acc + tp[k] * bf2f(r[k]);
+    const uint16_t cy = f2bf(acc);
+    out[(size_t)t * H + i] = f2bf(bf2f(row[H + i]) * bf2f(cy));
+  }
+#pragma unroll
+  for (int k = 0; k < NT; k++) ring[(size_t)k * H + i] = r[k];
+}
+
+// ------------------------------------------------------- silu(gate) * up
+// Rows of the fused gate/up GEMV output: gate = row[0:F], up = row[F:2F].
+// One workgroup of F/E threads per position; E consecutive elements per
+// thread so the Q8_0 output can be formed in the same pass.
+template <int E>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, uint16_t *__restrict__ y,
+                                                        int8_t *__restrict__ qx, float *__restrict__ dx, int F) {
+  const size_t t = blockIdx.y;
+  const int e0 = (blockIdx.x * blockDim.x + threadIdx.x) * E;
+  const uint16_t *g = gu + t * 2 * F, *u = g + F;
+  float o[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    const float a = bf2f(g[e0 + i]);
+    const float sg = 1.0f / (1.0f + expf_pq(-a));
+    o[i] = bf2f(f2bf((a * sg) * bf2f(u[e0 + i])));
+  }
+  if (y != nullptr) {
+#pragma unroll
+    for (int i = 0; i < E; i++) y[t * F + e0 + i] = f2bf(o[i]);
+  }
+  if (qx != nullptr) quant_store<E>(o, qx + t * F, dx + t * (F / 32), e0);
+}
+
+// ------------------------------------------------------------------ argmax
+// Lowest index among the maxima: strict > scans ascending per thread, then a
+// tree that keeps the larger value and, on ties, the smaller index.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ v, int n, int32_t *__restrict__ out) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  float best = -__builtin_inff();
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float x = v[i];
+    if (x > best) { best = x; idx = i; }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { bv[wave] = best; bi[wave] = idx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
+    *out = idx == 0x7fffffff ? 0 : idx;
+  }
+}
+
+// --------------------------------------------------------------- embedding
+// Row tok of the tied Q8_0 table, read from the packed layout:
+// bf16(fl(code * scale)) (k_dequant_row, lfm3_nanode.cu:138-142). Tokens
+// outside [0, vocab) give a zero row.
+__global__ __launch_bounds__(256) void embed_kernel(const int8_t *__restrict__ pc, const uint16_t *__restrict__ ps,
+                                                     const int32_t *__restrict__ tok, uint16_t *__restrict__ out,
+                                                     int H, int vocab) {
+  const int t = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= H) return;
+  const int id = tok[t];
+  if (id < 0 || id >= vocab) {
+    out[(size_t)t * H + k] = 0;
+    return;
+  }
+  const int nb = H / 32, nch = (nb + 7) / 8;
+  const int tile = id / 64, r = id % 64, b = k / 32, h = (k % 32) / 16, j = k % 16;
+  const int8_t c = pc[(((size_t)tile * nb + b) * 2 + h) * 1024 + r * 16 + j];
+  const uint16_t s = ps[(((size_t)tile * nch + b / 8) * 64 + r) * 8 + (b % 8)];
+  out[(size_t)t * H + k] = f2bf((float)c * h2f(s));
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+static bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+extern "C" int pq_rmsnorm(uint16_t *x, const uint16_t *h, const float *w0, const float *w1, uint16_t *y, int8_t *qx,
+                          float *dx, int H, int T, float eps, void *stream) {
+  PQ_REQUIRE(x && w0 && (y || qx), PQ_ERR_ARG, "pq_rmsnorm: null pointer");
+  PQ_REQUIRE(!h || w1, PQ_ERR_ARG, "pq_rmsnorm: the residual form needs w1");
+  PQ_REQUIRE(!qx || dx, PQ_ERR_ARG, "pq_rmsnorm: qx without dx");
+  PQ_REQUIRE(pow2(H) && H >= 64 && H <= 8192 && T > 0, PQ_ERR_ARG, "pq_rmsnorm: H=%d (power of two, 64..8192)", H);
+  const int threads = H >= 256 ? 256 : H;
+  const int E = H / threads;
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(T), block(threads);
+#define PQ_RMS(EE)                                                                                                 \
+  if (h) launch(rmsnorm_kernel<EE, true>, grid, block, 0, st, x, h, w0, w1, y, qx, dx, H, eps);                    \
+  else launch(rmsnorm_kernel<EE, false>, grid, block, 0, st, x, h, w0, w1, y, qx, dx, H, eps);
+  switch (E) {
+    case 1: PQ_RMS(1) break;
+    case 2: PQ_RMS(2) break;
+    case 4: PQ_RMS(4) break;
+    case 8: PQ_RMS(8) break;
+    case 16: PQ_RMS(16) break;
+    default: PQ_RMS(32) break;
+  }
+#undef PQ_RMS
+  return check_launch("pq_rmsnorm");
+}
+
+extern "C" int pq_qk_prep(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm, const float *rope_cs,
+                          uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv, int hd, int rot, int T,
+                          float eps, void *stream) {
+  PQ_REQUIRE(qkv && q_norm && k_norm && rope_cs && kcache && vcache, PQ_ERR_ARG, "pq_qk_prep: null pointer");
+  PQ_REQUIRE(hd == 64, PQ_ERR_ARG, "pq_qk_prep: head_dim %d (this build: 64)", hd);
+  PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && rot >= 0 && rot <= hd && rot % 2 == 0 && T > 0 && pos0 >= 0,
+             PQ_ERR_ARG, "pq_qk_prep: nh=%d nkv=%d rot=%d T=%d pos0=%d", nh, nkv, rot, T, pos0);
+  PQ_REQUIRE(row_stride >= (nh + 2 * nkv) * hd, PQ_ERR_ARG, "pq_qk_prep: row stride %d too small", row_stride);
+  launch(qk_prep_kernel, dim3(nh + 2 * nkv, T), dim3(64), 0, as_stream(stream), qkv, row_stride, q_norm, k_norm,
+         rope_cs, kcache, vcache, pos0, nh, nkv, rot, eps);
+  return check_launch("pq_qk_prep");
+}
+
+extern "C" int pq_conv(uint16_t *ring, const float *taps, const uint16_t *bcx, uint16_t *out, int H, int T, int ntaps,
+                       void *stream) {
+  PQ_REQUIRE(ring && taps && bcx && out, PQ_ERR_ARG, "pq_conv: null pointer");
+  PQ_REQUIRE(H > 0 && T > 0, PQ_ERR_ARG, "pq_conv: H=%d T=%d", H, T);
+  const dim3 grid((H + 255) / 256), block(256);
+  hipStream_t st = as_stream(stream);
+  switch (ntaps) {
+    case 2: launch(conv_kernel<2>, grid, block, 0, st, ring, taps, bcx, out, H, T); break;
+    case 3: launch(conv_kernel<3>, grid, block, 0, st, ring, taps, bcx, out, H, T); break;
+    case 4: launch(conv_kernel<4>, grid, block, 0, st, ring, taps, bcx, out, H, T); break;
+    case 7: launch(conv_kernel<7>, grid, block, 0, st, ring, taps, bcx, out, H, T); break;
+    default: return fail(PQ_ERR_ARG, "pq_conv: ntaps %d (2, 3, 4 or 7)", ntaps);
+  }
+  return check_launch("pq_conv");
+}
+
+extern "C" int pq_silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T, void *stream) {
+  PQ_REQUIRE(gu && (y || qx) && (!qx || dx), PQ_ERR_ARG, "pq_silu_mul: null pointer");
+  PQ_REQUIRE(F > 0 && F % 256 == 0 && T > 0, PQ_ERR_ARG, "pq_silu_mul: F=%d (a multiple of 256)", F);
+  constexpr int E = 8;
+  const int threads = F / E < 256 ? F / E : 256;
+  launch(silu_mul_kernel<E>, dim3(F / E / threads, T), dim3(threads), 0, as_stream(stream), gu, y, qx, dx, F);
+  return check_launch("pq_silu_mul");
+}
+
+extern "C" int pq_argmax(const float *v, int n, int32_t *out, void *stream) {
+  PQ_REQUIRE(v && out && n > 0, PQ_ERR_ARG, "pq_argmax: n=%d", n);
+  launch(argmax_kernel, dim3(1), dim3(1024), 0, as_stream(stream), v, n, out);
+  return check_launch("pq_argmax");
+}
+
+extern "C" int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *tokens, uint16_t *out, int H,
+                        int vocab, int T, void *stream) {
+  PQ_REQUIRE(pcodes && pscales && tokens && out, PQ_ERR_ARG, "pq_embed: null pointer");
+  PQ_REQUIRE(H > 0 && H % 32 == 0 && vocab > 0 && T > 0, PQ_ERR_ARG, "pq_embed: H=%d vocab=%d T=%d", H, vocab, T);
+  launch(embed_kernel, dim3((H + 255) / 256, T), dim3(256), 0, as_stream(stream), pcodes, pscales, tokens, out, H,
+         vocab);
+  return check_launch("pq_embed");
+}

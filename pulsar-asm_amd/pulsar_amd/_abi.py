@@ -5,6 +5,16 @@ P = C.c_void_p
 I = C.c_int
 Z = C.c_size_t
 F = C.c_float
+U64 = C.c_uint64
+
+
+class ModelCfg(C.Structure):
+    """pq_model_cfg."""
+    _fields_ = [("hidden", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("nlayers", C.c_int),
+                ("nh", C.c_int), ("nkv", C.c_int), ("hd", C.c_int), ("rot", C.c_int),
+                ("ntaps", C.c_int), ("ctx", C.c_int), ("eps", C.c_float), ("theta", C.c_float),
+                ("seed", C.c_uint64), ("attn_mask", C.c_uint32), ("prefill_chunk", C.c_int)]
+
 
 SIGNATURES = {
     "pq_version": (C.c_char_p, []),
@@ -17,6 +27,30 @@ SIGNATURES = {
     "pq_q8_pack": (I, [P, P, I, I, P, P, P]),
     "pq_q8_gemv": (I, [P, P, P, P, P, I, I, I, P]),
     "pq_q8_gemm": (I, [P, P, P, P, P, I, I, I, I, P]),
+    "pq_rmsnorm": (I, [P, P, P, P, P, P, P, I, I, F, P]),
+    "pq_qk_prep": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, F, P]),
+    "pq_attn_workspace_bytes": (Z, [I, I, I]),
+    "pq_attn_decode": (I, [P, I, P, P, P, I, P, I, P, P, I, I, I, I, I, F, P, Z, P]),
+    "pq_conv": (I, [P, P, P, P, I, I, I, P]),
+    "pq_silu_mul": (I, [P, P, P, P, I, I, P]),
+    "pq_argmax": (I, [P, I, P, P]),
+    "pq_embed": (I, [P, P, P, P, I, I, I, P]),
+    "pq_synth_fill": (I, [I, U64, P, Z, F, F]),
+    "pq_engine_create": (P, [C.POINTER(ModelCfg)]),
+    "pq_engine_destroy": (I, [P]),
+    "pq_engine_load_synthetic": (I, [P]),
+    "pq_engine_set_q8": (I, [P, I, I, P, P]),
+    "pq_engine_set_f32": (I, [P, I, I, P, Z]),
+    "pq_engine_mark_loaded": (I, [P]),
+    "pq_engine_reset": (I, [P]),
+    "pq_engine_feed": (I, [P, P, I, P, P]),
+    "pq_engine_greedy": (I, [P, P, I, I, P]),
+    "pq_engine_decode": (I, [P, I, P]),
+    "pq_engine_sync": (I, [P]),
+    "pq_engine_stream": (P, [P]),
+    "pq_engine_position": (I, [P]),
+    "pq_engine_hidden": (I, [P, P]),
+    "pq_engine_weight_bytes": (Z, [P]),
 }
 
 

@@ -8,7 +8,8 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16"]
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
+           "attn_decode", "conv", "silu_mul", "argmax", "embed"]
 
 DT_F32 = 0
 DT_BF16 = 1
@@ -88,4 +89,70 @@ def q8_gemm(w, qx, dx, out_dtype=DT_F32, out=None):
                           device=qx.device)
     check(lib().pq_q8_gemm(w.pcodes.data_ptr(), w.pscales.data_ptr(), qx.data_ptr(), dx.data_ptr(),
                            out.data_ptr(), out_dtype, w.N, w.K, T, stream_ptr()), "pq_q8_gemm")
+    return out
+
+
+# ---------------------------------------------------------------- layer ops
+def _bits16(t):
+    """bf16 / int16 / uint16 tensor -> its raw 16-bit storage pointer."""
+    if t.element_size() != 2:
+        raise ValueError("expected a 16-bit tensor")
+    return t.data_ptr()
+
+
+def rmsnorm(x, w0, eps=1e-5, h=None, w1=None, out=True, quant=False):
+    """RMSNorm of the rows of x (bf16 [T][H]); residual form when h is given
+    (x is updated in place). Returns (y or None, qx or None, dx or None)."""
+    T, H = (1, x.numel()) if x.dim() == 1 else x.shape
+    y = torch.empty_like(x) if out else None
+    qx = torch.empty((T, H), dtype=torch.int8, device=x.device) if quant else None
+    dx = torch.empty((T, H // 32), dtype=torch.float32, device=x.device) if quant else None
+    check(lib().pq_rmsnorm(_bits16(x), _bits16(h) if h is not None else None, w0.data_ptr(),
+                           w1.data_ptr() if w1 is not None else None, _bits16(y) if y is not None else None,
+                           _ptr(qx), _ptr(dx), H, T, eps, stream_ptr()), "pq_rmsnorm")
+    return y, qx, dx
+
+
+def qk_prep(qkv, row_stride, q_norm, k_norm, rope_cs, kc, vc, pos0, nh, nkv, hd, rot, T, eps=1e-5):
+    check(lib().pq_qk_prep(_bits16(qkv), row_stride, q_norm.data_ptr(), k_norm.data_ptr(), rope_cs.data_ptr(),
+                           _bits16(kc), _bits16(vc), pos0, nh, nkv, hd, rot, T, eps, stream_ptr()), "pq_qk_prep")
+
+
+def attn_decode(q, q_stride, kc, vc, pos0, nh, nkv, hd, T, scale, gate=None, gate_stride=0, out=None,
+                out_stride=0, qx=None, dx=None, ws=None):
+    L = lib()
+    need = L.pq_attn_workspace_bytes(nh, pos0 + T, T)
+    if ws is None:
+        ws = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    check(L.pq_attn_decode(_bits16(q), q_stride, _bits16(kc), _bits16(vc),
+                           _bits16(gate) if gate is not None else None, gate_stride,
+                           _bits16(out) if out is not None else None, out_stride, _ptr(qx), _ptr(dx), pos0, nh, nkv,
+                           hd, T, scale, ws.data_ptr(), ws.numel(), stream_ptr()), "pq_attn_decode")
+
+
+def conv(ring, taps, bcx, out, H, T, ntaps):
+    check(lib().pq_conv(_bits16(ring), taps.data_ptr(), _bits16(bcx), _bits16(out), H, T, ntaps, stream_ptr()),
+          "pq_conv")
+
+
+def silu_mul(gu, F, T, out=True, quant=False):
+    y = torch.empty((T, F), dtype=gu.dtype, device=gu.device) if out else None
+    qx = torch.empty((T, F), dtype=torch.int8, device=gu.device) if quant else None
+    dx = torch.empty((T, F // 32), dtype=torch.float32, device=gu.device) if quant else None
+    check(lib().pq_silu_mul(_bits16(gu), _bits16(y) if y is not None else None, _ptr(qx), _ptr(dx), F, T,
+                            stream_ptr()), "pq_silu_mul")
+    return y, qx, dx
+
+
+def argmax(v):
+    out = torch.empty(1, dtype=torch.int32, device=v.device)
+    check(lib().pq_argmax(v.data_ptr(), v.numel(), out.data_ptr(), stream_ptr()), "pq_argmax")
+    return out
+
+
+def embed(w, tokens, H, vocab):
+    T = tokens.numel()
+    out = torch.empty((T, H), dtype=torch.int16, device=tokens.device)
+    check(lib().pq_embed(w.pcodes.data_ptr(), w.pscales.data_ptr(), tokens.data_ptr(), out.data_ptr(), H, vocab, T,
+                         stream_ptr()), "pq_embed")
     return out

@@ -41,3 +41,11 @@ def test_loads_and_rejects_bad_args():
     assert L.pq_q8_quant_f32(8, 8, 8, 33, 1, None) == -1          # K not a multiple of 32
     assert b"multiple of 32" in L.pq_last_error()
     assert L.pq_time_next_launch(None, 8) == -1
+
+
+def test_python_wrappers_exported():
+    import pulsar_amd as pq
+    for name in ("q8_quant", "q8_gemv", "q8_gemm", "rmsnorm", "qk_prep", "attn_decode", "conv", "silu_mul",
+                 "argmax", "embed", "Q8Weight"):
+        assert callable(getattr(pq, name)), name
+    from pulsar_amd.engine import Engine, synth_fill  # noqa: F401

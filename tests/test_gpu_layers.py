@@ -1,0 +1,162 @@
+"""GPU parity of the layer kernels (norms, q/k prep, attention, conv, silu, argmax,
+embedding) against the oracle: bf16 / fp16 / int8 outputs compared bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SEED = 777
+
+
+def _t16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+
+
+def _u16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("H,T", [(2048, 1), (2048, 5), (256, 3), (8192, 2)])
+def test_rmsnorm_plain_and_quant(orc, pq, dev, H, T):
+    x = orc.f2bf(orc.gen_normal(SEED + H, T * H).reshape(T, H) * 7)
+    w = orc.gen_affine(SEED + 1, H, 1.0, 0.1)
+    want = orc.rmsnorm(x, w)
+    qx_r, dx_r = orc.q8_quant_bf16(want)
+    y, qx, dx = pq.rmsnorm(_t16(x, dev), torch.from_numpy(w).to(dev), quant=True)
+    assert np.array_equal(_u16(y), want)
+    assert np.array_equal(qx.cpu().numpy(), qx_r)
+    assert np.array_equal(dx.cpu().numpy().view(np.uint32), dx_r.view(np.uint32))
+
+
+def test_rmsnorm_residual(orc, pq, dev):
+    H, T = 2048, 3
+    x = orc.f2bf(orc.gen_normal(SEED + 2, T * H).reshape(T, H) * 5)
+    h = orc.f2bf(orc.gen_normal(SEED + 3, T * H).reshape(T, H) * 40)
+    w0 = orc.gen_affine(SEED + 4, H, 4.0, 0.4)
+    w1 = orc.gen_affine(SEED + 5, H, 1.0, 0.1)
+    h3 = orc.rmsnorm(h, w0)
+    xn = orc.add(x, h3)
+    want = orc.rmsnorm(xn, w1)
+    xd = _t16(x, dev)
+    y, qx, dx = pq.rmsnorm(xd, torch.from_numpy(w0).to(dev), h=_t16(h, dev), w1=torch.from_numpy(w1).to(dev),
+                           quant=True)
+    assert np.array_equal(_u16(xd), xn)
+    assert np.array_equal(_u16(y), want)
+    assert np.array_equal(qx.cpu().numpy(), orc.q8_quant_bf16(want)[0])
+
+
+def _qkv_case(orc, nh, nkv, hd, T, ctx, seed):
+    nin = nh * hd + 2 * nkv * hd + nh
+    rows = orc.f2bf(orc.gen_normal(seed, T * nin).reshape(T, nin) * 30)
+    qn = orc.gen_affine(seed + 1, hd, 1.0, 0.1)
+    kn = orc.gen_affine(seed + 2, hd, 1.0, 0.1)
+    cs = orc.rope_table(ctx, hd, 32, 1e6)
+    return nin, rows, qn, kn, cs
+
+
+@pytest.mark.parametrize("pos0,T", [(0, 1), (77, 1), (100, 9), (2000, 3)])
+def test_qk_prep(orc, pq, dev, pos0, T):
+    nh, nkv, hd, ctx = 32, 8, 64, 2048
+    nin, rows, qn, kn, cs = _qkv_case(orc, nh, nkv, hd, T, ctx, SEED + pos0)
+    kvd = nkv * hd
+    want_rows = rows.copy()
+    kc_r = np.zeros((ctx, kvd), np.uint16)
+    vc_r = np.zeros((ctx, kvd), np.uint16)
+    for t in range(T):
+        r = want_rows[t]
+        q = orc.headnorm(r[:nh * hd], qn, nh, hd)
+        k = orc.headnorm(r[nh * hd:nh * hd + kvd], kn, nkv, hd)
+        q = orc.rope(q, cs, pos0 + t, nh, hd, 32)
+        k = orc.rope(k, cs, pos0 + t, nkv, hd, 32)
+        r[:nh * hd] = q
+        kc_r[pos0 + t] = orc.bf2f(k).astype(np.float16).view(np.uint16)
+        vc_r[pos0 + t] = orc.bf2f(r[nh * hd + kvd:nh * hd + 2 * kvd]).astype(np.float16).view(np.uint16)
+    qkv = _t16(rows, dev)
+    kc = torch.zeros((ctx, kvd), dtype=torch.int16, device=dev)
+    vc = torch.zeros((ctx, kvd), dtype=torch.int16, device=dev)
+    pq.qk_prep(qkv, nin, torch.from_numpy(qn).to(dev), torch.from_numpy(kn).to(dev), torch.from_numpy(cs).to(dev),
+               kc, vc, pos0, nh, nkv, hd, 32, T)
+    got = _u16(qkv)
+    assert np.array_equal(got[:, :nh * hd], want_rows[:, :nh * hd])
+    assert np.array_equal(_u16(kc), kc_r) and np.array_equal(_u16(vc), vc_r)
+
+
+@pytest.mark.parametrize("npos_last,T,nh,nkv", [(1, 1, 32, 8), (64, 1, 32, 8), (65, 1, 32, 8), (300, 1, 32, 8),
+                                                (2048, 1, 32, 8), (40, 33, 32, 8), (130, 7, 8, 8), (70, 2, 16, 2)])
+def test_attention(orc, pq, dev, npos_last, T, nh, nkv):
+    hd = 64
+    pos0 = npos_last - T
+    kvd = nkv * hd
+    q = orc.f2bf(orc.gen_normal(SEED + 9 * npos_last, T * nh * hd).reshape(T, nh * hd) * 2)
+    gate = orc.f2bf(orc.gen_normal(SEED + 9 * npos_last + 1, T * nh).reshape(T, nh) * 3)
+    kc = (orc.gen_normal(SEED + 9 * npos_last + 2, npos_last * kvd) * 2).astype(np.float16).view(np.uint16)
+    vc = (orc.gen_normal(SEED + 9 * npos_last + 3, npos_last * kvd) * 5).astype(np.float16).view(np.uint16)
+    scale = 0.125
+    want = np.stack([orc.sigmoid_gate(gate[t], orc.attn(q[t], kc, vc, pos0 + t + 1, nh, nkv, hd, scale), nh, hd)
+                     for t in range(T)])
+    out = torch.zeros((T, nh * hd), dtype=torch.int16, device=dev)
+    qx = torch.empty((T, nh * hd), dtype=torch.int8, device=dev)
+    dx = torch.empty((T, nh * hd // 32), dtype=torch.float32, device=dev)
+    pq.attn_decode(_t16(q, dev), nh * hd, _t16(kc, dev), _t16(vc, dev), pos0, nh, nkv, hd, T, scale,
+                   gate=_t16(gate, dev), gate_stride=nh, out=out, out_stride=nh * hd, qx=qx, dx=dx)
+    got = _u16(out)
+    bad = np.argwhere(got != want)
+    assert bad.shape[0] == 0, f"{bad.shape[0]} differ, first {bad[:4].tolist()}"
+    assert np.array_equal(qx.cpu().numpy(), orc.q8_quant_bf16(want)[0])
+
+
+@pytest.mark.parametrize("ntaps,T", [(3, 1), (3, 32), (7, 5)])
+def test_conv(orc, pq, dev, ntaps, T):
+    H = 2048
+    taps = orc.gen_affine(SEED + 20, H * ntaps, 0.0, 0.5)
+    ring0 = orc.f2bf(orc.gen_normal(SEED + 21, ntaps * H) * 3)
+    bcx = orc.f2bf(orc.gen_normal(SEED + 22, T * 3 * H).reshape(T, 3 * H) * 10)
+    ring = ring0.copy()
+    want = []
+    for t in range(T):
+        o, ring = orc.conv_step(ring, taps, bcx[t], H, ntaps)
+        want.append(o)
+    rd = _t16(ring0, dev)
+    out = torch.empty((T, H), dtype=torch.int16, device=dev)
+    pq.conv(rd, torch.from_numpy(taps).to(dev), _t16(bcx, dev), out, H, T, ntaps)
+    assert np.array_equal(_u16(out), np.stack(want))
+    assert np.array_equal(_u16(rd), ring)
+
+
+@pytest.mark.parametrize("F,T", [(8192, 1), (8192, 4), (512, 2)])
+def test_silu_mul(orc, pq, dev, F, T):
+    gu = orc.f2bf(orc.gen_normal(SEED + F + T, T * 2 * F).reshape(T, 2 * F) * 20)
+    want = np.stack([orc.silu_mul(gu[t, :F], gu[t, F:]) for t in range(T)])
+    y, qx, dx = pq.silu_mul(_t16(gu, dev), F, T, quant=True)
+    assert np.array_equal(_u16(y), want)
+    assert np.array_equal(qx.cpu().numpy(), orc.q8_quant_bf16(want)[0])
+
+
+def test_argmax_and_ties(orc, pq, dev):
+    v = orc.gen_normal(SEED + 30, 65536)
+    assert int(pq.argmax(torch.from_numpy(v).to(dev)).item()) == orc.argmax(v)
+    v2 = np.zeros(65536, np.float32)
+    v2[[7, 300, 65535]] = 5.0
+    assert int(pq.argmax(torch.from_numpy(v2).to(dev)).item()) == 7
+
+
+def test_embed(orc, pq, dev):
+    vocab, H = 1000, 2048
+    W, S = orc.q8_weights(SEED + 40, vocab, H)
+    w = pq.Q8Weight(torch.from_numpy(W).to(dev), torch.from_numpy(S.view(np.int16)).to(dev))
+    toks = np.array([0, 999, 64, 513, -1, 1000], np.int32)
+    got = pq.embed(w, torch.from_numpy(toks).to(dev), H, vocab).cpu().numpy().view(np.uint16)
+    for i, t in enumerate(toks[:4]):
+        assert np.array_equal(got[i], orc.embed_row(W, S, int(t)))
+    assert not got[4:].any()
+
+
+def test_expf_on_device_matches_host(orc, pq, dev):
+    """silu over a sweep of inputs exercises the device e^x against the host one."""
+    x = np.concatenate([np.linspace(-100, 100, 8192 - 6), [0.0, -0.0, 88.0, -88.0, 1e-30, -1e-30]]).astype(np.float32)
+    a = orc.f2bf(x)
+    b = orc.f2bf(np.ones_like(x))
+    gu = np.concatenate([a, b])[None, :]
+    y, _, _ = pq.silu_mul(_t16(gu, dev), 8192, 1)
+    assert np.array_equal(_u16(y)[0], orc.silu_mul(a, b))

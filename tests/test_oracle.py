@@ -359,3 +359,27 @@ def test_model_head_composition(orc):
     ids = m.greedy(prompt, 16)
     assert len(set(ids.tolist())) >= 6
     m.close()
+
+
+# --------------------------------------------------------- golden fixtures
+def test_oracle_reproduces_kernel_fixtures(orc):
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "kernels.npz"))
+    for tag in ("g1", "g2", "g3"):
+        qx, dx = orc.q8_quant(d[f"{tag}_x"])
+        assert np.array_equal(qx, d[f"{tag}_qx"]) and np.array_equal(f32bits(dx), f32bits(d[f"{tag}_dx"]))
+        y = orc.q8_gemm(d[f"{tag}_W"], d[f"{tag}_S"], qx, dx)
+        assert np.array_equal(f32bits(y), f32bits(d[f"{tag}_y"]))
+    N, K = d["t_y"].size, d["t_x"].size
+    assert np.array_equal(orc.q8k_quant(d["t_x"]), d["t_xq"])
+    assert np.array_equal(f32bits(orc.tq2_gemv(d["t_codes"], d["t_S"], d["t_xq"], N, K)), f32bits(d["t_y"]))
+    assert np.array_equal(orc.attn(d["a_q"], d["a_k"], d["a_v"], 130, 8, 2, 64, 0.125), d["a_out"])
+
+
+def test_oracle_reproduces_tiny_greedy(orc):
+    import json
+    import os
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "tiny_greedy.json")))
+    m = orc.Model(**g["cfg"])
+    assert m.greedy(np.array(g["prompt"], np.int32), len(g["ids"])).tolist() == g["ids"]
+    m.close()
