@@ -35,6 +35,17 @@ SHAPES = [  # name, N, K, output dtype
 ]
 
 
+def measured_traffic():
+    """HBM bytes per step of the 5 GEMV launches, from the two rocprofv3 --pmc
+    passes summarised in profiles/q8_gemv_hbm_traffic.md (None if absent)."""
+    import re
+    path = os.path.join(ROOT, "profiles", "q8_gemv_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"\| step \(5 GEMVs\) \| [0-9.]+ \| ([0-9.]+) \|", open(path).read())
+    return int(float(m.group(1)) * 1e6) if m else None
+
+
 def gemv_bytes(N, K, out):
     return N * K + N * (K // 32) * 2 + K + (K // 32) * 4 + N * (4 if out == "f32" else 2)
 
@@ -80,12 +91,135 @@ def cpu_baseline(seconds=10.0):
                       f"(q8_gemv_cpu.c:29-58, OpenMP over rows; fp32 x and fp32 scales, {nbytes / 1e6:.1f} MB/pass)"}
 
 
+def decode_bench(pq, n_steps=64, n_prompt=256):
+    """Backbone decode tok/s: the synthetic 24-layer LFM3-style model, a 256-token
+    prompt (chunked prefill), then n_steps T=1 greedy steps timed on the engine's stream."""
+    import numpy as np
+    from pulsar_amd.engine import LFM3_SYNTH, Engine, synth_fill
+    from pulsar_amd.hiptime import Event
+    e = Engine(**LFM3_SYNTH)
+    e.load_synthetic()
+    prompt = synth_fill(5, LFM3_SYNTH["seed"] + 4 * 5000, n_prompt, float(LFM3_SYNTH["vocab"]))
+    st = e.stream()
+    a, b, c = Event(), Event(), Event()
+    e.reset()
+    a.record(st)
+    e.feed(prompt)
+    b.record(st)
+    e.decode(4, want_ids=False)          # warm-up steps
+    e.sync()
+    e.reset()
+    e.feed(prompt)
+    b2 = Event()
+    b2.record(st)
+    e.decode(n_steps, want_ids=False)
+    c.record(st)
+    e.sync()
+    prefill_ms = a.elapsed_ms(b)
+    ms = b2.elapsed_ms(c) / n_steps
+    wbytes = e.weight_bytes()
+    kv = 8 * 2 * 8 * 64 * 2  # attention layers x (k, v) x kv heads x dim x fp16, per position
+    mean_pos = n_prompt + n_steps / 2
+    tok_bytes = wbytes + kv * mean_pos
+    e.close()
+    return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4), "steps": n_steps,
+            "positions": f"{n_prompt}..{n_prompt + n_steps}", "bytes_per_token": int(tok_bytes),
+            "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "prefill_ms_256": round(prefill_ms, 2)}
+
+
+def prefill_gemm_bench(pq, torch, dev, g, T=512, chunk=32, reps=5):
+    """The layer's four GEMMs over T=512 positions in 32-position chunks (int8 MFMA)."""
+    from pulsar_amd.hiptime import Event
+    shapes = [("qkv", 3072, 2048), ("o_proj", 2048, 2048), ("gate_up", 16384, 2048), ("down", 2048, 8192)]
+    ws = {}
+    for (name, N, K) in shapes:
+        codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        scales = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().view(torch.int16)
+        ws[name] = pq.Q8Weight(codes, scales)
+    xs = {K: pq.q8_quant(torch.randn((T, K), device=dev, generator=g)) for K in (2048, 8192)}
+    outs = {name: torch.empty((chunk, N), dtype=torch.bfloat16, device=dev) for (name, N, K) in shapes}
+    stream = pq.stream_ptr()
+
+    def run():
+        for c0 in range(0, T, chunk):
+            for (name, N, K) in shapes:
+                qx, dx = xs[K]
+                pq.q8_gemm(ws[name], qx[c0:c0 + chunk], dx[c0:c0 + chunk], out_dtype=pq.DT_BF16, out=outs[name])
+
+    run()
+    torch.cuda.synchronize()
+    a, b = Event(), Event()
+    a.record(stream)
+    for _ in range(reps):
+        run()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_ms(b) / reps
+    ops = sum(2 * N * K * T for (_, N, K) in shapes)
+    return {"T": T, "chunk": chunk, "ms": round(ms, 4), "TOPS": round(ops / (ms * 1e-3) / 1e12, 2),
+            "int8_peak_frac": round(ops / (ms * 1e-3) / 1e12 / 5000.0, 4), "ops": ops}
+
+
+def ternary_codes(torch, N, K, dev, g):
+    """Weights uniform in {-1, 0, +1}: codes {0, 1, 2} packed four per byte."""
+    c = torch.randint(0, 3, (N, K // 4, 4), dtype=torch.uint8, device=dev, generator=g)
+    return (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).contiguous()
+
+
+def ternary_bench(pq, torch, dev, g, reps=50, rotate_mb=400):
+    """PQ2_0 x Q8_K GEMVs of a Qwen3-8B-shaped FFN at T=1: gate and up 12288x4096,
+    down 4096x12288, weights rotated over > 256 MB."""
+    from pulsar_amd.hiptime import Event
+    shapes = [("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+    per_set = sum(N * K // 4 + N * K // 128 * 2 for (_, N, K) in shapes)
+    ncopy = max(2, -(-rotate_mb * 1000000 // per_set))
+    sets = []
+    for _ in range(ncopy):
+        sets.append({name: (ternary_codes(torch, N, K, dev, g),
+                            (torch.randn((N, K // 128), device=dev, generator=g).abs() * 0.01).half()
+                            .view(torch.int16))
+                     for (name, N, K) in shapes})
+    x4 = pq.q8k_quant(torch.randn(4096, device=dev, generator=g))
+    x12 = pq.q8k_quant(torch.randn(12288, device=dev, generator=g))
+    outs = {name: torch.empty(N, dtype=torch.float32, device=dev) for (name, N, K) in shapes}
+    stream = pq.stream_ptr()
+
+    def run(i, ev=None):
+        ws = sets[i % ncopy]
+        for j, (name, N, K) in enumerate(shapes):
+            if ev is not None:
+                pq.lib().pq_time_next_launch(ev[j][0].h, ev[j][1].h)
+            pq.tq2_gemv(ws[name][0], ws[name][1], x12 if K == 12288 else x4, N, K, out=outs[name])
+
+    for i in range(5):
+        run(i)
+    torch.cuda.synchronize()
+    per = [0.0, 0.0, 0.0]
+    ev = [(Event(), Event()) for _ in shapes]
+    for i in range(reps):
+        run(i, ev)
+        torch.cuda.synchronize()
+        for j in range(3):
+            per[j] += ev[j][0].elapsed_ms(ev[j][1]) / reps
+    step_bytes = sum(N * K // 4 + N * K // 128 * 2 + K // 256 * 292 + N * 4 for (_, N, K) in shapes)
+    us = sum(per) * 1e3
+    return {"shapes": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "us_per_step": round(us, 2),
+            "bytes_per_step": step_bytes, "GB/s": round(step_bytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "per_shape_us": [round(p * 1e3, 2) for p in per], "weight_copies_rotated": ncopy}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the decode and prefill measurements")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run a plain elementwise kernel over 256 MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--rotate-mb", type=int, default=600)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -178,10 +312,23 @@ def main():
                    "bytes_per_step": step_bytes, "weight_copies_rotated": ncopy,
                    "rotated_MB": round(ncopy * set_bytes / 1e6, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "q8_gemv_kernel", "per_shape": per_shape},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
     }
+    if args.calib:
+        src = torch.randn(64 << 20, device=dev)          # 256 MiB read + 256 MiB written per call
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+    if not args.no_extra:
+        del copies
+        torch.cuda.empty_cache()
+        line["decode"] = decode_bench(pq)
+        line["prefill_gemm"] = prefill_gemm_bench(pq, torch, dev, g)
+        line["ternary_gemv"] = ternary_bench(pq, torch, dev, g)
     print(json.dumps(line))
 
 

@@ -143,6 +143,20 @@ int pq_argmax(const float *v, int n, int32_t *out, void *stream);
 int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *tokens, uint16_t *out,
              int H, int vocab, int T, void *stream);
 
+/* ======================================================= ternary GEMV
+ * PQ2_0 x Q8_K, the Bonsai ternary path. codes u8 [N][K/4] (weight i of a
+ * byte = bits 2i..2i+1, value = code - 1), fp16 scale per 128 weights
+ * [N][K/128] -- the split layout of pq2_split_repack (pq2_host.c:40-57);
+ * xq = Q8_K activations (292 B per 256: fp32 d, 256 int8, 16 int16 bsums).
+ * y[N] fp32, per row groups ascending: acc = fl(acc + fl(fl(ws*db) * isum))
+ * with isum the exact int32 group dot (pq2_host.c:82-104). K a multiple of
+ * 256, at most 32768. Replaces pq2_gemv_sm53_launch (pq2_wrap.h:24-28). */
+int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int N,
+                int K, void *stream);
+/* x [T][K] fp32 -> Q8_K blocks (quantize_row_q8_K_ref as restated in
+ * fwd8.c:61-137); K a multiple of 256. */
+int pq_q8k_quant(const float *x, uint8_t *out, int K, int T, void *stream);
+
 /* ==================================================== synthetic generator
  * Host-side fill of a synthetic tensor (there is no checkpoint offline):
  * splitmix64 output n = mix(seed + (n+1)*0x9e3779b97f4a7c15), used as

@@ -1,0 +1,162 @@
+// tq2.hip -- ternary PQ2_0 x Q8_K GEMV and the Q8_K activation quantizer (gfx950).
+//
+// Weights: the reference's split layout (pq2_wrap.h:9-17, pq2_split_repack):
+// codes u8 [N][K/4], weight i of a byte in bits 2i..2i+1, value = code - 1;
+// fp16 scale per 128-weight group [N][K/128]. Activations: Q8_K blocks of 256
+// (fp32 d, 256 int8 qs, 16 int16 bsums; 292 B). Per row, groups ascending
+// (pq2_host.c:82-104):
+//   isum_g = sum (code-1) * qs            int32, exact
+//   acc    = fl(acc + fl(fl(ws_g * db_g) * (float)isum_g))     from 0
+// where db_g is the d of Q8_K block g/2 and qs its half g%2.
+//
+// The int32 group dots run lane-parallel; the fp32 chain is sequential per row
+// over all groups, so each workgroup owns 16 whole rows: 16 lanes per row
+// compute the group partials p_g into LDS, then one lane per row folds them in
+// group order.
+//
+// Group dot without unpacking the codes to bytes: for a code dword w (16
+// weights), d_k = (w >> 2k) & 0x03030303 holds the codes of weights
+// {k, k+4, k+8, k+12}; the activations are staged in LDS permuted the same
+// way (dword k of each 16 = x[k], x[k+4], x[k+8], x[k+12]), so
+// sum code*x = sum_k dot4(d_k, xperm_k), and isum = that - sum x over the group.
+#include "pq_device.h"
+#include "pq_host.h"
+
+namespace pq {
+
+constexpr int kTqGroup = 128;
+constexpr int kQ8K = 256;
+constexpr int kQ8KBytes = 292;
+constexpr int kTqRows = 16;     // rows per workgroup
+constexpr int kTqSlots = 16;    // lanes per row (group slots)
+
+__global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict__ codes,
+                                                        const uint16_t *__restrict__ scales,
+                                                        const uint8_t *__restrict__ xq, float *__restrict__ y, int N,
+                                                        int K) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int ng = K / kTqGroup;
+  int *xperm = reinterpret_cast<int *>(smem);                  // K bytes, permuted
+  int *gsum = reinterpret_cast<int *>(smem + K);               // [ng] sum of qs over the group
+  float *db = reinterpret_cast<float *>(gsum + ng);            // [ng] Q8_K d of the group's block
+  float *pg = db + ng;                                         // [16 rows][ng] group partials
+  const int tid = threadIdx.x;
+  // stage x: dword position m of the K/16 sixteen-element runs, permutation k
+  for (int i = tid; i < K / 4; i += blockDim.x) {
+    const int m = i >> 2, k = i & 3;                 // run m, permuted dword k
+    const int blk = (m * 16) / kQ8K, off = (m * 16) % kQ8K;
+    const int8_t *qs = reinterpret_cast<const int8_t *>(xq + (size_t)blk * kQ8KBytes + 4) + off;
+    const uint32_t b0 = (uint8_t)qs[k], b1 = (uint8_t)qs[k + 4], b2 = (uint8_t)qs[k + 8], b3 = (uint8_t)qs[k + 12];
+    xperm[i] = (int)(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24));
+  }
+  for (int g = tid; g < ng; g += blockDim.x) {
+    const uint8_t *b = xq + (size_t)(g >> 1) * kQ8KBytes;
+    const int8_t *qs = reinterpret_cast<const int8_t *>(b + 4) + (g & 1) * kTqGroup;
+    int s = 0;
+    for (int i = 0; i < kTqGroup; i++) s += qs[i];
+    gsum[g] = s;
+    db[g] = *reinterpret_cast<const float *>(b);
+  }
+  __syncthreads();
+  const int r = tid / kTqSlots, gs = tid % kTqSlots;
+  const int row = blockIdx.x * kTqRows + r;
+  if (row < N) {
+    const uint8_t *cr = codes + (size_t)row * (K / 4);
+    const uint16_t *sr = scales + (size_t)row * ng;
+    for (int g = gs; g < ng; g += kTqSlots) {
+      const uint4 c0 = *reinterpret_cast<const uint4 *>(cr + g * 32);
+      const uint4 c1 = *reinterpret_cast<const uint4 *>(cr + g * 32 + 16);
+      const uint32_t w[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const int *xp = xperm + g * (kTqGroup / 4);
+      int s = 0;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * j);
+        s = __builtin_amdgcn_sdot4((int)(w[j] & 0x03030303u), xv.x, s, false);
+        s = __builtin_amdgcn_sdot4((int)((w[j] >> 2) & 0x03030303u), xv.y, s, false);
+        s = __builtin_amdgcn_sdot4((int)((w[j] >> 4) & 0x03030303u), xv.z, s, false);
+        s = __builtin_amdgcn_sdot4((int)((w[j] >> 6) & 0x03030303u), xv.w, s, false);
+      }
+      const int isum = s - gsum[g];
+      const float t = h2f(sr[g]) * db[g];
+      pg[r * ng + g] = t * (float)isum;
+    }
+  }
+  __syncthreads();
+  if (gs == 0 && row < N) {
+    float acc = 0.0f;
+    for (int g = 0; g < ng; g++) acc = acc + pg[r * ng + g];
+    y[row] = acc;
+  }
+}
+
+// Q8_K quantizer (fwd8.c:61-137, the fork's quantize_row_q8_K_ref): one wave
+// per 256-block, 4 consecutive elements per lane. max = the x at the FIRST
+// index reaching amax; iscale = -127/max; q = min(127, nearest_int(iscale*x))
+// with nearest_int the 1.5*2^23 magic add; bsums of 16; d = 1/iscale. An
+// all-zero block writes d = 0, qs = 0 and zero bsums.
+__global__ __launch_bounds__(64) void q8k_quant_kernel(const float *__restrict__ x, uint8_t *__restrict__ out) {
+  const int blk = blockIdx.x, lane = threadIdx.x;
+  const float *xb = x + (size_t)blk * kQ8K;
+  uint8_t *ob = out + (size_t)blk * kQ8KBytes;
+  const float4 v4 = *reinterpret_cast<const float4 *>(xb + 4 * lane);
+  const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  a = wave_max(a);
+  int idx = 0x7fffffff;
+#pragma unroll
+  for (int i = 3; i >= 0; i--)
+    if (fabsf(v[i]) == a) idx = 4 * lane + i;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) idx = min(idx, __shfl_xor(idx, o, 64));
+  int8_t *qs = reinterpret_cast<int8_t *>(ob + 4);
+  int16_t *bs = reinterpret_cast<int16_t *>(ob + 4 + kQ8K);
+  if (a == 0.0f) {
+    *reinterpret_cast<uint32_t *>(qs + 4 * lane) = 0u;
+    if (lane < 16) bs[lane] = 0;
+    if (lane == 0) *reinterpret_cast<float *>(ob) = 0.0f;
+    return;
+  }
+  const float mx = xb[idx];
+  const float iscale = -127.f / mx;
+  int q[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float val = iscale * v[i] + 12582912.f;
+    const int n = (__float_as_int(val) & 0x007fffff) - 0x00400000;
+    q[i] = n < 127 ? n : 127;
+  }
+  *reinterpret_cast<uint32_t *>(qs + 4 * lane) =
+      (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) | ((uint32_t)(uint8_t)q[2] << 16) |
+      ((uint32_t)(uint8_t)q[3] << 24);
+  int s = q[0] + q[1] + q[2] + q[3];
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  if ((lane & 3) == 0) bs[lane >> 2] = (int16_t)s;
+  if (lane == 0) *reinterpret_cast<float *>(ob) = 1.0f / iscale;
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" int pq_q8k_quant(const float *x, uint8_t *out, int K, int T, void *stream) {
+  PQ_REQUIRE(x && out, PQ_ERR_ARG, "pq_q8k_quant: null pointer");
+  PQ_REQUIRE(K > 0 && K % kQ8K == 0 && T > 0, PQ_ERR_ARG, "pq_q8k_quant: K=%d (a multiple of 256)", K);
+  PQ_REQUIRE(aligned(x, 16) && aligned(out, 4), PQ_ERR_ALIGN, "pq_q8k_quant: x must be 16-byte aligned");
+  launch(q8k_quant_kernel, dim3((unsigned)((size_t)T * (K / kQ8K))), dim3(64), 0, as_stream(stream), x, out);
+  return check_launch("pq_q8k_quant");
+}
+
+extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int N, int K,
+                           void *stream) {
+  PQ_REQUIRE(codes && scales && xq && y, PQ_ERR_ARG, "pq_tq2_gemv: null pointer");
+  PQ_REQUIRE(N > 0 && K > 0 && K % kQ8K == 0 && K <= 32768, PQ_ERR_ARG,
+             "pq_tq2_gemv: N=%d K=%d (K a multiple of 256, at most 32768)", N, K);
+  PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
+  const int ng = K / kTqGroup;
+  const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)kTqRows * ng * 4;
+  launch(tq2_gemv_kernel, dim3((unsigned)((N + kTqRows - 1) / kTqRows)), dim3(kTqRows * kTqSlots), lds,
+         as_stream(stream), codes, scales, xq, y, N, K);
+  return check_launch("pq_tq2_gemv");
+}

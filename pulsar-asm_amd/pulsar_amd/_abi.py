@@ -35,6 +35,8 @@ SIGNATURES = {
     "pq_silu_mul": (I, [P, P, P, P, I, I, P]),
     "pq_argmax": (I, [P, I, P, P]),
     "pq_embed": (I, [P, P, P, P, I, I, I, P]),
+    "pq_tq2_gemv": (I, [P, P, P, P, I, I, P]),
+    "pq_q8k_quant": (I, [P, P, I, I, P]),
     "pq_synth_fill": (I, [I, U64, P, Z, F, F]),
     "pq_engine_create": (P, [C.POINTER(ModelCfg)]),
     "pq_engine_destroy": (I, [P]),

@@ -9,7 +9,7 @@ import torch
 from . import check, lib
 
 __all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
-           "attn_decode", "conv", "silu_mul", "argmax", "embed"]
+           "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv"]
 
 DT_F32 = 0
 DT_BF16 = 1
@@ -155,4 +155,23 @@ def embed(w, tokens, H, vocab):
     out = torch.empty((T, H), dtype=torch.int16, device=tokens.device)
     check(lib().pq_embed(w.pcodes.data_ptr(), w.pscales.data_ptr(), tokens.data_ptr(), out.data_ptr(), H, vocab, T,
                          stream_ptr()), "pq_embed")
+    return out
+
+
+# ------------------------------------------------------------- ternary path
+def q8k_quant(x):
+    """x fp32 [T][K] -> Q8_K blocks, uint8 [T][K/256*292]."""
+    x2 = x.reshape(1, -1) if x.dim() == 1 else x
+    T, K = x2.shape
+    out = torch.empty((T, K // 256 * 292), dtype=torch.uint8, device=x.device)
+    check(lib().pq_q8k_quant(x2.contiguous().data_ptr(), out.data_ptr(), K, T, stream_ptr()), "pq_q8k_quant")
+    return out[0] if x.dim() == 1 else out
+
+
+def tq2_gemv(codes, scales, xq, N, K, out=None):
+    """PQ2_0 codes uint8 [N][K/4], fp16 scale bits [N][K/128], Q8_K xq -> y fp32 [N]."""
+    if out is None:
+        out = torch.empty(N, dtype=torch.float32, device=codes.device)
+    check(lib().pq_tq2_gemv(codes.data_ptr(), scales.data_ptr(), xq.data_ptr(), out.data_ptr(), N, K, stream_ptr()),
+          "pq_tq2_gemv")
     return out
