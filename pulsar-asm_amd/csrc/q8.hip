@@ -258,79 +258,97 @@ __global__ __launch_bounds__(512) void q8_gemv_kernel(const int8_t *__restrict__
 }
 
 // ------------------------------------------------------------ prefill GEMM
-// Workgroup = 4 waves = one 64-row tile x 64 positions; wave w owns row
-// half (w & 1) and position tile (w >> 1), a 32x32 accumulator. Per block one
-// v_mfma_i32_32x32x32_i8: A = activations (i = position), B = weights (j =
-// row); lane l then holds D[i][j] for j = l % 32 and i = 8(r/4) + 4(l/32) + r%4
-// (r = 0..15), and applies the R1 epilogue to its 16 outputs. dx of the
-// workgroup's 64 positions is staged per chunk in LDS as [block][position].
-
-__global__ __launch_bounds__(256) void q8_gemm_kernel(const int8_t *__restrict__ pc, const uint16_t *__restrict__ ps,
-                                                       const int8_t *__restrict__ qx, const float *__restrict__ dx,
-                                                       void *__restrict__ y, int y_bf16, int N, int K, int T) {
-  __shared__ __align__(16) float dxs[kCB][64];
+// Workgroup = one 32-row half of a 64-row tile x 32 positions x all of K, W
+// waves. In round rd wave w takes R1 chunk c = rd*W + w: per block one
+// v_mfma_i32_32x32x32_i8 with A = activations (i = position) and B = weights
+// (j = row), so lane l holds D[i][j] for j = l % 32 and
+// i = 8(r/4) + 4(l/32) + r%4 (r = 0..15), and folds its 16 outputs into the
+// chunk partial a = fmaf(fl(dw*dx), (float)isum, a). The round's partials go
+// to LDS and the workgroup adds them to y in chunk order (y = y + a_c), each
+// thread owning 1024/(64W) of the 32x32 outputs. dx of the round's chunks is
+// staged in LDS as [wave][block][position].
+template <int W>
+__global__ __launch_bounds__(64 * W) void q8_gemm_kernel(const int8_t *__restrict__ pc,
+                                                          const uint16_t *__restrict__ ps,
+                                                          const int8_t *__restrict__ qx, const float *__restrict__ dx,
+                                                          void *__restrict__ y, int y_bf16, int N, int K, int T) {
+  constexpr int EPT = 1024 / (64 * W);          // outputs folded per thread
+  __shared__ float part[W][16][64];
+  __shared__ __align__(16) float dxs[W][kCB][32];
   const int nb = K / kQ, nch = nchunks(K);
-  const int tile = blockIdx.x;
-  const int p0 = blockIdx.y * 64;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int sub = wave & 1, pt = wave >> 1;
+  const int tile = blockIdx.x >> 1, sub = blockIdx.x & 1;
+  const int p0 = blockIdx.y * 32;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int h = lane >> 5, l32 = lane & 31;
-  const int jrow = sub * 32 + l32;                 // row within the tile
-  const int apos = p0 + pt * 32 + l32;             // A-operand position of this lane
+  const int jrow = sub * 32 + l32;
+  const int apos = p0 + l32;
   const bool aval = apos < T;
   const int8_t *arow = qx + (size_t)(aval ? apos : 0) * K + 16 * h;
-  float yacc[16];
+  float yv[EPT];
 #pragma unroll
-  for (int r = 0; r < 16; r++) yacc[r] = 0.0f;
-  for (int c = 0; c < nch; c++) {
+  for (int k = 0; k < EPT; k++) yv[k] = 0.0f;
+  const int nrounds = (nch + W - 1) / W;
+  for (int rd = 0; rd < nrounds; rd++) {
+    const int c = rd * W + wave;
     const int b0 = c * kCB;
-    const int nbc = (b0 + kCB <= nb) ? kCB : nb - b0;
-    __syncthreads();
-    for (int i = threadIdx.x; i < kCB * 64; i += 256) {
-      const int bi = i >> 6, p = i & 63;
-      const int pos = p0 + p;
-      dxs[bi][p] = (bi < nbc && pos < T) ? dx[(size_t)pos * nb + b0 + bi] : 0.0f;
+    const int nbc = c < nch ? (b0 + kCB <= nb ? kCB : nb - b0) : 0;
+    for (int i = lane; i < kCB * 32; i += 64) {
+      const int bi = i >> 5, p = i & 31, pos = p0 + p;
+      dxs[wave][bi][p] = (bi < nbc && pos < T) ? dx[(size_t)pos * nb + b0 + bi] : 0.0f;
     }
     __syncthreads();
-    const uint4 sv = *reinterpret_cast<const uint4 *>(ps + (((size_t)tile * nch + c) * kTR + jrow) * 8);
-    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
     float a[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) a[r] = 0.0f;
+    if (nbc > 0) {
+      const uint4 sv = *reinterpret_cast<const uint4 *>(ps + (((size_t)tile * nch + c) * kTR + jrow) * 8);
+      const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+      v4i bw[kCB], av[kCB];
 #pragma unroll
-    for (int i = 0; i < kCB; i++) {
-      if (i < nbc) {
-        const int b = b0 + i;
-        const v4i bw = *reinterpret_cast<const v4i *>(pc + ((size_t)tile * nb + b) * kSlab + (h * kTR + jrow) * 16);
-        v4i av = {0, 0, 0, 0};
-        if (aval) av = *reinterpret_cast<const v4i *>(arow + (size_t)b * kQ);
-        v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bw, acc, 0, 0, 0);
-        const float dw = half_of(sw[i >> 1], i & 1);
+      for (int i = 0; i < kCB; i++) {
+        if (i < nbc) {
+          bw[i] = __builtin_nontemporal_load(
+              reinterpret_cast<const v4i *>(pc + ((size_t)tile * nb + b0 + i) * kSlab + (h * kTR + jrow) * 16));
+          av[i] = aval ? *reinterpret_cast<const v4i *>(arow + (size_t)(b0 + i) * kQ) : v4i{0, 0, 0, 0};
+        }
+      }
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[i][pt * 32 + 8 * g + 4 * h]);
-          const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+      for (int i = 0; i < kCB; i++) {
+        if (i < nbc) {
+          v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bw[i], acc, 0, 0, 0);
+          const float dw = half_of(sw[i >> 1], i & 1);
 #pragma unroll
-          for (int k = 0; k < 4; k++) {
-            const int r = 4 * g + k;
-            const float s = dw * dv[k];
-            a[r] = __builtin_fmaf(s, (float)acc[r], a[r]);
+          for (int g = 0; g < 4; g++) {
+            const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[wave][i][8 * g + 4 * h]);
+            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) a[4 * g + k] = __builtin_fmaf(dw * dv[k], (float)acc[4 * g + k], a[4 * g + k]);
           }
         }
       }
     }
 #pragma unroll
-    for (int r = 0; r < 16; r++) yacc[r] = yacc[r] + a[r];
-  }
-  const int row = tile * kTR + jrow;
-  if (row >= N) return;
+    for (int r = 0; r < 16; r++) part[wave][r][lane] = a[r];
+    __syncthreads();
+    const int nvalid = nch - rd * W < W ? nch - rd * W : W;
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
-    const int pos = p0 + pt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-    if (pos < T) {
-      if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)pos * N + row] = f2bf(yacc[r]);
-      else reinterpret_cast<float *>(y)[(size_t)pos * N + row] = yacc[r];
+    for (int k = 0; k < EPT; k++) {
+      const int e = threadIdx.x + k * 64 * W;
+      const int r = e >> 6, l = e & 63;
+      for (int w = 0; w < nvalid; w++) yv[k] = yv[k] + part[w][r][l];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < EPT; k++) {
+    const int e = threadIdx.x + k * 64 * W;
+    const int r = e >> 6, l = e & 63;
+    const int pos = p0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+    const int row = tile * kTR + sub * 32 + (l & 31);
+    if (pos < T && row < N) {
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)pos * N + row] = f2bf(yv[k]);
+      else reinterpret_cast<float *>(y)[(size_t)pos * N + row] = yv[k];
     }
   }
 }
@@ -439,7 +457,16 @@ extern "C" int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const i
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemm: y_dtype %d", y_dtype);
   PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16) && aligned(qx, 16) && aligned(dx, 4), PQ_ERR_ALIGN,
              "pq_q8_gemm: packed weights and qx must be 16-byte aligned");
-  launch(q8_gemm_kernel, dim3((unsigned)ntiles(N), (unsigned)((T + 63) / 64)), dim3(256), 0,
-                     as_stream(stream), pcodes, pscales, qx, dx, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, T);
+  const int nch = nchunks(K);
+  const int W = nch >= 8 ? 8 : (nch >= 4 ? 4 : (nch >= 2 ? 2 : 1));
+  const dim3 grid((unsigned)(ntiles(N) * 2), (unsigned)((T + 31) / 32));
+  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  hipStream_t st = as_stream(stream);
+  switch (W) {
+    case 8: launch(q8_gemm_kernel<8>, grid, dim3(512), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
+    case 4: launch(q8_gemm_kernel<4>, grid, dim3(256), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
+    case 2: launch(q8_gemm_kernel<2>, grid, dim3(128), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
+    default: launch(q8_gemm_kernel<1>, grid, dim3(64), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
+  }
   return check_launch("pq_q8_gemm");
 }
