@@ -143,6 +143,65 @@ int pq_argmax(const float *v, int n, int32_t *out, void *stream);
 int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *tokens, uint16_t *out,
              int H, int vocab, int T, void *stream);
 
+
+/* ================================================== fused decode kernels
+ * The T=1 decode step with the small ops folded into the GEMV that consumes
+ * their output (each workgroup recomputes the vector in its prologue, after
+ * issuing its first weight loads). Same arithmetic and order as the unfused
+ * calls, so the results are bit-identical. Prologue kinds:
+ *   PQ_PRO_Q8       x given as (qx, dx)
+ *   PQ_PRO_RESNORM  h3 = rmsnorm(h, w0); x_out = bf16(x_in + h3) (written once);
+ *                   x = rmsnorm(x_out, w1)            -- rms1 -> eadd -> rms1
+ *   PQ_PRO_NORM     x = rmsnorm(x_in, w0)
+ *   PQ_PRO_EMBED    x_out = embedding row of *tok (packed table, written once);
+ *                   x = rmsnorm(x_out, w0)
+ *   PQ_PRO_SILU     x = silu(gu[0:K]) * gu[K:2K]
+ *   PQ_PRO_CONV     gated short conv of bcx [B|C|x] with ring_in -> ring_out
+ *                   (the shifted ring, written once; a ping-pong pair);
+ *                   ntaps must be 3, taps f32 [K][3] 16-byte aligned
+ * K is the GEMV's K (a power of two, 1024..8192). argmax_parts (optional,
+ * 2 floats per workgroup, pq_q8_gemv_parts(N, K) of them) receives each
+ * workgroup's (max, index) for pq_argmax_parts -- the LM head + k_argmax. */
+#define PQ_PRO_Q8 0
+#define PQ_PRO_RESNORM 1
+#define PQ_PRO_NORM 2
+#define PQ_PRO_EMBED 3
+#define PQ_PRO_SILU 4
+#define PQ_PRO_CONV 5
+typedef struct pq_gemv_prologue {
+  int kind;
+  const int8_t *qx;
+  const float *dx;
+  const uint16_t *h, *x_in;
+  uint16_t *x_out;
+  const float *w0, *w1;
+  float eps;
+  const uint16_t *gu;
+  const uint16_t *bcx, *ring_in;
+  uint16_t *ring_out;
+  const float *taps;
+  int ntaps;
+  const int8_t *emb_pc;
+  const uint16_t *emb_ps;
+  const int32_t *tok;
+  int vocab;
+} pq_gemv_prologue;
+int pq_q8_gemv_parts(int N, int K);
+int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
+                     void *y, int y_dtype, int N, int K, float *argmax_parts, void *stream);
+int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream);
+/* The attention mixer of one decode step (T=1, position pos) in one launch:
+ * q/k norm + RoPE, fp16 KV write at pos, every 64-position split, the ordered
+ * merge, the sigmoid gate, and the Q8_0 row (qx, dx) of o_proj's input; out
+ * (bf16, optional) gets the gated attention output. qkvg is the fused
+ * [q | k | v | gate] GEMV row. Same numerics as pq_qk_prep + pq_attn_decode.
+ * Replaces k_headnorm, k_rope, the KV write, k_attn_head and k_sigmoid_gate of
+ * layer_body (lfm3_nanode.cu:3749-3786). */
+int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float *k_norm,
+                         const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos, int nh,
+                         int nkv, int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx,
+                         float *dx, void *stream);
+
 /* ======================================================= ternary GEMV
  * PQ2_0 x Q8_K, the Bonsai ternary path. codes u8 [N][K/4] (weight i of a
  * byte = bits 2i..2i+1, value = code - 1), fp16 scale per 128 weights
@@ -208,6 +267,12 @@ int pq_engine_feed(void *engine, const int32_t *tokens, int n, int32_t *next_id,
 int pq_engine_greedy(void *engine, const int32_t *prompt, int n_prompt, int n_steps, int32_t *ids);
 /* n_steps T=1 decode steps from the current device-side token; ids may be NULL. */
 int pq_engine_decode(void *engine, int n_steps, int32_t *ids);
+/* Route T=1 steps through the fused decode kernels (1) or the unfused per-op
+ * calls (0); both give the same bits. The default is 1 where the fused kernels
+ * take the configuration (hidden and ffn powers of two in 1024..8192, 3 conv
+ * taps, GQA group 1/2/4, the context's splits in LDS); set_fused(1) on another
+ * configuration returns PQ_ERR_ARG. */
+int pq_engine_set_fused(void *engine, int on);
 int pq_engine_sync(void *engine);
 void *pq_engine_stream(void *engine);
 int pq_engine_position(void *engine);

@@ -1,0 +1,645 @@
+// decode_fused.hip -- the T=1 decode step with its small ops fused into the
+// kernels that consume them (gfx950).
+//
+// A decode step of the reference is ~15 launches per layer (layer_body,
+// lfm3_nanode.cu:3739-3856). Here the GEMV that consumes an activation computes
+// it in its own prologue, redundantly in every workgroup (the vectors are 2K-8K
+// elements), after issuing its first weight loads so the prologue hides under
+// their latency:
+//   RESNORM  h3 = rmsnorm(h, w0); x' = bf16(x + h3) (workgroup 0 writes x');
+//            y = rmsnorm(x', w1)          -- "rms1 -> eadd -> rms1" of layer_body
+//   NORM     y = rmsnorm(x, w0)
+//   EMBED    x = embedding row of the device token (workgroup 0 writes x);
+//            y = rmsnorm(x, w0)
+//   SILU     y = silu(gate) * up
+//   CONV     the gated short conv; workgroup 0 writes the shifted ring into the
+//            other buffer of a ping-pong pair
+//   Q8       y already quantized (qx, dx)
+// then quantizes y to Q8_0 in LDS and runs the GEMV of q8.hip on it. Every op
+// keeps the unfused kernels' arithmetic and order (pairwise sums of squares,
+// the same roundings), so the fused step is bit-identical to the unfused one.
+// The attention mixer of a decode step is one kernel per layer
+// (attn_layer_kernel): q/k norm, RoPE, KV write, every split, the ordered
+// merge, the sigmoid gate and the Q8_0 output for o_proj.
+#include "pq_device.h"
+#include "pq_host.h"
+#include "q8_common.h"
+
+namespace pq {
+
+// --------------------------------------------------------- block helpers
+// Workgroup barrier over LDS only: waits for this wave's LDS operations, not for
+// its outstanding global loads, so weight loads issued before a prologue stay
+// in flight while the prologue runs.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt left alone
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// E contiguous bf16 (E = 4, 8 or 16) as E/2 packed dwords, one 8- or 16-byte
+// vector load per 8 elements; lo/hi unpack to fp32.
+template <int E>
+__device__ __forceinline__ void ld_raw(const uint16_t *__restrict__ p, uint32_t *o) {
+  if constexpr (E == 4) {
+    const uint2 u = *reinterpret_cast<const uint2 *>(p);
+    o[0] = u.x; o[1] = u.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < E / 8; i++) {
+      const uint4 u = reinterpret_cast<const uint4 *>(p)[i];
+      o[4 * i] = u.x; o[4 * i + 1] = u.y; o[4 * i + 2] = u.z; o[4 * i + 3] = u.w;
+    }
+  }
+}
+__device__ __forceinline__ float bf_at(const uint32_t *w, int i) {
+  return __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+}
+template <int E>
+__device__ __forceinline__ void ld_f32(const float *__restrict__ p, float *o) {
+#pragma unroll
+  for (int i = 0; i < E / 4; i++) {
+    const float4 f = reinterpret_cast<const float4 *>(p)[i];
+    o[4 * i] = f.x; o[4 * i + 1] = f.y; o[4 * i + 2] = f.z; o[4 * i + 3] = f.w;
+  }
+}
+template <int E>
+__device__ __forceinline__ void st_bf16(uint16_t *__restrict__ p, const uint16_t *v) {
+  uint32_t w[E / 2];
+#pragma unroll
+  for (int i = 0; i < E / 2; i++) w[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
+  if constexpr (E == 4) {
+    *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < E / 8; i++)
+      reinterpret_cast<uint4 *>(p)[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  }
+}
+
+// Pairwise sum of the squares of a thread's E values, then over the workgroup
+// (wave butterfly, then a pairwise tree over the W waves): the pairwise tree
+// over all E*64*W elements in natural order.
+template <int E>
+__device__ __forceinline__ float wg_pairwise_sq(const float *v, float *red) {
+  float s[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) s[i] = v[i] * v[i];
+#pragma unroll
+  for (int n = E; n > 1; n >>= 1)
+#pragma unroll
+    for (int i = 0; i < n / 2; i++) s[i] = s[2 * i] + s[2 * i + 1];
+  const float t = wave_pairwise_sum(s[0]);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  lds_barrier();
+  const int W = blockDim.x >> 6;
+  float r;
+  if (W == 8) r = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+  else if (W == 4) r = (red[0] + red[1]) + (red[2] + red[3]);
+  else if (W == 2) r = red[0] + red[1];
+  else r = red[0];
+  lds_barrier();
+  return r;
+}
+
+// y = bf16(w * bf16(x * rs)) for the thread's E values.
+template <int E>
+__device__ __forceinline__ void norm_apply(float *x, const float *w, float ss, int K, float eps) {
+  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + eps);
+#pragma unroll
+  for (int i = 0; i < E; i++) x[i] = bf2f(f2bf(w[i] * bf2f(f2bf(x[i] * rs))));
+}
+
+// Q8_0 of the thread's E values (elements e0 .. e0+E-1) into the staged-x
+// layout in LDS (chunk c at c*kXStride, block i of the chunk at i*32) and dxs:
+// amax over the block's 32/E threads, d = amax/127, q = rne(x/d) clamped.
+template <int E>
+__device__ __forceinline__ void quant_lds(const float *v, int e0, int8_t *xs, float *dxs) {
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < E; i++) a = fmaxf(a, fabsf(v[i]));
+#pragma unroll
+  for (int o = 1; o < 32 / E; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  const float d = a / 127.0f;
+  uint32_t w[E / 4];
+#pragma unroll
+  for (int i = 0; i < E / 4; i++) w[i] = 0u;
+#pragma unroll
+  for (int i = 0; i < E; i++) {
+    int q = 0;
+    if (d != 0.0f) {
+      q = (int)__builtin_rintf(v[i] / d);
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+    }
+    w[i >> 2] |= (uint32_t)(uint8_t)q << (8 * (i & 3));
+  }
+  const int b = e0 >> 5;
+  int8_t *dst = xs + (b >> 3) * kXStride + (b & 7) * kQ + (e0 & 31);
+  if constexpr (E == 4) {
+    *reinterpret_cast<uint32_t *>(dst) = w[0];
+  } else {
+#pragma unroll
+    for (int i = 0; i < E / 8; i++) *reinterpret_cast<uint2 *>(dst + 8 * i) = make_uint2(w[2 * i], w[2 * i + 1]);
+  }
+  if ((e0 & 31) == 0) dxs[b] = d;
+}
+
+// ------------------------------------------------------------- prologues
+// Phase 1 (pro_load) issues every global load of the thread's E elements, raw;
+// the GEMV then issues its weight loads; phase 2 (pro_compute) does the math
+// with LDS-only barriers and leaves the Q8_0 x in LDS.
+constexpr int kFusedTaps = 3;  // the fused conv prologue's tap count
+
+template <int E>
+struct ProRegs {
+  uint32_t u0[E / 2], u1[E / 2], u2[E / 2];
+  uint32_t ring[kFusedTaps - 1][E / 2];
+  float f0[E], f1[E];
+  float taps[E * kFusedTaps];
+  uint32_t emb_c[E / 4];
+  uint16_t emb_s;
+};
+
+template <int PRO, int E>
+__device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int K, ProRegs<E> &r) {
+  if constexpr (PRO == PQ_PRO_RESNORM) {
+    ld_raw<E>(p.h + e0, r.u0);
+    ld_raw<E>(p.x_in + e0, r.u1);
+    ld_f32<E>(p.w0 + e0, r.f0);
+    ld_f32<E>(p.w1 + e0, r.f1);
+  } else if constexpr (PRO == PQ_PRO_NORM) {
+    ld_raw<E>(p.x_in + e0, r.u0);
+    ld_f32<E>(p.w0 + e0, r.f0);
+  } else if constexpr (PRO == PQ_PRO_EMBED) {
+    const int id = *p.tok;
+    const bool ok = id >= 0 && id < p.vocab;
+    const int nb = K / kQ, nch = nchunks(K), tile = ok ? id / kTR : 0, rr = ok ? id % kTR : 0;
+    const int b = e0 / kQ, hh = (e0 % kQ) / 16, jj = e0 % 16;
+    const int8_t *src = p.emb_pc + (((size_t)tile * nb + b) * 2 + hh) * (kTR * 16) + rr * 16 + jj;
+#pragma unroll
+    for (int i = 0; i < E / 4; i++) r.emb_c[i] = ok ? reinterpret_cast<const uint32_t *>(src)[i] : 0u;
+    r.emb_s = ok ? p.emb_ps[(((size_t)tile * nch + b / kCB) * kTR + rr) * kCB + (b % kCB)] : (uint16_t)0;
+    ld_f32<E>(p.w0 + e0, r.f0);
+  } else if constexpr (PRO == PQ_PRO_SILU) {
+    ld_raw<E>(p.gu + e0, r.u0);
+    ld_raw<E>(p.gu + K + e0, r.u1);
+  } else if constexpr (PRO == PQ_PRO_CONV) {
+    ld_raw<E>(p.bcx + e0, r.u0);          // B
+    ld_raw<E>(p.bcx + K + e0, r.u1);      // C
+    ld_raw<E>(p.bcx + 2 * K + e0, r.u2);  // x
+#pragma unroll
+    for (int k = 1; k < kFusedTaps; k++) ld_raw<E>(p.ring_in + (size_t)k * K + e0, r.ring[k - 1]);
+    ld_f32<E * kFusedTaps>(p.taps + (size_t)e0 * kFusedTaps, r.taps);
+  }
+}
+
+template <int PRO, int E>
+__device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, int K, ProRegs<E> &r, float *red,
+                                            int8_t *xs, float *dxs) {
+  const bool writer = blockIdx.x == 0;
+  float v[E];
+  if constexpr (PRO == PQ_PRO_RESNORM) {
+#pragma unroll
+    for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
+    const float ss = wg_pairwise_sq<E>(v, red);
+    const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + p.eps);
+    uint16_t xn[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const float h3 = bf2f(f2bf(r.f0[i] * bf2f(f2bf(v[i] * rs))));
+      xn[i] = f2bf(bf_at(r.u1, i) + h3);
+      v[i] = bf2f(xn[i]);
+    }
+    if (writer) st_bf16<E>(p.x_out + e0, xn);
+    norm_apply<E>(v, r.f1, wg_pairwise_sq<E>(v, red), K, p.eps);
+  } else if constexpr (PRO == PQ_PRO_NORM) {
+#pragma unroll
+    for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
+    norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
+  } else if constexpr (PRO == PQ_PRO_EMBED) {
+    const float sc = h2f(r.emb_s);
+    uint16_t xb[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const int8_t c = (int8_t)((r.emb_c[i >> 2] >> (8 * (i & 3))) & 0xffu);
+      xb[i] = f2bf((float)c * sc);
+      v[i] = bf2f(xb[i]);
+    }
+    if (writer) st_bf16<E>(p.x_out + e0, xb);
+    norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
+  } else if constexpr (PRO == PQ_PRO_SILU) {
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const float a = bf_at(r.u0, i);
+      const float sg = 1.0f / (1.0f + expf_pq(-a));
+      v[i] = bf2f(f2bf((a * sg) * bf_at(r.u1, i)));
+    }
+  } else if constexpr (PRO == PQ_PRO_CONV) {
+    uint16_t rout[kFusedTaps][E];
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      const uint16_t bx = f2bf(bf_at(r.u0, i) * bf_at(r.u2, i));
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kFusedTaps; k++) {
+        const float rk = k + 1 < kFusedTaps ? bf_at(r.ring[k], i) : bf2f(bx);
+        rout[k][i] = f2bf(rk);
+        acc = acc + r.taps[i * kFusedTaps + k] * rk;
+      }
+      const uint16_t cy = f2bf(acc);
+      v[i] = bf2f(f2bf(bf_at(r.u1, i) * bf2f(cy)));
+    }
+    if (writer) {
+#pragma unroll
+      for (int k = 0; k < kFusedTaps; k++) st_bf16<E>(p.ring_out + (size_t)k * K + e0, rout[k]);
+    }
+  }
+  quant_lds<E>(v, e0, xs, dxs);
+  lds_barrier();
+}
+
+// ------------------------------------------------------------ fused GEMV
+// The GEMV of q8.hip (R rows per workgroup, chunk slots per lane, rounds with an
+// ordered LDS fold) with x from the prologue: 64*W threads, E = K/(64*W)
+// contiguous elements of the prologue per thread. Optional argmax partials:
+// each workgroup writes the (value, index) of the largest of its outputs
+// (lowest index on ties) for pq_argmax_parts.
+template <int R, int PRO, int E>
+__global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__restrict__ pc,
+                                                             const uint16_t *__restrict__ ps, pq_gemv_prologue p,
+                                                             void *__restrict__ y, int y_bf16, int N, int K,
+                                                             float *__restrict__ parts) {
+  constexpr int C = 64 / R;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float red[8];
+  const int nb = K / kQ, nch = nchunks(K);
+  const int W = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int cs = lane / R, r = lane % R;
+  const int tile = blockIdx.x / C, trow = (blockIdx.x % C) * R + r;
+  const int row = tile * kTR + trow;
+  float *sp = reinterpret_cast<float *>(smem);                       // [W*C][R]
+  int8_t *xs = reinterpret_cast<int8_t *>(smem + (size_t)W * 64 * 4);
+  float *dxs = reinterpret_cast<float *>(xs + (size_t)nch * kXStride);
+  const int per_round = W * C;
+  const int nrounds = (nch + per_round - 1) / per_round;
+  const int slot = wave * C + cs;
+  const int e0 = threadIdx.x * E;
+  ProRegs<E> pr;
+  if constexpr (PRO != PQ_PRO_Q8) pro_load<PRO, E>(p, e0, K, pr);
+  float yv = 0.0f;
+  for (int rd = 0; rd < nrounds; rd++) {
+    const int c = rd * per_round + slot;
+    const int b0 = c * kCB;
+    const bool full = c < nch && b0 + kCB <= nb;
+    const int8_t *slab0 = pc + ((size_t)tile * nb + b0) * kSlab;
+    const uint16_t *sp8 = ps + (((size_t)tile * nch + c) * kTR + trow) * 8;
+    ChunkRegs regs;
+    if (full) load_chunk(regs, slab0, sp8, trow);
+    if (rd == 0) {
+      if constexpr (PRO == PQ_PRO_Q8) {
+        for (int i = threadIdx.x; i < nb * 2; i += blockDim.x)
+          *reinterpret_cast<v4i *>(xs + (i >> 4) * kXStride + (i & 15) * 16) =
+              *reinterpret_cast<const v4i *>(p.qx + i * 16);
+        for (int i = threadIdx.x; i < nb; i += blockDim.x) dxs[i] = p.dx[i];
+        __syncthreads();
+      } else {
+        pro_compute<PRO, E>(p, e0, K, pr, red, xs, dxs);
+      }
+    }
+    float a = 0.0f;
+    if (c < nch) {
+      const int8_t *xc = xs + (size_t)c * kXStride;
+      auto XS = [&](int i, int *x) {
+        const v4i lo = *reinterpret_cast<const v4i *>(xc + i * 32);
+        const v4i hi = *reinterpret_cast<const v4i *>(xc + i * 32 + 16);
+        x[0] = lo.x; x[1] = lo.y; x[2] = lo.z; x[3] = lo.w;
+        x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
+      };
+      auto DX = [&](int i) { return dxs[b0 + i]; };
+      a = full ? dot_chunk(regs, XS, DX) : tail_chunk(slab0, sp8, nb - b0, trow, XS, DX);
+    }
+    sp[slot * R + r] = a;
+    __syncthreads();
+    if (wave == 0 && lane < R) {
+      const int n = nch - rd * per_round < per_round ? nch - rd * per_round : per_round;
+      for (int k = 0; k < n; k++) yv = yv + sp[k * R + lane];
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+    if (lane < R && row < N) {
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yv);
+      else reinterpret_cast<float *>(y)[row] = yv;
+    }
+    if (parts != nullptr) {
+      float v = (lane < R && row < N) ? yv : -__builtin_inff();
+      int idx = (lane < R && row < N) ? row : 0x7fffffff;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+      }
+      if (lane == 0) {
+        parts[2 * blockIdx.x] = v;
+        parts[2 * blockIdx.x + 1] = __int_as_float(idx);
+      }
+    }
+  }
+}
+
+// (value, index) partials -> the lowest index among the maxima.
+__global__ __launch_bounds__(1024) void argmax_parts_kernel(const float *__restrict__ parts, int n,
+                                                             int32_t *__restrict__ out) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  float best = -__builtin_inff();
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float v = parts[2 * i];
+    const int j = __float_as_int(parts[2 * i + 1]);
+    if (v > best || (v == best && j < idx)) { best = v; idx = j; }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { bv[wave] = best; bi[wave] = idx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
+    *out = idx == 0x7fffffff ? 0 : idx;
+  }
+}
+
+// --------------------------------------------------------- attention mixer
+// One workgroup of 8 waves per kv head g at T=1, position pos (keys 0..pos):
+//  1. waves 0..G-1 norm + rope the group's q heads into LDS; wave G norms and
+//     ropes k and writes it (fp16) to the cache at pos; wave G+1 writes v.
+//  2. wave w computes splits w, w+8, ... (64 positions each) for the G heads:
+//     m, l and o exactly as attn_split_kernel, into LDS.
+//  3. waves 0..G-1 merge their head's splits in ascending order, apply the
+//     sigmoid gate and write the Q8_0 row of o_proj's input.
+constexpr int kHDf = 64;
+constexpr int kPartf = kHDf + 2;
+constexpr int kSplitF = 64;   // positions per attention split
+
+__device__ __forceinline__ float qk_norm_rope(float x, const float *__restrict__ w, const float *__restrict__ cs,
+                                               int pos, int rot, float eps, int d) {
+  const float ss = wave_pairwise_sum(x * x);
+  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)kHDf) + eps);
+  float v = bf2f(f2bf(w[d] * bf2f(f2bf(x * rs))));
+  const int half = rot / 2;
+  const float up = __shfl_down(v, kHDf / 2, 64);
+  const float dn = __shfl_up(v, kHDf / 2, 64);
+  if (d < kHDf / 2 && d < half) {
+    const float c = cs[((size_t)pos * half + d) * 2], s = cs[((size_t)pos * half + d) * 2 + 1];
+    v = v * c - up * s;
+  } else if (d >= kHDf / 2 && d - kHDf / 2 < half) {
+    const int i = d - kHDf / 2;
+    const float c = cs[((size_t)pos * half + i) * 2], s = cs[((size_t)pos * half + i) * 2 + 1];
+    v = v * c + dn * s;
+  }
+  return bf2f(f2bf(v));
+}
+
+template <int G>
+__global__ __launch_bounds__(512) void attn_layer_kernel(const uint16_t *__restrict__ qkvg,
+                                                          const float *__restrict__ qn, const float *__restrict__ kn,
+                                                          const float *__restrict__ cs, uint16_t *__restrict__ kc,
+                                                          uint16_t *__restrict__ vc, int pos, int nh, int nkv, int rot,
+                                                          float eps, float scale, uint16_t *__restrict__ out,
+                                                          int8_t *__restrict__ qx, float *__restrict__ dx) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float *qs = reinterpret_cast<float *>(smem);                  // [G][64]
+  float *es = qs + G * kHDf;                                    // [8 waves][G][64]
+  float *st = es + 8 * G * kSplitF;                           // [nsplit][G][66]
+  const int g = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kvd = nkv * kHDf;
+  const int npos = pos + 1;
+  const int ns = (npos + kSplitF - 1) / kSplitF;
+  // 1. q/k norm + rope, KV write
+  for (int hw = wave; hw < G + 2; hw += 8) {
+    if (hw < G) {
+      const int hq = g * G + hw;
+      qs[hw * kHDf + lane] = qk_norm_rope(bf2f(qkvg[hq * kHDf + lane]), qn, cs, pos, rot, eps, lane);
+    } else if (hw == G) {
+      const float k = qk_norm_rope(bf2f(qkvg[nh * kHDf + g * kHDf + lane]), kn, cs, pos, rot, eps, lane);
+      kc[(size_t)pos * kvd + g * kHDf + lane] = f2h(k);
+    } else {
+      vc[(size_t)pos * kvd + g * kHDf + lane] = f2h(bf2f(qkvg[nh * kHDf + kvd + g * kHDf + lane]));
+    }
+  }
+  __syncthreads();
+  // 2. splits
+  for (int j = wave; j < ns; j += 8) {
+    const int p0 = j * kSplitF;
+    const int pn = npos - p0 < kSplitF ? npos - p0 : kSplitF;
+    const bool valid = lane < pn;
+    float dot[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) dot[h] = 0.0f;
+    if (valid) {
+      const uint16_t *kr = kc + (size_t)(p0 + lane) * kvd + g * kHDf;
+      uint4 k8[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) k8[q] = *reinterpret_cast<const uint4 *>(kr + 8 * q);
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const uint32_t kw[4] = {k8[q].x, k8[q].y, k8[q].z, k8[q].w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float kf = h2f((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
+#pragma unroll
+          for (int h = 0; h < G; h++) dot[h] = __builtin_fmaf(qs[h * kHDf + 8 * q + i], kf, dot[h]);
+        }
+      }
+    }
+    float m[G], l[G];
+    float *ew = es + wave * G * kSplitF;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      const float s = valid ? dot[h] * scale : -__builtin_inff();
+      m[h] = wave_max(s);
+      const float e = valid ? expf_pq(s - m[h]) : 0.0f;
+      l[h] = wave_pairwise_sum(e);
+      ew[h * kSplitF + lane] = e;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float o[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) o[h] = 0.0f;
+    const uint16_t *vcol = vc + (size_t)p0 * kvd + g * kHDf + lane;
+    for (int p = 0; p < pn; p += 8) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = p + i < pn ? h2f(vcol[(size_t)(p + i) * kvd]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (p + i < pn) {
+#pragma unroll
+          for (int h = 0; h < G; h++) o[h] = __builtin_fmaf(ew[h * kSplitF + p + i], v[i], o[h]);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      float *sj = st + ((size_t)j * G + h) * kPartf;
+      sj[lane] = o[h];
+      if (lane == 0) {
+        sj[kHDf] = m[h];
+        sj[kHDf + 1] = l[h];
+      }
+    }
+  }
+  __syncthreads();
+  // 3. merge, gate, Q8_0 out
+  for (int hw = wave; hw < G; hw += 8) {
+    const int hq = g * G + hw;
+    float M = -__builtin_inff();
+    for (int j = 0; j < ns; j++) M = fmaxf(M, st[((size_t)j * G + hw) * kPartf + kHDf]);
+    float L = 0.0f, O = 0.0f;
+    for (int j = 0; j < ns; j++) {
+      const float *sj = st + ((size_t)j * G + hw) * kPartf;
+      const float w = expf_pq(sj[kHDf] - M);
+      L = __builtin_fmaf(sj[kHDf + 1], w, L);
+      O = __builtin_fmaf(sj[lane], w, O);
+    }
+    uint16_t rb = f2bf(O / L);
+    const float gs = 1.0f / (1.0f + expf_pq(-bf2f(qkvg[nh * kHDf + 2 * kvd + hq])));
+    rb = f2bf(bf2f(rb) * gs);
+    if (out != nullptr) out[hq * kHDf + lane] = rb;
+    const float v = bf2f(rb);
+    float a = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    const float dq = a / 127.0f;
+    int qv = 0;
+    if (dq != 0.0f) {
+      qv = (int)__builtin_rintf(v / dq);
+      qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
+    }
+    qx[hq * kHDf + lane] = (int8_t)qv;
+    if ((lane & 31) == 0) dx[(hq * kHDf + lane) / 32] = dq;
+  }
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" int pq_q8_gemv_parts(int N, int K) {
+  if (N <= 0 || K <= 0 || K % kQ) return 0;
+  return ntiles(N) * (64 / gemv_shape(N, K).R);
+}
+
+extern "C" int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro, void *y,
+                                int y_dtype, int N, int K, float *argmax_parts, void *stream) {
+  PQ_REQUIRE(pcodes && pscales && pro && y, PQ_ERR_ARG, "pq_q8_gemv_fused: null pointer");
+  PQ_REQUIRE(N > 0 && K >= 1024 && K <= 8192 && (K & (K - 1)) == 0, PQ_ERR_ARG,
+             "pq_q8_gemv_fused: N=%d K=%d (K a power of two, 1024..8192)", N, K);
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemv_fused: y_dtype %d", y_dtype);
+  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16), PQ_ERR_ALIGN, "pq_q8_gemv_fused: packed weights alignment");
+  const pq_gemv_prologue &p = *pro;
+  switch (p.kind) {
+    case PQ_PRO_Q8:
+      PQ_REQUIRE(p.qx && p.dx && aligned(p.qx, 16), PQ_ERR_ARG, "pq_q8_gemv_fused: Q8 prologue needs aligned qx, dx");
+      break;
+    case PQ_PRO_RESNORM:
+      PQ_REQUIRE(p.h && p.x_in && p.x_out && p.w0 && p.w1 && p.x_in != p.x_out, PQ_ERR_ARG,
+                 "pq_q8_gemv_fused: RESNORM needs h, x_in, x_out (distinct), w0, w1");
+      break;
+    case PQ_PRO_NORM:
+      PQ_REQUIRE(p.x_in && p.w0, PQ_ERR_ARG, "pq_q8_gemv_fused: NORM needs x_in, w0");
+      break;
+    case PQ_PRO_EMBED:
+      PQ_REQUIRE(p.tok && p.emb_pc && p.emb_ps && p.x_out && p.w0 && p.vocab > 0, PQ_ERR_ARG,
+                 "pq_q8_gemv_fused: EMBED needs tok, the table, x_out, w0");
+      break;
+    case PQ_PRO_SILU:
+      PQ_REQUIRE(p.gu, PQ_ERR_ARG, "pq_q8_gemv_fused: SILU needs gu");
+      break;
+    case PQ_PRO_CONV:
+      PQ_REQUIRE(p.bcx && p.ring_in && p.ring_out && p.taps && p.ring_in != p.ring_out &&
+                     p.ntaps == kFusedTaps && aligned(p.taps, 16),
+                 PQ_ERR_ARG, "pq_q8_gemv_fused: CONV needs bcx, taps, distinct ring_in / ring_out, ntaps 3");
+      break;
+    default:
+      return fail(PQ_ERR_ARG, "pq_q8_gemv_fused: prologue kind %d", p.kind);
+  }
+  const GemvShape g = gemv_shape(N, K);
+  const int C = 64 / g.R;
+  // 256 or 512 threads: the prologue spreads K over them, E = K/(64W) <= 16 each
+  int W = g.W >= 8 ? 8 : 4;
+  if (K / (64 * W) < 4) W = 4;   // K = 1024
+  if (K / (64 * W) > 16) W = 8;  // K = 8192
+  const int E = K / (64 * W);
+  const int nch = nchunks(K), nb = K / kQ;
+  const size_t lds = (size_t)W * 64 * 4 + (size_t)nch * kXStride + (size_t)nb * 4;
+  const dim3 grid((unsigned)(ntiles(N) * C)), block(64 * W);
+  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  hipStream_t st = as_stream(stream);
+#define PQ_FUSED_E(RR, PP, EE) \
+  launch(q8_gemv_fused_kernel<RR, PP, EE>, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, argmax_parts)
+#define PQ_FUSED_R(RR, PP)                          \
+  switch (E) {                                      \
+    case 4: PQ_FUSED_E(RR, PP, 4); break;           \
+    case 8: PQ_FUSED_E(RR, PP, 8); break;           \
+    default: PQ_FUSED_E(RR, PP, 16); break;         \
+  }
+#define PQ_FUSED(PP)                        \
+  switch (g.R) {                            \
+    case 64: PQ_FUSED_R(64, PP) break;      \
+    case 32: PQ_FUSED_R(32, PP) break;      \
+    case 16: PQ_FUSED_R(16, PP) break;      \
+    default: PQ_FUSED_R(8, PP) break;       \
+  }
+  switch (p.kind) {
+    case PQ_PRO_Q8: PQ_FUSED(PQ_PRO_Q8) break;
+    case PQ_PRO_RESNORM: PQ_FUSED(PQ_PRO_RESNORM) break;
+    case PQ_PRO_NORM: PQ_FUSED(PQ_PRO_NORM) break;
+    case PQ_PRO_EMBED: PQ_FUSED(PQ_PRO_EMBED) break;
+    case PQ_PRO_SILU: PQ_FUSED(PQ_PRO_SILU) break;
+    default: PQ_FUSED(PQ_PRO_CONV) break;
+  }
+#undef PQ_FUSED
+#undef PQ_FUSED_R
+#undef PQ_FUSED_E
+  return check_launch("pq_q8_gemv_fused");
+}
+
+extern "C" int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream) {
+  PQ_REQUIRE(parts && out && nparts > 0, PQ_ERR_ARG, "pq_argmax_parts: nparts=%d", nparts);
+  launch(argmax_parts_kernel, dim3(1), dim3(1024), 0, as_stream(stream), parts, nparts, out);
+  return check_launch("pq_argmax_parts");
+}
+
+extern "C" int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float *k_norm,
+                                    const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos, int nh, int nkv,
+                                    int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
+                                    void *stream) {
+  PQ_REQUIRE(qkvg && q_norm && k_norm && rope_cs && kcache && vcache && qx && dx, PQ_ERR_ARG,
+             "pq_attn_layer_decode: null pointer");
+  PQ_REQUIRE(hd == kHDf && nh > 0 && nkv > 0 && nh % nkv == 0 && pos >= 0 && rot >= 0 && rot <= hd, PQ_ERR_ARG,
+             "pq_attn_layer_decode: hd=%d nh=%d nkv=%d pos=%d", hd, nh, nkv, pos);
+  PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "pq_attn_layer_decode: cache alignment");
+  const int G = nh / nkv;
+  const int ns = (pos + 1 + kSplitF - 1) / kSplitF;
+  const size_t lds = ((size_t)G * kHDf + 8 * (size_t)G * kSplitF + (size_t)ns * G * kPartf) * 4;
+  PQ_REQUIRE(lds <= 65536, PQ_ERR_ARG, "pq_attn_layer_decode: position %d needs %zu B of LDS", pos, lds);
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(nkv), block(512);
+  switch (G) {
+    case 1: launch(attn_layer_kernel<1>, grid, block, lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nh, nkv, rot, eps, scale, out, qx, dx); break;
+    case 2: launch(attn_layer_kernel<2>, grid, block, lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nh, nkv, rot, eps, scale, out, qx, dx); break;
+    case 4: launch(attn_layer_kernel<4>, grid, block, lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nh, nkv, rot, eps, scale, out, qx, dx); break;
+    default: return fail(PQ_ERR_ARG, "pq_attn_layer_decode: %d q heads per kv head (1, 2 or 4)", G);
+  }
+  return check_launch("pq_attn_layer_decode");
+}

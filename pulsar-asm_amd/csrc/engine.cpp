@@ -20,6 +20,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <memory>
 #include <vector>
 
@@ -38,7 +39,10 @@ struct LayerDev {
   Q8Dev in, out, ug, down;
   float *op_norm = nullptr, *post_op_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
   float *q_norm = nullptr, *k_norm = nullptr, *taps = nullptr;
-  uint16_t *kc = nullptr, *vc = nullptr, *ring = nullptr;
+  uint16_t *kc = nullptr, *vc = nullptr;
+  uint16_t *rings[2] = {nullptr, nullptr};  // conv ring ping-pong pair; rings[rc] is current
+  int rc = 0;
+  uint16_t *ring() const { return rings[rc]; }
 };
 
 struct Engine {
@@ -48,6 +52,11 @@ struct Engine {
   Q8Dev emb;
   float *final_norm = nullptr, *rope = nullptr;
   int pos = 0, tmax = 0, qd = 0, kvd = 0, nin = 0, last_t = 1;
+  bool fused = false;             // T=1 steps through the fused kernels (when supported)
+  uint16_t *Xd[2] = {nullptr, nullptr};  // decode residual ping-pong
+  const uint16_t *last_resid = nullptr;
+  float *parts = nullptr;
+  int nparts = 0;
   // activations, sized for tmax positions
   uint16_t *X = nullptr, *Hb = nullptr, *Wd = nullptr, *A = nullptr;
   int8_t *qx = nullptr;
@@ -115,7 +124,8 @@ static int create(Engine &E, const pq_model_cfg &c) {
       PQ_TRY(alloc_q8(E, D.in, 3 * H, H));
       PQ_TRY(alloc_q8(E, D.out, H, H));
       PQ_TRY(E.dalloc(&D.taps, (size_t)H * c.ntaps));
-      PQ_TRY(E.dalloc(&D.ring, (size_t)H * c.ntaps));
+      PQ_TRY(E.dalloc(&D.rings[0], (size_t)H * c.ntaps));
+      PQ_TRY(E.dalloc(&D.rings[1], (size_t)H * c.ntaps));
     }
     PQ_TRY(alloc_q8(E, D.ug, 2 * F, H));
     PQ_TRY(alloc_q8(E, D.down, H, F));
@@ -131,6 +141,10 @@ static int create(Engine &E, const pq_model_cfg &c) {
   const int wide = std::max(std::max(3 * H, 2 * F), E.nin);
   const int kmax = std::max(std::max(H, F), E.qd);
   PQ_TRY(E.dalloc(&E.X, (size_t)T * H));
+  PQ_TRY(E.dalloc(&E.Xd[0], (size_t)H));
+  PQ_TRY(E.dalloc(&E.Xd[1], (size_t)H));
+  E.nparts = pq_q8_gemv_parts(c.vocab, H);
+  PQ_TRY(E.dalloc(&E.parts, (size_t)E.nparts * 2));
   PQ_TRY(E.dalloc(&E.Hb, (size_t)T * H));
   PQ_TRY(E.dalloc(&E.Wd, (size_t)T * wide));
   PQ_TRY(E.dalloc(&E.A, (size_t)T * kmax));
@@ -280,8 +294,11 @@ static int reset(Engine &E) {
       if (hipMemcpyAsync(D.kc, z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess ||
           hipMemcpyAsync(D.vc, z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess)
         return fail(PQ_ERR_LAUNCH, "reset copy failed");
-    } else if (hipMemcpyAsync(D.ring, z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess) {
-      return fail(PQ_ERR_LAUNCH, "reset copy failed");
+    } else {
+      D.rc = 0;
+      if (hipMemcpyAsync(D.rings[0], z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+          hipMemcpyAsync(D.rings[1], z.data(), n * 2, hipMemcpyHostToDevice, E.st) != hipSuccess)
+        return fail(PQ_ERR_LAUNCH, "reset copy failed");
     }
     if (hipStreamSynchronize(E.st) != hipSuccess) return fail(PQ_ERR_LAUNCH, "reset sync failed");
   }
@@ -315,7 +332,7 @@ static int forward(Engine &E, int T, int32_t *next) {
       PQ_TRY(gemv_or_gemm(E, D.out, E.Hb, T));
     } else {
       PQ_TRY(gemv_or_gemm(E, D.in, E.Wd, T));
-      PQ_TRY(pq_conv(D.ring, D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
+      PQ_TRY(pq_conv(D.ring(), D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
       PQ_TRY(pq_q8_quant_bf16(E.A, E.qx, E.dx, H, T, E.st));
       PQ_TRY(gemv_or_gemm(E, D.out, E.Hb, T));
     }
@@ -332,6 +349,102 @@ static int forward(Engine &E, int T, int32_t *next) {
   PQ_TRY(pq_argmax(E.logits, c.vocab, next, E.st));
   E.pos += T;
   E.last_t = T;
+  E.last_resid = E.X + (size_t)(T - 1) * H;
+  return PQ_OK;
+}
+
+// Whether the fused decode kernels take this configuration: power-of-two
+// hidden and FFN widths of 1024..8192 (the fused GEMV prologue), 3 conv taps,
+// head_dim 64 with a GQA group of 1, 2 or 4 and the attention mixer's LDS at
+// the full context.
+static bool fused_supported(const pq_model_cfg &c, const char **why) {
+  auto pow2 = [](int v) { return v >= 1024 && v <= 8192 && (v & (v - 1)) == 0; };
+  bool conv = false, attn = false;
+  for (int l = 0; l < c.nlayers; l++) ((c.attn_mask >> l) & 1u ? attn : conv) = true;
+  *why = nullptr;
+  if (!pow2(c.hidden) || !pow2(c.ffn)) *why = "hidden and ffn must be powers of two in 1024..8192";
+  else if (conv && c.ntaps != 3) *why = "the fused conv prologue takes 3 taps";
+  else if (attn) {
+    const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
+    const size_t ns = ((size_t)c.ctx + 63) / 64;
+    if (c.hd != 64 || (G != 1 && G != 2 && G != 4)) *why = "the fused attention mixer takes head_dim 64, GQA group 1, 2 or 4";
+    else if (((size_t)G * 64 + 8 * (size_t)G * 64 + ns * G * 66) * 4 > 65536) *why = "context too long for the fused attention mixer";
+  }
+  return *why == nullptr;
+}
+
+// One T=1 decode step through the fused kernels: four GEMV launches per conv
+// layer, five per attention layer (incl. the attention mixer), the LM head with
+// per-workgroup argmax partials and the final argmax -- 107 launches for the
+// 24-layer backbone. Reads the token from E.tok and writes the next one there.
+static int forward_decode(Engine &E) {
+  const pq_model_cfg &c = E.c;
+  const int H = c.hidden;
+  if (E.pos + 1 > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + 1 > %d", E.pos, c.ctx);
+  uint16_t *xa = E.Xd[0], *xb = E.Xd[1];
+  pq_gemv_prologue p;
+  auto resnorm = [&](const float *w0, const float *w1) {
+    p = pq_gemv_prologue{};
+    p.kind = PQ_PRO_RESNORM;
+    p.h = E.Hb;
+    p.x_in = xa;
+    p.x_out = xb;
+    p.w0 = w0;
+    p.w1 = w1;
+    p.eps = c.eps;
+    std::swap(xa, xb);
+  };
+  auto gemv = [&](const Q8Dev &w, void *y, int dt, float *parts) {
+    return pq_q8_gemv_fused(w.pc, w.ps, &p, y, dt, w.N, w.K, parts, E.st);
+  };
+  const float scale = 1.0f / sqrtf((float)c.hd);
+  for (int l = 0; l < c.nlayers; l++) {
+    LayerDev &D = E.L[l];
+    if (l == 0) {
+      p = pq_gemv_prologue{};
+      p.kind = PQ_PRO_EMBED;
+      p.tok = E.tok;
+      p.emb_pc = E.emb.pc;
+      p.emb_ps = E.emb.ps;
+      p.vocab = c.vocab;
+      p.x_out = xa;
+      p.w0 = D.op_norm;
+      p.eps = c.eps;
+    } else {
+      resnorm(E.L[l - 1].post_ffn_norm, D.op_norm);
+    }
+    PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
+    p = pq_gemv_prologue{};
+    if (D.attn) {
+      PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd, c.rot,
+                                  c.eps, scale, nullptr, E.qx, E.dx, E.st));
+      p.kind = PQ_PRO_Q8;
+      p.qx = E.qx;
+      p.dx = E.dx;
+    } else {
+      p.kind = PQ_PRO_CONV;
+      p.bcx = E.Wd;
+      p.ring_in = D.rings[D.rc];
+      p.ring_out = D.rings[1 - D.rc];
+      p.taps = D.taps;
+      p.ntaps = c.ntaps;
+      D.rc = 1 - D.rc;
+    }
+    PQ_TRY(gemv(D.out, E.Hb, PQ_DTYPE_BF16, nullptr));
+    resnorm(D.post_op_norm, D.ffn_norm);
+    PQ_TRY(gemv(D.ug, E.Wd, PQ_DTYPE_BF16, nullptr));
+    p = pq_gemv_prologue{};
+    p.kind = PQ_PRO_SILU;
+    p.gu = E.Wd;
+    PQ_TRY(gemv(D.down, E.Hb, PQ_DTYPE_BF16, nullptr));
+  }
+  resnorm(E.L[c.nlayers - 1].post_ffn_norm, E.final_norm);
+  PQ_TRY(gemv(E.emb, E.logits, PQ_DTYPE_F32, E.parts));
+  PQ_TRY(pq_argmax_parts(E.parts, E.nparts, E.tok, E.st));
+  E.pos += 1;
+  E.last_t = 1;
+  E.last_resid = xa;
+  (void)H;
   return PQ_OK;
 }
 
@@ -351,7 +464,8 @@ static int prefill(Engine &E, const int32_t *prompt, int n, int32_t *next) {
 // of step s-1 and writes its own into ids[s] and E.tok (no host round trip).
 static int decode(Engine &E, int n, int first_slot) {
   for (int s = 0; s < n; s++) {
-    PQ_TRY(forward(E, 1, E.tok));
+    if (E.fused) PQ_TRY(forward_decode(E));
+    else PQ_TRY(forward(E, 1, E.tok));
     if (hipMemcpyAsync(E.ids + first_slot + s, E.tok, 4, hipMemcpyDeviceToDevice, E.st) != hipSuccess)
       return fail(PQ_ERR_LAUNCH, "id copy failed");
   }
@@ -374,6 +488,8 @@ extern "C" void *pq_engine_create(const pq_model_cfg *cfg) {
   auto E = std::make_unique<Engine>();
   if (create(*E, c) != PQ_OK) return nullptr;
   if (upload_rope(*E) != PQ_OK || reset(*E) != PQ_OK) return nullptr;
+  const char *why;
+  E->fused = fused_supported(c, &why);
   return E.release();
 }
 
@@ -459,6 +575,15 @@ extern "C" int pq_engine_decode(void *h, int n_steps, int32_t *ids) {
   return PQ_OK;
 }
 
+extern "C" int pq_engine_set_fused(void *h, int on) {
+  PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
+  Engine &E = *static_cast<Engine *>(h);
+  const char *why;
+  if (on && !fused_supported(E.c, &why)) return fail(PQ_ERR_ARG, "pq_engine_set_fused: %s", why);
+  E.fused = on != 0;
+  return PQ_OK;
+}
+
 extern "C" int pq_engine_sync(void *h) {
   PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
   return hipStreamSynchronize(static_cast<Engine *>(h)->st) == hipSuccess ? PQ_OK
@@ -473,8 +598,8 @@ extern "C" int pq_engine_hidden(void *h, uint16_t *out) {
   PQ_REQUIRE(h && out, PQ_ERR_ARG, "pq_engine_hidden: null pointer");
   Engine &E = *static_cast<Engine *>(h);
   // The residual stream of the last position fed.
-  return hipMemcpy(out, E.X + (size_t)(E.last_t - 1) * E.c.hidden, (size_t)E.c.hidden * 2, hipMemcpyDeviceToHost) ==
-                 hipSuccess
+  if (!E.last_resid) return fail(PQ_ERR_STATE, "pq_engine_hidden: nothing fed yet");
+  return hipMemcpy(out, E.last_resid, (size_t)E.c.hidden * 2, hipMemcpyDeviceToHost) == hipSuccess
              ? PQ_OK
              : fail(PQ_ERR_LAUNCH, "hidden copy failed");
 }

@@ -16,6 +16,15 @@ class ModelCfg(C.Structure):
                 ("seed", C.c_uint64), ("attn_mask", C.c_uint32), ("prefill_chunk", C.c_int)]
 
 
+class GemvPrologue(C.Structure):
+    """pq_gemv_prologue."""
+    _fields_ = [("kind", C.c_int), ("qx", C.c_void_p), ("dx", C.c_void_p), ("h", C.c_void_p), ("x_in", C.c_void_p),
+                ("x_out", C.c_void_p), ("w0", C.c_void_p), ("w1", C.c_void_p), ("eps", C.c_float),
+                ("gu", C.c_void_p), ("bcx", C.c_void_p), ("ring_in", C.c_void_p), ("ring_out", C.c_void_p),
+                ("taps", C.c_void_p), ("ntaps", C.c_int), ("emb_pc", C.c_void_p), ("emb_ps", C.c_void_p),
+                ("tok", C.c_void_p), ("vocab", C.c_int)]
+
+
 SIGNATURES = {
     "pq_version": (C.c_char_p, []),
     "pq_last_error": (C.c_char_p, []),
@@ -35,6 +44,10 @@ SIGNATURES = {
     "pq_silu_mul": (I, [P, P, P, P, I, I, P]),
     "pq_argmax": (I, [P, I, P, P]),
     "pq_embed": (I, [P, P, P, P, I, I, I, P]),
+    "pq_q8_gemv_parts": (I, [I, I]),
+    "pq_q8_gemv_fused": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, I, P, P]),
+    "pq_argmax_parts": (I, [P, I, P, P]),
+    "pq_attn_layer_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, F, F, P, P, P, P]),
     "pq_tq2_gemv": (I, [P, P, P, P, I, I, P]),
     "pq_q8k_quant": (I, [P, P, I, I, P]),
     "pq_synth_fill": (I, [I, U64, P, Z, F, F]),
@@ -48,6 +61,7 @@ SIGNATURES = {
     "pq_engine_feed": (I, [P, P, I, P, P]),
     "pq_engine_greedy": (I, [P, P, I, I, P]),
     "pq_engine_decode": (I, [P, I, P]),
+    "pq_engine_set_fused": (I, [P, I]),
     "pq_engine_sync": (I, [P]),
     "pq_engine_stream": (P, [P]),
     "pq_engine_position": (I, [P]),

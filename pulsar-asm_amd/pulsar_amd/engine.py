@@ -75,6 +75,9 @@ class Engine:
         check(lib().pq_engine_decode(self.h, n_steps, _p(ids) if ids is not None else None), "pq_engine_decode")
         return ids
 
+    def set_fused(self, on):
+        check(lib().pq_engine_set_fused(self.h, 1 if on else 0), "pq_engine_set_fused")
+
     def sync(self):
         check(lib().pq_engine_sync(self.h), "pq_engine_sync")
 

@@ -9,7 +9,11 @@ import torch
 from . import check, lib
 
 __all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
-           "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv"]
+           "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "gemv_fused",
+           "argmax_parts", "attn_layer_decode", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
+           "PRO_CONV"]
+
+PRO_Q8, PRO_RESNORM, PRO_NORM, PRO_EMBED, PRO_SILU, PRO_CONV = 0, 1, 2, 3, 4, 5
 
 DT_F32 = 0
 DT_BF16 = 1
@@ -175,3 +179,43 @@ def tq2_gemv(codes, scales, xq, N, K, out=None):
     check(lib().pq_tq2_gemv(codes.data_ptr(), scales.data_ptr(), xq.data_ptr(), out.data_ptr(), N, K, stream_ptr()),
           "pq_tq2_gemv")
     return out
+
+
+# ------------------------------------------------------- fused decode path
+def gemv_fused(w, kind, out_dtype=DT_BF16, out=None, parts=None, eps=1e-5, **ptrs):
+    """GEMV whose input x is produced by a prologue (pq_q8_gemv_fused). ptrs are
+    tensors for the pq_gemv_prologue fields (qx, dx, h, x_in, x_out, w0, w1, gu,
+    bcx, ring_in, ring_out, taps, emb (a Q8Weight), tok) plus ints ntaps, vocab."""
+    import ctypes as C
+    from ._abi import GemvPrologue
+    p = GemvPrologue()
+    p.kind = kind
+    p.eps = eps
+    for k, v in ptrs.items():
+        if k == "emb":
+            p.emb_pc, p.emb_ps = v.pcodes.data_ptr(), v.pscales.data_ptr()
+        elif k in ("ntaps", "vocab"):
+            setattr(p, k, int(v))
+        else:
+            setattr(p, k, v.data_ptr())
+    if out is None:
+        out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=w.pcodes.device)
+    check(lib().pq_q8_gemv_fused(w.pcodes.data_ptr(), w.pscales.data_ptr(), C.byref(p), out.data_ptr(), out_dtype,
+                                 w.N, w.K, _ptr(parts), stream_ptr()), "pq_q8_gemv_fused")
+    return out
+
+
+def argmax_parts(parts, nparts):
+    out = torch.empty(1, dtype=torch.int32, device=parts.device)
+    check(lib().pq_argmax_parts(parts.data_ptr(), nparts, out.data_ptr(), stream_ptr()), "pq_argmax_parts")
+    return out
+
+
+def attn_layer_decode(qkvg, q_norm, k_norm, rope_cs, kc, vc, pos, nh, nkv, hd, rot, scale, eps=1e-5, out=None):
+    qx = torch.empty(nh * hd, dtype=torch.int8, device=qkvg.device)
+    dx = torch.empty(nh * hd // 32, dtype=torch.float32, device=qkvg.device)
+    check(lib().pq_attn_layer_decode(_bits16(qkvg), q_norm.data_ptr(), k_norm.data_ptr(), rope_cs.data_ptr(),
+                                     _bits16(kc), _bits16(vc), pos, nh, nkv, hd, rot, eps, scale,
+                                     _bits16(out) if out is not None else None, qx.data_ptr(), dx.data_ptr(),
+                                     stream_ptr()), "pq_attn_layer_decode")
+    return qx, dx

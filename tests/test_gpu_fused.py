@@ -1,0 +1,155 @@
+"""The fused decode kernels equal the unfused op sequences bit for bit (and hence
+the oracle): every GEMV prologue kind, the LM head's argmax partials, the
+one-launch attention mixer, and the engine's fused decode path."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+SEED = 4242
+
+
+def _t16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+
+
+def _u16(t):
+    if t.dtype == torch.bfloat16:
+        t = t.view(torch.int16)
+    return t.cpu().numpy().view(np.uint16)
+
+
+def _w(orc, pq, dev, N, K, seed):
+    W, S = orc.q8_weights(seed, N, K)
+    return W, S, pq.Q8Weight(torch.from_numpy(W).to(dev), torch.from_numpy(S.view(np.int16)).to(dev))
+
+
+def _ref_gemv(orc, W, S, xb):
+    qx, dx = orc.q8_quant_bf16(xb)
+    return orc.f2bf(orc.q8_gemv(W, S, qx, dx))
+
+
+@pytest.mark.parametrize("N", [3104, 16384, 2048, 65536])
+def test_resnorm_prologue(orc, pq, dev, N):
+    H = 2048
+    W, S, w = _w(orc, pq, dev, N, H, SEED + N)
+    x = orc.f2bf(orc.gen_normal(SEED + 1, H) * 5)
+    h = orc.f2bf(orc.gen_normal(SEED + 2, H) * 40)
+    w0 = orc.gen_affine(SEED + 3, H, 4.0, 0.4)
+    w1 = orc.gen_affine(SEED + 4, H, 1.0, 0.1)
+    xn = orc.add(x, orc.rmsnorm(h, w0))
+    y_in = orc.rmsnorm(xn, w1)
+    xo = torch.zeros(H, dtype=torch.int16, device=dev)
+    dt = pq.DT_F32 if N == 65536 else pq.DT_BF16
+    parts = torch.empty(2 * pq.lib().pq_q8_gemv_parts(N, H), dtype=torch.float32, device=dev) if N == 65536 else None
+    y = pq.gemv_fused(w, pq.PRO_RESNORM, out_dtype=dt, parts=parts, h=_t16(h, dev), x_in=_t16(x, dev), x_out=xo,
+                      w0=torch.from_numpy(w0).to(dev), w1=torch.from_numpy(w1).to(dev))
+    assert np.array_equal(_u16(xo), xn)
+    qx, dx = orc.q8_quant_bf16(y_in)
+    yr = orc.q8_gemv(W, S, qx, dx)
+    if dt == pq.DT_F32:
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32))
+        nparts = pq.lib().pq_q8_gemv_parts(N, H)
+        assert int(pq.argmax_parts(parts, nparts).item()) == orc.argmax(yr)
+    else:
+        assert np.array_equal(_u16(y), orc.f2bf(yr))
+
+
+def test_norm_and_embed_prologues(orc, pq, dev):
+    H, N, vocab = 2048, 6144, 3000
+    W, S, w = _w(orc, pq, dev, N, H, SEED + 10)
+    E, ES, emb = _w(orc, pq, dev, vocab, H, SEED + 11)
+    w0 = orc.gen_affine(SEED + 12, H, 1.0, 0.1)
+    x = orc.f2bf(orc.gen_normal(SEED + 13, H) * 3)
+    y = pq.gemv_fused(w, pq.PRO_NORM, x_in=_t16(x, dev), w0=torch.from_numpy(w0).to(dev))
+    assert np.array_equal(_u16(y), _ref_gemv(orc, W, S, orc.rmsnorm(x, w0)))
+    for tok in (0, 2999, 64, 1234):
+        xo = torch.zeros(H, dtype=torch.int16, device=dev)
+        y = pq.gemv_fused(w, pq.PRO_EMBED, tok=torch.tensor([tok], dtype=torch.int32, device=dev), emb=emb,
+                          vocab=vocab, x_out=xo, w0=torch.from_numpy(w0).to(dev))
+        e = orc.embed_row(E, ES, tok)
+        assert np.array_equal(_u16(xo), e)
+        assert np.array_equal(_u16(y), _ref_gemv(orc, W, S, orc.rmsnorm(e, w0)))
+
+
+def test_silu_prologue(orc, pq, dev):
+    F, N = 8192, 2048
+    W, S, w = _w(orc, pq, dev, N, F, SEED + 20)
+    gu = orc.f2bf(orc.gen_normal(SEED + 21, 2 * F) * 30)
+    y = pq.gemv_fused(w, pq.PRO_SILU, gu=_t16(gu, dev))
+    assert np.array_equal(_u16(y), _ref_gemv(orc, W, S, orc.silu_mul(gu[:F], gu[F:])))
+
+
+def test_conv_prologue(orc, pq, dev):
+    H, N, nt = 2048, 2048, 3
+    W, S, w = _w(orc, pq, dev, N, H, SEED + 30)
+    taps = orc.gen_affine(SEED + 31, H * nt, 0.0, 0.5)
+    ring = orc.f2bf(orc.gen_normal(SEED + 32, nt * H) * 3)
+    bcx = orc.f2bf(orc.gen_normal(SEED + 33, 3 * H) * 10)
+    o, ring_new = orc.conv_step(ring, taps, bcx, H, nt)
+    rin, rout = _t16(ring, dev), torch.zeros(nt * H, dtype=torch.int16, device=dev)
+    y = pq.gemv_fused(w, pq.PRO_CONV, bcx=_t16(bcx, dev), ring_in=rin, ring_out=rout,
+                      taps=torch.from_numpy(taps).to(dev), ntaps=nt)
+    assert np.array_equal(_u16(rout), ring_new)
+    assert np.array_equal(_u16(rin), ring)
+    assert np.array_equal(_u16(y), _ref_gemv(orc, W, S, o))
+
+
+def test_q8_prologue(orc, pq, dev):
+    N, K = 2048, 2048
+    W, S, w = _w(orc, pq, dev, N, K, SEED + 40)
+    x = orc.gen_normal(SEED + 41, K)
+    qx, dx = pq.q8_quant(torch.from_numpy(x).to(dev))
+    y = pq.gemv_fused(w, pq.PRO_Q8, qx=qx, dx=dx)
+    assert torch.equal(y.view(torch.int16), pq.q8_gemv(w, qx, dx, out_dtype=pq.DT_BF16).view(torch.int16))
+
+
+@pytest.mark.parametrize("pos", [0, 63, 64, 300, 2047])
+def test_attn_layer_decode(orc, pq, dev, pos):
+    nh, nkv, hd, rot, ctx = 32, 8, 64, 32, 2048
+    nin = nh * hd + 2 * nkv * hd + nh
+    kvd = nkv * hd
+    row = orc.f2bf(orc.gen_normal(SEED + pos, nin) * 30)
+    qn = orc.gen_affine(SEED + 50, hd, 1.0, 0.1)
+    kn = orc.gen_affine(SEED + 51, hd, 1.0, 0.1)
+    cs = orc.rope_table(ctx, hd, rot, 1e6)
+    kc0 = np.zeros((ctx, kvd), np.float16)
+    vc0 = np.zeros((ctx, kvd), np.float16)
+    kc0[:pos] = orc.gen_normal(SEED + 52, pos * kvd).reshape(pos, kvd) * 2
+    vc0[:pos] = orc.gen_normal(SEED + 53, pos * kvd).reshape(pos, kvd) * 5
+    args = [torch.from_numpy(qn).to(dev), torch.from_numpy(kn).to(dev), torch.from_numpy(cs).to(dev)]
+    # unfused: qk_prep then attn_decode
+    r1 = _t16(row, dev)
+    kc1, vc1 = _t16(kc0.view(np.uint16), dev), _t16(vc0.view(np.uint16), dev)
+    pq.qk_prep(r1, nin, *args, kc1, vc1, pos, nh, nkv, hd, rot, 1)
+    out1 = torch.empty(nh * hd, dtype=torch.int16, device=dev)
+    qx1 = torch.empty(nh * hd, dtype=torch.int8, device=dev)
+    dx1 = torch.empty(nh * hd // 32, dtype=torch.float32, device=dev)
+    pq.attn_decode(r1, nin, kc1, vc1, pos, nh, nkv, hd, 1, 0.125, gate=r1[nh * hd + 2 * kvd:], gate_stride=nin,
+                   out=out1, out_stride=nh * hd, qx=qx1, dx=dx1)
+    # fused
+    r2 = _t16(row, dev)
+    kc2, vc2 = _t16(kc0.view(np.uint16), dev), _t16(vc0.view(np.uint16), dev)
+    out2 = torch.empty(nh * hd, dtype=torch.int16, device=dev)
+    qx2, dx2 = pq.attn_layer_decode(r2, *args, kc2, vc2, pos, nh, nkv, hd, rot, 0.125, out=out2)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(out1, out2)
+    assert torch.equal(qx1, qx2) and torch.equal(dx1.view(torch.int32), dx2.view(torch.int32))
+
+
+def test_engine_fused_equals_unfused(orc, pq, dev):
+    from pulsar_amd.engine import Engine
+    cfg = dict(hidden=2048, ffn=8192, vocab=65536, nlayers=3, nh=32, nkv=8, hd=64, rot=32, ntaps=3, ctx=512,
+               eps=1e-5, theta=1e6, seed=77, attn_mask=0b010)
+    prompt = orc.gen_tokens(9, 70, cfg["vocab"])
+    ids = []
+    for fused in (True, False):
+        e = Engine(**cfg)
+        e.load_synthetic()
+        e.set_fused(fused)
+        ids.append(e.greedy(prompt, 12))
+        e.close()
+    assert np.array_equal(ids[0], ids[1])
+    m = orc.Model(**{k: v for k, v in cfg.items()})
+    assert np.array_equal(ids[0], m.greedy(prompt, 12))
+    m.close()
