@@ -65,6 +65,14 @@ size_t pq_q8_packed_codes_bytes(int N, int K);
 size_t pq_q8_packed_scales_bytes(int N, int K);
 int pq_q8_pack(const int8_t *codes, const uint16_t *scales, int N, int K,
                int8_t *pcodes, uint16_t *pscales, void *stream);
+/* The fused gate/up weight [2F][K] (gate rows 0..F-1, up rows F..2F-1, as
+ * the MERGE:gate_up tensor, lfm3_nanode.cu:3825-3833) packed with its rows
+ * interleaved in groups of 32: packed rows 64t..64t+31 are gate rows
+ * 32t..32t+31, rows 64t+32..64t+63 the up rows F+32t... Every GEMV/GEMM over
+ * it returns its outputs in that order; pq_silu_mul_interleaved and
+ * pq_q8_gemv_fused_swiglu read it. F a multiple of 32. */
+int pq_q8_pack_gate_up(const int8_t *codes, const uint16_t *scales, int F, int K,
+                       int8_t *pcodes, uint16_t *pscales, void *stream);
 
 /* ------------------------------------------------------------ Q8_0 GEMV, T=1
  * y[N] = W[N][K] . x, W packed, x as (qx, dx) from pq_q8_quant_*. y_dtype
@@ -132,6 +140,10 @@ int pq_conv(uint16_t *ring, const float *taps, const uint16_t *bcx, uint16_t *ou
 /* silu(gate) * up over rows [gate (F) | up (F)]; output bf16 and/or Q8_0.
  * Replaces k_silu_mul_bf(v) (821-847). */
 int pq_silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T, void *stream);
+/* The same over rows in the pq_q8_pack_gate_up order (gate element i at
+ * 64*(i/32) + i%32, up element i 32 further). */
+int pq_silu_mul_interleaved(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T,
+                            void *stream);
 
 /* Greedy id: the lowest index among the maxima of v[n]. Replaces k_argmax
  * (942-964; the reference breaks ties by thread slot). */
@@ -190,6 +202,13 @@ int pq_q8_gemv_parts(int N, int K);
 int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
                      void *y, int y_dtype, int N, int K, float *argmax_parts, void *stream);
 int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream);
+/* The FFN's gate/up GEMV (weights from pq_q8_pack_gate_up, N = 2F) with the
+ * prologue pro and silu(gate) * up as its epilogue: writes the Q8_0 row
+ * (qx [F], dx [F/32]) that the down projection reads (PQ_PRO_Q8) -- the
+ * gemv(gate_up), k_silu_mul_bf sequence of layer_body (3830-3833).
+ * Same bits as the GEMV, pq_silu_mul_interleaved and its Q8_0 output. */
+int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
+                            int8_t *qx, float *dx, int F, int K, void *stream);
 /* The attention mixer of one decode step (T=1, position pos) in one launch:
  * q/k norm + RoPE, fp16 KV write at pos, every 64-position split, the ordered
  * merge, the sigmoid gate, and the Q8_0 row (qx, dx) of o_proj's input; out

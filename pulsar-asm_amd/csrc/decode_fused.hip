@@ -79,8 +79,10 @@ __device__ __forceinline__ void st_bf16(uint16_t *__restrict__ p, const uint16_t
 }
 
 // Pairwise sum of the squares of a thread's E values, then over the workgroup
-// (wave butterfly, then a pairwise tree over the W waves): the pairwise tree
-// over all E*64*W elements in natural order.
+// (wave butterfly, then a pairwise tree over 8 wave slots): the pairwise tree
+// over all E*64*W elements in natural order. red holds 8 slots whose entries
+// for absent waves (W < 8) are zero, which leaves every sum of the tree exact.
+// Each call uses its own red slots, so one barrier suffices.
 template <int E>
 __device__ __forceinline__ float wg_pairwise_sq(const float *v, float *red) {
   float s[E];
@@ -93,14 +95,7 @@ __device__ __forceinline__ float wg_pairwise_sq(const float *v, float *red) {
   const float t = wave_pairwise_sum(s[0]);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
   lds_barrier();
-  const int W = blockDim.x >> 6;
-  float r;
-  if (W == 8) r = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
-  else if (W == 4) r = (red[0] + red[1]) + (red[2] + red[3]);
-  else if (W == 2) r = red[0] + red[1];
-  else r = red[0];
-  lds_barrier();
-  return r;
+  return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
 }
 
 // y = bf16(w * bf16(x * rs)) for the thread's E values.
@@ -109,6 +104,20 @@ __device__ __forceinline__ void norm_apply(float *x, const float *w, float ss, i
   const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + eps);
 #pragma unroll
   for (int i = 0; i < E; i++) x[i] = bf2f(f2bf(w[i] * bf2f(f2bf(x[i] * rs))));
+}
+
+// E int8 codes (E/4 dwords) of elements e0.. into the staged-x layout in LDS:
+// chunk c at c*kXStride, block i of the chunk at i*32.
+template <int E>
+__device__ __forceinline__ void store_q8_lds(const uint32_t *w, int e0, int8_t *xs) {
+  const int b = e0 >> 5;
+  int8_t *dst = xs + (b >> 3) * kXStride + (b & 7) * kQ + (e0 & 31);
+  if constexpr (E == 4) {
+    *reinterpret_cast<uint32_t *>(dst) = w[0];
+  } else {
+#pragma unroll
+    for (int i = 0; i < E / 8; i++) *reinterpret_cast<uint2 *>(dst + 8 * i) = make_uint2(w[2 * i], w[2 * i + 1]);
+  }
 }
 
 // Q8_0 of the thread's E values (elements e0 .. e0+E-1) into the staged-x
@@ -134,15 +143,8 @@ __device__ __forceinline__ void quant_lds(const float *v, int e0, int8_t *xs, fl
     }
     w[i >> 2] |= (uint32_t)(uint8_t)q << (8 * (i & 3));
   }
-  const int b = e0 >> 5;
-  int8_t *dst = xs + (b >> 3) * kXStride + (b & 7) * kQ + (e0 & 31);
-  if constexpr (E == 4) {
-    *reinterpret_cast<uint32_t *>(dst) = w[0];
-  } else {
-#pragma unroll
-    for (int i = 0; i < E / 8; i++) *reinterpret_cast<uint2 *>(dst + 8 * i) = make_uint2(w[2 * i], w[2 * i + 1]);
-  }
-  if ((e0 & 31) == 0) dxs[b] = d;
+  store_q8_lds<E>(w, e0, xs);
+  if ((e0 & 31) == 0) dxs[e0 >> 5] = d;
 }
 
 // ------------------------------------------------------------- prologues
@@ -163,7 +165,11 @@ struct ProRegs {
 
 template <int PRO, int E>
 __device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int K, ProRegs<E> &r) {
-  if constexpr (PRO == PQ_PRO_RESNORM) {
+  if constexpr (PRO == PQ_PRO_Q8) {
+#pragma unroll
+    for (int i = 0; i < E / 4; i++) r.emb_c[i] = reinterpret_cast<const uint32_t *>(p.qx + e0)[i];
+    r.f0[0] = (e0 & 31) == 0 ? p.dx[e0 >> 5] : 0.0f;
+  } else if constexpr (PRO == PQ_PRO_RESNORM) {
     ld_raw<E>(p.h + e0, r.u0);
     ld_raw<E>(p.x_in + e0, r.u1);
     ld_f32<E>(p.w0 + e0, r.f0);
@@ -199,7 +205,12 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
                                             int8_t *xs, float *dxs) {
   const bool writer = blockIdx.x == 0;
   float v[E];
-  if constexpr (PRO == PQ_PRO_RESNORM) {
+  if constexpr (PRO == PQ_PRO_Q8) {
+    store_q8_lds<E>(r.emb_c, e0, xs);
+    if ((e0 & 31) == 0) dxs[e0 >> 5] = r.f0[0];
+    lds_barrier();
+    return;
+  } else if constexpr (PRO == PQ_PRO_RESNORM) {
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
     const float ss = wg_pairwise_sq<E>(v, red);
@@ -212,7 +223,7 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
       v[i] = bf2f(xn[i]);
     }
     if (writer) st_bf16<E>(p.x_out + e0, xn);
-    norm_apply<E>(v, r.f1, wg_pairwise_sq<E>(v, red), K, p.eps);
+    norm_apply<E>(v, r.f1, wg_pairwise_sq<E>(v, red + 8), K, p.eps);
   } else if constexpr (PRO == PQ_PRO_NORM) {
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
@@ -269,11 +280,12 @@ template <int R, int PRO, int E>
 __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__restrict__ pc,
                                                              const uint16_t *__restrict__ ps, pq_gemv_prologue p,
                                                              void *__restrict__ y, int y_bf16, int N, int K,
-                                                             float *__restrict__ parts) {
+                                                             float *__restrict__ parts, int8_t *__restrict__ qo,
+                                                             float *__restrict__ dqo) {
   constexpr int C = 64 / R;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float red[8];
-  const int nb = K / kQ, nch = nchunks(K);
+  __shared__ float red[16];
+  const int nb = K / kQ, nch = nchunks(K);  // K a power of two >= 1024: every chunk is full
   const int W = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int cs = lane / R, r = lane % R;
@@ -286,31 +298,27 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
   const int nrounds = (nch + per_round - 1) / per_round;
   const int slot = wave * C + cs;
   const int e0 = threadIdx.x * E;
+  if (threadIdx.x >= W && threadIdx.x < 8) red[threadIdx.x] = red[8 + threadIdx.x] = 0.0f;
+  // 1. the prologue's global loads, then round 0's weight loads, then the
+  //    prologue math: its waits leave the weight loads in flight
   ProRegs<E> pr;
-  if constexpr (PRO != PQ_PRO_Q8) pro_load<PRO, E>(p, e0, K, pr);
+  pro_load<PRO, E>(p, e0, K, pr);
+  const TileRsrc tr = tile_rsrc(pc, ps, tile, nb, nch);
+  int c = slot;
+  ChunkRegs regs;
+  load_chunk_rsrc(regs, tr, c, nch, trow);
+  pro_compute<PRO, E>(p, e0, K, pr, red, xs, dxs);
+  // 2. the GEMV: rounds of W*C chunks, each folded in chunk order
   float yv = 0.0f;
   for (int rd = 0; rd < nrounds; rd++) {
-    const int c = rd * per_round + slot;
-    const int b0 = c * kCB;
-    const bool full = c < nch && b0 + kCB <= nb;
-    const int8_t *slab0 = pc + ((size_t)tile * nb + b0) * kSlab;
-    const uint16_t *sp8 = ps + (((size_t)tile * nch + c) * kTR + trow) * 8;
-    ChunkRegs regs;
-    if (full) load_chunk(regs, slab0, sp8, trow);
-    if (rd == 0) {
-      if constexpr (PRO == PQ_PRO_Q8) {
-        for (int i = threadIdx.x; i < nb * 2; i += blockDim.x)
-          *reinterpret_cast<v4i *>(xs + (i >> 4) * kXStride + (i & 15) * 16) =
-              *reinterpret_cast<const v4i *>(p.qx + i * 16);
-        for (int i = threadIdx.x; i < nb; i += blockDim.x) dxs[i] = p.dx[i];
-        __syncthreads();
-      } else {
-        pro_compute<PRO, E>(p, e0, K, pr, red, xs, dxs);
-      }
+    if (rd > 0) {
+      c = rd * per_round + slot;
+      load_chunk_rsrc(regs, tr, c, nch, trow);
     }
     float a = 0.0f;
     if (c < nch) {
       const int8_t *xc = xs + (size_t)c * kXStride;
+      const int b0 = c * kCB;
       auto XS = [&](int i, int *x) {
         const v4i lo = *reinterpret_cast<const v4i *>(xc + i * 32);
         const v4i hi = *reinterpret_cast<const v4i *>(xc + i * 32 + 16);
@@ -318,7 +326,7 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
         x[4] = hi.x; x[5] = hi.y; x[6] = hi.z; x[7] = hi.w;
       };
       auto DX = [&](int i) { return dxs[b0 + i]; };
-      a = full ? dot_chunk(regs, XS, DX) : tail_chunk(slab0, sp8, nb - b0, trow, XS, DX);
+      a = dot_chunk(regs, XS, DX);
     }
     sp[slot * R + r] = a;
     __syncthreads();
@@ -326,9 +334,28 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
       const int n = nch - rd * per_round < per_round ? nch - rd * per_round : per_round;
       for (int k = 0; k < n; k++) yv = yv + sp[k * R + lane];
     }
-    __syncthreads();
+    if (rd + 1 < nrounds) __syncthreads();
   }
-  if (wave == 0) {
+  if (wave == 0 && qo != nullptr) {
+    // SwiGLU epilogue (R = 64, rows interleaved by pq_q8_pack_gate_up): lane l
+    // < 32 holds gate row 32*tile + l, lane l + 32 its up row; the Q8_0 block
+    // tile of silu(gate) * up as silu_mul_kernel + quant_store form it.
+    if constexpr (R == 64) {
+      const float u = bf2f(f2bf(__shfl_down(yv, 32, 64)));
+      const float a = bf2f(f2bf(yv));
+      const float sg = 1.0f / (1.0f + expf_pq(-a));
+      const float o = bf2f(f2bf((a * sg) * u));
+      const float m = wave_max(lane < 32 ? fabsf(o) : 0.0f);
+      const float d = m / 127.0f;
+      int q = 0;
+      if (d != 0.0f) {
+        q = (int)__builtin_rintf(o / d);
+        q = q > 127 ? 127 : (q < -127 ? -127 : q);
+      }
+      if (lane < 32) qo[32 * tile + lane] = (int8_t)q;
+      if (lane == 0) dqo[tile] = d;
+    }
+  } else if (wave == 0) {
     if (lane < R && row < N) {
       if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yv);
       else reinterpret_cast<float *>(y)[row] = yv;
@@ -379,140 +406,199 @@ __global__ __launch_bounds__(1024) void argmax_parts_kernel(const float *__restr
 }
 
 // --------------------------------------------------------- attention mixer
-// One workgroup of 8 waves per kv head g at T=1, position pos (keys 0..pos):
-//  1. waves 0..G-1 norm + rope the group's q heads into LDS; wave G norms and
-//     ropes k and writes it (fp16) to the cache at pos; wave G+1 writes v.
-//  2. wave w computes splits w, w+8, ... (64 positions each) for the G heads:
-//     m, l and o exactly as attn_split_kernel, into LDS.
-//  3. waves 0..G-1 merge their head's splits in ascending order, apply the
-//     sigmoid gate and write the Q8_0 row of o_proj's input.
+// One workgroup of 8 waves per q head hq (kv head g = hq / G) at T=1, position
+// pos (keys 0..pos). Wave w owns splits w, w+8, ... (64 positions each).
+// Every global load a wave needs for its first split is issued before
+// anything waits: the step-1 inputs, then the K and V blocks of its split,
+// 8 lanes per 128-byte row (whole cache lines per load), through buffer
+// resources that end at position pos (rows >= pos read zeros, no branch).
+//  1. wave 0 norms + ropes q into LDS; wave 1 norms + ropes k, wave 2 rounds
+//     v, both into LDS as fp16 bits and (workgroup G*g only) to the cache.
+//  2. per split: K goes through LDS so lane p holds key p: s = q.k (fmaf
+//     chain over d), m, e, l as attn_split_kernel; then V goes through the same
+//     LDS buffer so lane d runs the fmaf chain over positions for o.
+//  3. wave 0 merges the splits in ascending order, applies the sigmoid gate
+//     and writes the head's Q8_0 blocks of o_proj's input.
 constexpr int kHDf = 64;
 constexpr int kPartf = kHDf + 2;
-constexpr int kSplitF = 64;   // positions per attention split
+constexpr int kSplitF = 64;       // positions per attention split
+constexpr int kVRow = kHDf + 8;   // padded fp16 row of a K/V block in LDS
 
-__device__ __forceinline__ float qk_norm_rope(float x, const float *__restrict__ w, const float *__restrict__ cs,
-                                               int pos, int rot, float eps, int d) {
+// q/k head norm + RoPE of one head (lane d holds x_d, its norm weight wd and
+// the RoPE (cos, sin) of its pair index d mod 32), the arithmetic of
+// qk_prep_kernel.
+__device__ __forceinline__ float qk_norm_rope(float x, float wd, float2 csv, int rot, float eps, int d) {
   const float ss = wave_pairwise_sum(x * x);
   const float rs = 1.0f / sqrtf(ss * (1.0f / (float)kHDf) + eps);
-  float v = bf2f(f2bf(w[d] * bf2f(f2bf(x * rs))));
+  float v = bf2f(f2bf(wd * bf2f(f2bf(x * rs))));
   const int half = rot / 2;
   const float up = __shfl_down(v, kHDf / 2, 64);
   const float dn = __shfl_up(v, kHDf / 2, 64);
   if (d < kHDf / 2 && d < half) {
-    const float c = cs[((size_t)pos * half + d) * 2], s = cs[((size_t)pos * half + d) * 2 + 1];
-    v = v * c - up * s;
+    v = v * csv.x - up * csv.y;
   } else if (d >= kHDf / 2 && d - kHDf / 2 < half) {
-    const int i = d - kHDf / 2;
-    const float c = cs[((size_t)pos * half + i) * 2], s = cs[((size_t)pos * half + i) * 2 + 1];
-    v = v * c + dn * s;
+    v = v * csv.x + dn * csv.y;
   }
   return bf2f(f2bf(v));
 }
 
-template <int G>
-__global__ __launch_bounds__(512) void attn_layer_kernel(const uint16_t *__restrict__ qkvg,
-                                                          const float *__restrict__ qn, const float *__restrict__ kn,
-                                                          const float *__restrict__ cs, uint16_t *__restrict__ kc,
-                                                          uint16_t *__restrict__ vc, int pos, int nh, int nkv, int rot,
-                                                          float eps, float scale, uint16_t *__restrict__ out,
-                                                          int8_t *__restrict__ qx, float *__restrict__ dx) {
+__global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restrict__ qkvg, const float *__restrict__ qn,
+                                                         const float *__restrict__ kn, const float *__restrict__ cs,
+                                                         uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, int pos,
+                                                         int nh, int nkv, int rot, float eps, float scale,
+                                                         uint16_t *__restrict__ out, int8_t *__restrict__ qx,
+                                                         float *__restrict__ dx) {
   extern __shared__ __align__(16) unsigned char smem[];
-  float *qs = reinterpret_cast<float *>(smem);                  // [G][64]
-  float *es = qs + G * kHDf;                                    // [8 waves][G][64]
-  float *st = es + 8 * G * kSplitF;                           // [nsplit][G][66]
-  const int g = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  float *qs = reinterpret_cast<float *>(smem);                    // [64] q
+  float *ew = qs + kHDf;                                           // [8 waves][64] e
+  uint16_t *kvnew = reinterpret_cast<uint16_t *>(ew + 8 * kSplitF);  // [2][64] fp16 k, v at pos
+  uint16_t *blk = kvnew + 2 * kHDf;                                // [8 waves][64][kVRow] K, then V
+  float *st = reinterpret_cast<float *>(blk + 8 * kSplitF * kVRow);  // [nsplit][66]
+  const int hq = blockIdx.x, G = nh / nkv, g = hq / G;
+  const bool writer = hq % G == 0;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int kvd = nkv * kHDf;
   const int npos = pos + 1;
   const int ns = (npos + kSplitF - 1) / kSplitF;
-  // 1. q/k norm + rope, KV write
-  for (int hw = wave; hw < G + 2; hw += 8) {
-    if (hw < G) {
-      const int hq = g * G + hw;
-      qs[hw * kHDf + lane] = qk_norm_rope(bf2f(qkvg[hq * kHDf + lane]), qn, cs, pos, rot, eps, lane);
-    } else if (hw == G) {
-      const float k = qk_norm_rope(bf2f(qkvg[nh * kHDf + g * kHDf + lane]), kn, cs, pos, rot, eps, lane);
-      kc[(size_t)pos * kvd + g * kHDf + lane] = f2h(k);
-    } else {
-      vc[(size_t)pos * kvd + g * kHDf + lane] = f2h(bf2f(qkvg[nh * kHDf + kvd + g * kHDf + lane]));
-    }
+  const int half = rot / 2;
+  // step-1 and step-3 inputs: wave 0 q, wave 1 k, others v (valid addresses)
+  const int xoff = wave == 0 ? hq * kHDf : wave == 1 ? nh * kHDf + g * kHDf : nh * kHDf + kvd + g * kHDf;
+  const uint16_t xraw = qkvg[xoff + lane];
+  const float wd = (wave == 1 ? kn : qn)[lane];
+  const __amdgpu_buffer_rsrc_t rcs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(cs), (short)0, (pos + 1) * half * 8, kRsrcWord3);
+  const v2i csw = __builtin_amdgcn_raw_buffer_load_b64(
+      rcs, (pos * half + max(0, min(lane & (kHDf / 2 - 1), half - 1))) * 8, 0, 0);
+  const float2 csv = make_float2(__int_as_float(csw.x), __int_as_float(csw.y));
+  const uint16_t graw = qkvg[nh * kHDf + 2 * kvd + hq];
+  // K, V blocks of split J: lane l loads 16 B (chunk l%8) of rows 8i + l/8
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kc, (short)0, pos * kvd * 2, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vc, (short)0, pos * kvd * 2, kRsrcWord3);
+  const int lr = lane >> 3, lc = lane & 7;
+  v4i kr[8], vr[8];
+#define PQ_LOAD_BLOCKS(J)                                                                              \
+  {                                                                                                    \
+    const int off_ = (((J) * kSplitF + lr) * kvd + g * kHDf) * 2 + lc * 16;                          \
+    _Pragma("unroll") for (int i = 0; i < 8; i++) kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off_ + i * 8 * kvd * 2, 0, 0); \
+    _Pragma("unroll") for (int i = 0; i < 8; i++) vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off_ + i * 8 * kvd * 2, 0, 0); \
   }
-  __syncthreads();
+  PQ_LOAD_BLOCKS(wave)
+  // 1. q/k norm + rope, KV write
+  const float x1 = bf2f(xraw);
+  if (wave == 0) {
+    qs[lane] = qk_norm_rope(x1, wd, csv, rot, eps, lane);
+  } else if (wave == 1) {
+    const uint16_t k = f2h(qk_norm_rope(x1, wd, csv, rot, eps, lane));
+    if (writer) kc[(size_t)pos * kvd + g * kHDf + lane] = k;
+    kvnew[lane] = k;
+  } else if (wave == 2) {
+    const uint16_t v = f2h(x1);
+    if (writer) vc[(size_t)pos * kvd + g * kHDf + lane] = v;
+    kvnew[kHDf + lane] = v;
+  }
+  lds_barrier();
   // 2. splits
+  float *eww = ew + wave * kSplitF;
+  uint16_t *bw = blk + wave * kSplitF * kVRow;
   for (int j = wave; j < ns; j += 8) {
+    if (j != wave) PQ_LOAD_BLOCKS(j)
     const int p0 = j * kSplitF;
     const int pn = npos - p0 < kSplitF ? npos - p0 : kSplitF;
     const bool valid = lane < pn;
-    float dot[G];
+    // K block -> LDS -> lane p's row (the row at pos from kvnew)
 #pragma unroll
-    for (int h = 0; h < G; h++) dot[h] = 0.0f;
-    if (valid) {
-      const uint16_t *kr = kc + (size_t)(p0 + lane) * kvd + g * kHDf;
-      uint4 k8[8];
+    for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = kr[i];
+    const uint16_t *krow = p0 + lane == pos ? kvnew : bw + lane * kVRow;
+    float kf[kHDf];
 #pragma unroll
-      for (int q = 0; q < 8; q++) k8[q] = *reinterpret_cast<const uint4 *>(kr + 8 * q);
+    for (int q = 0; q < 8; q++) {
+      const v4i w4 = *reinterpret_cast<const v4i *>(krow + 8 * q);
+      const uint32_t kw[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
 #pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const uint32_t kw[4] = {k8[q].x, k8[q].y, k8[q].z, k8[q].w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float kf = h2f((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
-#pragma unroll
-          for (int h = 0; h < G; h++) dot[h] = __builtin_fmaf(qs[h * kHDf + 8 * q + i], kf, dot[h]);
-        }
-      }
+      for (int i = 0; i < 8; i++) kf[8 * q + i] = h2f((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
     }
-    float m[G], l[G];
-    float *ew = es + wave * G * kSplitF;
+    float4 q4[kHDf / 4];
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-      const float s = valid ? dot[h] * scale : -__builtin_inff();
-      m[h] = wave_max(s);
-      const float e = valid ? expf_pq(s - m[h]) : 0.0f;
-      l[h] = wave_pairwise_sum(e);
-      ew[h * kSplitF + lane] = e;
+    for (int i = 0; i < kHDf / 4; i++) q4[i] = reinterpret_cast<const float4 *>(qs)[i];
+    float d = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kHDf / 4; i++) {
+      d = __builtin_fmaf(q4[i].x, kf[4 * i], d);
+      d = __builtin_fmaf(q4[i].y, kf[4 * i + 1], d);
+      d = __builtin_fmaf(q4[i].z, kf[4 * i + 2], d);
+      d = __builtin_fmaf(q4[i].w, kf[4 * i + 3], d);
     }
-    __builtin_amdgcn_wave_barrier();
+    const float sc = valid ? d * scale : -__builtin_inff();
+    const float m = wave_max(sc);
+    const float e = valid ? expf_pq(sc - m) : 0.0f;
+    const float l = wave_pairwise_sum(e);
+    eww[lane] = e;
+    // V block -> the same LDS buffer (this wave's K reads precede it in LDS
+    // order); the row at pos from kvnew
+#pragma unroll
+    for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = vr[i];
+    if (pos - p0 < kSplitF && lane < 8)
+      *reinterpret_cast<v4i *>(bw + (pos - p0) * kVRow + lane * 8) = reinterpret_cast<const v4i *>(kvnew + kHDf)[lane];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    float o[G];
+    __builtin_amdgcn_wave_barrier();
+    // o = sum_p e[p] v[p][lane] (fmaf chain over p < pn), 16 positions per batch
+    float o = 0.0f;
+    for (int b0 = 0; b0 < pn; b0 += 16) {
+      float v[16];
 #pragma unroll
-    for (int h = 0; h < G; h++) o[h] = 0.0f;
-    const uint16_t *vcol = vc + (size_t)p0 * kvd + g * kHDf + lane;
-    for (int p = 0; p < pn; p += 8) {
-      float v[8];
+      for (int i = 0; i < 16; i++) v[i] = h2f(bw[(b0 + i) * kVRow + lane]);
+      float4 e4[4];
 #pragma unroll
-      for (int i = 0; i < 8; i++) v[i] = p + i < pn ? h2f(vcol[(size_t)(p + i) * kvd]) : 0.0f;
+      for (int k = 0; k < 4; k++) e4[k] = reinterpret_cast<const float4 *>(eww + b0)[k];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 8; i++)
-        if (p + i < pn) {
-#pragma unroll
-          for (int h = 0; h < G; h++) o[h] = __builtin_fmaf(ew[h * kSplitF + p + i], v[i], o[h]);
+      for (int i = 0; i < 16; i++)
+        if (b0 + i < pn) {
+          const float4 &q = e4[i >> 2];
+          const float ei = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+          o = __builtin_fmaf(ei, v[i], o);
         }
     }
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      float *sj = st + ((size_t)j * G + h) * kPartf;
-      sj[lane] = o[h];
-      if (lane == 0) {
-        sj[kHDf] = m[h];
-        sj[kHDf + 1] = l[h];
-      }
+    float *sj = st + (size_t)j * kPartf;
+    sj[lane] = o;
+    if (lane == 0) {
+      sj[kHDf] = m;
+      sj[kHDf + 1] = l;
     }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
-  __syncthreads();
+#undef PQ_LOAD_BLOCKS
+  lds_barrier();
   // 3. merge, gate, Q8_0 out
-  for (int hw = wave; hw < G; hw += 8) {
-    const int hq = g * G + hw;
+  if (wave == 0) {
+    // M = max m_j; w_j = e^(m_j - M) for 64 splits at a time, one per lane;
+    // then L and O as fmaf chains over j ascending (w_j, l_j by v_readlane)
     float M = -__builtin_inff();
-    for (int j = 0; j < ns; j++) M = fmaxf(M, st[((size_t)j * G + hw) * kPartf + kHDf]);
+    for (int j0 = 0; j0 < ns; j0 += 64)
+      M = fmaxf(M, wave_max(j0 + lane < ns ? st[(size_t)(j0 + lane) * kPartf + kHDf] : -__builtin_inff()));
     float L = 0.0f, O = 0.0f;
-    for (int j = 0; j < ns; j++) {
-      const float *sj = st + ((size_t)j * G + hw) * kPartf;
-      const float w = expf_pq(sj[kHDf] - M);
-      L = __builtin_fmaf(sj[kHDf + 1], w, L);
-      O = __builtin_fmaf(sj[lane], w, O);
+    for (int j0 = 0; j0 < ns; j0 += 64) {
+      const int jl = j0 + lane < ns ? j0 + lane : ns - 1;
+      const float w = expf_pq(st[(size_t)jl * kPartf + kHDf] - M);
+      const float lj = st[(size_t)jl * kPartf + kHDf + 1];
+      const int n = ns - j0 < 64 ? ns - j0 : 64;
+      for (int b = 0; b < n; b += 8) {
+        float oj[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) oj[i] = st[(size_t)(j0 + (b + i < n ? b + i : 0)) * kPartf + lane];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          if (b + i < n) {
+            const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b + i));
+            L = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj), b + i)), wi, L);
+            O = __builtin_fmaf(oj[i], wi, O);
+          }
+      }
     }
     uint16_t rb = f2bf(O / L);
-    const float gs = 1.0f / (1.0f + expf_pq(-bf2f(qkvg[nh * kHDf + 2 * kvd + hq])));
+    const float gs = 1.0f / (1.0f + expf_pq(-bf2f(graw)));
     rb = f2bf(bf2f(rb) * gs);
     if (out != nullptr) out[hq * kHDf + lane] = rb;
     const float v = bf2f(rb);
@@ -539,43 +625,48 @@ extern "C" int pq_q8_gemv_parts(int N, int K) {
   return ntiles(N) * (64 / gemv_shape(N, K).R);
 }
 
-extern "C" int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro, void *y,
-                                int y_dtype, int N, int K, float *argmax_parts, void *stream) {
-  PQ_REQUIRE(pcodes && pscales && pro && y, PQ_ERR_ARG, "pq_q8_gemv_fused: null pointer");
+// Argument checks shared by the fused GEMV entry points (out: y or qx).
+static int check_fused_args(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
+                            const void *out, int N, int K, const char *who) {
+  PQ_REQUIRE(pcodes && pscales && pro && out, PQ_ERR_ARG, "%s: null pointer", who);
   PQ_REQUIRE(N > 0 && K >= 1024 && K <= 8192 && (K & (K - 1)) == 0, PQ_ERR_ARG,
-             "pq_q8_gemv_fused: N=%d K=%d (K a power of two, 1024..8192)", N, K);
-  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemv_fused: y_dtype %d", y_dtype);
-  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16), PQ_ERR_ALIGN, "pq_q8_gemv_fused: packed weights alignment");
+             "%s: N=%d K=%d (K a power of two, 1024..8192)", who, N, K);
+  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16), PQ_ERR_ALIGN, "%s: packed weights alignment", who);
   const pq_gemv_prologue &p = *pro;
   switch (p.kind) {
     case PQ_PRO_Q8:
-      PQ_REQUIRE(p.qx && p.dx && aligned(p.qx, 16), PQ_ERR_ARG, "pq_q8_gemv_fused: Q8 prologue needs aligned qx, dx");
+      PQ_REQUIRE(p.qx && p.dx && aligned(p.qx, 16), PQ_ERR_ARG, "%s: Q8 prologue needs aligned qx, dx", who);
       break;
     case PQ_PRO_RESNORM:
       PQ_REQUIRE(p.h && p.x_in && p.x_out && p.w0 && p.w1 && p.x_in != p.x_out, PQ_ERR_ARG,
-                 "pq_q8_gemv_fused: RESNORM needs h, x_in, x_out (distinct), w0, w1");
+                 "%s: RESNORM needs h, x_in, x_out (distinct), w0, w1", who);
       break;
     case PQ_PRO_NORM:
-      PQ_REQUIRE(p.x_in && p.w0, PQ_ERR_ARG, "pq_q8_gemv_fused: NORM needs x_in, w0");
+      PQ_REQUIRE(p.x_in && p.w0, PQ_ERR_ARG, "%s: NORM needs x_in, w0", who);
       break;
     case PQ_PRO_EMBED:
       PQ_REQUIRE(p.tok && p.emb_pc && p.emb_ps && p.x_out && p.w0 && p.vocab > 0, PQ_ERR_ARG,
-                 "pq_q8_gemv_fused: EMBED needs tok, the table, x_out, w0");
+                 "%s: EMBED needs tok, the table, x_out, w0", who);
       break;
     case PQ_PRO_SILU:
-      PQ_REQUIRE(p.gu, PQ_ERR_ARG, "pq_q8_gemv_fused: SILU needs gu");
+      PQ_REQUIRE(p.gu, PQ_ERR_ARG, "%s: SILU needs gu", who);
       break;
     case PQ_PRO_CONV:
       PQ_REQUIRE(p.bcx && p.ring_in && p.ring_out && p.taps && p.ring_in != p.ring_out &&
                      p.ntaps == kFusedTaps && aligned(p.taps, 16),
-                 PQ_ERR_ARG, "pq_q8_gemv_fused: CONV needs bcx, taps, distinct ring_in / ring_out, ntaps 3");
+                 PQ_ERR_ARG, "%s: CONV needs bcx, taps, distinct ring_in / ring_out, ntaps 3", who);
       break;
     default:
-      return fail(PQ_ERR_ARG, "pq_q8_gemv_fused: prologue kind %d", p.kind);
+      return fail(PQ_ERR_ARG, "%s: prologue kind %d", who, p.kind);
   }
-  const GemvShape g = gemv_shape(N, K);
+  return PQ_OK;
+}
+
+// 256 or 512 threads: the prologue spreads K over them, E = K/(64W) in 4..16.
+static int launch_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue &p, void *y, int yb,
+                        int N, int K, float *parts, int8_t *qo, float *dqo, GemvShape g, hipStream_t st,
+                        const char *who) {
   const int C = 64 / g.R;
-  // 256 or 512 threads: the prologue spreads K over them, E = K/(64W) <= 16 each
   int W = g.W >= 8 ? 8 : 4;
   if (K / (64 * W) < 4) W = 4;   // K = 1024
   if (K / (64 * W) > 16) W = 8;  // K = 8192
@@ -583,10 +674,8 @@ extern "C" int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, c
   const int nch = nchunks(K), nb = K / kQ;
   const size_t lds = (size_t)W * 64 * 4 + (size_t)nch * kXStride + (size_t)nb * 4;
   const dim3 grid((unsigned)(ntiles(N) * C)), block(64 * W);
-  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
-  hipStream_t st = as_stream(stream);
 #define PQ_FUSED_E(RR, PP, EE) \
-  launch(q8_gemv_fused_kernel<RR, PP, EE>, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, argmax_parts)
+  launch(q8_gemv_fused_kernel<RR, PP, EE>, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo)
 #define PQ_FUSED_R(RR, PP)                          \
   switch (E) {                                      \
     case 4: PQ_FUSED_E(RR, PP, 4); break;           \
@@ -611,7 +700,30 @@ extern "C" int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, c
 #undef PQ_FUSED
 #undef PQ_FUSED_R
 #undef PQ_FUSED_E
-  return check_launch("pq_q8_gemv_fused");
+  return check_launch(who);
+}
+
+extern "C" int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro, void *y,
+                                int y_dtype, int N, int K, float *argmax_parts, void *stream) {
+  const int rc = check_fused_args(pcodes, pscales, pro, y, N, K, "pq_q8_gemv_fused");
+  if (rc) return rc;
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemv_fused: y_dtype %d", y_dtype);
+  const pq_gemv_prologue &p = *pro;
+  return launch_fused(pcodes, pscales, p, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, argmax_parts, nullptr, nullptr,
+                      gemv_shape(N, K), as_stream(stream), "pq_q8_gemv_fused");
+}
+
+extern "C" int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
+                                       int8_t *qx, float *dx, int F, int K, void *stream) {
+  PQ_REQUIRE(pro && qx && dx, PQ_ERR_ARG, "pq_q8_gemv_fused_swiglu: null pointer");
+  PQ_REQUIRE(F > 0 && F % 32 == 0, PQ_ERR_ARG, "pq_q8_gemv_fused_swiglu: F=%d (a multiple of 32)", F);
+  PQ_REQUIRE(aligned(dx, 4), PQ_ERR_ALIGN, "pq_q8_gemv_fused_swiglu: dx alignment");
+  const int rc = check_fused_args(pcodes, pscales, pro, qx, 2 * F, K, "pq_q8_gemv_fused_swiglu");
+  if (rc) return rc;
+  const int nch = nchunks(K);
+  const GemvShape g{64, nch < 8 ? nch : 8};
+  return launch_fused(pcodes, pscales, *pro, nullptr, 0, 2 * F, K, nullptr, qx, dx, g, as_stream(stream),
+                      "pq_q8_gemv_fused_swiglu");
 }
 
 extern "C" int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream) {
@@ -631,15 +743,11 @@ extern "C" int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, c
   PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "pq_attn_layer_decode: cache alignment");
   const int G = nh / nkv;
   const int ns = (pos + 1 + kSplitF - 1) / kSplitF;
-  const size_t lds = ((size_t)G * kHDf + 8 * (size_t)G * kSplitF + (size_t)ns * G * kPartf) * 4;
-  PQ_REQUIRE(lds <= 65536, PQ_ERR_ARG, "pq_attn_layer_decode: position %d needs %zu B of LDS", pos, lds);
-  hipStream_t st = as_stream(stream);
-  const dim3 grid(nkv), block(512);
-  switch (G) {
-    case 1: launch(attn_layer_kernel<1>, grid, block, lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nh, nkv, rot, eps, scale, out, qx, dx); break;
-    case 2: launch(attn_layer_kernel<2>, grid, block, lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nh, nkv, rot, eps, scale, out, qx, dx); break;
-    case 4: launch(attn_layer_kernel<4>, grid, block, lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nh, nkv, rot, eps, scale, out, qx, dx); break;
-    default: return fail(PQ_ERR_ARG, "pq_attn_layer_decode: %d q heads per kv head (1, 2 or 4)", G);
-  }
+  const size_t lds = ((size_t)kHDf + 8 * (size_t)kSplitF + (size_t)ns * kPartf) * 4 +
+                     (2 * (size_t)kHDf + 8 * (size_t)kSplitF * kVRow) * 2;
+  PQ_REQUIRE(G == 1 || G == 2 || G == 4, PQ_ERR_ARG, "pq_attn_layer_decode: %d q heads per kv head (1, 2 or 4)", G);
+  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_attn_layer_decode: position %d needs %zu B of LDS", pos, lds);
+  launch(attn_head_kernel, dim3(nh), dim3(512), lds, as_stream(stream), qkvg, q_norm, k_norm, rope_cs, kcache, vcache,
+         pos, nh, nkv, rot, eps, scale, out, qx, dx);
   return check_launch("pq_attn_layer_decode");
 }

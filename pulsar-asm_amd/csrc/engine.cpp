@@ -32,6 +32,7 @@ struct Q8Dev {
   int8_t *pc = nullptr;
   uint16_t *ps = nullptr;
   int N = 0, K = 0;
+  bool gate_up = false;  // packed by pq_q8_pack_gate_up (rows interleaved in groups of 32)
 };
 
 struct LayerDev {
@@ -128,6 +129,7 @@ static int create(Engine &E, const pq_model_cfg &c) {
       PQ_TRY(E.dalloc(&D.rings[1], (size_t)H * c.ntaps));
     }
     PQ_TRY(alloc_q8(E, D.ug, 2 * F, H));
+    D.ug.gate_up = true;
     PQ_TRY(alloc_q8(E, D.down, H, F));
     PQ_TRY(E.dalloc(&D.op_norm, H));
     PQ_TRY(E.dalloc(&D.post_op_norm, H));
@@ -173,7 +175,9 @@ static int upload_q8(Engine &E, Q8Dev &q, const int8_t *codes, const uint16_t *s
   if (hipMemcpyAsync(dc, codes, nc, hipMemcpyHostToDevice, E.st) != hipSuccess ||
       hipMemcpyAsync(ds, scales, ns * 2, hipMemcpyHostToDevice, E.st) != hipSuccess)
     rc = fail(PQ_ERR_LAUNCH, "weight upload failed");
-  if (rc == PQ_OK) rc = pq_q8_pack(dc, ds, q.N, q.K, q.pc, q.ps, E.st);
+  if (rc == PQ_OK)
+    rc = q.gate_up ? pq_q8_pack_gate_up(dc, ds, q.N / 2, q.K, q.pc, q.ps, E.st)
+                   : pq_q8_pack(dc, ds, q.N, q.K, q.pc, q.ps, E.st);
   if (hipStreamSynchronize(E.st) != hipSuccess && rc == PQ_OK) rc = fail(PQ_ERR_LAUNCH, "weight pack failed");
   hipFree(dc);
   hipFree(ds);
@@ -338,7 +342,7 @@ static int forward(Engine &E, int T, int32_t *next) {
     }
     PQ_TRY(pq_rmsnorm(E.X, E.Hb, D.post_op_norm, D.ffn_norm, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
     PQ_TRY(gemv_or_gemm(E, D.ug, E.Wd, T));
-    PQ_TRY(pq_silu_mul(E.Wd, nullptr, E.qx, E.dx, F, T, E.st));
+    PQ_TRY(pq_silu_mul_interleaved(E.Wd, nullptr, E.qx, E.dx, F, T, E.st));
     PQ_TRY(gemv_or_gemm(E, D.down, E.Hb, T));
     const float *next_norm = l + 1 < c.nlayers ? E.L[l + 1].op_norm : E.final_norm;
     PQ_TRY(pq_rmsnorm(E.X, E.Hb, D.post_ffn_norm, next_norm, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
@@ -368,7 +372,8 @@ static bool fused_supported(const pq_model_cfg &c, const char **why) {
     const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
     const size_t ns = ((size_t)c.ctx + 63) / 64;
     if (c.hd != 64 || (G != 1 && G != 2 && G != 4)) *why = "the fused attention mixer takes head_dim 64, GQA group 1, 2 or 4";
-    else if (((size_t)G * 64 + 8 * (size_t)G * 64 + ns * G * 66) * 4 > 65536) *why = "context too long for the fused attention mixer";
+    else if ((64 + 8 * 64 + ns * 66) * 4 + (2 * 64 + 8 * 64 * 72) * 2 > 160 * 1024)
+      *why = "context too long for the fused attention mixer";
   }
   return *why == nullptr;
 }
@@ -432,10 +437,11 @@ static int forward_decode(Engine &E) {
     }
     PQ_TRY(gemv(D.out, E.Hb, PQ_DTYPE_BF16, nullptr));
     resnorm(D.post_op_norm, D.ffn_norm);
-    PQ_TRY(gemv(D.ug, E.Wd, PQ_DTYPE_BF16, nullptr));
+    PQ_TRY(pq_q8_gemv_fused_swiglu(D.ug.pc, D.ug.ps, &p, E.qx, E.dx, c.ffn, H, E.st));
     p = pq_gemv_prologue{};
-    p.kind = PQ_PRO_SILU;
-    p.gu = E.Wd;
+    p.kind = PQ_PRO_Q8;
+    p.qx = E.qx;
+    p.dx = E.dx;
     PQ_TRY(gemv(D.down, E.Hb, PQ_DTYPE_BF16, nullptr));
   }
   resnorm(E.L[c.nlayers - 1].post_ffn_norm, E.final_norm);

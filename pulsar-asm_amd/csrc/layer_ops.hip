@@ -194,12 +194,16 @@ __global__ __launch_bounds__(256) void conv_kernel(uint16_t *__restrict__ ring, 
 // Rows of the fused gate/up GEMV output: gate = row[0:F], up = row[F:2F].
 // One workgroup of F/E threads per position; E consecutive elements per
 // thread so the Q8_0 output can be formed in the same pass.
-template <int E>
+// IL: the row holds the gate/up pair interleaved in groups of 32 (the output
+// of weights packed by pq_q8_pack_gate_up): gate element i at 64*(i/32) + i%32,
+// up element i 32 further.
+template <int E, bool IL>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, uint16_t *__restrict__ y,
                                                         int8_t *__restrict__ qx, float *__restrict__ dx, int F) {
   const size_t t = blockIdx.y;
   const int e0 = (blockIdx.x * blockDim.x + threadIdx.x) * E;
-  const uint16_t *g = gu + t * 2 * F, *u = g + F;
+  const uint16_t *g = gu + t * 2 * F + (IL ? 32 * (e0 / 32) : 0);
+  const uint16_t *u = IL ? g + 32 : g + F;
   float o[E];
 #pragma unroll
   for (int i = 0; i < E; i++) {
@@ -324,13 +328,26 @@ extern "C" int pq_conv(uint16_t *ring, const float *taps, const uint16_t *bcx, u
   return check_launch("pq_conv");
 }
 
-extern "C" int pq_silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T, void *stream) {
-  PQ_REQUIRE(gu && (y || qx) && (!qx || dx), PQ_ERR_ARG, "pq_silu_mul: null pointer");
-  PQ_REQUIRE(F > 0 && F % 256 == 0 && T > 0, PQ_ERR_ARG, "pq_silu_mul: F=%d (a multiple of 256)", F);
+static int silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T, bool il, void *stream,
+                    const char *who) {
+  PQ_REQUIRE(gu && (y || qx) && (!qx || dx), PQ_ERR_ARG, "%s: null pointer", who);
+  PQ_REQUIRE(F > 0 && F % 256 == 0 && T > 0, PQ_ERR_ARG, "%s: F=%d (a multiple of 256)", who, F);
   constexpr int E = 8;
   const int threads = F / E < 256 ? F / E : 256;
-  launch(silu_mul_kernel<E>, dim3(F / E / threads, T), dim3(threads), 0, as_stream(stream), gu, y, qx, dx, F);
-  return check_launch("pq_silu_mul");
+  if (il)
+    launch(silu_mul_kernel<E, true>, dim3(F / E / threads, T), dim3(threads), 0, as_stream(stream), gu, y, qx, dx, F);
+  else
+    launch(silu_mul_kernel<E, false>, dim3(F / E / threads, T), dim3(threads), 0, as_stream(stream), gu, y, qx, dx, F);
+  return check_launch(who);
+}
+
+extern "C" int pq_silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T, void *stream) {
+  return silu_mul(gu, y, qx, dx, F, T, false, stream, "pq_silu_mul");
+}
+
+extern "C" int pq_silu_mul_interleaved(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T,
+                                       void *stream) {
+  return silu_mul(gu, y, qx, dx, F, T, true, stream, "pq_silu_mul_interleaved");
 }
 
 extern "C" int pq_argmax(const float *v, int n, int32_t *out, void *stream) {

@@ -54,18 +54,52 @@ __device__ __forceinline__ float expf_pq(float x) {
   return (p * fa) * fb;
 }
 
-// Wave64 xor-butterfly sum: after it every lane holds the pairwise (balanced
-// binary) sum of the 64 lanes' values in lane order -- the order the host
-// side writes as a recursive halving sum.
+// Wave64 xor-butterfly reductions. After step k every aligned group of 2^k
+// lanes holds the same value, so the partner of step k can be any lane of the
+// neighbouring group: steps 1-2 are DPP quad permutes (lane ^ 1, lane ^ 2),
+// steps 3-4 DPP half-row / row mirrors (lane i <-> 7-i, 15-i), steps 5-6 the
+// gfx950 permlane16/32 swaps. Every lane ends with the pairwise (balanced
+// binary) sum of the 64 lanes' values in lane order -- the order the host side
+// writes as a recursive halving sum. All 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// v + (the value of the other 16-lane row of the pair), rows uniform
+__device__ __forceinline__ float add_row_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_half_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_row_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_half_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float wave_pairwise_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
+  v = v + dpp_f<kDppXor1>(v);
+  v = v + dpp_f<kDppXor2>(v);
+  v = v + dpp_f<kDppHalfMirror>(v);
+  v = v + dpp_f<kDppMirror>(v);
+  v = add_row_pair(v);
+  return add_half_pair(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  v = max_row_pair(v);
+  return max_half_pair(v);
 }
 
 }  // namespace pq

@@ -55,8 +55,17 @@ __global__ __launch_bounds__(256) void q8_quant_kernel(const TX *__restrict__ x,
 
 // -------------------------------------------------------------------- packing
 // One thread per 16-byte slab piece (tile, b, h, r).
+// Source row of packed row `row`: itself, or with il = F > 0 the gate/up pair
+// interleave (packed rows 64t..64t+31 = gate rows 32t.., 64t+32.. = up rows
+// F+32t..).
+__device__ __forceinline__ long long src_row(long long row, int il) {
+  if (il == 0) return row;
+  const long long t = row / kTR, r = row % kTR;
+  return r < 32 ? 32 * t + r : il + 32 * t + (r - 32);
+}
+
 __global__ __launch_bounds__(256) void q8_pack_codes_kernel(const int8_t *__restrict__ codes, int8_t *__restrict__ pc,
-                                                             int N, int K, long long npieces) {
+                                                             int N, int K, long long npieces, int il) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= npieces) return;
   const int nb = K / kQ;
@@ -67,13 +76,13 @@ __global__ __launch_bounds__(256) void q8_pack_codes_kernel(const int8_t *__rest
   const long long tile = tb / nb;
   const long long row = tile * kTR + r;
   int4 v = make_int4(0, 0, 0, 0);
-  if (row < N) v = *reinterpret_cast<const int4 *>(codes + row * K + (long long)b * kQ + 16 * h);
+  if (row < N) v = *reinterpret_cast<const int4 *>(codes + src_row(row, il) * K + (long long)b * kQ + 16 * h);
   *reinterpret_cast<int4 *>(pc + i * 16) = v;
 }
 
 // One thread per (tile, chunk, row): its 8 scales.
 __global__ __launch_bounds__(256) void q8_pack_scales_kernel(const uint16_t *__restrict__ sc, uint16_t *__restrict__ ps,
-                                                              int N, int K, long long nitems) {
+                                                              int N, int K, long long nitems, int il) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nitems) return;
   const int nb = K / kQ, nch = nchunks(K);
@@ -86,7 +95,7 @@ __global__ __launch_bounds__(256) void q8_pack_scales_kernel(const uint16_t *__r
 #pragma unroll
   for (int k = 0; k < 8; k++) {
     const int b = c * kCB + k;
-    v[k] = (row < N && b < nb) ? sc[row * nb + b] : (uint16_t)0;
+    v[k] = (row < N && b < nb) ? sc[src_row(row, il) * nb + b] : (uint16_t)0;
   }
   uint4 o;
   o.x = v[0] | ((uint32_t)v[1] << 16);
@@ -304,21 +313,32 @@ extern "C" int pq_q8_quant_bf16(const uint16_t *x, int8_t *qx, float *dx, int K,
   return check_launch("pq_q8_quant_bf16");
 }
 
-extern "C" int pq_q8_pack(const int8_t *codes, const uint16_t *scales, int N, int K, int8_t *pcodes,
-                          uint16_t *pscales, void *stream) {
-  PQ_REQUIRE(codes && scales && pcodes && pscales, PQ_ERR_ARG, "pq_q8_pack: null pointer");
-  PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0, PQ_ERR_ARG, "pq_q8_pack: N=%d K=%d", N, K);
+static int pack(const int8_t *codes, const uint16_t *scales, int N, int K, int8_t *pcodes, uint16_t *pscales, int il,
+                void *stream, const char *who) {
+  PQ_REQUIRE(codes && scales && pcodes && pscales, PQ_ERR_ARG, "%s: null pointer", who);
+  PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0, PQ_ERR_ARG, "%s: N=%d K=%d", who, N, K);
   PQ_REQUIRE(aligned(codes, 16) && aligned(pcodes, 16) && aligned(pscales, 16), PQ_ERR_ALIGN,
-             "pq_q8_pack: codes and packed buffers must be 16-byte aligned");
+             "%s: codes and packed buffers must be 16-byte aligned", who);
   const long long npieces = (long long)ntiles(N) * (K / kQ) * 2 * kTR;
   launch(q8_pack_codes_kernel, dim3((unsigned)((npieces + 255) / 256)), dim3(256), 0, as_stream(stream),
-                     codes, pcodes, N, K, npieces);
-  int rc = check_launch("pq_q8_pack codes");
+                     codes, pcodes, N, K, npieces, il);
+  int rc = check_launch(who);
   if (rc) return rc;
   const long long nitems = (long long)ntiles(N) * nchunks(K) * kTR;
   launch(q8_pack_scales_kernel, dim3((unsigned)((nitems + 255) / 256)), dim3(256), 0, as_stream(stream),
-                     scales, pscales, N, K, nitems);
-  return check_launch("pq_q8_pack scales");
+                     scales, pscales, N, K, nitems, il);
+  return check_launch(who);
+}
+
+extern "C" int pq_q8_pack(const int8_t *codes, const uint16_t *scales, int N, int K, int8_t *pcodes,
+                          uint16_t *pscales, void *stream) {
+  return pack(codes, scales, N, K, pcodes, pscales, 0, stream, "pq_q8_pack");
+}
+
+extern "C" int pq_q8_pack_gate_up(const int8_t *codes, const uint16_t *scales, int F, int K, int8_t *pcodes,
+                                  uint16_t *pscales, void *stream) {
+  PQ_REQUIRE(F > 0 && F % 32 == 0, PQ_ERR_ARG, "pq_q8_pack_gate_up: F=%d (a multiple of 32)", F);
+  return pack(codes, scales, 2 * F, K, pcodes, pscales, F, stream, "pq_q8_pack_gate_up");
 }
 
 extern "C" int pq_q8_gemv(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,

@@ -15,6 +15,7 @@ constexpr int kTR = PQ_TILE_ROWS;       // 64 rows per tile
 constexpr int kSlab = 2 * kTR * 16;     // bytes per (tile, block): 2 halves x 64 rows x 16 B
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 __host__ __device__ inline int nchunks(int K) { return (K / kQ + kCB - 1) / kCB; }
@@ -43,6 +44,37 @@ __device__ __forceinline__ void load_chunk(ChunkRegs &R, const int8_t *__restric
         __builtin_nontemporal_load(reinterpret_cast<const v4i *>(slab0 + (size_t)i * kSlab + kTR * 16 + trow * 16));
   }
   const uint4 sv = *reinterpret_cast<const uint4 *>(sp8);
+  R.sw[0] = sv.x; R.sw[1] = sv.y; R.sw[2] = sv.z; R.sw[3] = sv.w;
+}
+
+// The same loads through buffer resources over one 64-row tile's codes and
+// scales. A slot without a chunk (c >= nch) reads at an offset past
+// num_records, which returns zeros without a memory access: every lane issues
+// the same loads with no branch, so the waits the compiler counts for loads
+// issued earlier stay exact.
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (32-bit data format)
+constexpr int kRsrcOob = 0x40000000;    // an offset past every tile's num_records
+constexpr int kAuxNT = 2;               // nontemporal cache policy
+struct TileRsrc {
+  __amdgpu_buffer_rsrc_t codes, scales;
+};
+__device__ __forceinline__ TileRsrc tile_rsrc(const int8_t *pc, const uint16_t *ps, int tile, int nb, int nch) {
+  TileRsrc t;
+  t.codes = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(pc + (size_t)tile * nb * kSlab), (short)0,
+                                              nb * kSlab, kRsrcWord3);
+  t.scales = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(ps + (size_t)tile * nch * kTR * 8), (short)0,
+                                               nch * kTR * 16, kRsrcWord3);
+  return t;
+}
+__device__ __forceinline__ void load_chunk_rsrc(ChunkRegs &R, const TileRsrc &t, int c, int nch, int trow) {
+  const int oc = c < nch ? c * kCB * kSlab + trow * 16 : kRsrcOob;
+  const int os = c < nch ? (c * kTR + trow) * 16 : kRsrcOob;
+#pragma unroll
+  for (int i = 0; i < kCB; i++) {
+    R.w[2 * i] = __builtin_amdgcn_raw_buffer_load_b128(t.codes, oc + i * kSlab, 0, kAuxNT);
+    R.w[2 * i + 1] = __builtin_amdgcn_raw_buffer_load_b128(t.codes, oc + i * kSlab + kTR * 16, 0, kAuxNT);
+  }
+  const v4i sv = __builtin_amdgcn_raw_buffer_load_b128(t.scales, os, 0, 0);
   R.sw[0] = sv.x; R.sw[1] = sv.y; R.sw[2] = sv.z; R.sw[3] = sv.w;
 }
 
@@ -91,7 +123,8 @@ __device__ __forceinline__ float tail_chunk(const int8_t *__restrict__ slab0, co
 }
 
 constexpr int kXStride = 256 + 16;    // LDS bytes per staged x chunk (the pad spreads chunks over banks)
-constexpr int kMaxStagedK = 32768;   // x staged in LDS only up to this K (35 KB)
+constexpr int kMaxStagedK = 32768;     // x staged in LDS only up to this K (35 KB)
+constexpr size_t kMaxLds = 160 * 1024;  // LDS one gfx950 workgroup may allocate
 
 
 // Decode GEMV launch shape: R rows per workgroup (64, or narrower slices when

@@ -34,6 +34,7 @@ SIGNATURES = {
     "pq_q8_packed_codes_bytes": (Z, [I, I]),
     "pq_q8_packed_scales_bytes": (Z, [I, I]),
     "pq_q8_pack": (I, [P, P, I, I, P, P, P]),
+    "pq_q8_pack_gate_up": (I, [P, P, I, I, P, P, P]),
     "pq_q8_gemv": (I, [P, P, P, P, P, I, I, I, P]),
     "pq_q8_gemm": (I, [P, P, P, P, P, I, I, I, I, P]),
     "pq_rmsnorm": (I, [P, P, P, P, P, P, P, I, I, F, P]),
@@ -42,11 +43,13 @@ SIGNATURES = {
     "pq_attn_decode": (I, [P, I, P, P, P, I, P, I, P, P, I, I, I, I, I, F, P, Z, P]),
     "pq_conv": (I, [P, P, P, P, I, I, I, P]),
     "pq_silu_mul": (I, [P, P, P, P, I, I, P]),
+    "pq_silu_mul_interleaved": (I, [P, P, P, P, I, I, P]),
     "pq_argmax": (I, [P, I, P, P]),
     "pq_embed": (I, [P, P, P, P, I, I, I, P]),
     "pq_q8_gemv_parts": (I, [I, I]),
     "pq_q8_gemv_fused": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, I, P, P]),
     "pq_argmax_parts": (I, [P, I, P, P]),
+    "pq_q8_gemv_fused_swiglu": (I, [P, P, C.POINTER(GemvPrologue), P, P, I, I, P]),
     "pq_attn_layer_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, F, F, P, P, P, P]),
     "pq_tq2_gemv": (I, [P, P, P, P, I, I, P]),
     "pq_q8k_quant": (I, [P, P, I, I, P]),

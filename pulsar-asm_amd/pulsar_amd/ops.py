@@ -10,6 +10,7 @@ from . import check, lib
 
 __all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "gemv_fused",
+           "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
            "PRO_CONV"]
 
@@ -28,9 +29,11 @@ def _ptr(t):
 
 
 class Q8Weight:
-    """A Q8_0 weight in the packed tile layout (from row-major codes/scales)."""
+    """A Q8_0 weight in the packed tile layout (from row-major codes/scales).
+    gate_up=True packs a stacked [gate; up] [2F][K] weight with its rows
+    interleaved in groups of 32 (pq_q8_pack_gate_up)."""
 
-    def __init__(self, codes, scales):
+    def __init__(self, codes, scales, gate_up=False):
         if codes.dtype != torch.int8 or codes.dim() != 2:
             raise ValueError("codes must be int8 [N][K]")
         N, K = codes.shape
@@ -45,8 +48,15 @@ class Q8Weight:
         self.pscales = torch.empty(L.pq_q8_packed_scales_bytes(N, K) // 2, dtype=torch.int16, device=dev)
         codes = codes.contiguous()
         scales = scales.contiguous()
-        check(L.pq_q8_pack(codes.data_ptr(), scales.data_ptr(), N, K, self.pcodes.data_ptr(),
-                           self.pscales.data_ptr(), stream_ptr()), "pq_q8_pack")
+        self.gate_up = gate_up
+        if gate_up:
+            if N % 64:
+                raise ValueError("gate_up weights need 2F rows with F a multiple of 32")
+            check(L.pq_q8_pack_gate_up(codes.data_ptr(), scales.data_ptr(), N // 2, K, self.pcodes.data_ptr(),
+                                       self.pscales.data_ptr(), stream_ptr()), "pq_q8_pack_gate_up")
+        else:
+            check(L.pq_q8_pack(codes.data_ptr(), scales.data_ptr(), N, K, self.pcodes.data_ptr(),
+                               self.pscales.data_ptr(), stream_ptr()), "pq_q8_pack")
 
     @property
     def nbytes(self):
@@ -139,12 +149,13 @@ def conv(ring, taps, bcx, out, H, T, ntaps):
           "pq_conv")
 
 
-def silu_mul(gu, F, T, out=True, quant=False):
+def silu_mul(gu, F, T, out=True, quant=False, interleaved=False):
     y = torch.empty((T, F), dtype=gu.dtype, device=gu.device) if out else None
     qx = torch.empty((T, F), dtype=torch.int8, device=gu.device) if quant else None
     dx = torch.empty((T, F // 32), dtype=torch.float32, device=gu.device) if quant else None
-    check(lib().pq_silu_mul(_bits16(gu), _bits16(y) if y is not None else None, _ptr(qx), _ptr(dx), F, T,
-                            stream_ptr()), "pq_silu_mul")
+    fn = "pq_silu_mul_interleaved" if interleaved else "pq_silu_mul"
+    check(getattr(lib(), fn)(_bits16(gu), _bits16(y) if y is not None else None, _ptr(qx), _ptr(dx), F, T,
+                             stream_ptr()), fn)
     return y, qx, dx
 
 
@@ -182,11 +193,7 @@ def tq2_gemv(codes, scales, xq, N, K, out=None):
 
 
 # ------------------------------------------------------- fused decode path
-def gemv_fused(w, kind, out_dtype=DT_BF16, out=None, parts=None, eps=1e-5, **ptrs):
-    """GEMV whose input x is produced by a prologue (pq_q8_gemv_fused). ptrs are
-    tensors for the pq_gemv_prologue fields (qx, dx, h, x_in, x_out, w0, w1, gu,
-    bcx, ring_in, ring_out, taps, emb (a Q8Weight), tok) plus ints ntaps, vocab."""
-    import ctypes as C
+def _prologue(kind, eps, ptrs):
     from ._abi import GemvPrologue
     p = GemvPrologue()
     p.kind = kind
@@ -198,11 +205,35 @@ def gemv_fused(w, kind, out_dtype=DT_BF16, out=None, parts=None, eps=1e-5, **ptr
             setattr(p, k, int(v))
         else:
             setattr(p, k, v.data_ptr())
+    return p
+
+
+def gemv_fused(w, kind, out_dtype=DT_BF16, out=None, parts=None, eps=1e-5, **ptrs):
+    """GEMV whose input x is produced by a prologue (pq_q8_gemv_fused). ptrs are
+    tensors for the pq_gemv_prologue fields (qx, dx, h, x_in, x_out, w0, w1, gu,
+    bcx, ring_in, ring_out, taps, emb (a Q8Weight), tok) plus ints ntaps, vocab."""
+    import ctypes as C
+    p = _prologue(kind, eps, ptrs)
     if out is None:
         out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=w.pcodes.device)
     check(lib().pq_q8_gemv_fused(w.pcodes.data_ptr(), w.pscales.data_ptr(), C.byref(p), out.data_ptr(), out_dtype,
                                  w.N, w.K, _ptr(parts), stream_ptr()), "pq_q8_gemv_fused")
     return out
+
+
+def gemv_fused_swiglu(w, kind, eps=1e-5, **ptrs):
+    """gate/up GEMV (w packed with gate_up=True) with prologue `kind` and the
+    silu(gate)*up epilogue: returns the Q8_0 row (qx int8 [F], dx fp32 [F/32])."""
+    import ctypes as C
+    if not getattr(w, "gate_up", False):
+        raise ValueError("gemv_fused_swiglu needs a Q8Weight packed with gate_up=True")
+    p = _prologue(kind, eps, ptrs)
+    F = w.N // 2
+    qx = torch.empty(F, dtype=torch.int8, device=w.pcodes.device)
+    dx = torch.empty(F // 32, dtype=torch.float32, device=w.pcodes.device)
+    check(lib().pq_q8_gemv_fused_swiglu(w.pcodes.data_ptr(), w.pscales.data_ptr(), C.byref(p), qx.data_ptr(),
+                                        dx.data_ptr(), F, w.K, stream_ptr()), "pq_q8_gemv_fused_swiglu")
+    return qx, dx
 
 
 def argmax_parts(parts, nparts):

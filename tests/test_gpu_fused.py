@@ -104,9 +104,10 @@ def test_q8_prologue(orc, pq, dev):
     assert torch.equal(y.view(torch.int16), pq.q8_gemv(w, qx, dx, out_dtype=pq.DT_BF16).view(torch.int16))
 
 
-@pytest.mark.parametrize("pos", [0, 63, 64, 300, 2047])
+@pytest.mark.parametrize("pos", [0, 63, 64, 300, 2047, 4500])
 def test_attn_layer_decode(orc, pq, dev, pos):
-    nh, nkv, hd, rot, ctx = 32, 8, 64, 32, 2048
+    nh, nkv, hd, rot = 32, 8, 64, 32
+    ctx = max(2048, pos + 1)
     nin = nh * hd + 2 * nkv * hd + nh
     kvd = nkv * hd
     row = orc.f2bf(orc.gen_normal(SEED + pos, nin) * 30)
@@ -153,3 +154,35 @@ def test_engine_fused_equals_unfused(orc, pq, dev):
     m = orc.Model(**{k: v for k, v in cfg.items()})
     assert np.array_equal(ids[0], m.greedy(prompt, 12))
     m.close()
+
+
+def test_gate_up_interleave_and_swiglu(orc, pq, dev):
+    """Interleaved gate/up packing: the GEMV returns the rows in 32-row groups,
+    silu_mul over that order equals the plain one, and the fused SwiGLU
+    epilogue gives the Q8_0 row of silu(gate)*up bit for bit."""
+    H, F = 2048, 8192
+    W, S = orc.q8_weights(SEED + 60, 2 * F, H)
+    w = pq.Q8Weight(torch.from_numpy(W).to(dev), torch.from_numpy(S.view(np.int16)).to(dev), gate_up=True)
+    x = orc.f2bf(orc.gen_normal(SEED + 61, H) * 5)
+    h = orc.f2bf(orc.gen_normal(SEED + 62, H) * 40)
+    w0 = orc.gen_affine(SEED + 63, H, 4.0, 0.4)
+    w1 = orc.gen_affine(SEED + 64, H, 1.0, 0.1)
+    xin = orc.rmsnorm(orc.add(x, orc.rmsnorm(h, w0)), w1)
+    qx, dx = orc.q8_quant_bf16(xin)
+    gu = orc.f2bf(orc.q8_gemv(W, S, qx, dx))                       # [gate | up], bf16
+    act = orc.silu_mul(gu[:F], gu[F:])
+    qa, da = orc.q8_quant_bf16(act)
+    # the GEMV over the interleaved packing
+    y = pq.q8_gemv(w, torch.from_numpy(qx).to(dev), torch.from_numpy(dx).to(dev), out_dtype=pq.DT_BF16)
+    yi = _u16(y).reshape(F // 32, 2, 32)
+    assert np.array_equal(yi[:, 0, :].reshape(-1), gu[:F]) and np.array_equal(yi[:, 1, :].reshape(-1), gu[F:])
+    # silu over the interleaved row
+    ys, q1, d1 = pq.silu_mul(y.view(torch.bfloat16), F, 1, out=True, quant=True, interleaved=True)
+    assert np.array_equal(_u16(ys).reshape(-1), act)
+    assert np.array_equal(q1.cpu().numpy().reshape(-1), qa) and np.array_equal(d1.cpu().numpy().reshape(-1), da)
+    # RESNORM prologue + SwiGLU epilogue in one launch
+    xo = torch.zeros(H, dtype=torch.int16, device=dev)
+    q2, d2 = pq.gemv_fused_swiglu(w, pq.PRO_RESNORM, h=_t16(h, dev), x_in=_t16(x, dev), x_out=xo,
+                                  w0=torch.from_numpy(w0).to(dev), w1=torch.from_numpy(w1).to(dev))
+    assert np.array_equal(q2.cpu().numpy(), qa)
+    assert np.array_equal(d2.cpu().numpy().view(np.uint32), da.view(np.uint32))
