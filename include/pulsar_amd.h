@@ -93,6 +93,15 @@ int pq_q8_gemv(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, 
  * (lfm3_nanode.cu:4840-4968) and the q8_partial_TL{b,f,g}/Tb/Tp kernels. */
 int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
                void *y, int y_dtype, int N, int K, int T, void *stream);
+/* The same with a workspace: when N is too small to fill the chip, K is split
+ * over workgroups that write each 256-wide chunk's partial to ws [nch][T][N]
+ * fp32, then a fold adds them in chunk order -- the same bits. ws_bytes from
+ * pq_q8_gemm_workspace_bytes (0: no split for this shape; ws may be NULL). The
+ * counterpart of the reference's chunked partials + k_combine_bf_T
+ * (lfm3_nanode.cu:4840-4968). */
+size_t pq_q8_gemm_workspace_bytes(int N, int K, int T);
+int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
+                  void *y, int y_dtype, int N, int K, int T, void *ws, size_t ws_bytes, void *stream);
 
 /* ======================================================= layer operations
  * bf16 activations are raw uint16 bits. T positions are rows of the given

@@ -28,15 +28,6 @@
 namespace pq {
 
 // --------------------------------------------------------- block helpers
-// Workgroup barrier over LDS only: waits for this wave's LDS operations, not for
-// its outstanding global loads, so weight loads issued before a prologue stay
-// in flight while the prologue runs.
-__device__ __forceinline__ void lds_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt left alone
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // E contiguous bf16 (E = 4, 8 or 16) as E/2 packed dwords, one 8- or 16-byte
 // vector load per 8 elements; lo/hi unpack to fp32.

@@ -66,6 +66,8 @@ struct Engine {
   int max_ids = 0;
   void *attn_ws = nullptr;
   size_t attn_ws_bytes = 0;
+  void *gemm_ws = nullptr;
+  size_t gemm_ws_bytes = 0;
   std::vector<void *> allocs;
   bool loaded = false;
 
@@ -158,6 +160,10 @@ static int create(Engine &E, const pq_model_cfg &c) {
   PQ_TRY(E.dalloc(&E.ids, (size_t)E.max_ids));
   E.attn_ws_bytes = pq_attn_workspace_bytes(c.nh, c.ctx, T);
   PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.attn_ws), E.attn_ws_bytes));
+  // the split-K GEMM workspace: the largest of the layer shapes at tmax positions
+  const int shapes[6][2] = {{E.nin, H}, {3 * H, H}, {H, E.qd}, {H, H}, {2 * F, H}, {H, F}};
+  for (const auto &nk : shapes) E.gemm_ws_bytes = std::max(E.gemm_ws_bytes, pq_q8_gemm_workspace_bytes(nk[0], nk[1], T));
+  if (E.gemm_ws_bytes) PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.gemm_ws), E.gemm_ws_bytes));
   return PQ_OK;
 }
 
@@ -313,7 +319,7 @@ static int reset(Engine &E) {
 // ---------------------------------------------------------------- forward
 static int gemv_or_gemm(Engine &E, const Q8Dev &w, void *y, int T) {
   if (T == 1) return pq_q8_gemv(w.pc, w.ps, E.qx, E.dx, y, PQ_DTYPE_BF16, w.N, w.K, E.st);
-  return pq_q8_gemm(w.pc, w.ps, E.qx, E.dx, y, PQ_DTYPE_BF16, w.N, w.K, T, E.st);
+  return pq_q8_gemm_ws(w.pc, w.ps, E.qx, E.dx, y, PQ_DTYPE_BF16, w.N, w.K, T, E.gemm_ws, E.gemm_ws_bytes, E.st);
 }
 
 // Runs T <= tmax positions whose token ids are in E.tok (device) through all

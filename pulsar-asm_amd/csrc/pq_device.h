@@ -102,4 +102,14 @@ __device__ __forceinline__ float wave_max(float v) {
   return max_half_pair(v);
 }
 
+// Workgroup barrier over LDS only: waits for this wave's LDS operations, not for
+// its outstanding global loads, so weight loads issued before a prologue stay
+// in flight while the prologue runs.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt left alone
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 }  // namespace pq

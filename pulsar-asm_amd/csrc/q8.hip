@@ -184,99 +184,323 @@ __global__ __launch_bounds__(512) void q8_gemv_kernel(const int8_t *__restrict__
 }
 
 // ------------------------------------------------------------ prefill GEMM
-// Workgroup = one 32-row half of a 64-row tile x 32 positions x all of K, W
-// waves. In round rd wave w takes R1 chunk c = rd*W + w: per block one
-// v_mfma_i32_32x32x32_i8 with A = activations (i = position) and B = weights
-// (j = row), so lane l holds D[i][j] for j = l % 32 and
+// Persistent workgroups of 8 waves. A work item is a group of 8 32-row slices
+// (256 rows) x one K split x one 32-position block; wave w of the workgroup
+// takes slice w of the group and walks the split's chunks in order, so each
+// output's chunk partials fold into y = y + a_c in registers -- no barrier
+// between waves. The activations of 8 chunks (2048 K) x 32 positions (64 KB)
+// and their dx sit in LDS, shared by the 8 waves; they are re-staged only when
+// the chunks or positions move out of them (with K <= 2048, one split and
+// T <= 32: once per workgroup). Each wave keeps the weights of its next two
+// chunks in flight -- across item boundaries -- while it computes one. Per
+// block one v_mfma_i32_32x32x32_i8 with A = activations (i = position) and B =
+// weights (j = row): lane l holds D[i][j] for j = l % 32 and
 // i = 8(r/4) + 4(l/32) + r%4 (r = 0..15), and folds its 16 outputs into the
-// chunk partial a = fmaf(fl(dw*dx), (float)isum, a). The round's partials go
-// to LDS and the workgroup adds them to y in chunk order (y = y + a_c), each
-// thread owning 1024/(64W) of the 32x32 outputs. dx of the round's chunks is
-// staged in LDS as [wave][block][position].
-template <int W>
-__global__ __launch_bounds__(64 * W) void q8_gemm_kernel(const int8_t *__restrict__ pc,
-                                                          const uint16_t *__restrict__ ps,
-                                                          const int8_t *__restrict__ qx, const float *__restrict__ dx,
-                                                          void *__restrict__ y, int y_bf16, int N, int K, int T) {
-  constexpr int EPT = 1024 / (64 * W);          // outputs folded per thread
-  __shared__ float part[W][16][64];
-  __shared__ __align__(16) float dxs[W][kCB][32];
+// chunk partial a = fmaf(fl(dw*dx), (float)isum, a).
+// Several K splits (small N): every chunk partial goes to the workspace
+// [nch][T][N] and q8_gemm_fold_kernel adds them in chunk order.
+// Weights and scales come through buffer resources (rows past N and absent
+// chunks read zeros, no branch).
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+constexpr int kGemmSegChunks = 8;                          // chunks of K staged at once
+constexpr int kGemmSegK = kGemmSegChunks * kCB * kQ;       // 2048
+constexpr int kGemmARow = kGemmSegK + 16;                  // padded LDS row (bytes)
+constexpr size_t kGemmLds = 32 * (size_t)kGemmARow + (size_t)kGemmSegChunks * kCB * 32 * 4;
+
+struct GemmW {
+  v4i w[kCB];
+  v4i s;
+};
+
+struct GemmCur {     // one chunk step of a wave: item it, 32-row slice, chunk c
+  int it, slice, c0, c1, p0, c;
+  bool ok;
+};
+
+__global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__restrict__ pc,
+                                                                const uint16_t *__restrict__ ps,
+                                                                const int8_t *__restrict__ qx,
+                                                                const float *__restrict__ dx, void *__restrict__ y,
+                                                                int y_bf16, int N, int K, int T,
+                                                                float *__restrict__ ws, int cps) {
+  extern __shared__ __align__(16) unsigned char gsm[];
+  int8_t(*as)[kGemmARow] = reinterpret_cast<int8_t(*)[kGemmARow]>(gsm);              // [32 positions]
+  float(*dxs)[32] = reinterpret_cast<float(*)[32]>(gsm + 32 * kGemmARow);            // [64 blocks][32]
   const int nb = K / kQ, nch = nchunks(K);
-  const int tile = blockIdx.x >> 1, sub = blockIdx.x & 1;
-  const int p0 = blockIdx.y * 32;
+  const int nsl = (N + 31) / 32, ngr = (nsl + kGemmWaves - 1) / kGemmWaves;
+  const int S = (nch + cps - 1) / cps;
+  const int nitems = ngr * S * ((T + 31) / 32);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int h = lane >> 5, l32 = lane & 31;
-  const int jrow = sub * 32 + l32;
-  const int apos = p0 + l32;
-  const bool aval = apos < T;
-  const int8_t *arow = qx + (size_t)(aval ? apos : 0) * K + 16 * h;
-  float yv[EPT];
-#pragma unroll
-  for (int k = 0; k < EPT; k++) yv[k] = 0.0f;
-  const int nrounds = (nch + W - 1) / W;
-  for (int rd = 0; rd < nrounds; rd++) {
-    const int c = rd * W + wave;
-    const int b0 = c * kCB;
-    const int nbc = c < nch ? (b0 + kCB <= nb ? kCB : nb - b0) : 0;
-    for (int i = lane; i < kCB * 32; i += 64) {
-      const int bi = i >> 5, p = i & 31, pos = p0 + p;
-      dxs[wave][bi][p] = (bi < nbc && pos < T) ? dx[(size_t)pos * nb + b0 + bi] : 0.0f;
+  if ((int)blockIdx.x >= nitems) return;
+  auto item = [&](int it, GemmCur &g) {
+    const int gr = it % ngr, s = (it / ngr) % S;
+    g.it = it;
+    g.slice = gr * kGemmWaves + wave;
+    g.p0 = (it / ngr / S) * 32;
+    g.c0 = s * cps;
+    g.c1 = min(nch, g.c0 + cps);
+    g.c = g.c0;
+  };
+  auto next = [&](GemmCur g) {
+    if (!g.ok) return g;
+    if (++g.c >= g.c1) {
+      const int it = g.it + (int)gridDim.x;
+      g.ok = it < nitems;
+      if (g.ok) item(it, g);
     }
-    __syncthreads();
+    return g;
+  };
+  auto wload = [&](GemmW &w, const GemmCur &g) {
+    const bool live = g.ok && g.slice < nsl;
+    const int tile = live ? g.slice >> 1 : 0;
+    const int jt = (g.slice & 1) * 32 + l32;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(pc + (size_t)tile * nb * kSlab), (short)0, live ? nb * kSlab : 0, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(ps + (size_t)tile * nch * kTR * 8), (short)0, live ? nch * kTR * 16 : 0, kRsrcWord3);
+    const int oc = g.c * kCB * kSlab + (h * kTR + jt) * 16;
+#pragma unroll
+    for (int i = 0; i < kCB; i++) w.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, oc + i * kSlab, 0, kAuxNT);
+    w.s = __builtin_amdgcn_raw_buffer_load_b128(rs, (g.c * kTR + jt) * 16, 0, 0);
+  };
+  GemmCur g0;
+  g0.ok = true;
+  item(blockIdx.x, g0);
+  GemmCur g1 = next(g0);
+  GemmW w0, w1;
+  wload(w0, g0);
+  wload(w1, g1);
+  int seg_k = -1, seg_c1 = 0, seg_p = -1;   // staged chunks [seg_k, min(seg_k + 8, seg_c1)), position block
+  float yv[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) yv[r] = 0.0f;
+  for (;;) {
+    const GemmCur g2 = next(g1);
+    GemmW w2;
+    wload(w2, g2);
+    const int c = g0.c;
+    // activations and dx: the 8 chunks from c of position block p0 (uniform:
+    // every wave of the workgroup walks the same chunk sequence)
+    if (seg_k < 0 || c < seg_k || c >= seg_k + kGemmSegChunks || c >= seg_c1 || g0.p0 != seg_p) {
+      if (seg_k >= 0) lds_barrier();   // every wave is done with the staged segment
+      seg_k = c;
+      seg_c1 = g0.c1;
+      seg_p = g0.p0;
+      const int np = T - seg_p < 32 ? T - seg_p : 32;
+      const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int8_t *>(qx + (size_t)seg_p * K), (short)0, np * K, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rdx = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float *>(dx + (size_t)seg_p * nb), (short)0, np * nb * 4, kRsrcWord3);
+      const int kb0 = seg_k * kCB * kQ;          // byte offset of the segment in a row
+      const int kend = min(K, min(g0.c1, seg_k + kGemmSegChunks) * kCB * kQ);   // the item's part of it
+      const int bend = kend / kQ;
+      const int t = threadIdx.x;
+      v4i av[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {              // 32 rows x 128 pieces of 16 B: thread t, pieces t + 512 i
+        const int pc16 = t + i * kGemmThreads;
+        const int p = pc16 >> 7, q = pc16 & 127;
+        av[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, kb0 + q * 16 < kend ? p * K + kb0 + q * 16 : kRsrcOob, 0, 0);
+      }
+      float dv[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {              // 32 positions x 64 blocks: thread t, entries t + 512 i
+        const int e = t + i * kGemmThreads;
+        const int p = e >> 6, b = seg_k * kCB + (e & 63);
+        dv[i] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rdx, b < bend ? (p * nb + b) * 4 : kRsrcOob, 0, 0));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int pc16 = t + i * kGemmThreads;
+        *reinterpret_cast<v4i *>(&as[pc16 >> 7][(pc16 & 127) * 16]) = av[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int e = t + i * kGemmThreads;
+        dxs[e & 63][e >> 6] = dv[i];
+      }
+      lds_barrier();
+    }
+    // chunk c of this wave's slice
     float a[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) a[r] = 0.0f;
-    if (nbc > 0) {
-      const uint4 sv = *reinterpret_cast<const uint4 *>(ps + (((size_t)tile * nch + c) * kTR + jrow) * 8);
-      const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
-      v4i bw[kCB], av[kCB];
+    {
+      const uint32_t sw[4] = {(uint32_t)w0.s.x, (uint32_t)w0.s.y, (uint32_t)w0.s.z, (uint32_t)w0.s.w};
 #pragma unroll
       for (int i = 0; i < kCB; i++) {
-        if (i < nbc) {
-          bw[i] = __builtin_nontemporal_load(
-              reinterpret_cast<const v4i *>(pc + ((size_t)tile * nb + b0 + i) * kSlab + (h * kTR + jrow) * 16));
-          av[i] = aval ? *reinterpret_cast<const v4i *>(arow + (size_t)(b0 + i) * kQ) : v4i{0, 0, 0, 0};
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kCB; i++) {
-        if (i < nbc) {
+        const int b = c * kCB + i;
+        if (b < nb) {
+          const int kb = b - seg_k * kCB;   // block within the staged segment
+          const v4i avv = *reinterpret_cast<const v4i *>(&as[l32][kb * kQ + 16 * h]);
           v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bw[i], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(avv, w0.w[i], acc, 0, 0, 0);
           const float dw = half_of(sw[i >> 1], i & 1);
 #pragma unroll
-          for (int g = 0; g < 4; g++) {
-            const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[wave][i][8 * g + 4 * h]);
-            const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+          for (int q = 0; q < 4; q++) {
+            const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[kb][8 * q + 4 * h]);
+            const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
-            for (int k = 0; k < 4; k++) a[4 * g + k] = __builtin_fmaf(dw * dv[k], (float)acc[4 * g + k], a[4 * g + k]);
+            for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)acc[4 * q + k], a[4 * q + k]);
           }
         }
       }
     }
+    const int row = g0.slice * 32 + l32;
+    if (ws == nullptr) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) part[wave][r][lane] = a[r];
-    __syncthreads();
-    const int nvalid = nch - rd * W < W ? nch - rd * W : W;
+      for (int r = 0; r < 16; r++) yv[r] = yv[r] + a[r];
+      if (c + 1 >= g0.c1) {   // the slice's last chunk: write y
 #pragma unroll
-    for (int k = 0; k < EPT; k++) {
-      const int e = threadIdx.x + k * 64 * W;
-      const int r = e >> 6, l = e & 63;
-      for (int w = 0; w < nvalid; w++) yv[k] = yv[k] + part[w][r][l];
+        for (int r = 0; r < 16; r++) {
+          const int pos = g0.p0 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (pos < T && row < N) {
+            if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)pos * N + row] = f2bf(yv[r]);
+            else reinterpret_cast<float *>(y)[(size_t)pos * N + row] = yv[r];
+          }
+          yv[r] = 0.0f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int pos = g0.p0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (pos < T && row < N) ws[((size_t)c * T + pos) * N + row] = a[r];
+      }
     }
-    __syncthreads();
+    if (!g1.ok) break;
+    g0 = g1;
+    g1 = g2;
+    w0 = w1;
+    w1 = w2;
+  }
+}
+
+// The tile-parallel form for mid-sized N (enough 64-row tiles to fill the
+// chip, too few 256-row groups for the walking form): workgroup = one 64-row
+// tile x 32 positions, 16 waves; wave w takes rows 32*(w&1).. and chunk
+// 8*rd + (w>>1) of round rd, so a round's 8 chunks load at once; the round's
+// activations (32 positions x 2048 K) and dx are staged in LDS and the 8 chunk
+// partials fold into y through LDS in chunk order. Same numerics.
+constexpr int kTileSlots = 8;
+constexpr int kTileThreads = 64 * 2 * kTileSlots;   // 1024
+constexpr size_t kTileLds = (size_t)kTileSlots * 2 * 16 * 64 * 4 + 32 * (size_t)kGemmARow + (size_t)kTileSlots * kCB * 32 * 4;
+
+__global__ __launch_bounds__(kTileThreads) void q8_gemm_tile_kernel(const int8_t *__restrict__ pc,
+                                                                     const uint16_t *__restrict__ ps,
+                                                                     const int8_t *__restrict__ qx,
+                                                                     const float *__restrict__ dx,
+                                                                     void *__restrict__ y, int y_bf16, int N, int K,
+                                                                     int T) {
+  extern __shared__ __align__(16) unsigned char gsm[];
+  float(*part)[2][16][64] = reinterpret_cast<float(*)[2][16][64]>(gsm);
+  int8_t(*as)[kGemmARow] = reinterpret_cast<int8_t(*)[kGemmARow]>(gsm + kTileSlots * 2 * 16 * 64 * 4);
+  float(*dxs)[32] = reinterpret_cast<float(*)[32]>(gsm + kTileSlots * 2 * 16 * 64 * 4 + 32 * kGemmARow);
+  const int nb = K / kQ, nch = nchunks(K);
+  const int tile = blockIdx.x, p0 = blockIdx.z * 32;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int sub = wave & 1, slot = wave >> 1;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int jt = sub * 32 + l32;
+  const int np = T - p0 < 32 ? T - p0 : 32;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t *>(pc + (size_t)tile * nb * kSlab), (short)0, nb * kSlab, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(ps + (size_t)tile * nch * kTR * 8), (short)0, nch * kTR * 16, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t *>(qx + (size_t)p0 * K), (short)0, np * K, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rdx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(dx + (size_t)p0 * nb), (short)0, np * nb * 4, kRsrcWord3);
+  const int nrounds = (nch + kTileSlots - 1) / kTileSlots;
+  float yv[2] = {0.0f, 0.0f};
+  for (int rd = 0; rd < nrounds; rd++) {
+    const int rbase = rd * kTileSlots;
+    const int c = rbase + slot;
+    const bool valid = c < nch;
+    const int t = threadIdx.x;
+    // the round's activations (thread t: position t/32, 64 bytes) and dx
+    // (blocks 2*(t%32), +1), then this wave's weights
+    v4i av[4];
+    const int oa = (t >> 5) * K + rbase * kCB * kQ + (t & 31) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      av[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, rbase * kCB * kQ + (t & 31) * 64 + 16 * i < K ? oa + 16 * i : kRsrcOob, 0, 0);
+    float dv[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int b = rbase * kCB + 2 * (t & 31) + i;
+      dv[i] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rdx, b < nb ? ((t >> 5) * nb + b) * 4 : kRsrcOob, 0, 0));
+    }
+    v4i wv[kCB];
+    const int oc = valid ? c * kCB * kSlab + (h * kTR + jt) * 16 : kRsrcOob;
+#pragma unroll
+    for (int i = 0; i < kCB; i++) wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, oc + i * kSlab, 0, kAuxNT);
+    const v4i sv = __builtin_amdgcn_raw_buffer_load_b128(rs, valid ? (c * kTR + jt) * 16 : kRsrcOob, 0, 0);
+    if (rd > 0) lds_barrier();   // the previous round's as / dxs / part reads are done
+#pragma unroll
+    for (int i = 0; i < 4; i++) *reinterpret_cast<v4i *>(&as[t >> 5][(t & 31) * 64 + 16 * i]) = av[i];
+#pragma unroll
+    for (int i = 0; i < 2; i++) dxs[2 * (t & 31) + i][t >> 5] = dv[i];
+    lds_barrier();
+    float a[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) a[r] = 0.0f;
+    if (valid) {
+      const uint32_t sw[4] = {(uint32_t)sv.x, (uint32_t)sv.y, (uint32_t)sv.z, (uint32_t)sv.w};
+#pragma unroll
+      for (int i = 0; i < kCB; i++) {
+        if (c * kCB + i < nb) {
+          const int kb = slot * kCB + i;
+          const v4i avv = *reinterpret_cast<const v4i *>(&as[l32][kb * kQ + 16 * h]);
+          v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(avv, wv[i], acc, 0, 0, 0);
+          const float dw = half_of(sw[i >> 1], i & 1);
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[kb][8 * q + 4 * h]);
+            const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)acc[4 * q + k], a[4 * q + k]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one MFMA result live at a time (register budget)
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) part[slot][sub][r][lane] = a[r];
+    lds_barrier();
+    const int n = nch - rbase < kTileSlots ? nch - rbase : kTileSlots;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int e = threadIdx.x + k * kTileThreads;
+      const int s2 = e >> 10, r = (e >> 6) & 15, l = e & 63;
+      for (int w = 0; w < n; w++) yv[k] = yv[k] + part[w][s2][r][l];
+    }
   }
 #pragma unroll
-  for (int k = 0; k < EPT; k++) {
-    const int e = threadIdx.x + k * 64 * W;
-    const int r = e >> 6, l = e & 63;
+  for (int k = 0; k < 2; k++) {
+    const int e = threadIdx.x + k * kTileThreads;
+    const int s2 = e >> 10, r = (e >> 6) & 15, l = e & 63;
     const int pos = p0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-    const int row = tile * kTR + sub * 32 + (l & 31);
+    const int row = tile * kTR + s2 * 32 + (l & 31);
     if (pos < T && row < N) {
       if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)pos * N + row] = f2bf(yv[k]);
       else reinterpret_cast<float *>(y)[(size_t)pos * N + row] = yv[k];
     }
   }
+}
+
+// y[pos][row] = sum over chunks of the workspace partials, chunk order, from 0.
+__global__ __launch_bounds__(256) void q8_gemm_fold_kernel(const float *__restrict__ ws, void *__restrict__ y,
+                                                            int y_bf16, long long TN, int nch) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= TN) return;
+  float v = 0.0f;
+  for (int c = 0; c < nch; c++) v = v + ws[(size_t)c * TN + i];
+  if (y_bf16) reinterpret_cast<uint16_t *>(y)[i] = f2bf(v);
+  else reinterpret_cast<float *>(y)[i] = v;
 }
 
 }  // namespace pq
@@ -363,23 +587,65 @@ extern "C" int pq_q8_gemv(const int8_t *pcodes, const uint16_t *pscales, const i
   return check_launch("pq_q8_gemv");
 }
 
-extern "C" int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,
-                          int y_dtype, int N, int K, int T, void *stream) {
+// K splits for the T-wide GEMM: with a workspace, enough 8-slice work items
+// to give every CU one.
+static int gemm_splits(int N, int K, int T, bool have_ws) {
+  const int nch = nchunks(K), tb = (T + 31) / 32;
+  const long long items = (long long)((N + 255) / 256) * tb;
+  int cps = nch;
+  if (have_ws)
+    while (cps > 1 && items * ((nch + cps - 1) / cps) < 256) cps = (cps + 1) / 2;
+  return cps;
+}
+
+static bool gemm_tile_form(int N, int T) {
+  const long long tb = (T + 31) / 32;
+  return (long long)ntiles(N) * tb >= 192 && (N + 255) / 256 * tb < 256;
+}
+
+extern "C" size_t pq_q8_gemm_workspace_bytes(int N, int K, int T) {
+  if (N <= 0 || K <= 0 || K % kQ || T <= 0) return 0;
+  if (gemm_tile_form(N, T)) return 0;
+  const int nch = nchunks(K);
+  return gemm_splits(N, K, T, true) < nch ? (size_t)nch * T * N * sizeof(float) : 0;
+}
+
+extern "C" int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,
+                             int y_dtype, int N, int K, int T, void *ws, size_t ws_bytes, void *stream) {
   PQ_REQUIRE(pcodes && pscales && qx && dx && y, PQ_ERR_ARG, "pq_q8_gemm: null pointer");
   PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0 && T > 0, PQ_ERR_ARG, "pq_q8_gemm: N=%d K=%d T=%d", N, K, T);
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemm: y_dtype %d", y_dtype);
   PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 16) && aligned(qx, 16) && aligned(dx, 4), PQ_ERR_ALIGN,
              "pq_q8_gemm: packed weights and qx must be 16-byte aligned");
+  PQ_REQUIRE((long long)T * K < (1ll << 31) && (long long)ntiles(N) * (K / kQ) * kSlab < (1ll << 31), PQ_ERR_ARG,
+             "pq_q8_gemm: N=%d K=%d T=%d too large", N, K, T);
   const int nch = nchunks(K);
-  const int W = nch >= 8 ? 8 : (nch >= 4 ? 4 : (nch >= 2 ? 2 : 1));
-  const dim3 grid((unsigned)(ntiles(N) * 2), (unsigned)((T + 31) / 32));
+  const size_t need = pq_q8_gemm_workspace_bytes(N, K, T);
+  const bool split = ws != nullptr && need > 0 && ws_bytes >= need;
+  const int cps = gemm_splits(N, K, T, split);
+  const int S = (nch + cps - 1) / cps;
+  const long long items = (long long)((N + 255) / 256) * S * ((T + 31) / 32);
+  PQ_REQUIRE(items < (1ll << 31), PQ_ERR_ARG, "pq_q8_gemm: N=%d T=%d too large", N, T);
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
   hipStream_t st = as_stream(stream);
-  switch (W) {
-    case 8: launch(q8_gemm_kernel<8>, grid, dim3(512), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
-    case 4: launch(q8_gemm_kernel<4>, grid, dim3(256), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
-    case 2: launch(q8_gemm_kernel<2>, grid, dim3(128), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
-    default: launch(q8_gemm_kernel<1>, grid, dim3(64), 0, st, pcodes, pscales, qx, dx, y, yb, N, K, T); break;
+  if (gemm_tile_form(N, T)) {
+    // enough 64-row tiles, too few 256-row groups: the tile-parallel form
+    launch(q8_gemm_tile_kernel, dim3((unsigned)ntiles(N), 1, (unsigned)((T + 31) / 32)), dim3(kTileThreads), kTileLds,
+           st, pcodes, pscales, qx, dx, y, yb, N, K, T);
+    return check_launch("pq_q8_gemm");
   }
-  return check_launch("pq_q8_gemm");
+  const unsigned grid = (unsigned)(items < 256 ? items : 256);   // one persistent workgroup per CU
+  launch(q8_gemm_kernel, dim3(grid), dim3(kGemmThreads), kGemmLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T,
+         split ? static_cast<float *>(ws) : nullptr, cps);
+  int rc = check_launch("pq_q8_gemm");
+  if (rc || !split) return rc;
+  const long long TN = (long long)T * N;
+  launch(q8_gemm_fold_kernel, dim3((unsigned)((TN + 255) / 256)), dim3(256), 0, st, static_cast<const float *>(ws), y,
+         yb, TN, nch);
+  return check_launch("pq_q8_gemm fold");
+}
+
+extern "C" int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,
+                          int y_dtype, int N, int K, int T, void *stream) {
+  return pq_q8_gemm_ws(pcodes, pscales, qx, dx, y, y_dtype, N, K, T, nullptr, 0, stream);
 }

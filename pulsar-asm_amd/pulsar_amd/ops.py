@@ -93,16 +93,21 @@ def q8_gemv(w, qx, dx, out_dtype=DT_F32, out=None):
     return out
 
 
-def q8_gemm(w, qx, dx, out_dtype=DT_F32, out=None):
-    """y [T][N] for T positions (position-first)."""
+def q8_gemm(w, qx, dx, out_dtype=DT_F32, out=None, split=True, ws=None):
+    """y [T][N] for T positions (position-first). split=True gives the kernel a
+    workspace (pq_q8_gemm_ws) so small-N shapes split K over workgroups."""
     T = qx.shape[0]
     if qx.shape[1] != w.K or dx.shape != (T, w.K // 32):
         raise ValueError("x does not match K")
     if out is None:
         out = torch.empty((T, w.N), dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16,
                           device=qx.device)
-    check(lib().pq_q8_gemm(w.pcodes.data_ptr(), w.pscales.data_ptr(), qx.data_ptr(), dx.data_ptr(),
-                           out.data_ptr(), out_dtype, w.N, w.K, T, stream_ptr()), "pq_q8_gemm")
+    nbytes = lib().pq_q8_gemm_workspace_bytes(w.N, w.K, T) if split else 0
+    if nbytes and (ws is None or ws.numel() * ws.element_size() < nbytes):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=qx.device)
+    check(lib().pq_q8_gemm_ws(w.pcodes.data_ptr(), w.pscales.data_ptr(), qx.data_ptr(), dx.data_ptr(),
+                              out.data_ptr(), out_dtype, w.N, w.K, T, _ptr(ws) if nbytes else None, nbytes,
+                              stream_ptr()), "pq_q8_gemm")
     return out
 
 

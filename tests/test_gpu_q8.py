@@ -122,6 +122,9 @@ def test_gemm_bitexact(orc, pq, dev, N, K, T):
     y = pq.q8_gemm(w, qx, dx).cpu().numpy()
     bad = np.argwhere(_bits(y) != _bits(y_r))
     assert bad.shape[0] == 0, f"{bad.shape[0]} cells differ, first {bad[:5].tolist()}"
+    # without a workspace (no K split) the same bits
+    y_ns = pq.q8_gemm(w, qx, dx, split=False).cpu().numpy()
+    assert np.array_equal(_bits(y_ns), _bits(y_r))
     # batched == per-position T=1 GEMVs (prefill_chunk_test's invariant)
     yb = pq.q8_gemm(w, qx, dx, out_dtype=pq.DT_BF16)
     for t in range(0, T, max(1, T // 4)):
