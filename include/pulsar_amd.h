@@ -301,6 +301,10 @@ int pq_engine_decode(void *engine, int n_steps, int32_t *ids);
  * taps, GQA group 1/2/4, the context's splits in LDS); set_fused(1) on another
  * configuration returns PQ_ERR_ARG. */
 int pq_engine_set_fused(void *engine, int on);
+/* Fused decode steps replay a captured HIP graph (1, the default; the position
+ * and the id slot live on the device) or launch kernel by kernel (0); both give
+ * the same bits. */
+int pq_engine_set_graph(void *engine, int on);
 int pq_engine_sync(void *engine);
 void *pq_engine_stream(void *engine);
 int pq_engine_position(void *engine);

@@ -24,6 +24,7 @@
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
+#include "pq_internal.h"
 
 namespace pq {
 
@@ -369,8 +370,11 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
 }
 
 // (value, index) partials -> the lowest index among the maxima.
+// With ctr (the engine's replayed decode step): also ids[ctr[0]++] = the id and
+// ctr[1]++ (the position).
 __global__ __launch_bounds__(1024) void argmax_parts_kernel(const float *__restrict__ parts, int n,
-                                                             int32_t *__restrict__ out) {
+                                                             int32_t *__restrict__ out, int32_t *__restrict__ ids,
+                                                             int32_t *__restrict__ ctr) {
   __shared__ float bv[16];
   __shared__ int bi[16];
   float best = -__builtin_inff();
@@ -392,7 +396,13 @@ __global__ __launch_bounds__(1024) void argmax_parts_kernel(const float *__restr
   if (threadIdx.x == 0) {
     for (int w = 1; w < (int)(blockDim.x >> 6); w++)
       if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
-    *out = idx == 0x7fffffff ? 0 : idx;
+    const int id = idx == 0x7fffffff ? 0 : idx;
+    *out = id;
+    if (ctr != nullptr) {
+      ids[ctr[0]] = id;
+      ctr[0] += 1;
+      ctr[1] += 1;
+    }
   }
 }
 
@@ -435,8 +445,9 @@ __device__ __forceinline__ float qk_norm_rope(float x, float wd, float2 csv, int
 
 __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restrict__ qkvg, const float *__restrict__ qn,
                                                          const float *__restrict__ kn, const float *__restrict__ cs,
-                                                         uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, int pos,
-                                                         int nh, int nkv, int rot, float eps, float scale,
+                                                         uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+                                                         int pos_arg, const int32_t *__restrict__ pos_dev, int nh,
+                                                         int nkv, int rot, float eps, float scale,
                                                          uint16_t *__restrict__ out, int8_t *__restrict__ qx,
                                                          float *__restrict__ dx) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -445,6 +456,7 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
   uint16_t *kvnew = reinterpret_cast<uint16_t *>(ew + 8 * kSplitF);  // [2][64] fp16 k, v at pos
   uint16_t *blk = kvnew + 2 * kHDf;                                // [8 waves][64][kVRow] K, then V
   float *st = reinterpret_cast<float *>(blk + 8 * kSplitF * kVRow);  // [nsplit][66]
+  const int pos = pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_arg;
   const int hq = blockIdx.x, G = nh / nkv, g = hq / G;
   const bool writer = hq % G == 0;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -719,26 +731,51 @@ extern "C" int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *psc
 
 extern "C" int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream) {
   PQ_REQUIRE(parts && out && nparts > 0, PQ_ERR_ARG, "pq_argmax_parts: nparts=%d", nparts);
-  launch(argmax_parts_kernel, dim3(1), dim3(1024), 0, as_stream(stream), parts, nparts, out);
+  launch(argmax_parts_kernel, dim3(1), dim3(1024), 0, as_stream(stream), parts, nparts, out, nullptr, nullptr);
   return check_launch("pq_argmax_parts");
 }
 
-extern "C" int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float *k_norm,
-                                    const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos, int nh, int nkv,
-                                    int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
-                                    void *stream) {
+namespace pq {
+int argmax_parts_step(const float *parts, int nparts, int32_t *out, int32_t *ids, int32_t *ctr, hipStream_t st) {
+  PQ_REQUIRE(parts && out && ids && ctr && nparts > 0, PQ_ERR_ARG, "argmax_parts_step: bad arguments");
+  launch(argmax_parts_kernel, dim3(1), dim3(1024), 0, st, parts, nparts, out, ids, ctr);
+  return check_launch("argmax_parts_step");
+}
+}  // namespace pq
+
+static int attn_layer(const uint16_t *qkvg, const float *q_norm, const float *k_norm, const float *rope_cs,
+                      uint16_t *kcache, uint16_t *vcache, int pos, const int32_t *pos_dev, int ctx, int nh, int nkv,
+                      int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx, hipStream_t st) {
   PQ_REQUIRE(qkvg && q_norm && k_norm && rope_cs && kcache && vcache && qx && dx, PQ_ERR_ARG,
              "pq_attn_layer_decode: null pointer");
   PQ_REQUIRE(hd == kHDf && nh > 0 && nkv > 0 && nh % nkv == 0 && pos >= 0 && rot >= 0 && rot <= hd, PQ_ERR_ARG,
              "pq_attn_layer_decode: hd=%d nh=%d nkv=%d pos=%d", hd, nh, nkv, pos);
   PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "pq_attn_layer_decode: cache alignment");
   const int G = nh / nkv;
-  const int ns = (pos + 1 + kSplitF - 1) / kSplitF;
+  const int ns = (ctx + kSplitF - 1) / kSplitF;   // LDS for the splits of positions 0..ctx-1
   const size_t lds = ((size_t)kHDf + 8 * (size_t)kSplitF + (size_t)ns * kPartf) * 4 +
                      (2 * (size_t)kHDf + 8 * (size_t)kSplitF * kVRow) * 2;
   PQ_REQUIRE(G == 1 || G == 2 || G == 4, PQ_ERR_ARG, "pq_attn_layer_decode: %d q heads per kv head (1, 2 or 4)", G);
-  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_attn_layer_decode: position %d needs %zu B of LDS", pos, lds);
-  launch(attn_head_kernel, dim3(nh), dim3(512), lds, as_stream(stream), qkvg, q_norm, k_norm, rope_cs, kcache, vcache,
-         pos, nh, nkv, rot, eps, scale, out, qx, dx);
+  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_attn_layer_decode: %d positions need %zu B of LDS", ctx, lds);
+  launch(attn_head_kernel, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, pos_dev,
+         nh, nkv, rot, eps, scale, out, qx, dx);
   return check_launch("pq_attn_layer_decode");
 }
+
+extern "C" int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float *k_norm,
+                                    const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos, int nh, int nkv,
+                                    int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
+                                    void *stream) {
+  return attn_layer(qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nullptr, pos + 1, nh, nkv, hd, rot, eps, scale,
+                    out, qx, dx, as_stream(stream));
+}
+
+namespace pq {
+int attn_layer_decode_dev(const uint16_t *qkvg, const float *q_norm, const float *k_norm, const float *rope_cs,
+                          uint16_t *kcache, uint16_t *vcache, const int32_t *pos_dev, int ctx, int nh, int nkv, int hd,
+                          int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx, hipStream_t st) {
+  PQ_REQUIRE(pos_dev && ctx > 0, PQ_ERR_ARG, "attn_layer_decode_dev: bad arguments");
+  return attn_layer(qkvg, q_norm, k_norm, rope_cs, kcache, vcache, 0, pos_dev, ctx, nh, nkv, hd, rot, eps, scale, out,
+                    qx, dx, st);
+}
+}  // namespace pq

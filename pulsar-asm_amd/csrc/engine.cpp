@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "pq_host.h"
+#include "pq_internal.h"
 
 namespace pq {
 
@@ -54,8 +55,13 @@ struct Engine {
   float *final_norm = nullptr, *rope = nullptr;
   int pos = 0, tmax = 0, qd = 0, kvd = 0, nin = 0, last_t = 1;
   bool fused = false;             // T=1 steps through the fused kernels (when supported)
+  bool graph = true;              // fused steps replay as captured HIP graphs
+  int32_t *ctr = nullptr;         // device [id slot, position] of the replayed step
+  int32_t hctr[2] = {0, 0};       // its host source (outlives the async upload)
+  hipGraphExec_t gexec[2] = {nullptr, nullptr};  // the step, by conv-ring parity
   uint16_t *Xd[2] = {nullptr, nullptr};  // decode residual ping-pong
   const uint16_t *last_resid = nullptr;
+  const uint16_t *step_resid = nullptr;  // where a replayed decode step leaves the residual
   float *parts = nullptr;
   int nparts = 0;
   // activations, sized for tmax positions
@@ -73,6 +79,8 @@ struct Engine {
 
   ~Engine() {
     if (st) hipStreamSynchronize(st);
+    for (hipGraphExec_t g : gexec)
+      if (g) hipGraphExecDestroy(g);
     for (void *p : allocs) hipFree(p);
     if (st) hipStreamDestroy(st);
   }
@@ -158,6 +166,7 @@ static int create(Engine &E, const pq_model_cfg &c) {
   PQ_TRY(E.dalloc(&E.tok, (size_t)T));
   E.max_ids = c.ctx + 1;
   PQ_TRY(E.dalloc(&E.ids, (size_t)E.max_ids));
+  PQ_TRY(E.dalloc(&E.ctr, 2));
   E.attn_ws_bytes = pq_attn_workspace_bytes(c.nh, c.ctx, T);
   PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.attn_ws), E.attn_ws_bytes));
   // the split-K GEMM workspace: the largest of the layer shapes at tmax positions
@@ -388,7 +397,9 @@ static bool fused_supported(const pq_model_cfg &c, const char **why) {
 // layer, five per attention layer (incl. the attention mixer), the LM head with
 // per-workgroup argmax partials and the final argmax -- 107 launches for the
 // 24-layer backbone. Reads the token from E.tok and writes the next one there.
-static int forward_decode(Engine &E) {
+// dev: the position comes from E.ctr[1] and the id is appended at E.ids[E.ctr[0]]
+// on the device (the form captured for replay); otherwise E.pos is passed.
+static int forward_decode(Engine &E, bool dev) {
   const pq_model_cfg &c = E.c;
   const int H = c.hidden;
   if (E.pos + 1 > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + 1 > %d", E.pos, c.ctx);
@@ -427,8 +438,12 @@ static int forward_decode(Engine &E) {
     PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
     p = pq_gemv_prologue{};
     if (D.attn) {
-      PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd, c.rot,
-                                  c.eps, scale, nullptr, E.qx, E.dx, E.st));
+      if (dev)
+        PQ_TRY(attn_layer_decode_dev(E.Wd, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.ctr + 1, c.ctx, c.nh, c.nkv,
+                                     c.hd, c.rot, c.eps, scale, nullptr, E.qx, E.dx, E.st));
+      else
+        PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd, c.rot,
+                                    c.eps, scale, nullptr, E.qx, E.dx, E.st));
       p.kind = PQ_PRO_Q8;
       p.qx = E.qx;
       p.dx = E.dx;
@@ -452,7 +467,8 @@ static int forward_decode(Engine &E) {
   }
   resnorm(E.L[c.nlayers - 1].post_ffn_norm, E.final_norm);
   PQ_TRY(gemv(E.emb, E.logits, PQ_DTYPE_F32, E.parts));
-  PQ_TRY(pq_argmax_parts(E.parts, E.nparts, E.tok, E.st));
+  if (dev) PQ_TRY(argmax_parts_step(E.parts, E.nparts, E.tok, E.ids, E.ctr, E.st));
+  else PQ_TRY(pq_argmax_parts(E.parts, E.nparts, E.tok, E.st));
   E.pos += 1;
   E.last_t = 1;
   E.last_resid = xa;
@@ -474,9 +490,68 @@ static int prefill(Engine &E, const int32_t *prompt, int n, int32_t *next) {
 
 // n decode steps from the device-resident token *E.tok: step s feeds the id
 // of step s-1 and writes its own into ids[s] and E.tok (no host round trip).
+// The conv rings' parity: every conv layer flips its ping-pong pair each step.
+static int ring_parity(const Engine &E) {
+  for (const LayerDev &D : E.L)
+    if (!D.attn) return D.rc;
+  return 0;
+}
+static void set_ring_parity(Engine &E, int rc) {
+  for (LayerDev &D : E.L)
+    if (!D.attn) D.rc = rc;
+}
+
+// Capture the fused step (device position and id slot) for ring parity p. The
+// capture only records: the host-side state it advances is put back.
+static int capture_step(Engine &E, int p) {
+  const int pos = E.pos, rc = ring_parity(E), last_t = E.last_t;
+  const uint16_t *last_resid = E.last_resid;
+  set_ring_parity(E, p);
+  hipGraph_t g = nullptr;
+  if (hipStreamBeginCapture(E.st, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "hipStreamBeginCapture failed");
+  const int rc_step = forward_decode(E, true);
+  const hipError_t ec = hipStreamEndCapture(E.st, &g);
+  E.step_resid = E.last_resid;   // the residual buffer a step ends in
+  E.pos = pos;
+  E.last_t = last_t;
+  E.last_resid = last_resid;
+  set_ring_parity(E, rc);
+  if (rc_step != PQ_OK) {
+    if (g) hipGraphDestroy(g);
+    return rc_step;
+  }
+  if (ec != hipSuccess || g == nullptr) return fail(PQ_ERR_LAUNCH, "hipStreamEndCapture failed");
+  const hipError_t ei = hipGraphInstantiate(&E.gexec[p], g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (ei != hipSuccess) return fail(PQ_ERR_LAUNCH, "hipGraphInstantiate failed: %s", hipGetErrorString(ei));
+  return PQ_OK;
+}
+
+// n decode steps from the device-resident token *E.tok: step s feeds the id
+// of step s-1 and writes its own into ids[first_slot + s] and E.tok (no host
+// round trip). Fused steps replay a captured graph per step.
 static int decode(Engine &E, int n, int first_slot) {
+  if (E.fused && E.graph) {
+    if (E.pos + n > E.c.ctx) return fail(PQ_ERR_STATE, "context full: %d + %d > %d", E.pos, n, E.c.ctx);
+    for (int p = 0; p < 2; p++)
+      if (!E.gexec[p]) PQ_TRY(capture_step(E, p));
+    E.hctr[0] = first_slot;
+    E.hctr[1] = E.pos;
+    if (hipMemcpyAsync(E.ctr, E.hctr, sizeof E.hctr, hipMemcpyHostToDevice, E.st) != hipSuccess)
+      return fail(PQ_ERR_LAUNCH, "counter upload failed");
+    const int rc0 = ring_parity(E);
+    for (int s = 0; s < n; s++)
+      if (hipGraphLaunch(E.gexec[(rc0 + s) & 1], E.st) != hipSuccess) return fail(PQ_ERR_LAUNCH, "hipGraphLaunch failed");
+    // the host-side state the steps advanced
+    E.pos += n;
+    E.last_t = 1;
+    E.last_resid = E.step_resid;
+    set_ring_parity(E, (rc0 + n) & 1);
+    return PQ_OK;
+  }
   for (int s = 0; s < n; s++) {
-    if (E.fused) PQ_TRY(forward_decode(E));
+    if (E.fused) PQ_TRY(forward_decode(E, false));
     else PQ_TRY(forward(E, 1, E.tok));
     if (hipMemcpyAsync(E.ids + first_slot + s, E.tok, 4, hipMemcpyDeviceToDevice, E.st) != hipSuccess)
       return fail(PQ_ERR_LAUNCH, "id copy failed");
@@ -593,6 +668,12 @@ extern "C" int pq_engine_set_fused(void *h, int on) {
   const char *why;
   if (on && !fused_supported(E.c, &why)) return fail(PQ_ERR_ARG, "pq_engine_set_fused: %s", why);
   E.fused = on != 0;
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_set_graph(void *h, int on) {
+  PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
+  static_cast<Engine *>(h)->graph = on != 0;
   return PQ_OK;
 }
 

@@ -1,0 +1,19 @@
+// pq_internal.h -- entry points the engine shares with the kernels' files but
+// that are not part of the C ABI: the decode step with its position and id slot
+// on the device, so a captured step replays unchanged.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pq {
+
+// pq_attn_layer_decode with the position read from *pos_dev on the device; LDS
+// sized for any position below ctx.
+int attn_layer_decode_dev(const uint16_t *qkvg, const float *q_norm, const float *k_norm, const float *rope_cs,
+                          uint16_t *kcache, uint16_t *vcache, const int32_t *pos_dev, int ctx, int nh, int nkv, int hd,
+                          int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx, hipStream_t st);
+
+// pq_argmax_parts that also appends the id: ids[ctr[0]++] = id, ctr[1]++.
+int argmax_parts_step(const float *parts, int nparts, int32_t *out, int32_t *ids, int32_t *ctr, hipStream_t st);
+
+}  // namespace pq

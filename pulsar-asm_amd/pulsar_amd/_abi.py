@@ -67,6 +67,7 @@ SIGNATURES = {
     "pq_engine_greedy": (I, [P, P, I, I, P]),
     "pq_engine_decode": (I, [P, I, P]),
     "pq_engine_set_fused": (I, [P, I]),
+    "pq_engine_set_graph": (I, [P, I]),
     "pq_engine_sync": (I, [P]),
     "pq_engine_stream": (P, [P]),
     "pq_engine_position": (I, [P]),

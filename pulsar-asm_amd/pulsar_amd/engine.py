@@ -78,6 +78,9 @@ class Engine:
     def set_fused(self, on):
         check(lib().pq_engine_set_fused(self.h, 1 if on else 0), "pq_engine_set_fused")
 
+    def set_graph(self, on):
+        check(lib().pq_engine_set_graph(self.h, 1 if on else 0), "pq_engine_set_graph")
+
     def sync(self):
         check(lib().pq_engine_sync(self.h), "pq_engine_sync")
 

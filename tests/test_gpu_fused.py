@@ -139,21 +139,35 @@ def test_attn_layer_decode(orc, pq, dev, pos):
 
 
 def test_engine_fused_equals_unfused(orc, pq, dev):
+    """Fused steps replayed as captured graphs, fused steps launched one by one,
+    and the unfused op sequence give the oracle's ids; graph replays are split
+    into several decode calls with eager work (state reads, a non-graph step)
+    between them."""
     from pulsar_amd.engine import Engine
     cfg = dict(hidden=2048, ffn=8192, vocab=65536, nlayers=3, nh=32, nkv=8, hd=64, rot=32, ntaps=3, ctx=512,
                eps=1e-5, theta=1e6, seed=77, attn_mask=0b010)
     prompt = orc.gen_tokens(9, 70, cfg["vocab"])
-    ids = []
-    for fused in (True, False):
+    m = orc.Model(**{k: v for k, v in cfg.items()})
+    ref = m.greedy(prompt, 12)
+    m.close()
+    for fused, graph in ((True, True), (True, False), (False, False)):
         e = Engine(**cfg)
         e.load_synthetic()
         e.set_fused(fused)
-        ids.append(e.greedy(prompt, 12))
+        e.set_graph(graph)
+        ids = e.greedy(prompt, 12)
         e.close()
-    assert np.array_equal(ids[0], ids[1])
-    m = orc.Model(**{k: v for k, v in cfg.items()})
-    assert np.array_equal(ids[0], m.greedy(prompt, 12))
-    m.close()
+        assert np.array_equal(ids, ref), (fused, graph)
+    e = Engine(**cfg)
+    e.load_synthetic()
+    assert e.feed(prompt) == ref[0]
+    out = []
+    for k, graph in ((3, True), (1, False), (4, True), (2, True)):
+        e.set_graph(graph)
+        out.extend(e.decode(k).tolist())
+        e.hidden()
+    e.close()
+    assert np.array_equal(np.array(out), ref[1:11]), (out, ref[1:11].tolist())
 
 
 def test_gate_up_interleave_and_swiglu(orc, pq, dev):
