@@ -2,18 +2,21 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-A step is one pass of the decode hot path over one synthetic layer at T=1:
-quantize x (K=2048 and K=8192) to Q8_0, then the GEMVs fused q|k|v 3072x2048,
-o_proj 2048x2048, gate+up 16384x2048, down 2048x8192 and the LM head
-65536x2048 (fp32 logits), all from packed Q8_0 weights resident in HBM. The
-weights rotate over enough copies (>= 600 MB) that no step reads another
-step's weights out of the 256 MB Infinity Cache.
+A step is one pass of the decode hot path over one synthetic layer at T=1: the
+GEMVs fused q|k|v 3072x2048, o_proj 2048x2048, gate+up 16384x2048, down
+2048x8192 and the LM head 65536x2048 (fp32 logits), from packed Q8_0 weights
+resident in HBM, each quantizing its fp32 x (K=2048 or 8192) to Q8_0 in its own
+prologue (q8_gemv_fused_kernel, PQ_PRO_F32). The weights rotate over enough
+copies (>= 600 MB) that no step reads another step's weights out of the 256 MB
+Infinity Cache.
 
 Prints ONE JSON line. value = algorithmic bytes per step / time per step (GB/s);
-roofline = the GEMV kernel's algorithmic bytes / its HIP-event-timed launch
-durations on the launch stream, against 8 TB/s; cpu_baseline = the reference's
-own CPU GEMV (.auto/lfm3/q8_gemv_cpu.c gemv_q8, compiled into oracle/_ref) on
-the host cores over a bounded sample of the same shapes.
+roofline = the GEMV kernel's algorithmic bytes / its launch period, timed with
+HIP events on the launch stream over back-to-back launches of each shape (the
+period includes the dispatch gap between launches), against 8 TB/s;
+cpu_baseline = the reference's own CPU GEMV (.auto/lfm3/q8_gemv_cpu.c gemv_q8,
+compiled into oracle/_ref) on the host cores over a bounded sample of the same
+shapes.
 """
 import argparse
 import json
@@ -46,8 +49,40 @@ def measured_traffic():
     return int(float(m.group(1)) * 1e6) if m else None
 
 
+def graph_of(torch, fn):
+    """fn's launches (on torch's current stream) captured into one HIP graph,
+    after one eager run on a side stream: the timed regions replay graphs so the
+    GPU, not the Python launch loop, sets the pace."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def timed_replay(torch, g, stream, reps=1):
+    """Milliseconds per replay of g, HIP events on the launch stream."""
+    from pulsar_amd.hiptime import Event
+    a, b = Event(), Event()
+    g.replay()
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        g.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_ms(b) / reps
+
+
 def gemv_bytes(N, K, out):
-    return N * K + N * (K // 32) * 2 + K + (K // 32) * 4 + N * (4 if out == "f32" else 2)
+    """Algorithmic HBM bytes of one GEMV: codes, fp16 scales, the fp32 x, y."""
+    return N * K + N * (K // 32) * 2 + 4 * K + N * (4 if out == "f32" else 2)
 
 
 def cpu_baseline(seconds=10.0):
@@ -129,53 +164,59 @@ def decode_bench(pq, n_steps=64, n_prompt=256):
             "prefill_ms_256": round(prefill_ms, 2)}
 
 
-def prefill_gemm_bench(pq, torch, dev, g, T=512, chunk=32, reps=5):
-    """The layer's four GEMMs over T=512 positions in 32-position chunks (int8 MFMA)."""
+def prefill_gemm_bench(pq, torch, dev, g, T=512, chunk=32, reps=3, rotate_mb=600):
+    """The layer's GEMMs and the LM head (config-2 weights) over T=512 positions
+    in 32-position chunks (int8 MFMA), each chunk reading a different copy of the
+    weights (>= 600 MB rotated) as a layer-by-layer prefill re-reads its weights
+    from HBM per chunk. Its roofline is HBM (weight bytes per chunk); the same
+    work as one T=512 launch per GEMM is reported against the int8 MFMA peak."""
     from pulsar_amd.hiptime import Event
-    shapes = [("qkv", 3072, 2048), ("o_proj", 2048, 2048), ("gate_up", 16384, 2048), ("down", 2048, 8192)]
-    ws = {}
-    for (name, N, K) in shapes:
-        codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
-        scales = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().view(torch.int16)
-        ws[name] = pq.Q8Weight(codes, scales)
+    shapes = [(name, N, K) for (name, N, K, _) in SHAPES]
+    per_set = sum(pq.lib().pq_q8_packed_codes_bytes(N, K) + pq.lib().pq_q8_packed_scales_bytes(N, K)
+                  for (_, N, K) in shapes)
+    ncopy = max(2, -(-rotate_mb * 1000000 // per_set))
+    sets = []
+    for _ in range(ncopy):
+        ws = {}
+        for (name, N, K) in shapes:
+            codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+            scales = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().view(torch.int16)
+            ws[name] = pq.Q8Weight(codes, scales)
+            del codes, scales
+        sets.append(ws)
     xs = {K: pq.q8_quant(torch.randn((T, K), device=dev, generator=g)) for K in (2048, 8192)}
-    outs = {name: torch.empty((chunk, N), dtype=torch.bfloat16, device=dev) for (name, N, K) in shapes}
+    outs = {name: torch.empty((T, N), dtype=torch.bfloat16, device=dev) for (name, N, K) in shapes}
+    wsz = max(pq.lib().pq_q8_gemm_workspace_bytes(N, K, t) for (_, N, K) in shapes for t in (chunk, T))
+    wsp = torch.empty(max(wsz, 16), dtype=torch.uint8, device=dev)
     stream = pq.stream_ptr()
 
     def run():
-        for c0 in range(0, T, chunk):
+        for ci, c0 in enumerate(range(0, T, chunk)):
+            ws = sets[ci % ncopy]
             for (name, N, K) in shapes:
                 qx, dx = xs[K]
-                pq.q8_gemm(ws[name], qx[c0:c0 + chunk], dx[c0:c0 + chunk], out_dtype=pq.DT_BF16, out=outs[name])
+                pq.q8_gemm(ws[name], qx[c0:c0 + chunk], dx[c0:c0 + chunk], out_dtype=pq.DT_BF16,
+                           out=outs[name][c0:c0 + chunk], ws=wsp)
 
-    run()
-    torch.cuda.synchronize()
-    a, b = Event(), Event()
-    a.record(stream)
-    for _ in range(reps):
-        run()
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms = a.elapsed_ms(b) / reps
-    ops = sum(2 * N * K * T for (_, N, K) in shapes)
-    # the same work as one T=512 launch per GEMM (every 32-position tile in one grid)
-    outs_full = {name: torch.empty((T, N), dtype=torch.bfloat16, device=dev) for (name, N, K) in shapes}
-
-    def run_full():
+    def run_full(r):
+        ws = sets[r % ncopy]
         for (name, N, K) in shapes:
             qx, dx = xs[K]
-            pq.q8_gemm(ws[name], qx, dx, out_dtype=pq.DT_BF16, out=outs_full[name])
+            pq.q8_gemm(ws[name], qx, dx, out_dtype=pq.DT_BF16, out=outs[name], ws=wsp)
 
-    run_full()
-    torch.cuda.synchronize()
-    a.record(stream)
-    for _ in range(reps):
-        run_full()
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms_full = a.elapsed_ms(b) / reps
-    return {"T": T, "chunk": chunk, "ms": round(ms, 4), "TOPS": round(ops / (ms * 1e-3) / 1e12, 2),
-            "int8_peak_frac": round(ops / (ms * 1e-3) / 1e12 / 5000.0, 4), "ops": ops,
+    g_run = graph_of(torch, run)
+    ms = timed_replay(torch, g_run, stream, reps)
+    del g_run
+    ops = sum(2 * N * K * T for (_, N, K) in shapes)
+    wbytes = per_set * (T // chunk)
+    g_full = graph_of(torch, lambda: [run_full(r) for r in range(ncopy)])
+    ms_full = timed_replay(torch, g_full, stream, reps) / ncopy
+    del g_full
+    return {"T": T, "chunk": chunk, "gemms": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "ms": round(ms, 4),
+            "TOPS": round(ops / (ms * 1e-3) / 1e12, 2), "int8_peak_frac": round(ops / (ms * 1e-3) / 1e12 / 5000.0, 4),
+            "weight_bytes_read": wbytes, "GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "ops": ops,
+            "weight_copies_rotated": ncopy,
             "single_launch_ms": round(ms_full, 4), "single_launch_TOPS": round(ops / (ms_full * 1e-3) / 1e12, 2),
             "single_launch_int8_peak_frac": round(ops / (ms_full * 1e-3) / 1e12 / 5000.0, 4)}
 
@@ -204,23 +245,16 @@ def ternary_bench(pq, torch, dev, g, reps=50, rotate_mb=400):
     outs = {name: torch.empty(N, dtype=torch.float32, device=dev) for (name, N, K) in shapes}
     stream = pq.stream_ptr()
 
-    def run(i, ev=None):
+    def gemv(i, name, N, K):
         ws = sets[i % ncopy]
-        for j, (name, N, K) in enumerate(shapes):
-            if ev is not None:
-                pq.lib().pq_time_next_launch(ev[j][0].h, ev[j][1].h)
-            pq.tq2_gemv(ws[name][0], ws[name][1], x12 if K == 12288 else x4, N, K, out=outs[name])
+        pq.tq2_gemv(ws[name][0], ws[name][1], x12 if K == 12288 else x4, N, K, out=outs[name])
 
-    for i in range(5):
-        run(i)
-    torch.cuda.synchronize()
-    per = [0.0, 0.0, 0.0]
-    ev = [(Event(), Event()) for _ in shapes]
-    for i in range(reps):
-        run(i, ev)
-        torch.cuda.synchronize()
-        for j in range(3):
-            per[j] += ev[j][0].elapsed_ms(ev[j][1]) / reps
+    # launch period per shape: back-to-back launches, weights rotating, HIP events on the launch stream
+    per = []
+    for (name, N, K) in shapes:
+        gsh = graph_of(torch, lambda: [gemv(i, name, N, K) for i in range(reps)])
+        per.append(timed_replay(torch, gsh, stream, 3) / reps)
+        del gsh
     step_bytes = sum(N * K // 4 + N * K // 128 * 2 + K // 256 * 292 + N * 4 for (_, N, K) in shapes)
     us = sum(per) * 1e3
     return {"shapes": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "us_per_step": round(us, 2),
@@ -273,36 +307,31 @@ def main():
     from pulsar_amd.hiptime import Event
     stream = pq.stream_ptr()
 
-    def step(i, ev=None):
+    def gemv(ws, name, N, K, o):
+        pq.gemv_fused(ws[name], pq.PRO_F32, out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name],
+                      xf=x8 if K == 8192 else x2)
+
+    def step(i):
         ws = copies[i % ncopy]
-        q2, d2 = pq.q8_quant(x2)
-        q8, d8 = pq.q8_quant(x8)
-        for j, (name, N, K, o) in enumerate(SHAPES):
-            q, d = (q8, d8) if K == 8192 else (q2, d2)
-            if ev is not None:
-                pq.lib().pq_time_next_launch(ev[j][0].h, ev[j][1].h)
-            pq.q8_gemv(ws[name], q, d, out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name])
+        for (name, N, K, o) in SHAPES:
+            gemv(ws, name, N, K, o)
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    start, stop = Event(), Event()
-    start.record(stream)
-    for i in range(args.steps):
-        step(i)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_ms(stop) / args.steps
+    # the K timed steps, captured as one graph (launches as the engine issues them)
+    g_steps = graph_of(torch, lambda: [step(i) for i in range(args.steps)])
+    ms_per_step = timed_replay(torch, g_steps, stream) / args.steps
+    del g_steps
 
-    # per-launch durations of the GEMV kernel: events attached to its own dispatch packets
-    per = {name: 0.0 for (name, *_r) in SHAPES}
-    ev = [(Event(), Event()) for _ in SHAPES]
-    for i in range(args.steps):
-        step(i, ev)
-        torch.cuda.synchronize()
-        for j, (name, *_r) in enumerate(SHAPES):
-            per[name] += ev[j][0].elapsed_ms(ev[j][1])
-    per = {k: v / args.steps for k, v in per.items()}
+    # launch period of the GEMV kernel per shape: back-to-back launches of that
+    # shape (weights rotating over the copies), HIP events on the launch stream
+    per = {}
+    nper = 30
+    for (name, N, K, o) in SHAPES:
+        gsh = graph_of(torch, lambda: [gemv(copies[i % ncopy], name, N, K, o) for i in range(nper)])
+        per[name] = timed_replay(torch, gsh, stream, reps=3) / nper
+        del gsh
 
     step_bytes = sum(gemv_bytes(N, K, o) for (_, N, K, o) in SHAPES)
     gemv_ms = sum(per.values())
@@ -311,6 +340,7 @@ def main():
     per_shape = {name: {"us": round(per[name] * 1e3, 2),
                         "GB/s": round(gemv_bytes(N, K, o) / (per[name] * 1e-3) / 1e9, 1)}
                  for (name, N, K, o) in SHAPES}
+    lm = [s_ for s_ in SHAPES if s_[0] == "lm_head"][0]
 
     line = {
         "metric": "Q8 GEMV HBM GB/s (% of peak); backbone decode tok/s on 1 MI355X",
@@ -331,7 +361,8 @@ def main():
                    "rotated_MB": round(ncopy * set_bytes / 1e6, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "q8_gemv_kernel", "per_shape": per_shape},
+                     "kernel": "q8_gemv_fused_kernel (5 shapes, launch period)", "per_shape": per_shape,
+                     "lm_head_frac": round(gemv_bytes(*lm[1:]) / (per["lm_head"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         "cpu_baseline": None if args.no_cpu else cpu_baseline(),
     }
     if args.calib:

@@ -180,6 +180,8 @@ int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *token
  *   PQ_PRO_CONV     gated short conv of bcx [B|C|x] with ring_in -> ring_out
  *                   (the shifted ring, written once; a ping-pong pair);
  *                   ntaps must be 3, taps f32 [K][3] 16-byte aligned
+ *   PQ_PRO_F32      x = xf, fp32 [K] (16-byte aligned), quantized in-kernel
+ *                   exactly as pq_q8_quant_f32
  * K is the GEMV's K (a power of two, 1024..8192). argmax_parts (optional,
  * 2 floats per workgroup, pq_q8_gemv_parts(N, K) of them) receives each
  * workgroup's (max, index) for pq_argmax_parts -- the LM head + k_argmax. */
@@ -189,6 +191,7 @@ int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *token
 #define PQ_PRO_EMBED 3
 #define PQ_PRO_SILU 4
 #define PQ_PRO_CONV 5
+#define PQ_PRO_F32 6
 typedef struct pq_gemv_prologue {
   int kind;
   const int8_t *qx;
@@ -206,6 +209,7 @@ typedef struct pq_gemv_prologue {
   const uint16_t *emb_ps;
   const int32_t *tok;
   int vocab;
+  const float *xf;
 } pq_gemv_prologue;
 int pq_q8_gemv_parts(int N, int K);
 int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,

@@ -15,6 +15,7 @@
 //   CONV     the gated short conv; workgroup 0 writes the shifted ring into the
 //            other buffer of a ping-pong pair
 //   Q8       y already quantized (qx, dx)
+//   F32      y = fp32 x, quantized here
 // then quantizes y to Q8_0 in LDS and runs the GEMV of q8.hip on it. Every op
 // keeps the unfused kernels' arithmetic and order (pairwise sums of squares,
 // the same roundings), so the fused step is bit-identical to the unfused one.
@@ -161,6 +162,8 @@ __device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int 
 #pragma unroll
     for (int i = 0; i < E / 4; i++) r.emb_c[i] = reinterpret_cast<const uint32_t *>(p.qx + e0)[i];
     r.f0[0] = (e0 & 31) == 0 ? p.dx[e0 >> 5] : 0.0f;
+  } else if constexpr (PRO == PQ_PRO_F32) {
+    ld_f32<E>(p.xf + e0, r.f0);
   } else if constexpr (PRO == PQ_PRO_RESNORM) {
     ld_raw<E>(p.h + e0, r.u0);
     ld_raw<E>(p.x_in + e0, r.u1);
@@ -216,6 +219,9 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
     }
     if (writer) st_bf16<E>(p.x_out + e0, xn);
     norm_apply<E>(v, r.f1, wg_pairwise_sq<E>(v, red + 8), K, p.eps);
+  } else if constexpr (PRO == PQ_PRO_F32) {
+#pragma unroll
+    for (int i = 0; i < E; i++) v[i] = r.f0[i];
   } else if constexpr (PRO == PQ_PRO_NORM) {
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
@@ -654,6 +660,9 @@ static int check_fused_args(const int8_t *pcodes, const uint16_t *pscales, const
     case PQ_PRO_SILU:
       PQ_REQUIRE(p.gu, PQ_ERR_ARG, "%s: SILU needs gu", who);
       break;
+    case PQ_PRO_F32:
+      PQ_REQUIRE(p.xf && aligned(p.xf, 16), PQ_ERR_ARG, "%s: F32 prologue needs 16-byte aligned xf", who);
+      break;
     case PQ_PRO_CONV:
       PQ_REQUIRE(p.bcx && p.ring_in && p.ring_out && p.taps && p.ring_in != p.ring_out &&
                      p.ntaps == kFusedTaps && aligned(p.taps, 16),
@@ -698,6 +707,7 @@ static int launch_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_
     case PQ_PRO_NORM: PQ_FUSED(PQ_PRO_NORM) break;
     case PQ_PRO_EMBED: PQ_FUSED(PQ_PRO_EMBED) break;
     case PQ_PRO_SILU: PQ_FUSED(PQ_PRO_SILU) break;
+    case PQ_PRO_F32: PQ_FUSED(PQ_PRO_F32) break;
     default: PQ_FUSED(PQ_PRO_CONV) break;
   }
 #undef PQ_FUSED

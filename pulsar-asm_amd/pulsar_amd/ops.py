@@ -12,9 +12,9 @@ __all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
-           "PRO_CONV"]
+           "PRO_CONV", "PRO_F32"]
 
-PRO_Q8, PRO_RESNORM, PRO_NORM, PRO_EMBED, PRO_SILU, PRO_CONV = 0, 1, 2, 3, 4, 5
+PRO_Q8, PRO_RESNORM, PRO_NORM, PRO_EMBED, PRO_SILU, PRO_CONV, PRO_F32 = 0, 1, 2, 3, 4, 5, 6
 
 DT_F32 = 0
 DT_BF16 = 1

@@ -95,6 +95,16 @@ def test_conv_prologue(orc, pq, dev):
     assert np.array_equal(_u16(y), _ref_gemv(orc, W, S, o))
 
 
+@pytest.mark.parametrize("N,K", [(3072, 2048), (65536, 2048), (2048, 8192), (130, 1024)])
+def test_f32_prologue(orc, pq, dev, N, K):
+    W, S, w = _w(orc, pq, dev, N, K, SEED + 70 + N)
+    x = orc.gen_normal(SEED + 71 + K, K)
+    qx, dx = orc.q8_quant(x)
+    yr = orc.q8_gemv(W, S, qx, dx)
+    y = pq.gemv_fused(w, pq.PRO_F32, out_dtype=pq.DT_F32, xf=torch.from_numpy(x).to(dev))
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32))
+
+
 def test_q8_prologue(orc, pq, dev):
     N, K = 2048, 2048
     W, S, w = _w(orc, pq, dev, N, K, SEED + 40)
