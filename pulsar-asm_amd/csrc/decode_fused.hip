@@ -176,10 +176,13 @@ __device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int 
     const int id = *p.tok;
     const bool ok = id >= 0 && id < p.vocab;
     const int nb = K / kQ, nch = nchunks(K), tile = ok ? id / kTR : 0, rr = ok ? id % kTR : 0;
-    const int b = e0 / kQ, hh = (e0 % kQ) / 16, jj = e0 % 16;
-    const int8_t *src = p.emb_pc + (((size_t)tile * nb + b) * 2 + hh) * (kTR * 16) + rr * 16 + jj;
+    const int b = e0 / kQ;   // E <= 32 elements, all in block b
 #pragma unroll
-    for (int i = 0; i < E / 4; i++) r.emb_c[i] = ok ? reinterpret_cast<const uint32_t *>(src)[i] : 0u;
+    for (int i = 0; i < E / 4; i++) {   // element e0+4i: half (e % 32) / 16 of the block's slab
+      const int e = e0 + 4 * i, hh = (e % kQ) / 16, jj = e % 16;
+      const int8_t *src = p.emb_pc + (((size_t)tile * nb + b) * 2 + hh) * (kTR * 16) + rr * 16 + jj;
+      r.emb_c[i] = ok ? *reinterpret_cast<const uint32_t *>(src) : 0u;
+    }
     r.emb_s = ok ? p.emb_ps[(((size_t)tile * nch + b / kCB) * kTR + rr) * kCB + (b % kCB)] : (uint16_t)0;
     ld_f32<E>(p.w0 + e0, r.f0);
   } else if constexpr (PRO == PQ_PRO_SILU) {

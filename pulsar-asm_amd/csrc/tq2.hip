@@ -21,6 +21,7 @@
 // sum code*x = sum_k dot4(d_k, xperm_k), and isum = that - sum x over the group.
 #include "pq_device.h"
 #include "pq_host.h"
+#include "q8_common.h"
 
 namespace pq {
 
@@ -30,6 +31,42 @@ constexpr int kQ8KBytes = 292;
 constexpr int kTqRows = 16;     // rows per workgroup
 constexpr int kTqSlots = 16;    // lanes per row (group slots)
 
+// The activations' Q8_K row staged once per workgroup: permuted qs (dword k of
+// each 16 = x[k], x[k+4], x[k+8], x[k+12]), per-group sums from the bsums
+// (exact int16 sums of 16), and each group's block scale d.
+__device__ __forceinline__ void tq2_stage_x(const uint8_t *__restrict__ xq, int K, int *xperm, int *gsum, float *db) {
+  const int ng = K / kTqGroup;
+  const int nblk = K / kQ8K;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(xq), (short)0,
+                                                                      nblk * kQ8KBytes, kRsrcWord3);
+  for (int m = threadIdx.x; m < K / 16; m += blockDim.x) {   // run m: 16 qs of block m/16
+    const int blk = m >> 4, off = (m & 15) * 16;
+    const v4i w = __builtin_amdgcn_raw_buffer_load_b128(rx, blk * kQ8KBytes + 4 + off, 0, 0);
+    const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
+    int4 o;
+    o.x = (int)((w0 & 0xffu) | ((w1 & 0xffu) << 8) | ((w2 & 0xffu) << 16) | ((w3 & 0xffu) << 24));
+    o.y = (int)(((w0 >> 8) & 0xffu) | (((w1 >> 8) & 0xffu) << 8) | (((w2 >> 8) & 0xffu) << 16) |
+                (((w3 >> 8) & 0xffu) << 24));
+    o.z = (int)(((w0 >> 16) & 0xffu) | (((w1 >> 16) & 0xffu) << 8) | (((w2 >> 16) & 0xffu) << 16) |
+                (((w3 >> 16) & 0xffu) << 24));
+    o.w = (int)((w0 >> 24) | ((w1 >> 24) << 8) | ((w2 >> 24) << 16) | ((w3 >> 24) << 24));
+    reinterpret_cast<int4 *>(xperm)[m] = o;
+  }
+  for (int g = threadIdx.x; g < ng; g += blockDim.x) {
+    const int blk = g >> 1, half = g & 1;
+    // bsums 8*half .. 8*half+7 of the block (16 bytes at an even offset)
+    const v4i bs = __builtin_amdgcn_raw_buffer_load_b128(rx, blk * kQ8KBytes + 4 + kQ8K + 16 * half, 0, 0);
+    const int v[4] = {bs.x, bs.y, bs.z, bs.w};
+    int t = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) t += (int)(int16_t)(v[i] & 0xffff) + (int)(int16_t)((uint32_t)v[i] >> 16);
+    gsum[g] = t;
+    db[g] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, blk * kQ8KBytes, 0, 0));
+  }
+}
+
+// GPL groups per lane per round (16*GPL groups = 2048*GPL of K).
+template <int GPL>
 __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict__ codes,
                                                         const uint16_t *__restrict__ scales,
                                                         const uint8_t *__restrict__ xq, float *__restrict__ y, int N,
@@ -41,51 +78,63 @@ __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict
   float *db = reinterpret_cast<float *>(gsum + ng);            // [ng] Q8_K d of the group's block
   float *pg = db + ng;                                         // [16 rows][ng] group partials
   const int tid = threadIdx.x;
-  // stage x: dword position m of the K/16 sixteen-element runs, permutation k
-  for (int i = tid; i < K / 4; i += blockDim.x) {
-    const int m = i >> 2, k = i & 3;                 // run m, permuted dword k
-    const int blk = (m * 16) / kQ8K, off = (m * 16) % kQ8K;
-    const int8_t *qs = reinterpret_cast<const int8_t *>(xq + (size_t)blk * kQ8KBytes + 4) + off;
-    const uint32_t b0 = (uint8_t)qs[k], b1 = (uint8_t)qs[k + 4], b2 = (uint8_t)qs[k + 8], b3 = (uint8_t)qs[k + 12];
-    xperm[i] = (int)(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24));
-  }
-  for (int g = tid; g < ng; g += blockDim.x) {
-    const uint8_t *b = xq + (size_t)(g >> 1) * kQ8KBytes;
-    const int8_t *qs = reinterpret_cast<const int8_t *>(b + 4) + (g & 1) * kTqGroup;
-    int s = 0;
-    for (int i = 0; i < kTqGroup; i++) s += qs[i];
-    gsum[g] = s;
-    db[g] = *reinterpret_cast<const float *>(b);
-  }
-  __syncthreads();
   const int r = tid / kTqSlots, gs = tid % kTqSlots;
   const int row = blockIdx.x * kTqRows + r;
-  if (row < N) {
-    const uint8_t *cr = codes + (size_t)row * (K / 4);
-    const uint16_t *sr = scales + (size_t)row * ng;
-    for (int g = gs; g < ng; g += kTqSlots) {
-      const uint4 c0 = *reinterpret_cast<const uint4 *>(cr + g * 32);
-      const uint4 c1 = *reinterpret_cast<const uint4 *>(cr + g * 32 + 16);
-      const uint32_t w[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-      const int *xp = xperm + g * (kTqGroup / 4);
-      int s = 0;
+  const bool live = row < N;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(codes + (size_t)(live ? row : 0) * (K / 4)), (short)0, live ? K / 4 : 0, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(scales + (size_t)(live ? row : 0) * ng), (short)0, live ? ng * 2 : 0, kRsrcWord3);
+  for (int g0 = 0; g0 < ng; g0 += kTqSlots * GPL) {
+    // this round's codes (32 B per group) and scales, before anything waits
+    v4i c[GPL][2];
+    uint32_t sc[GPL];
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * j);
-        s = __builtin_amdgcn_sdot4((int)(w[j] & 0x03030303u), xv.x, s, false);
-        s = __builtin_amdgcn_sdot4((int)((w[j] >> 2) & 0x03030303u), xv.y, s, false);
-        s = __builtin_amdgcn_sdot4((int)((w[j] >> 4) & 0x03030303u), xv.z, s, false);
-        s = __builtin_amdgcn_sdot4((int)((w[j] >> 6) & 0x03030303u), xv.w, s, false);
+    for (int j = 0; j < GPL; j++) {
+      const int g = g0 + j * kTqSlots + gs;
+      const int off = g < ng ? g * 32 : kRsrcOob;
+      c[j][0] = __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0);
+      c[j][1] = __builtin_amdgcn_raw_buffer_load_b128(rc, off + 16, 0, 0);
+      sc[j] = __builtin_amdgcn_raw_buffer_load_b32(rsc, g < ng ? (g & ~1) * 2 : kRsrcOob, 0, 0);
+    }
+    if (g0 == 0) {
+      tq2_stage_x(xq, K, xperm, gsum, db);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < GPL; j++) {
+      const int g = g0 + j * kTqSlots + gs;
+      if (g < ng) {
+        const uint32_t w[8] = {(uint32_t)c[j][0].x, (uint32_t)c[j][0].y, (uint32_t)c[j][0].z, (uint32_t)c[j][0].w,
+                               (uint32_t)c[j][1].x, (uint32_t)c[j][1].y, (uint32_t)c[j][1].z, (uint32_t)c[j][1].w};
+        const int *xp = xperm + g * (kTqGroup / 4);
+        int sacc = 0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * q);
+          sacc = __builtin_amdgcn_sdot4((int)(w[q] & 0x03030303u), xv.x, sacc, false);
+          sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 2) & 0x03030303u), xv.y, sacc, false);
+          sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 4) & 0x03030303u), xv.z, sacc, false);
+          sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 6) & 0x03030303u), xv.w, sacc, false);
+        }
+        const int isum = sacc - gsum[g];
+        const float t = h2f((uint16_t)(sc[j] >> (16 * (g & 1)))) * db[g];
+        pg[r * ng + g] = t * (float)isum;
       }
-      const int isum = s - gsum[g];
-      const float t = h2f(sr[g]) * db[g];
-      pg[r * ng + g] = t * (float)isum;
     }
   }
   __syncthreads();
-  if (gs == 0 && row < N) {
+  if (gs == 0 && live) {   // groups ascending; partials read 8 at a time
     float acc = 0.0f;
-    for (int g = 0; g < ng; g++) acc = acc + pg[r * ng + g];
+    const float *pr = pg + r * ng;
+    const int ng8 = (ng & 7) == 0 ? ng : 0;   // 16-byte aligned rows when ng % 8 == 0
+    for (int g = ng8; g < ng; g++) acc = acc + pr[g];
+    for (int g = 0; g < ng8; g += 8) {
+      const float4 a4 = reinterpret_cast<const float4 *>(pr + g)[0];
+      const float4 b4 = reinterpret_cast<const float4 *>(pr + g)[1];
+      acc = acc + a4.x; acc = acc + a4.y; acc = acc + a4.z; acc = acc + a4.w;
+      acc = acc + b4.x; acc = acc + b4.y; acc = acc + b4.z; acc = acc + b4.w;
+    }
     y[row] = acc;
   }
 }
@@ -156,7 +205,11 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
   const int ng = K / kTqGroup;
   const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)kTqRows * ng * 4;
-  launch(tq2_gemv_kernel, dim3((unsigned)((N + kTqRows - 1) / kTqRows)), dim3(kTqRows * kTqSlots), lds,
-         as_stream(stream), codes, scales, xq, y, N, K);
+  const dim3 grid((unsigned)((N + kTqRows - 1) / kTqRows)), block(kTqRows * kTqSlots);
+  hipStream_t st = as_stream(stream);
+  const int gpl = (ng + kTqSlots - 1) / kTqSlots;   // groups per lane for one round
+  if (gpl <= 2) launch(tq2_gemv_kernel<2>, grid, block, lds, st, codes, scales, xq, y, N, K);
+  else if (gpl <= 4) launch(tq2_gemv_kernel<4>, grid, block, lds, st, codes, scales, xq, y, N, K);
+  else launch(tq2_gemv_kernel<6>, grid, block, lds, st, codes, scales, xq, y, N, K);
   return check_launch("pq_tq2_gemv");
 }
