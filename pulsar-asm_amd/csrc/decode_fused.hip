@@ -677,45 +677,71 @@ static int check_fused_args(const int8_t *pcodes, const uint16_t *pscales, const
   return PQ_OK;
 }
 
-// 256 or 512 threads: the prologue spreads K over them, E = K/(64W) in 4..16.
+// Launch shape of a fused GEMV: W waves (4 or 8; fewer waves leave each
+// thread a longer prologue and measured slower, even where a wave has no chunk
+// of its own and only issues loads that read nothing), enough to give every
+// chunk slot of the R-row slice a lane, and E = K/(64W) prologue elements per
+// thread, 4..16.
+static int fused_waves(int R, int K) {
+  const int C = 64 / R;
+  const int need = (nchunks(K) + C - 1) / C;
+  int W = need > 4 ? 8 : 4;
+  if (K / (64 * W) > 16) W = 8;
+  if (K / (64 * W) < 4) W = 4;
+  return W;
+}
+
+template <int R, int PRO, int E>
+static void launch_fused_t(dim3 grid, dim3 block, size_t lds, hipStream_t st, const int8_t *pcodes,
+                           const uint16_t *pscales, const pq_gemv_prologue &p, void *y, int yb, int N, int K,
+                           float *parts, int8_t *qo, float *dqo) {
+  launch(q8_gemv_fused_kernel<R, PRO, E>, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo);
+}
+
+template <int R, int PRO>
+static void launch_fused_e(int E, dim3 grid, dim3 block, size_t lds, hipStream_t st, const int8_t *pcodes,
+                           const uint16_t *pscales, const pq_gemv_prologue &p, void *y, int yb, int N, int K,
+                           float *parts, int8_t *qo, float *dqo) {
+  switch (E) {
+    case 4: launch_fused_t<R, PRO, 4>(grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo); break;
+    case 8: launch_fused_t<R, PRO, 8>(grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo); break;
+    default: launch_fused_t<R, PRO, 16>(grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo); break;
+  }
+}
+
+template <int PRO>
+static void launch_fused_r(int R, int E, dim3 grid, dim3 block, size_t lds, hipStream_t st, const int8_t *pcodes,
+                           const uint16_t *pscales, const pq_gemv_prologue &p, void *y, int yb, int N, int K,
+                           float *parts, int8_t *qo, float *dqo) {
+  switch (R) {
+    case 64: launch_fused_e<64, PRO>(E, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo); break;
+    case 32: launch_fused_e<32, PRO>(E, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo); break;
+    case 16: launch_fused_e<16, PRO>(E, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo); break;
+    default: launch_fused_e<8, PRO>(E, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo); break;
+  }
+}
+
 static int launch_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue &p, void *y, int yb,
-                        int N, int K, float *parts, int8_t *qo, float *dqo, GemvShape g, hipStream_t st,
-                        const char *who) {
-  const int C = 64 / g.R;
-  int W = g.W >= 8 ? 8 : 4;
-  if (K / (64 * W) < 4) W = 4;   // K = 1024
-  if (K / (64 * W) > 16) W = 8;  // K = 8192
+                        int N, int K, float *parts, int8_t *qo, float *dqo, int R, hipStream_t st, const char *who) {
+  const int C = 64 / R;
+  const int W = fused_waves(R, K);
   const int E = K / (64 * W);
+  PQ_REQUIRE(E >= 4 && E <= 16 && 64 * W * E == K, PQ_ERR_ARG, "%s: no launch shape for K=%d", who, K);
   const int nch = nchunks(K), nb = K / kQ;
   const size_t lds = (size_t)W * 64 * 4 + (size_t)nch * kXStride + (size_t)nb * 4;
   const dim3 grid((unsigned)(ntiles(N) * C)), block(64 * W);
-#define PQ_FUSED_E(RR, PP, EE) \
-  launch(q8_gemv_fused_kernel<RR, PP, EE>, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo)
-#define PQ_FUSED_R(RR, PP)                          \
-  switch (E) {                                      \
-    case 4: PQ_FUSED_E(RR, PP, 4); break;           \
-    case 8: PQ_FUSED_E(RR, PP, 8); break;           \
-    default: PQ_FUSED_E(RR, PP, 16); break;         \
-  }
-#define PQ_FUSED(PP)                        \
-  switch (g.R) {                            \
-    case 64: PQ_FUSED_R(64, PP) break;      \
-    case 32: PQ_FUSED_R(32, PP) break;      \
-    case 16: PQ_FUSED_R(16, PP) break;      \
-    default: PQ_FUSED_R(8, PP) break;       \
-  }
+#define PQ_FUSED(PP) \
+  launch_fused_r<PP>(R, E, grid, block, lds, st, pcodes, pscales, p, y, yb, N, K, parts, qo, dqo)
   switch (p.kind) {
-    case PQ_PRO_Q8: PQ_FUSED(PQ_PRO_Q8) break;
-    case PQ_PRO_RESNORM: PQ_FUSED(PQ_PRO_RESNORM) break;
-    case PQ_PRO_NORM: PQ_FUSED(PQ_PRO_NORM) break;
-    case PQ_PRO_EMBED: PQ_FUSED(PQ_PRO_EMBED) break;
-    case PQ_PRO_SILU: PQ_FUSED(PQ_PRO_SILU) break;
-    case PQ_PRO_F32: PQ_FUSED(PQ_PRO_F32) break;
-    default: PQ_FUSED(PQ_PRO_CONV) break;
+    case PQ_PRO_Q8: PQ_FUSED(PQ_PRO_Q8); break;
+    case PQ_PRO_RESNORM: PQ_FUSED(PQ_PRO_RESNORM); break;
+    case PQ_PRO_NORM: PQ_FUSED(PQ_PRO_NORM); break;
+    case PQ_PRO_EMBED: PQ_FUSED(PQ_PRO_EMBED); break;
+    case PQ_PRO_SILU: PQ_FUSED(PQ_PRO_SILU); break;
+    case PQ_PRO_F32: PQ_FUSED(PQ_PRO_F32); break;
+    default: PQ_FUSED(PQ_PRO_CONV); break;
   }
 #undef PQ_FUSED
-#undef PQ_FUSED_R
-#undef PQ_FUSED_E
   return check_launch(who);
 }
 
@@ -726,7 +752,7 @@ extern "C" int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, c
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemv_fused: y_dtype %d", y_dtype);
   const pq_gemv_prologue &p = *pro;
   return launch_fused(pcodes, pscales, p, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, argmax_parts, nullptr, nullptr,
-                      gemv_shape(N, K), as_stream(stream), "pq_q8_gemv_fused");
+                      gemv_shape(N, K).R, as_stream(stream), "pq_q8_gemv_fused");
 }
 
 extern "C" int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
@@ -736,9 +762,7 @@ extern "C" int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *psc
   PQ_REQUIRE(aligned(dx, 4), PQ_ERR_ALIGN, "pq_q8_gemv_fused_swiglu: dx alignment");
   const int rc = check_fused_args(pcodes, pscales, pro, qx, 2 * F, K, "pq_q8_gemv_fused_swiglu");
   if (rc) return rc;
-  const int nch = nchunks(K);
-  const GemvShape g{64, nch < 8 ? nch : 8};
-  return launch_fused(pcodes, pscales, *pro, nullptr, 0, 2 * F, K, nullptr, qx, dx, g, as_stream(stream),
+  return launch_fused(pcodes, pscales, *pro, nullptr, 0, 2 * F, K, nullptr, qx, dx, 64, as_stream(stream),
                       "pq_q8_gemv_fused_swiglu");
 }
 

@@ -18,6 +18,8 @@
 #include "pq_host.h"
 #include "q8_common.h"
 
+#include <type_traits>
+
 namespace pq {
 
 // ------------------------------------------------------------------ quantizer
@@ -270,21 +272,26 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
   item(blockIdx.x, g0);
   GemmCur g1 = next(g0);
   GemmW w0, w1;
-  wload(w0, g0);
-  wload(w1, g1);
   int seg_k = -1, seg_c1 = 0, seg_p = -1;   // staged chunks [seg_k, min(seg_k + 8, seg_c1)), position block
   float yv[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) yv[r] = 0.0f;
-  for (;;) {
-    const GemmCur g2 = next(g1);
-    GemmW w2;
-    wload(w2, g2);
+  // One chunk step of the wave. Loads are issued in the order they are needed:
+  // a new segment's activations first, then (first step only) the weights of
+  // chunks 0 and 1, then the weights two chunks ahead -- so staging waits only
+  // on the activations. The first step is a separate copy (FIRST) so every
+  // wait the compiler places stays exact.
+  auto step = [&](auto FIRST) -> bool {
     const int c = g0.c;
     // activations and dx: the 8 chunks from c of position block p0 (uniform:
     // every wave of the workgroup walks the same chunk sequence)
-    if (seg_k < 0 || c < seg_k || c >= seg_k + kGemmSegChunks || c >= seg_c1 || g0.p0 != seg_p) {
-      if (seg_k >= 0) lds_barrier();   // every wave is done with the staged segment
+    const bool restage =
+        seg_k < 0 || c < seg_k || c >= seg_k + kGemmSegChunks || c >= seg_c1 || g0.p0 != seg_p;
+    const bool had = seg_k >= 0;
+    v4i av[8];
+    float dv[4];
+    const int t = threadIdx.x;
+    if (restage) {
       seg_k = c;
       seg_c1 = g0.c1;
       seg_p = g0.p0;
@@ -296,21 +303,21 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
       const int kb0 = seg_k * kCB * kQ;          // byte offset of the segment in a row
       const int kend = min(K, min(g0.c1, seg_k + kGemmSegChunks) * kCB * kQ);   // the item's part of it
       const int bend = kend / kQ;
-      const int t = threadIdx.x;
-      v4i av[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {              // 32 rows x 128 pieces of 16 B: thread t, pieces t + 512 i
         const int pc16 = t + i * kGemmThreads;
         const int p = pc16 >> 7, q = pc16 & 127;
         av[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, kb0 + q * 16 < kend ? p * K + kb0 + q * 16 : kRsrcOob, 0, 0);
       }
-      float dv[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {              // 32 positions x 64 blocks: thread t, entries t + 512 i
         const int e = t + i * kGemmThreads;
         const int p = e >> 6, b = seg_k * kCB + (e & 63);
         dv[i] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rdx, b < bend ? (p * nb + b) * 4 : kRsrcOob, 0, 0));
       }
+    }
+    auto stage_store = [&]() {
+      if (had) lds_barrier();   // every wave is done with the previous segment
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const int pc16 = t + i * kGemmThreads;
@@ -322,6 +329,21 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
         dxs[e & 63][e >> 6] = dv[i];
       }
       lds_barrier();
+    };
+    GemmCur g2;
+    GemmW w2;
+    if constexpr (decltype(FIRST)::value) {
+      // first step: only chunk 0's weights go out with the activations (a
+      // deeper prefetch from every CU queues ahead of them in memory)
+      wload(w0, g0);
+      stage_store();
+      wload(w1, g1);
+      g2 = next(g1);
+      wload(w2, g2);
+    } else {
+      g2 = next(g1);
+      wload(w2, g2);
+      if (restage) stage_store();
     }
     // chunk c of this wave's slice
     float a[16];
@@ -370,79 +392,99 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
         if (pos < T && row < N) ws[((size_t)c * T + pos) * N + row] = a[r];
       }
     }
-    if (!g1.ok) break;
+    if (!g1.ok) return false;
     g0 = g1;
     g1 = g2;
     w0 = w1;
     w1 = w2;
-  }
+    return true;
+  };
+  if (step(std::integral_constant<bool, true>{}))
+    while (step(std::integral_constant<bool, false>{})) {
+    }
 }
 
-// The tile-parallel form for mid-sized N (enough 64-row tiles to fill the
-// chip, too few 256-row groups for the walking form): workgroup = one 64-row
-// tile x 32 positions, 16 waves; wave w takes rows 32*(w&1).. and chunk
-// 8*rd + (w>>1) of round rd, so a round's 8 chunks load at once; the round's
-// activations (32 positions x 2048 K) and dx are staged in LDS and the 8 chunk
-// partials fold into y through LDS in chunk order. Same numerics.
+// The tile-parallel form (small and mid-sized N): a workgroup = S 32-row
+// slices x 32 positions, 8*S waves; wave w takes slice w % S and chunk
+// 8*rd + w / S of round rd, so a round's 8 chunks of every slice load at once.
+// Per round the 32 positions' activations (2048 K) and dx are loaded first,
+// then the wave's weights, so the staging waits only on the activations; the
+// 8 chunk partials then fold into y through LDS in chunk order (the partials
+// reuse the activation buffer once every wave has read it, which leaves room
+// for two workgroups per CU). Same numerics as the walking form.
 constexpr int kTileSlots = 8;
-constexpr int kTileThreads = 64 * 2 * kTileSlots;   // 1024
-constexpr size_t kTileLds = (size_t)kTileSlots * 2 * 16 * 64 * 4 + 32 * (size_t)kGemmARow + (size_t)kTileSlots * kCB * 32 * 4;
+constexpr size_t kTileActBytes = 32 * (size_t)kGemmARow;
+constexpr size_t kTileLds = kTileActBytes + (size_t)kTileSlots * kCB * 32 * 4;
 
-__global__ __launch_bounds__(kTileThreads) void q8_gemm_tile_kernel(const int8_t *__restrict__ pc,
-                                                                     const uint16_t *__restrict__ ps,
-                                                                     const int8_t *__restrict__ qx,
-                                                                     const float *__restrict__ dx,
-                                                                     void *__restrict__ y, int y_bf16, int N, int K,
-                                                                     int T) {
+template <int S>
+__global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const int8_t *__restrict__ pc,
+                                                                        const uint16_t *__restrict__ ps,
+                                                                        const int8_t *__restrict__ qx,
+                                                                        const float *__restrict__ dx,
+                                                                        void *__restrict__ y, int y_bf16, int N,
+                                                                        int K, int T) {
+  constexpr int NT = 64 * kTileSlots * S;
+  constexpr int APT = 32 * (kGemmSegK / 16) / NT;   // 16-byte activation pieces per thread per round
+  constexpr int DPT = 32 * kTileSlots * kCB / NT;   // dx entries per thread per round
+  static_assert(kTileSlots * S * 16 * 64 * 4 <= kTileActBytes, "partials must fit the activation buffer");
   extern __shared__ __align__(16) unsigned char gsm[];
-  float(*part)[2][16][64] = reinterpret_cast<float(*)[2][16][64]>(gsm);
-  int8_t(*as)[kGemmARow] = reinterpret_cast<int8_t(*)[kGemmARow]>(gsm + kTileSlots * 2 * 16 * 64 * 4);
-  float(*dxs)[32] = reinterpret_cast<float(*)[32]>(gsm + kTileSlots * 2 * 16 * 64 * 4 + 32 * kGemmARow);
+  int8_t(*as)[kGemmARow] = reinterpret_cast<int8_t(*)[kGemmARow]>(gsm);
+  float(*part)[S][16][64] = reinterpret_cast<float(*)[S][16][64]>(gsm);   // aliases as
+  float(*dxs)[32] = reinterpret_cast<float(*)[32]>(gsm + kTileActBytes);
   const int nb = K / kQ, nch = nchunks(K);
-  const int tile = blockIdx.x, p0 = blockIdx.z * 32;
+  const int p0 = blockIdx.z * 32;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int sub = wave & 1, slot = wave >> 1;
+  const int sub = wave % S, slot = wave / S;
   const int h = lane >> 5, l32 = lane & 31;
-  const int jt = sub * 32 + l32;
+  const int sl = blockIdx.x * S + sub;                 // 32-row slice
+  const bool live = sl * 32 < N;
+  const int tile = live ? sl >> 1 : 0, jt = (sl & 1) * 32 + l32;
   const int np = T - p0 < 32 ? T - p0 : 32;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t *>(pc + (size_t)tile * nb * kSlab), (short)0, nb * kSlab, kRsrcWord3);
+      const_cast<int8_t *>(pc + (size_t)tile * nb * kSlab), (short)0, live ? nb * kSlab : 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t *>(ps + (size_t)tile * nch * kTR * 8), (short)0, nch * kTR * 16, kRsrcWord3);
+      const_cast<uint16_t *>(ps + (size_t)tile * nch * kTR * 8), (short)0, live ? nch * kTR * 16 : 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int8_t *>(qx + (size_t)p0 * K), (short)0, np * K, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rdx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(dx + (size_t)p0 * nb), (short)0, np * nb * 4, kRsrcWord3);
   const int nrounds = (nch + kTileSlots - 1) / kTileSlots;
+  const int t = threadIdx.x;
   float yv[2] = {0.0f, 0.0f};
   for (int rd = 0; rd < nrounds; rd++) {
     const int rbase = rd * kTileSlots;
     const int c = rbase + slot;
     const bool valid = c < nch;
-    const int t = threadIdx.x;
-    // the round's activations (thread t: position t/32, 64 bytes) and dx
-    // (blocks 2*(t%32), +1), then this wave's weights
-    v4i av[4];
-    const int oa = (t >> 5) * K + rbase * kCB * kQ + (t & 31) * 64;
+    // the round's activations (piece q = t + NT*i: position q / 128, bytes
+    // 16*(q % 128) of the round's 2048) and dx, then this wave's weights
+    v4i av[APT];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      av[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, rbase * kCB * kQ + (t & 31) * 64 + 16 * i < K ? oa + 16 * i : kRsrcOob, 0, 0);
-    float dv[2];
+    for (int i = 0; i < APT; i++) {
+      const int q = t + NT * i, p = q >> 7, col = rbase * kCB * kQ + (q & 127) * 16;
+      av[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, col < K ? p * K + col : kRsrcOob, 0, 0);
+    }
+    float dv[DPT];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int b = rbase * kCB + 2 * (t & 31) + i;
-      dv[i] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rdx, b < nb ? ((t >> 5) * nb + b) * 4 : kRsrcOob, 0, 0));
+    for (int i = 0; i < DPT; i++) {
+      const int e = t + NT * i, p = e >> 6, b = rbase * kCB + (e & 63);
+      dv[i] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rdx, b < nb ? (p * nb + b) * 4 : kRsrcOob, 0, 0));
     }
     v4i wv[kCB];
     const int oc = valid ? c * kCB * kSlab + (h * kTR + jt) * 16 : kRsrcOob;
 #pragma unroll
     for (int i = 0; i < kCB; i++) wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, oc + i * kSlab, 0, kAuxNT);
     const v4i sv = __builtin_amdgcn_raw_buffer_load_b128(rs, valid ? (c * kTR + jt) * 16 : kRsrcOob, 0, 0);
-    if (rd > 0) lds_barrier();   // the previous round's as / dxs / part reads are done
+    if (rd > 0) lds_barrier();   // the previous round's fold reads of the partials are done
 #pragma unroll
-    for (int i = 0; i < 4; i++) *reinterpret_cast<v4i *>(&as[t >> 5][(t & 31) * 64 + 16 * i]) = av[i];
+    for (int i = 0; i < APT; i++) {
+      const int q = t + NT * i;
+      *reinterpret_cast<v4i *>(&as[q >> 7][(q & 127) * 16]) = av[i];
+    }
 #pragma unroll
-    for (int i = 0; i < 2; i++) dxs[2 * (t & 31) + i][t >> 5] = dv[i];
+    for (int i = 0; i < DPT; i++) {
+      const int e = t + NT * i;
+      dxs[e & 63][e >> 6] = dv[i];
+    }
     lds_barrier();
     float a[16];
 #pragma unroll
@@ -468,23 +510,24 @@ __global__ __launch_bounds__(kTileThreads) void q8_gemm_tile_kernel(const int8_t
         __builtin_amdgcn_sched_barrier(0);  // one MFMA result live at a time (register budget)
       }
     }
+    lds_barrier();   // every wave is done with the activations: the partials overwrite them
 #pragma unroll
     for (int r = 0; r < 16; r++) part[slot][sub][r][lane] = a[r];
     lds_barrier();
     const int n = nch - rbase < kTileSlots ? nch - rbase : kTileSlots;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
-      const int e = threadIdx.x + k * kTileThreads;
+      const int e = t + k * NT;
       const int s2 = e >> 10, r = (e >> 6) & 15, l = e & 63;
       for (int w = 0; w < n; w++) yv[k] = yv[k] + part[w][s2][r][l];
     }
   }
 #pragma unroll
   for (int k = 0; k < 2; k++) {
-    const int e = threadIdx.x + k * kTileThreads;
+    const int e = t + k * NT;
     const int s2 = e >> 10, r = (e >> 6) & 15, l = e & 63;
     const int pos = p0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-    const int row = tile * kTR + s2 * 32 + (l & 31);
+    const int row = (blockIdx.x * S + s2) * 32 + (l & 31);
     if (pos < T && row < N) {
       if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)pos * N + row] = f2bf(yv[k]);
       else reinterpret_cast<float *>(y)[(size_t)pos * N + row] = yv[k];
@@ -498,7 +541,14 @@ __global__ __launch_bounds__(256) void q8_gemm_fold_kernel(const float *__restri
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= TN) return;
   float v = 0.0f;
-  for (int c = 0; c < nch; c++) v = v + ws[(size_t)c * TN + i];
+  for (int c0 = 0; c0 < nch; c0 += 8) {   // 8 loads in flight, then their adds in chunk order
+    float p[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) p[k] = c0 + k < nch ? ws[(size_t)(c0 + k) * TN + i] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (c0 + k < nch) v = v + p[k];
+  }
   if (y_bf16) reinterpret_cast<uint16_t *>(y)[i] = f2bf(v);
   else reinterpret_cast<float *>(y)[i] = v;
 }
@@ -598,14 +648,29 @@ static int gemm_splits(int N, int K, int T, bool have_ws) {
   return cps;
 }
 
-static bool gemm_tile_form(int N, int T) {
-  const long long tb = (T + 31) / 32;
-  return (long long)ntiles(N) * tb >= 192 && (N + 255) / 256 * tb < 256;
+// Which form runs a T-wide GEMM: 1 = the walking form (persistent, split K
+// with a workspace), 2 = tile form over 64-row tiles, 3 = tile form over 32-row
+// slices. PQ_GEMM_FORM (1..3) overrides the choice.
+enum { kFormWalk = 1, kFormTile = 2, kFormSlice = 3 };
+// Measured on the LFM-style shapes (hidden 2048): 32-row slices win at one
+// position block with K <= 2048 (one round), the walking form for the LM head
+// and for deeper K at one position block (split over workgroups), 64-row
+// tiles for mid-sized N over many position blocks.
+static int gemm_form(int N, int K, int T) {
+  static int env = -1;
+  if (env < 0) {
+    const char *e = getenv("PQ_GEMM_FORM");
+    env = e ? atoi(e) : 0;
+  }
+  if (env >= kFormWalk && env <= kFormSlice) return env;
+  if (N >= 32768) return kFormWalk;
+  if (T <= 32) return K > kGemmSegK ? kFormWalk : kFormSlice;
+  return N >= 16384 ? kFormWalk : kFormTile;
 }
 
 extern "C" size_t pq_q8_gemm_workspace_bytes(int N, int K, int T) {
   if (N <= 0 || K <= 0 || K % kQ || T <= 0) return 0;
-  if (gemm_tile_form(N, T)) return 0;
+  if (gemm_form(N, K, T) != kFormWalk) return 0;
   const int nch = nchunks(K);
   return gemm_splits(N, K, T, true) < nch ? (size_t)nch * T * N * sizeof(float) : 0;
 }
@@ -628,10 +693,15 @@ extern "C" int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, cons
   PQ_REQUIRE(items < (1ll << 31), PQ_ERR_ARG, "pq_q8_gemm: N=%d T=%d too large", N, T);
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
   hipStream_t st = as_stream(stream);
-  if (gemm_tile_form(N, T)) {
-    // enough 64-row tiles, too few 256-row groups: the tile-parallel form
-    launch(q8_gemm_tile_kernel, dim3((unsigned)ntiles(N), 1, (unsigned)((T + 31) / 32)), dim3(kTileThreads), kTileLds,
-           st, pcodes, pscales, qx, dx, y, yb, N, K, T);
+  const int form = gemm_form(N, K, T);
+  if (form == kFormTile) {
+    launch(q8_gemm_tile_kernel<2>, dim3((unsigned)ntiles(N), 1, (unsigned)((T + 31) / 32)), dim3(64 * kTileSlots * 2),
+           kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
+    return check_launch("pq_q8_gemm");
+  }
+  if (form == kFormSlice) {
+    launch(q8_gemm_tile_kernel<1>, dim3((unsigned)((N + 31) / 32), 1, (unsigned)((T + 31) / 32)),
+           dim3(64 * kTileSlots), kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
     return check_launch("pq_q8_gemm");
   }
   const unsigned grid = (unsigned)(items < 256 ? items : 256);   // one persistent workgroup per CU
