@@ -203,6 +203,65 @@ __global__ __launch_bounds__(512) void q8_gemv_kernel(const int8_t *__restrict__
 // [nch][T][N] and q8_gemm_fold_kernel adds them in chunk order.
 // Weights and scales come through buffer resources (rows past N and absent
 // chunks read zeros, no branch).
+// One chunk (up to 8 blocks) of a 32 x 32 (position x row) MFMA tile into the
+// lane's 16 chunk partials: per block b one v_mfma_i32_32x32x32_i8 (A = the
+// activations AV(b), B = the weights w[b]), then a = fmaf(fl(dw*dx), (float)isum, a)
+// for the lane's 16 outputs (row = lane % 32, positions 8(r/4) + 4(lane/32) + r%4;
+// dx of block b at dxs[kb0 + b][position]). Block b+1's MFMA and LDS reads are
+// issued before block b's fold, so the matrix core and the LDS work while the
+// VALU folds; the fold order per output is unchanged.
+template <bool PIPE, typename AF>
+__device__ __forceinline__ void mfma_chunk(float *a, const v4i *w, const v4i sv, AF AV, const float (*dxs)[32],
+                                           int kb0, int h, int nbc) {
+  if constexpr (!PIPE) {   // one MFMA result live at a time (for a tight register budget)
+    const uint32_t sw[4] = {(uint32_t)sv.x, (uint32_t)sv.y, (uint32_t)sv.z, (uint32_t)sv.w};
+#pragma unroll
+    for (int i = 0; i < kCB; i++) {
+      if (i < nbc) {
+        v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(i), w[i], acc, 0, 0, 0);
+        const float dw = half_of(sw[i >> 1], i & 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[kb0 + i][8 * q + 4 * h]);
+          const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)acc[4 * q + k], a[4 * q + k]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  }
+  const uint32_t sw[4] = {(uint32_t)sv.x, (uint32_t)sv.y, (uint32_t)sv.z, (uint32_t)sv.w};
+  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  v16i acc[2];
+  float4 d[2][4];
+  if (nbc > 0) {
+    acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(0), w[0], zero, 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; q++) d[0][q] = *reinterpret_cast<const float4 *>(&dxs[kb0][8 * q + 4 * h]);
+  }
+#pragma unroll
+  for (int i = 0; i < kCB; i++) {
+    if (i + 1 < kCB && i + 1 < nbc) {
+      acc[(i + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(i + 1), w[i + 1], zero, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 4; q++) d[(i + 1) & 1][q] = *reinterpret_cast<const float4 *>(&dxs[kb0 + i + 1][8 * q + 4 * h]);
+    }
+    if (i < nbc) {
+      const float dw = half_of(sw[i >> 1], i & 1);
+      const v16i &ac = acc[i & 1];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float dq[4] = {d[i & 1][q].x, d[i & 1][q].y, d[i & 1][q].z, d[i & 1][q].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)ac[4 * q + k], a[4 * q + k]);
+      }
+    }
+  }
+}
+
 constexpr int kGemmWaves = 8;
 constexpr int kGemmThreads = 64 * kGemmWaves;
 constexpr int kGemmSegChunks = 8;                          // chunks of K staged at once
@@ -350,25 +409,9 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
 #pragma unroll
     for (int r = 0; r < 16; r++) a[r] = 0.0f;
     {
-      const uint32_t sw[4] = {(uint32_t)w0.s.x, (uint32_t)w0.s.y, (uint32_t)w0.s.z, (uint32_t)w0.s.w};
-#pragma unroll
-      for (int i = 0; i < kCB; i++) {
-        const int b = c * kCB + i;
-        if (b < nb) {
-          const int kb = b - seg_k * kCB;   // block within the staged segment
-          const v4i avv = *reinterpret_cast<const v4i *>(&as[l32][kb * kQ + 16 * h]);
-          v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(avv, w0.w[i], acc, 0, 0, 0);
-          const float dw = half_of(sw[i >> 1], i & 1);
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[kb][8 * q + 4 * h]);
-            const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)acc[4 * q + k], a[4 * q + k]);
-          }
-        }
-      }
+      const int kb0 = (c - seg_k) * kCB;   // the chunk's first block within the staged segment
+      auto AV = [&](int i) { return *reinterpret_cast<const v4i *>(&as[l32][(kb0 + i) * kQ + 16 * h]); };
+      mfma_chunk<true>(a, w0.w, w0.s, AV, dxs, kb0, h, min(kCB, nb - c * kCB));
     }
     const int row = g0.slice * 32 + l32;
     if (ws == nullptr) {
@@ -416,7 +459,7 @@ constexpr int kTileSlots = 8;
 constexpr size_t kTileActBytes = 32 * (size_t)kGemmARow;
 constexpr size_t kTileLds = kTileActBytes + (size_t)kTileSlots * kCB * 32 * 4;
 
-template <int S>
+template <int S, bool PIPE>
 __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const int8_t *__restrict__ pc,
                                                                         const uint16_t *__restrict__ ps,
                                                                         const int8_t *__restrict__ qx,
@@ -490,25 +533,9 @@ __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const
 #pragma unroll
     for (int r = 0; r < 16; r++) a[r] = 0.0f;
     if (valid) {
-      const uint32_t sw[4] = {(uint32_t)sv.x, (uint32_t)sv.y, (uint32_t)sv.z, (uint32_t)sv.w};
-#pragma unroll
-      for (int i = 0; i < kCB; i++) {
-        if (c * kCB + i < nb) {
-          const int kb = slot * kCB + i;
-          const v4i avv = *reinterpret_cast<const v4i *>(&as[l32][kb * kQ + 16 * h]);
-          v16i acc = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(avv, wv[i], acc, 0, 0, 0);
-          const float dw = half_of(sw[i >> 1], i & 1);
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[kb][8 * q + 4 * h]);
-            const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)acc[4 * q + k], a[4 * q + k]);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one MFMA result live at a time (register budget)
-      }
+      const int kb0 = slot * kCB;
+      auto AV = [&](int i) { return *reinterpret_cast<const v4i *>(&as[l32][(kb0 + i) * kQ + 16 * h]); };
+      mfma_chunk<PIPE>(a, wv, sv, AV, dxs, kb0, h, min(kCB, nb - c * kCB));
     }
     lds_barrier();   // every wave is done with the activations: the partials overwrite them
 #pragma unroll
@@ -695,13 +722,19 @@ extern "C" int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, cons
   hipStream_t st = as_stream(stream);
   const int form = gemm_form(N, K, T);
   if (form == kFormTile) {
-    launch(q8_gemm_tile_kernel<2>, dim3((unsigned)ntiles(N), 1, (unsigned)((T + 31) / 32)), dim3(64 * kTileSlots * 2),
+    launch(q8_gemm_tile_kernel<2, false>, dim3((unsigned)ntiles(N), 1, (unsigned)((T + 31) / 32)), dim3(64 * kTileSlots * 2),
            kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
     return check_launch("pq_q8_gemm");
   }
   if (form == kFormSlice) {
-    launch(q8_gemm_tile_kernel<1>, dim3((unsigned)((N + 31) / 32), 1, (unsigned)((T + 31) / 32)),
-           dim3(64 * kTileSlots), kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
+    // the pipelined fold holds two MFMA results (one workgroup per CU): worth it
+    // while there is at most one workgroup per CU anyway
+    if ((long long)((N + 31) / 32) * ((T + 31) / 32) <= 256)
+      launch(q8_gemm_tile_kernel<1, true>, dim3((unsigned)((N + 31) / 32), 1, (unsigned)((T + 31) / 32)),
+             dim3(64 * kTileSlots), kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
+    else
+      launch(q8_gemm_tile_kernel<1, false>, dim3((unsigned)((N + 31) / 32), 1, (unsigned)((T + 31) / 32)),
+             dim3(64 * kTileSlots), kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
     return check_launch("pq_q8_gemm");
   }
   const unsigned grid = (unsigned)(items < 256 ? items : 256);   // one persistent workgroup per CU

@@ -10,9 +10,9 @@
 // where db_g is the d of Q8_K block g/2 and qs its half g%2.
 //
 // The int32 group dots run lane-parallel; the fp32 chain is sequential per row
-// over all groups, so each workgroup owns 16 whole rows: 16 lanes per row
-// compute the group partials p_g into LDS, then one lane per row folds them in
-// group order.
+// over all groups, so each workgroup owns whole rows (8 rows of 32 lanes, or
+// 16 of 16 for short rows): the lanes compute the group partials p_g into
+// LDS, then one lane per row folds them in group order.
 //
 // Group dot without unpacking the codes to bytes: for a code dword w (16
 // weights), d_k = (w >> 2k) & 0x03030303 holds the codes of weights
@@ -28,8 +28,6 @@ namespace pq {
 constexpr int kTqGroup = 128;
 constexpr int kQ8K = 256;
 constexpr int kQ8KBytes = 292;
-constexpr int kTqRows = 16;     // rows per workgroup
-constexpr int kTqSlots = 16;    // lanes per row (group slots)
 
 // The activations' Q8_K row staged once per workgroup: permuted qs (dword k of
 // each 16 = x[k], x[k+4], x[k+8], x[k+12]), per-group sums from the bsums
@@ -65,58 +63,62 @@ __device__ __forceinline__ void tq2_stage_x(const uint8_t *__restrict__ xq, int 
   }
 }
 
-// GPL groups per lane per round (16*GPL groups = 2048*GPL of K).
-template <int GPL>
+// LPR lanes per row (16, 32 or 64), 256/LPR rows per workgroup. Lane gs of a row
+// reads the row's 16-byte pieces gs, gs + LPR, ... (a row's lanes cover
+// 16*LPR contiguous bytes per load, whole cache lines): piece p is half p % 2 of group p / 2, so lanes
+// gs and gs ^ 1 hold the two halves of the same groups; their exact int32
+// half-dots add across the pair, and the even lane forms the group partial.
+// PPL pieces per lane per round (LPR*PPL pieces = 64*LPR*PPL of K).
+template <int LPR, int PPL>
 __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict__ codes,
                                                         const uint16_t *__restrict__ scales,
                                                         const uint8_t *__restrict__ xq, float *__restrict__ y, int N,
                                                         int K) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const int ng = K / kTqGroup;
+  const int ng = K / kTqGroup, npc = 2 * ng;                 // groups, 16-byte pieces per row
   int *xperm = reinterpret_cast<int *>(smem);                  // K bytes, permuted
   int *gsum = reinterpret_cast<int *>(smem + K);               // [ng] sum of qs over the group
   float *db = reinterpret_cast<float *>(gsum + ng);            // [ng] Q8_K d of the group's block
-  float *pg = db + ng;                                         // [16 rows][ng] group partials
+  float *pg = db + ng;                                         // [256/LPR rows][ng] group partials
   const int tid = threadIdx.x;
-  const int r = tid / kTqSlots, gs = tid % kTqSlots;
-  const int row = blockIdx.x * kTqRows + r;
+  const int r = tid / LPR, gs = tid % LPR;
+  const int row = blockIdx.x * (256 / LPR) + r;
   const bool live = row < N;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(codes + (size_t)(live ? row : 0) * (K / 4)), (short)0, live ? K / 4 : 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(scales + (size_t)(live ? row : 0) * ng), (short)0, live ? ng * 2 : 0, kRsrcWord3);
-  for (int g0 = 0; g0 < ng; g0 += kTqSlots * GPL) {
-    // this round's codes (32 B per group) and scales, before anything waits
-    v4i c[GPL][2];
-    uint32_t sc[GPL];
+  for (int p0 = 0; p0 < npc; p0 += LPR * PPL) {
+    // this round's codes (16 B per piece) and, on even lanes, the scale pair
+    // of each piece's group, before anything waits
+    v4i c[PPL];
+    uint32_t sc[PPL];
 #pragma unroll
-    for (int j = 0; j < GPL; j++) {
-      const int g = g0 + j * kTqSlots + gs;
-      const int off = g < ng ? g * 32 : kRsrcOob;
-      c[j][0] = __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0);
-      c[j][1] = __builtin_amdgcn_raw_buffer_load_b128(rc, off + 16, 0, 0);
-      sc[j] = __builtin_amdgcn_raw_buffer_load_b32(rsc, g < ng ? (g & ~1) * 2 : kRsrcOob, 0, 0);
+    for (int j = 0; j < PPL; j++) {
+      const int pc = p0 + j * LPR + gs, g = pc >> 1;
+      c[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, pc < npc ? pc * 16 : kRsrcOob, 0, 0);
+      sc[j] = (gs & 1) == 0 ? __builtin_amdgcn_raw_buffer_load_b32(rsc, pc < npc ? (g & ~1) * 2 : kRsrcOob, 0, 0) : 0u;
     }
-    if (g0 == 0) {
+    if (p0 == 0) {
       tq2_stage_x(xq, K, xperm, gsum, db);
       __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < GPL; j++) {
-      const int g = g0 + j * kTqSlots + gs;
-      if (g < ng) {
-        const uint32_t w[8] = {(uint32_t)c[j][0].x, (uint32_t)c[j][0].y, (uint32_t)c[j][0].z, (uint32_t)c[j][0].w,
-                               (uint32_t)c[j][1].x, (uint32_t)c[j][1].y, (uint32_t)c[j][1].z, (uint32_t)c[j][1].w};
-        const int *xp = xperm + g * (kTqGroup / 4);
-        int sacc = 0;
+    for (int j = 0; j < PPL; j++) {
+      const int pc = p0 + j * LPR + gs, g = pc >> 1;
+      const uint32_t w[4] = {(uint32_t)c[j].x, (uint32_t)c[j].y, (uint32_t)c[j].z, (uint32_t)c[j].w};
+      const int *xp = xperm + (pc < npc ? pc : 0) * 16;
+      int sacc = 0;
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-          const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * q);
-          sacc = __builtin_amdgcn_sdot4((int)(w[q] & 0x03030303u), xv.x, sacc, false);
-          sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 2) & 0x03030303u), xv.y, sacc, false);
-          sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 4) & 0x03030303u), xv.z, sacc, false);
-          sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 6) & 0x03030303u), xv.w, sacc, false);
-        }
+      for (int q = 0; q < 4; q++) {
+        const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * q);
+        sacc = __builtin_amdgcn_sdot4((int)(w[q] & 0x03030303u), xv.x, sacc, false);
+        sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 2) & 0x03030303u), xv.y, sacc, false);
+        sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 4) & 0x03030303u), xv.z, sacc, false);
+        sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 6) & 0x03030303u), xv.w, sacc, false);
+      }
+      sacc += __shfl_xor(sacc, 1, 64);   // the group's two halves
+      if ((gs & 1) == 0 && pc < npc) {
         const int isum = sacc - gsum[g];
         const float t = h2f((uint16_t)(sc[j] >> (16 * (g & 1)))) * db[g];
         pg[r * ng + g] = t * (float)isum;
@@ -204,12 +206,33 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
              "pq_tq2_gemv: N=%d K=%d (K a multiple of 256, at most 32768)", N, K);
   PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
   const int ng = K / kTqGroup;
-  const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)kTqRows * ng * 4;
-  const dim3 grid((unsigned)((N + kTqRows - 1) / kTqRows)), block(kTqRows * kTqSlots);
   hipStream_t st = as_stream(stream);
-  const int gpl = (ng + kTqSlots - 1) / kTqSlots;   // groups per lane for one round
-  if (gpl <= 2) launch(tq2_gemv_kernel<2>, grid, block, lds, st, codes, scales, xq, y, N, K);
-  else if (gpl <= 4) launch(tq2_gemv_kernel<4>, grid, block, lds, st, codes, scales, xq, y, N, K);
-  else launch(tq2_gemv_kernel<6>, grid, block, lds, st, codes, scales, xq, y, N, K);
+  // 32 lanes per row (8 rows per workgroup) when the rows are long enough to
+  // give them 4 pieces each; PPL covers a row in one round up to K = 12288
+  static int env = -1;
+  if (env < 0) {
+    const char *e = getenv("PQ_TQ2_LPR");
+    env = e ? atoi(e) : 0;
+  }
+  const int lpr = env == 16 || env == 32 || env == 64 ? env : (2 * ng >= 64 ? 32 : 16);
+  const int ppl = (2 * ng + lpr - 1) / lpr;   // pieces per lane for one round
+  const int rows = 256 / lpr;
+  const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)rows * ng * 4;
+  const dim3 grid((unsigned)((N + rows - 1) / rows)), block(256);
+#define PQ_TQ2(L, P) launch(tq2_gemv_kernel<L, P>, grid, block, lds, st, codes, scales, xq, y, N, K)
+  if (lpr == 16) {
+    if (ppl <= 4) PQ_TQ2(16, 4);
+    else if (ppl <= 8) PQ_TQ2(16, 8);
+    else PQ_TQ2(16, 12);
+  } else if (lpr == 32) {
+    if (ppl <= 2) PQ_TQ2(32, 2);
+    else if (ppl <= 4) PQ_TQ2(32, 4);
+    else PQ_TQ2(32, 6);
+  } else {
+    if (ppl <= 1) PQ_TQ2(64, 1);
+    else if (ppl <= 2) PQ_TQ2(64, 2);
+    else PQ_TQ2(64, 3);
+  }
+#undef PQ_TQ2
   return check_launch("pq_tq2_gemv");
 }
