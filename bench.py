@@ -67,17 +67,20 @@ def graph_of(torch, fn):
 
 
 def timed_replay(torch, g, stream, reps=1):
-    """Milliseconds per replay of g, HIP events on the launch stream."""
+    """Milliseconds per replay of g, HIP events on the launch stream: two
+    untimed replays (clocks settle), then the median of reps timed replays."""
     from pulsar_amd.hiptime import Event
-    a, b = Event(), Event()
-    g.replay()
-    torch.cuda.synchronize()
-    a.record(stream)
-    for _ in range(reps):
+    for _ in range(2):
         g.replay()
-    b.record(stream)
     torch.cuda.synchronize()
-    return a.elapsed_ms(b) / reps
+    ev = [Event() for _ in range(reps + 1)]
+    ev[0].record(stream)
+    for i in range(reps):
+        g.replay()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    t = sorted(ev[i].elapsed_ms(ev[i + 1]) for i in range(reps))
+    return t[len(t) // 2]
 
 
 def gemv_bytes(N, K, out):
@@ -330,7 +333,7 @@ def main():
     nper = 30
     for (name, N, K, o) in SHAPES:
         gsh = graph_of(torch, lambda: [gemv(copies[i % ncopy], name, N, K, o) for i in range(nper)])
-        per[name] = timed_replay(torch, gsh, stream, reps=3) / nper
+        per[name] = timed_replay(torch, gsh, stream, reps=5) / nper
         del gsh
 
     step_bytes = sum(gemv_bytes(N, K, o) for (_, N, K, o) in SHAPES)

@@ -116,11 +116,10 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
 #pragma unroll
     for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
     const float dq = a / 127.0f;
-    int qv = 0;
-    if (dq != 0.0f) {
-      qv = (int)__builtin_rintf(v / dq);
-      qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
-    }
+    // d = 0 only when every |x| of the block is below 127 * 2^-149: dividing
+    // by 1 then gives q = 0 as the zero-block rule does, with no branch
+    int qv = (int)__builtin_rintf(v / (dq != 0.0f ? dq : 1.0f));
+    qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
     const size_t K = (size_t)nh * kHD;
     qx[(size_t)t * K + h * kHD + d] = (int8_t)qv;
     if ((d & 31) == 0) dx[(size_t)t * (K / 32) + (h * kHD + d) / 32] = dq;

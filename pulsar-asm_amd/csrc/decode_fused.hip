@@ -127,13 +127,14 @@ __device__ __forceinline__ void quant_lds(const float *v, int e0, int8_t *xs, fl
   uint32_t w[E / 4];
 #pragma unroll
   for (int i = 0; i < E / 4; i++) w[i] = 0u;
+  // d = 0 only when every |x| of the block is below 127 * 2^-149: dividing by 1
+  // then gives q = 0 as the zero-block rule does, and the E divisions carry no
+  // branch (they overlap)
+  const float dd = d != 0.0f ? d : 1.0f;
 #pragma unroll
   for (int i = 0; i < E; i++) {
-    int q = 0;
-    if (d != 0.0f) {
-      q = (int)__builtin_rintf(v[i] / d);
-      q = q > 127 ? 127 : (q < -127 ? -127 : q);
-    }
+    int q = (int)__builtin_rintf(v[i] / dd);
+    q = q > 127 ? 127 : (q < -127 ? -127 : q);
     w[i >> 2] |= (uint32_t)(uint8_t)q << (8 * (i & 3));
   }
   store_q8_lds<E>(w, e0, xs);
@@ -348,11 +349,8 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
       const float o = bf2f(f2bf((a * sg) * u));
       const float m = wave_max(lane < 32 ? fabsf(o) : 0.0f);
       const float d = m / 127.0f;
-      int q = 0;
-      if (d != 0.0f) {
-        q = (int)__builtin_rintf(o / d);
-        q = q > 127 ? 127 : (q < -127 ? -127 : q);
-      }
+      int q = (int)__builtin_rintf(o / (d != 0.0f ? d : 1.0f));   // d = 0: the block is all zero
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
       if (lane < 32) qo[32 * tile + lane] = (int8_t)q;
       if (lane == 0) dqo[tile] = d;
     }
@@ -618,11 +616,8 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
 #pragma unroll
     for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
     const float dq = a / 127.0f;
-    int qv = 0;
-    if (dq != 0.0f) {
-      qv = (int)__builtin_rintf(v / dq);
-      qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
-    }
+    int qv = (int)__builtin_rintf(v / (dq != 0.0f ? dq : 1.0f));   // dq = 0: the block is all zero
+    qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
     qx[hq * kHDf + lane] = (int8_t)qv;
     if ((lane & 31) == 0) dx[(hq * kHDf + lane) / 32] = dq;
   }

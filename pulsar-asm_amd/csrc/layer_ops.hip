@@ -54,13 +54,11 @@ __device__ __forceinline__ void quant_store(const float *v, int8_t *qx, float *d
   for (int o = 1; o < 32 / E; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
   const float d = a / 127.0f;
   int8_t q[E];
+  const float dd = d != 0.0f ? d : 1.0f;   // d = 0: the block is all zero (q = 0), no branch
 #pragma unroll
   for (int i = 0; i < E; i++) {
-    int t = 0;
-    if (d != 0.0f) {
-      t = (int)__builtin_rintf(v[i] / d);
-      t = t > 127 ? 127 : (t < -127 ? -127 : t);
-    }
+    int t = (int)__builtin_rintf(v[i] / dd);
+    t = t > 127 ? 127 : (t < -127 ? -127 : t);
     q[i] = (int8_t)t;
   }
 #pragma unroll

@@ -44,11 +44,8 @@ __global__ __launch_bounds__(256) void q8_quant_kernel(const TX *__restrict__ x,
 #pragma unroll
   for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
   const float d = a / 127.0f;
-  int q = 0;
-  if (d != 0.0f) {
-    q = (int)__builtin_rintf(v / d);
-    q = q > 127 ? 127 : (q < -127 ? -127 : q);
-  }
+  int q = (int)__builtin_rintf(v / (d != 0.0f ? d : 1.0f));   // d = 0: the block is all zero (q = 0)
+  q = q > 127 ? 127 : (q < -127 ? -127 : q);
   if (valid) {
     qx[blk * kQ + j] = (int8_t)q;
     if (j == 0) dx[blk] = d;
