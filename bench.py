@@ -224,6 +224,49 @@ def prefill_gemm_bench(pq, torch, dev, g, T=512, chunk=32, reps=3, rotate_mb=600
             "single_launch_int8_peak_frac": round(ops / (ms_full * 1e-3) / 1e12 / 5000.0, 4)}
 
 
+def ref_numerics_bench(pq, torch, dev, g, reps=20, rotate_mb=700):
+    """The config-2 step through the reference-numerics GEMV (pq_q8r_gemv: the
+    reference's own order, bf16 x, fp32 weight scales, row-major codes),
+    weights rotated over > 256 MB. Bytes per step: codes + fp32 scales + the
+    bf16 x + y."""
+    set_bytes = sum(N * K + N * (K // 32) * 4 for (_, N, K, _) in SHAPES)
+    ncopy = max(2, math.ceil(rotate_mb * 1e6 / set_bytes))
+    copies = []
+    for _ in range(ncopy):
+        ws = {}
+        for (name, N, K, _) in SHAPES:
+            ws[name] = (torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g),
+                        torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01)
+        copies.append(ws)
+    xs = {K: torch.randn(K, device=dev, generator=g).to(torch.bfloat16) for K in (2048, 8192)}
+    outs = {name: torch.empty(N, dtype=torch.float32 if o == "f32" else torch.bfloat16, device=dev)
+            for (name, N, K, o) in SHAPES}
+    stream = pq.stream_ptr()
+
+    def gemv(ws, name, N, K, o):
+        c, sc = ws[name]
+        pq.q8r_gemv(c, sc, xs[K], out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name])
+
+    def step(i):
+        for (name, N, K, o) in SHAPES:
+            gemv(copies[i % ncopy], name, N, K, o)
+
+    gr = graph_of(torch, lambda: [step(i) for i in range(reps)])
+    ms = timed_replay(torch, gr, stream, 3) / reps
+    del gr
+    per = {}
+    for (name, N, K, o) in SHAPES:
+        gsh = graph_of(torch, lambda: [gemv(copies[i % ncopy], name, N, K, o) for i in range(30)])
+        per[name] = round(timed_replay(torch, gsh, stream, 5) / 30 * 1e3, 2)
+        del gsh
+    nbytes = sum(N * K + N * (K // 32) * 4 + 2 * K + N * (4 if o == "f32" else 2) for (_, N, K, o) in SHAPES)
+    del copies
+    torch.cuda.empty_cache()
+    return {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "per_shape_us": per,
+            "weight_copies_rotated": ncopy}
+
+
 def ternary_codes(torch, N, K, dev, g):
     """Weights uniform in {-1, 0, +1}: codes {0, 1, 2} packed four per byte."""
     c = torch.randint(0, 3, (N, K // 4, 4), dtype=torch.uint8, device=dev, generator=g)
@@ -381,6 +424,7 @@ def main():
         line["decode"] = decode_bench(pq)
         line["prefill_gemm"] = prefill_gemm_bench(pq, torch, dev, g)
         line["ternary_gemv"] = ternary_bench(pq, torch, dev, g)
+        line["ref_numerics_gemv"] = ref_numerics_bench(pq, torch, dev, g)
     print(json.dumps(line))
 
 

@@ -103,6 +103,21 @@ size_t pq_q8_gemm_workspace_bytes(int N, int K, int T);
 int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
                   void *y, int y_dtype, int N, int K, int T, void *ws, size_t ws_bytes, void *stream);
 
+/* The reference's own GEMV numerics (R2), the order of its CPU transcription
+ * (cpuchk_run, lfm3_nanode.cu:4658-4684): codes int8 [N][K] row-major and an
+ * fp32 scale per 32-block [N][K/32] (the .lfm3q8 tensors, untiled); x bf16
+ * [T][K] position-first; y [T][N] bf16 or fp32. Per output: chunks of 2048 of
+ * K (all of K when K is not a multiple of 2048), 32 leaves per chunk (leaf L
+ * folds blocks L, L+32, ...: dot = fmaf((float)c_j, x_j, dot) over j
+ * ascending, acc = fmaf(s_b, dot, acc)), the shfl_down tree 16..1 over the
+ * leaves, chunk partials summed in order from 0. K a multiple of 32, and of
+ * 2048 above 8192. Replaces q8_partial<bf16, FMA=1> + k_combine_bf /
+ * k_combine_f (lfm3_nanode.cu:222-374) as gemv / gemv_f call them
+ * (1916-1966, 3634-3663); T > 1 gives the tiled prefill twin's bits
+ * (q8_partial_TLb, 4051-4509) on the shapes that use it. */
+int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint16_t *x, void *y, int y_dtype, int N,
+                int K, int T, void *stream);
+
 /* ======================================================= layer operations
  * bf16 activations are raw uint16 bits. T positions are rows of the given
  * stride (position-first). Each op rounds once to bf16 where the reference's

@@ -352,6 +352,53 @@ void orc_q8_gemv_a11(const int8_t *W, const float *S, const float *x, float *y, 
   }
 }
 
+/* R2, the reference's own GEMV numerics (q8_partial<bf16, FMA=1> and
+ * k_combine_bf / k_combine_f, lfm3_nanode.cu:222-374, with the chunk rule of
+ * pick(), 1750-1782): x is bf16 widened to fp32, weight scales are fp32.
+ * Per chunk of KC = 2048 of K (K >= 2048 and K % 2048 == 0; otherwise all of
+ * K): leaf L = 0..31 folds blocks b = L, L+32, ... of the chunk in ascending
+ * order, each block's dot an fmaf chain over its 32 codes ascending from 0
+ * (274-323), acc_L = fmaf(s_b, dot_b, acc_L) from 0; the chunk partial is the
+ * shfl_down tree over the leaves, offsets 16, 8, 4, 2, 1 with
+ * v_i = v_i + v_{i+o} (326); y = ((0 + p_0) + p_1) + ... over the chunks
+ * ascending (338-345). The tiled prefill twin (q8_partial_TLb, 4051-4509, and
+ * its transcription cpuchk_run, 4658-4684) runs only on single-chunk shapes
+ * (pf_tilable, 4533-4542) and gives the same bits: its bit-reversed leaf
+ * order with the binary counter is this tree. y[t][r] for T positions. */
+static float q8r_row(const int8_t *w, const float *s, const float *x, int K) {
+  const int KC = (K >= 2048 && K % 2048 == 0) ? 2048 : K;
+  const int nbc = KC / ORC_QBLK;
+  float y = 0.0f;
+  for (int c = 0; c < K / KC; c++) {
+    float leaf[32];
+    for (int L = 0; L < 32; L++) {
+      float acc = 0.0f;
+      for (int b = L; b < nbc; b += 32) {
+        const int k0 = c * KC + b * ORC_QBLK;
+        float dot = 0.0f;
+        for (int j = 0; j < ORC_QBLK; j++) dot = fmaf((float)w[k0 + j], x[k0 + j], dot);
+        acc = fmaf(s[c * nbc + b], dot, acc);
+      }
+      leaf[L] = acc;
+    }
+    for (int o = 16; o > 0; o >>= 1)
+      for (int i = 0; i < o; i++) leaf[i] = leaf[i] + leaf[i + o];
+    y = y + leaf[0];
+  }
+  return y;
+}
+
+void orc_q8r_gemm(const int8_t *W, const float *S, const uint16_t *x, float *y, int N, int K, int T) {
+  const int nb = K / ORC_QBLK;
+  float *xf = (float *)malloc(sizeof(float) * (size_t)K * T);
+  for (size_t i = 0; i < (size_t)K * T; i++) xf[i] = orc_bf2f(x[i]);
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int r = 0; r < N; r++)
+    for (int t = 0; t < T; t++)
+      y[(size_t)t * N + r] = q8r_row(W + (size_t)r * K, S + (size_t)r * nb, xf + (size_t)t * K, K);
+  free(xf);
+}
+
 /* Exact value of the quantized product, sum_b (S_b*dx_b as real) * isum_b, in
  * double (every term is exact in double: S_b and dx_b have 11 and 24 bit
  * mantissas, isum_b < 2^20; the sum rounds at most nb times at 2^-53). */

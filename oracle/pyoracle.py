@@ -173,6 +173,18 @@ def q8_gemv_a11(W, S32, x):
     return y
 
 
+def q8r_gemm(W, S32, xb):
+    """R2 (the reference's GEMV order): codes [N][K], fp32 scales [N][K/32],
+    x bf16 bits [T][K] (or [K]) -> y fp32 [T][N] (or [N])."""
+    N, K = W.shape
+    xb2 = np.ascontiguousarray(xb, np.uint16).reshape(-1, K)
+    T = xb2.shape[0]
+    y = np.empty((T, N), np.float32)
+    lib().orc_q8r_gemm(_p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(S32, np.float32)), _p(xb2), _p(y),
+                       C.c_int(N), C.c_int(K), C.c_int(T))
+    return y if np.ndim(xb) == 2 else y[0]
+
+
 def q8_gemv_exact(W, S, qx, dx):
     N, K = W.shape
     y = np.empty(N, np.float64)

@@ -1,0 +1,158 @@
+// q8r.hip -- the reference's own Q8_0 GEMV numerics (R2) on gfx950.
+//
+// The arithmetic of q8_partial<bf16, FMA=1> + k_combine_bf / k_combine_f
+// (lfm3_nanode.cu:222-374), as gemv / gemv_f call them (1916-1966,
+// 3634-3663), on the reference's untiled data: codes int8 [N][K] row-major and
+// one fp32 scale per 32-block [N][K/32] (the .lfm3q8 tensors), x bf16 [T][K]
+// position-first, y [T][N] bf16 or fp32. Per output (row r, position t):
+//   chunks of KC = 2048 of K (all of K when K is not a multiple of 2048);
+//   in each chunk, leaf L = 0..31 folds blocks L, L+32, ... ascending:
+//     dot = fmaf((float)c_j, x_j, dot) over the block's 32 codes, from 0,
+//     acc = fmaf(s_b, dot, acc), from 0;
+//   the chunk partial is the shfl_down tree over the leaves (offsets 16, 8,
+//   4, 2, 1: v_i = v_i + v_{i+o});
+//   y = ((0 + p_0) + p_1) + ... over the chunks; out = bf16(y) or y.
+//
+// As in the reference, 32 lanes own a row and lane L owns leaf L, so a row's
+// lanes read 32 consecutive blocks (1 KB of whole cache lines) per load. Two
+// rows per wave, 8 rows per workgroup. x is staged once per workgroup as
+// fp32 in LDS with each 32-element block padded to 36 floats, so the 16-byte
+// reads of any 8 consecutive lanes cover all 32 banks. A lane's weight loads
+// for a chunk are issued before the previous chunk's arithmetic.
+#include "pq_device.h"
+#include "pq_host.h"
+#include "q8_common.h"
+
+namespace pq {
+
+constexpr int kRRows = 8;        // rows per workgroup
+constexpr int kRThreads = 32 * kRRows;
+constexpr int kRXStride = 36;    // LDS floats per staged 32-block of x
+
+__host__ __device__ inline int q8r_chunk(int K) { return (K >= 2048 && K % 2048 == 0) ? 2048 : K; }
+
+struct RBlocks {
+  v4i c[2 * 8];
+  float s[8];
+};
+
+// The lane's BPL blocks of chunk c (block L + 32 i of the chunk; blocks past
+// the chunk, and rows past N, read zeros: offsets past num_records).
+template <int BPL>
+__device__ __forceinline__ void q8r_load(RBlocks &B, __amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rs, int row,
+                                         int N, int K, int nb, int nbc, int c, int L) {
+#pragma unroll
+  for (int i = 0; i < BPL; i++) {
+    const int b = L + 32 * i;
+    const bool ok = b < nbc && row < N;
+    const int g = c * nbc + b;
+    const int oc = ok ? row * K + g * kQ : kRsrcOob;
+    B.c[2 * i] = __builtin_amdgcn_raw_buffer_load_b128(rc, oc, 0, kAuxNT);
+    B.c[2 * i + 1] = __builtin_amdgcn_raw_buffer_load_b128(rc, ok ? oc + 16 : kRsrcOob, 0, kAuxNT);
+    B.s[i] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (row * nb + g) * 4 : kRsrcOob, 0, 0));
+  }
+}
+
+template <int BPL>
+__device__ __forceinline__ float q8r_leaf(const RBlocks &B, const float *__restrict__ xs, int nbc, int c, int L) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < BPL; i++) {
+    const int b = L + 32 * i;
+    // a block past the chunk has zero codes and scale: fmaf(0, 0, acc) = acc
+    // exactly (acc is never -0), so it is folded without a branch
+    const float *xb = xs + (size_t)(b < nbc ? c * nbc + b : 0) * kRXStride;
+    const uint32_t w[8] = {(uint32_t)B.c[2 * i].x, (uint32_t)B.c[2 * i].y, (uint32_t)B.c[2 * i].z,
+                           (uint32_t)B.c[2 * i].w, (uint32_t)B.c[2 * i + 1].x, (uint32_t)B.c[2 * i + 1].y,
+                           (uint32_t)B.c[2 * i + 1].z, (uint32_t)B.c[2 * i + 1].w};
+    float dot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const float4 x4 = *reinterpret_cast<const float4 *>(xb + 4 * q);
+      dot = __builtin_fmaf((float)(int8_t)(w[q] & 0xffu), x4.x, dot);
+      dot = __builtin_fmaf((float)(int8_t)((w[q] >> 8) & 0xffu), x4.y, dot);
+      dot = __builtin_fmaf((float)(int8_t)((w[q] >> 16) & 0xffu), x4.z, dot);
+      dot = __builtin_fmaf((float)(int8_t)(w[q] >> 24), x4.w, dot);
+    }
+    acc = __builtin_fmaf(B.s[i], dot, acc);
+  }
+  return acc;
+}
+
+// BPL = blocks per leaf per chunk (ceil(chunk blocks / 32)).
+template <int BPL>
+__global__ __launch_bounds__(kRThreads) void q8r_gemv_kernel(const int8_t *__restrict__ codes,
+                                                             const float *__restrict__ scales,
+                                                             const uint16_t *__restrict__ x, void *__restrict__ y,
+                                                             int y_bf16, int N, int K) {
+  extern __shared__ __align__(16) float xs[];   // [nb][kRXStride]
+  const int t = blockIdx.y;
+  const int nb = K / kQ, KC = q8r_chunk(K), nbc = KC / kQ, nch = K / KC;
+  const int row = blockIdx.x * kRRows + (threadIdx.x >> 5);
+  const int L = threadIdx.x & 31;
+  // wave-uniform resources over the whole tensors; a row past N reads at an
+  // offset past them
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(codes), (short)0, N * K, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scales), (short)0, N * nb * 4, kRsrcWord3);
+  RBlocks B;
+  q8r_load<BPL>(B, rc, rs, row, N, K, nb, nbc, 0, L);
+  // x of position t: 8 bf16 per thread per step, widened into the padded blocks
+  const uint16_t *xt = x + (size_t)t * K;
+  for (int e = threadIdx.x * 8; e < K; e += kRThreads * 8) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(xt + e);
+    const uint32_t v[4] = {u.x, u.y, u.z, u.w};
+    float f[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      f[2 * k] = __uint_as_float(v[k] << 16);
+      f[2 * k + 1] = __uint_as_float(v[k] & 0xffff0000u);
+    }
+    float *d = xs + (size_t)(e >> 5) * kRXStride + (e & 31);
+    *reinterpret_cast<float4 *>(d) = make_float4(f[0], f[1], f[2], f[3]);
+    *reinterpret_cast<float4 *>(d + 4) = make_float4(f[4], f[5], f[6], f[7]);
+  }
+  __syncthreads();
+  float yv = 0.0f;
+  for (int c = 0; c < nch; c++) {
+    RBlocks Bn;
+    if (c + 1 < nch) q8r_load<BPL>(Bn, rc, rs, row, N, K, nb, nbc, c + 1, L);
+    float acc = q8r_leaf<BPL>(B, xs, nbc, c, L);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) acc = acc + __shfl_down(acc, o, 32);
+    yv = yv + acc;   // lane L = 0 holds the chunk partial
+    if (c + 1 < nch) B = Bn;
+  }
+  if (L == 0 && row < N) {
+    if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)t * N + row] = f2bf(yv);
+    else reinterpret_cast<float *>(y)[(size_t)t * N + row] = yv;
+  }
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint16_t *x, void *y, int y_dtype, int N,
+                           int K, int T, void *stream) {
+  PQ_REQUIRE(codes && scales && x && y, PQ_ERR_ARG, "pq_q8r_gemv: null pointer");
+  PQ_REQUIRE(N > 0 && T > 0 && K >= kQ && K % kQ == 0, PQ_ERR_ARG, "pq_q8r_gemv: N=%d K=%d T=%d (K a multiple of 32)",
+             N, K, T);
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8r_gemv: y_dtype %d", y_dtype);
+  PQ_REQUIRE(aligned(codes, 16) && aligned(scales, 4) && aligned(x, 16) && K % 8 == 0, PQ_ERR_ALIGN,
+             "pq_q8r_gemv: codes and x must be 16-byte aligned");
+  const int KC = q8r_chunk(K), bpl = (KC / kQ + 31) / 32;
+  PQ_REQUIRE(bpl <= 8, PQ_ERR_ARG, "pq_q8r_gemv: K=%d (above 8192, K must be a multiple of 2048)", K);
+  PQ_REQUIRE((long long)N * K < (1ll << 31), PQ_ERR_ARG, "pq_q8r_gemv: N=%d K=%d too large", N, K);
+  const size_t lds = (size_t)(K / kQ) * kRXStride * sizeof(float);
+  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_q8r_gemv: K=%d too large for LDS", K);
+  const dim3 grid((unsigned)((N + kRRows - 1) / kRRows), (unsigned)T), block(kRThreads);
+  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  hipStream_t st = as_stream(stream);
+  if (bpl <= 1) launch(q8r_gemv_kernel<1>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  else if (bpl <= 2) launch(q8r_gemv_kernel<2>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  else if (bpl <= 4) launch(q8r_gemv_kernel<4>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  else launch(q8r_gemv_kernel<8>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  return check_launch("pq_q8r_gemv");
+}

@@ -8,7 +8,7 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
@@ -109,6 +109,21 @@ def q8_gemm(w, qx, dx, out_dtype=DT_F32, out=None, split=True, ws=None):
                               out.data_ptr(), out_dtype, w.N, w.K, T, _ptr(ws) if nbytes else None, nbytes,
                               stream_ptr()), "pq_q8_gemm")
     return out
+
+
+def q8r_gemv(codes, scales, x, out_dtype=DT_BF16, out=None):
+    """The reference's own GEMV numerics (pq_q8r_gemv): codes int8 [N][K],
+    fp32 scales [N][K/32], x bf16 [K] or [T][K] -> y [N] or [T][N]."""
+    N, K = codes.shape
+    if scales.shape != (N, K // 32) or scales.dtype != torch.float32:
+        raise ValueError("scales must be fp32 [N][K/32]")
+    x2 = x.reshape(-1, K)
+    T = x2.shape[0]
+    if out is None:
+        out = torch.empty((T, N), dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=codes.device)
+    check(lib().pq_q8r_gemv(codes.data_ptr(), scales.data_ptr(), _bits16(x2), out.data_ptr(), out_dtype, N, K, T,
+                            stream_ptr()), "pq_q8r_gemv")
+    return out if x.dim() == 2 else out.reshape(N)
 
 
 # ---------------------------------------------------------------- layer ops

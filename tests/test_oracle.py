@@ -383,3 +383,108 @@ def test_oracle_reproduces_tiny_greedy(orc):
     m = orc.Model(**g["cfg"])
     assert m.greedy(np.array(g["prompt"], np.int32), len(g["ids"])).tolist() == g["ids"]
     m.close()
+
+
+# ------------------------------------------------- R2: the reference's own GEMV order
+def _bf16(v):
+    """float32 values that are bf16-exact -> their bf16 bits."""
+    u = np.asarray(v, np.float32).view(np.uint32)
+    assert np.all((u & 0xffff) == 0)
+    return (u >> 16).astype(np.uint16)
+
+
+def _leaf_case(values, K=1024):
+    """One row whose leaf L (= block L, K = 1024 gives one block per leaf) has
+    the value values[L] exactly: code 1 and x = v at the block's first element,
+    zeros elsewhere, scale 1."""
+    W = np.zeros((1, K), np.int8)
+    x = np.zeros(K, np.float32)
+    for L, v in enumerate(values):
+        W[0, 32 * L] = 1
+        x[32 * L] = v
+    return W, np.ones((1, K // 32), np.float32), _bf16(x)
+
+
+def test_r2_leaf_tree_order(orc):
+    """The chunk partial is the shfl_down tree 16, 8, 4, 2, 1 over the 32 leaves
+    (lfm3_nanode.cu:326). Case A separates it from a sequential fold, case B
+    from the ascending tree 1, 2, ..., 16 (closed forms by hand; 2^24 + 1 ties
+    to 2^24)."""
+    big = float(2 ** 24)
+    A = [big] + [1.0] * 31          # tree: 2^24 + 30; sequential: 2^24
+    y = orc.q8r_gemm(*_leaf_case(A))
+    assert y[0] == np.float32(big + 30)
+    B = [0.0] * 32                  # tree 16..1: 2^24; ascending tree: 2^24 + 2
+    B[0], B[16], B[24] = big, 1.0, 1.0
+    y = orc.q8r_gemm(*_leaf_case(B))
+    assert y[0] == np.float32(big)
+
+
+def test_r2_scale_fma_is_fused(orc):
+    """acc = fmaf(s_b, dot_b, acc) (lfm3_nanode.cu:322): leaf 0 of K = 2048 folds
+    blocks 0 and 32; block 0 leaves acc = -1, block 32 has s = 1 + 2^-22 and
+    dot = 1 + 2^-23, so the fused result 3*2^-23 + 2^-45 differs from the
+    unfused 3*2^-23. (The code*x products are exact in fp32, so the dot chain's
+    fusing cannot show.)"""
+    K = 2048
+    W = np.zeros((1, K), np.int8)
+    x = np.zeros(K, np.float32)
+    S = np.ones((1, K // 32), np.float32)
+    W[0, 0], x[0] = -1, 1.0                      # block 0: dot = -1
+    W[0, 32 * 32], x[32 * 32] = 1, 1.0           # block 32: dot = 1 + 2^-23
+    W[0, 32 * 32 + 1], x[32 * 32 + 1] = 1, 2.0 ** -23
+    S[0, 32] = np.float32(1 + 2.0 ** -22)
+    y = orc.q8r_gemm(W, S, _bf16(x))
+    assert y[0] == np.float32(3 * 2.0 ** -23 + 2.0 ** -45)
+    assert y[0] != np.float32(3 * 2.0 ** -23)
+
+
+def _r2_case(orc, seed, N, K, T=1):
+    W, S16 = orc.q8_weights(seed, N, K)
+    S = S16.view(np.float16).astype(np.float32)
+    xb = orc.f2bf(orc.gen_normal(seed + 3, T * K)).reshape(T, K)
+    return W, S, xb
+
+
+def test_r2_chunks_of_2048(orc):
+    """K a multiple of 2048: the chunk partials (each a 32-leaf tree over 64
+    blocks) sum from 0 in chunk order (pick(), lfm3_nanode.cu:1763, and
+    k_combine_*, 338-345) -- K = 8192 is the in-order sum of its four K = 2048
+    slices."""
+    W, S, xb = _r2_case(orc, 41, 19, 8192)
+    y = orc.q8r_gemm(W, S, xb[0])
+    acc = np.zeros(19, np.float32)
+    for c in range(4):
+        sl = slice(2048 * c, 2048 * (c + 1))
+        p = orc.q8r_gemm(np.ascontiguousarray(W[:, sl]), np.ascontiguousarray(S[:, 64 * c:64 * (c + 1)]),
+                         np.ascontiguousarray(xb[0, sl]))
+        acc = (acc + p).astype(np.float32)
+    assert np.array_equal(f32bits(y), f32bits(acc))
+
+
+@pytest.mark.parametrize("N,K", [(53, 2048), (29, 8192), (17, 7680), (11, 512)])
+def test_r2_vs_exact_and_reference_cpu(orc, N, K):
+    """Within 1e-5 of sum |terms| of the exact double result and of the
+    reference's own CPU GEMV (q8_gemv_cpu.c:29-58, oracle/_ref) on the same
+    fp32 scales and bf16 x."""
+    W, S, xb = _r2_case(orc, 50 + K, N, K)
+    x = orc.bf2f(xb[0])
+    y = orc.q8r_gemm(W, S, xb[0]).astype(np.float64)
+    terms = W.reshape(N, -1, 32).astype(np.float64) * x.reshape(-1, 32)
+    exact = (terms.sum(-1) * S).sum(-1)
+    den = (np.abs(terms).sum(-1) * np.abs(S)).sum(-1)
+    assert (np.abs(y - exact) / den).max() <= 1e-6
+    ref = orc.ref()
+    if ref is not None:
+        import ctypes as C
+        yr = np.empty(N, np.float32)
+        ref.ref_q8_gemv(W.ctypes.data_as(C.c_void_p), S.ctypes.data_as(C.c_void_p),
+                        x.ctypes.data_as(C.c_void_p), yr.ctypes.data_as(C.c_void_p), C.c_int(N), C.c_int(K))
+        assert (np.abs(y - yr) / den).max() <= 1e-5
+
+
+def test_r2_gemm_is_per_position(orc):
+    W, S, xb = _r2_case(orc, 61, 23, 2048, T=3)
+    Y = orc.q8r_gemm(W, S, xb)
+    for t in range(3):
+        assert np.array_equal(f32bits(Y[t]), f32bits(orc.q8r_gemm(W, S, xb[t])))
