@@ -26,6 +26,7 @@ extern "C" {
 #define PQ_ERR_WORKSPACE (-3)  /* workspace missing or too small                */
 #define PQ_ERR_LAUNCH (-4)     /* the HIP launch or a HIP runtime call failed   */
 #define PQ_ERR_STATE (-5)      /* engine state (context full, not loaded, ...)  */
+#define PQ_ERR_DATA (-6)       /* stored data failed its check (a blob's crc32)  */
 
 #define PQ_QBLK 32             /* Q8_0 block: 32 codes, one fp16 scale           */
 #define PQ_CHUNK_BLOCKS 8      /* R1 chunk: the fp32 partial covers 8 blocks     */
@@ -117,6 +118,35 @@ int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, const int8_t *q
  * (q8_partial_TLb, 4051-4509) on the shapes that use it. */
 int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint16_t *x, void *y, int y_dtype, int N,
                 int K, int T, void *stream);
+
+/* ============================================================ weight blob
+ * The .lfm3q8 file the reference's exporter writes (export_lfm3_q8.py) and
+ * load_blob reads (lfm3_nanode.cu:1219-1733): 8-byte magic "LFM3Q8\x01\x00",
+ * uint32 header length, a JSON header {cfg, table: [{name, dtype, ne, off,
+ * ncodes, nscales, crc}]}, then each tensor's payload (dtype 1: int8 codes
+ * then one fp32 scale per 32; 2: fp32; 3: bf16) with the zlib crc32 of its
+ * bytes. Host-side only: no GPU is needed to open or read one. */
+typedef struct pq_blob_tensor {
+  char name[128];
+  int dtype;          /* 1 Q8 (codes + fp32 scales), 2 fp32, 3 bf16 */
+  int ndim;
+  long long ne[4];    /* shape, as the table lists it ([N][K] for a Linear) */
+  long long ncodes;   /* payload bytes: codes (or the fp32 / bf16 values) */
+  long long nscales;  /* then the fp32 scales (dtype 1) */
+  unsigned crc;
+} pq_blob_tensor;
+void *pq_blob_open(const char *path);    /* NULL on error (pq_last_error) */
+int pq_blob_close(void *blob);
+int pq_blob_count(void *blob);
+int pq_blob_find(void *blob, const char *name);   /* table index, or -1 */
+int pq_blob_tensor_info(void *blob, int i, pq_blob_tensor *out);
+/* Tensor i's payload into host memory: ncodes bytes to codes, nscales bytes
+ * to scales; PQ_ERR_DATA when the crc32 of the bytes read differs from the
+ * table's (the reference's load-time check, 1358-1362). */
+int pq_blob_read(void *blob, int i, void *codes, void *scales);
+/* The header's "cfg" object, re-serialized as JSON (valid until close). */
+const char *pq_blob_config(void *blob);
+unsigned pq_crc32(unsigned crc, const void *data, size_t n);
 
 /* ======================================================= layer operations
  * bf16 activations are raw uint16 bits. T positions are rows of the given
@@ -306,6 +336,16 @@ int pq_engine_load_synthetic(void *engine);
 int pq_engine_set_q8(void *engine, int layer, int slot, const int8_t *codes, const uint16_t *scales);
 int pq_engine_set_f32(void *engine, int layer, int slot, const float *v, size_t n);
 int pq_engine_mark_loaded(void *engine);
+/* Every backbone tensor from an .lfm3q8 blob (the reference's load_blob,
+ * lfm3_nanode.cu:1404-1733, on the names layer_body reads, 3739-3856): each
+ * payload's crc32 is checked (PQ_ERR_DATA on a mismatch) on a reader thread
+ * that stays ahead of the uploads; q/k/v/gate_proj stack into the attention
+ * input GEMV, feed_forward.w1 / w3 into gate/up; fp32 weight scales are
+ * rounded to the engine's fp16 scales (exact for blobs written from fp16
+ * scales); the tied embedding must be Q8 (dtype 1). Shapes must match the
+ * engine's configuration; sliding-window attention layers are refused.
+ * Marks the engine loaded on success. */
+int pq_engine_load_blob(void *engine, const char *path);
 int pq_engine_reset(void *engine);
 /* Feed n tokens (prefill chunks); the greedy id after the last one and its
  * fp32 logits (either may be NULL) come back to the host. */

@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <memory>
+#include <string>
 #include <vector>
 
 #include "pq_host.h"
@@ -608,6 +609,148 @@ extern "C" int pq_engine_set_f32(void *h, int layer, int slot, const float *v, s
   float *dst = vec_slot(E, layer, slot, &want);
   PQ_REQUIRE(dst && n == want, PQ_ERR_ARG, "pq_engine_set_f32: layer %d slot %d expects %zu values", layer, slot, want);
   return upload_f32(E, dst, v, n);
+}
+
+// ------------------------------------------------------------ .lfm3q8 load
+// fp32 -> binary16 bits, round to nearest even (overflow to inf, NaN kept).
+static uint16_t host_f2h(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u, e = (u >> 23) & 0xffu, m = u & 0x7fffffu;
+  if (e == 0xff) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u | (m >> 13) : 0u));
+  const int ex = (int)e - 127 + 15;
+  if (ex >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (ex <= 0) {   // binary16 subnormal (or zero): shift the full mantissa, round to even
+    if (ex < -10) return (uint16_t)sign;
+    const uint32_t mm = m | 0x800000u;
+    const int sh = 14 - ex;
+    uint32_t q = mm >> sh;
+    const uint32_t rem = mm & ((1u << sh) - 1), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (q & 1))) q++;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t q = ((uint32_t)ex << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;   // a carry into the exponent is still right
+  return (uint16_t)(sign | q);
+}
+
+namespace {
+struct BlobSrc {
+  std::string name;
+  long long n0, n1;   // Q8: rows, columns; fp32: element count in n0
+};
+struct BlobTarget {
+  int layer, slot;
+  bool q8;
+  std::vector<BlobSrc> src;
+};
+}  // namespace
+
+// The reference's tensor names (layer_body, lfm3_nanode.cu:3739-3856; the
+// exporter's table) onto the engine's slots: q|k|v|gate_proj stack into the
+// attention layer's input GEMV, w1 (gate) and w3 (up) into gate/up; fp32
+// weight scales become the engine's fp16 scales (round to nearest even:
+// exact for blobs written from fp16 scales).
+static int load_blob(Engine &E, void *blob) {
+  const pq_model_cfg &c = E.c;
+  const long long H = c.hidden, F = c.ffn;
+  PQ_REQUIRE(!strstr(pq_blob_config(blob), "\"sliding_attention\""), PQ_ERR_ARG,
+             "pq_engine_load_blob: the blob has sliding-window attention layers, which this engine does not run");
+  auto LN = [](int l, const char *suf) { return "lfm.model.layers." + std::to_string(l) + "." + suf; };
+  std::vector<BlobTarget> T;
+  T.push_back({-1, 0, true, {{"lfm.model.embed_tokens.weight", c.vocab, H}}});
+  for (int l = 0; l < c.nlayers; l++) {
+    if (E.L[l].attn) {
+      T.push_back({l, 0, true, {{LN(l, "self_attn.q_proj.weight"), (long long)c.nh * c.hd, H},
+                                {LN(l, "self_attn.k_proj.weight"), (long long)c.nkv * c.hd, H},
+                                {LN(l, "self_attn.v_proj.weight"), (long long)c.nkv * c.hd, H},
+                                {LN(l, "self_attn.gate_proj.weight"), (long long)c.nh, H}}});
+      T.push_back({l, 1, true, {{LN(l, "self_attn.o_proj.weight"), H, (long long)c.nh * c.hd}}});
+      T.push_back({l, 8, false, {{LN(l, "self_attn.q_norm.weight"), c.hd, 0}}});
+      T.push_back({l, 9, false, {{LN(l, "self_attn.k_norm.weight"), c.hd, 0}}});
+    } else {
+      T.push_back({l, 0, true, {{LN(l, "conv.in_proj.weight"), 3 * H, H}}});
+      T.push_back({l, 1, true, {{LN(l, "conv.out_proj.weight"), H, H}}});
+      T.push_back({l, 10, false, {{LN(l, "conv.conv.weight"), H * c.ntaps, 0}}});
+    }
+    T.push_back({l, 2, true, {{LN(l, "feed_forward.w1.weight"), F, H}, {LN(l, "feed_forward.w3.weight"), F, H}}});
+    T.push_back({l, 3, true, {{LN(l, "feed_forward.w2.weight"), H, F}}});
+    T.push_back({l, 4, false, {{LN(l, "operator_norm.weight"), H, 0}}});
+    T.push_back({l, 5, false, {{LN(l, "post_operator_norm.weight"), H, 0}}});
+    T.push_back({l, 6, false, {{LN(l, "ffn_norm.weight"), H, 0}}});
+    T.push_back({l, 7, false, {{LN(l, "post_ffn_norm.weight"), H, 0}}});
+  }
+  T.push_back({-1, 1, false, {{"lfm.model.embedding_norm.weight", H, 0}}});
+  // every source present, with the dtype and shape its slot needs
+  std::vector<int> order;
+  for (const BlobTarget &t : T)
+    for (const BlobSrc &s : t.src) {
+      const int i = pq::blob_find(blob, s.name.c_str());
+      PQ_REQUIRE(i >= 0, PQ_ERR_ARG, "pq_engine_load_blob: the blob has no %s", s.name.c_str());
+      pq_blob_tensor ti;
+      PQ_TRY(pq_blob_tensor_info(blob, i, &ti));
+      long long elems = 1;
+      for (int d = 0; d < ti.ndim; d++) elems *= ti.ne[d];
+      if (t.q8) {
+        PQ_REQUIRE(ti.dtype == 1 && ti.ndim == 2 && ti.ne[0] == s.n0 && ti.ne[1] == s.n1, PQ_ERR_ARG,
+                   "pq_engine_load_blob: %s is dtype %d [%lld x %lld], the engine needs Q8 [%lld x %lld]",
+                   s.name.c_str(), ti.dtype, ti.ne[0], ti.ndim > 1 ? ti.ne[1] : 0, s.n0, s.n1);
+      } else {
+        PQ_REQUIRE(ti.dtype == 2 && elems == s.n0, PQ_ERR_ARG,
+                   "pq_engine_load_blob: %s is dtype %d with %lld values, the engine needs %lld fp32", s.name.c_str(),
+                   ti.dtype, elems, s.n0);
+      }
+      order.push_back(i);
+    }
+  // read ahead on a thread of its own while the tensors before convert and upload
+  pq::BlobReader rd(blob, order, 2);
+  std::vector<char> buf;
+  std::vector<int8_t> codes;
+  std::vector<uint16_t> sc16;
+  for (const BlobTarget &t : T) {
+    if (!t.q8) {
+      PQ_TRY(rd.take(buf));
+      size_t n = 0;
+      float *dst = vec_slot(E, t.layer, t.slot, &n);
+      PQ_REQUIRE(dst && n == (size_t)t.src[0].n0, PQ_ERR_ARG, "pq_engine_load_blob: slot %d of layer %d", t.slot,
+                 t.layer);
+      PQ_TRY(upload_f32(E, dst, reinterpret_cast<const float *>(buf.data()), n));
+      continue;
+    }
+    Q8Dev *q = q8_slot(E, t.layer, t.slot);
+    long long rows = 0;
+    for (const BlobSrc &s : t.src) rows += s.n0;
+    PQ_REQUIRE(q && q->N == rows && q->K == t.src[0].n1, PQ_ERR_ARG,
+               "pq_engine_load_blob: slot %d of layer %d holds [%d x %d]", t.slot, t.layer, q ? q->N : 0,
+               q ? q->K : 0);
+    codes.resize((size_t)rows * q->K);
+    sc16.resize((size_t)rows * (q->K / 32));
+    size_t r0 = 0;
+    for (const BlobSrc &s : t.src) {
+      PQ_TRY(rd.take(buf));
+      const size_t nc = (size_t)s.n0 * s.n1, ns = nc / 32;
+      memcpy(codes.data() + r0 * q->K, buf.data(), nc);
+      const float *sf = reinterpret_cast<const float *>(buf.data() + nc);
+      for (size_t k = 0; k < ns; k++) sc16[r0 * (q->K / 32) + k] = host_f2h(sf[k]);
+      r0 += (size_t)s.n0;
+    }
+    PQ_TRY(upload_q8(E, *q, codes.data(), sc16.data()));
+  }
+  return PQ_OK;
+}
+
+extern "C" int pq_engine_load_blob(void *h, const char *path) {
+  PQ_REQUIRE(h && path, PQ_ERR_ARG, "pq_engine_load_blob: null argument");
+  Engine &E = *static_cast<Engine *>(h);
+  void *blob = pq_blob_open(path);
+  if (!blob) return PQ_ERR_ARG;
+  E.loaded = false;
+  const int rc = load_blob(E, blob);
+  pq_blob_close(blob);
+  if (rc != PQ_OK) return rc;
+  E.loaded = true;
+  return PQ_OK;
 }
 
 extern "C" int pq_engine_mark_loaded(void *h) {

@@ -3,7 +3,11 @@
 // on the device, so a captured step replays unchanged.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
+
+#include <memory>
+#include <vector>
 
 namespace pq {
 
@@ -15,5 +19,25 @@ int attn_layer_decode_dev(const uint16_t *qkvg, const float *q_norm, const float
 
 // pq_argmax_parts that also appends the id: ids[ctr[0]++] = id, ctr[1]++.
 int argmax_parts_step(const float *parts, int nparts, int32_t *out, int32_t *ids, int32_t *ctr, hipStream_t st);
+
+// zlib-compatible crc32 (blob.cpp).
+uint32_t crc32_update(uint32_t crc, const void *data, size_t n);
+
+// Index of the blob tensor called name, or -1.
+int blob_find(void *blob, const char *name);
+
+// Reads the blob tensors listed in order (table indices) on a thread of its
+// own, each into a host buffer (codes then scales) with its crc checked, at
+// most depth ahead of the caller; take() hands them over in order.
+class BlobReader {
+ public:
+  BlobReader(void *blob, const std::vector<int> &order, size_t depth);
+  ~BlobReader();
+  int take(std::vector<char> &out);
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl;
+};
 
 }  // namespace pq

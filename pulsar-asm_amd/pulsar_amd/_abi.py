@@ -16,6 +16,12 @@ class ModelCfg(C.Structure):
                 ("seed", C.c_uint64), ("attn_mask", C.c_uint32), ("prefill_chunk", C.c_int)]
 
 
+class BlobTensor(C.Structure):
+    """pq_blob_tensor."""
+    _fields_ = [("name", C.c_char * 128), ("dtype", C.c_int), ("ndim", C.c_int), ("ne", C.c_longlong * 4),
+                ("ncodes", C.c_longlong), ("nscales", C.c_longlong), ("crc", C.c_uint)]
+
+
 class GemvPrologue(C.Structure):
     """pq_gemv_prologue."""
     _fields_ = [("kind", C.c_int), ("qx", C.c_void_p), ("dx", C.c_void_p), ("h", C.c_void_p), ("x_in", C.c_void_p),
@@ -63,6 +69,15 @@ SIGNATURES = {
     "pq_engine_set_q8": (I, [P, I, I, P, P]),
     "pq_engine_set_f32": (I, [P, I, I, P, Z]),
     "pq_engine_mark_loaded": (I, [P]),
+    "pq_engine_load_blob": (I, [P, C.c_char_p]),
+    "pq_blob_open": (P, [C.c_char_p]),
+    "pq_blob_close": (I, [P]),
+    "pq_blob_count": (I, [P]),
+    "pq_blob_find": (I, [P, C.c_char_p]),
+    "pq_blob_tensor_info": (I, [P, I, C.POINTER(BlobTensor)]),
+    "pq_blob_read": (I, [P, I, P, P]),
+    "pq_blob_config": (C.c_char_p, [P]),
+    "pq_crc32": (C.c_uint, [C.c_uint, P, Z]),
     "pq_engine_reset": (I, [P]),
     "pq_engine_feed": (I, [P, P, I, P, P]),
     "pq_engine_greedy": (I, [P, P, I, I, P]),

@@ -41,6 +41,10 @@ class Engine:
     def load_synthetic(self):
         check(lib().pq_engine_load_synthetic(self.h), "pq_engine_load_synthetic")
 
+    def load_blob(self, path):
+        """Every backbone tensor from an .lfm3q8 file (pq_engine_load_blob)."""
+        check(lib().pq_engine_load_blob(self.h, str(path).encode()), "pq_engine_load_blob")
+
     def set_q8(self, layer, slot, codes, scales):
         codes = np.ascontiguousarray(codes, np.int8)
         scales = np.ascontiguousarray(scales, np.uint16)
