@@ -267,6 +267,45 @@ def ref_numerics_bench(pq, torch, dev, g, reps=20, rotate_mb=700):
             "weight_copies_rotated": ncopy}
 
 
+def qlow_bench(pq, torch, dev, g, rotate_mb=600):
+    """The four layer GEMVs of the config-2 workload (q|k|v, o_proj, gate+up,
+    down) in the reference's Q4 and Q5 formats (pq_qlow_gemv), weights
+    rotated. Bytes: packed codes + half2 scales + bf16 x + bf16 y."""
+    shapes = [s_ for s_ in SHAPES if s_[0] != "lm_head"]
+    stream = pq.stream_ptr()
+    res = {}
+    for bits in (4, 5):
+        set_bytes = sum(pq.lib().pq_qlow_packed_codes_bytes(N, K, bits) + pq.lib().pq_qlow_packed_scales_bytes(N, K, bits)
+                        for (_, N, K, _) in shapes)
+        ncopy = max(2, math.ceil(rotate_mb * 1e6 / set_bytes))
+        copies = []
+        for _ in range(ncopy):
+            ws = {}
+            for (name, N, K, _) in shapes:
+                q = torch.randint(0, 2 ** bits, (N, K), dtype=torch.uint8, device=dev, generator=g)
+                sc = torch.randn((N, K // 32, 2), device=dev, generator=g).abs().mul(0.01).half().view(torch.int16)
+                ws[name] = pq.QlowWeight(q, sc, bits)
+                del q, sc
+            copies.append(ws)
+        xs = {K: torch.randn(K, device=dev, generator=g).to(torch.bfloat16) for K in (2048, 8192)}
+        outs = {name: torch.empty(N, dtype=torch.bfloat16, device=dev) for (name, N, K, _) in shapes}
+
+        def step(i):
+            for (name, N, K, _) in shapes:
+                pq.qlow_gemv(copies[i % ncopy][name], xs[K], out=outs[name])
+
+        reps = 20
+        gr = graph_of(torch, lambda: [step(i) for i in range(reps)])
+        ms = timed_replay(torch, gr, stream, 3) / reps
+        del gr, copies
+        torch.cuda.empty_cache()
+        nbytes = set_bytes + sum(2 * K + 2 * N for (_, N, K, _) in shapes)
+        res[f"q{bits}"] = {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
+                           "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                           "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "weight_copies_rotated": ncopy}
+    return res
+
+
 def ternary_codes(torch, N, K, dev, g):
     """Weights uniform in {-1, 0, +1}: codes {0, 1, 2} packed four per byte."""
     c = torch.randint(0, 3, (N, K // 4, 4), dtype=torch.uint8, device=dev, generator=g)
@@ -425,6 +464,7 @@ def main():
         line["prefill_gemm"] = prefill_gemm_bench(pq, torch, dev, g)
         line["ternary_gemv"] = ternary_bench(pq, torch, dev, g)
         line["ref_numerics_gemv"] = ref_numerics_bench(pq, torch, dev, g)
+        line["qlow_gemv"] = qlow_bench(pq, torch, dev, g)
     print(json.dumps(line))
 
 

@@ -119,6 +119,27 @@ int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, const int8_t *q
 int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint16_t *x, void *y, int y_dtype, int N,
                 int K, int T, void *stream);
 
+/* ====================================================== Q4 / Q5 low-bit GEMV
+ * The reference's low-bit backbone format and order (lfm3_qlow.cuh:1-113,
+ * qlow_gemv lfm3_nanode.cu:1894-1915). Per 32-group along K: w = d*q + mn,
+ * q in [0, 2^bits) (bits 4 or 5), d' = 128*d and mn fp16. N a multiple of
+ * 32, K a multiple of 256 (at most 16384). pq_qlow_pack turns row-major codes
+ * (one per byte, [N][K]) and scales ([N][K/32][2] fp16 bits: d', mn) into the
+ * reference's tiled payload (the exporter's dtype 6 / 7 tensors: 32-row
+ * tiles of nibbles, the bit-4 plane for Q5, half2 scales per row and group). */
+size_t pq_qlow_packed_codes_bytes(int N, int K, int bits);
+size_t pq_qlow_packed_scales_bytes(int N, int K, int bits);
+int pq_qlow_pack(const uint8_t *codes, const uint16_t *scales, int N, int K, int bits, uint8_t *pcodes,
+                 uint16_t *pscales, void *stream);
+/* y [N] (bf16 or fp32) from x bf16 [K] on the packed payload: K in KS = 4
+ * slices for K >= 4096, else 2; per slice and group: acc from four fmaf
+ * chains over (1 + q/128) * x (elements b, b+4, ...), (a0 + a1) + (a2 + a3);
+ * y_s = fmaf(d', acc - sg, fmaf(mn, sg, y_s)) with sg the group's sum of x;
+ * slices added in order from 0. Replaces k_qlow + k_qlow_combine
+ * (lfm3_qlow.cuh:39-113) as qlow_gemv launches them. */
+int pq_qlow_gemv(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y, int y_dtype, int N,
+                 int K, int bits, void *stream);
+
 /* ============================================================ weight blob
  * The .lfm3q8 file the reference's exporter writes (export_lfm3_q8.py) and
  * load_blob reads (lfm3_nanode.cu:1219-1733): 8-byte magic "LFM3Q8\x01\x00",

@@ -399,6 +399,51 @@ void orc_q8r_gemm(const int8_t *W, const float *S, const uint16_t *x, float *y, 
   free(xf);
 }
 
+/* Q4 / Q5 low-bit GEMV, the reference's order (k_qlow + k_qlow_combine,
+ * lfm3_qlow.cuh:39-113, with qlow_gemv's K split, lfm3_nanode.cu:1894-1915).
+ * Per 32-group along K: w = d*q + mn, q in [0, 2^B), stored d' = 128*d and
+ * mn (fp16). x is bf16 widened to fp32. K is cut into KS slices of whole
+ * groups, KS = 4 for K >= 4096 else 2; per slice from 0, groups ascending:
+ *   sg  = the group's 32 x summed in order from 0 (k_qlow's sx, 68-73);
+ *   a_b = fmaf chain from 0 over k = b, b+4, ..., b+28 of (1 + q_k/128)*x_k,
+ *         b = 0..3 (qlow_group: the code read as the float 1 + q/128, 22-37);
+ *   acc = (a0 + a1) + (a2 + a3);
+ *   y_s = fmaf(d', acc - sg, fmaf(mn, sg, y_s))                   (99-101);
+ * then y = ((0 + y_0) + y_1) + ... over the slices (107-112). Codes Q
+ * [N][K], one value per byte (row-major, unpacked); S [N][K/32][2] fp16 bits
+ * (d', mn). y fp32; the reference stores bf16(y). */
+void orc_qlow_gemv(const uint8_t *Q, const uint16_t *S, const uint16_t *x, float *y, int N, int K) {
+  const int G = K / ORC_QBLK, KS = K >= 4096 ? 4 : 2, GL = G / KS;
+  float *xf = (float *)malloc(sizeof(float) * (size_t)K);
+  float *sx = (float *)malloc(sizeof(float) * (size_t)G);
+  for (int i = 0; i < K; i++) xf[i] = orc_bf2f(x[i]);
+  for (int g = 0; g < G; g++) {
+    float t = 0.0f;
+    for (int k = 0; k < ORC_QBLK; k++) t += xf[g * ORC_QBLK + k];
+    sx[g] = t;
+  }
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < N; r++) {
+    const uint8_t *qr = Q + (size_t)r * K;
+    float yt = 0.0f;
+    for (int sl = 0; sl < KS; sl++) {
+      float ys = 0.0f;
+      for (int g = sl * GL; g < (sl + 1) * GL; g++) {
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < ORC_QBLK; k++)
+          a[k & 3] = fmaf(1.0f + (float)qr[g * ORC_QBLK + k] / 128.0f, xf[g * ORC_QBLK + k], a[k & 3]);
+        const float acc = (a[0] + a[1]) + (a[2] + a[3]);
+        const float dp = orc_h2f(S[((size_t)r * G + g) * 2]), mn = orc_h2f(S[((size_t)r * G + g) * 2 + 1]);
+        ys = fmaf(dp, acc - sx[g], fmaf(mn, sx[g], ys));
+      }
+      yt = yt + ys;
+    }
+    y[r] = yt;
+  }
+  free(xf);
+  free(sx);
+}
+
 /* Exact value of the quantized product, sum_b (S_b*dx_b as real) * isum_b, in
  * double (every term is exact in double: S_b and dx_b have 11 and 24 bit
  * mantissas, isum_b < 2^20; the sum rounds at most nb times at 2^-53). */

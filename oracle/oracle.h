@@ -62,6 +62,8 @@ void orc_q8_gemm(const int8_t *W, const uint16_t *S, const int8_t *qx, const flo
 void orc_q8_gemv_a11(const int8_t *W, const float *S, const float *x, float *y, int N, int K);
 /* R2: the reference's own GEMV order (bf16 x, fp32 scales, 32-leaf tree); y [T][N] */
 void orc_q8r_gemm(const int8_t *W, const float *S, const uint16_t *x, float *y, int N, int K, int T);
+/* Q4/Q5 low-bit GEMV in the reference's order; Q [N][K] one code per byte, S [N][K/32][2] fp16 (d', mn) */
+void orc_qlow_gemv(const uint8_t *Q, const uint16_t *S, const uint16_t *x, float *y, int N, int K);
 void orc_q8_gemv_exact(const int8_t *W, const uint16_t *S, const int8_t *qx, const float *dx,
                        double *y, int N, int K);
 void orc_tq2_gemv(const uint8_t *codes, const uint16_t *S, const uint8_t *xq, float *y,

@@ -185,6 +185,16 @@ def q8r_gemm(W, S32, xb):
     return y if np.ndim(xb) == 2 else y[0]
 
 
+def qlow_gemv(Q, S, xb):
+    """Q4/Q5 (reference order): codes uint8 [N][K] (one per byte), S fp16 bits
+    [N][K/32][2] (d' = 128 d, mn), x bf16 bits [K] -> y fp32 [N]."""
+    N, K = Q.shape
+    y = np.empty(N, np.float32)
+    lib().orc_qlow_gemv(_p(np.ascontiguousarray(Q, np.uint8)), _p(np.ascontiguousarray(S, np.uint16)),
+                        _p(np.ascontiguousarray(xb, np.uint16)), _p(y), C.c_int(N), C.c_int(K))
+    return y
+
+
 def q8_gemv_exact(W, S, qx, dx):
     N, K = W.shape
     y = np.empty(N, np.float64)

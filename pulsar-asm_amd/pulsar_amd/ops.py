@@ -8,7 +8,7 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "QlowWeight", "qlow_gemv", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
@@ -124,6 +124,34 @@ def q8r_gemv(codes, scales, x, out_dtype=DT_BF16, out=None):
     check(lib().pq_q8r_gemv(codes.data_ptr(), scales.data_ptr(), _bits16(x2), out.data_ptr(), out_dtype, N, K, T,
                             stream_ptr()), "pq_q8r_gemv")
     return out if x.dim() == 2 else out.reshape(N)
+
+
+class QlowWeight:
+    """A Q4 / Q5 tensor packed for pq_qlow_gemv: codes uint8 [N][K] (one code
+    per byte, 0 .. 2^bits - 1) and scales fp16 bits [N][K/32][2] (d' = 128 d, mn)."""
+
+    def __init__(self, codes, scales, bits):
+        N, K = codes.shape
+        if codes.dtype != torch.uint8 or scales.shape != (N, K // 32, 2) or scales.element_size() != 2:
+            raise ValueError("codes uint8 [N][K], scales 16-bit [N][K/32][2]")
+        self.N, self.K, self.bits = N, K, bits
+        nc = lib().pq_qlow_packed_codes_bytes(N, K, bits)
+        ns = lib().pq_qlow_packed_scales_bytes(N, K, bits)
+        if nc == 0:
+            raise ValueError("N a multiple of 32, K of 256, bits 4 or 5")
+        self.pcodes = torch.empty(nc, dtype=torch.uint8, device=codes.device)
+        self.pscales = torch.empty(ns // 2, dtype=torch.int16, device=codes.device)
+        check(lib().pq_qlow_pack(codes.contiguous().data_ptr(), scales.contiguous().data_ptr(), N, K, bits,
+                                 self.pcodes.data_ptr(), self.pscales.data_ptr(), stream_ptr()), "pq_qlow_pack")
+
+
+def qlow_gemv(w, x, out_dtype=DT_BF16, out=None):
+    """y [N] = the reference's Q4/Q5 GEMV of x (bf16 [K])."""
+    if out is None:
+        out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=x.device)
+    check(lib().pq_qlow_gemv(w.pcodes.data_ptr(), w.pscales.data_ptr(), _bits16(x), out.data_ptr(), out_dtype, w.N,
+                             w.K, w.bits, stream_ptr()), "pq_qlow_gemv")
+    return out
 
 
 # ---------------------------------------------------------------- layer ops

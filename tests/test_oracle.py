@@ -488,3 +488,68 @@ def test_r2_gemm_is_per_position(orc):
     Y = orc.q8r_gemm(W, S, xb)
     for t in range(3):
         assert np.array_equal(f32bits(Y[t]), f32bits(orc.q8r_gemm(W, S, xb[t])))
+
+
+# ------------------------------------------------ Q4 / Q5: the reference's low-bit order
+def _h16(v):
+    return np.asarray(v, np.float16).view(np.uint16)
+
+
+def _qlow_zero(N, K):
+    return np.zeros((N, K), np.uint8), np.zeros((N, K // 32, 2), np.uint16), np.zeros(K, np.uint16)
+
+
+def test_qlow_four_accumulators(orc):
+    """a_b folds elements b, b+4, ... (lfm3_qlow.cuh:22-37) and
+    acc = (a0 + a1) + (a2 + a3): x = 2^24, 1, 1, 1 at k = 0..3 (q = 0) gives
+    acc = 2^24 + 2 where a sequential sum gives 2^24; with d' = 1, mn = 0 the
+    output is acc - sg = (2^24 + 2) - 2^24 = 2."""
+    Q, S, x = _qlow_zero(1, 2048)
+    x[:4] = _bf16([2.0 ** 24, 1.0, 1.0, 1.0])
+    S[0, 0] = _h16([1.0, 0.0])
+    assert orc.qlow_gemv(Q, S, x)[0] == np.float32(2.0)
+
+
+def test_qlow_scale_fmas_are_fused(orc):
+    """y = fmaf(d', acc - sg, fmaf(mn, sg, y)) (99-101): group 0 leaves y = -1
+    (mn = -1, sg = 1), group 1 has d' = 0, mn = 1 + 2^-10 and sg = 1 + 2^-23,
+    so the fused inner fma gives 2^-10 + 2^-23 + 2^-33 (unfused: 2^-10 + 2^-23)."""
+    Q, S, x = _qlow_zero(1, 2048)
+    x[0] = _bf16([1.0])[0]
+    x[32], x[33] = _bf16([1.0, 2.0 ** -23])
+    S[0, 0] = _h16([0.0, -1.0])
+    S[0, 1] = _h16([0.0, 1.0 + 2.0 ** -10])
+    want = 2.0 ** -10 + 2.0 ** -23 + 2.0 ** -33
+    assert orc.qlow_gemv(Q, S, x)[0] == np.float32(want)
+    assert np.float32(want) != np.float32(2.0 ** -10 + 2.0 ** -23)
+
+
+def test_qlow_k_slices(orc):
+    """K = 4096 runs KS = 4 slices (lfm3_nanode.cu:1899) summed in order from 0:
+    y_0 = 2^24 from group 0, y_1 = 1 + 1 from groups 40 and 41 gives 2^24 + 2;
+    two slices (groups 40, 41 in slice 0) or one chain would give 2^24."""
+    Q, S, x = _qlow_zero(1, 4096)
+    for g, v in ((0, 2.0 ** 24), (40, 1.0), (41, 1.0)):
+        x[32 * g] = _bf16([v])[0]
+        S[0, g] = _h16([0.0, 1.0])       # y += mn * sg
+    assert orc.qlow_gemv(Q, S, x)[0] == np.float32(2.0 ** 24 + 2)
+
+
+@pytest.mark.parametrize("bits,N,K", [(4, 37, 2048), (5, 21, 8192), (4, 9, 4096)])
+def test_qlow_vs_exact(orc, bits, N, K):
+    """Within 1e-5 of sum |terms| of the exact dequantized product
+    sum_g (d'/128 * sum q x + mn * sum x) (the identity the decode relies on)."""
+    rng = np.random.default_rng(K + bits)
+    Q = rng.integers(0, 2 ** bits, (N, K)).astype(np.uint8)
+    d = (np.abs(rng.standard_normal((N, K // 32))) * 0.02).astype(np.float16)
+    mn = (-rng.random((N, K // 32)) * 0.3).astype(np.float16)
+    S = np.stack([(d.astype(np.float32) * 128).astype(np.float16).view(np.uint16), mn.view(np.uint16)], -1)
+    xb = orc.f2bf(orc.gen_normal(K + 1, K))
+    x = orc.bf2f(xb).astype(np.float64).reshape(-1, 32)
+    dp = S[..., 0].view(np.float16).astype(np.float64)
+    m = S[..., 1].view(np.float16).astype(np.float64)
+    q = Q.reshape(N, -1, 32).astype(np.float64)
+    exact = (dp / 128 * (q * x).sum(-1) + m * x.sum(-1)).sum(-1)
+    den = (np.abs(dp) * ((1 + q / 128) * np.abs(x)).sum(-1) + np.abs(m) * np.abs(x).sum(-1)).sum(-1)
+    y = orc.qlow_gemv(Q, S, xb).astype(np.float64)
+    assert (np.abs(y - exact) / den).max() <= 1e-5
