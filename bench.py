@@ -297,12 +297,20 @@ def qlow_bench(pq, torch, dev, g, rotate_mb=600):
         reps = 20
         gr = graph_of(torch, lambda: [step(i) for i in range(reps)])
         ms = timed_replay(torch, gr, stream, 3) / reps
-        del gr, copies
+        del gr
+        per = {}
+        for (name, N, K, _) in shapes:
+            gsh = graph_of(torch, lambda: [pq.qlow_gemv(copies[i % ncopy][name], xs[K], out=outs[name])
+                                           for i in range(30)])
+            per[name] = round(timed_replay(torch, gsh, stream, 5) / 30 * 1e3, 2)
+            del gsh
+        del copies
         torch.cuda.empty_cache()
         nbytes = set_bytes + sum(2 * K + 2 * N for (_, N, K, _) in shapes)
         res[f"q{bits}"] = {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
                            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                           "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "weight_copies_rotated": ncopy}
+                           "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "per_shape_us": per,
+                           "weight_copies_rotated": ncopy}
     return res
 
 

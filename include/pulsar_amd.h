@@ -139,6 +139,14 @@ int pq_qlow_pack(const uint8_t *codes, const uint16_t *scales, int N, int K, int
  * (lfm3_qlow.cuh:39-113) as qlow_gemv launches them. */
 int pq_qlow_gemv(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y, int y_dtype, int N,
                  int K, int bits, void *stream);
+/* The same with a workspace (ws_bytes >= pq_qlow_workspace_bytes: KS x N
+ * fp32, the reference's part): for K >= 4096 on fewer than 256 tiles, or a K
+ * whose whole-row staging exceeds LDS, one workgroup per (tile, slice) writes
+ * the slice sums there and a second pass adds them in order -- the same bits.
+ * Without the workspace such a K is rejected with PQ_ERR_ARG. */
+size_t pq_qlow_workspace_bytes(int N, int K, int bits);
+int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y, int y_dtype,
+                    int N, int K, int bits, void *ws, size_t ws_bytes, void *stream);
 
 /* ============================================================ weight blob
  * The .lfm3q8 file the reference's exporter writes (export_lfm3_q8.py) and

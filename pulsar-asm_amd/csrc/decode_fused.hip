@@ -272,6 +272,51 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
   lds_barrier();
 }
 
+// The fused GEMV's outputs from wave 0 (lane l < R holds row tile*64 + l's
+// y): the SwiGLU epilogue when qo is given (R = 64, rows interleaved by
+// pq_q8_pack_gate_up: lane l < 32 holds gate row 32*tile + l, lane l + 32 its
+// up row; writes the Q8_0 block tile of silu(gate) * up as silu_mul_kernel +
+// quant_store form it), else y (bf16 or fp32) and, with parts, the (value,
+// index) of the largest output (lowest index on ties) at parts[2*part].
+template <int R>
+__device__ __forceinline__ void fused_epilogue(float yv, int lane, int tile, int row, int part, void *__restrict__ y,
+                                               int y_bf16, int N, float *__restrict__ parts, int8_t *__restrict__ qo,
+                                               float *__restrict__ dqo) {
+  if (qo != nullptr) {
+    if constexpr (R == 64) {
+      const float u = bf2f(f2bf(__shfl_down(yv, 32, 64)));
+      const float a = bf2f(f2bf(yv));
+      const float sg = 1.0f / (1.0f + expf_pq(-a));
+      const float o = bf2f(f2bf((a * sg) * u));
+      const float m = wave_max(lane < 32 ? fabsf(o) : 0.0f);
+      const float d = m / 127.0f;
+      int q = (int)__builtin_rintf(o / (d != 0.0f ? d : 1.0f));   // d = 0: the block is all zero
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+      if (lane < 32) qo[32 * tile + lane] = (int8_t)q;
+      if (lane == 0) dqo[tile] = d;
+    }
+    return;
+  }
+  if (lane < R && row < N) {
+    if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yv);
+    else reinterpret_cast<float *>(y)[row] = yv;
+  }
+  if (parts != nullptr) {
+    float v = (lane < R && row < N) ? yv : -__builtin_inff();
+    int idx = (lane < R && row < N) ? row : 0x7fffffff;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float ov = __shfl_xor(v, o, 64);
+      const int oi = __shfl_xor(idx, o, 64);
+      if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    }
+    if (lane == 0) {
+      parts[2 * part] = v;
+      parts[2 * part + 1] = __int_as_float(idx);
+    }
+  }
+}
+
 // ------------------------------------------------------------ fused GEMV
 // The GEMV of q8.hip (R rows per workgroup, chunk slots per lane, rounds with an
 // ordered LDS fold) with x from the prologue: 64*W threads, E = K/(64*W)
@@ -338,42 +383,7 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
     }
     if (rd + 1 < nrounds) __syncthreads();
   }
-  if (wave == 0 && qo != nullptr) {
-    // SwiGLU epilogue (R = 64, rows interleaved by pq_q8_pack_gate_up): lane l
-    // < 32 holds gate row 32*tile + l, lane l + 32 its up row; the Q8_0 block
-    // tile of silu(gate) * up as silu_mul_kernel + quant_store form it.
-    if constexpr (R == 64) {
-      const float u = bf2f(f2bf(__shfl_down(yv, 32, 64)));
-      const float a = bf2f(f2bf(yv));
-      const float sg = 1.0f / (1.0f + expf_pq(-a));
-      const float o = bf2f(f2bf((a * sg) * u));
-      const float m = wave_max(lane < 32 ? fabsf(o) : 0.0f);
-      const float d = m / 127.0f;
-      int q = (int)__builtin_rintf(o / (d != 0.0f ? d : 1.0f));   // d = 0: the block is all zero
-      q = q > 127 ? 127 : (q < -127 ? -127 : q);
-      if (lane < 32) qo[32 * tile + lane] = (int8_t)q;
-      if (lane == 0) dqo[tile] = d;
-    }
-  } else if (wave == 0) {
-    if (lane < R && row < N) {
-      if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yv);
-      else reinterpret_cast<float *>(y)[row] = yv;
-    }
-    if (parts != nullptr) {
-      float v = (lane < R && row < N) ? yv : -__builtin_inff();
-      int idx = (lane < R && row < N) ? row : 0x7fffffff;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float ov = __shfl_xor(v, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
-      }
-      if (lane == 0) {
-        parts[2 * blockIdx.x] = v;
-        parts[2 * blockIdx.x + 1] = __int_as_float(idx);
-      }
-    }
-  }
+  if (wave == 0) fused_epilogue<R>(yv, lane, tile, row, (int)blockIdx.x, y, y_bf16, N, parts, qo, dqo);
 }
 
 // (value, index) partials -> the lowest index among the maxima.

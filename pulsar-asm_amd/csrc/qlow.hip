@@ -63,24 +63,32 @@ __device__ __forceinline__ float qlow_acc(v4i w4, uint32_t hp, const float *__re
   return (a0 + a1) + (a2 + a3);
 }
 
+// With ws (the split form): workgroup (tile, s) covers only slice s =
+// blockIdx.y and writes its y_s to ws[s][N]; qlow_combine_kernel adds the
+// slices in order. Without ws: one workgroup per tile, all slices.
 template <int B>
 __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__restrict__ pc,
                                                               const uint32_t *__restrict__ ps,
                                                               const uint16_t *__restrict__ x, void *__restrict__ y,
-                                                              int y_bf16, int N, int K) {
+                                                              int y_bf16, int N, int K, float *__restrict__ ws) {
   extern __shared__ __align__(16) float lsm[];
-  const int G = K / kQ, KS = qlow_ks(K), GL = G / KS, GW = qlow_gw(B);
-  float *xs = lsm;                      // [K]
-  float *sx = xs + K;                   // [G]
+  const int GA = K / kQ, KSA = qlow_ks(K), GW = qlow_gw(B);
+  // the groups this workgroup covers: [gb, gb + G), in KS slices of GL
+  const int KS = ws ? 1 : KSA, G = ws ? GA / KSA : GA, GL = G / KS, gb = ws ? (int)blockIdx.y * G : 0;
+  float *xs = lsm;                      // [G*32]
+  float *sx = xs + G * kQ;              // [G]
   float *u = sx + G;                    // [32 rows][G + 1]: acc - sg
   float *ys = u + 32 * (G + 1);         // [KS][32]
+  uint32_t *scl = reinterpret_cast<uint32_t *>(ys + KS * 32);   // [G][32] half2 (d', mn)
   const int tid = threadIdx.x, tile = blockIdx.x;
   const int r = tid & 31, slot = tid >> 5;
-  // the tile's codes and scales (wave-uniform resources)
+  // the tile's codes and scales from group gb (wave-uniform resources)
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t *>(pc + (size_t)tile * G * GW * 16), (short)0, G * GW * 16, kRsrcWord3);
+      const_cast<uint8_t *>(pc + ((size_t)tile * GA + gb) * GW * 16), (short)0, G * GW * 16, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t *>(ps + (size_t)tile * G * 32), (short)0, G * 32 * 4, kRsrcWord3);
+      const_cast<uint32_t *>(ps + ((size_t)tile * GA + gb) * 32), (short)0, G * 32 * 4, kRsrcWord3);
+  x += (size_t)gb * kQ;
+  K = G * kQ;
   // this lane's first PF groups' codes, before anything waits
   constexpr int PF = 4;
   v4i w[PF];
@@ -92,6 +100,11 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
     hpl[k] = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, g < G ? (g * GW + 32) * 16 + r * 4 : kRsrcOob, 0,
                                                                      kAuxNT)
                     : 0u;
+  }
+  // the tile's scales into LDS (16-byte loads over the contiguous [G][32])
+  for (int i = tid; i < G * 8; i += kLoThreads) {
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsc, i * 16, 0, 0);
+    *reinterpret_cast<v4i *>(scl + 4 * i) = v;
   }
   // x widened into LDS, then each group's sum of x in order
   for (int e = tid * 8; e < K; e += kLoThreads * 8) {
@@ -140,32 +153,38 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
   if (tid < 32 * KS) {
     const int s = tid >> 5;
     float yv = 0.0f;
-    for (int g0 = s * GL; g0 < (s + 1) * GL; g0 += 16) {
-      uint32_t sc[16];
-#pragma unroll
-      for (int k = 0; k < 16; k++)
-        sc[k] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-            rsc, g0 + k < (s + 1) * GL ? ((g0 + k) * 32 + r) * 4 : kRsrcOob, 0, 0);
-#pragma unroll
-      for (int k = 0; k < 16; k++)
-        if (g0 + k < (s + 1) * GL) {
-          const int g = g0 + k;
-          const float dp = h2f((uint16_t)(sc[k] & 0xffffu)), mn = h2f((uint16_t)(sc[k] >> 16));
-          yv = __builtin_fmaf(dp, u[r * (G + 1) + g], __builtin_fmaf(mn, sx[g], yv));
-        }
+    for (int g = s * GL; g < (s + 1) * GL; g++) {
+      const uint32_t sc = scl[g * 32 + r];
+      const float dp = h2f((uint16_t)(sc & 0xffffu)), mn = h2f((uint16_t)(sc >> 16));
+      yv = __builtin_fmaf(dp, u[r * (G + 1) + g], __builtin_fmaf(mn, sx[g], yv));
     }
     ys[s * 32 + r] = yv;
   }
   __syncthreads();
   if (tid < 32) {
+    const int row = tile * 32 + r;
+    if (ws) {
+      if (row < N) ws[(size_t)blockIdx.y * N + row] = ys[r];
+      return;
+    }
     float yt = 0.0f;
     for (int s = 0; s < KS; s++) yt = yt + ys[s * 32 + r];
-    const int row = tile * 32 + r;
     if (row < N) {
       if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yt);
       else reinterpret_cast<float *>(y)[row] = yt;
     }
   }
+}
+
+// y = ((0 + ws[0]) + ws[1]) + ... (k_qlow_combine, lfm3_qlow.cuh:107-113).
+__global__ __launch_bounds__(256) void qlow_combine_kernel(const float *__restrict__ ws, void *__restrict__ y,
+                                                            int y_bf16, int N, int KS) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= N) return;
+  float yt = 0.0f;
+  for (int s = 0; s < KS; s++) yt = yt + ws[(size_t)s * N + row];
+  if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yt);
+  else reinterpret_cast<float *>(y)[row] = yt;
 }
 
 // Row-major codes q [N][K] (one per byte) and scales [N][K/32][2] fp16 ->
@@ -223,24 +242,50 @@ extern "C" int pq_qlow_pack(const uint8_t *codes, const uint16_t *scales, int N,
   return check_launch("pq_qlow_pack");
 }
 
+extern "C" size_t pq_qlow_workspace_bytes(int N, int K, int bits) {
+  if (!qlow_shape(N, K, bits)) return 0;
+  return (size_t)qlow_ks(K) * N * sizeof(float);
+}
+
 extern "C" int pq_qlow_gemv(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y, int y_dtype,
                             int N, int K, int bits, void *stream) {
+  return pq_qlow_gemv_ws(pcodes, pscales, x, y, y_dtype, N, K, bits, nullptr, 0, stream);
+}
+
+extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y,
+                               int y_dtype, int N, int K, int bits, void *ws, size_t ws_bytes, void *stream) {
   PQ_REQUIRE(pcodes && pscales && x && y, PQ_ERR_ARG, "pq_qlow_gemv: null pointer");
   PQ_REQUIRE(qlow_shape(N, K, bits), PQ_ERR_ARG, "pq_qlow_gemv: N=%d K=%d bits=%d (N %% 32, K %% 256, bits 4 or 5)", N,
              K, bits);
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_qlow_gemv: y_dtype %d", y_dtype);
   PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 4) && aligned(x, 16), PQ_ERR_ALIGN,
              "pq_qlow_gemv: packed codes and x must be 16-byte aligned");
-  const int G = K / kQ, KS = qlow_ks(K);
-  const size_t lds = ((size_t)K + G + 32 * (size_t)(G + 1) + (size_t)KS * 32) * sizeof(float);
-  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_qlow_gemv: K=%d too large", K);
-  const dim3 grid((unsigned)(N / 32)), block(kLoThreads);
+  const int KS = qlow_ks(K);
+  auto lds_of = [&](int G, int ks) {
+    return ((size_t)G * kQ + G + 32 * (size_t)(G + 1) + (size_t)ks * 32 + 32 * (size_t)G) * sizeof(float);
+  };
+  // the split form (one workgroup per (tile, slice), then the ordered
+  // combine): for long rows on too few tiles to fill the chip (K = 2048 rows
+  // measured faster whole), or when a whole row's staging exceeds LDS
+  const bool whole_fits = lds_of(K / kQ, KS) <= kMaxLds;
+  const bool split = ws != nullptr && ws_bytes >= pq_qlow_workspace_bytes(N, K, bits) &&
+                     ((N / 32 < 256 && K >= 4096) || !whole_fits);
+  PQ_REQUIRE(!split || aligned(ws, 4), PQ_ERR_ALIGN, "pq_qlow_gemv: workspace alignment");
+  const int G = split ? K / kQ / KS : K / kQ, KSW = split ? 1 : KS;
+  const size_t lds = lds_of(G, KSW);
+  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_qlow_gemv: K=%d needs the workspace form", K);
+  const dim3 grid((unsigned)(N / 32), split ? (unsigned)KS : 1u), block(kLoThreads);
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  float *wsf = split ? static_cast<float *>(ws) : nullptr;
+  hipStream_t st = as_stream(stream);
   if (bits == 4)
-    launch(qlow_gemv_kernel<4>, grid, block, lds, as_stream(stream), pcodes,
-           reinterpret_cast<const uint32_t *>(pscales), x, y, yb, N, K);
+    launch(qlow_gemv_kernel<4>, grid, block, lds, st, pcodes, reinterpret_cast<const uint32_t *>(pscales), x, y, yb,
+           N, K, wsf);
   else
-    launch(qlow_gemv_kernel<5>, grid, block, lds, as_stream(stream), pcodes,
-           reinterpret_cast<const uint32_t *>(pscales), x, y, yb, N, K);
-  return check_launch("pq_qlow_gemv");
+    launch(qlow_gemv_kernel<5>, grid, block, lds, st, pcodes, reinterpret_cast<const uint32_t *>(pscales), x, y, yb,
+           N, K, wsf);
+  int rc = check_launch("pq_qlow_gemv");
+  if (rc || !split) return rc;
+  launch(qlow_combine_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, wsf, y, yb, N, KS);
+  return check_launch("pq_qlow_gemv combine");
 }

@@ -50,6 +50,8 @@ SIGNATURES = {
     "pq_qlow_packed_scales_bytes": (Z, [I, I, I]),
     "pq_qlow_pack": (I, [P, P, I, I, I, P, P, P]),
     "pq_qlow_gemv": (I, [P, P, P, P, I, I, I, I, P]),
+    "pq_qlow_workspace_bytes": (Z, [I, I, I]),
+    "pq_qlow_gemv_ws": (I, [P, P, P, P, I, I, I, I, P, Z, P]),
     "pq_rmsnorm": (I, [P, P, P, P, P, P, P, I, I, F, P]),
     "pq_qk_prep": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, F, P]),
     "pq_attn_workspace_bytes": (Z, [I, I, I]),

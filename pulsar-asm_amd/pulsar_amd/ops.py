@@ -145,12 +145,16 @@ class QlowWeight:
                                  self.pcodes.data_ptr(), self.pscales.data_ptr(), stream_ptr()), "pq_qlow_pack")
 
 
-def qlow_gemv(w, x, out_dtype=DT_BF16, out=None):
-    """y [N] = the reference's Q4/Q5 GEMV of x (bf16 [K])."""
+def qlow_gemv(w, x, out_dtype=DT_BF16, out=None, split=True, ws=None):
+    """y [N] = the reference's Q4/Q5 GEMV of x (bf16 [K]); split=True gives
+    the kernel a workspace (pq_qlow_gemv_ws) so small N splits K."""
     if out is None:
         out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=x.device)
-    check(lib().pq_qlow_gemv(w.pcodes.data_ptr(), w.pscales.data_ptr(), _bits16(x), out.data_ptr(), out_dtype, w.N,
-                             w.K, w.bits, stream_ptr()), "pq_qlow_gemv")
+    nbytes = lib().pq_qlow_workspace_bytes(w.N, w.K, w.bits) if split else 0
+    if nbytes and (ws is None or ws.numel() * ws.element_size() < nbytes):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    check(lib().pq_qlow_gemv_ws(w.pcodes.data_ptr(), w.pscales.data_ptr(), _bits16(x), out.data_ptr(), out_dtype,
+                                w.N, w.K, w.bits, _ptr(ws) if nbytes else None, nbytes, stream_ptr()), "pq_qlow_gemv")
     return out
 
 
