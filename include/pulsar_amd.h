@@ -45,6 +45,19 @@ const char *pq_last_error(void);
  * reference's LFM_KTIME per-statement event brackets (lfm3_nanode.cu:1030-1051). */
 int pq_time_next_launch(void *start_event, void *stop_event);
 
+/* Self-check of the hardware f32 -> bf16 conversion the kernels use
+ * (v_cvt_pk_bf16_f32) against the reference's rounding (round to nearest
+ * even, inf/nan passed through; lfm3_nanode.cu:114-121) over all 2^32 float
+ * bit patterns. counts, first: device arrays of 65536 uint32; block b reports
+ * its mismatches among patterns [b*65536, (b+1)*65536) and the lowest one
+ * (0xffffffff if none). No counterpart in the reference. */
+int pq_check_bf16_cvt(uint32_t *counts, uint32_t *first, void *stream);
+/* Self-check of the quantizers' shared-divisor division against x / d: 2^24
+ * random Q8_0 blocks (d = amax/127), 64 values each (ties +-2 ulps, tiny
+ * values, +-amax among them); counts/first per 256-block group as above
+ * (first = the lowest mismatching thread). No counterpart in the reference. */
+int pq_check_quant_div(uint32_t *counts, uint32_t *first, uint32_t seed, void *stream);
+
 /* --------------------------------------------------------- Q8_0 activations
  * x [T][K] -> qx [T][K] int8, dx [T][K/32] fp32. Per 32-block:
  * d = amax/127, q = rne(x/d) clamped to [-127,127]; an all-zero block gives

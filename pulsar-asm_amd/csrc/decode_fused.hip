@@ -57,11 +57,10 @@ __device__ __forceinline__ void ld_f32(const float *__restrict__ p, float *o) {
     o[4 * i] = f.x; o[4 * i + 1] = f.y; o[4 * i + 2] = f.z; o[4 * i + 3] = f.w;
   }
 }
+
+// E bf16 already packed in pairs (E/2 dwords)
 template <int E>
-__device__ __forceinline__ void st_bf16(uint16_t *__restrict__ p, const uint16_t *v) {
-  uint32_t w[E / 2];
-#pragma unroll
-  for (int i = 0; i < E / 2; i++) w[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
+__device__ __forceinline__ void st_bf16w(uint16_t *__restrict__ p, const uint32_t *w) {
   if constexpr (E == 4) {
     *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
   } else {
@@ -96,7 +95,13 @@ template <int E>
 __device__ __forceinline__ void norm_apply(float *x, const float *w, float ss, int K, float eps) {
   const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + eps);
 #pragma unroll
-  for (int i = 0; i < E; i++) x[i] = bf2f(f2bf(w[i] * bf2f(f2bf(x[i] * rs))));
+  for (int i = 0; i < E; i += 2) {
+    float a = x[i] * rs, b = x[i + 1] * rs;
+    bfr2(a, b);
+    x[i] = w[i] * a;
+    x[i + 1] = w[i + 1] * b;
+    bfr2(x[i], x[i + 1]);
+  }
 }
 
 // E int8 codes (E/4 dwords) of elements e0.. into the staged-x layout in LDS:
@@ -124,19 +129,12 @@ __device__ __forceinline__ void quant_lds(const float *v, int e0, int8_t *xs, fl
 #pragma unroll
   for (int o = 1; o < 32 / E; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
   const float d = a / 127.0f;
+  const Q8Div qd(d);
   uint32_t w[E / 4];
 #pragma unroll
   for (int i = 0; i < E / 4; i++) w[i] = 0u;
-  // d = 0 only when every |x| of the block is below 127 * 2^-149: dividing by 1
-  // then gives q = 0 as the zero-block rule does, and the E divisions carry no
-  // branch (they overlap)
-  const float dd = d != 0.0f ? d : 1.0f;
 #pragma unroll
-  for (int i = 0; i < E; i++) {
-    int q = (int)__builtin_rintf(v[i] / dd);
-    q = q > 127 ? 127 : (q < -127 ? -127 : q);
-    w[i >> 2] |= (uint32_t)(uint8_t)q << (8 * (i & 3));
-  }
+  for (int i = 0; i < E; i++) w[i >> 2] |= (uint32_t)(uint8_t)q8_code(qd.div(v[i])) << (8 * (i & 3));
   store_q8_lds<E>(w, e0, xs);
   if ((e0 & 31) == 0) dxs[e0 >> 5] = d;
 }
@@ -214,14 +212,19 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
     for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
     const float ss = wg_pairwise_sq<E>(v, red);
     const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + p.eps);
-    uint16_t xn[E];
+    uint32_t xn[E / 2];
 #pragma unroll
-    for (int i = 0; i < E; i++) {
-      const float h3 = bf2f(f2bf(r.f0[i] * bf2f(f2bf(v[i] * rs))));
-      xn[i] = f2bf(bf_at(r.u1, i) + h3);
-      v[i] = bf2f(xn[i]);
+    for (int i = 0; i < E; i += 2) {
+      float a = v[i] * rs, b = v[i + 1] * rs;
+      bfr2(a, b);
+      a = r.f0[i] * a;
+      b = r.f0[i + 1] * b;
+      bfr2(a, b);   // h3
+      v[i] = bf_at(r.u1, i) + a;
+      v[i + 1] = bf_at(r.u1, i + 1) + b;
+      xn[i >> 1] = bfr2(v[i], v[i + 1]);
     }
-    if (writer) st_bf16<E>(p.x_out + e0, xn);
+    if (writer) st_bf16w<E>(p.x_out + e0, xn);
     norm_apply<E>(v, r.f1, wg_pairwise_sq<E>(v, red + 8), K, p.eps);
   } else if constexpr (PRO == PQ_PRO_F32) {
 #pragma unroll
@@ -232,40 +235,49 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
     norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
   } else if constexpr (PRO == PQ_PRO_EMBED) {
     const float sc = h2f(r.emb_s);
-    uint16_t xb[E];
+    uint32_t xb[E / 2];
 #pragma unroll
-    for (int i = 0; i < E; i++) {
-      const int8_t c = (int8_t)((r.emb_c[i >> 2] >> (8 * (i & 3))) & 0xffu);
-      xb[i] = f2bf((float)c * sc);
-      v[i] = bf2f(xb[i]);
-    }
-    if (writer) st_bf16<E>(p.x_out + e0, xb);
+    for (int i = 0; i < E; i++) v[i] = (float)(int8_t)((r.emb_c[i >> 2] >> (8 * (i & 3))) & 0xffu) * sc;
+#pragma unroll
+    for (int i = 0; i < E; i += 2) xb[i >> 1] = bfr2(v[i], v[i + 1]);
+    if (writer) st_bf16w<E>(p.x_out + e0, xb);
     norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
   } else if constexpr (PRO == PQ_PRO_SILU) {
 #pragma unroll
     for (int i = 0; i < E; i++) {
       const float a = bf_at(r.u0, i);
       const float sg = 1.0f / (1.0f + expf_pq(-a));
-      v[i] = bf2f(f2bf((a * sg) * bf_at(r.u1, i)));
+      v[i] = (a * sg) * bf_at(r.u1, i);
     }
+#pragma unroll
+    for (int i = 0; i < E; i += 2) bfr2(v[i], v[i + 1]);
   } else if constexpr (PRO == PQ_PRO_CONV) {
-    uint16_t rout[kFusedTaps][E];
+    // the shifted ring keeps the stored bf16 bits; its new entry is bx = bf16(B*x)
+    uint32_t bxw[E / 2];
+#pragma unroll
+    for (int i = 0; i < E; i += 2) {
+      float a = bf_at(r.u0, i) * bf_at(r.u2, i), b = bf_at(r.u0, i + 1) * bf_at(r.u2, i + 1);
+      bxw[i >> 1] = bfr2(a, b);
+    }
 #pragma unroll
     for (int i = 0; i < E; i++) {
-      const uint16_t bx = f2bf(bf_at(r.u0, i) * bf_at(r.u2, i));
       float acc = 0.0f;
 #pragma unroll
-      for (int k = 0; k < kFusedTaps; k++) {
-        const float rk = k + 1 < kFusedTaps ? bf_at(r.ring[k], i) : bf2f(bx);
-        rout[k][i] = f2bf(rk);
-        acc = acc + r.taps[i * kFusedTaps + k] * rk;
-      }
-      const uint16_t cy = f2bf(acc);
-      v[i] = bf2f(f2bf(bf_at(r.u1, i) * bf2f(cy)));
+      for (int k = 0; k < kFusedTaps; k++)
+        acc = acc + r.taps[i * kFusedTaps + k] * bf_at(k + 1 < kFusedTaps ? r.ring[k] : bxw, i);
+      v[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < E; i += 2) {
+      bfr2(v[i], v[i + 1]);   // cy
+      v[i] = bf_at(r.u1, i) * v[i];
+      v[i + 1] = bf_at(r.u1, i + 1) * v[i + 1];
+      bfr2(v[i], v[i + 1]);
     }
     if (writer) {
 #pragma unroll
-      for (int k = 0; k < kFusedTaps; k++) st_bf16<E>(p.ring_out + (size_t)k * K + e0, rout[k]);
+      for (int k = 0; k + 1 < kFusedTaps; k++) st_bf16w<E>(p.ring_out + (size_t)k * K + e0, r.ring[k]);
+      st_bf16w<E>(p.ring_out + (size_t)(kFusedTaps - 1) * K + e0, bxw);
     }
   }
   quant_lds<E>(v, e0, xs, dxs);

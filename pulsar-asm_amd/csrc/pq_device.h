@@ -11,12 +11,76 @@
 namespace pq {
 
 // bf16 <-> f32. bf16 is raw 16-bit storage; f32 -> bf16 is round-to-nearest-
-// even with inf/nan passed through (lfm3_nanode.cu:114-121).
+// even with inf/nan passed through (lfm3_nanode.cu:114-121), written out in
+// integer steps here (f2bf_bits) and done by gfx950's v_cvt_pk_bf16_f32 in
+// f2bf / f2bf2 (pq_check_bf16_cvt compares the two over all 2^32 inputs).
 __device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
-__device__ __forceinline__ uint16_t f2bf(float v) {
+__device__ __forceinline__ uint16_t f2bf_bits(float v) {
   const uint32_t u = __float_as_uint(v);
   if (((u >> 23) & 0xffu) == 0xffu) return (uint16_t)(u >> 16);
   return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+typedef float pq_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 pq_bf16x2 __attribute__((ext_vector_type(2)));
+// (bf16(a), bf16(b)) packed low, high: one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+  const pq_f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, pq_bf16x2));
+}
+__device__ __forceinline__ uint16_t f2bf(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+// x rounded to bf16 and back
+__device__ __forceinline__ float bfr(float v) { return bf2f(f2bf(v)); }
+// a, b rounded to bf16 in place (one convert for the pair); returns the pair's
+// bf16 bits packed low, high
+__device__ __forceinline__ uint32_t bfr2(float &a, float &b) {
+  const uint32_t w = f2bf2(a, b);
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+  return w;
+}
+
+// Correctly rounded a / d for many a over one divisor d with
+// 2^-90 <= |d| <= 2^100: the divide sequence with the divisor's part done
+// once -- r = rcp(d) refined by one Newton step, then per quotient q = a*r and
+// two remainder corrections q += r*(a - d*q), each an fma. In that range the
+// hardware divide's operand scaling is the identity and its fixup passes a
+// finite quotient through, so the steps are the same as a / d's.
+struct SharedDiv {
+  float d, r;
+  __device__ __forceinline__ explicit SharedDiv(float dv) : d(dv) {
+    const float r0 = __builtin_amdgcn_rcpf(dv);
+    r = __builtin_fmaf(__builtin_fmaf(-dv, r0, 1.0f), r0, r0);
+  }
+  __device__ __forceinline__ float div(float a) const {
+    float q = a * r;
+    q = __builtin_fmaf(__builtin_fmaf(-d, q, a), r, q);
+    return __builtin_fmaf(__builtin_fmaf(-d, q, a), r, q);
+  }
+};
+// The Q8_0 quotient x / d of a block (d = amax/127), without branches: a d
+// outside SharedDiv's range is brought into it by an exact power-of-two scale
+// of both operands (the quotient of the scaled pair is the same real number,
+// so the same rounded one; x is at most ~127.5 |d|, so scaling it up cannot
+// overflow, and an x that underflows when scaled down is below 2^-100 |d|,
+// whose code is 0 either way). d = 0 (an all-zero block up to values below
+// 127 * 2^-149) divides by 1, whose codes are 0 as the zero-block rule wants.
+// pq_check_quant_div compares the codes with x / d's on the GPU.
+struct Q8Div {
+  float sc;
+  SharedDiv sd;
+  __device__ __forceinline__ static float scale_of(float d) {
+    const float m = __builtin_fabsf(d);
+    return m < 0x1p-90f ? 0x1p64f : (m > 0x1p100f ? 0x1p-64f : 1.0f);
+  }
+  __device__ __forceinline__ explicit Q8Div(float d)
+      : sc(scale_of(d != 0.0f ? d : 1.0f)), sd((d != 0.0f ? d : 1.0f) * scale_of(d != 0.0f ? d : 1.0f)) {}
+  __device__ __forceinline__ float div(float x) const { return sd.div(x * sc); }
+};
+// Q8_0 code of x in a block with scale d (d = amax/127; d = 0 only for an
+// all-zero block, whose codes are 0): rne(x/d) clamped to [-127, 127]
+__device__ __forceinline__ int q8_code(float q) {
+  const int c = (int)__builtin_rintf(q);
+  return c > 127 ? 127 : (c < -127 ? -127 : c);
 }
 
 // binary16 <-> f32 through the hardware converts (v_cvt_f32_f16 is exact;

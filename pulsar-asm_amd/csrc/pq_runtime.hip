@@ -1,6 +1,7 @@
 // pq_runtime.hip -- error state and version of the C ABI.
 #include <string.h>
 
+#include "pq_device.h"
 #include "pq_host.h"
 
 namespace pq {
@@ -20,7 +21,124 @@ TimedLaunch &timed_launch() {
   return t;
 }
 
+// Block b checks the float bit patterns [b*2^16, (b+1)*2^16): the hardware
+// conversion (single and packed forms) against the integer-step rounding.
+// Writes the block's mismatch count and its lowest mismatching pattern
+// (0xffffffff if none). Per-thread vector stores only.
+__global__ __launch_bounds__(256) void bf16_cvt_check_kernel(uint32_t *__restrict__ counts,
+                                                             uint32_t *__restrict__ first) {
+  __shared__ uint32_t sc[256], sf[256];
+  const uint32_t base = (uint32_t)blockIdx.x << 16;
+  uint32_t n = 0, f = 0xffffffffu;
+  for (uint32_t j = 0; j < 256; j += 2) {
+    const uint32_t u0 = base + threadIdx.x + 256u * j, u1 = u0 + 256u;
+    const float a = __uint_as_float(u0), b = __uint_as_float(u1);
+    const uint32_t want = (uint32_t)f2bf_bits(a) | ((uint32_t)f2bf_bits(b) << 16);
+    const uint32_t pk = f2bf2(a, b);
+    const uint32_t sg = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+    const bool bad0 = (pk & 0xffffu) != (want & 0xffffu) || (sg & 0xffffu) != (want & 0xffffu);
+    const bool bad1 = (pk >> 16) != (want >> 16) || (sg >> 16) != (want >> 16);
+    n += (uint32_t)bad0 + (uint32_t)bad1;
+    if (bad0 && u0 < f) f = u0;
+    if (bad1 && u1 < f) f = u1;
+  }
+  sc[threadIdx.x] = n;
+  sf[threadIdx.x] = f;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      sc[threadIdx.x] += sc[threadIdx.x + o];
+      sf[threadIdx.x] = sf[threadIdx.x] < sf[threadIdx.x + o] ? sf[threadIdx.x] : sf[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    counts[blockIdx.x] = sc[0];
+    first[blockIdx.x] = sf[0];
+  }
+}
+
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {   // an integer hash (xorshift-multiply rounds)
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// Each thread draws a block maximum amax (exponent field 0..254 -- subnormal
+// to the largest binade -- and mantissa at random; thread 0 of each block
+// takes amax = 0), d = amax/127 as the quantizers form it, and 64 values v of
+// that block: uniform multiples of d in [-128d, 128d], the rounded
+// half-integers (k + 1/2)*d and their neighbours within 2 ulps, small values,
+// and +-amax, each clamped to [-amax, amax]. A mismatch: the Q8_0 code of Q8Div's quotient differs from that
+// of v / d (v / 1 for d = 0), or (for |v| >= 2^-20 |d| and a normal v) the
+// quotients differ at all.
+__global__ __launch_bounds__(256) void quant_div_check_kernel(uint32_t *__restrict__ counts,
+                                                              uint32_t *__restrict__ first, uint32_t seed) {
+  __shared__ uint32_t sc[256], sf[256];
+  const uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+  uint32_t h = mix32(tid ^ mix32(seed));
+  const uint32_t e = h % 255u;
+  h = mix32(h);
+  const float amax = threadIdx.x == 0 ? 0.0f : __uint_as_float((e << 23) | (h & 0x7fffffu));
+  const float d = amax / 127.0f;
+  uint32_t n = 0, f = 0xffffffffu;
+  {
+    const Q8Div qd(d);
+    const float dd = d != 0.0f ? d : 1.0f;
+    for (uint32_t j = 0; j < 64; j++) {
+      h = mix32(h + j);
+      const float sgn = (h & 1u) ? -1.0f : 1.0f;
+      float v;
+      switch (j & 3u) {
+        case 0: v = d * ((float)(h >> 8) * 0x1p-24f * 256.0f - 128.0f); break;
+        case 1: {
+          const float t = d * ((float)((int)((h >> 4) & 255u) - 128) + 0.5f);
+          v = __uint_as_float(__float_as_uint(t) + ((h >> 12) % 5u) - 2u);
+          break;
+        }
+        case 2: v = sgn * d * __uint_as_float(((127u - 1u - ((h >> 4) % 60u)) << 23) | ((h >> 9) & 0x7fffffu)); break;
+        default: v = sgn * amax; break;
+      }
+      v = fminf(fmaxf(v, -amax), amax);   // a block's values lie within its amax
+      const float qi = v / dd, qs = qd.div(v);
+      const bool exact = __builtin_fabsf(v) >= __builtin_fabsf(d) * 0x1p-20f && __builtin_fabsf(v) >= 0x1p-126f;
+      const bool bad = q8_code(qi) != q8_code(qs) || (exact && __float_as_uint(qi) != __float_as_uint(qs));
+      n += bad ? 1u : 0u;
+      if (bad && tid < f) f = tid;
+    }
+  }
+  sc[threadIdx.x] = n;
+  sf[threadIdx.x] = f;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      sc[threadIdx.x] += sc[threadIdx.x + o];
+      sf[threadIdx.x] = sf[threadIdx.x] < sf[threadIdx.x + o] ? sf[threadIdx.x] : sf[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    counts[blockIdx.x] = sc[0];
+    first[blockIdx.x] = sf[0];
+  }
+}
+
 }  // namespace pq
+
+extern "C" int pq_check_quant_div(uint32_t *counts, uint32_t *first, uint32_t seed, void *stream) {
+  PQ_REQUIRE(counts && first, PQ_ERR_ARG, "pq_check_quant_div: null pointer");
+  pq::launch(pq::quant_div_check_kernel, dim3(65536), dim3(256), 0, pq::as_stream(stream), counts, first, seed);
+  return pq::check_launch("pq_check_quant_div");
+}
+
+extern "C" int pq_check_bf16_cvt(uint32_t *counts, uint32_t *first, void *stream) {
+  PQ_REQUIRE(counts && first, PQ_ERR_ARG, "pq_check_bf16_cvt: null pointer");
+  pq::launch(pq::bf16_cvt_check_kernel, dim3(65536), dim3(256), 0, pq::as_stream(stream), counts, first);
+  return pq::check_launch("pq_check_bf16_cvt");
+}
 
 extern "C" const char *pq_version(void) { return "pulsar-amd 0.1 gfx950"; }
 
