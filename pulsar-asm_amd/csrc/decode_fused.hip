@@ -649,9 +649,11 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
 
 using namespace pq;
 
+static int fused_rows(int N, int K);
+
 extern "C" int pq_q8_gemv_parts(int N, int K) {
   if (N <= 0 || K <= 0 || K % kQ) return 0;
-  return ntiles(N) * (64 / gemv_shape(N, K).R);
+  return ntiles(N) * (64 / fused_rows(N, K));
 }
 
 // Argument checks shared by the fused GEMV entry points (out: y or qx).
@@ -694,15 +696,46 @@ static int check_fused_args(const int8_t *pcodes, const uint16_t *pscales, const
   return PQ_OK;
 }
 
+// Rows per workgroup of a fused GEMV: the largest R of 64, 32, 16, 8 that
+// still gives at least 192 workgroups for K <= 4096 (256 for longer rows).
+// Every workgroup repeats the prologue, so fewer and longer workgroups win
+// until too few are left to keep HBM busy. Measured per decode launch at
+// K = 2048: conv in_proj 6144 rows with the RESNORM prologue 5.0 us at R = 32
+// (192 workgroups) against 5.7 at R = 16 and 6.1 at R = 64; q|k|v|gate 3136
+// rows 4.5 us at R = 16 against 5.5 at R = 8; 2048-row shapes equal at R = 8
+// and 16; at K = 8192 (down) R = 8 is fastest. PQ_GEMV_R forces R,
+// PQ_FUSED_MINWG the workgroup target.
+static int fused_rows(int N, int K) {
+  static int fR = -1, fM = -1;
+  if (fR < 0) {
+    const char *e = getenv("PQ_GEMV_R");
+    const char *m = getenv("PQ_FUSED_MINWG");
+    fR = e ? atoi(e) : 0;
+    fM = m ? atoi(m) : 0;
+  }
+  if (fR == 8 || fR == 16 || fR == 32 || fR == 64) return fR;
+  const int target = fM > 0 ? fM : (K <= 4096 ? 192 : 256);
+  const long long nt = ntiles(N);
+  int R = 64;
+  while (R > 8 && nt * (64 / R) < target) R >>= 1;
+  return R;
+}
+
 // Launch shape of a fused GEMV: W waves (4 or 8; fewer waves leave each
 // thread a longer prologue and measured slower, even where a wave has no chunk
 // of its own and only issues loads that read nothing), enough to give every
 // chunk slot of the R-row slice a lane, and E = K/(64W) prologue elements per
 // thread, 4..16.
 static int fused_waves(int R, int K) {
+  static int fW = -1;
+  if (fW < 0) {
+    const char *f = getenv("PQ_FUSED_W");   // launch-shape override for sweeps (4 or 8)
+    fW = f ? atoi(f) : 0;
+  }
   const int C = 64 / R;
   const int need = (nchunks(K) + C - 1) / C;
   int W = need > 4 ? 8 : 4;
+  if (fW == 4 || fW == 8) W = fW;
   if (K / (64 * W) > 16) W = 8;
   if (K / (64 * W) < 4) W = 4;
   return W;
@@ -769,7 +802,7 @@ extern "C" int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, c
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_q8_gemv_fused: y_dtype %d", y_dtype);
   const pq_gemv_prologue &p = *pro;
   return launch_fused(pcodes, pscales, p, y, y_dtype == PQ_DTYPE_BF16 ? 1 : 0, N, K, argmax_parts, nullptr, nullptr,
-                      gemv_shape(N, K).R, as_stream(stream), "pq_q8_gemv_fused");
+                      fused_rows(N, K), as_stream(stream), "pq_q8_gemv_fused");
 }
 
 extern "C" int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
