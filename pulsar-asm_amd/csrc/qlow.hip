@@ -16,27 +16,31 @@
 //   y_s = fmaf(d', acc - sg, fmaf(mn, sg, y_s)) over the slice's groups from 0;
 //   y = ((0 + y_0) + y_1) + ...; out bf16(y) or y.
 //
-// A workgroup owns one 32-row tile: lane r of each of the 16 32-lane slots
-// takes row r, slot j takes groups j, j+16, ... (a slot's 32 lanes read a
-// tile-group's 512 contiguous bytes), computes acc - sg into LDS; then one
-// lane per (row, slice) runs the slice's fmaf chain, and the slices add in
-// order.
+// A workgroup owns an RS-row slice of a 32-row tile (RS = 32 when that
+// still leaves 512 workgroups, else 8): lane r of each of its 256/RS slots
+// takes row r of the slice, slot j takes groups j, j + 256/RS, ... (a slot's
+// lanes read 16*RS contiguous bytes of the tile-group, whole 128-byte lines),
+// and computes acc - sg into LDS; then one lane per (row, slice of K) runs
+// that slice's fmaf chain, and the K slices add in order. The slices of a tile
+// run on one XCD (workgroups go round-robin over the 8 XCDs), so the tile's
+// scale and bit-4 plane lines, which all of them read, are fetched into one
+// L2. The code bytes become floats by one byte permute each.
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
 
 namespace pq {
 
-constexpr int kLoThreads = 512;
-constexpr int kLoSlots = kLoThreads / 32;   // group slots per round
+constexpr int kLoThreads = 256;   // threads per workgroup: 256 / RS group slots of RS rows
 
 __host__ __device__ inline int qlow_ks(int K) { return K >= 4096 ? 4 : 2; }
 __host__ __device__ inline int qlow_gw(int B) { return B == 4 ? 32 : 40; }   // 16-byte units per tile-group
 
-// The code byte q as the float 1 + q/128 (q < 128: exponent of 1.0, q in
-// mantissa bits 16..22).
-__device__ __forceinline__ float qlow_f(uint32_t m, int b) {
-  return __uint_as_float(0x3F800000u | (((m >> (8 * b)) & 0xffu) << 16));
+// The code q (< 128) as the float 1 + q/128: bits 0x3F800000 | q << 16. mm
+// holds four codes, one per byte, each with 0x80 (the mantissa's top bit of
+// 1.0's byte 2) or'ed in; one byte permute builds [0x3F, 0x80 | q, 0, 0].
+__device__ __forceinline__ float qlow_f(uint32_t mm, int b) {
+  return __uint_as_float(__builtin_amdgcn_perm(mm, 0x3F3F3F3Fu, ((uint32_t)(4 + b) << 16) | 0x0C0Cu));
 }
 
 template <int B>
@@ -47,7 +51,7 @@ __device__ __forceinline__ float qlow_acc(v4i w4, uint32_t hp, const float *__re
   for (int i = 0; i < 4; i++) {
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
-      uint32_t m = (hf ? (w[i] >> 4) : w[i]) & 0x0F0F0F0Fu;
+      uint32_t m = ((hf ? (w[i] >> 4) : w[i]) & 0x0F0F0F0Fu) | 0x80808080u;
       if constexpr (B == 5) {   // bit 4 of quad p's four codes from the plane's bits p, 8+p, 16+p, 24+p
         const int p = 2 * i + hf;
         const uint32_t hs = p <= 4 ? (hp << (4 - p)) : (hp >> (p - 4));
@@ -63,10 +67,31 @@ __device__ __forceinline__ float qlow_acc(v4i w4, uint32_t hp, const float *__re
   return (a0 + a1) + (a2 + a3);
 }
 
-// With ws (the split form): workgroup (tile, s) covers only slice s =
-// blockIdx.y and writes its y_s to ws[s][N]; qlow_combine_kernel adds the
-// slices in order. Without ws: one workgroup per tile, all slices.
-template <int B>
+// One step of a slice's chain: y = fmaf(d', acc - sg, fmaf(mn, sg, y)), the
+// scale pair sc = (d', mn) as half2.
+__device__ __forceinline__ float qlow_step(float y, float u, float sg, uint32_t sc) {
+  const float dp = h2f((uint16_t)(sc & 0xffffu)), mn = h2f((uint16_t)(sc >> 16));
+  return __builtin_fmaf(dp, u, __builtin_fmaf(mn, sg, y));
+}
+
+// Workgroup b -> (tile, RS-row slice of it): with a multiple of 8 tiles, the
+// 32/RS slices of a tile get workgroup ids equal mod 8 (one XCD).
+template <int RS>
+__device__ __forceinline__ void qlow_place(int b, int ntiles, int &tile, int &sub) {
+  constexpr int SUBS = 32 / RS;
+  if (ntiles % 8 == 0) {
+    tile = (b / (8 * SUBS)) * 8 + (b % 8);
+    sub = (b / 8) % SUBS;
+  } else {
+    tile = b / SUBS;
+    sub = b % SUBS;
+  }
+}
+
+// With ws (the split form): workgroup (slice of rows, s) covers only K slice
+// s = blockIdx.y and writes its y_s to ws[s][N]; qlow_combine_kernel adds the
+// slices in order. Without ws: all K slices in one workgroup.
+template <int B, int RS, int XL>
 __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__restrict__ pc,
                                                               const uint32_t *__restrict__ ps,
                                                               const uint16_t *__restrict__ x, void *__restrict__ y,
@@ -75,13 +100,20 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
   const int GA = K / kQ, KSA = qlow_ks(K), GW = qlow_gw(B);
   // the groups this workgroup covers: [gb, gb + G), in KS slices of GL
   const int KS = ws ? 1 : KSA, G = ws ? GA / KSA : GA, GL = G / KS, gb = ws ? (int)blockIdx.y * G : 0;
+  // per row, the groups' partials and scale pairs at a padded stride GP
+  // (16-byte aligned rows, rows 4 banks apart)
+  constexpr int kLoSlots = kLoThreads / RS;   // group slots per round
+  const int GP = G + 4;
   float *xs = lsm;                      // [G*32]
   float *sx = xs + G * kQ;              // [G]
-  float *u = sx + G;                    // [32 rows][G + 1]: acc - sg
-  float *ys = u + 32 * (G + 1);         // [KS][32]
-  uint32_t *scl = reinterpret_cast<uint32_t *>(ys + KS * 32);   // [G][32] half2 (d', mn)
-  const int tid = threadIdx.x, tile = blockIdx.x;
-  const int r = tid & 31, slot = tid >> 5;
+  float *u = sx + G;                    // [8 rows][GP]: acc - sg
+  uint32_t *scl = reinterpret_cast<uint32_t *>(u + RS * GP);   // [8 rows][GP] half2 (d', mn)
+  float *ys = reinterpret_cast<float *>(scl + RS * GP);          // [KS][8]
+  const int tid = threadIdx.x;
+  int tile, sub;
+  qlow_place<RS>(blockIdx.x, N / 32, tile, sub);
+  const int r = tid % RS, slot = tid / RS;
+  const int tr = sub * RS + r;          // this lane's row within the tile
   // the tile's codes and scales from group gb (wave-uniform resources)
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(pc + ((size_t)tile * GA + gb) * GW * 16), (short)0, G * GW * 16, kRsrcWord3);
@@ -89,37 +121,66 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
       const_cast<uint32_t *>(ps + ((size_t)tile * GA + gb) * 32), (short)0, G * 32 * 4, kRsrcWord3);
   x += (size_t)gb * kQ;
   K = G * kQ;
-  // this lane's first PF groups' codes, before anything waits
-  constexpr int PF = 4;
+  // Loads in the order their data is needed (they return in issue order):
+  // x (8 bf16 per 16-byte load, XL loads per thread: K <= 2048 XL), this
+  // lane's first PF groups' codes, then the slice's scale pairs (4 rows per
+  // 16-byte load, up to kScl loads per thread; any more come after the
+  // partials).
+  constexpr int kXLoads = XL, PF = 4, kScl = 4;
+  constexpr int HQ = RS / 4;
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, K * 2, kRsrcWord3);
+  uint4 xr[kXLoads];
+#pragma unroll
+  for (int it = 0; it < kXLoads; it++) {
+    const int e = tid * 8 + it * kLoThreads * 8;
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, e < K ? e * 2 : kRsrcOob, 0, 0);
+    xr[it] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+  }
   v4i w[PF];
   uint32_t hpl[PF];
 #pragma unroll
   for (int k = 0; k < PF; k++) {
     const int g = slot + kLoSlots * k;
-    w[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, g < G ? (g * GW + r) * 16 : kRsrcOob, 0, kAuxNT);
-    hpl[k] = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, g < G ? (g * GW + 32) * 16 + r * 4 : kRsrcOob, 0,
-                                                                     kAuxNT)
+    w[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, g < G ? (g * GW + tr) * 16 : kRsrcOob, 0, kAuxNT);
+    hpl[k] = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, g < G ? (g * GW + 32) * 16 + tr * 4 : kRsrcOob,
+                                                                     0, kAuxNT)
                     : 0u;
   }
-  // the tile's scales into LDS (16-byte loads over the contiguous [G][32])
-  for (int i = tid; i < G * 8; i += kLoThreads) {
-    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rsc, i * 16, 0, 0);
-    *reinterpret_cast<v4i *>(scl + 4 * i) = v;
+  v4i sr[kScl];
+#pragma unroll
+  for (int k = 0; k < kScl; k++) {
+    const int i = tid + k * kLoThreads;
+    sr[k] = __builtin_amdgcn_raw_buffer_load_b128(
+        rsc, i < G * HQ ? ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4 : kRsrcOob, 0, 0);
   }
   // x widened into LDS, then each group's sum of x in order
-  for (int e = tid * 8; e < K; e += kLoThreads * 8) {
-    const uint4 v = *reinterpret_cast<const uint4 *>(x + e);
-    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      xs[e + 2 * k] = __uint_as_float(vv[k] << 16);
-      xs[e + 2 * k + 1] = __uint_as_float(vv[k] & 0xffff0000u);
+  for (int it = 0; it < kXLoads; it++) {
+    const int e = tid * 8 + it * kLoThreads * 8;
+    if (e < K) {
+      const uint32_t vv[4] = {xr[it].x, xr[it].y, xr[it].z, xr[it].w};
+      float f[8];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        f[2 * k] = __uint_as_float(vv[k] << 16);
+        f[2 * k + 1] = __uint_as_float(vv[k] & 0xffff0000u);
+      }
+      *reinterpret_cast<float4 *>(xs + e) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4 *>(xs + e + 4) = make_float4(f[4], f[5], f[6], f[7]);
     }
   }
   __syncthreads();
   for (int g = tid; g < G; g += kLoThreads) {
+    float xv[kQ];
+#pragma unroll
+    for (int k = 0; k < kQ; k += 4) {
+      const float4 q = *reinterpret_cast<const float4 *>(xs + g * kQ + k);
+      xv[k] = q.x; xv[k + 1] = q.y; xv[k + 2] = q.z; xv[k + 3] = q.w;
+    }
     float t = 0.0f;
-    for (int k = 0; k < kQ; k++) t += xs[g * kQ + k];
+#pragma unroll
+    for (int k = 0; k < kQ; k++) t += xv[k];
     sx[g] = t;
   }
   __syncthreads();
@@ -132,43 +193,88 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
 #pragma unroll
       for (int k = 0; k < PF; k++) {
         const int g = g0 + kLoSlots * PF + slot + kLoSlots * k;
-        wn[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, g < G ? (g * GW + r) * 16 : kRsrcOob, 0, kAuxNT);
+        wn[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, g < G ? (g * GW + tr) * 16 : kRsrcOob, 0, kAuxNT);
         hn[k] = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-                             rc, g < G ? (g * GW + 32) * 16 + r * 4 : kRsrcOob, 0, kAuxNT)
+                             rc, g < G ? (g * GW + 32) * 16 + tr * 4 : kRsrcOob, 0, kAuxNT)
                        : 0u;
       }
     }
 #pragma unroll
     for (int k = 0; k < PF; k++) {
       const int g = g0 + slot + kLoSlots * k;
-      if (g < G) u[r * (G + 1) + g] = qlow_acc<B>(w[k], hpl[k], xs + g * kQ) - sx[g];
+      if (g < G) u[r * GP + g] = qlow_acc<B>(w[k], hpl[k], xs + g * kQ) - sx[g];
     }
     if (more) {
 #pragma unroll
       for (int k = 0; k < PF; k++) { w[k] = wn[k]; hpl[k] = hn[k]; }
     }
   }
+  // the scale pairs, each row's to its row
+  auto put_scales = [&](int i, v4i v) {
+    const int g = i / HQ, h = i % HQ;
+    scl[(4 * h) * GP + g] = (uint32_t)v.x;
+    scl[(4 * h + 1) * GP + g] = (uint32_t)v.y;
+    scl[(4 * h + 2) * GP + g] = (uint32_t)v.z;
+    scl[(4 * h + 3) * GP + g] = (uint32_t)v.w;
+  };
+#pragma unroll
+  for (int k = 0; k < kScl; k++)
+    if (tid + k * kLoThreads < G * HQ) put_scales(tid + k * kLoThreads, sr[k]);
+  for (int i = tid + kScl * kLoThreads; i < G * HQ; i += kLoThreads)
+    put_scales(i, __builtin_amdgcn_raw_buffer_load_b128(rsc, ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4, 0, 0));
   __syncthreads();
-  // per (row, slice): the slice's chain over its groups in order
-  if (tid < 32 * KS) {
-    const int s = tid >> 5;
+  // per (row, K slice): the slice's chain over its groups in order. Its LDS
+  // operands come 4 groups per 16-byte read (2 where the slice length is not
+  // a multiple of 4), the next reads issued before the current steps.
+  if (tid < RS * KS) {
+    const int s = tid / RS, rr = tid % RS;
+    const int gs = s * GL;
+    const float *up = u + rr * GP + gs;
+    const uint32_t *cp = scl + rr * GP + gs;
+    const float *sp = sx + gs;
     float yv = 0.0f;
-    for (int g = s * GL; g < (s + 1) * GL; g++) {
-      const uint32_t sc = scl[g * 32 + r];
-      const float dp = h2f((uint16_t)(sc & 0xffffu)), mn = h2f((uint16_t)(sc >> 16));
-      yv = __builtin_fmaf(dp, u[r * (G + 1) + g], __builtin_fmaf(mn, sx[g], yv));
+    if (GL % 4 == 0) {
+      const int n = GL / 4;
+      float4 uq = *reinterpret_cast<const float4 *>(up), sq = *reinterpret_cast<const float4 *>(sp);
+      uint4 cq = *reinterpret_cast<const uint4 *>(cp);
+      for (int it = 0; it < n; it++) {
+        const int nx = (it + 1 < n ? it + 1 : it) * 4;
+        const float4 un = *reinterpret_cast<const float4 *>(up + nx), sn = *reinterpret_cast<const float4 *>(sp + nx);
+        const uint4 cn = *reinterpret_cast<const uint4 *>(cp + nx);
+        yv = qlow_step(yv, uq.x, sq.x, cq.x);
+        yv = qlow_step(yv, uq.y, sq.y, cq.y);
+        yv = qlow_step(yv, uq.z, sq.z, cq.z);
+        yv = qlow_step(yv, uq.w, sq.w, cq.w);
+        uq = un;
+        sq = sn;
+        cq = cn;
+      }
+    } else {
+      const int n = GL / 2;   // G is a multiple of 8 and KS of 2 or 4: GL is even
+      float2 uq = *reinterpret_cast<const float2 *>(up), sq = *reinterpret_cast<const float2 *>(sp);
+      uint2 cq = *reinterpret_cast<const uint2 *>(cp);
+      for (int it = 0; it < n; it++) {
+        const int nx = (it + 1 < n ? it + 1 : it) * 2;
+        const float2 un = *reinterpret_cast<const float2 *>(up + nx), sn = *reinterpret_cast<const float2 *>(sp + nx);
+        const uint2 cn = *reinterpret_cast<const uint2 *>(cp + nx);
+        yv = qlow_step(yv, uq.x, sq.x, cq.x);
+        yv = qlow_step(yv, uq.y, sq.y, cq.y);
+        uq = un;
+        sq = sn;
+        cq = cn;
+      }
     }
-    ys[s * 32 + r] = yv;
+    ys[s * RS + rr] = yv;
   }
   __syncthreads();
-  if (tid < 32) {
-    const int row = tile * 32 + r;
+  if (tid < RS) {
+    const int row = tile * 32 + sub * RS + tid;
     if (ws) {
-      if (row < N) ws[(size_t)blockIdx.y * N + row] = ys[r];
+      if (row < N) ws[(size_t)blockIdx.y * N + row] = ys[tid];
       return;
     }
     float yt = 0.0f;
-    for (int s = 0; s < KS; s++) yt = yt + ys[s * 32 + r];
+    for (int s = 0; s < KS; s++) yt = yt + ys[s * RS + tid];
     if (row < N) {
       if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yt);
       else reinterpret_cast<float *>(y)[row] = yt;
@@ -219,6 +325,20 @@ static bool qlow_shape(int N, int K, int bits) {
   return (bits == 4 || bits == 5) && N > 0 && N % 32 == 0 && K > 0 && K % 256 == 0 && K <= 16384;
 }
 
+// Rows per workgroup: 32 (whole tiles) when that still gives 512
+// workgroups, else 8. Each workgroup stages x and its group sums, which
+// longer row slices amortize; small N needs the 8-row slices to fill the
+// chip. PQ_QLOW_RS forces 8, 16 or 32.
+static int qlow_rows(int N) {
+  static int fR = -1;
+  if (fR < 0) {
+    const char *e = getenv("PQ_QLOW_RS");
+    fR = e ? atoi(e) : 0;
+  }
+  if (fR == 8 || fR == 16 || fR == 32) return fR;
+  return N / 32 >= 512 ? 32 : 8;
+}
+
 extern "C" size_t pq_qlow_packed_codes_bytes(int N, int K, int bits) {
   if (!qlow_shape(N, K, bits)) return 0;
   return (size_t)N / 32 * (K / kQ) * qlow_gw(bits) * 16;
@@ -261,29 +381,47 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 4) && aligned(x, 16), PQ_ERR_ALIGN,
              "pq_qlow_gemv: packed codes and x must be 16-byte aligned");
   const int KS = qlow_ks(K);
+  const int RS = qlow_rows(N);
   auto lds_of = [&](int G, int ks) {
-    return ((size_t)G * kQ + G + 32 * (size_t)(G + 1) + (size_t)ks * 32 + 32 * (size_t)G) * sizeof(float);
+    return ((size_t)G * kQ + G + 2 * RS * (size_t)(G + 4) + (size_t)ks * RS) * sizeof(float);
   };
-  // the split form (one workgroup per (tile, slice), then the ordered
-  // combine): for long rows on too few tiles to fill the chip (K = 2048 rows
-  // measured faster whole), or when a whole row's staging exceeds LDS
+  // the split form (one workgroup per (8 rows, K slice), then the ordered
+  // combine): for long rows on too few row slices to fill the chip, or when
+  // a whole row's staging exceeds LDS
   const bool whole_fits = lds_of(K / kQ, KS) <= kMaxLds;
   const bool split = ws != nullptr && ws_bytes >= pq_qlow_workspace_bytes(N, K, bits) &&
-                     ((N / 32 < 256 && K >= 4096) || !whole_fits);
+                     ((N / RS < 128 && K >= 4096) || !whole_fits);
   PQ_REQUIRE(!split || aligned(ws, 4), PQ_ERR_ALIGN, "pq_qlow_gemv: workspace alignment");
   const int G = split ? K / kQ / KS : K / kQ, KSW = split ? 1 : KS;
   const size_t lds = lds_of(G, KSW);
   PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_qlow_gemv: K=%d needs the workspace form", K);
-  const dim3 grid((unsigned)(N / 32), split ? (unsigned)KS : 1u), block(kLoThreads);
+  const dim3 grid((unsigned)(N / RS), split ? (unsigned)KS : 1u), block(kLoThreads);
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
   float *wsf = split ? static_cast<float *>(ws) : nullptr;
   hipStream_t st = as_stream(stream);
-  if (bits == 4)
-    launch(qlow_gemv_kernel<4>, grid, block, lds, st, pcodes, reinterpret_cast<const uint32_t *>(pscales), x, y, yb,
-           N, K, wsf);
-  else
-    launch(qlow_gemv_kernel<5>, grid, block, lds, st, pcodes, reinterpret_cast<const uint32_t *>(pscales), x, y, yb,
-           N, K, wsf);
+  const uint32_t *ps32 = reinterpret_cast<const uint32_t *>(pscales);
+  // x loads per thread for the K one workgroup covers (256 threads x 8)
+  const int kw = G * kQ, XL = kw <= 2048 ? 1 : kw <= 4096 ? 2 : kw <= 8192 ? 4 : 8;
+#define PQ_QLOW(BB, RR, XX) \
+  launch(qlow_gemv_kernel<BB, RR, XX>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf)
+#define PQ_QLOW_X(BB, RR)          \
+  switch (XL) {                    \
+    case 1: PQ_QLOW(BB, RR, 1); break; \
+    case 2: PQ_QLOW(BB, RR, 2); break; \
+    case 4: PQ_QLOW(BB, RR, 4); break; \
+    default: PQ_QLOW(BB, RR, 8); break; \
+  }
+  if (bits == 4) {
+    if (RS == 32) PQ_QLOW_X(4, 32)
+    else if (RS == 16) PQ_QLOW_X(4, 16)
+    else PQ_QLOW_X(4, 8)
+  } else {
+    if (RS == 32) PQ_QLOW_X(5, 32)
+    else if (RS == 16) PQ_QLOW_X(5, 16)
+    else PQ_QLOW_X(5, 8)
+  }
+#undef PQ_QLOW_X
+#undef PQ_QLOW
   int rc = check_launch("pq_qlow_gemv");
   if (rc || !split) return rc;
   launch(qlow_combine_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, wsf, y, yb, N, KS);
