@@ -31,35 +31,60 @@ constexpr int kQ8KBytes = 292;
 
 // The activations' Q8_K row staged once per workgroup: permuted qs (dword k of
 // each 16 = x[k], x[k+4], x[k+8], x[k+12]), per-group sums from the bsums
-// (exact int16 sums of 16), and each group's block scale d.
-__device__ __forceinline__ void tq2_stage_x(const uint8_t *__restrict__ xq, int K, int *xperm, int *gsum, float *db) {
-  const int ng = K / kTqGroup;
-  const int nblk = K / kQ8K;
+// (exact int16 sums of 16), and each group's block scale d. Split in two: the
+// loads (XR runs of 16 qs per thread, one group's bsums and d per thread),
+// issued before the weight codes so they return first, then the LDS stores.
+template <int XR>
+struct TqX {
+  v4i run[XR];
+  v4i bs;
+  uint32_t d;
+};
+
+template <int XR>
+__device__ __forceinline__ void tq2_load_x(const uint8_t *__restrict__ xq, int K, TqX<XR> &t) {
+  const int ng = K / kTqGroup, nrun = K / 16;
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(xq), (short)0,
-                                                                      nblk * kQ8KBytes, kRsrcWord3);
-  for (int m = threadIdx.x; m < K / 16; m += blockDim.x) {   // run m: 16 qs of block m/16
-    const int blk = m >> 4, off = (m & 15) * 16;
-    const v4i w = __builtin_amdgcn_raw_buffer_load_b128(rx, blk * kQ8KBytes + 4 + off, 0, 0);
-    const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
-    int4 o;
-    o.x = (int)((w0 & 0xffu) | ((w1 & 0xffu) << 8) | ((w2 & 0xffu) << 16) | ((w3 & 0xffu) << 24));
-    o.y = (int)(((w0 >> 8) & 0xffu) | (((w1 >> 8) & 0xffu) << 8) | (((w2 >> 8) & 0xffu) << 16) |
-                (((w3 >> 8) & 0xffu) << 24));
-    o.z = (int)(((w0 >> 16) & 0xffu) | (((w1 >> 16) & 0xffu) << 8) | (((w2 >> 16) & 0xffu) << 16) |
-                (((w3 >> 16) & 0xffu) << 24));
-    o.w = (int)((w0 >> 24) | ((w1 >> 24) << 8) | ((w2 >> 24) << 16) | ((w3 >> 24) << 24));
-    reinterpret_cast<int4 *>(xperm)[m] = o;
-  }
-  for (int g = threadIdx.x; g < ng; g += blockDim.x) {
-    const int blk = g >> 1, half = g & 1;
-    // bsums 8*half .. 8*half+7 of the block (16 bytes at an even offset)
-    const v4i bs = __builtin_amdgcn_raw_buffer_load_b128(rx, blk * kQ8KBytes + 4 + kQ8K + 16 * half, 0, 0);
-    const int v[4] = {bs.x, bs.y, bs.z, bs.w};
-    int t = 0;
+                                                                      (K / kQ8K) * kQ8KBytes, kRsrcWord3);
 #pragma unroll
-    for (int i = 0; i < 4; i++) t += (int)(int16_t)(v[i] & 0xffff) + (int)(int16_t)((uint32_t)v[i] >> 16);
-    gsum[g] = t;
-    db[g] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, blk * kQ8KBytes, 0, 0));
+  for (int i = 0; i < XR; i++) {   // run m: 16 qs of block m/16
+    const int m = threadIdx.x + i * 256;
+    t.run[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, m < nrun ? (m >> 4) * kQ8KBytes + 4 + (m & 15) * 16 : kRsrcOob,
+                                                     0, 0);
+  }
+  // group g = threadIdx.x: bsums 8*half .. 8*half+7 of its block (16 bytes at
+  // an even offset) and the block's d
+  const int g = threadIdx.x, blk = g >> 1, half = g & 1;
+  t.bs = __builtin_amdgcn_raw_buffer_load_b128(rx, g < ng ? blk * kQ8KBytes + 4 + kQ8K + 16 * half : kRsrcOob, 0, 0);
+  t.d = __builtin_amdgcn_raw_buffer_load_b32(rx, g < ng ? blk * kQ8KBytes : kRsrcOob, 0, 0);
+}
+
+template <int XR>
+__device__ __forceinline__ void tq2_store_x(const TqX<XR> &t, int K, int *xperm, int *gsum, float *db) {
+  const int ng = K / kTqGroup, nrun = K / 16;
+#pragma unroll
+  for (int i = 0; i < XR; i++) {
+    const int m = threadIdx.x + i * 256;
+    if (m < nrun) {
+      const uint32_t w0 = t.run[i].x, w1 = t.run[i].y, w2 = t.run[i].z, w3 = t.run[i].w;
+      int4 o;
+      o.x = (int)((w0 & 0xffu) | ((w1 & 0xffu) << 8) | ((w2 & 0xffu) << 16) | ((w3 & 0xffu) << 24));
+      o.y = (int)(((w0 >> 8) & 0xffu) | (((w1 >> 8) & 0xffu) << 8) | (((w2 >> 8) & 0xffu) << 16) |
+                  (((w3 >> 8) & 0xffu) << 24));
+      o.z = (int)(((w0 >> 16) & 0xffu) | (((w1 >> 16) & 0xffu) << 8) | (((w2 >> 16) & 0xffu) << 16) |
+                  (((w3 >> 16) & 0xffu) << 24));
+      o.w = (int)((w0 >> 24) | ((w1 >> 24) << 8) | ((w2 >> 24) << 16) | ((w3 >> 24) << 24));
+      reinterpret_cast<int4 *>(xperm)[m] = o;
+    }
+  }
+  const int g = threadIdx.x;
+  if (g < ng) {
+    const int v[4] = {t.bs.x, t.bs.y, t.bs.z, t.bs.w};
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s += (int)(int16_t)(v[i] & 0xffff) + (int)(int16_t)((uint32_t)v[i] >> 16);
+    gsum[g] = s;
+    db[g] = __int_as_float(t.d);
   }
 }
 
@@ -69,7 +94,7 @@ __device__ __forceinline__ void tq2_stage_x(const uint8_t *__restrict__ xq, int 
 // gs and gs ^ 1 hold the two halves of the same groups; their exact int32
 // half-dots add across the pair, and the even lane forms the group partial.
 // PPL pieces per lane per round (LPR*PPL pieces = 64*LPR*PPL of K).
-template <int LPR, int PPL>
+template <int LPR, int PPL, int XR>
 __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict__ codes,
                                                         const uint16_t *__restrict__ scales,
                                                         const uint8_t *__restrict__ xq, float *__restrict__ y, int N,
@@ -88,6 +113,8 @@ __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict
       const_cast<uint8_t *>(codes + (size_t)(live ? row : 0) * (K / 4)), (short)0, live ? K / 4 : 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(scales + (size_t)(live ? row : 0) * ng), (short)0, live ? ng * 2 : 0, kRsrcWord3);
+  TqX<XR> xt;
+  tq2_load_x<XR>(xq, K, xt);
   for (int p0 = 0; p0 < npc; p0 += LPR * PPL) {
     // this round's codes (16 B per piece) and, on even lanes, the scale pair
     // of each piece's group, before anything waits
@@ -100,7 +127,7 @@ __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict
       sc[j] = (gs & 1) == 0 ? __builtin_amdgcn_raw_buffer_load_b32(rsc, pc < npc ? (g & ~1) * 2 : kRsrcOob, 0, 0) : 0u;
     }
     if (p0 == 0) {
-      tq2_stage_x(xq, K, xperm, gsum, db);
+      tq2_store_x<XR>(xt, K, xperm, gsum, db);
       __syncthreads();
     }
 #pragma unroll
@@ -207,19 +234,32 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
   const int ng = K / kTqGroup;
   hipStream_t st = as_stream(stream);
-  // 32 lanes per row (8 rows per workgroup) when the rows are long enough to
-  // give them 4 pieces each; PPL covers a row in one round up to K = 12288
+  // lanes per row by row length: 64 (4 rows per workgroup) from 192 pieces
+  // (K = 12288: 6.8 us against 7.0 at 32 for 4096 rows), 32 from 64 pieces
+  // (K = 4096: 5.9 us against 6.2 at 64 and 6.5 at 16), else 16; PPL covers
+  // a row in one round up to K = 12288
   static int env = -1;
   if (env < 0) {
     const char *e = getenv("PQ_TQ2_LPR");
     env = e ? atoi(e) : 0;
   }
-  const int lpr = env == 16 || env == 32 || env == 64 ? env : (2 * ng >= 64 ? 32 : 16);
+  const int lpr = env == 16 || env == 32 || env == 64 ? env : (2 * ng >= 192 ? 64 : 2 * ng >= 64 ? 32 : 16);
   const int ppl = (2 * ng + lpr - 1) / lpr;   // pieces per lane for one round
   const int rows = 256 / lpr;
   const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)rows * ng * 4;
   const dim3 grid((unsigned)((N + rows - 1) / rows)), block(256);
-#define PQ_TQ2(L, P) launch(tq2_gemv_kernel<L, P>, grid, block, lds, st, codes, scales, xq, y, N, K)
+  // 16-qs runs of x per thread (K/16 runs over 256 threads)
+  const int xr = K <= 4096 ? 1 : K <= 8192 ? 2 : K <= 16384 ? 4 : 8;
+#define PQ_TQ2_X(L, P, X) launch(tq2_gemv_kernel<L, P, X>, grid, block, lds, st, codes, scales, xq, y, N, K)
+#define PQ_TQ2(L, P)                    \
+  do {                                  \
+    switch (xr) {                       \
+      case 1: PQ_TQ2_X(L, P, 1); break; \
+      case 2: PQ_TQ2_X(L, P, 2); break; \
+      case 4: PQ_TQ2_X(L, P, 4); break; \
+      default: PQ_TQ2_X(L, P, 8); break; \
+    }                                   \
+  } while (0)
   if (lpr == 16) {
     if (ppl <= 4) PQ_TQ2(16, 4);
     else if (ppl <= 8) PQ_TQ2(16, 8);
@@ -234,5 +274,6 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
     else PQ_TQ2(64, 3);
   }
 #undef PQ_TQ2
+#undef PQ_TQ2_X
   return check_launch("pq_tq2_gemv");
 }
