@@ -396,7 +396,7 @@ static bool fused_supported(const pq_model_cfg &c, const char **why) {
 
 // One T=1 decode step through the fused kernels: four GEMV launches per conv
 // layer, five per attention layer (incl. the attention mixer), the LM head with
-// per-workgroup argmax partials and the final argmax -- 107 launches for the
+// per-workgroup argmax partials and the final argmax -- 106 launches for the
 // 24-layer backbone. Reads the token from E.tok and writes the next one there.
 // dev: the position comes from E.ctr[1] and the id is appended at E.ids[E.ctr[0]]
 // on the device (the form captured for replay); otherwise E.pos is passed.
