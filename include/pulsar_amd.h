@@ -50,7 +50,9 @@ int pq_time_next_launch(void *start_event, void *stop_event);
  * even, inf/nan passed through; lfm3_nanode.cu:114-121) over all 2^32 float
  * bit patterns. counts, first: device arrays of 65536 uint32; block b reports
  * its mismatches among patterns [b*65536, (b+1)*65536) and the lowest one
- * (0xffffffff if none). No counterpart in the reference. */
+ * (0xffffffff if none). Expected: exactly the 2*(2^22 - 1) signaling NaNs
+ * differ (the hardware quiets them; the kernels never convert one). No
+ * counterpart in the reference. */
 int pq_check_bf16_cvt(uint32_t *counts, uint32_t *first, void *stream);
 /* Self-check of the quantizers' shared-divisor division against x / d: 2^24
  * random Q8_0 blocks (d = amax/127), 64 values each (ties +-2 ulps, tiny
