@@ -88,6 +88,16 @@ def gemv_bytes(N, K, out):
     return N * K + N * (K // 32) * 2 + 4 * K + N * (4 if out == "f32" else 2)
 
 
+def gpu_desc(torch, pq):
+    """Device name, CU count and the shader clock measured on the device (pq_clock_mhz)."""
+    p = torch.cuda.get_device_properties(0)
+    out = torch.zeros(2, dtype=torch.float32, device="cuda:0")
+    pq.check(pq.lib().pq_clock_mhz(out.data_ptr(), pq.stream_ptr()), "pq_clock_mhz")
+    torch.cuda.synchronize()
+    return {"name": p.name, "gcn_arch": getattr(p, "gcnArchName", None), "cus": p.multi_processor_count,
+            "clock_MHz": round(float(out[0].item()))}
+
+
 def cpu_baseline(seconds=10.0):
     """The reference's gemv_q8 (fp32 x, fp32 scales) over the same shapes, on all host cores."""
     import ctypes as C
@@ -114,17 +124,36 @@ def cpu_baseline(seconds=10.0):
             else:
                 y[:] = pyoracle.q8_gemv_a11(W, S, x)
 
-    run_step()
     nbytes = sum(N * K + N * (K // 32) * 4 + K * 4 + N * 4 for (N, K, *_r) in data)
-    steps = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+
+    def timed(sec):
         run_step()
-        steps += 1
-    dt = (time.perf_counter() - t0) / steps
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        steps = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < sec:
+            run_step()
+            steps += 1
+        return steps, (time.perf_counter() - t0) / steps
+
+    threads = int(ref.ref_max_threads()) if ref is not None else 1
+    steps, dt = timed(seconds)
+    one = None
+    if ref is not None and threads > 1:   # the same routine on one core, a shorter sample
+        ref.ref_set_threads(1)
+        s1, dt1 = timed(seconds / 2)
+        ref.ref_set_threads(threads)
+        one = {"value": round(nbytes / dt1 / 1e9, 2), "ms_per_step": round(dt1 * 1e3, 3), "passes": s1}
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
-            "ms_per_step": round(dt * 1e3, 3),
+            "ms_per_step": round(dt * 1e3, 3), "one_core": one,
+            "host": f"{model}, nproc {os.cpu_count()}",
             "sample": f"{steps} passes of the 5 layer+LM-head GEMV shapes through gemv_q8 "
                       f"(q8_gemv_cpu.c:29-58, OpenMP over rows; fp32 x and fp32 scales, {nbytes / 1e6:.1f} MB/pass)"}
 
@@ -449,6 +478,7 @@ def main():
         "dtype": "int8xint8->int32, fp32 scales",
         "data": "synthetic (seeded uniform int8 codes, |N(0,1)|*0.01 fp16 scales, N(0,1) x)",
         "config": {"workload": "one LFM-style layer's T=1 Q8_0 GEMVs + LM head (hidden 2048)",
+                   "gpu": gpu_desc(torch, pq),
                    "gemvs": [f"{n}:{N}x{K}" for (n, N, K, _) in SHAPES],
                    "bytes_per_step": step_bytes, "weight_copies_rotated": ncopy,
                    "rotated_MB": round(ncopy * set_bytes / 1e6, 1)},

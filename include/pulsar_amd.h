@@ -59,6 +59,10 @@ int pq_check_bf16_cvt(uint32_t *counts, uint32_t *first, void *stream);
  * values, +-amax among them); counts/first per 256-block group as above
  * (first = the lowest mismatching thread). No counterpart in the reference. */
 int pq_check_quant_div(uint32_t *counts, uint32_t *first, uint32_t seed, void *stream);
+/* The shader clock in MHz, measured by one wave over ~0.2 ms (cycle counter
+ * against the 100 MHz real-time counter). out: 2 floats of device memory,
+ * out[0] = MHz. No counterpart in the reference. */
+int pq_clock_mhz(float *out, void *stream);
 
 /* --------------------------------------------------------- Q8_0 activations
  * x [T][K] -> qx [T][K] int8, dx [T][K/32] fp32. Per 32-block:

@@ -6,11 +6,18 @@
  * The output goes to oracle/_ref/ and is used only to pin the oracle:
  *   ref_q8_gemv   -> gemv_q8   (.auto/lfm3/q8_gemv_cpu.c:29-58)
  *   ref_q8_quant  -> quant_row (.auto/lfm3/q8_gemv_cpu.c:63-81)
+ *   ref_set_threads / ref_max_threads -> the OpenMP team size
  *   pq2_gemv_cpu / pq2_h2f are exported by pulsar_arm/bonsai2/pq2_host.c itself.
  */
+#include <omp.h>
+
 #define main q8_gemv_cpu_reference_main
 #include REF_Q8_CPU
 #undef main
+
+/* OpenMP team size for the routines below (the CPU baseline times all cores and one). */
+void ref_set_threads(int n) { omp_set_num_threads(n); }
+int ref_max_threads(void) { return omp_get_max_threads(); }
 
 void ref_q8_gemv(const signed char *q, const float *s, const float *x, float *y, int N, int K) {
   gemv_q8(q, s, x, y, N, K);

@@ -126,7 +126,26 @@ __global__ __launch_bounds__(256) void quant_div_check_kernel(uint32_t *__restri
   }
 }
 
+// One wave: shader clock cycles (s_memtime) against the 100 MHz real-time
+// counter (s_memrealtime) over a bounded dependent-FMA loop of ~0.2 ms.
+__global__ __launch_bounds__(64) void clock_probe_kernel(float *__restrict__ out, int iters) {
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime(), r0 = wall_clock64();
+  float x = (float)threadIdx.x;
+  for (int i = 0; i < iters; i++) x = __builtin_fmaf(x, 0.999999f, 1e-7f);
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime(), r1 = wall_clock64();
+  if (threadIdx.x == 0) {
+    out[0] = (float)((double)(c1 - c0) / (double)(r1 - r0) * 100.0);   // MHz
+    out[1] = x;   // keeps the loop
+  }
+}
+
 }  // namespace pq
+
+extern "C" int pq_clock_mhz(float *out, void *stream) {
+  PQ_REQUIRE(out, PQ_ERR_ARG, "pq_clock_mhz: null pointer");
+  pq::launch(pq::clock_probe_kernel, dim3(1), dim3(64), 0, pq::as_stream(stream), out, 50000);
+  return pq::check_launch("pq_clock_mhz");
+}
 
 extern "C" int pq_check_quant_div(uint32_t *counts, uint32_t *first, uint32_t seed, void *stream) {
   PQ_REQUIRE(counts && first, PQ_ERR_ARG, "pq_check_quant_div: null pointer");

@@ -50,3 +50,11 @@ def test_quant_shared_divisor_matches_division(pq, dev, seed):
     c = counts.cpu().numpy().view(np.uint32)
     f = first.cpu().numpy().view(np.uint32)
     assert int(c.sum()) == 0, f"{int(c.sum())} mismatches; first threads {[int(x) for x in f[c > 0][:8]]}"
+
+
+def test_clock_probe(pq, dev):
+    """pq_clock_mhz reports a shader clock in MI355X's range (its boost clock is 2.4 GHz)."""
+    out = torch.zeros(2, dtype=torch.float32, device=dev)
+    pq.check(pq.lib().pq_clock_mhz(out.data_ptr(), pq.stream_ptr()), "pq_clock_mhz")
+    torch.cuda.synchronize()
+    assert 500.0 < float(out[0]) < 3000.0
