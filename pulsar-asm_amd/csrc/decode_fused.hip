@@ -573,23 +573,37 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
       *reinterpret_cast<v4i *>(bw + (pos - p0) * kVRow + lane * 8) = reinterpret_cast<const v4i *>(kvnew + kHDf)[lane];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    // o = sum_p e[p] v[p][lane] (fmaf chain over p < pn), 16 positions per batch
+    // o = sum_p e[p] v[p][lane] (fmaf chain over p < pn), 16 positions per
+    // batch, the next batch's LDS reads issued before this batch's fmafs (rows
+    // past pn are read but not used; e[p] = 0 there)
     float o = 0.0f;
-    for (int b0 = 0; b0 < pn; b0 += 16) {
-      float v[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) v[i] = h2f(bw[(b0 + i) * kVRow + lane]);
+    {
+      uint16_t vb[16];
       float4 e4[4];
 #pragma unroll
-      for (int k = 0; k < 4; k++) e4[k] = reinterpret_cast<const float4 *>(eww + b0)[k];
-      __builtin_amdgcn_sched_barrier(0);
+      for (int i = 0; i < 16; i++) vb[i] = bw[i * kVRow + lane];
 #pragma unroll
-      for (int i = 0; i < 16; i++)
-        if (b0 + i < pn) {
-          const float4 &q = e4[i >> 2];
-          const float ei = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
-          o = __builtin_fmaf(ei, v[i], o);
-        }
+      for (int k = 0; k < 4; k++) e4[k] = reinterpret_cast<const float4 *>(eww)[k];
+      for (int b0 = 0; b0 < pn; b0 += 16) {
+        const int nb0 = b0 + 16 < kSplitF ? b0 + 16 : b0;
+        uint16_t vn[16];
+        float4 en[4];
+#pragma unroll
+        for (int i = 0; i < 16; i++) vn[i] = bw[(nb0 + i) * kVRow + lane];
+#pragma unroll
+        for (int k = 0; k < 4; k++) en[k] = reinterpret_cast<const float4 *>(eww + nb0)[k];
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+          if (b0 + i < pn) {
+            const float4 &q = e4[i >> 2];
+            const float ei = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+            o = __builtin_fmaf(ei, h2f(vb[i]), o);
+          }
+#pragma unroll
+        for (int i = 0; i < 16; i++) vb[i] = vn[i];
+#pragma unroll
+        for (int k = 0; k < 4; k++) e4[k] = en[k];
+      }
     }
     float *sj = st + (size_t)j * kPartf;
     sj[lane] = o;
@@ -634,13 +648,16 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
     rb = f2bf(bf2f(rb) * gs);
     if (out != nullptr) out[hq * kHDf + lane] = rb;
     const float v = bf2f(rb);
+    // amax over each 32-lane half (one Q8_0 block): DPP within 16-lane rows,
+    // then the row-pair swap
     float a = fabsf(v);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    a = fmaxf(a, dpp_f<kDppXor1>(a));
+    a = fmaxf(a, dpp_f<kDppXor2>(a));
+    a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
+    a = fmaxf(a, dpp_f<kDppMirror>(a));
+    a = max_row_pair(a);
     const float dq = a / 127.0f;
-    int qv = (int)__builtin_rintf(v / (dq != 0.0f ? dq : 1.0f));   // dq = 0: the block is all zero
-    qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
-    qx[hq * kHDf + lane] = (int8_t)qv;
+    qx[hq * kHDf + lane] = (int8_t)q8_code(Q8Div(dq).div(v));
     if ((lane & 31) == 0) dx[(hq * kHDf + lane) / 32] = dq;
   }
 }
