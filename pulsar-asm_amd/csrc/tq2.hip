@@ -41,14 +41,14 @@ struct TqX {
   uint32_t d;
 };
 
-template <int XR>
+template <int XR, int NT>
 __device__ __forceinline__ void tq2_load_x(const uint8_t *__restrict__ xq, int K, TqX<XR> &t) {
   const int ng = K / kTqGroup, nrun = K / 16;
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(xq), (short)0,
                                                                       (K / kQ8K) * kQ8KBytes, kRsrcWord3);
 #pragma unroll
   for (int i = 0; i < XR; i++) {   // run m: 16 qs of block m/16
-    const int m = threadIdx.x + i * 256;
+    const int m = threadIdx.x + i * NT;
     t.run[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, m < nrun ? (m >> 4) * kQ8KBytes + 4 + (m & 15) * 16 : kRsrcOob,
                                                      0, 0);
   }
@@ -59,12 +59,12 @@ __device__ __forceinline__ void tq2_load_x(const uint8_t *__restrict__ xq, int K
   t.d = __builtin_amdgcn_raw_buffer_load_b32(rx, g < ng ? blk * kQ8KBytes : kRsrcOob, 0, 0);
 }
 
-template <int XR>
+template <int XR, int NT>
 __device__ __forceinline__ void tq2_store_x(const TqX<XR> &t, int K, int *xperm, int *gsum, float *db) {
   const int ng = K / kTqGroup, nrun = K / 16;
 #pragma unroll
   for (int i = 0; i < XR; i++) {
-    const int m = threadIdx.x + i * 256;
+    const int m = threadIdx.x + i * NT;
     if (m < nrun) {
       const uint32_t w0 = t.run[i].x, w1 = t.run[i].y, w2 = t.run[i].z, w3 = t.run[i].w;
       int4 o;
@@ -88,14 +88,14 @@ __device__ __forceinline__ void tq2_store_x(const TqX<XR> &t, int K, int *xperm,
   }
 }
 
-// LPR lanes per row (16, 32 or 64), 256/LPR rows per workgroup. Lane gs of a row
+// LPR lanes per row (16, 32 or 64), NT/LPR rows per workgroup of NT threads. Lane gs of a row
 // reads the row's 16-byte pieces gs, gs + LPR, ... (a row's lanes cover
 // 16*LPR contiguous bytes per load, whole cache lines): piece p is half p % 2 of group p / 2, so lanes
 // gs and gs ^ 1 hold the two halves of the same groups; their exact int32
 // half-dots add across the pair, and the even lane forms the group partial.
 // PPL pieces per lane per round (LPR*PPL pieces = 64*LPR*PPL of K).
-template <int LPR, int PPL, int XR>
-__global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict__ codes,
+template <int LPR, int PPL, int XR, int NT>
+__global__ __launch_bounds__(NT) void tq2_gemv_kernel(const uint8_t *__restrict__ codes,
                                                         const uint16_t *__restrict__ scales,
                                                         const uint8_t *__restrict__ xq, float *__restrict__ y, int N,
                                                         int K) {
@@ -104,17 +104,17 @@ __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict
   int *xperm = reinterpret_cast<int *>(smem);                  // K bytes, permuted
   int *gsum = reinterpret_cast<int *>(smem + K);               // [ng] sum of qs over the group
   float *db = reinterpret_cast<float *>(gsum + ng);            // [ng] Q8_K d of the group's block
-  float *pg = db + ng;                                         // [256/LPR rows][ng] group partials
+  float *pg = db + ng;                                         // [NT/LPR rows][ng] group partials
   const int tid = threadIdx.x;
   const int r = tid / LPR, gs = tid % LPR;
-  const int row = blockIdx.x * (256 / LPR) + r;
+  const int row = blockIdx.x * (NT / LPR) + r;
   const bool live = row < N;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(codes + (size_t)(live ? row : 0) * (K / 4)), (short)0, live ? K / 4 : 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(scales + (size_t)(live ? row : 0) * ng), (short)0, live ? ng * 2 : 0, kRsrcWord3);
   TqX<XR> xt;
-  tq2_load_x<XR>(xq, K, xt);
+  tq2_load_x<XR, NT>(xq, K, xt);
   for (int p0 = 0; p0 < npc; p0 += LPR * PPL) {
     // this round's codes (16 B per piece) and, on even lanes, the scale pair
     // of each piece's group, before anything waits
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void tq2_gemv_kernel(const uint8_t *__restrict
       sc[j] = (gs & 1) == 0 ? __builtin_amdgcn_raw_buffer_load_b32(rsc, pc < npc ? (g & ~1) * 2 : kRsrcOob, 0, 0) : 0u;
     }
     if (p0 == 0) {
-      tq2_store_x<XR>(xt, K, xperm, gsum, db);
+      tq2_store_x<XR, NT>(xt, K, xperm, gsum, db);
       __syncthreads();
     }
 #pragma unroll
@@ -234,10 +234,9 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
   const int ng = K / kTqGroup;
   hipStream_t st = as_stream(stream);
-  // lanes per row by row length: 64 (4 rows per workgroup) from 192 pieces
-  // (K = 12288: 6.8 us against 7.0 at 32 for 4096 rows), 32 from 64 pieces
-  // (K = 4096: 5.9 us against 6.2 at 64 and 6.5 at 16), else 16; PPL covers
-  // a row in one round up to K = 12288
+  // lanes per row by row length: 64 from 192 pieces (K = 12288), 32 from 64
+  // pieces (K = 4096), else 16 (measured at 256 and at 512 threads); PPL
+  // covers a row in one round up to K = 12288
   static int env = -1;
   if (env < 0) {
     const char *e = getenv("PQ_TQ2_LPR");
@@ -245,35 +244,52 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   }
   const int lpr = env == 16 || env == 32 || env == 64 ? env : (2 * ng >= 192 ? 64 : 2 * ng >= 64 ? 32 : 16);
   const int ppl = (2 * ng + lpr - 1) / lpr;   // pieces per lane for one round
-  const int rows = 256 / lpr;
+  static int envt = -1;
+  if (envt < 0) {
+    const char *e = getenv("PQ_TQ2_NT");
+    envt = e ? atoi(e) : 0;
+  }
+  // 512 threads per workgroup: every workgroup stages x (K bytes permuted,
+  // the group sums), which more rows amortize; measured per shape (gate/up
+  // 12288x4096 5.8 us against 6.0 at 256 and 6.7 at 1024 threads, down
+  // 4096x12288 6.0 against 6.8 and 6.7)
+  const int nt = envt == 256 || envt == 512 || envt == 1024 ? envt : 512;
+  const int rows = nt / lpr;
   const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)rows * ng * 4;
-  const dim3 grid((unsigned)((N + rows - 1) / rows)), block(256);
-  // 16-qs runs of x per thread (K/16 runs over 256 threads)
-  const int xr = K <= 4096 ? 1 : K <= 8192 ? 2 : K <= 16384 ? 4 : 8;
-#define PQ_TQ2_X(L, P, X) launch(tq2_gemv_kernel<L, P, X>, grid, block, lds, st, codes, scales, xq, y, N, K)
-#define PQ_TQ2(L, P)                    \
-  do {                                  \
-    switch (xr) {                       \
-      case 1: PQ_TQ2_X(L, P, 1); break; \
-      case 2: PQ_TQ2_X(L, P, 2); break; \
-      case 4: PQ_TQ2_X(L, P, 4); break; \
-      default: PQ_TQ2_X(L, P, 8); break; \
-    }                                   \
+  const dim3 grid((unsigned)((N + rows - 1) / rows)), block(nt);
+  // 16-qs runs of x per thread (K/16 runs over nt threads)
+  const int runs = (K / 16 + nt - 1) / nt, xr = runs <= 1 ? 1 : runs <= 2 ? 2 : runs <= 4 ? 4 : 8;
+#define PQ_TQ2_X(L, P, X, T) launch(tq2_gemv_kernel<L, P, X, T>, grid, block, lds, st, codes, scales, xq, y, N, K)
+#define PQ_TQ2_T(L, P)                                             \
+  do {                                                             \
+    if (nt == 1024) {                                              \
+      if (xr <= 1) PQ_TQ2_X(L, P, 1, 1024);                        \
+      else PQ_TQ2_X(L, P, 2, 1024);                                \
+    } else if (nt == 512) {                                        \
+      if (xr <= 1) PQ_TQ2_X(L, P, 1, 512);                         \
+      else if (xr <= 2) PQ_TQ2_X(L, P, 2, 512);                    \
+      else PQ_TQ2_X(L, P, 4, 512);                                 \
+    } else {                                                       \
+      if (xr <= 1) PQ_TQ2_X(L, P, 1, 256);                         \
+      else if (xr <= 2) PQ_TQ2_X(L, P, 2, 256);                    \
+      else if (xr <= 4) PQ_TQ2_X(L, P, 4, 256);                    \
+      else PQ_TQ2_X(L, P, 8, 256);                                 \
+    }                                                              \
   } while (0)
   if (lpr == 16) {
-    if (ppl <= 4) PQ_TQ2(16, 4);
-    else if (ppl <= 8) PQ_TQ2(16, 8);
-    else PQ_TQ2(16, 12);
+    if (ppl <= 4) PQ_TQ2_T(16, 4);
+    else if (ppl <= 8) PQ_TQ2_T(16, 8);
+    else PQ_TQ2_T(16, 12);
   } else if (lpr == 32) {
-    if (ppl <= 2) PQ_TQ2(32, 2);
-    else if (ppl <= 4) PQ_TQ2(32, 4);
-    else PQ_TQ2(32, 6);
+    if (ppl <= 2) PQ_TQ2_T(32, 2);
+    else if (ppl <= 4) PQ_TQ2_T(32, 4);
+    else PQ_TQ2_T(32, 6);
   } else {
-    if (ppl <= 1) PQ_TQ2(64, 1);
-    else if (ppl <= 2) PQ_TQ2(64, 2);
-    else PQ_TQ2(64, 3);
+    if (ppl <= 1) PQ_TQ2_T(64, 1);
+    else if (ppl <= 2) PQ_TQ2_T(64, 2);
+    else PQ_TQ2_T(64, 3);
   }
-#undef PQ_TQ2
+#undef PQ_TQ2_T
 #undef PQ_TQ2_X
   return check_launch("pq_tq2_gemv");
 }
