@@ -16,9 +16,9 @@
 //   y_s = fmaf(d', acc - sg, fmaf(mn, sg, y_s)) over the slice's groups from 0;
 //   y = ((0 + y_0) + y_1) + ...; out bf16(y) or y.
 //
-// A workgroup owns an RS-row slice of a 32-row tile (RS = 32 when that
-// still leaves 512 workgroups, else 8): lane r of each of its 256/RS slots
-// takes row r of the slice, slot j takes groups j, j + 256/RS, ... (a slot's
+// A workgroup of NT = 512 threads owns an RS-row slice of a 32-row tile (RS =
+// 32, 16 or 8 by N): lane r of each of its NT/RS slots takes row r of the
+// slice, slot j takes groups j, j + NT/RS, ... (a slot's
 // lanes read 16*RS contiguous bytes of the tile-group, whole 128-byte lines),
 // and computes acc - sg into LDS; then one lane per (row, slice of K) runs
 // that slice's fmaf chain, and the K slices add in order. The slices of a tile
@@ -31,7 +31,6 @@
 
 namespace pq {
 
-constexpr int kLoThreads = 256;   // threads per workgroup: 256 / RS group slots of RS rows
 
 __host__ __device__ inline int qlow_ks(int K) { return K >= 4096 ? 4 : 2; }
 __host__ __device__ inline int qlow_gw(int B) { return B == 4 ? 32 : 40; }   // 16-byte units per tile-group
@@ -91,8 +90,8 @@ __device__ __forceinline__ void qlow_place(int b, int ntiles, int &tile, int &su
 // With ws (the split form): workgroup (slice of rows, s) covers only K slice
 // s = blockIdx.y and writes its y_s to ws[s][N]; qlow_combine_kernel adds the
 // slices in order. Without ws: all K slices in one workgroup.
-template <int B, int RS, int XL>
-__global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__restrict__ pc,
+template <int B, int RS, int XL, int NT>
+__global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict__ pc,
                                                               const uint32_t *__restrict__ ps,
                                                               const uint16_t *__restrict__ x, void *__restrict__ y,
                                                               int y_bf16, int N, int K, float *__restrict__ ws) {
@@ -102,7 +101,7 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
   const int KS = ws ? 1 : KSA, G = ws ? GA / KSA : GA, GL = G / KS, gb = ws ? (int)blockIdx.y * G : 0;
   // per row, the groups' partials and scale pairs at a padded stride GP
   // (16-byte aligned rows, rows 4 banks apart)
-  constexpr int kLoSlots = kLoThreads / RS;   // group slots per round
+  constexpr int kLoSlots = NT / RS;   // group slots per round (NT threads: NT/RS slots of RS rows)
   const int GP = G + 4;
   float *xs = lsm;                      // [G*32]
   float *sx = xs + G * kQ;              // [G]
@@ -133,7 +132,7 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
   uint4 xr[kXLoads];
 #pragma unroll
   for (int it = 0; it < kXLoads; it++) {
-    const int e = tid * 8 + it * kLoThreads * 8;
+    const int e = tid * 8 + it * NT * 8;
     const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, e < K ? e * 2 : kRsrcOob, 0, 0);
     xr[it] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
   }
@@ -150,14 +149,14 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
   v4i sr[kScl];
 #pragma unroll
   for (int k = 0; k < kScl; k++) {
-    const int i = tid + k * kLoThreads;
+    const int i = tid + k * NT;
     sr[k] = __builtin_amdgcn_raw_buffer_load_b128(
         rsc, i < G * HQ ? ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4 : kRsrcOob, 0, 0);
   }
   // x widened into LDS, then each group's sum of x in order
 #pragma unroll
   for (int it = 0; it < kXLoads; it++) {
-    const int e = tid * 8 + it * kLoThreads * 8;
+    const int e = tid * 8 + it * NT * 8;
     if (e < K) {
       const uint32_t vv[4] = {xr[it].x, xr[it].y, xr[it].z, xr[it].w};
       float f[8];
@@ -171,7 +170,7 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
     }
   }
   __syncthreads();
-  for (int g = tid; g < G; g += kLoThreads) {
+  for (int g = tid; g < G; g += NT) {
     float xv[kQ];
 #pragma unroll
     for (int k = 0; k < kQ; k += 4) {
@@ -219,8 +218,8 @@ __global__ __launch_bounds__(kLoThreads) void qlow_gemv_kernel(const uint8_t *__
   };
 #pragma unroll
   for (int k = 0; k < kScl; k++)
-    if (tid + k * kLoThreads < G * HQ) put_scales(tid + k * kLoThreads, sr[k]);
-  for (int i = tid + kScl * kLoThreads; i < G * HQ; i += kLoThreads)
+    if (tid + k * NT < G * HQ) put_scales(tid + k * NT, sr[k]);
+  for (int i = tid + kScl * NT; i < G * HQ; i += NT)
     put_scales(i, __builtin_amdgcn_raw_buffer_load_b128(rsc, ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4, 0, 0));
   __syncthreads();
   // per (row, K slice): the slice's chain over its groups in order. Its LDS
@@ -326,9 +325,12 @@ static bool qlow_shape(int N, int K, int bits) {
 }
 
 // Rows per workgroup: 32 (whole tiles) when that still gives 512
-// workgroups, else 8. Each workgroup stages x and its group sums, which
-// longer row slices amortize; small N needs the 8-row slices to fill the
-// chip. PQ_QLOW_RS forces 8, 16 or 32.
+// workgroups, else 16 when that gives 192, else 8. Each workgroup stages x
+// and its group sums, which longer row slices amortize; small N needs the
+// short slices to fill the chip (measured at 512 threads, Q4: gate+up 16384
+// rows 8.0 us at 32 rows against 10.1 at 16; q|k|v 3072 rows 4.75 at 16
+// against 5.2 at 8 and 5.4 at 32; o_proj and down 2048 rows 4.4 and 7.6 at 8).
+// PQ_QLOW_RS forces 8, 16 or 32.
 static int qlow_rows(int N) {
   static int fR = -1;
   if (fR < 0) {
@@ -336,7 +338,7 @@ static int qlow_rows(int N) {
     fR = e ? atoi(e) : 0;
   }
   if (fR == 8 || fR == 16 || fR == 32) return fR;
-  return N / 32 >= 512 ? 32 : 8;
+  return N / 32 >= 512 ? 32 : N / 16 >= 192 ? 16 : 8;
 }
 
 extern "C" size_t pq_qlow_packed_codes_bytes(int N, int K, int bits) {
@@ -395,21 +397,35 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   const int G = split ? K / kQ / KS : K / kQ, KSW = split ? 1 : KS;
   const size_t lds = lds_of(G, KSW);
   PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_qlow_gemv: K=%d needs the workspace form", K);
-  const dim3 grid((unsigned)(N / RS), split ? (unsigned)KS : 1u), block(kLoThreads);
+  static int envt = -1;
+  if (envt < 0) {
+    const char *e = getenv("PQ_QLOW_NT");
+    envt = e ? atoi(e) : 0;
+  }
+  const int NT = envt == 256 || envt == 512 ? envt : 512;   // threads per workgroup (512 measured faster)
+  const dim3 grid((unsigned)(N / RS), split ? (unsigned)KS : 1u), block(NT);
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
   float *wsf = split ? static_cast<float *>(ws) : nullptr;
   hipStream_t st = as_stream(stream);
   const uint32_t *ps32 = reinterpret_cast<const uint32_t *>(pscales);
-  // x loads per thread for the K one workgroup covers (256 threads x 8)
-  const int kw = G * kQ, XL = kw <= 2048 ? 1 : kw <= 4096 ? 2 : kw <= 8192 ? 4 : 8;
-#define PQ_QLOW(BB, RR, XX) \
-  launch(qlow_gemv_kernel<BB, RR, XX>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf)
-#define PQ_QLOW_X(BB, RR)          \
-  switch (XL) {                    \
-    case 1: PQ_QLOW(BB, RR, 1); break; \
-    case 2: PQ_QLOW(BB, RR, 2); break; \
-    case 4: PQ_QLOW(BB, RR, 4); break; \
-    default: PQ_QLOW(BB, RR, 8); break; \
+  // x loads per thread for the K one workgroup covers (NT threads x 8)
+  const int xl = (G * kQ + 8 * NT - 1) / (8 * NT), XL = xl <= 1 ? 1 : xl <= 2 ? 2 : xl <= 4 ? 4 : 8;
+#define PQ_QLOW(BB, RR, XX, TT) \
+  launch(qlow_gemv_kernel<BB, RR, XX, TT>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf)
+#define PQ_QLOW_X(BB, RR)                                  \
+  if (NT == 512) {                                         \
+    switch (XL) {                                          \
+      case 1: PQ_QLOW(BB, RR, 1, 512); break;              \
+      case 2: PQ_QLOW(BB, RR, 2, 512); break;              \
+      default: PQ_QLOW(BB, RR, 4, 512); break;             \
+    }                                                      \
+  } else {                                                 \
+    switch (XL) {                                          \
+      case 1: PQ_QLOW(BB, RR, 1, 256); break;              \
+      case 2: PQ_QLOW(BB, RR, 2, 256); break;              \
+      case 4: PQ_QLOW(BB, RR, 4, 256); break;              \
+      default: PQ_QLOW(BB, RR, 8, 256); break;             \
+    }                                                      \
   }
   if (bits == 4) {
     if (RS == 32) PQ_QLOW_X(4, 32)
