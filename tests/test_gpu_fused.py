@@ -29,7 +29,7 @@ def _ref_gemv(orc, W, S, xb):
     return orc.f2bf(orc.q8_gemv(W, S, qx, dx))
 
 
-@pytest.mark.parametrize("N", [3104, 16384, 2048, 65536])
+@pytest.mark.parametrize("N", [3104, 6144, 16384, 2048, 65536])
 def test_resnorm_prologue(orc, pq, dev, N):
     H = 2048
     W, S, w = _w(orc, pq, dev, N, H, SEED + N)
