@@ -723,13 +723,7 @@ static int check_fused_args(const int8_t *pcodes, const uint16_t *pscales, const
 // and 16; at K = 8192 (down) R = 8 is fastest. PQ_GEMV_R forces R,
 // PQ_FUSED_MINWG the workgroup target.
 static int fused_rows(int N, int K) {
-  static int fR = -1, fM = -1;
-  if (fR < 0) {
-    const char *e = getenv("PQ_GEMV_R");
-    const char *m = getenv("PQ_FUSED_MINWG");
-    fR = e ? atoi(e) : 0;
-    fM = m ? atoi(m) : 0;
-  }
+  static const int fR = env_int("PQ_GEMV_R"), fM = env_int("PQ_FUSED_MINWG");
   if (fR == 8 || fR == 16 || fR == 32 || fR == 64) return fR;
   const int target = fM > 0 ? fM : (K <= 4096 ? 192 : 256);
   const long long nt = ntiles(N);
@@ -744,11 +738,7 @@ static int fused_rows(int N, int K) {
 // chunk slot of the R-row slice a lane, and E = K/(64W) prologue elements per
 // thread, 4..16.
 static int fused_waves(int R, int K) {
-  static int fW = -1;
-  if (fW < 0) {
-    const char *f = getenv("PQ_FUSED_W");   // launch-shape override for sweeps (4 or 8)
-    fW = f ? atoi(f) : 0;
-  }
+  static const int fW = env_int("PQ_FUSED_W");   // launch-shape override for sweeps (4 or 8)
   const int C = 64 / R;
   const int need = (nchunks(K) + C - 1) / C;
   int W = need > 4 ? 8 : 4;

@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "../../include/pulsar_amd.h"
 
@@ -14,6 +15,13 @@ namespace pq {
 int fail(int code, const char *fmt, ...);
 
 inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// An integer launch-shape override from the environment (0 when unset); read
+// once per call site into a function-local static (thread-safe initialization).
+inline int env_int(const char *name) {
+  const char *e = getenv(name);
+  return e ? atoi(e) : 0;
+}
 
 // Checks the launch that was just queued; a failed launch returns
 // PQ_ERR_LAUNCH and produces no output (the reference's rule: no number from

@@ -681,11 +681,7 @@ enum { kFormWalk = 1, kFormTile = 2, kFormSlice = 3 };
 // and for deeper K at one position block (split over workgroups), 64-row
 // tiles for mid-sized N over many position blocks.
 static int gemm_form(int N, int K, int T) {
-  static int env = -1;
-  if (env < 0) {
-    const char *e = getenv("PQ_GEMM_FORM");
-    env = e ? atoi(e) : 0;
-  }
+  static const int env = env_int("PQ_GEMM_FORM");
   if (env >= kFormWalk && env <= kFormSlice) return env;
   if (N >= 32768) return kFormWalk;
   if (T <= 32) return K > kGemmSegK ? kFormWalk : kFormSlice;

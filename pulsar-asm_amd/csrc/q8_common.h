@@ -5,6 +5,7 @@
 #include <stdlib.h>
 
 #include "pq_device.h"
+#include "pq_host.h"
 #include "../../include/pulsar_amd.h"
 
 namespace pq {
@@ -132,13 +133,7 @@ constexpr size_t kMaxLds = 160 * 1024;  // LDS one gfx950 workgroup may allocate
 // W waves, enough to give every chunk of K a lane.
 struct GemvShape { int R, W; };
 inline GemvShape gemv_shape(int N, int K) {
-  static int fR = -1, fW = -1;
-  if (fR < 0) {
-    const char *e = getenv("PQ_GEMV_R");
-    const char *f = getenv("PQ_GEMV_W");
-    fR = e ? atoi(e) : 0;
-    fW = f ? atoi(f) : 0;
-  }
+  static const int fR = env_int("PQ_GEMV_R"), fW = env_int("PQ_GEMV_W");
   const int nt = ntiles(N), nch = nchunks(K);
   int R = 64;
   while (R > 8 && (long long)nt * (64 / R) < 256) R >>= 1;

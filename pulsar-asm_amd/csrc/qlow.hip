@@ -332,11 +332,7 @@ static bool qlow_shape(int N, int K, int bits) {
 // against 5.2 at 8 and 5.4 at 32; o_proj and down 2048 rows 4.4 and 7.6 at 8).
 // PQ_QLOW_RS forces 8, 16 or 32.
 static int qlow_rows(int N) {
-  static int fR = -1;
-  if (fR < 0) {
-    const char *e = getenv("PQ_QLOW_RS");
-    fR = e ? atoi(e) : 0;
-  }
+  static const int fR = env_int("PQ_QLOW_RS");
   if (fR == 8 || fR == 16 || fR == 32) return fR;
   return N / 32 >= 512 ? 32 : N / 16 >= 192 ? 16 : 8;
 }
@@ -397,11 +393,7 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   const int G = split ? K / kQ / KS : K / kQ, KSW = split ? 1 : KS;
   const size_t lds = lds_of(G, KSW);
   PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_qlow_gemv: K=%d needs the workspace form", K);
-  static int envt = -1;
-  if (envt < 0) {
-    const char *e = getenv("PQ_QLOW_NT");
-    envt = e ? atoi(e) : 0;
-  }
+  static const int envt = env_int("PQ_QLOW_NT");
   const int NT = envt == 256 || envt == 512 ? envt : 512;   // threads per workgroup (512 measured faster)
   const dim3 grid((unsigned)(N / RS), split ? (unsigned)KS : 1u), block(NT);
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;

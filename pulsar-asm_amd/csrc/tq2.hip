@@ -237,18 +237,10 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   // lanes per row by row length: 64 from 192 pieces (K = 12288), 32 from 64
   // pieces (K = 4096), else 16 (measured at 256 and at 512 threads); PPL
   // covers a row in one round up to K = 12288
-  static int env = -1;
-  if (env < 0) {
-    const char *e = getenv("PQ_TQ2_LPR");
-    env = e ? atoi(e) : 0;
-  }
+  static const int env = env_int("PQ_TQ2_LPR");
   const int lpr = env == 16 || env == 32 || env == 64 ? env : (2 * ng >= 192 ? 64 : 2 * ng >= 64 ? 32 : 16);
   const int ppl = (2 * ng + lpr - 1) / lpr;   // pieces per lane for one round
-  static int envt = -1;
-  if (envt < 0) {
-    const char *e = getenv("PQ_TQ2_NT");
-    envt = e ? atoi(e) : 0;
-  }
+  static const int envt = env_int("PQ_TQ2_NT");
   // 512 threads per workgroup: every workgroup stages x (K bytes permuted,
   // the group sums), which more rows amortize; measured per shape (gate/up
   // 12288x4096 5.8 us against 6.0 at 256 and 6.7 at 1024 threads, down
