@@ -397,8 +397,8 @@ def main():
     ap.add_argument("--rotate-mb", type=int, default=600)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMV would shard by rows; "
-              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (the GEMV would shard by rows, with an "
+              "all-gather of the outputs). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
