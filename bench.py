@@ -253,6 +253,30 @@ def prefill_gemm_bench(pq, torch, dev, g, T=512, chunk=32, reps=3, rotate_mb=600
             "single_launch_int8_peak_frac": round(ops / (ms_full * 1e-3) / 1e12 / 5000.0, 4)}
 
 
+def prefill_profile_workload(pq, torch, dev, reps=3):
+    """A workload for rocprofv3 counter runs (--prefill-profile): each GEMM of
+    the layer and the LM head, one weight copy, `reps` eager launches over T=512
+    positions and then `reps` over one 32-position chunk, bf16 y. Prints a line
+    per (GEMM, T) as it finishes; nothing is timed here."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    for (name, N, K, _) in SHAPES:
+        codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        scales = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().view(torch.int16)
+        w = pq.Q8Weight(codes, scales)
+        del codes, scales
+        for T in (512, 32):
+            qx, dx = pq.q8_quant(torch.randn(T, K, device=dev, generator=g))
+            y = torch.empty(T, N, dtype=torch.bfloat16, device=dev)
+            wsp = torch.empty(max(16, pq.lib().pq_q8_gemm_workspace_bytes(N, K, T)), dtype=torch.uint8, device=dev)
+            for _ in range(reps):
+                pq.q8_gemm(w, qx, dx, out_dtype=pq.DT_BF16, out=y, ws=wsp)
+            torch.cuda.synchronize()
+            print(f"prefill profile: {name} {N}x{K} T={T} x{reps}", flush=True)
+        del w
+        torch.cuda.empty_cache()
+
+
 def ref_numerics_bench(pq, torch, dev, g, reps=20, rotate_mb=700):
     """The config-2 step through the reference-numerics GEMV (pq_q8r_gemv: the
     reference's own order, bf16 x, fp32 weight scales, row-major codes),
@@ -395,6 +419,8 @@ def main():
     ap.add_argument("--calib", action="store_true",
                     help="also run a plain elementwise kernel over 256 MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--rotate-mb", type=int, default=600)
+    ap.add_argument("--prefill-profile", action="store_true",
+                    help="only run the prefill GEMMs (3 launches each at T=512 and T=32) for counter runs; no JSON")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: there is no multi-GPU path (the GEMV would shard by rows, with an "
@@ -405,6 +431,9 @@ def main():
     import pulsar_amd as pq
 
     dev = torch.device("cuda:0")
+    if args.prefill_profile:
+        prefill_profile_workload(pq, torch, dev)
+        return
     torch.manual_seed(20261201)
     g = torch.Generator(device=dev)
     g.manual_seed(20261201)
