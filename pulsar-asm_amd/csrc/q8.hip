@@ -207,6 +207,49 @@ __global__ __launch_bounds__(512) void q8_gemv_kernel(const int8_t *__restrict__
 // dx of block b at dxs[kb0 + b][position]). Block b+1's MFMA and LDS reads are
 // issued before block b's fold, so the matrix core and the LDS work while the
 // VALU folds; the fold order per output is unchanged.
+// The pipelined form: block b+1's MFMA is issued, then block b+2's activations
+// and block b+1's dx are read from LDS, then block b is folded -- so each LDS
+// read has a whole fold to arrive in, and the MFMA result it folds was issued
+// one fold earlier. The scheduling barriers keep the reads ahead of the fold.
+// NB = kCB compiles the whole-chunk case without the per-block bounds.
+template <int NB, typename AF>
+__device__ __forceinline__ void mfma_chunk_pipe(float *a, const v4i *w, const v4i sv, AF AV,
+                                                const float (*dxs)[32], int kb0, int h, int nbc_rt) {
+  const int nbc = NB ? NB : nbc_rt;
+  const uint32_t sw[4] = {(uint32_t)sv.x, (uint32_t)sv.y, (uint32_t)sv.z, (uint32_t)sv.w};
+  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  v16i acc[2];
+  float4 d[2][4];
+  v4i an;   // the activations of the next block's MFMA
+  if (nbc > 0) {
+    acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(0), w[0], zero, 0, 0, 0);
+    if (nbc > 1) an = AV(1);
+#pragma unroll
+    for (int q = 0; q < 4; q++) d[0][q] = *reinterpret_cast<const float4 *>(&dxs[kb0][8 * q + 4 * h]);
+  }
+#pragma unroll
+  for (int i = 0; i < kCB; i++) {
+    if (i + 1 < kCB && i + 1 < nbc) {
+      acc[(i + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(an, w[i + 1], zero, 0, 0, 0);
+      if (i + 2 < kCB && i + 2 < nbc) an = AV(i + 2);
+#pragma unroll
+      for (int q = 0; q < 4; q++) d[(i + 1) & 1][q] = *reinterpret_cast<const float4 *>(&dxs[kb0 + i + 1][8 * q + 4 * h]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (i < nbc) {
+      const float dw = half_of(sw[i >> 1], i & 1);
+      const v16i &ac = acc[i & 1];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float dq[4] = {d[i & 1][q].x, d[i & 1][q].y, d[i & 1][q].z, d[i & 1][q].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)ac[4 * q + k], a[4 * q + k]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 template <bool PIPE, typename AF>
 __device__ __forceinline__ void mfma_chunk(float *a, const v4i *w, const v4i sv, AF AV, const float (*dxs)[32],
                                            int kb0, int h, int nbc) {
@@ -230,33 +273,8 @@ __device__ __forceinline__ void mfma_chunk(float *a, const v4i *w, const v4i sv,
     }
     return;
   }
-  const uint32_t sw[4] = {(uint32_t)sv.x, (uint32_t)sv.y, (uint32_t)sv.z, (uint32_t)sv.w};
-  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  v16i acc[2];
-  float4 d[2][4];
-  if (nbc > 0) {
-    acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(0), w[0], zero, 0, 0, 0);
-#pragma unroll
-    for (int q = 0; q < 4; q++) d[0][q] = *reinterpret_cast<const float4 *>(&dxs[kb0][8 * q + 4 * h]);
-  }
-#pragma unroll
-  for (int i = 0; i < kCB; i++) {
-    if (i + 1 < kCB && i + 1 < nbc) {
-      acc[(i + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(i + 1), w[i + 1], zero, 0, 0, 0);
-#pragma unroll
-      for (int q = 0; q < 4; q++) d[(i + 1) & 1][q] = *reinterpret_cast<const float4 *>(&dxs[kb0 + i + 1][8 * q + 4 * h]);
-    }
-    if (i < nbc) {
-      const float dw = half_of(sw[i >> 1], i & 1);
-      const v16i &ac = acc[i & 1];
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float dq[4] = {d[i & 1][q].x, d[i & 1][q].y, d[i & 1][q].z, d[i & 1][q].w};
-#pragma unroll
-        for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)ac[4 * q + k], a[4 * q + k]);
-      }
-    }
-  }
+  if (nbc == kCB) mfma_chunk_pipe<kCB>(a, w, sv, AV, dxs, kb0, h, kCB);   // whole chunks: no branches
+  else mfma_chunk_pipe<0>(a, w, sv, AV, dxs, kb0, h, nbc);
 }
 
 constexpr int kGemmWaves = 8;
