@@ -306,15 +306,32 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
   const int nb = K / kQ, nch = nchunks(K);
   const int nsl = (N + 31) / 32, ngr = (nsl + kGemmWaves - 1) / kGemmWaves;
   const int S = (nch + cps - 1) / cps;
-  const int nitems = ngr * S * ((T + 31) / 32);
+  const int P = (T + 31) / 32, nitems = ngr * S * P;
+  // Item it -> (group, split) gs and position block pb. Workgroups are placed
+  // on the 8 XCDs round-robin (XCD = id % 8) and a workgroup's items are
+  // gridDim.x apart, so with several position blocks the items are laid out to
+  // give the P position blocks of one (group, split) to P workgroups of one
+  // XCD at the same time: the group's weights are read from HBM once and from
+  // that XCD's L2 P-1 times, and each workgroup keeps its position block's
+  // activations. A bijection on [0, nitems) whenever 8 divides ngr * S.
+  const bool xcd_map = P > 1 && (ngr * S) % 8 == 0;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int h = lane >> 5, l32 = lane & 31;
   if ((int)blockIdx.x >= nitems) return;
   auto item = [&](int it, GemmCur &g) {
-    const int gr = it % ngr, s = (it / ngr) % S;
+    int gs, pb;
+    if (xcd_map) {
+      const int j = it >> 3;
+      pb = j % P;
+      gs = (j / P) * 8 + (it & 7);
+    } else {
+      gs = it % (ngr * S);
+      pb = it / (ngr * S);
+    }
+    const int gr = gs % ngr, s = gs / ngr;
     g.it = it;
     g.slice = gr * kGemmWaves + wave;
-    g.p0 = (it / ngr / S) * 32;
+    g.p0 = pb * 32;
     g.c0 = s * cps;
     g.c1 = min(nch, g.c0 + cps);
     g.c = g.c0;
