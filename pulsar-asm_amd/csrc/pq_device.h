@@ -176,4 +176,17 @@ __device__ __forceinline__ void lds_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// An LDS pointer whose address sits in one VGPR the optimizer cannot split
+// into a uniform and a per-lane part: reads at constant offsets from it fold
+// into the DS instruction's offset field, where a split address costs one
+// VALU add per read. p must point into LDS.
+template <typename T>
+using lds_ptr = const __attribute__((address_space(3))) T *;
+template <typename T>
+__device__ __forceinline__ lds_ptr<T> lds_base(const T *p) {
+  uint32_t a = (uint32_t)(size_t)(lds_ptr<T>)p;
+  asm("" : "+v"(a));
+  return (lds_ptr<T>)(size_t)a;
+}
+
 }  // namespace pq

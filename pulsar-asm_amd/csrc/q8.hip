@@ -219,13 +219,14 @@ __device__ __forceinline__ void mfma_chunk_pipe(float *a, const v4i *w, const v4
   const uint32_t sw[4] = {(uint32_t)sv.x, (uint32_t)sv.y, (uint32_t)sv.z, (uint32_t)sv.w};
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   v16i acc[2];
-  float4 d[2][4];
+  f4v d[2][4];
   v4i an;   // the activations of the next block's MFMA
+  const lds_ptr<f4v> dp = lds_base(reinterpret_cast<const f4v *>(&dxs[kb0][4 * h]));   // block i, q: dp[8i + 2q]
   if (nbc > 0) {
     acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(0), w[0], zero, 0, 0, 0);
     if (nbc > 1) an = AV(1);
 #pragma unroll
-    for (int q = 0; q < 4; q++) d[0][q] = *reinterpret_cast<const float4 *>(&dxs[kb0][8 * q + 4 * h]);
+    for (int q = 0; q < 4; q++) d[0][q] = dp[2 * q];
   }
 #pragma unroll
   for (int i = 0; i < kCB; i++) {
@@ -233,7 +234,7 @@ __device__ __forceinline__ void mfma_chunk_pipe(float *a, const v4i *w, const v4
       acc[(i + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(an, w[i + 1], zero, 0, 0, 0);
       if (i + 2 < kCB && i + 2 < nbc) an = AV(i + 2);
 #pragma unroll
-      for (int q = 0; q < 4; q++) d[(i + 1) & 1][q] = *reinterpret_cast<const float4 *>(&dxs[kb0 + i + 1][8 * q + 4 * h]);
+      for (int q = 0; q < 4; q++) d[(i + 1) & 1][q] = dp[8 * (i + 1) + 2 * q];
     }
     __builtin_amdgcn_sched_barrier(0);
     if (i < nbc) {
@@ -442,7 +443,8 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
     for (int r = 0; r < 16; r++) a[r] = 0.0f;
     {
       const int kb0 = (c - seg_k) * kCB;   // the chunk's first block within the staged segment
-      auto AV = [&](int i) { return *reinterpret_cast<const v4i *>(&as[l32][(kb0 + i) * kQ + 16 * h]); };
+      const lds_ptr<v4i> ap = lds_base(reinterpret_cast<const v4i *>(&as[l32][kb0 * kQ + 16 * h]));
+      auto AV = [&](int i) { return ap[2 * i]; };   // block i: 32 bytes on
       mfma_chunk<true>(a, w0.w, w0.s, AV, dxs, kb0, h, min(kCB, nb - c * kCB));
     }
     const int row = g0.slice * 32 + l32;
@@ -566,7 +568,8 @@ __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const
     for (int r = 0; r < 16; r++) a[r] = 0.0f;
     if (valid) {
       const int kb0 = slot * kCB;
-      auto AV = [&](int i) { return *reinterpret_cast<const v4i *>(&as[l32][(kb0 + i) * kQ + 16 * h]); };
+      const lds_ptr<v4i> ap = lds_base(reinterpret_cast<const v4i *>(&as[l32][kb0 * kQ + 16 * h]));
+      auto AV = [&](int i) { return ap[2 * i]; };   // block i: 32 bytes on
       mfma_chunk<PIPE>(a, wv, sv, AV, dxs, kb0, h, min(kCB, nb - c * kCB));
     }
     lds_barrier();   // every wave is done with the activations: the partials overwrite them

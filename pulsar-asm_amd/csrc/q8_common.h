@@ -18,6 +18,7 @@ constexpr int kSlab = 2 * kTR * 16;     // bytes per (tile, block): 2 halves x 6
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
 
 __host__ __device__ inline int nchunks(int K) { return (K / kQ + kCB - 1) / kCB; }
 __host__ __device__ inline int ntiles(int N) { return (N + kTR - 1) / kTR; }
