@@ -112,7 +112,8 @@ def test_gemv_repeat_and_inplace(orc, pq, dev):
 
 @pytest.mark.parametrize("N,K,T", [(64, 2048, 1), (97, 96, 5), (130, 288, 33), (3104, 2048, 32),
                                    (2048, 8192, 32), (16384, 2048, 64), (2048, 2048, 77),
-                                   (16384, 2048, 100), (16416, 2048, 40)])
+                                   (16384, 2048, 100), (16416, 2048, 40), (16384, 4096, 48),
+                                   (16384, 2048, 512), (65536, 2048, 96)])
 def test_gemm_bitexact(orc, pq, dev, N, K, T):
     print(f"gemm N={N} K={K} T={T}", flush=True)
     W, S, w = _weights(orc, pq, dev, N, K, SEED + 11 * N + K)
