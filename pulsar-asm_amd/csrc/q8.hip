@@ -211,8 +211,10 @@ __global__ __launch_bounds__(512) void q8_gemv_kernel(const int8_t *__restrict__
 // and block b+1's dx are read from LDS, then block b is folded -- so each LDS
 // read has a whole fold to arrive in, and the MFMA result it folds was issued
 // one fold earlier. The scheduling barriers keep the reads ahead of the fold.
-// NB = kCB compiles the whole-chunk case without the per-block bounds.
-template <int NB, typename AF>
+// NB = kCB compiles the whole-chunk case without the per-block bounds. Only
+// the first NQ position quads (outputs a[0 .. 4*NQ)) are folded: NQ = 2 when
+// the tile's A operand holds 16 positions.
+template <int NB, int NQ, typename AF>
 __device__ __forceinline__ void mfma_chunk_pipe(float *a, const v4i *w, const v4i sv, AF AV,
                                                 const float (*dxs)[32], int kb0, int h, int nbc_rt) {
   const int nbc = NB ? NB : nbc_rt;
@@ -226,7 +228,7 @@ __device__ __forceinline__ void mfma_chunk_pipe(float *a, const v4i *w, const v4
     acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(0), w[0], zero, 0, 0, 0);
     if (nbc > 1) an = AV(1);
 #pragma unroll
-    for (int q = 0; q < 4; q++) d[0][q] = dp[2 * q];
+    for (int q = 0; q < NQ; q++) d[0][q] = dp[2 * q];
   }
 #pragma unroll
   for (int i = 0; i < kCB; i++) {
@@ -234,14 +236,14 @@ __device__ __forceinline__ void mfma_chunk_pipe(float *a, const v4i *w, const v4
       acc[(i + 1) & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(an, w[i + 1], zero, 0, 0, 0);
       if (i + 2 < kCB && i + 2 < nbc) an = AV(i + 2);
 #pragma unroll
-      for (int q = 0; q < 4; q++) d[(i + 1) & 1][q] = dp[8 * (i + 1) + 2 * q];
+      for (int q = 0; q < NQ; q++) d[(i + 1) & 1][q] = dp[8 * (i + 1) + 2 * q];
     }
     __builtin_amdgcn_sched_barrier(0);
     if (i < nbc) {
       const float dw = half_of(sw[i >> 1], i & 1);
       const v16i &ac = acc[i & 1];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
+      for (int q = 0; q < NQ; q++) {
         const float dq[4] = {d[i & 1][q].x, d[i & 1][q].y, d[i & 1][q].z, d[i & 1][q].w};
 #pragma unroll
         for (int k = 0; k < 4; k++) a[4 * q + k] = __builtin_fmaf(dw * dq[k], (float)ac[4 * q + k], a[4 * q + k]);
@@ -251,7 +253,7 @@ __device__ __forceinline__ void mfma_chunk_pipe(float *a, const v4i *w, const v4
   }
 }
 
-template <bool PIPE, typename AF>
+template <bool PIPE, int NQ = 4, typename AF>
 __device__ __forceinline__ void mfma_chunk(float *a, const v4i *w, const v4i sv, AF AV, const float (*dxs)[32],
                                            int kb0, int h, int nbc) {
   if constexpr (!PIPE) {   // one MFMA result live at a time (for a tight register budget)
@@ -263,7 +265,7 @@ __device__ __forceinline__ void mfma_chunk(float *a, const v4i *w, const v4i sv,
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(AV(i), w[i], acc, 0, 0, 0);
         const float dw = half_of(sw[i >> 1], i & 1);
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int q = 0; q < NQ; q++) {
           const float4 d4 = *reinterpret_cast<const float4 *>(&dxs[kb0 + i][8 * q + 4 * h]);
           const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
@@ -274,8 +276,8 @@ __device__ __forceinline__ void mfma_chunk(float *a, const v4i *w, const v4i sv,
     }
     return;
   }
-  if (nbc == kCB) mfma_chunk_pipe<kCB>(a, w, sv, AV, dxs, kb0, h, kCB);   // whole chunks: no branches
-  else mfma_chunk_pipe<0>(a, w, sv, AV, dxs, kb0, h, nbc);
+  if (nbc == kCB) mfma_chunk_pipe<kCB, NQ>(a, w, sv, AV, dxs, kb0, h, kCB);   // whole chunks: no branches
+  else mfma_chunk_pipe<0, NQ>(a, w, sv, AV, dxs, kb0, h, nbc);
 }
 
 constexpr int kGemmWaves = 8;
@@ -489,11 +491,14 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
 // 8 chunk partials then fold into y through LDS in chunk order (the partials
 // reuse the activation buffer once every wave has read it, which leaves room
 // for two workgroups per CU). Same numerics as the walking form.
+// PH = 16 gives a workgroup 16 positions (the A operand's other 16 rows read
+// zeros and their outputs are neither folded nor written): twice the
+// workgroups and half the fold per wave, for GEMMs with few slices.
 constexpr int kTileSlots = 8;
 constexpr size_t kTileActBytes = 32 * (size_t)kGemmARow;
 constexpr size_t kTileLds = kTileActBytes + (size_t)kTileSlots * kCB * 32 * 4;
 
-template <int S, bool PIPE>
+template <int S, bool PIPE, int PH = 32>
 __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const int8_t *__restrict__ pc,
                                                                         const uint16_t *__restrict__ ps,
                                                                         const int8_t *__restrict__ qx,
@@ -509,14 +514,16 @@ __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const
   float(*part)[S][16][64] = reinterpret_cast<float(*)[S][16][64]>(gsm);   // aliases as
   float(*dxs)[32] = reinterpret_cast<float(*)[32]>(gsm + kTileActBytes);
   const int nb = K / kQ, nch = nchunks(K);
-  const int p0 = blockIdx.z * 32;
+  static_assert(PH == 32 || PH == 16, "16 or 32 positions per workgroup");
+  constexpr int NQ = PH / 8;                          // position quads folded per lane
+  const int p0 = blockIdx.z * PH;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int sub = wave % S, slot = wave / S;
   const int h = lane >> 5, l32 = lane & 31;
   const int sl = blockIdx.x * S + sub;                 // 32-row slice
   const bool live = sl * 32 < N;
   const int tile = live ? sl >> 1 : 0, jt = (sl & 1) * 32 + l32;
-  const int np = T - p0 < 32 ? T - p0 : 32;
+  const int np = T - p0 < PH ? T - p0 : PH;   // rows past np of the A operand read zeros
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int8_t *>(pc + (size_t)tile * nb * kSlab), (short)0, live ? nb * kSlab : 0, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -570,7 +577,7 @@ __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const
       const int kb0 = slot * kCB;
       const lds_ptr<v4i> ap = lds_base(reinterpret_cast<const v4i *>(&as[l32][kb0 * kQ + 16 * h]));
       auto AV = [&](int i) { return ap[2 * i]; };   // block i: 32 bytes on
-      mfma_chunk<PIPE>(a, wv, sv, AV, dxs, kb0, h, min(kCB, nb - c * kCB));
+      mfma_chunk<PIPE, NQ>(a, wv, sv, AV, dxs, kb0, h, min(kCB, nb - c * kCB));
     }
     lds_barrier();   // every wave is done with the activations: the partials overwrite them
 #pragma unroll
@@ -581,7 +588,8 @@ __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const
     for (int k = 0; k < 2; k++) {
       const int e = t + k * NT;
       const int s2 = e >> 10, r = (e >> 6) & 15, l = e & 63;
-      for (int w = 0; w < n; w++) yv[k] = yv[k] + part[w][s2][r][l];
+      if ((r >> 2) < NQ)
+        for (int w = 0; w < n; w++) yv[k] = yv[k] + part[w][s2][r][l];
     }
   }
 #pragma unroll
@@ -590,7 +598,7 @@ __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const
     const int s2 = e >> 10, r = (e >> 6) & 15, l = e & 63;
     const int pos = p0 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
     const int row = (blockIdx.x * S + s2) * 32 + (l & 31);
-    if (pos < T && row < N) {
+    if ((r >> 2) < NQ && pos < T && row < N) {
       if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)pos * N + row] = f2bf(yv[k]);
       else reinterpret_cast<float *>(y)[(size_t)pos * N + row] = yv[k];
     }
@@ -759,8 +767,15 @@ extern "C" int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, cons
   }
   if (form == kFormSlice) {
     // the pipelined fold holds two MFMA results (one workgroup per CU): worth it
-    // while there is at most one workgroup per CU anyway
-    if ((long long)((N + 31) / 32) * ((T + 31) / 32) <= 256)
+    // while there is at most one workgroup per CU anyway; with at most 128
+    // (slice, 32 positions) items, 16 positions per workgroup spread them over
+    // twice the CUs (PQ_GEMM_PH = 32 / 16 overrides)
+    static const int env_ph = env_int("PQ_GEMM_PH");
+    const long long items32 = (long long)((N + 31) / 32) * ((T + 31) / 32);
+    if (env_ph != 32 && (env_ph == 16 ? items32 <= 256 : items32 <= 128))
+      launch(q8_gemm_tile_kernel<1, true, 16>, dim3((unsigned)((N + 31) / 32), 1, (unsigned)((T + 15) / 16)),
+             dim3(64 * kTileSlots), kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
+    else if (items32 <= 256)
       launch(q8_gemm_tile_kernel<1, true>, dim3((unsigned)((N + 31) / 32), 1, (unsigned)((T + 31) / 32)),
              dim3(64 * kTileSlots), kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
     else
