@@ -99,6 +99,7 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(const uint8_t *__restrict_
                                                         const uint16_t *__restrict__ scales,
                                                         const uint8_t *__restrict__ xq, float *__restrict__ y, int N,
                                                         int K) {
+  static_assert(64 % LPR == 0, "a row's lanes must sit in one wave");
   extern __shared__ __align__(16) unsigned char smem[];
   const int ng = K / kTqGroup, npc = 2 * ng;                 // groups, 16-byte pieces per row
   int *xperm = reinterpret_cast<int *>(smem);                  // K bytes, permuted
@@ -152,7 +153,10 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(const uint8_t *__restrict_
       }
     }
   }
-  __syncthreads();
+  // a row's LPR lanes sit in one wave (64 % LPR == 0), so its partials need
+  // only this wave's LDS writes to land
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
   if (gs == 0 && live) {   // groups ascending; partials read 8 at a time
     float acc = 0.0f;
     const float *pr = pg + r * ng;
