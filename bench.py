@@ -392,7 +392,7 @@ def ternary_bench(pq, torch, dev, g, reps=50, rotate_mb=400):
 
     def gemv(i, name, N, K):
         ws = sets[i % ncopy]
-        pq.tq2_gemv(ws[name][0], ws[name][1], x12 if K == 12288 else x4, N, K, out=outs[name])
+        pq.tq2_gemv(ws[name][0], ws[name][1], x12 if K == 12288 else x4, K, N, out=outs[name])
 
     # launch period per shape: back-to-back launches, weights rotating, HIP events on the launch stream
     per = []

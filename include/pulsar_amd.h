@@ -334,9 +334,11 @@ int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float 
  * xq = Q8_K activations (292 B per 256: fp32 d, 256 int8, 16 int16 bsums).
  * y[N] fp32, per row groups ascending: acc = fl(acc + fl(fl(ws*db) * isum))
  * with isum the exact int32 group dot (pq2_host.c:82-104). K a multiple of
- * 256, at most 32768. Replaces pq2_gemv_sm53_launch (pq2_wrap.h:24-28). */
-int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int N,
-                int K, void *stream);
+ * 256, at most 32768. Replaces pq2_gemv_sm53_launch (pq2_wrap.h:24-28) with
+ * its arguments in its order -- (..., y, K, N, stream) -- and its convention
+ * of a negative status on error. */
+int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int K,
+                int N, void *stream);
 /* x [T][K] fp32 -> Q8_K blocks (quantize_row_q8_K_ref as restated in
  * fwd8.c:61-137); K a multiple of 256. */
 int pq_q8k_quant(const float *x, uint8_t *out, int K, int T, void *stream);

@@ -531,17 +531,28 @@ void orc_headnorm(uint16_t *x, const float *w, int nheads, int hd, float eps) {
   }
 }
 
-/* RoPE table [pos][rot/2][cos, sin]: invf_i = 1/theta^(2i/hd) and the angle
- * fl((float)pos * invf_i) as the reference forms them (lfm3_nanode.cu:3719-3723
- * build_invf, 483-498 k_rope), cos/sin evaluated in double and rounded once.
- * Device and CPU both read a table (the reference notes it could not match
- * torch's cos/sin on the device, lfm3_nanode.cu:43-44). */
+/* RoPE inverse frequencies as the reference's host builds them
+ * (lfm3_nanode.cu:3719-3723 build_invf, dim = head_dim): in float,
+ * invf_i = 1.0f / powf(theta, (float)(2i) / (float)hd) for i < rot/2, and 0
+ * past them (the zero tail). */
+void orc_rope_invf(float *invf, int hd, int rot, float theta) {
+  for (int i = 0; i < hd / 2; i++)
+    invf[i] = i < rot / 2 ? 1.0f / powf(theta, (float)(2 * i) / (float)hd) : 0.0f;
+}
+
+/* RoPE table [pos][rot/2][cos, sin]: the angle is the fp32 product
+ * fl((float)pos * invf_i) (k_rope, lfm3_nanode.cu:483-498), and cos/sin of
+ * that float angle are evaluated in double and rounded once to float (the
+ * reference evaluates cosf/sinf on the device and notes it could not match
+ * torch's cos/sin there, lfm3_nanode.cu:43-44; a table read on both sides
+ * fixes one value). */
 void orc_rope_table(float *cs, int maxpos, int hd, int rot, float theta) {
   const int half = rot / 2;
+  float invf[512];
+  orc_rope_invf(invf, hd, rot, theta);
   for (int p = 0; p < maxpos; p++)
     for (int i = 0; i < half; i++) {
-      const float invf = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)hd));
-      const float ang = (float)p * invf;
+      const float ang = (float)p * invf[i];
       cs[((size_t)p * half + i) * 2 + 0] = (float)cos((double)ang);
       cs[((size_t)p * half + i) * 2 + 1] = (float)sin((double)ang);
     }

@@ -244,6 +244,12 @@ def headnorm(x, w, nheads, hd, eps=1e-5):
     return x
 
 
+def rope_invf(hd, rot, theta):
+    invf = np.empty(hd // 2, np.float32)
+    lib().orc_rope_invf(_p(invf), C.c_int(hd), C.c_int(rot), C.c_float(theta))
+    return invf
+
+
 def rope_table(maxpos, hd, rot, theta):
     cs = np.empty(maxpos * (rot // 2) * 2 + 2, np.float32)
     lib().orc_rope_table(_p(cs), C.c_int(maxpos), C.c_int(hd), C.c_int(rot), C.c_float(theta))

@@ -302,26 +302,33 @@ static Blob *blob_open(const char *path) {
     e.dtype = (int)dt->num;
     e.crc = (uint32_t)crc;
     e.ndim = (int)ne->arr.size();
-    long long elems = 1;
+    // every size is bounded by the file's: an element count past fsize (or a
+    // product that would overflow on the way there) cannot be a real tensor
+    uint64_t elems = 1;
     for (int d = 0; d < e.ndim; d++) {
       if (ne->arr[d].kind != Json::Num || ne->arr[d].num < 1 || ne->arr[d].num > 1e12) {
         fail(PQ_ERR_ARG, "blob: %s has a bad shape", e.name.c_str());
         return nullptr;
       }
       e.ne[d] = (long long)ne->arr[d].num;
-      elems *= e.ne[d];
+      if (__builtin_mul_overflow(elems, (uint64_t)e.ne[d], &elems) || elems > B->fsize) {
+        fail(PQ_ERR_ARG, "blob: %s has more elements than the file has bytes", e.name.c_str());
+        return nullptr;
+      }
     }
     // the payload must be what the shape and dtype say (export_lfm3_q8.py:132-155)
     bool ok = false;
-    if (e.dtype == 1) ok = e.ndim == 2 && e.ne[1] % 32 == 0 && e.ncodes == (uint64_t)elems && e.nscales == (uint64_t)elems / 8;
-    else if (e.dtype == 2) ok = e.ncodes == (uint64_t)elems * 4 && e.nscales == 0;
-    else if (e.dtype == 3) ok = e.ncodes == (uint64_t)elems * 2 && e.nscales == 0;
+    if (e.dtype == 1) ok = e.ndim == 2 && e.ne[1] % 32 == 0 && e.ncodes == elems && e.nscales == elems / 8;
+    else if (e.dtype == 2) ok = e.ncodes == elems * 4 && e.nscales == 0;      // elems <= fsize: no overflow
+    else if (e.dtype == 3) ok = e.ncodes == elems * 2 && e.nscales == 0;
     if (!ok) {
       fail(PQ_ERR_ARG, "blob: %s: dtype %d with %llu + %llu payload bytes does not match its shape", e.name.c_str(),
            e.dtype, (unsigned long long)e.ncodes, (unsigned long long)e.nscales);
       return nullptr;
     }
-    if (B->base + e.off + e.ncodes + e.nscales > B->fsize) {
+    // each term is checked against fsize before the sum, so it cannot wrap
+    if (e.off > B->fsize || e.ncodes > B->fsize || e.nscales > B->fsize ||
+        B->base + e.off + e.ncodes + e.nscales > B->fsize) {
       fail(PQ_ERR_ARG, "blob: %s extends past the end of the file (truncated?)", e.name.c_str());
       return nullptr;
     }

@@ -246,7 +246,8 @@ static void rope_table(std::vector<float> &cs, int ctx, int hd, int rot, float t
   cs.assign((size_t)ctx * half * 2 + 2, 0.0f);
   for (int p = 0; p < ctx; p++)
     for (int i = 0; i < half; i++) {
-      const float invf = (float)(1.0 / pow((double)theta, (double)(2 * i) / (double)hd));
+      // build_invf (lfm3_nanode.cu:3719-3723): float powf and a float divide.
+      const float invf = 1.0f / powf(theta, (float)(2 * i) / (float)hd);
       const float ang = (float)p * invf;
       cs[((size_t)p * half + i) * 2] = (float)cos((double)ang);
       cs[((size_t)p * half + i) * 2 + 1] = (float)sin((double)ang);
@@ -768,6 +769,10 @@ extern "C" int pq_engine_feed(void *h, const int32_t *tokens, int n, int32_t *ne
   PQ_REQUIRE(h && tokens && n > 0, PQ_ERR_ARG, "pq_engine_feed: bad arguments");
   Engine &E = *static_cast<Engine *>(h);
   PQ_REQUIRE(E.loaded, PQ_ERR_STATE, "pq_engine_feed: weights not loaded");
+  // refused before the first chunk, so a prompt too long for the context
+  // leaves the KV cache, the conv rings and the position as they were
+  PQ_REQUIRE(n <= E.c.ctx - E.pos, PQ_ERR_STATE, "pq_engine_feed: %d tokens at position %d exceed the context %d", n,
+             E.pos, E.c.ctx);
   PQ_TRY(prefill(E, tokens, n, E.tok));
   if (next_id && hipMemcpy(next_id, E.tok, 4, hipMemcpyDeviceToHost) != hipSuccess)
     return fail(PQ_ERR_LAUNCH, "id copy failed");

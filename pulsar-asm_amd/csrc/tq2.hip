@@ -230,7 +230,7 @@ extern "C" int pq_q8k_quant(const float *x, uint8_t *out, int K, int T, void *st
   return check_launch("pq_q8k_quant");
 }
 
-extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int N, int K,
+extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int K, int N,
                            void *stream) {
   PQ_REQUIRE(codes && scales && xq && y, PQ_ERR_ARG, "pq_tq2_gemv: null pointer");
   PQ_REQUIRE(N > 0 && K > 0 && K % kQ8K == 0 && K <= 32768, PQ_ERR_ARG,

@@ -235,11 +235,12 @@ def q8k_quant(x):
     return out[0] if x.dim() == 1 else out
 
 
-def tq2_gemv(codes, scales, xq, N, K, out=None):
-    """PQ2_0 codes uint8 [N][K/4], fp16 scale bits [N][K/128], Q8_K xq -> y fp32 [N]."""
+def tq2_gemv(codes, scales, xq, K, N, out=None):
+    """PQ2_0 codes uint8 [N][K/4], fp16 scale bits [N][K/128], Q8_K xq -> y fp32 [N].
+    K before N, as pq2_gemv_sm53_launch takes them (pq2_wrap.h:24-28)."""
     if out is None:
         out = torch.empty(N, dtype=torch.float32, device=codes.device)
-    check(lib().pq_tq2_gemv(codes.data_ptr(), scales.data_ptr(), xq.data_ptr(), out.data_ptr(), N, K, stream_ptr()),
+    check(lib().pq_tq2_gemv(codes.data_ptr(), scales.data_ptr(), xq.data_ptr(), out.data_ptr(), K, N, stream_ptr()),
           "pq_tq2_gemv")
     return out
 

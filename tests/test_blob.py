@@ -108,3 +108,34 @@ def test_header_matches_exporter_layout(tmp_path):
     e = h["table"][0]
     body = raw[12 + n + e["off"]:12 + n + e["off"] + e["ncodes"] + e["nscales"]]
     assert zlib.crc32(body) & 0xFFFFFFFF == e["crc"]
+
+
+def _rewrite_entry(raw, idx, **fields):
+    """The blob with table entry idx's fields replaced (header re-serialized
+    compactly; payload offsets are relative to the data start, so they hold)."""
+    import json
+    n = struct.unpack("<I", raw[8:12])[0]
+    h = json.loads(raw[12:12 + n])
+    h["table"][idx].update(fields)
+    hj = json.dumps(h, separators=(",", ":")).encode()
+    return raw[:8] + struct.pack("<I", len(hj)) + hj + raw[12 + n:]
+
+
+def test_oversized_sizes_are_refused(tmp_path):
+    """Shape products and offsets that would overflow 64 bits (or wrap the
+    end-of-payload sum) are refused, not taken as small tensors."""
+    p = tmp_path / "m.lfm3q8"
+    write_blob(p, {}, _tensors())
+    raw = p.read_bytes()
+    cases = {
+        # 2^96 elements: wraps to 0 in 64 bits, so ncodes 0 would have matched
+        "wrap_ne": dict(dtype=2, ne=[2 ** 32, 2 ** 32, 2 ** 32], ncodes=0, nscales=0),
+        "big_ne": dict(dtype=3, ne=[10 ** 12, 10 ** 12], ncodes=2 * 10 ** 24 % 2 ** 64, nscales=0),
+        "big_off": dict(off=2 ** 64 - 2048),
+        "big_ncodes": dict(dtype=2, ne=[2 ** 61], ncodes=2 ** 63, nscales=0),
+    }
+    for why, f in cases.items():
+        q = tmp_path / why
+        q.write_bytes(_rewrite_entry(raw, 1, **f))
+        with pytest.raises(PQError):
+            Blob(q)

@@ -160,3 +160,23 @@ def test_blob_load_matches_synthetic(orc, pq, dev, tmp_path):
     with pytest.raises(pq.PQError, match="feed_forward"):
         e.load_blob(p)
     e.close()
+
+
+def test_feed_past_context_is_refused_whole(orc, pq, dev):
+    """A prompt longer than the room left in the context is refused before the
+    first chunk: the position, KV cache and conv rings stay as they were."""
+    cfg = dict(TINY, ctx=64)
+    e = _engine(pq, cfg)
+    ref = _engine(pq, cfg)
+    first = orc.gen_tokens(11, 40, cfg["vocab"])
+    e.feed(first)
+    ref.feed(first)
+    with pytest.raises(pq.PQError, match="exceed the context"):
+        e.feed(orc.gen_tokens(12, 25, cfg["vocab"]))      # 40 + 25 > 64
+    assert e.position() == 40
+    more = orc.gen_tokens(13, 24, cfg["vocab"])            # 40 + 24 == 64 still fits
+    r_e, lg_e = e.feed(more, True)
+    r_r, lg_r = ref.feed(more, True)
+    assert r_e == r_r and np.array_equal(lg_e.view(np.uint32), lg_r.view(np.uint32))
+    e.close()
+    ref.close()

@@ -54,6 +54,8 @@ GEMV_SHAPES = [
     (3104, 2048), (2048, 2048), (16384, 2048),       # fused q|k|v|gate, o_proj, gate+up
     (2048, 8192),                                    # down projection (split-K across workgroups)
     (6144, 2048),                                    # conv in_proj
+    # the reference's own K set (q8_gemv_neon_test.c:152-157: N = 256 for K <= 128, else 97)
+    (256, 32), (256, 64), (256, 96), (256, 128), (97, 2048), (97, 4096), (97, 7680),
 ]
 
 

@@ -20,15 +20,23 @@ def test_q8k_quant(orc, pq, dev, K, T):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 12288), (37, 9728), (61, 2560), (3, 256)])
+# config-5 shapes, then the reference's parity set (bonsai2 pq1t_parity.c:71-74:
+# 151669 x 2560 is the LM head, 1001 x 2560 an odd row count), then small ones
+TQ2_SHAPES = [(12288, 4096), (4096, 12288),
+              (6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728), (151669, 2560), (1001, 2560), (37, 9728),
+              (61, 2560), (3, 256)]
+
+
+@pytest.mark.parametrize("N,K", TQ2_SHAPES)
 def test_tq2_gemv(orc, pq, dev, N, K):
+    print(f"tq2 N={N} K={K}", flush=True)
     codes = orc.gen_ternary(N + K, N * K // 4).reshape(N, K // 4)
     S = orc.gen_scales(N + K + 1, N * K // 128).reshape(N, K // 128)
     x = orc.gen_normal(N + K + 2, K)
     xq = orc.q8k_quant(x)
     want = orc.tq2_gemv(codes, S, xq, N, K)
     xqd = pq.q8k_quant(torch.from_numpy(x).to(dev))
-    y = pq.tq2_gemv(torch.from_numpy(codes).to(dev), torch.from_numpy(S.view(np.int16)).to(dev), xqd, N, K)
+    y = pq.tq2_gemv(torch.from_numpy(codes).to(dev), torch.from_numpy(S.view(np.int16)).to(dev), xqd, K, N)
     got = y.cpu().numpy()
     bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
     assert bad.size == 0, f"{bad.size} rows differ, first {bad[:4]}"
@@ -38,5 +46,28 @@ def test_tq2_golden(pq, dev):
     d = np.load(os.path.join(os.path.dirname(__file__), "golden", "kernels.npz"))
     N, K = d["t_y"].size, d["t_x"].size
     y = pq.tq2_gemv(torch.from_numpy(d["t_codes"]).to(dev), torch.from_numpy(d["t_S"].view(np.int16)).to(dev),
-                    torch.from_numpy(d["t_xq"]).to(dev), N, K)
+                    torch.from_numpy(d["t_xq"]).to(dev), K, N)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), d["t_y"].view(np.uint32))
+
+
+@pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 12288)])
+def test_tq2_reference_call_order(orc, pq, dev, N, K):
+    """The entry point called as pq2_parity.c:79 calls pq2_gemv_sm53_launch:
+    (w_codes, w_scales_h, xq, y, K, rows, stream), returning 0."""
+    import ctypes
+    codes = orc.gen_ternary(7 * N + K, N * K // 4).reshape(N, K // 4)
+    S = orc.gen_scales(7 * N + K + 1, N * K // 128).reshape(N, K // 128)
+    x = orc.gen_normal(7 * N + K + 2, K)
+    xq = orc.q8k_quant(x)
+    d_cd, d_sc = torch.from_numpy(codes).to(dev), torch.from_numpy(S.view(np.int16)).to(dev)
+    d_xq = torch.from_numpy(xq).to(dev)
+    d_y = torch.zeros(N, dtype=torch.float32, device=dev)
+    rows = N
+    rc = pq.lib().pq_tq2_gemv(ctypes.c_void_p(d_cd.data_ptr()), ctypes.c_void_p(d_sc.data_ptr()),
+                              ctypes.c_void_p(d_xq.data_ptr()), ctypes.c_void_p(d_y.data_ptr()), K, rows, None)
+    torch.cuda.synchronize()
+    assert rc == 0
+    assert np.array_equal(d_y.cpu().numpy().view(np.uint32), orc.tq2_gemv(codes, S, xq, N, K).view(np.uint32))
+    # K that is not a multiple of 256 is refused with a negative status
+    assert pq.lib().pq_tq2_gemv(ctypes.c_void_p(d_cd.data_ptr()), ctypes.c_void_p(d_sc.data_ptr()),
+                                ctypes.c_void_p(d_xq.data_ptr()), ctypes.c_void_p(d_y.data_ptr()), 100, rows, None) < 0

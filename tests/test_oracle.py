@@ -326,6 +326,160 @@ def test_argmax_lowest_index(orc):
     assert orc.argmax(v) == 1
 
 
+def _bf16_rne_exact(v):
+    """bf16 bits of the exact rational v rounded to nearest even (normal range)."""
+    from fractions import Fraction
+    v = Fraction(v)
+    if v == 0:
+        return 0
+    sign, a = (0x8000, -v) if v < 0 else (0, v)
+    e = 0
+    while a >= 2:
+        a /= 2
+        e += 1
+    while a < 1:
+        a *= 2
+        e -= 1
+    q = a * 128                      # 8 significant bits: q in [128, 256)
+    n = q.numerator // q.denominator
+    r = q - n
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    val = Fraction(n, 128) * Fraction(2) ** e
+    return sign | int(np.float32(float(val)).view(np.uint32) >> 16)
+
+
+def test_rmsnorm_rounds_before_weight(orc):
+    """k_rmsnorm (lfm3_nanode.cu:433-436) rounds x*rs to bf16 and only then
+    multiplies by the weight. x = 1 everywhere gives rs = 1/sqrt(1 + eps) and
+    bf16(x*rs) = 1, so the two-round form is bf16(w); with w = 1 + 2^-8 + 2^-20,
+    just above the bf16 midpoint between 1 and 1 + 2^-7, that is 1 + 2^-7
+    (0x3f81), while one rounding of w*rs (below the midpoint) gives 1 (0x3f80)."""
+    n = 2048
+    x = np.full(n, 0x3F80, np.uint16)
+    w = np.full(n, 1 + 2.0 ** -8 + 2.0 ** -20, np.float32)
+    assert np.all(orc.rmsnorm(x, w, 1e-5) == 0x3F81)
+    rs = np.float32(1) / np.sqrt(np.float32(1) + np.float32(1e-5))
+    assert orc.f2bf(np.float32(w[0]) * rs) == 0x3F80          # the one-round form differs
+    # eps = 0: rs = 1 exactly, so both forms give bf16(w)
+    assert np.all(orc.rmsnorm(x, w, 0.0) == 0x3F81)
+
+
+def test_headnorm_is_rmsnorm_per_head(orc):
+    """k_headnorm (lfm3_nanode.cu:460-479) is RMSNorm over each hd slice with the
+    shared [hd] weight."""
+    for nh, hd in ((4, 64), (3, 128)):
+        x = orc.f2bf(orc.gen_normal(70 + hd, nh * hd) * 2)
+        w = orc.gen_affine(71 + hd, hd, 1.0, 0.1)
+        got = orc.headnorm(x, w, nh, hd)
+        want = np.concatenate([orc.rmsnorm(x[h * hd:(h + 1) * hd], w) for h in range(nh)])
+        assert np.array_equal(got, want)
+        assert not np.array_equal(got, orc.rmsnorm(x, np.tile(w, nh)))   # not one norm over all heads
+
+
+def test_embed_row_closed_form(orc):
+    """k_dequant_row (lfm3_nanode.cu:138-142): bf16(code * scale), one RNE
+    rounding of the product (exact in fp32: 8 x 11 significant bits), with the
+    scale of the element's own 32-block."""
+    from fractions import Fraction
+    # hand-computed: 87 * 1.5009765625 (fp16 0x3e01) = 130.5849609375 -> bf16 131 (0x4303);
+    # truncation would give 130 (0x4302)
+    W = np.zeros((2, 64), np.int8)
+    S = np.full((2, 2), 0x3C00, np.uint16)
+    W[1, 0], S[1, 0] = 87, 0x3E01
+    W[1, 40], S[1, 1] = -3, 0x3555        # block 1 has its own scale
+    row = orc.embed_row(W, S, 1)
+    assert row[0] == 0x4303
+    assert row[40] == _bf16_rne_exact(-3 * Fraction(int(np.uint16(0x3555).view(np.float16).astype(np.float64) * 2 ** 24), 2 ** 24))
+    assert np.all(row[1:32] == 0) and row[32] == 0
+    # random rows, every element against the exact rational product
+    Wr, Sr = orc.q8_weights(72, 8, 256)
+    for tok in (0, 5, 7):
+        row = orc.embed_row(Wr, Sr, tok)
+        for i in range(256):
+            sc = Fraction(float(Sr[tok, i // 32].view(np.float16)))
+            assert row[i] == _bf16_rne_exact(int(Wr[tok, i]) * sc), (tok, i)
+
+
+def _same_rotation(orc, got, want, a, b):
+    """The pair (a, b) bit for bit; the other dims are zeros (of either sign:
+    0*c - 0*s keeps IEEE's signed zero)."""
+    assert got[a] == want[a] and got[b] == want[b], (a, b, got[a], got[b], want[a], want[b])
+    assert np.array_equal(orc.bf2f(got), orc.bf2f(want))
+
+
+@pytest.mark.parametrize("theta,hd,rot", [(1e6, 64, 32), (1e6, 128, 64), (1e4, 64, 64)])
+def test_rope_invf_is_build_invf(orc, theta, hd, rot):
+    """build_invf (lfm3_nanode.cu:3719-3723) runs on the host in float:
+    invf_i = 1.0f / powf(base, (float)(2i) / (float)dim), 0 past rot/2. Pinned
+    against the correctly rounded powf (mpmath at 200 bits) and an IEEE float
+    divide; the double-precision formula differs in several entries."""
+    import mpmath
+    mpmath.mp.prec = 200
+    invf = orc.rope_invf(hd, rot, theta)
+    t = np.float32(theta)
+    want = np.zeros(hd // 2, np.float32)
+    for i in range(rot // 2):
+        e = np.float32(2 * i) / np.float32(hd)
+        p = np.float32(float(mpmath.power(mpmath.mpf(float(t)), mpmath.mpf(float(e)))))
+        want[i] = np.float32(1) / p
+    assert np.array_equal(invf.view(np.uint32), want.view(np.uint32))
+    dbl = np.array([1.0 / theta ** (2 * i / hd) for i in range(rot // 2)]).astype(np.float32)
+    assert np.count_nonzero(dbl != want[:rot // 2]) >= 5
+
+
+def test_rope_table_float_angle(orc):
+    """Table entries are cos/sin of the fp32 angle fl(pos * invf_i) (k_rope's
+    __fmul_rn, lfm3_nanode.cu:491), each correctly rounded to float."""
+    import mpmath
+    mpmath.mp.prec = 120
+    maxpos, hd, rot, theta = 4096, 64, 32, 1e6
+    cs = orc.rope_table(maxpos, hd, rot, theta).reshape(maxpos, rot // 2, 2)
+    invf = orc.rope_invf(hd, rot, theta)[: rot // 2]
+    ang = np.arange(maxpos, dtype=np.float32)[:, None] * invf[None, :]
+    assert np.array_equal(cs[..., 0], np.cos(ang.astype(np.float64)).astype(np.float32))
+    assert np.array_equal(cs[..., 1], np.sin(ang.astype(np.float64)).astype(np.float32))
+    # independent spot checks at 120 bits
+    rng = np.random.default_rng(73)
+    for p, i in zip(rng.integers(0, maxpos, 48), rng.integers(0, rot // 2, 48)):
+        a = mpmath.mpf(float(ang[p, i]))
+        assert cs[p, i, 0] == np.float32(float(mpmath.cos(a)))
+        assert cs[p, i, 1] == np.float32(float(mpmath.sin(a)))
+    # an angle formed in double would give a different table
+    ang_d = np.arange(maxpos, dtype=np.float64)[:, None] * invf.astype(np.float64)[None, :]
+    assert np.count_nonzero(np.cos(ang_d).astype(np.float32) != cs[..., 0]) > 1000
+
+
+def test_rope_pairing_sign_and_tail(orc):
+    """k_rope (lfm3_nanode.cu:483-498): pairs (i, i + hd/2) for i < rot/2,
+    lo' = bf16(lo*c - hi*s), hi' = bf16(hi*c + lo*s); dims in [rot/2, hd/2) and
+    their partners are left as they are; position 0 is the identity."""
+    maxpos, hd, rot, nh = 1100, 64, 32, 3
+    cs = orc.rope_table(maxpos, hd, rot, 1e6).reshape(maxpos, rot // 2, 2)
+    x = orc.f2bf(orc.gen_normal(74, nh * hd))
+    assert np.array_equal(orc.rope(x, cs.ravel(), 0, nh, hd, rot), x)
+    pos = 1000
+    for i in range(rot // 2):
+        c, s = cs[pos, i]
+        for h in range(nh):
+            e = np.zeros(nh * hd, np.uint16)
+            e[h * hd + i] = 0x3F80                          # lo = 1
+            got = orc.rope(e, cs.ravel(), pos, nh, hd, rot)
+            want = np.zeros_like(e)
+            want[h * hd + i], want[h * hd + i + hd // 2] = orc.f2bf([c])[0], orc.f2bf([s])[0]
+            _same_rotation(orc, got, want, h * hd + i, h * hd + i + hd // 2)
+            e = np.zeros(nh * hd, np.uint16)
+            e[h * hd + i + hd // 2] = 0x3F80                # hi = 1
+            got = orc.rope(e, cs.ravel(), pos, nh, hd, rot)
+            want = np.zeros_like(e)
+            want[h * hd + i], want[h * hd + i + hd // 2] = orc.f2bf([-s])[0], orc.f2bf([c])[0]
+            _same_rotation(orc, got, want, h * hd + i, h * hd + i + hd // 2)
+    got = orc.rope(x, cs.ravel(), 777, nh, hd, rot).reshape(nh, hd)
+    xr = x.reshape(nh, hd)
+    for lo, hi in ((rot // 2, hd // 2), (hd // 2 + rot // 2, hd)):
+        assert np.array_equal(got[:, lo:hi], xr[:, lo:hi])
+
+
 # ----------------------------------------------------------------- backbone
 TINY = dict(hidden=256, ffn=512, vocab=1000, nlayers=4, nh=4, nkv=2, hd=64, rot=32, ntaps=3, ctx=256,
             eps=1e-5, theta=1e6, seed=20261201, attn_mask=0b1010)
