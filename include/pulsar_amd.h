@@ -123,6 +123,20 @@ size_t pq_q8_gemm_workspace_bytes(int N, int K, int T);
 int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
                   void *y, int y_dtype, int N, int K, int T, void *ws, size_t ws_bytes, void *stream);
 
+/* The same GEMM without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the split-K partials go to a library-owned device array
+ * of pq_q8_gemm_scratch_bytes() (16 MiB) per GPU, held until the process ends.
+ * No counterpart in the reference. It calls no allocator. Shapes whose split
+ * needs more than the array (pq_q8_gemm_workspace_bytes > the array) are
+ * refused with PQ_ERR_WORKSPACE. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race
+ * and must be serialized by the caller. The stream must belong to the
+ * current device. Same bits as pq_q8_gemm_ws. */
+size_t pq_q8_gemm_scratch_bytes(void);
+int pq_q8_gemm_noalloc(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
+                       void *y, int y_dtype, int N, int K, int T, void *stream);
+
 /* The reference's own GEMV numerics (R2), the order of its CPU transcription
  * (cpuchk_run, lfm3_nanode.cu:4658-4684): codes int8 [N][K] row-major and an
  * fp32 scale per 32-block [N][K/32] (the .lfm3q8 tensors, untiled); x bf16

@@ -18,6 +18,7 @@
 #include "pq_host.h"
 #include "q8_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace pq {
@@ -797,4 +798,65 @@ extern "C" int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, cons
 extern "C" int pq_q8_gemm(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx, void *y,
                           int y_dtype, int N, int K, int T, void *stream) {
   return pq_q8_gemm_ws(pcodes, pscales, qx, dx, y, y_dtype, N, K, T, nullptr, 0, stream);
+}
+
+// ------------------------------------------------- the allocation-free GEMM
+// pq_q8_gemm_ws with its split-K partials in a library-owned device array
+// instead of a caller workspace, for callers that cannot allocate. The array
+// is one per GPU (each device gets its own copy of the module's globals) and
+// lives until the process ends. Its device address comes from
+// hipGetSymbolAddress once per device, with that device current, and only
+// that address is ever handed to kernels: in host code `scratch` names a
+// host-side stand-in, not device memory.
+namespace pq {
+constexpr size_t kScratchBytes = (size_t)16 << 20;   // 16 MiB per GPU
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kMaxDevices];
+
+// The scratch array's device address on the current device (looked up on the
+// first call there). The stream, if given, must belong to the current device.
+static int scratch_address(hipStream_t st, void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(PQ_ERR_LAUNCH, "pq_q8_gemm_noalloc: no current device");
+  if (st != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev)
+      return fail(PQ_ERR_ARG, "pq_q8_gemm_noalloc: the stream does not belong to the current device %d", dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(PQ_ERR_LAUNCH, "pq_q8_gemm_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PQ_OK;
+}
+}  // namespace pq
+
+extern "C" size_t pq_q8_gemm_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int pq_q8_gemm_noalloc(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
+                                  void *y, int y_dtype, int N, int K, int T, void *stream) {
+  PQ_REQUIRE(N > 0 && K > 0 && K % kQ == 0 && T > 0, PQ_ERR_ARG, "pq_q8_gemm_noalloc: N=%d K=%d T=%d", N, K, T);
+  const size_t need = pq_q8_gemm_workspace_bytes(N, K, T);
+  PQ_REQUIRE(need <= kScratchBytes, PQ_ERR_WORKSPACE,
+             "pq_q8_gemm_noalloc: N=%d K=%d T=%d splits K into %zu bytes of partials, more than the %zu-byte "
+             "scratch array (call pq_q8_gemm_ws with a workspace)",
+             N, K, T, need, kScratchBytes);
+  void *ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(as_stream(stream), &ws);
+    if (rc != PQ_OK) return rc;
+  }
+  // every partial the split writes is written before the fold reads it, so
+  // nothing in the array needs clearing between calls
+  return pq_q8_gemm_ws(pcodes, pscales, qx, dx, y, y_dtype, N, K, T, ws, need, stream);
 }
