@@ -6,22 +6,26 @@ A step is one pass of the decode hot path over one synthetic layer at T=1: the
 GEMVs fused q|k|v 3072x2048, o_proj 2048x2048, gate+up 16384x2048, down
 2048x8192 and the LM head 65536x2048 (fp32 logits), from packed Q8_0 weights
 resident in HBM, each quantizing its fp32 x (K=2048 or 8192) to Q8_0 in its own
-prologue (q8_gemv_fused_kernel, PQ_PRO_F32). The weights rotate over enough
-copies (>= 600 MB) that no step reads another step's weights out of the 256 MB
-Infinity Cache.
+prologue (q8_gemv_fused_kernel, PQ_PRO_F32). Every shape reads its weights from
+its own pool of >= 300 MB of distinct copies, rotated launch by launch, so no
+launch finds its weights in the 256 MB Infinity Cache.
 
-Prints ONE JSON line. value = algorithmic bytes per step / time per step (GB/s);
-roofline = the GEMV kernel's algorithmic bytes / its launch period, timed with
-HIP events on the launch stream over back-to-back launches of each shape (the
-period includes the dispatch gap between launches), against 8 TB/s;
-cpu_baseline = the reference's own CPU GEMV (.auto/lfm3/q8_gemv_cpu.c gemv_q8,
-compiled into oracle/_ref) on the host cores over a bounded sample of the same
-shapes.
+Prints ONE JSON line. value = algorithmic bytes per step / time per step (GB/s;
+the K steps are one captured graph, the median of 5 timed replays). roofline =
+the GEMV kernel's algorithmic bytes / its mean launch duration, each launch
+timed by HIP events attached to its own dispatch (the quantity rocprofv3's
+kernel trace reports), against 8 TB/s. cpu_baseline = the reference's own CPU
+GEMV (.auto/lfm3/q8_gemv_cpu.c gemv_q8, compiled into oracle/_ref) on the host
+cores over a bounded sample of the same shapes. The other keys are the single
+8192x2048 GEMV, the 24-layer backbone decode and its prompt prefill, the prefill
+GEMMs, the ternary GEMVs, the reference-numerics GEMVs and Q4/Q5, each with its
+own roofline and, where the reference has a CPU path, its CPU figure.
 """
 import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -29,6 +33,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "pulsar-asm_amd"))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+ROTATE_MB = 300          # distinct weight bytes per shape, rotated (> the 256 MB Infinity Cache)
 SHAPES = [  # name, N, K, output dtype
     ("qkv", 3072, 2048, "bf16"),
     ("o_proj", 2048, 2048, "bf16"),
@@ -66,7 +72,7 @@ def graph_of(torch, fn):
     return g
 
 
-def timed_replay(torch, g, stream, reps=1):
+def timed_replay(torch, g, stream, reps=5):
     """Milliseconds per replay of g, HIP events on the launch stream: two
     untimed replays (clocks settle), then the median of reps timed replays."""
     from pulsar_amd.hiptime import Event
@@ -79,8 +85,49 @@ def timed_replay(torch, g, stream, reps=1):
         g.replay()
         ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    t = sorted(ev[i].elapsed_ms(ev[i + 1]) for i in range(reps))
-    return t[len(t) // 2]
+    return statistics.median(ev[i].elapsed_ms(ev[i + 1]) for i in range(reps))
+
+
+def period_ms(torch, launch, n, stream):
+    """Launch period: n back-to-back launches (launch(i), rotating weights) in one
+    graph, median of 5 replays, divided by n (includes the gap between launches)."""
+    g = graph_of(torch, lambda: [launch(i) for i in range(n)])
+    ms = timed_replay(torch, g, stream) / n
+    del g
+    return ms
+
+
+def dispatch_ms(pq, torch, launch, n, warm=3):
+    """Mean and median duration of n eager launches (launch(i), rotating weights),
+    each timed by two HIP events attached to its own dispatch
+    (pq_time_next_launch): the kernel's own start-to-end, as rocprofv3 reports it."""
+    from pulsar_amd.hiptime import Event
+    for i in range(warm):
+        launch(i)
+    torch.cuda.synchronize()
+    ev = [(Event(), Event()) for _ in range(n)]
+    for i in range(n):
+        pq.check(pq.lib().pq_time_next_launch(ev[i][0].h, ev[i][1].h), "pq_time_next_launch")
+        launch(warm + i)
+    torch.cuda.synchronize()
+    d = [a.elapsed_ms(b) for a, b in ev]
+    return statistics.fmean(d), statistics.median(d)
+
+
+def copies_for(nbytes, min_mb=ROTATE_MB):
+    return max(2, math.ceil(min_mb * 1e6 / nbytes))
+
+
+def q8_pool(pq, torch, dev, g, N, K, min_mb=ROTATE_MB):
+    """Distinct packed Q8_0 copies of an N x K weight, >= min_mb in all."""
+    per = pq.lib().pq_q8_packed_codes_bytes(N, K) + pq.lib().pq_q8_packed_scales_bytes(N, K)
+    pool = []
+    for _ in range(copies_for(per, min_mb)):
+        codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        scales = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().view(torch.int16)
+        pool.append(pq.Q8Weight(codes, scales))
+        del codes, scales
+    return pool, per
 
 
 def gemv_bytes(N, K, out):
@@ -98,51 +145,14 @@ def gpu_desc(torch, pq):
             "clock_MHz": round(float(out[0].item()))}
 
 
-def cpu_baseline(seconds=10.0):
-    """The reference's gemv_q8 (fp32 x, fp32 scales) over the same shapes, on all host cores."""
-    import ctypes as C
-    import numpy as np
+# ------------------------------------------------------------------ CPU side
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
-    ref = pyoracle.ref()
-    kind = "reference"
-    if ref is None:
-        kind = "port"
-    data = []
-    for i, (name, N, K, _) in enumerate(SHAPES):
-        W = pyoracle.gen_codes(20261201 + 4 * i, N * K).reshape(N, K)
-        S = pyoracle.gen_scales(20261201 + 4 * i + 1, N * (K // 32)).view(np.float16).astype(np.float32)
-        x = pyoracle.gen_normal(20261201 + 4 * i + 2, K)
-        y = np.empty(N, np.float32)
-        data.append((N, K, W, S.reshape(N, K // 32), x, y))
+    return pyoracle
 
-    def run_step():
-        for (N, K, W, S, x, y) in data:
-            if ref is not None:
-                ref.ref_q8_gemv(W.ctypes.data_as(C.c_void_p), S.ctypes.data_as(C.c_void_p),
-                                x.ctypes.data_as(C.c_void_p), y.ctypes.data_as(C.c_void_p), C.c_int(N), C.c_int(K))
-            else:
-                y[:] = pyoracle.q8_gemv_a11(W, S, x)
 
-    nbytes = sum(N * K + N * (K // 32) * 4 + K * 4 + N * 4 for (N, K, *_r) in data)
-
-    def timed(sec):
-        run_step()
-        steps = 0
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < sec:
-            run_step()
-            steps += 1
-        return steps, (time.perf_counter() - t0) / steps
-
-    threads = int(ref.ref_max_threads()) if ref is not None else 1
-    steps, dt = timed(seconds)
-    one = None
-    if ref is not None and threads > 1:   # the same routine on one core, a shorter sample
-        ref.ref_set_threads(1)
-        s1, dt1 = timed(seconds / 2)
-        ref.ref_set_threads(threads)
-        one = {"value": round(nbytes / dt1 / 1e9, 2), "ms_per_step": round(dt1 * 1e3, 3), "passes": s1}
+def _host():
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -151,61 +161,195 @@ def cpu_baseline(seconds=10.0):
                 break
     except OSError:
         pass
-    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
-            "ms_per_step": round(dt * 1e3, 3), "one_core": one,
-            "host": f"{model}, nproc {os.cpu_count()}",
-            "sample": f"{steps} passes of the 5 layer+LM-head GEMV shapes through gemv_q8 "
-                      f"(q8_gemv_cpu.c:29-58, OpenMP over rows; fp32 x and fp32 scales, {nbytes / 1e6:.1f} MB/pass)"}
+    return f"{model}, nproc {os.cpu_count()}"
 
 
-def decode_bench(pq, n_steps=64, n_prompt=256):
-    """Backbone decode tok/s: the synthetic 24-layer LFM3-style model, a 256-token
-    prompt (chunked prefill), then n_steps T=1 greedy steps timed on the engine's stream."""
+def _timed(fn, sec):
+    """(passes, seconds per pass) of fn over about sec seconds, after one untimed pass."""
+    fn()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= sec:
+            return n, dt / n
+
+
+def _all_and_one_core(ref, fn, sec):
+    """fn timed on the OpenMP team (all cores), then on one core for half as long."""
+    threads = int(ref.ref_max_threads())
+    n_all, dt_all = _timed(fn, sec)
+    n_one, dt_one = None, None
+    if threads > 1:
+        ref.ref_set_threads(1)
+        try:
+            n_one, dt_one = _timed(fn, sec / 2)
+        finally:
+            ref.ref_set_threads(threads)
+    return threads, (n_all, dt_all), (n_one, dt_one)
+
+
+def cpu_q8_gemv(shapes, seconds):
+    """The reference's gemv_q8 (fp32 x, fp32 scales; q8_gemv_cpu.c:29-58, OpenMP
+    over rows) over the given (N, K) shapes: GB/s of its own bytes per pass, on
+    all host cores and on one."""
+    import ctypes as C
     import numpy as np
+    orc = _oracle()
+    ref = orc.ref()
+    if ref is None:
+        return None
+    data = []
+    for i, (N, K) in enumerate(shapes):
+        W = orc.gen_codes(20261201 + 4 * i, N * K).reshape(N, K)
+        S = orc.gen_scales(20261201 + 4 * i + 1, N * (K // 32)).view(np.float16).astype(np.float32)
+        x = orc.gen_normal(20261201 + 4 * i + 2, K)
+        data.append((N, K, W, S.reshape(N, K // 32), x, np.empty(N, np.float32)))
+
+    def run():
+        for (N, K, W, S, x, y) in data:
+            ref.ref_q8_gemv(W.ctypes.data_as(C.c_void_p), S.ctypes.data_as(C.c_void_p),
+                            x.ctypes.data_as(C.c_void_p), y.ctypes.data_as(C.c_void_p), C.c_int(N), C.c_int(K))
+
+    nbytes = sum(N * K + N * (K // 32) * 4 + K * 4 + N * 4 for (N, K) in shapes)
+    threads, (n, dt), (n1, dt1) = _all_and_one_core(ref, run, seconds)
+    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "ms_per_pass": round(dt * 1e3, 3),
+            "one_core": None if dt1 is None else {"value": round(nbytes / dt1 / 1e9, 2),
+                                                  "ms_per_pass": round(dt1 * 1e3, 3), "passes": n1},
+            "host": _host(),
+            "sample": f"{n} passes of {len(shapes)} GEMV shape(s) {['%dx%d' % s for s in shapes]} through gemv_q8 "
+                      f"(q8_gemv_cpu.c:29-58; fp32 x and fp32 scales, {nbytes / 1e6:.1f} MB/pass)"}
+
+
+def cpu_ternary(shapes, seconds):
+    """The reference's pq2_gemv_cpu (pq2_host.c:82-104) on the config-5 shapes:
+    row slices on an OpenMP team (ref_pq2_gemv_rows; rows are independent), and
+    the serial routine on one core."""
+    import ctypes as C
+    import numpy as np
+    orc = _oracle()
+    ref = orc.ref()
+    if ref is None:
+        return None
+    data = []
+    for i, (N, K) in enumerate(shapes):
+        codes = orc.gen_ternary(777 + i, N * K // 4)
+        S = orc.gen_scales(778 + i, N * K // 128)
+        xq = orc.q8k_quant(orc.gen_normal(779 + i, K))
+        data.append((N, K, codes, S, xq, np.empty(N, np.float32)))
+
+    def run():
+        for (N, K, c, s, xq, y) in data:
+            ref.ref_pq2_gemv_rows(C.c_int(N), C.c_int(K), c.ctypes.data_as(C.c_void_p), s.ctypes.data_as(C.c_void_p),
+                                  xq.ctypes.data_as(C.c_void_p), y.ctypes.data_as(C.c_void_p))
+
+    nbytes = sum(N * K // 4 + N * K // 128 * 2 + K // 256 * 292 + N * 4 for (N, K) in shapes)
+    threads, (n, dt), (n1, dt1) = _all_and_one_core(ref, run, seconds)
+    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "us_per_pass": round(dt * 1e6, 1),
+            "one_core": None if dt1 is None else {"value": round(nbytes / dt1 / 1e9, 2),
+                                                  "us_per_pass": round(dt1 * 1e6, 1), "passes": n1},
+            "host": _host(),
+            "sample": f"{n} passes of the gate, up and down GEMVs through pq2_gemv_cpu "
+                      f"({nbytes / 1e6:.1f} MB/pass)"}
+
+
+def cpu_backbone(cfg, n_prompt=8, n_steps=12):
+    """The oracle's 24-layer backbone (this build's C restatement, OpenMP over
+    GEMV rows): decode tok/s after a short prompt. A port, not the reference's
+    code: the reference's x86 LFM3 engine is a stub."""
+    import numpy as np
+    orc = _oracle()
+    m = orc.Model(**{k: v for k, v in cfg.items() if k != "prefill_chunk"})
+    r = m.feed(orc.gen_tokens(5, n_prompt, cfg["vocab"]))
+    t0 = time.perf_counter()
+    for _ in range(n_steps):
+        r = m.feed(np.array([r], np.int32))
+    dt = (time.perf_counter() - t0) / n_steps
+    m.close()
+    return {"value": round(1.0 / dt, 2), "unit": "tok/s", "cores": int(orc.lib().orc_max_threads()), "kind": "port",
+            "ms_per_token": round(dt * 1e3, 1), "host": _host(),
+            "sample": f"{n_steps} greedy T=1 steps of the oracle backbone after a {n_prompt}-token prompt"}
+
+
+# ------------------------------------------------------------------ GPU side
+def config1_bench(pq, torch, dev, g, stream, n=40):
+    """The single Q8_0 GEMV, 8192x2048, fp32 x quantized in the prologue, fp32 y."""
+    N, K = 8192, 2048
+    pool, per = q8_pool(pq, torch, dev, g, N, K)
+    x = torch.randn(K, device=dev, generator=g)
+    y = torch.empty(N, dtype=torch.float32, device=dev)
+
+    def launch(i):
+        pq.gemv_fused(pool[i % len(pool)], pq.PRO_F32, out_dtype=pq.DT_F32, out=y, xf=x)
+
+    mean, med = dispatch_ms(pq, torch, launch, n)
+    per_ms = period_ms(torch, launch, 60, stream)
+    nb = gemv_bytes(N, K, "f32")
+    ncopy = len(pool)
+    del pool
+    torch.cuda.empty_cache()
+    return {"gemv": f"{N}x{K}", "bytes": nb, "us": round(mean * 1e3, 2), "us_median": round(med * 1e3, 2),
+            "GB/s": round(nb / (mean * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "period_us": round(per_ms * 1e3, 2), "period_GB/s": round(nb / (per_ms * 1e-3) / 1e9, 1),
+            "weight_copies_rotated": ncopy, "rotated_MB": round(ncopy * per / 1e6, 1)}
+
+
+def decode_bench(pq, n_steps=64, n_prompt=256, reps=3):
+    """Backbone decode tok/s: the synthetic 24-layer LFM3-style model, a 256-token
+    prompt (chunked prefill), then n_steps T=1 greedy steps timed on the engine's
+    stream; the median over reps prompt + decode runs."""
     from pulsar_amd.engine import LFM3_SYNTH, Engine, synth_fill
     from pulsar_amd.hiptime import Event
     e = Engine(**LFM3_SYNTH)
     e.load_synthetic()
     prompt = synth_fill(5, LFM3_SYNTH["seed"] + 4 * 5000, n_prompt, float(LFM3_SYNTH["vocab"]))
     st = e.stream()
-    a, c = Event(), Event()
     e.reset()
     e.feed(prompt)                       # warm-up prefill and steps
     e.decode(4, want_ids=False)
     e.sync()
-    e.reset()
-    a.record(st)
-    e.feed(prompt)                       # the timed prefill (32-position chunks)
-    b2 = Event()
-    b2.record(st)
-    e.decode(n_steps, want_ids=False)
-    c.record(st)
-    e.sync()
-    prefill_ms = a.elapsed_ms(b2)
-    ms = b2.elapsed_ms(c) / n_steps
+    pre, dec = [], []
+    for _ in range(reps):
+        a, b, c = Event(), Event(), Event()
+        e.reset()
+        a.record(st)
+        e.feed(prompt)                   # the timed prefill (32-position chunks)
+        b.record(st)
+        e.decode(n_steps, want_ids=False)
+        c.record(st)
+        e.sync()
+        pre.append(a.elapsed_ms(b))
+        dec.append(b.elapsed_ms(c) / n_steps)
+    ms, prefill_ms = statistics.median(dec), statistics.median(pre)
     wbytes = e.weight_bytes()
     kv = 8 * 2 * 8 * 64 * 2  # attention layers x (k, v) x kv heads x dim x fp16, per position
     mean_pos = n_prompt + n_steps / 2
     tok_bytes = wbytes + kv * mean_pos
     e.close()
-    return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4), "steps": n_steps,
+    return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4), "steps": n_steps, "runs": reps,
             "positions": f"{n_prompt}..{n_prompt + n_steps}", "bytes_per_token": int(tok_bytes),
             "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "prefill_ms_256": round(prefill_ms, 2)}
+            "prefill_ms_256": round(prefill_ms, 2), "prefill_tok_s": round(n_prompt / (prefill_ms * 1e-3), 1)}
 
 
-def prefill_gemm_bench(pq, torch, dev, g, T=512, chunk=32, reps=3, rotate_mb=600):
-    """The layer's GEMMs and the LM head (config-2 weights) over T=512 positions
-    in 32-position chunks (int8 MFMA), each chunk reading a different copy of the
-    weights (>= 600 MB rotated) as a layer-by-layer prefill re-reads its weights
-    from HBM per chunk. Its roofline is HBM (weight bytes per chunk); the same
-    work as one T=512 launch per GEMM is reported against the int8 MFMA peak."""
-    from pulsar_amd.hiptime import Event
+def prefill_gemm_bench(pq, torch, dev, g, stream, gpu, T=512, chunk=32):
+    """Config 3: the layer's GEMMs and the LM head on fp32 activations over
+    T=512 positions in 32-position chunks. Each chunk quantizes its fp32 rows
+    (pq_q8_quant_f32, inside the timed region) and runs the five int8-MFMA
+    GEMMs on a different copy of the weights (>= 300 MB rotated), as a prefill
+    that streams its weights per chunk re-reads them from HBM. Reported against
+    HBM (weight bytes per chunk), the int8 MFMA peak, and the VALU ceiling of
+    the R1 epilogue (three VALU lane-ops per 32-MAC block product); the same
+    work as one T=512 launch per GEMM is reported beside it."""
     shapes = [(name, N, K) for (name, N, K, _) in SHAPES]
     per_set = sum(pq.lib().pq_q8_packed_codes_bytes(N, K) + pq.lib().pq_q8_packed_scales_bytes(N, K)
                   for (_, N, K) in shapes)
-    ncopy = max(2, -(-rotate_mb * 1000000 // per_set))
+    ncopy = copies_for(per_set)
     sets = []
     for _ in range(ncopy):
         ws = {}
@@ -215,41 +359,59 @@ def prefill_gemm_bench(pq, torch, dev, g, T=512, chunk=32, reps=3, rotate_mb=600
             ws[name] = pq.Q8Weight(codes, scales)
             del codes, scales
         sets.append(ws)
-    xs = {K: pq.q8_quant(torch.randn((T, K), device=dev, generator=g)) for K in (2048, 8192)}
+    xf = {K: torch.randn((T, K), device=dev, generator=g) for K in (2048, 8192)}
+    q = {K: (torch.empty((T, K), dtype=torch.int8, device=dev), torch.empty((T, K // 32), dtype=torch.float32,
+                                                                             device=dev)) for K in (2048, 8192)}
     outs = {name: torch.empty((T, N), dtype=torch.bfloat16, device=dev) for (name, N, K) in shapes}
     wsz = max(pq.lib().pq_q8_gemm_workspace_bytes(N, K, t) for (_, N, K) in shapes for t in (chunk, T))
     wsp = torch.empty(max(wsz, 16), dtype=torch.uint8, device=dev)
-    stream = pq.stream_ptr()
+
+    def quant(K, c0, c1):
+        qx, dx = q[K]
+        pq.check(pq.lib().pq_q8_quant_f32(xf[K][c0:c1].data_ptr(), qx[c0:c1].data_ptr(), dx[c0:c1].data_ptr(), K,
+                                          c1 - c0, pq.stream_ptr()), "pq_q8_quant_f32")
 
     def run():
         for ci, c0 in enumerate(range(0, T, chunk)):
             ws = sets[ci % ncopy]
+            for K in (2048, 8192):
+                quant(K, c0, c0 + chunk)
             for (name, N, K) in shapes:
-                qx, dx = xs[K]
+                qx, dx = q[K]
                 pq.q8_gemm(ws[name], qx[c0:c0 + chunk], dx[c0:c0 + chunk], out_dtype=pq.DT_BF16,
                            out=outs[name][c0:c0 + chunk], ws=wsp)
 
     def run_full(r):
         ws = sets[r % ncopy]
+        for K in (2048, 8192):
+            quant(K, 0, T)
         for (name, N, K) in shapes:
-            qx, dx = xs[K]
+            qx, dx = q[K]
             pq.q8_gemm(ws[name], qx, dx, out_dtype=pq.DT_BF16, out=outs[name], ws=wsp)
 
     g_run = graph_of(torch, run)
-    ms = timed_replay(torch, g_run, stream, reps)
+    ms = timed_replay(torch, g_run, stream)
     del g_run
     ops = sum(2 * N * K * T for (_, N, K) in shapes)
     wbytes = per_set * (T // chunk)
     g_full = graph_of(torch, lambda: [run_full(r) for r in range(ncopy)])
-    ms_full = timed_replay(torch, g_full, stream, reps) / ncopy
-    del g_full
+    ms_full = timed_replay(torch, g_full, stream) / ncopy
+    del g_full, sets
+    torch.cuda.empty_cache()
+    # VALU ceiling of the R1 fold: per (row, position, block) one convert, one
+    # multiply and one fma on 64 fp32 lanes per CU per clock
+    valu_tops = 64 * gpu["cus"] * gpu["clock_MHz"] * 1e6 * (64 / 3) / 1e12
+    tops, tops_full = ops / (ms * 1e-3) / 1e12, ops / (ms_full * 1e-3) / 1e12
     return {"T": T, "chunk": chunk, "gemms": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "ms": round(ms, 4),
-            "TOPS": round(ops / (ms * 1e-3) / 1e12, 2), "int8_peak_frac": round(ops / (ms * 1e-3) / 1e12 / 5000.0, 4),
+            "includes": "fp32 -> Q8_0 activation quantization of every chunk",
+            "TOPS": round(tops, 2), "int8_peak_frac": round(tops / INT8_PEAK_TOPS, 4),
+            "valu_ceiling_TOPS": round(valu_tops, 1), "valu_ceiling_frac": round(tops / valu_tops, 4),
             "weight_bytes_read": wbytes, "GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "ops": ops,
             "weight_copies_rotated": ncopy,
-            "single_launch_ms": round(ms_full, 4), "single_launch_TOPS": round(ops / (ms_full * 1e-3) / 1e12, 2),
-            "single_launch_int8_peak_frac": round(ops / (ms_full * 1e-3) / 1e12 / 5000.0, 4)}
+            "single_launch_ms": round(ms_full, 4), "single_launch_TOPS": round(tops_full, 2),
+            "single_launch_int8_peak_frac": round(tops_full / INT8_PEAK_TOPS, 4),
+            "single_launch_valu_ceiling_frac": round(tops_full / valu_tops, 4)}
 
 
 def prefill_profile_workload(pq, torch, dev, reps=3):
@@ -276,93 +438,102 @@ def prefill_profile_workload(pq, torch, dev, reps=3):
         torch.cuda.empty_cache()
 
 
-def ref_numerics_bench(pq, torch, dev, g, reps=20, rotate_mb=700):
+def _per_shape(pq, torch, stream, shapes, launch_of, nbytes_of, n=30):
+    """Per shape: mean dispatch duration and launch period over its rotated pool."""
+    per = {}
+    for s in shapes:
+        name = s[0]
+        mean, _ = dispatch_ms(pq, torch, launch_of(s), n)
+        prd = period_ms(torch, launch_of(s), n, stream)
+        nb = nbytes_of(s)
+        per[name] = {"us": round(mean * 1e3, 2), "period_us": round(prd * 1e3, 2),
+                     "GB/s": round(nb / (mean * 1e-3) / 1e9, 1)}
+    return per
+
+
+def ref_numerics_bench(pq, torch, dev, g, stream, reps=20):
     """The config-2 step through the reference-numerics GEMV (pq_q8r_gemv: the
-    reference's own order, bf16 x, fp32 weight scales, row-major codes),
-    weights rotated over > 256 MB. Bytes per step: codes + fp32 scales + the
-    bf16 x + y."""
-    set_bytes = sum(N * K + N * (K // 32) * 4 for (_, N, K, _) in SHAPES)
-    ncopy = max(2, math.ceil(rotate_mb * 1e6 / set_bytes))
-    copies = []
-    for _ in range(ncopy):
-        ws = {}
-        for (name, N, K, _) in SHAPES:
-            ws[name] = (torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g),
+    reference's own order, bf16 x, fp32 weight scales, row-major codes), each
+    shape from its own >= 300 MB pool. Bytes: codes + fp32 scales + bf16 x + y."""
+    pools = {}
+    for (name, N, K, _) in SHAPES:
+        pools[name] = [(torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g),
                         torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01)
-        copies.append(ws)
+                       for _ in range(copies_for(N * K + N * (K // 32) * 4))]
     xs = {K: torch.randn(K, device=dev, generator=g).to(torch.bfloat16) for K in (2048, 8192)}
     outs = {name: torch.empty(N, dtype=torch.float32 if o == "f32" else torch.bfloat16, device=dev)
             for (name, N, K, o) in SHAPES}
-    stream = pq.stream_ptr()
 
-    def gemv(ws, name, N, K, o):
-        c, sc = ws[name]
-        pq.q8r_gemv(c, sc, xs[K], out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name])
+    def launch_of(s):
+        name, N, K, o = s
+
+        def f(i):
+            c, sc = pools[name][i % len(pools[name])]
+            pq.q8r_gemv(c, sc, xs[K], out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name])
+        return f
 
     def step(i):
-        for (name, N, K, o) in SHAPES:
-            gemv(copies[i % ncopy], name, N, K, o)
+        for s in SHAPES:
+            launch_of(s)(i)
 
     gr = graph_of(torch, lambda: [step(i) for i in range(reps)])
-    ms = timed_replay(torch, gr, stream, 3) / reps
+    ms = timed_replay(torch, gr, stream) / reps
     del gr
-    per = {}
-    for (name, N, K, o) in SHAPES:
-        gsh = graph_of(torch, lambda: [gemv(copies[i % ncopy], name, N, K, o) for i in range(30)])
-        per[name] = round(timed_replay(torch, gsh, stream, 5) / 30 * 1e3, 2)
-        del gsh
-    nbytes = sum(N * K + N * (K // 32) * 4 + 2 * K + N * (4 if o == "f32" else 2) for (_, N, K, o) in SHAPES)
-    del copies
+    nb = {s[0]: s[1] * s[2] + s[1] * (s[2] // 32) * 4 + 2 * s[2] + s[1] * (4 if s[3] == "f32" else 2) for s in SHAPES}
+    per = _per_shape(pq, torch, stream, SHAPES, launch_of, lambda s: nb[s[0]])
+    nbytes = sum(nb.values())
+    kern = sum(p["us"] for p in per.values())
+    del pools
     torch.cuda.empty_cache()
     return {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "per_shape_us": per,
-            "weight_copies_rotated": ncopy}
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel_us": round(kern, 2), "kernel_hbm_frac": round(nbytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "per_shape": per, "rotated_MB_per_shape": ROTATE_MB}
 
 
-def qlow_bench(pq, torch, dev, g, rotate_mb=600):
+def qlow_bench(pq, torch, dev, g, stream, reps=20):
     """The four layer GEMVs of the config-2 workload (q|k|v, o_proj, gate+up,
-    down) in the reference's Q4 and Q5 formats (pq_qlow_gemv), weights
-    rotated. Bytes: packed codes + half2 scales + bf16 x + bf16 y."""
+    down) in the reference's Q4 and Q5 formats (pq_qlow_gemv), each shape from
+    its own >= 300 MB pool. Bytes: packed codes + half2 scales + bf16 x + bf16 y."""
     shapes = [s_ for s_ in SHAPES if s_[0] != "lm_head"]
-    stream = pq.stream_ptr()
     res = {}
     for bits in (4, 5):
-        set_bytes = sum(pq.lib().pq_qlow_packed_codes_bytes(N, K, bits) + pq.lib().pq_qlow_packed_scales_bytes(N, K, bits)
-                        for (_, N, K, _) in shapes)
-        ncopy = max(2, math.ceil(rotate_mb * 1e6 / set_bytes))
-        copies = []
-        for _ in range(ncopy):
-            ws = {}
-            for (name, N, K, _) in shapes:
-                q = torch.randint(0, 2 ** bits, (N, K), dtype=torch.uint8, device=dev, generator=g)
+        pools, wb = {}, {}
+        for (name, N, K, _) in shapes:
+            wb[name] = pq.lib().pq_qlow_packed_codes_bytes(N, K, bits) + pq.lib().pq_qlow_packed_scales_bytes(N, K, bits)
+            pool = []
+            for _ in range(copies_for(wb[name])):
+                qc = torch.randint(0, 2 ** bits, (N, K), dtype=torch.uint8, device=dev, generator=g)
                 sc = torch.randn((N, K // 32, 2), device=dev, generator=g).abs().mul(0.01).half().view(torch.int16)
-                ws[name] = pq.QlowWeight(q, sc, bits)
-                del q, sc
-            copies.append(ws)
+                pool.append(pq.QlowWeight(qc, sc, bits))
+                del qc, sc
+            pools[name] = pool
         xs = {K: torch.randn(K, device=dev, generator=g).to(torch.bfloat16) for K in (2048, 8192)}
         outs = {name: torch.empty(N, dtype=torch.bfloat16, device=dev) for (name, N, K, _) in shapes}
 
-        def step(i):
-            for (name, N, K, _) in shapes:
-                pq.qlow_gemv(copies[i % ncopy][name], xs[K], out=outs[name])
+        def launch_of(s):
+            name, N, K, _ = s
+            return lambda i: pq.qlow_gemv(pools[name][i % len(pools[name])], xs[K], out=outs[name])
 
-        reps = 20
+        def step(i):
+            for s in shapes:
+                launch_of(s)(i)
+
         gr = graph_of(torch, lambda: [step(i) for i in range(reps)])
-        ms = timed_replay(torch, gr, stream, 3) / reps
+        ms = timed_replay(torch, gr, stream) / reps
         del gr
-        per = {}
-        for (name, N, K, _) in shapes:
-            gsh = graph_of(torch, lambda: [pq.qlow_gemv(copies[i % ncopy][name], xs[K], out=outs[name])
-                                           for i in range(30)])
-            per[name] = round(timed_replay(torch, gsh, stream, 5) / 30 * 1e3, 2)
-            del gsh
-        del copies
+        nb = {s[0]: wb[s[0]] + 2 * s[2] + 2 * s[1] for s in shapes}
+        per = _per_shape(pq, torch, stream, shapes, launch_of, lambda s: nb[s[0]])
+        nbytes = sum(nb.values())
+        kern = sum(p["us"] for p in per.values())
+        del pools
         torch.cuda.empty_cache()
-        nbytes = set_bytes + sum(2 * K + 2 * N for (_, N, K, _) in shapes)
         res[f"q{bits}"] = {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
                            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                           "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "per_shape_us": per,
-                           "weight_copies_rotated": ncopy}
+                           "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "kernel_us": round(kern, 2),
+                           "kernel_hbm_frac": round(nbytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                           "per_shape": per, "rotated_MB_per_shape": ROTATE_MB}
     return res
 
 
@@ -372,40 +543,45 @@ def ternary_codes(torch, N, K, dev, g):
     return (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).contiguous()
 
 
-def ternary_bench(pq, torch, dev, g, reps=50, rotate_mb=400):
-    """PQ2_0 x Q8_K GEMVs of a Qwen3-8B-shaped FFN at T=1: gate and up 12288x4096,
-    down 4096x12288, weights rotated over > 256 MB."""
-    from pulsar_amd.hiptime import Event
+def ternary_bench(pq, torch, dev, g, stream, reps=20):
+    """Config 5: PQ2_0 x Q8_K GEMVs of a Qwen3-8B-shaped FFN at T=1 (gate and up
+    12288x4096, down 4096x12288), each shape from its own >= 300 MB pool."""
     shapes = [("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
-    per_set = sum(N * K // 4 + N * K // 128 * 2 for (_, N, K) in shapes)
-    ncopy = max(2, -(-rotate_mb * 1000000 // per_set))
-    sets = []
-    for _ in range(ncopy):
-        sets.append({name: (ternary_codes(torch, N, K, dev, g),
-                            (torch.randn((N, K // 128), device=dev, generator=g).abs() * 0.01).half()
-                            .view(torch.int16))
-                     for (name, N, K) in shapes})
+    pools = {}
+    for (name, N, K) in shapes:
+        pools[name] = [(ternary_codes(torch, N, K, dev, g),
+                        (torch.randn((N, K // 128), device=dev, generator=g).abs() * 0.01).half().view(torch.int16))
+                       for _ in range(copies_for(N * K // 4 + N * K // 128 * 2))]
     x4 = pq.q8k_quant(torch.randn(4096, device=dev, generator=g))
     x12 = pq.q8k_quant(torch.randn(12288, device=dev, generator=g))
     outs = {name: torch.empty(N, dtype=torch.float32, device=dev) for (name, N, K) in shapes}
-    stream = pq.stream_ptr()
 
-    def gemv(i, name, N, K):
-        ws = sets[i % ncopy]
-        pq.tq2_gemv(ws[name][0], ws[name][1], x12 if K == 12288 else x4, K, N, out=outs[name])
+    def launch_of(s):
+        name, N, K = s
 
-    # launch period per shape: back-to-back launches, weights rotating, HIP events on the launch stream
-    per = []
-    for (name, N, K) in shapes:
-        gsh = graph_of(torch, lambda: [gemv(i, name, N, K) for i in range(reps)])
-        per.append(timed_replay(torch, gsh, stream, 3) / reps)
-        del gsh
-    step_bytes = sum(N * K // 4 + N * K // 128 * 2 + K // 256 * 292 + N * 4 for (_, N, K) in shapes)
-    us = sum(per) * 1e3
-    return {"shapes": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "us_per_step": round(us, 2),
-            "bytes_per_step": step_bytes, "GB/s": round(step_bytes / (us * 1e-6) / 1e9, 1),
-            "hbm_frac": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "per_shape_us": [round(p * 1e3, 2) for p in per], "weight_copies_rotated": ncopy}
+        def f(i):
+            c, sc = pools[name][i % len(pools[name])]
+            pq.tq2_gemv(c, sc, x12 if K == 12288 else x4, K, N, out=outs[name])
+        return f
+
+    def step(i):
+        for s in shapes:
+            launch_of(s)(i)
+
+    gr = graph_of(torch, lambda: [step(i) for i in range(reps)])
+    ms = timed_replay(torch, gr, stream) / reps
+    del gr
+    nb = {n: N * K // 4 + N * K // 128 * 2 + K // 256 * 292 + N * 4 for (n, N, K) in shapes}
+    per = _per_shape(pq, torch, stream, shapes, launch_of, lambda s: nb[s[0]])
+    step_bytes = sum(nb.values())
+    kern = sum(p["us"] for p in per.values())
+    del pools
+    torch.cuda.empty_cache()
+    return {"shapes": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "us_per_step": round(ms * 1e3, 2),
+            "bytes_per_step": step_bytes, "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel_us": round(kern, 2), "kernel_hbm_frac": round(step_bytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "per_shape": per, "rotated_MB_per_shape": ROTATE_MB}
 
 
 def main():
@@ -417,7 +593,6 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode and prefill measurements")
     ap.add_argument("--calib", action="store_true",
                     help="also run a plain elementwise kernel over 256 MiB (counter calibration for rocprofv3 --pmc)")
-    ap.add_argument("--rotate-mb", type=int, default=600)
     ap.add_argument("--prefill-profile", action="store_true",
                     help="only run the prefill GEMMs (3 launches each at T=512 and T=32) for counter runs; no JSON")
     args = ap.parse_args()
@@ -436,35 +611,25 @@ def main():
     torch.manual_seed(20261201)
     g = torch.Generator(device=dev)
     g.manual_seed(20261201)
-    set_bytes = sum(pq.lib().pq_q8_packed_codes_bytes(N, K) + pq.lib().pq_q8_packed_scales_bytes(N, K)
-                    for (_, N, K, _) in SHAPES)
-    ncopy = max(2, math.ceil(args.rotate_mb * 1e6 / set_bytes))
-    copies = []
-    for c in range(ncopy):
-        ws = {}
-        for (name, N, K, _) in SHAPES:
-            codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
-            scales = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().view(torch.int16)
-            ws[name] = pq.Q8Weight(codes, scales)
-            del codes, scales
-        copies.append(ws)
+    pools, per_copy = {}, {}
+    for (name, N, K, _) in SHAPES:
+        pools[name], per_copy[name] = q8_pool(pq, torch, dev, g, N, K)
     x2 = torch.randn(2048, device=dev, generator=g)
     x8 = torch.randn(8192, device=dev, generator=g)
     outs = {name: torch.empty(N, dtype=torch.float32 if o == "f32" else torch.bfloat16, device=dev)
             for (name, N, K, o) in SHAPES}
     torch.cuda.synchronize()
-
-    from pulsar_amd.hiptime import Event
     stream = pq.stream_ptr()
 
-    def gemv(ws, name, N, K, o):
-        pq.gemv_fused(ws[name], pq.PRO_F32, out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name],
-                      xf=x8 if K == 8192 else x2)
+    def launch_of(s):
+        name, N, K, o = s
+        return lambda i: pq.gemv_fused(pools[name][i % len(pools[name])], pq.PRO_F32,
+                                       out_dtype=pq.DT_F32 if o == "f32" else pq.DT_BF16, out=outs[name],
+                                       xf=x8 if K == 8192 else x2)
 
     def step(i):
-        ws = copies[i % ncopy]
-        for (name, N, K, o) in SHAPES:
-            gemv(ws, name, N, K, o)
+        for s in SHAPES:
+            launch_of(s)(i)
 
     for i in range(args.warmup):
         step(i)
@@ -474,23 +639,14 @@ def main():
     ms_per_step = timed_replay(torch, g_steps, stream) / args.steps
     del g_steps
 
-    # launch period of the GEMV kernel per shape: back-to-back launches of that
-    # shape (weights rotating over the copies), HIP events on the launch stream
-    per = {}
-    nper = 30
-    for (name, N, K, o) in SHAPES:
-        gsh = graph_of(torch, lambda: [gemv(copies[i % ncopy], name, N, K, o) for i in range(nper)])
-        per[name] = timed_replay(torch, gsh, stream, reps=5) / nper
-        del gsh
-
+    # the GEMV kernel's launch duration per shape (dispatch events, rotating
+    # pool), and its back-to-back launch period
+    per = _per_shape(pq, torch, stream, SHAPES, launch_of, lambda s: gemv_bytes(*s[1:]), n=40)
     step_bytes = sum(gemv_bytes(N, K, o) for (_, N, K, o) in SHAPES)
-    gemv_ms = sum(per.values())
-    achieved = step_bytes / (gemv_ms * 1e-3) / 1e9
+    kern_ms = sum(p["us"] for p in per.values()) * 1e-3
+    achieved = step_bytes / (kern_ms * 1e-3) / 1e9
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    per_shape = {name: {"us": round(per[name] * 1e3, 2),
-                        "GB/s": round(gemv_bytes(N, K, o) / (per[name] * 1e-3) / 1e9, 1)}
-                 for (name, N, K, o) in SHAPES}
-    lm = [s_ for s_ in SHAPES if s_[0] == "lm_head"][0]
+    gpu = gpu_desc(torch, pq)
 
     line = {
         "metric": "Q8 GEMV HBM GB/s (% of peak); backbone decode tok/s on 1 MI355X",
@@ -503,19 +659,23 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8xint8->int32, fp32 scales",
-        "data": "synthetic (seeded uniform int8 codes, |N(0,1)|*0.01 fp16 scales, N(0,1) x)",
+        "dtype": "int8 x int8 -> int32 block dots; fp16 weight scales, fp32 activation scales, fp32 accumulate",
+        "data": "synthetic (seeded uniform int8 codes, |N(0,1)|*0.01 fp16 scales, N(0,1) fp32 x)",
         "config": {"workload": "one LFM-style layer's T=1 Q8_0 GEMVs + LM head (hidden 2048)",
-                   "gpu": gpu_desc(torch, pq),
+                   "gpu": gpu,
                    "gemvs": [f"{n}:{N}x{K}" for (n, N, K, _) in SHAPES],
-                   "bytes_per_step": step_bytes, "weight_copies_rotated": ncopy,
-                   "rotated_MB": round(ncopy * set_bytes / 1e6, 1)},
+                   "bytes_per_step": step_bytes, "timed": f"{args.steps} steps in one graph, median of 5 replays",
+                   "weight_copies_rotated": {n: len(p) for n, p in pools.items()},
+                   "rotated_MB_per_shape": {n: round(len(pools[n]) * per_copy[n] / 1e6, 1) for n in pools}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "q8_gemv_fused_kernel (5 shapes, launch period)", "per_shape": per_shape,
-                     "lm_head_frac": round(gemv_bytes(*lm[1:]) / (per["lm_head"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(),
+                     "kernel": "q8_gemv_fused_kernel (5 shapes, mean dispatch duration)",
+                     "kernel_us_per_step": round(kern_ms * 1e3, 2), "per_shape": per,
+                     "lm_head_frac": round(per["lm_head"]["GB/s"] / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": None,
     }
+    del pools
+    torch.cuda.empty_cache()
     if args.calib:
         src = torch.randn(64 << 20, device=dev)          # 256 MiB read + 256 MiB written per call
         dst = torch.empty_like(src)
@@ -524,13 +684,19 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if not args.no_extra:
-        del copies
-        torch.cuda.empty_cache()
+        line["config1_gemv"] = config1_bench(pq, torch, dev, g, stream)
         line["decode"] = decode_bench(pq)
-        line["prefill_gemm"] = prefill_gemm_bench(pq, torch, dev, g)
-        line["ternary_gemv"] = ternary_bench(pq, torch, dev, g)
-        line["ref_numerics_gemv"] = ref_numerics_bench(pq, torch, dev, g)
-        line["qlow_gemv"] = qlow_bench(pq, torch, dev, g)
+        line["prefill_gemm"] = prefill_gemm_bench(pq, torch, dev, g, stream, gpu)
+        line["ternary_gemv"] = ternary_bench(pq, torch, dev, g, stream)
+        line["ref_numerics_gemv"] = ref_numerics_bench(pq, torch, dev, g, stream)
+        line["qlow_gemv"] = qlow_bench(pq, torch, dev, g, stream)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_q8_gemv([(N, K) for (_, N, K, _) in SHAPES], 10.0)
+        if not args.no_extra:
+            from pulsar_amd.engine import LFM3_SYNTH
+            line["config1_gemv"]["cpu"] = cpu_q8_gemv([(8192, 2048)], 3.0)
+            line["ternary_gemv"]["cpu"] = cpu_ternary([(12288, 4096), (12288, 4096), (4096, 12288)], 4.0)
+            line["decode"]["cpu"] = cpu_backbone(LFM3_SYNTH)
     print(json.dumps(line))
 
 

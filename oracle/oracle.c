@@ -17,6 +17,9 @@
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
+
+/* The OpenMP team size the oracle's parallel loops use (reported beside the CPU baseline). */
+int orc_max_threads(void) { return omp_get_max_threads(); }
 #endif
 
 /* ===================================================================== scalars */

@@ -73,6 +73,7 @@ void orc_tq2_gemv(const uint8_t *codes, const uint16_t *S, const uint8_t *xq, fl
 float orc_pairwise(const float *v, int n);
 void orc_rmsnorm(const uint16_t *x, const float *w, uint16_t *y, int n, float eps);
 void orc_headnorm(uint16_t *x, const float *w, int nheads, int hd, float eps);
+int orc_max_threads(void);
 void orc_rope_invf(float *invf, int hd, int rot, float theta);
 void orc_rope_table(float *cs, int maxpos, int hd, int rot, float theta);
 void orc_rope(uint16_t *x, const float *cs, int pos, int nheads, int hd, int rot);

@@ -24,3 +24,20 @@ void ref_q8_gemv(const signed char *q, const float *s, const float *x, float *y,
 }
 
 void ref_q8_quant(const float *w, int K, signed char *q, float *s) { quant_row(w, K, q, s); }
+
+/* The reference's pq2_gemv_cpu (pulsar_arm/bonsai2/pq2_host.c:82-104) is
+ * serial; rows are independent, so the CPU baseline runs it on row slices in
+ * an OpenMP team (same outputs, row for row). */
+#include <stdint.h>
+void pq2_gemv_cpu(int rows, int K, const uint8_t *w_codes, const uint16_t *w_scales_h, const uint8_t *xq, float *y);
+
+void ref_pq2_gemv_rows(int rows, int K, const uint8_t *w_codes, const uint16_t *w_scales_h, const uint8_t *xq,
+                       float *y) {
+  const int nb = omp_get_max_threads() * 4;
+#pragma omp parallel for schedule(static)
+  for (int b = 0; b < nb; b++) {
+    const long r0 = (long)rows * b / nb, r1 = (long)rows * (b + 1) / nb;
+    if (r1 > r0)
+      pq2_gemv_cpu((int)(r1 - r0), K, w_codes + r0 * (K / 4), w_scales_h + r0 * (K / 128), xq, y + r0);
+  }
+}

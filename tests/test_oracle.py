@@ -247,6 +247,11 @@ def test_tq2_is_reference_code(orc, N, K):
     ref.pq2_gemv_cpu(C.c_int(N), C.c_int(K), codes.ctypes.data_as(C.c_void_p), S.ctypes.data_as(C.c_void_p),
                      xq.ctypes.data_as(C.c_void_p), yr.ctypes.data_as(C.c_void_p))
     assert np.array_equal(f32bits(y), f32bits(yr))
+    # the row-sliced OpenMP wrapper the CPU baseline times gives the same rows
+    ys = np.full(N, np.nan, np.float32)
+    ref.ref_pq2_gemv_rows(C.c_int(N), C.c_int(K), codes.ctypes.data_as(C.c_void_p), S.ctypes.data_as(C.c_void_p),
+                          xq.ctypes.data_as(C.c_void_p), ys.ctypes.data_as(C.c_void_p))
+    assert np.array_equal(f32bits(ys), f32bits(yr))
 
 
 def test_tq2_exact_int(orc):
