@@ -300,8 +300,9 @@ def config1_bench(pq, torch, dev, g, stream, n=40):
 
 def decode_bench(pq, n_steps=64, n_prompt=256, reps=3):
     """Backbone decode tok/s: the synthetic 24-layer LFM3-style model, a 256-token
-    prompt (chunked prefill), then n_steps T=1 greedy steps timed on the engine's
-    stream; the median over reps prompt + decode runs."""
+    prompt (layer-major prefill), then n_steps T=1 greedy steps timed on the
+    engine's stream; the median over reps prompt + decode runs. The prompt is
+    also timed in the reference's 32-position chunks."""
     from pulsar_amd.engine import LFM3_SYNTH, Engine, synth_fill
     from pulsar_amd.hiptime import Event
     e = Engine(**LFM3_SYNTH)
@@ -317,7 +318,7 @@ def decode_bench(pq, n_steps=64, n_prompt=256, reps=3):
         a, b, c = Event(), Event(), Event()
         e.reset()
         a.record(st)
-        e.feed(prompt)                   # the timed prefill (32-position chunks)
+        e.feed(prompt)                   # the timed prefill (one 256-position chunk per layer)
         b.record(st)
         e.decode(n_steps, want_ids=False)
         c.record(st)
@@ -325,6 +326,17 @@ def decode_bench(pq, n_steps=64, n_prompt=256, reps=3):
         pre.append(a.elapsed_ms(b))
         dec.append(b.elapsed_ms(c) / n_steps)
     ms, prefill_ms = statistics.median(dec), statistics.median(pre)
+    e.set_chunk(32)                      # the reference's 32-position chunks, layer-major
+    pre32 = []
+    for _ in range(reps):
+        a, b = Event(), Event()
+        e.reset()
+        a.record(st)
+        e.feed(prompt)
+        b.record(st)
+        e.sync()
+        pre32.append(a.elapsed_ms(b))
+    prefill32_ms = statistics.median(pre32)
     wbytes = e.weight_bytes()
     kv = 8 * 2 * 8 * 64 * 2  # attention layers x (k, v) x kv heads x dim x fp16, per position
     mean_pos = n_prompt + n_steps / 2
@@ -334,7 +346,9 @@ def decode_bench(pq, n_steps=64, n_prompt=256, reps=3):
             "positions": f"{n_prompt}..{n_prompt + n_steps}", "bytes_per_token": int(tok_bytes),
             "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "prefill_ms_256": round(prefill_ms, 2), "prefill_tok_s": round(n_prompt / (prefill_ms * 1e-3), 1)}
+            "prefill_ms_256": round(prefill_ms, 2), "prefill_tok_s": round(n_prompt / (prefill_ms * 1e-3), 1),
+            "prefill_chunk": LFM3_SYNTH["prefill_chunk"], "prefill_order": "layer-major",
+            "prefill_ms_256_chunk32": round(prefill32_ms, 2)}
 
 
 def prefill_gemm_bench(pq, torch, dev, g, stream, gpu, T=512, chunk=32):

@@ -270,6 +270,11 @@ int pq_argmax(const float *v, int n, int32_t *out, void *stream);
  * k_dequant_row (138-142). */
 int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *tokens, uint16_t *out,
              int H, int vocab, int T, void *stream);
+/* The same from the table as an .lfm3q8 file stores it: row-major codes
+ * [vocab][H] and one fp32 scale per 32 ([vocab][H/32]). Replaces k_dequant_row
+ * (138-142) on the blob's tensor, as the reference runs it. */
+int pq_embed_rows(const int8_t *codes, const float *scales, const int32_t *tokens, uint16_t *out, int H,
+                  int vocab, int T, void *stream);
 
 
 /* ================================================== fused decode kernels
@@ -373,9 +378,10 @@ int pq_synth_fill(int kind, uint64_t seed, void *out_host, size_t n, float a, fl
 
 /* ================================================================ engine
  * The backbone on one GPU: weights resident in HBM (packed Q8_0), fp16 KV
- * cache, conv rings, a prefill path in chunks of prefill_chunk positions (the
- * batched MFMA GEMM) and a T=1 decode path (the GEMV), all on the engine's own
- * stream. Layer kinds come from attn_mask (bit L set = attention layer).
+ * cache, conv rings, a prefill path that runs the prompt layer by layer in
+ * chunks of up to prefill_chunk positions (the batched MFMA GEMM; the
+ * reference's layer-major order, lfm3_nanode.cu:5935-5955) and a T=1 decode
+ * path (the GEMV), all on the engine's own stream. Layer kinds come from attn_mask (bit L set = attention layer).
  * Host pointers: tokens, ids, logits, tensors passed to pq_engine_set_*.
  * The call sequence restates lfm3_nanode.cu main()/layer_body (3739-3856,
  * 5828-6340) with the reference's host contract: arenas allocated once at
@@ -388,7 +394,21 @@ typedef struct pq_model_cfg {
   uint64_t seed;             /* synthetic weights                              */
   uint32_t attn_mask;
   int prefill_chunk;         /* positions per prefill launch (32)               */
+  int numerics;              /* PQ_NUMERICS_Q8 or PQ_NUMERICS_REF               */
+  uint32_t slide_mask;       /* bit L set = sliding-window attention layer     */
+  int slide_win;             /* keys a sliding layer sees (the last slide_win)  */
+  int slide_rot;             /* rotated dims of a sliding layer                 */
+  float slide_theta;         /* RoPE base of a sliding layer                    */
 } pq_model_cfg;
+/* numerics: PQ_NUMERICS_Q8 runs the Q8_0 x Q8_0 GEMVs (activations quantized
+ * per 32-block, fp16 weight scales, the packed tile layout, int8 MFMA for
+ * prefill, the fused decode kernels); PQ_NUMERICS_REF keeps the .lfm3q8
+ * tensors as stored (row-major codes, fp32 scales) and runs every GEMV through
+ * pq_q8r_gemv on bf16 activations -- the reference's own GEMV order
+ * (gemv / gemv_f, lfm3_nanode.cu:1916-1966, 3634-3663) -- with unfused T=1
+ * steps. */
+#define PQ_NUMERICS_Q8 0
+#define PQ_NUMERICS_REF 1
 
 void *pq_engine_create(const pq_model_cfg *cfg);             /* NULL on failure */
 int pq_engine_destroy(void *engine);
@@ -398,16 +418,22 @@ int pq_engine_load_synthetic(void *engine);
  * slot 0 = tied embedding); fp32 slots 4..7 norms, 8/9 q/k norm, 10 conv taps
  * (layer -1 slot 1 = final norm). Call pq_engine_mark_loaded when done. */
 int pq_engine_set_q8(void *engine, int layer, int slot, const int8_t *codes, const uint16_t *scales);
+/* The same with fp32 scales (the .lfm3q8 form). Under PQ_NUMERICS_Q8 every
+ * scale must be an fp16 value: otherwise PQ_ERR_DATA, with the count of those
+ * that are not (and of those below fp16's normal range) in pq_last_error. */
+int pq_engine_set_q8_f32(void *engine, int layer, int slot, const int8_t *codes, const float *scales);
 int pq_engine_set_f32(void *engine, int layer, int slot, const float *v, size_t n);
 int pq_engine_mark_loaded(void *engine);
 /* Every backbone tensor from an .lfm3q8 blob (the reference's load_blob,
  * lfm3_nanode.cu:1404-1733, on the names layer_body reads, 3739-3856): each
  * payload's crc32 is checked (PQ_ERR_DATA on a mismatch) on a reader thread
  * that stays ahead of the uploads; q/k/v/gate_proj stack into the attention
- * input GEMV, feed_forward.w1 / w3 into gate/up; fp32 weight scales are
- * rounded to the engine's fp16 scales (exact for blobs written from fp16
- * scales); the tied embedding must be Q8 (dtype 1). Shapes must match the
- * engine's configuration; sliding-window attention layers are refused.
+ * input GEMV, feed_forward.w1 / w3 into gate/up. The fp32 weight scales are
+ * kept under PQ_NUMERICS_REF; under PQ_NUMERICS_Q8 they must be fp16 values
+ * (a blob written from fp16 scales), else PQ_ERR_DATA naming the tensor and
+ * counting the scales fp16 cannot hold -- nothing is rounded silently. The
+ * tied embedding must be Q8 (dtype 1). Shapes must match the engine's
+ * configuration; sliding-window attention layers are refused.
  * Marks the engine loaded on success. */
 int pq_engine_load_blob(void *engine, const char *path);
 int pq_engine_reset(void *engine);
@@ -424,6 +450,11 @@ int pq_engine_decode(void *engine, int n_steps, int32_t *ids);
  * taps, GQA group 1/2/4, the context's splits in LDS); set_fused(1) on another
  * configuration returns PQ_ERR_ARG. */
 int pq_engine_set_fused(void *engine, int on);
+/* Positions per prefill chunk from now on: 1 .. the configuration's
+ * prefill_chunk (the arenas' size). Any chunk size gives the same bits; the
+ * prompt runs layer by layer over its chunks, so larger chunks read each
+ * layer's weights fewer times. */
+int pq_engine_set_chunk(void *engine, int n);
 /* Fused decode steps replay a captured HIP graph (1, the default; the position
  * and the id slot live on the device) or launch kernel by kernel (0); both give
  * the same bits. */

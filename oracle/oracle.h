@@ -99,6 +99,12 @@ typedef struct orc_cfg {
   float eps, theta;
   uint64_t seed;
   uint32_t attn_mask;        /* bit L set -> layer L is attention, else conv  */
+  int numerics;              /* 0: Q8_0 x Q8_0 (R1); 1: the reference's GEMV
+                                order (R2: bf16 x, fp32 scales)               */
+  uint32_t slide_mask;       /* bit L set -> layer L is sliding-window attention */
+  int slide_win;             /* keys a sliding layer sees (the last slide_win)  */
+  int slide_rot;             /* rotated dims of a sliding layer                */
+  float slide_theta;         /* RoPE base of a sliding layer                   */
 } orc_cfg;
 
 typedef struct orc_model orc_model;

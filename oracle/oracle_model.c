@@ -2,7 +2,9 @@
  *
  * The layer sequence restates layer_body (lfm3_nanode.cu:3739-3856) with the
  * hot-path numerics of oracle.c: Q8_0 x Q8_0 GEMVs (activations quantized per
- * 32-block), fp16 KV cache with split-K flash decode, table RoPE, one expf.
+ * 32-block; or, with numerics = 1, the reference's own GEMV order on bf16 x
+ * and fp32 scales, orc_q8r_gemm), fp16 KV cache with split-K flash decode,
+ * table RoPE, one expf.
  *   operator_norm -> {attention | gated conv} -> post_operator_norm -> +residual
  *   ffn_norm -> gate/up GEMV -> silu(gate)*up -> down GEMV -> post_ffn_norm -> +residual
  * Attention: fused [q | k | v | gate] GEMV (gate = one value per q head), per-head
@@ -31,7 +33,8 @@
 
 typedef struct {
   int8_t *w;
-  uint16_t *s;
+  uint16_t *s;   /* fp16 scales (the R1 GEMV)                          */
+  float *sf;     /* the same scales widened to fp32 (the R2 GEMV)      */
   int N, K;
 } q8t;
 
@@ -61,6 +64,8 @@ static void q8_make(q8t *q, const orc_cfg *c, int t, int N, int K) {
   q->s = (uint16_t *)malloc((size_t)N * (K / ORC_QBLK) * 2);
   orc_gen_codes(tseed(c, t, 0), q->w, (size_t)N * K);
   orc_gen_scales(tseed(c, t, 1), q->s, (size_t)N * (K / ORC_QBLK), 0.01f);
+  q->sf = (float *)malloc(sizeof(float) * (size_t)N * (K / ORC_QBLK));
+  for (size_t i = 0; i < (size_t)N * (K / ORC_QBLK); i++) q->sf[i] = orc_h2f(q->s[i]);
 }
 
 static float *vec_make(const orc_cfg *c, int t, int n, float a, float b) {
@@ -122,7 +127,7 @@ void orc_model_reset(orc_model *m) {
   m->pos = 0;
 }
 
-static void q8_free(q8t *q) { free(q->w); free(q->s); }
+static void q8_free(q8t *q) { free(q->w); free(q->s); free(q->sf); }
 
 void orc_model_free(orc_model *m) {
   if (!m) return;
@@ -176,14 +181,25 @@ int orc_model_debug_hidden(orc_model *m, uint16_t *out) {
   return 0;
 }
 
-/* y_bf16[T][N] = bf16(R1 GEMM of x_bf16[T][K]) -- quantize each position's
- * row to Q8_0, run the R1 GEMM, round each output (k_combine_bf, 336-343). */
+/* y_f32[T][N] = W . x_bf16[T][K] in the model's GEMV numerics: R1 quantizes
+ * each position's row to Q8_0 and runs the R1 GEMM; R2 runs the reference's
+ * own order on bf16 x and fp32 scales (orc_q8r_gemm). */
+static int g_numerics;   /* set per feed from the model's configuration */
+static void gemm_f32(const q8t *W, const uint16_t *x, float *y, int T, int8_t *qx, float *dx) {
+  const int K = W->K, N = W->N, nb = K / ORC_QBLK;
+  if (g_numerics == 1) {
+    orc_q8r_gemm(W->w, W->sf, x, y, N, K, T);
+    return;
+  }
+  for (int t = 0; t < T; t++) orc_q8_quant_bf16(x + (size_t)t * K, K, qx + (size_t)t * K, dx + (size_t)t * nb);
+  orc_q8_gemm(W->w, W->s, qx, dx, y, N, K, T);
+}
+
+/* y_bf16[T][N] = bf16 of the GEMM above (k_combine_bf, 336-343). */
 static void gemm_bf16(const q8t *W, const uint16_t *x, uint16_t *y, int T, float *scratch_f,
                       int8_t *qx, float *dx) {
-  const int K = W->K, N = W->N, nb = K / ORC_QBLK;
-  for (int t = 0; t < T; t++) orc_q8_quant_bf16(x + (size_t)t * K, K, qx + (size_t)t * K, dx + (size_t)t * nb);
-  orc_q8_gemm(W->w, W->s, qx, dx, scratch_f, N, K, T);
-  for (size_t i = 0; i < (size_t)T * N; i++) y[i] = orc_f2bf(scratch_f[i]);
+  gemm_f32(W, x, scratch_f, T, qx, dx);
+  for (size_t i = 0; i < (size_t)T * W->N; i++) y[i] = orc_f2bf(scratch_f[i]);
 }
 
 int orc_model_feed(orc_model *m, const int32_t *tok, int T, float *logits_out) {
@@ -195,6 +211,7 @@ int orc_model_feed(orc_model *m, const int32_t *tok, int T, float *logits_out) {
   int kmax = F > H ? F : H;
   if (qd > kmax) kmax = qd;
   if (m->pos + T > c->ctx) return -1;
+  g_numerics = c->numerics;
   uint16_t *X = (uint16_t *)malloc((size_t)T * H * 2);
   uint16_t *H1 = (uint16_t *)malloc((size_t)T * kmax * 2);
   uint16_t *H2 = (uint16_t *)malloc((size_t)T * kmax * 2);
@@ -251,8 +268,7 @@ int orc_model_feed(orc_model *m, const int32_t *tok, int T, float *logits_out) {
   const uint16_t *xl = X + (size_t)(T - 1) * H;
   memcpy(m->last_hidden, xl, (size_t)H * 2);
   orc_rmsnorm(xl, m->final_norm, H1, H, c->eps);
-  orc_q8_quant_bf16(H1, H, qx, dx);
-  orc_q8_gemv(m->emb.w, m->emb.s, qx, dx, yf, c->vocab, H);
+  gemm_f32(&m->emb, H1, yf, 1, qx, dx);
   const int id = orc_argmax(yf, c->vocab);
   if (logits_out) memcpy(logits_out, yf, sizeof(float) * (size_t)c->vocab);
   m->pos += T;

@@ -331,7 +331,9 @@ class Cfg(C.Structure):
     _fields_ = [("hidden", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("nlayers", C.c_int),
                 ("nh", C.c_int), ("nkv", C.c_int), ("hd", C.c_int), ("rot", C.c_int),
                 ("ntaps", C.c_int), ("ctx", C.c_int), ("eps", C.c_float), ("theta", C.c_float),
-                ("seed", C.c_uint64), ("attn_mask", C.c_uint32)]
+                ("seed", C.c_uint64), ("attn_mask", C.c_uint32), ("numerics", C.c_int),
+                ("slide_mask", C.c_uint32), ("slide_win", C.c_int), ("slide_rot", C.c_int),
+                ("slide_theta", C.c_float)]
 
 
 class Model:

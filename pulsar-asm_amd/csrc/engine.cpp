@@ -30,11 +30,15 @@
 
 namespace pq {
 
+// A Q8 weight on the device. PQ_NUMERICS_Q8: packed tiles (pc) and fp16
+// scales (ps). PQ_NUMERICS_REF: row-major codes (pc) and fp32 scales (sf), as
+// the .lfm3q8 file stores them.
 struct Q8Dev {
   int8_t *pc = nullptr;
   uint16_t *ps = nullptr;
+  float *sf = nullptr;
   int N = 0, K = 0;
-  bool gate_up = false;  // packed by pq_q8_pack_gate_up (rows interleaved in groups of 32)
+  bool gate_up = false;  // Q8: packed by pq_q8_pack_gate_up (rows interleaved in groups of 32)
 };
 
 struct LayerDev {
@@ -65,11 +69,14 @@ struct Engine {
   const uint16_t *step_resid = nullptr;  // where a replayed decode step leaves the residual
   float *parts = nullptr;
   int nparts = 0;
-  // activations, sized for tmax positions
+  // activations: the residual stream X, the layer input qin/din (Q8_0) and
+  // the prompt's token ids tokd hold every position of the context; the rest
+  // is sized for one chunk of tmax positions
   uint16_t *X = nullptr, *Hb = nullptr, *Wd = nullptr, *A = nullptr;
-  int8_t *qx = nullptr;
-  float *dx = nullptr, *logits = nullptr;
-  int32_t *tok = nullptr, *ids = nullptr;
+  int8_t *qx = nullptr, *qin = nullptr;
+  uint16_t *xin = nullptr;        // PQ_NUMERICS_REF: the bf16 layer input of every position
+  float *dx = nullptr, *din = nullptr, *logits = nullptr;
+  int32_t *tok = nullptr, *tokd = nullptr, *ids = nullptr;
   int max_ids = 0;
   void *attn_ws = nullptr;
   size_t attn_ws_bytes = 0;
@@ -104,9 +111,16 @@ struct Engine {
     if (_rc != PQ_OK) return _rc; \
   } while (0)
 
+static bool ref_numerics(const Engine &E) { return E.c.numerics == PQ_NUMERICS_REF; }
+
 static int alloc_q8(Engine &E, Q8Dev &q, int N, int K) {
   q.N = N;
   q.K = K;
+  if (ref_numerics(E)) {
+    PQ_TRY(E.dalloc(&q.pc, (size_t)N * K));
+    PQ_TRY(E.dalloc(&q.sf, (size_t)N * (K / 32)));
+    return PQ_OK;
+  }
   PQ_TRY(E.dalloc(&q.pc, pq_q8_packed_codes_bytes(N, K)));
   PQ_TRY(E.dalloc(&q.ps, pq_q8_packed_scales_bytes(N, K) / 2));
   return PQ_OK;
@@ -153,7 +167,12 @@ static int create(Engine &E, const pq_model_cfg &c) {
   const int T = E.tmax;
   const int wide = std::max(std::max(3 * H, 2 * F), E.nin);
   const int kmax = std::max(std::max(H, F), E.qd);
-  PQ_TRY(E.dalloc(&E.X, (size_t)T * H));
+  const size_t npos = (size_t)std::max(c.ctx, T);
+  PQ_TRY(E.dalloc(&E.X, npos * H));
+  PQ_TRY(E.dalloc(&E.qin, npos * H));
+  PQ_TRY(E.dalloc(&E.din, npos * (H / 32)));
+  PQ_TRY(E.dalloc(&E.tokd, npos));
+  if (ref_numerics(E)) PQ_TRY(E.dalloc(&E.xin, npos * H));
   PQ_TRY(E.dalloc(&E.Xd[0], (size_t)H));
   PQ_TRY(E.dalloc(&E.Xd[1], (size_t)H));
   E.nparts = pq_q8_gemv_parts(c.vocab, H);
@@ -178,10 +197,91 @@ static int create(Engine &E, const pq_model_cfg &c) {
 }
 
 // ------------------------------------------------------------ weight upload
-static int upload_q8(Engine &E, Q8Dev &q, const int8_t *codes, const uint16_t *scales) {
+static float host_h2f(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t u;
+  if (e == 0x1f) u = sign | 0x7f800000u | (m << 13);
+  else if (e) u = sign | ((e + 112u) << 23) | (m << 13);
+  else if (m == 0) u = sign;
+  else {   // subnormal: normalize
+    int ex = -1;
+    uint32_t mm = m;
+    do { mm <<= 1; ex++; } while (!(mm & 0x400u));
+    u = sign | ((uint32_t)(112 - ex) << 23) | ((mm & 0x3ffu) << 13);
+  }
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// fp32 -> binary16 bits, round to nearest even (overflow to inf, NaN kept).
+static uint16_t host_f2h(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u, e = (u >> 23) & 0xffu, m = u & 0x7fffffu;
+  if (e == 0xff) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u | (m >> 13) : 0u));
+  const int ex = (int)e - 127 + 15;
+  if (ex >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (ex <= 0) {   // binary16 subnormal (or zero): shift the full mantissa, round to even
+    if (ex < -10) return (uint16_t)sign;
+    const uint32_t mm = m | 0x800000u;
+    const int sh = 14 - ex;
+    uint32_t q = mm >> sh;
+    const uint32_t rem = mm & ((1u << sh) - 1), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (q & 1))) q++;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t q = ((uint32_t)ex << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;   // a carry into the exponent is still right
+  return (uint16_t)(sign | q);
+}
+
+// One Q8 weight, row-major codes [N][K] with scales [N][K/32] given either as
+// fp16 bits (s16) or as fp32 (s32), onto the device in the engine's format:
+// Q8 numerics pack it (fp32 scales must be fp16 values: the GEMV's scales
+// are fp16, and a scale fp16 cannot hold is refused with a count instead of
+// being rounded); reference numerics keep the codes as they are and the
+// scales as fp32 (fp16 widens exactly).
+static int upload_q8(Engine &E, Q8Dev &q, const int8_t *codes, const uint16_t *s16, const float *s32) {
+  const size_t nc = (size_t)q.N * q.K, ns = (size_t)q.N * (q.K / 32);
+  if (ref_numerics(E)) {
+    std::vector<float> wide;
+    if (s16) {
+      wide.resize(ns);
+      for (size_t i = 0; i < ns; i++) wide[i] = host_h2f(s16[i]);
+      s32 = wide.data();
+    }
+    if (hipMemcpyAsync(q.pc, codes, nc, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+        hipMemcpyAsync(q.sf, s32, ns * 4, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+        hipStreamSynchronize(E.st) != hipSuccess)
+      return fail(PQ_ERR_LAUNCH, "weight upload failed");
+    return PQ_OK;
+  }
+  std::vector<uint16_t> narrow;
+  if (!s16) {
+    narrow.resize(ns);
+    size_t inexact = 0, tiny = 0;
+    for (size_t i = 0; i < ns; i++) {
+      narrow[i] = host_f2h(s32[i]);
+      uint32_t a, b;
+      const float back = host_h2f(narrow[i]);
+      memcpy(&a, &s32[i], 4);
+      memcpy(&b, &back, 4);
+      if (a != b) {
+        inexact++;
+        if (fabsf(s32[i]) < 6.103515625e-05f) tiny++;   // below the fp16 normal range
+      }
+    }
+    if (inexact)
+      return fail(PQ_ERR_DATA,
+                  "%zu of %zu fp32 weight scales of a [%d x %d] tensor are not fp16 values (%zu below the fp16 "
+                  "normal range); the Q8 numerics would round them -- use PQ_NUMERICS_REF, which keeps fp32 scales",
+                  inexact, ns, q.N, q.K, tiny);
+    s16 = narrow.data();
+  }
   int8_t *dc = nullptr;
   uint16_t *ds = nullptr;
-  const size_t nc = (size_t)q.N * q.K, ns = (size_t)q.N * (q.K / 32);
   if (hipMalloc(&dc, nc) != hipSuccess) return fail(PQ_ERR_LAUNCH, "hipMalloc staging failed");
   if (hipMalloc(&ds, ns * 2) != hipSuccess) {
     hipFree(dc);
@@ -189,7 +289,7 @@ static int upload_q8(Engine &E, Q8Dev &q, const int8_t *codes, const uint16_t *s
   }
   int rc = PQ_OK;
   if (hipMemcpyAsync(dc, codes, nc, hipMemcpyHostToDevice, E.st) != hipSuccess ||
-      hipMemcpyAsync(ds, scales, ns * 2, hipMemcpyHostToDevice, E.st) != hipSuccess)
+      hipMemcpyAsync(ds, s16, ns * 2, hipMemcpyHostToDevice, E.st) != hipSuccess)
     rc = fail(PQ_ERR_LAUNCH, "weight upload failed");
   if (rc == PQ_OK)
     rc = q.gate_up ? pq_q8_pack_gate_up(dc, ds, q.N / 2, q.K, q.pc, q.ps, E.st)
@@ -267,7 +367,7 @@ static int load_synthetic(Engine &E) {
     scales.resize((size_t)q.N * (q.K / 32));
     pq_synth_fill(PQ_SYNTH_CODES, seed(t, 0), codes.data(), codes.size(), 0, 0);
     pq_synth_fill(PQ_SYNTH_SCALES, seed(t, 1), scales.data(), scales.size(), 0.01f, 0);
-    return upload_q8(E, q, codes.data(), scales.data());
+    return upload_q8(E, q, codes.data(), scales.data(), nullptr);
   };
   auto fv = [&](float *dst, int t, size_t n, float a, float b) -> int {
     vec.resize(n);
@@ -328,50 +428,118 @@ static int reset(Engine &E) {
 }
 
 // ---------------------------------------------------------------- forward
-static int gemv_or_gemm(Engine &E, const Q8Dev &w, void *y, int T) {
-  if (T == 1) return pq_q8_gemv(w.pc, w.ps, E.qx, E.dx, y, PQ_DTYPE_BF16, w.N, w.K, E.st);
-  return pq_q8_gemm_ws(w.pc, w.ps, E.qx, E.dx, y, PQ_DTYPE_BF16, w.N, w.K, T, E.gemm_ws, E.gemm_ws_bytes, E.st);
+static int gemm_T(Engine &E, const Q8Dev &w, const int8_t *qx, const float *dx, void *y, int T) {
+  if (T == 1) return pq_q8_gemv(w.pc, w.ps, qx, dx, y, PQ_DTYPE_BF16, w.N, w.K, E.st);
+  return pq_q8_gemm_ws(w.pc, w.ps, qx, dx, y, PQ_DTYPE_BF16, w.N, w.K, T, E.gemm_ws, E.gemm_ws_bytes, E.st);
 }
 
-// Runs T <= tmax positions whose token ids are in E.tok (device) through all
-// layers; leaves the greedy id of the last position in *next (device).
-static int forward(Engine &E, int T, int32_t *next) {
+// Runs n positions whose token ids are in toks (device) through all layers and
+// leaves the greedy id of the last position in *next (device). Layer-major: a
+// layer runs every chunk of up to tmax positions before the next layer starts,
+// so its weights serve all the chunks while they are warm in the Infinity
+// Cache (the reference's layer-major prefill order, lfm3_nanode.cu:5935-5955).
+// The residual stream X and the layer input qin/din hold every position; the
+// chunk's attention sees the KV entries its earlier chunks wrote at this layer
+// and the conv ring carries from chunk to chunk, so every position's
+// arithmetic is the chunk-major (and the one-position-at-a-time) arithmetic.
+// Per chunk the sequence restates layer_body (3739-3856) / layer_chunk_T
+// (4997-5131); the "rms1 -> eadd -> rms1" triple that ends a layer writes the
+// next layer's Q8_0 input for the chunk's rows.
+static int forward(Engine &E, const int32_t *toks, int n, int32_t *next) {
   const pq_model_cfg &c = E.c;
   const int H = c.hidden, F = c.ffn;
-  if (E.pos + T > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + %d > %d", E.pos, T, c.ctx);
-  PQ_TRY(pq_embed(E.emb.pc, E.emb.ps, E.tok, E.X, H, c.vocab, T, E.st));
-  PQ_TRY(pq_rmsnorm(E.X, nullptr, E.L[0].op_norm, nullptr, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
+  if (n <= 0 || E.pos + n > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + %d > %d", E.pos, n, c.ctx);
+  PQ_TRY(pq_embed(E.emb.pc, E.emb.ps, toks, E.X, H, c.vocab, n, E.st));
+  PQ_TRY(pq_rmsnorm(E.X, nullptr, E.L[0].op_norm, nullptr, nullptr, E.qin, E.din, H, n, c.eps, E.st));
   const float scale = 1.0f / sqrtf((float)c.hd);
   for (int l = 0; l < c.nlayers; l++) {
     LayerDev &D = E.L[l];
-    if (D.attn) {
-      PQ_TRY(gemv_or_gemm(E, D.in, E.Wd, T));
-      PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd, c.rot, T,
-                        c.eps, E.st));
-      PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, nullptr, 0, E.qx, E.dx, E.pos,
-                            c.nh, c.nkv, c.hd, T, scale, E.attn_ws, E.attn_ws_bytes, E.st));
-      PQ_TRY(gemv_or_gemm(E, D.out, E.Hb, T));
-    } else {
-      PQ_TRY(gemv_or_gemm(E, D.in, E.Wd, T));
-      PQ_TRY(pq_conv(D.ring(), D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
-      PQ_TRY(pq_q8_quant_bf16(E.A, E.qx, E.dx, H, T, E.st));
-      PQ_TRY(gemv_or_gemm(E, D.out, E.Hb, T));
-    }
-    PQ_TRY(pq_rmsnorm(E.X, E.Hb, D.post_op_norm, D.ffn_norm, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
-    PQ_TRY(gemv_or_gemm(E, D.ug, E.Wd, T));
-    PQ_TRY(pq_silu_mul_interleaved(E.Wd, nullptr, E.qx, E.dx, F, T, E.st));
-    PQ_TRY(gemv_or_gemm(E, D.down, E.Hb, T));
     const float *next_norm = l + 1 < c.nlayers ? E.L[l + 1].op_norm : E.final_norm;
-    PQ_TRY(pq_rmsnorm(E.X, E.Hb, D.post_ffn_norm, next_norm, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
+    for (int c0 = 0; c0 < n; c0 += E.tmax) {
+      const int T = std::min(E.tmax, n - c0);
+      const int pos0 = E.pos + c0;
+      uint16_t *Xc = E.X + (size_t)c0 * H;
+      int8_t *qin = E.qin + (size_t)c0 * H;
+      float *din = E.din + (size_t)c0 * (H / 32);
+      PQ_TRY(gemm_T(E, D.in, qin, din, E.Wd, T));
+      if (D.attn) {
+        PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, pos0, c.nh, c.nkv, c.hd, c.rot, T,
+                          c.eps, E.st));
+        PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, nullptr, 0, E.qx, E.dx, pos0,
+                              c.nh, c.nkv, c.hd, T, scale, E.attn_ws, E.attn_ws_bytes, E.st));
+      } else {
+        PQ_TRY(pq_conv(D.ring(), D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
+        PQ_TRY(pq_q8_quant_bf16(E.A, E.qx, E.dx, H, T, E.st));
+      }
+      PQ_TRY(gemm_T(E, D.out, E.qx, E.dx, E.Hb, T));
+      PQ_TRY(pq_rmsnorm(Xc, E.Hb, D.post_op_norm, D.ffn_norm, nullptr, E.qx, E.dx, H, T, c.eps, E.st));
+      PQ_TRY(gemm_T(E, D.ug, E.qx, E.dx, E.Wd, T));
+      PQ_TRY(pq_silu_mul_interleaved(E.Wd, nullptr, E.qx, E.dx, F, T, E.st));
+      PQ_TRY(gemm_T(E, D.down, E.qx, E.dx, E.Hb, T));
+      PQ_TRY(pq_rmsnorm(Xc, E.Hb, D.post_ffn_norm, next_norm, nullptr, qin, din, H, T, c.eps, E.st));
+    }
   }
   // tied LM head on the last position's final-normed row
-  PQ_TRY(pq_q8_gemv(E.emb.pc, E.emb.ps, E.qx + (size_t)(T - 1) * H, E.dx + (size_t)(T - 1) * (H / 32), E.logits,
+  PQ_TRY(pq_q8_gemv(E.emb.pc, E.emb.ps, E.qin + (size_t)(n - 1) * H, E.din + (size_t)(n - 1) * (H / 32), E.logits,
                     PQ_DTYPE_F32, c.vocab, H, E.st));
   PQ_TRY(pq_argmax(E.logits, c.vocab, next, E.st));
-  E.pos += T;
-  E.last_t = T;
-  E.last_resid = E.X + (size_t)(T - 1) * H;
+  E.pos += n;
+  E.last_t = n;
+  E.last_resid = E.X + (size_t)(n - 1) * H;
   return PQ_OK;
+}
+
+// The same layer sequence under PQ_NUMERICS_REF: every GEMV is pq_q8r_gemv
+// (the reference's own order on bf16 activations and fp32 scales, row-major
+// codes) and the activations between ops stay bf16, as in layer_body; the
+// bf16 layer input xin holds every position (the Q8_0 qin's counterpart).
+static int gemm_r2(Engine &E, const Q8Dev &w, const uint16_t *x, void *y, int y_dtype, int T) {
+  return pq_q8r_gemv(w.pc, w.sf, x, y, y_dtype, w.N, w.K, T, E.st);
+}
+
+static int forward_r2(Engine &E, const int32_t *toks, int n, int32_t *next) {
+  const pq_model_cfg &c = E.c;
+  const int H = c.hidden, F = c.ffn;
+  if (n <= 0 || E.pos + n > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + %d > %d", E.pos, n, c.ctx);
+  PQ_TRY(pq_embed_rows(E.emb.pc, E.emb.sf, toks, E.X, H, c.vocab, n, E.st));
+  PQ_TRY(pq_rmsnorm(E.X, nullptr, E.L[0].op_norm, nullptr, E.xin, nullptr, nullptr, H, n, c.eps, E.st));
+  const float scale = 1.0f / sqrtf((float)c.hd);
+  for (int l = 0; l < c.nlayers; l++) {
+    LayerDev &D = E.L[l];
+    const float *next_norm = l + 1 < c.nlayers ? E.L[l + 1].op_norm : E.final_norm;
+    for (int c0 = 0; c0 < n; c0 += E.tmax) {
+      const int T = std::min(E.tmax, n - c0);
+      const int pos0 = E.pos + c0;
+      uint16_t *Xc = E.X + (size_t)c0 * H;
+      uint16_t *xin = E.xin + (size_t)c0 * H;
+      PQ_TRY(gemm_r2(E, D.in, xin, E.Wd, PQ_DTYPE_BF16, T));
+      if (D.attn) {
+        PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, pos0, c.nh, c.nkv, c.hd, c.rot, T,
+                          c.eps, E.st));
+        PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr, nullptr,
+                              pos0, c.nh, c.nkv, c.hd, T, scale, E.attn_ws, E.attn_ws_bytes, E.st));
+      } else {
+        PQ_TRY(pq_conv(D.ring(), D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
+      }
+      PQ_TRY(gemm_r2(E, D.out, E.A, E.Hb, PQ_DTYPE_BF16, T));
+      PQ_TRY(pq_rmsnorm(Xc, E.Hb, D.post_op_norm, D.ffn_norm, E.A, nullptr, nullptr, H, T, c.eps, E.st));
+      PQ_TRY(gemm_r2(E, D.ug, E.A, E.Wd, PQ_DTYPE_BF16, T));      // [gate | up] rows
+      PQ_TRY(pq_silu_mul(E.Wd, E.A, nullptr, nullptr, F, T, E.st));
+      PQ_TRY(gemm_r2(E, D.down, E.A, E.Hb, PQ_DTYPE_BF16, T));
+      PQ_TRY(pq_rmsnorm(Xc, E.Hb, D.post_ffn_norm, next_norm, xin, nullptr, nullptr, H, T, c.eps, E.st));
+    }
+  }
+  // tied LM head (gemv_f: fp32 logits) on the last position's final-normed row
+  PQ_TRY(gemm_r2(E, E.emb, E.xin + (size_t)(n - 1) * H, E.logits, PQ_DTYPE_F32, 1));
+  PQ_TRY(pq_argmax(E.logits, c.vocab, next, E.st));
+  E.pos += n;
+  E.last_t = n;
+  E.last_resid = E.X + (size_t)(n - 1) * H;
+  return PQ_OK;
+}
+
+static int forward_any(Engine &E, const int32_t *toks, int n, int32_t *next) {
+  return ref_numerics(E) ? forward_r2(E, toks, n, next) : forward(E, toks, n, next);
 }
 
 // Whether the fused decode kernels take this configuration: power-of-two
@@ -383,7 +551,8 @@ static bool fused_supported(const pq_model_cfg &c, const char **why) {
   bool conv = false, attn = false;
   for (int l = 0; l < c.nlayers; l++) ((c.attn_mask >> l) & 1u ? attn : conv) = true;
   *why = nullptr;
-  if (!pow2(c.hidden) || !pow2(c.ffn)) *why = "hidden and ffn must be powers of two in 1024..8192";
+  if (c.numerics == PQ_NUMERICS_REF) *why = "the reference-numerics mode runs unfused steps";
+  else if (!pow2(c.hidden) || !pow2(c.ffn)) *why = "hidden and ffn must be powers of two in 1024..8192";
   else if (conv && c.ntaps != 3) *why = "the fused conv prologue takes 3 taps";
   else if (attn) {
     const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
@@ -478,16 +647,15 @@ static int forward_decode(Engine &E, bool dev) {
   return PQ_OK;
 }
 
-// Prompt in chunks of tmax positions; the greedy id after the last one goes to *next.
+// The prompt, uploaded once (the copy is waited for: the caller's host buffer
+// may go away when the call returns), then run layer-major in chunks of tmax
+// positions with no further host synchronization; the greedy id after the
+// last position goes to *next.
 static int prefill(Engine &E, const int32_t *prompt, int n, int32_t *next) {
-  for (int i = 0; i < n; i += E.tmax) {
-    const int T = std::min(E.tmax, n - i);
-    if (hipMemcpyAsync(E.tok, prompt + i, (size_t)T * 4, hipMemcpyHostToDevice, E.st) != hipSuccess)
-      return fail(PQ_ERR_LAUNCH, "token upload failed");
-    PQ_TRY(forward(E, T, next));
-    if (hipStreamSynchronize(E.st) != hipSuccess) return fail(PQ_ERR_LAUNCH, "prefill sync failed");
-  }
-  return PQ_OK;
+  if (hipMemcpyAsync(E.tokd, prompt, (size_t)n * 4, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+      hipStreamSynchronize(E.st) != hipSuccess)
+    return fail(PQ_ERR_LAUNCH, "token upload failed");
+  return forward_any(E, E.tokd, n, next);
 }
 
 // n decode steps from the device-resident token *E.tok: step s feeds the id
@@ -554,7 +722,7 @@ static int decode(Engine &E, int n, int first_slot) {
   }
   for (int s = 0; s < n; s++) {
     if (E.fused) PQ_TRY(forward_decode(E, false));
-    else PQ_TRY(forward(E, 1, E.tok));
+    else PQ_TRY(forward_any(E, E.tok, 1, E.tok));
     if (hipMemcpyAsync(E.ids + first_slot + s, E.tok, 4, hipMemcpyDeviceToDevice, E.st) != hipSuccess)
       return fail(PQ_ERR_LAUNCH, "id copy failed");
   }
@@ -572,8 +740,10 @@ extern "C" void *pq_engine_create(const pq_model_cfg *cfg) {
                   c.ffn > 0 && c.vocab > 0 && c.nlayers > 0 && c.nlayers <= 32 && c.hd == 64 && c.nkv > 0 &&
                   c.nh % c.nkv == 0 && c.nh * c.hd % 64 == 0 && c.rot >= 0 && c.rot <= c.hd && c.rot % 2 == 0 &&
                   (c.ntaps == 2 || c.ntaps == 3 || c.ntaps == 4 || c.ntaps == 7) && c.ctx > 0 &&
-                  c.prefill_chunk > 0 && c.prefill_chunk <= 512;
+                  c.prefill_chunk > 0 && c.prefill_chunk <= 512 &&
+                  (c.numerics == PQ_NUMERICS_Q8 || c.numerics == PQ_NUMERICS_REF);
   if (!ok) { fail(PQ_ERR_ARG, "pq_engine_create: unsupported configuration"); return nullptr; }
+  if (c.slide_mask != 0) { fail(PQ_ERR_ARG, "pq_engine_create: sliding-window layers are not supported"); return nullptr; }
   auto E = std::make_unique<Engine>();
   if (create(*E, c) != PQ_OK) return nullptr;
   if (upload_rope(*E) != PQ_OK || reset(*E) != PQ_OK) return nullptr;
@@ -600,7 +770,15 @@ extern "C" int pq_engine_set_q8(void *h, int layer, int slot, const int8_t *code
   Engine &E = *static_cast<Engine *>(h);
   Q8Dev *q = q8_slot(E, layer, slot);
   PQ_REQUIRE(q, PQ_ERR_ARG, "pq_engine_set_q8: no Q8 tensor at layer %d slot %d", layer, slot);
-  return upload_q8(E, *q, codes, scales);
+  return upload_q8(E, *q, codes, scales, nullptr);
+}
+
+extern "C" int pq_engine_set_q8_f32(void *h, int layer, int slot, const int8_t *codes, const float *scales) {
+  PQ_REQUIRE(h && codes && scales, PQ_ERR_ARG, "pq_engine_set_q8_f32: null pointer");
+  Engine &E = *static_cast<Engine *>(h);
+  Q8Dev *q = q8_slot(E, layer, slot);
+  PQ_REQUIRE(q, PQ_ERR_ARG, "pq_engine_set_q8_f32: no Q8 tensor at layer %d slot %d", layer, slot);
+  return upload_q8(E, *q, codes, nullptr, scales);
 }
 
 extern "C" int pq_engine_set_f32(void *h, int layer, int slot, const float *v, size_t n) {
@@ -613,29 +791,6 @@ extern "C" int pq_engine_set_f32(void *h, int layer, int slot, const float *v, s
 }
 
 // ------------------------------------------------------------ .lfm3q8 load
-// fp32 -> binary16 bits, round to nearest even (overflow to inf, NaN kept).
-static uint16_t host_f2h(float f) {
-  uint32_t u;
-  memcpy(&u, &f, 4);
-  const uint32_t sign = (u >> 16) & 0x8000u, e = (u >> 23) & 0xffu, m = u & 0x7fffffu;
-  if (e == 0xff) return (uint16_t)(sign | 0x7c00u | (m ? 0x200u | (m >> 13) : 0u));
-  const int ex = (int)e - 127 + 15;
-  if (ex >= 31) return (uint16_t)(sign | 0x7c00u);
-  if (ex <= 0) {   // binary16 subnormal (or zero): shift the full mantissa, round to even
-    if (ex < -10) return (uint16_t)sign;
-    const uint32_t mm = m | 0x800000u;
-    const int sh = 14 - ex;
-    uint32_t q = mm >> sh;
-    const uint32_t rem = mm & ((1u << sh) - 1), half = 1u << (sh - 1);
-    if (rem > half || (rem == half && (q & 1))) q++;
-    return (uint16_t)(sign | q);
-  }
-  uint32_t q = ((uint32_t)ex << 10) | (m >> 13);
-  const uint32_t rem = m & 0x1fffu;
-  if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;   // a carry into the exponent is still right
-  return (uint16_t)(sign | q);
-}
-
 namespace {
 struct BlobSrc {
   std::string name;
@@ -650,9 +805,10 @@ struct BlobTarget {
 
 // The reference's tensor names (layer_body, lfm3_nanode.cu:3739-3856; the
 // exporter's table) onto the engine's slots: q|k|v|gate_proj stack into the
-// attention layer's input GEMV, w1 (gate) and w3 (up) into gate/up; fp32
-// weight scales become the engine's fp16 scales (round to nearest even:
-// exact for blobs written from fp16 scales).
+// attention layer's input GEMV, w1 (gate) and w3 (up) into gate/up. The fp32
+// weight scales stay fp32 under PQ_NUMERICS_REF; under PQ_NUMERICS_Q8 they
+// must be fp16 values (a blob written from fp16 scales), else the load is
+// refused with a count of the scales fp16 cannot hold.
 static int load_blob(Engine &E, void *blob) {
   const pq_model_cfg &c = E.c;
   const long long H = c.hidden, F = c.ffn;
@@ -708,7 +864,7 @@ static int load_blob(Engine &E, void *blob) {
   pq::BlobReader rd(blob, order, 2);
   std::vector<char> buf;
   std::vector<int8_t> codes;
-  std::vector<uint16_t> sc16;
+  std::vector<float> sc32;
   for (const BlobTarget &t : T) {
     if (!t.q8) {
       PQ_TRY(rd.take(buf));
@@ -726,17 +882,23 @@ static int load_blob(Engine &E, void *blob) {
                "pq_engine_load_blob: slot %d of layer %d holds [%d x %d]", t.slot, t.layer, q ? q->N : 0,
                q ? q->K : 0);
     codes.resize((size_t)rows * q->K);
-    sc16.resize((size_t)rows * (q->K / 32));
+    sc32.resize((size_t)rows * (q->K / 32));
     size_t r0 = 0;
     for (const BlobSrc &s : t.src) {
       PQ_TRY(rd.take(buf));
       const size_t nc = (size_t)s.n0 * s.n1, ns = nc / 32;
       memcpy(codes.data() + r0 * q->K, buf.data(), nc);
-      const float *sf = reinterpret_cast<const float *>(buf.data() + nc);
-      for (size_t k = 0; k < ns; k++) sc16[r0 * (q->K / 32) + k] = host_f2h(sf[k]);
+      memcpy(sc32.data() + r0 * (q->K / 32), buf.data() + nc, ns * 4);
       r0 += (size_t)s.n0;
     }
-    PQ_TRY(upload_q8(E, *q, codes.data(), sc16.data()));
+    const int rc = upload_q8(E, *q, codes.data(), nullptr, sc32.data());
+    if (rc != PQ_OK) {
+      if (rc == PQ_ERR_DATA) {   // name the tensor in the message
+        const std::string why = pq_last_error();
+        return fail(PQ_ERR_DATA, "pq_engine_load_blob: %s: %s", t.src[0].name.c_str(), why.c_str());
+      }
+      return rc;
+    }
   }
   return PQ_OK;
 }
@@ -774,10 +936,13 @@ extern "C" int pq_engine_feed(void *h, const int32_t *tokens, int n, int32_t *ne
   PQ_REQUIRE(n <= E.c.ctx - E.pos, PQ_ERR_STATE, "pq_engine_feed: %d tokens at position %d exceed the context %d", n,
              E.pos, E.c.ctx);
   PQ_TRY(prefill(E, tokens, n, E.tok));
-  if (next_id && hipMemcpy(next_id, E.tok, 4, hipMemcpyDeviceToHost) != hipSuccess)
+  // the copies go on the engine's stream (a non-blocking stream: a null-stream
+  // copy would not wait for the forward pass) and are waited for
+  if (next_id && hipMemcpyAsync(next_id, E.tok, 4, hipMemcpyDeviceToHost, E.st) != hipSuccess)
     return fail(PQ_ERR_LAUNCH, "id copy failed");
-  if (logits && hipMemcpy(logits, E.logits, (size_t)E.c.vocab * 4, hipMemcpyDeviceToHost) != hipSuccess)
+  if (logits && hipMemcpyAsync(logits, E.logits, (size_t)E.c.vocab * 4, hipMemcpyDeviceToHost, E.st) != hipSuccess)
     return fail(PQ_ERR_LAUNCH, "logits copy failed");
+  if ((next_id || logits) && hipStreamSynchronize(E.st) != hipSuccess) return fail(PQ_ERR_LAUNCH, "stream sync failed");
   return PQ_OK;
 }
 
@@ -819,6 +984,16 @@ extern "C" int pq_engine_set_fused(void *h, int on) {
   return PQ_OK;
 }
 
+extern "C" int pq_engine_set_chunk(void *h, int n) {
+  PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
+  Engine &E = *static_cast<Engine *>(h);
+  PQ_REQUIRE(n >= 1 && n <= E.c.prefill_chunk, PQ_ERR_ARG,
+             "pq_engine_set_chunk: %d positions (1..%d, the prefill_chunk the engine was created with)", n,
+             E.c.prefill_chunk);
+  E.tmax = n;
+  return PQ_OK;
+}
+
 extern "C" int pq_engine_set_graph(void *h, int on) {
   PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
   static_cast<Engine *>(h)->graph = on != 0;
@@ -840,7 +1015,8 @@ extern "C" int pq_engine_hidden(void *h, uint16_t *out) {
   Engine &E = *static_cast<Engine *>(h);
   // The residual stream of the last position fed.
   if (!E.last_resid) return fail(PQ_ERR_STATE, "pq_engine_hidden: nothing fed yet");
-  return hipMemcpy(out, E.last_resid, (size_t)E.c.hidden * 2, hipMemcpyDeviceToHost) == hipSuccess
+  return hipMemcpyAsync(out, E.last_resid, (size_t)E.c.hidden * 2, hipMemcpyDeviceToHost, E.st) == hipSuccess &&
+                 hipStreamSynchronize(E.st) == hipSuccess
              ? PQ_OK
              : fail(PQ_ERR_LAUNCH, "hidden copy failed");
 }
@@ -849,7 +1025,8 @@ extern "C" size_t pq_engine_weight_bytes(void *h) {
   if (!h) return 0;
   Engine &E = *static_cast<Engine *>(h);
   size_t b = 0;
-  auto q8 = [&](const Q8Dev &q) { b += (size_t)q.N * q.K + (size_t)q.N * (q.K / 32) * 2; };
+  const size_t sb = ref_numerics(E) ? 4 : 2;   // fp32 or fp16 scale per 32
+  auto q8 = [&](const Q8Dev &q) { b += (size_t)q.N * q.K + (size_t)q.N * (q.K / 32) * sb; };
   for (const LayerDev &D : E.L) {
     q8(D.in); q8(D.out); q8(D.ug); q8(D.down);
   }

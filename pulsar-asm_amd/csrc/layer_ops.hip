@@ -155,37 +155,54 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv,
 }
 
 // ------------------------------------------------------------ short conv
-// One thread per channel walks the T positions with the ring in registers:
-// bx = bf16(B*x), shift, acc = sum_k fl(tap_k * ring_k) ascending, cy = bf16,
-// out = bf16(C*cy) (k_conv_chunk, lfm3_nanode.cu:917-941). Optional Q8_0
-// output of out for the next GEMV.
+// k_conv_chunk (lfm3_nanode.cu:917-941): per channel, bx = bf16(B*x); the
+// window of the last NT bx values (the ring holds the NT before the chunk,
+// newest last); acc = sum_k fl(tap_k * bx_{t-NT+1+k}) ascending from 0;
+// cy = bf16(acc); out = bf16(C*cy). The positions are independent once bx is
+// known, so a workgroup owns 64 channels and its waves take positions t = w,
+// w + W, ...; each thread forms the bx values of its window itself (the same
+// bf16 products), reading the ring for positions before the chunk. The new
+// ring (the last NT bx values) is written after a workgroup barrier, so every
+// read of the old ring has happened: a channel's ring is touched by its own
+// workgroup only, which makes the in-place update safe.
 template <int NT>
-__global__ __launch_bounds__(256) void conv_kernel(uint16_t *__restrict__ ring, const float *__restrict__ taps,
+__global__ __launch_bounds__(512) void conv_kernel(uint16_t *__restrict__ ring, const float *__restrict__ taps,
                                                     const uint16_t *__restrict__ bcx, uint16_t *__restrict__ out,
                                                     int H, int T) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= H) return;
-  uint16_t r[NT];
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int w = threadIdx.x >> 6, W = blockDim.x >> 6;
+  const bool live = c < H;
   float tp[NT];
+  uint16_t old[NT];
 #pragma unroll
   for (int k = 0; k < NT; k++) {
-    r[k] = ring[(size_t)k * H + i];
-    tp[k] = taps[(size_t)i * NT + k];
+    tp[k] = live ? taps[(size_t)c * NT + k] : 0.0f;
+    old[k] = live ? ring[(size_t)k * H + c] : (uint16_t)0;
   }
-  for (int t = 0; t < T; t++) {
-    const uint16_t *row = bcx + (size_t)t * 3 * H;
-    const uint16_t bx = f2bf(bf2f(row[i]) * bf2f(row[2 * H + i]));
+  auto bx = [&](int tau) -> uint16_t {   // tau < 0: the ring (tau = -1 is its newest entry)
+    if (tau < 0) return old[NT + tau];
+    const uint16_t *row = bcx + (size_t)tau * 3 * H;
+    return f2bf(bf2f(row[c]) * bf2f(row[2 * H + c]));
+  };
+  if (live) {
+    for (int t = w; t < T; t += W) {
+      float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NT - 1; k++) r[k] = r[k + 1];
-    r[NT - 1] = bx;
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < NT; k++) acc = acc + tp[k] * bf2f(r[k]);
-    const uint16_t cy = f2bf(acc);
-    out[(size_t)t * H + i] = f2bf(bf2f(row[H + i]) * bf2f(cy));
+      for (int k = 0; k < NT; k++) acc = acc + tp[k] * bf2f(bx(t - (NT - 1) + k));
+      const uint16_t cy = f2bf(acc);
+      out[(size_t)t * H + c] = f2bf(bf2f(bcx[(size_t)t * 3 * H + H + c]) * bf2f(cy));
+    }
   }
+  uint16_t nr[NT];
+  if (live && w == 0) {
 #pragma unroll
-  for (int k = 0; k < NT; k++) ring[(size_t)k * H + i] = r[k];
+    for (int k = 0; k < NT; k++) nr[k] = bx(T - NT + k);
+  }
+  __syncthreads();   // every thread's reads of the old ring are done
+  if (live && w == 0) {
+#pragma unroll
+    for (int k = 0; k < NT; k++) ring[(size_t)k * H + c] = nr[k];
+  }
 }
 
 // ------------------------------------------------------- silu(gate) * up
@@ -266,6 +283,26 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *__restrict__ p
   out[(size_t)t * H + k] = f2bf((float)c * h2f(s));
 }
 
+// The same lookup on the table as the .lfm3q8 file stores it (row-major
+// codes [vocab][H], one fp32 scale per 32): the reference-numerics engine's
+// table, k_dequant_row exactly as the reference calls it.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int8_t *__restrict__ codes,
+                                                          const float *__restrict__ scales,
+                                                          const int32_t *__restrict__ tok, uint16_t *__restrict__ out,
+                                                          int H, int vocab) {
+  const int t = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= H) return;
+  const int id = tok[t];
+  if (id < 0 || id >= vocab) {
+    out[(size_t)t * H + k] = 0;
+    return;
+  }
+  const int8_t c = codes[(size_t)id * H + k];
+  const float s = scales[(size_t)id * (H / 32) + k / 32];
+  out[(size_t)t * H + k] = f2bf((float)c * s);
+}
+
 }  // namespace pq
 
 using namespace pq;
@@ -314,7 +351,9 @@ extern "C" int pq_conv(uint16_t *ring, const float *taps, const uint16_t *bcx, u
                        void *stream) {
   PQ_REQUIRE(ring && taps && bcx && out, PQ_ERR_ARG, "pq_conv: null pointer");
   PQ_REQUIRE(H > 0 && T > 0, PQ_ERR_ARG, "pq_conv: H=%d T=%d", H, T);
-  const dim3 grid((H + 255) / 256), block(256);
+  // 64 channels per workgroup; up to 8 waves over the positions
+  const int waves = T < 8 ? T : 8;
+  const dim3 grid((H + 63) / 64), block(64 * waves);
   hipStream_t st = as_stream(stream);
   switch (ntaps) {
     case 2: launch(conv_kernel<2>, grid, block, 0, st, ring, taps, bcx, out, H, T); break;
@@ -361,4 +400,14 @@ extern "C" int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int
   launch(embed_kernel, dim3((H + 255) / 256, T), dim3(256), 0, as_stream(stream), pcodes, pscales, tokens, out, H,
          vocab);
   return check_launch("pq_embed");
+}
+
+extern "C" int pq_embed_rows(const int8_t *codes, const float *scales, const int32_t *tokens, uint16_t *out, int H,
+                             int vocab, int T, void *stream) {
+  PQ_REQUIRE(codes && scales && tokens && out, PQ_ERR_ARG, "pq_embed_rows: null pointer");
+  PQ_REQUIRE(H > 0 && H % 32 == 0 && vocab > 0 && T > 0, PQ_ERR_ARG, "pq_embed_rows: H=%d vocab=%d T=%d", H, vocab,
+             T);
+  launch(embed_rows_kernel, dim3((H + 255) / 256, T), dim3(256), 0, as_stream(stream), codes, scales, tokens, out, H,
+         vocab);
+  return check_launch("pq_embed_rows");
 }

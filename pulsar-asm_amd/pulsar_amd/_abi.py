@@ -13,7 +13,9 @@ class ModelCfg(C.Structure):
     _fields_ = [("hidden", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("nlayers", C.c_int),
                 ("nh", C.c_int), ("nkv", C.c_int), ("hd", C.c_int), ("rot", C.c_int),
                 ("ntaps", C.c_int), ("ctx", C.c_int), ("eps", C.c_float), ("theta", C.c_float),
-                ("seed", C.c_uint64), ("attn_mask", C.c_uint32), ("prefill_chunk", C.c_int)]
+                ("seed", C.c_uint64), ("attn_mask", C.c_uint32), ("prefill_chunk", C.c_int),
+                ("numerics", C.c_int), ("slide_mask", C.c_uint32), ("slide_win", C.c_int),
+                ("slide_rot", C.c_int), ("slide_theta", C.c_float)]
 
 
 class BlobTensor(C.Structure):
@@ -64,6 +66,8 @@ SIGNATURES = {
     "pq_silu_mul_interleaved": (I, [P, P, P, P, I, I, P]),
     "pq_argmax": (I, [P, I, P, P]),
     "pq_embed": (I, [P, P, P, P, I, I, I, P]),
+    "pq_embed_rows": (I, [P, P, P, P, I, I, I, P]),
+    "pq_engine_set_q8_f32": (I, [P, I, I, P, P]),
     "pq_q8_gemv_parts": (I, [I, I]),
     "pq_q8_gemv_fused": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, I, P, P]),
     "pq_argmax_parts": (I, [P, I, P, P]),
@@ -95,6 +99,7 @@ SIGNATURES = {
     "pq_engine_decode": (I, [P, I, P]),
     "pq_engine_set_fused": (I, [P, I]),
     "pq_engine_set_graph": (I, [P, I]),
+    "pq_engine_set_chunk": (I, [P, I]),
     "pq_engine_sync": (I, [P]),
     "pq_engine_stream": (P, [P]),
     "pq_engine_position": (I, [P]),

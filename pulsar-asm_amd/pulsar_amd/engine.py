@@ -10,7 +10,7 @@ from ._abi import ModelCfg
 # 32 q / 8 kv heads of dim 64 (RoPE on the first 32 dims, theta 1e6), 3-tap
 # gated short conv in layers 0-15 and GQA attention in layers 16-23.
 LFM3_SYNTH = dict(hidden=2048, ffn=8192, vocab=65536, nlayers=24, nh=32, nkv=8, hd=64, rot=32, ntaps=3,
-                  ctx=2048, eps=1e-5, theta=1e6, seed=20261201, attn_mask=0xFF0000, prefill_chunk=32)
+                  ctx=2048, eps=1e-5, theta=1e6, seed=20261201, attn_mask=0xFF0000, prefill_chunk=256)
 
 
 def _p(a):
@@ -81,6 +81,10 @@ class Engine:
 
     def set_fused(self, on):
         check(lib().pq_engine_set_fused(self.h, 1 if on else 0), "pq_engine_set_fused")
+
+    def set_chunk(self, n):
+        """Positions per prefill chunk (1 .. the prefill_chunk of the configuration)."""
+        check(lib().pq_engine_set_chunk(self.h, n), "pq_engine_set_chunk")
 
     def set_graph(self, on):
         check(lib().pq_engine_set_graph(self.h, 1 if on else 0), "pq_engine_set_graph")

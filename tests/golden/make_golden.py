@@ -1,11 +1,13 @@
 """Writes the golden fixtures of tests/golden/ from the CPU oracle.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [kernels] [tiny] [full] [full_ref]
 
 lfm3_synth_greedy.json  the synthetic 24-layer LFM3-style backbone (hidden 2048,
                         FFN 8192, vocab 65536, layers 0-15 gated conv, 16-23 GQA
                         attention 32/8 x 64, RoPE theta 1e6 on 32 dims): a 256-token
                         prompt and the 64 greedy ids the oracle decodes from it
+lfm3_synth_greedy_ref.json  the same model and prompt with every GEMV in the
+                        reference's own order (numerics = 1: bf16 x, fp32 scales)
 tiny_greedy.json        a 4-layer, hidden-256 model: prompt, ids, last logits digest
 kernels.npz             small kernel vectors (Q8_0 GEMV / GEMM, ternary GEMV,
                         attention) with their oracle outputs
@@ -71,6 +73,12 @@ def kernel_fixture(path):
 
 
 if __name__ == "__main__":
-    kernel_fixture(os.path.join(HERE, "kernels.npz"))
-    greedy_fixture(TINY, 40, 16, os.path.join(HERE, "tiny_greedy.json"))
-    greedy_fixture(FULL, 256, 64, os.path.join(HERE, "lfm3_synth_greedy.json"))
+    which = sys.argv[1:] or ["kernels", "tiny", "full", "full_ref"]
+    if "kernels" in which:
+        kernel_fixture(os.path.join(HERE, "kernels.npz"))
+    if "tiny" in which:
+        greedy_fixture(TINY, 40, 16, os.path.join(HERE, "tiny_greedy.json"))
+    if "full" in which:
+        greedy_fixture(FULL, 256, 64, os.path.join(HERE, "lfm3_synth_greedy.json"))
+    if "full_ref" in which:
+        greedy_fixture(dict(FULL, numerics=1), 256, 64, os.path.join(HERE, "lfm3_synth_greedy_ref.json"))

@@ -84,7 +84,7 @@ def test_lfm3_synth_greedy_64(orc, pq, dev):
     g = json.load(open(os.path.join(GOLDEN, "lfm3_synth_greedy.json")))
     cfg = dict(g["cfg"])
     t0 = time.time()
-    e = _engine(pq, cfg)
+    e = _engine(pq, cfg, chunk=256)       # the 256-token prompt as one layer-major chunk
     t1 = time.time()
     prompt = np.array(g["prompt"], np.int32)
     assert np.array_equal(prompt, orc.gen_tokens(g["prompt_seed"], g["n_prompt"], cfg["vocab"]))
@@ -95,6 +95,10 @@ def test_lfm3_synth_greedy_64(orc, pq, dev):
     e.reset()
     _, lg = e.feed(prompt, True)
     import hashlib
+    assert hashlib.sha256(lg.tobytes()).hexdigest() == g["prompt_logits_sha256"]
+    e.set_chunk(32)                       # eight 32-position chunks per layer: the same bits
+    e.reset()
+    _, lg = e.feed(prompt, True)
     assert hashlib.sha256(lg.tobytes()).hexdigest() == g["prompt_logits_sha256"]
     e.close()
 
@@ -180,3 +184,89 @@ def test_feed_past_context_is_refused_whole(orc, pq, dev):
     assert r_e == r_r and np.array_equal(lg_e.view(np.uint32), lg_r.view(np.uint32))
     e.close()
     ref.close()
+
+
+# ------------------------------------------------ the reference's GEMV numerics
+@pytest.mark.parametrize("cfg", [TINY, WIDE2], ids=["tiny", "wide2"])
+def test_ref_numerics_matches_oracle(orc, pq, dev, cfg):
+    """numerics = 1 (PQ_NUMERICS_REF): every GEMV through pq_q8r_gemv on bf16
+    activations and fp32 scales, bit for bit against the oracle backbone in the
+    same mode, over a 40-token prompt (layer-major, chunks of 32) and 4 steps."""
+    cfg = dict(cfg, numerics=1)
+    e = _engine(pq, cfg)
+    m = orc.Model(**cfg)
+    prompt = orc.gen_tokens(5, 40, cfg["vocab"])
+    r_e, lg_e = e.feed(prompt, True)
+    r_o, lg_o = m.feed(prompt, True)
+    assert np.array_equal(e.hidden(), m.hidden())
+    assert r_e == r_o and np.array_equal(lg_e.view(np.uint32), lg_o.view(np.uint32))
+    for step in range(4):
+        r_e, lg_e = e.feed(np.array([r_e], np.int32), True)
+        r_o, lg_o = m.feed(np.array([r_o], np.int32), True)
+        assert r_e == r_o and np.array_equal(lg_e.view(np.uint32), lg_o.view(np.uint32)), step
+    e.close()
+    m.close()
+
+
+def test_ref_numerics_greedy_64(orc, pq, dev):
+    """The synthetic 24-layer backbone under the reference's GEMV order: the
+    64 greedy ids of tests/golden/lfm3_synth_greedy_ref.json."""
+    g = json.load(open(os.path.join(GOLDEN, "lfm3_synth_greedy_ref.json")))
+    cfg = dict(g["cfg"])
+    assert cfg["numerics"] == 1
+    e = _engine(pq, cfg, chunk=256)
+    ids = e.greedy(np.array(g["prompt"], np.int32), 64)
+    assert ids.tolist() == g["ids"], f"first mismatch at step {int(np.argmax(ids != np.array(g['ids'])))}"
+    e.reset()
+    _, lg = e.feed(np.array(g["prompt"], np.int32), True)
+    import hashlib
+    assert hashlib.sha256(lg.tobytes()).hexdigest() == g["prompt_logits_sha256"]
+    e.close()
+
+
+def test_blob_scales_fp16_or_ref_numerics(orc, pq, dev, tmp_path):
+    """A blob whose fp32 scales fp16 cannot hold: the Q8 engine refuses it with
+    a count (nothing rounded silently); the reference-numerics engine loads it
+    with its fp32 scales. An exact blob loads in both modes and matches the
+    synthetic engines."""
+    from pulsar_amd.blob import Blob, write_blob
+    from pulsar_amd.engine import Engine
+    p = tmp_path / "tiny.lfm3q8"
+    _model_blob(orc, TINY, p)
+    ref_cfg = dict(TINY, numerics=1)
+    g = json.load(open(os.path.join(GOLDEN, "tiny_greedy.json")))
+    prompt = np.array(g["prompt"], np.int32)
+    e = Engine(**ref_cfg)
+    e.load_blob(p)
+    syn = _engine(pq, ref_cfg)
+    assert np.array_equal(e.greedy(prompt, 8), syn.greedy(prompt, 8))
+    assert np.array_equal(e.hidden(), syn.hidden())
+    e.close()
+    syn.close()
+    # nudge one tensor's scales off the fp16 grid
+    b = Blob(p)
+    ts = []
+    for i in range(len(b)):
+        info = b.info(i)
+        v = b.read(i)
+        if info["name"] == "lfm.model.layers.1.self_attn.o_proj.weight":
+            c, s = v
+            s = s.copy()
+            s[::3] *= np.float32(1 + 2 ** -20)
+            v = (c, s)
+        elif info["dtype"] == 3:
+            v = ("bf16", v)
+        ts.append((info["name"], v))
+    cfg_json = b.config()
+    b.close()
+    q = tmp_path / "nudged.lfm3q8"
+    write_blob(q, cfg_json, ts)
+    e = Engine(**TINY)
+    with pytest.raises(pq.PQError, match="o_proj.*not fp16 values"):
+        e.load_blob(q)
+    e.close()
+    e = Engine(**ref_cfg)
+    e.load_blob(q)                        # kept as fp32: loads
+    ids = e.greedy(prompt, 4)
+    assert len(ids) == 4
+    e.close()

@@ -490,8 +490,9 @@ TINY = dict(hidden=256, ffn=512, vocab=1000, nlayers=4, nh=4, nkv=2, hd=64, rot=
             eps=1e-5, theta=1e6, seed=20261201, attn_mask=0b1010)
 
 
-def test_model_batched_equals_sequential(orc):
-    m = orc.Model(**TINY)
+@pytest.mark.parametrize("numerics", [0, 1])
+def test_model_batched_equals_sequential(orc, numerics):
+    m = orc.Model(**TINY, numerics=numerics)
     prompt = orc.gen_tokens(5, 40, TINY["vocab"])
     r1, lg1 = m.feed(prompt, True)
     h1 = m.hidden()
@@ -518,6 +519,28 @@ def test_model_head_composition(orc):
     ids = m.greedy(prompt, 16)
     assert len(set(ids.tolist())) >= 6
     m.close()
+
+
+def test_model_ref_numerics(orc):
+    """numerics = 1: the same model with every GEMV in the reference's own order
+    (orc_q8r_gemm on bf16 x and the fp32 widening of the same scales): the
+    head is that GEMV of the final-normed residual, the greedy stream is live,
+    and the logits differ from the Q8_0 x Q8_0 model's (so the switch reaches
+    the GEMVs) while staying close to them."""
+    m = orc.Model(**TINY, numerics=1)
+    prompt = orc.gen_tokens(6, 17, TINY["vocab"])
+    r, lg = m.feed(prompt, True)
+    W, S = m.tensor(-1, 0)
+    h = orc.rmsnorm(m.hidden(), m.tensor(-1, 1), 1e-5)
+    want = orc.q8r_gemm(W, S.view(np.float16).astype(np.float32), h[None, :])[0]
+    assert np.array_equal(f32bits(want), f32bits(lg)) and r == orc.argmax(lg)
+    assert len(set(m.greedy(prompt, 16).tolist())) >= 6
+    m.close()
+    q = orc.Model(**TINY)
+    _, lq = q.feed(prompt, True)
+    q.close()
+    assert not np.array_equal(f32bits(lq), f32bits(lg))
+    assert np.corrcoef(lq, lg)[0, 1] > 0.9
 
 
 # --------------------------------------------------------- golden fixtures
