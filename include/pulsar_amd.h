@@ -228,23 +228,27 @@ int pq_rmsnorm(uint16_t *x, const uint16_t *h, const float *w0, const float *w1,
 /* Per-head q/k RMSNorm, zero-tail partial RoPE from a [pos][rot/2][cos,sin]
  * table, and the fp16 KV-cache write of k and v at positions pos0..pos0+T-1.
  * qkv rows hold [q (nh*hd) | k (nkv*hd) | v (nkv*hd) | ...] with row_stride
- * elements; q is updated in place. head_dim 64. Replaces k_headnorm,
+ * elements; q is updated in place. head_dim 64 or 128; the table and rot are
+ * the layer type's (full attention: partial rotation, theta 1e6; sliding:
+ * full rotation, theta 1e4 -- lfm3_nanode.cu:3756-3765). Replaces k_headnorm,
  * k_rope and the KV write (460-498, 157-162, 3749-3778). */
 int pq_qk_prep(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm,
                const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv,
                int hd, int rot, int T, float eps, void *stream);
 
 /* Split-K flash-decode attention over the fp16 cache [ctx][nkv][hd]: query t
- * (row t of q, stride q_stride) at position pos0+t attends keys 0..pos0+t.
+ * (row t of q, stride q_stride) at position pos0+t attends keys lo..pos0+t,
+ * lo = pos0+t+1-win when win > 0 and the context has outgrown the window
+ * (a sliding-window layer, as k_attn_head's win, lfm3_nanode.cu:515), else 0.
  * Splits of 64 positions, merged in ascending order; then the per-head
  * sigmoid gate (gate row t, stride gate_stride; NULL for none). Output to
  * out (bf16, stride out_stride) and/or (qx, dx) as Q8_0 for o_proj. ws holds
- * the split partials (pq_attn_workspace_bytes). Replaces k_attn_head(G) and
- * k_sigmoid_gate(4) (503-809, 852-888). */
-size_t pq_attn_workspace_bytes(int nh, int max_pos, int T);
+ * the split partials (pq_attn_workspace_bytes). head_dim 64 or 128. Replaces
+ * k_attn_head(G) and k_sigmoid_gate(4) (503-809, 852-888). */
+size_t pq_attn_workspace_bytes(int nh, int hd, int max_pos, int T);
 int pq_attn_decode(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
                    const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int8_t *qx,
-                   float *dx, int pos0, int nh, int nkv, int hd, int T, float scale, void *ws,
+                   float *dx, int pos0, int nh, int nkv, int hd, int T, float scale, int win, void *ws,
                    size_t ws_bytes, void *stream);
 
 /* Gated short conv over T positions: bcx rows [B | C | x] (3H), ring

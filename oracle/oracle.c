@@ -588,11 +588,21 @@ void orc_rope(uint16_t *x, const float *cs, int pos, int nheads, int hd, int rot
  *   M = max m_j; for j ascending: w = expf(fl(m_j - M)),
  *     L = fmaf(l_j, w, L), O_d = fmaf(o_jd, w, O_d)   (from 0)
  *   out_d = bf16(fl(O_d / L))
- * Pinned by: a double-precision two-pass softmax (orc_attn_twopass) within
- * bf16 rounding, and npos = 1 (out = v_0 exactly up to bf16). */
+ * win > 0 (sliding-window layers): only keys [lo, npos) take part, see below.
+ * Pinned by: a double-precision two-pass softmax (orc_attn_twopass) over the
+ * same keys within bf16 rounding, npos = 1 (out = v_0 exactly up to bf16) and
+ * win = 1 (out = v_{npos-1}). */
 void orc_attn(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, uint16_t *out,
-              int npos, int nh, int nkv, int hd, float scale) {
+              int npos, int nh, int nkv, int hd, float scale, int win) {
   const int grp = nh / nkv;
+  /* sliding window: the query at position npos-1 sees keys [lo, npos), with
+   * the reference's lo = (win > 0 && npos > win) ? npos - win : 0
+   * (k_attn_head, lfm3_nanode.cu:515). The splits stay the 64-aligned blocks
+   * of absolute positions; slots outside [lo, npos) hold nothing (e = 0, not
+   * in the max, skipped in the value chain), and splits with no visible
+   * position are left out of the merge. */
+  const int lo = (win > 0 && npos > win) ? npos - win : 0;
+  const int j0 = lo / ORC_ATT_SPLIT;
   const int nsplit = (npos + ORC_ATT_SPLIT - 1) / ORC_ATT_SPLIT;
   float *m = (float *)malloc(sizeof(float) * (size_t)nsplit);
   float *l = (float *)malloc(sizeof(float) * (size_t)nsplit);
@@ -601,33 +611,34 @@ void orc_attn(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, uint16_
   for (int h = 0; h < nh; h++) {
     const int g = h / grp;
     const uint16_t *qh = q + (size_t)h * hd;
-    for (int j = 0; j < nsplit; j++) {
+    for (int j = j0; j < nsplit; j++) {
       const int p0 = j * ORC_ATT_SPLIT;
       const int pn = npos - p0 < ORC_ATT_SPLIT ? npos - p0 : ORC_ATT_SPLIT;
+      const int i0 = lo > p0 ? lo - p0 : 0;   /* first visible slot */
       float mj = -INFINITY;
-      for (int i = 0; i < pn; i++) {
+      for (int i = i0; i < pn; i++) {
         const uint16_t *kr = Kc + ((size_t)(p0 + i) * nkv + g) * hd;
         float dot = 0.0f;
         for (int d = 0; d < hd; d++) dot = fmaf(orc_bf2f(qh[d]), orc_h2f(kr[d]), dot);
         sc[i] = dot * scale;
         if (sc[i] > mj) mj = sc[i];
       }
-      for (int i = 0; i < ORC_ATT_SPLIT; i++) e[i] = i < pn ? orc_expf(sc[i] - mj) : 0.0f;
+      for (int i = 0; i < ORC_ATT_SPLIT; i++) e[i] = i >= i0 && i < pn ? orc_expf(sc[i] - mj) : 0.0f;
       m[j] = mj;
       l[j] = orc_pairwise(e, ORC_ATT_SPLIT);
       for (int d = 0; d < hd; d++) {
         float acc = 0.0f;
-        for (int i = 0; i < pn; i++)
+        for (int i = i0; i < pn; i++)
           acc = fmaf(e[i], orc_h2f(Vc[((size_t)(p0 + i) * nkv + g) * hd + d]), acc);
         o[(size_t)j * hd + d] = acc;
       }
     }
     float M = -INFINITY;
-    for (int j = 0; j < nsplit; j++) if (m[j] > M) M = m[j];
+    for (int j = j0; j < nsplit; j++) if (m[j] > M) M = m[j];
     float L = 0.0f;
     float O[1024];
     for (int d = 0; d < hd; d++) O[d] = 0.0f;
-    for (int j = 0; j < nsplit; j++) {
+    for (int j = j0; j < nsplit; j++) {
       const float w = orc_expf(m[j] - M);
       L = fmaf(l[j], w, L);
       for (int d = 0; d < hd; d++) O[d] = fmaf(o[(size_t)j * hd + d], w, O[d]);
@@ -641,13 +652,14 @@ void orc_attn(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, uint16_
  * lfm3_nanode.cu:503-602, without its rounding steps): the referee for
  * orc_attn. out is fp32 [nh][hd]. */
 void orc_attn_twopass(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
-                      int npos, int nh, int nkv, int hd, float scale) {
+                      int npos, int nh, int nkv, int hd, float scale, int win) {
   const int grp = nh / nkv;
+  const int lo = (win > 0 && npos > win) ? npos - win : 0;
   double *s = (double *)malloc(sizeof(double) * (size_t)npos);
   for (int h = 0; h < nh; h++) {
     const int g = h / grp;
     double mx = -INFINITY;
-    for (int p = 0; p < npos; p++) {
+    for (int p = lo; p < npos; p++) {
       double dot = 0.0;
       for (int d = 0; d < hd; d++)
         dot += (double)orc_bf2f(q[(size_t)h * hd + d]) * (double)orc_h2f(Kc[((size_t)p * nkv + g) * hd + d]);
@@ -655,10 +667,10 @@ void orc_attn_twopass(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc,
       if (s[p] > mx) mx = s[p];
     }
     double sum = 0.0;
-    for (int p = 0; p < npos; p++) { s[p] = exp(s[p] - mx); sum += s[p]; }
+    for (int p = lo; p < npos; p++) { s[p] = exp(s[p] - mx); sum += s[p]; }
     for (int d = 0; d < hd; d++) {
       double acc = 0.0;
-      for (int p = 0; p < npos; p++) acc += s[p] * (double)orc_h2f(Vc[((size_t)p * nkv + g) * hd + d]);
+      for (int p = lo; p < npos; p++) acc += s[p] * (double)orc_h2f(Vc[((size_t)p * nkv + g) * hd + d]);
       out[(size_t)h * hd + d] = (float)(acc / sum);
     }
   }

@@ -10,6 +10,8 @@
  * Attention: fused [q | k | v | gate] GEMV (gate = one value per q head), per-head
  * q/k RMSNorm, zero-tail partial RoPE, KV write, attention, sigmoid gate, o_proj.
  * Conv: in_proj [B | C | x] GEMV, gated short conv, out_proj.
+ * Sliding-window attention layers (slide_mask) use their own RoPE table
+ * (slide_theta, slide_rot) and see only the last slide_win keys.
  * After the last layer: embedding_norm -> tied LM head (fp32 logits) -> argmax
  * (lfm3_nanode.cu:6183, 5171-5179, 6229).
  *
@@ -39,7 +41,7 @@ typedef struct {
 } q8t;
 
 typedef struct {
-  int attn;
+  int attn, slide;       /* slide: a sliding-window attention layer */
   q8t in, out, ug, down;
   float *op_norm, *post_op_norm, *ffn_norm, *post_ffn_norm, *q_norm, *k_norm, *taps;
   uint16_t *kc, *vc;    /* fp16 [ctx][nkv][hd] */
@@ -51,7 +53,7 @@ struct orc_model {
   layer_t *L;
   q8t emb;
   float *final_norm;
-  float *rope;
+  float *rope, *rope_slide;   /* cos/sin tables: full-attention and sliding layers */
   int pos;
   uint16_t *last_hidden;
 };
@@ -84,6 +86,7 @@ orc_model *orc_model_create(const orc_cfg *cfg) {
     layer_t *L = &m->L[l];
     const int t0 = 16 * l;
     L->attn = (int)((c->attn_mask >> l) & 1u);
+    L->slide = L->attn && ((c->slide_mask >> l) & 1u);
     if (L->attn) {
       q8_make(&L->in, c, t0 + 0, qd + 2 * kvd + c->nh, H);
       q8_make(&L->out, c, t0 + 1, H, qd);
@@ -108,6 +111,10 @@ orc_model *orc_model_create(const orc_cfg *cfg) {
   m->final_norm = vec_make(c, 4001, H, 1.0f, 0.1f);
   m->rope = (float *)malloc(sizeof(float) * (size_t)c->ctx * (c->rot / 2) * 2 + 8);
   orc_rope_table(m->rope, c->ctx, c->hd, c->rot, c->theta);
+  if (c->slide_mask) {
+    m->rope_slide = (float *)malloc(sizeof(float) * (size_t)c->ctx * (c->slide_rot / 2) * 2 + 8);
+    orc_rope_table(m->rope_slide, c->ctx, c->hd, c->slide_rot, c->slide_theta);
+  }
   m->last_hidden = (uint16_t *)calloc((size_t)H, 2);
   m->pos = 0;
   return m;
@@ -139,7 +146,7 @@ void orc_model_free(orc_model *m) {
   }
   free(m->L);
   q8_free(&m->emb);
-  free(m->final_norm); free(m->rope); free(m->last_hidden);
+  free(m->final_norm); free(m->rope); free(m->rope_slide); free(m->last_hidden);
   free(m);
 }
 
@@ -234,14 +241,20 @@ int orc_model_feed(orc_model *m, const int32_t *tok, int T, float *logits_out) {
         const int pos = m->pos + t;
         orc_headnorm(q, L->q_norm, c->nh, c->hd, c->eps);
         orc_headnorm(k, L->k_norm, c->nkv, c->hd, c->eps);
-        orc_rope(q, m->rope, pos, c->nh, c->hd, c->rot);
-        orc_rope(k, m->rope, pos, c->nkv, c->hd, c->rot);
+        /* per layer type (lfm3_nanode.cu:3756-3765, 5416-5422, 5486-5487): full
+         * attention rotates rot dims with theta; sliding attention its own
+         * rot (all of hd) with its own base and sees a window of keys */
+        const float *rt = L->slide ? m->rope_slide : m->rope;
+        const int rot = L->slide ? c->slide_rot : c->rot;
+        orc_rope(q, rt, pos, c->nh, c->hd, rot);
+        orc_rope(k, rt, pos, c->nkv, c->hd, rot);
         for (int i = 0; i < kvd; i++) {
           L->kc[(size_t)pos * kvd + i] = orc_f2h(orc_bf2f(k[i]));
           L->vc[(size_t)pos * kvd + i] = orc_f2h(orc_bf2f(v[i]));
         }
         uint16_t *a = H2 + (size_t)t * qd;
-        orc_attn(q, L->kc, L->vc, a, pos + 1, c->nh, c->nkv, c->hd, 1.0f / sqrtf((float)c->hd));
+        orc_attn(q, L->kc, L->vc, a, pos + 1, c->nh, c->nkv, c->hd, 1.0f / sqrtf((float)c->hd),
+                 L->slide ? c->slide_win : 0);
         orc_sigmoid_gate(g, a, c->nh, c->hd);
       }
       gemm_bf16(&L->out, H2, H1, T, yf, qx, dx);               /* [T][H] */

@@ -3,8 +3,9 @@
 // Positions are cut into splits of 64; pass 1 computes, per (kv head, split,
 // query), the G = nh/nkv heads' partial softmax state, pass 2 merges the
 // splits of each head in ascending order and applies the per-head sigmoid
-// gate (optionally emitting the Q8_0 input of o_proj). Order (the same on the
-// host side):
+// gate (optionally emitting the Q8_0 input of o_proj). head_dim 64 or 128; a
+// sliding-window layer (win > 0) sees keys [npos - win, npos) once npos > win.
+// Order (the same on the host side):
 //   dot_p = fmaf chain over d ascending of q_d * f16(k_pd), s_p = fl(dot_p * scale)
 //   split j: m_j = max s_p, e_p = expf(fl(s_p - m_j)), l_j = pairwise sum of the
 //            64 slots (zero past npos), o_jd = fmaf chain over p ascending of e_p * v_pd
@@ -19,35 +20,45 @@
 namespace pq {
 
 constexpr int kSplit = 64;
-constexpr int kHD = 64;
-constexpr int kPart = kHD + 2;  // o[64], m, l
+
+// Keys a query at npos - 1 sees: [lo, npos), lo = npos - win for a sliding
+// layer whose window the context has outgrown (k_attn_head, lfm3_nanode.cu:515).
+__device__ __forceinline__ int window_lo(int npos, int win) { return (win > 0 && npos > win) ? npos - win : 0; }
 
 // One wave per (kv head g, split j, query t); lane p = position 64j + p for the
-// scores, lane d = dimension d for the value sums; the G heads of the group
-// share every K and V load.
-template <int G>
+// scores, lane l = dimensions l + 64e (e < HD/64) for the value sums; the G
+// heads of the group share every K and V load. Splits with no key in the
+// window write nothing (the merge starts at the window's first split); the
+// slots before lo are absent (no score, e = 0, skipped in the value chain).
+template <int G, int HD>
 __global__ __launch_bounds__(64) void attn_split_kernel(const uint16_t *__restrict__ q, int q_stride,
                                                          const uint16_t *__restrict__ kc,
                                                          const uint16_t *__restrict__ vc, float *__restrict__ part,
-                                                         int pos0, int nh, int nkv, int nsplit_max, float scale) {
-  __shared__ __align__(16) float qs[G][kHD];
+                                                         int pos0, int nh, int nkv, int nsplit_max, float scale,
+                                                         int win) {
+  constexpr int E = HD / 64, PART = HD + 2;
+  __shared__ __align__(16) float qs[G][HD];
   __shared__ float es[G][kSplit];
   const int g = blockIdx.x, j = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
   const int npos = pos0 + t + 1;
+  const int lo = window_lo(npos, win);
   const int p0 = j * kSplit;
-  if (p0 >= npos) return;
+  if (p0 >= npos || p0 + kSplit <= lo) return;
   const int pn = npos - p0 < kSplit ? npos - p0 : kSplit;
-  const int kvd = nkv * kHD;
+  const int i0 = lo > p0 ? lo - p0 : 0;
+  const int kvd = nkv * HD;
 #pragma unroll
-  for (int h = 0; h < G; h++) qs[h][lane] = bf2f(q[(size_t)t * q_stride + (g * G + h) * kHD + lane]);
+  for (int h = 0; h < G; h++)
+#pragma unroll
+    for (int e = 0; e < E; e++) qs[h][lane + 64 * e] = bf2f(q[(size_t)t * q_stride + (g * G + h) * HD + lane + 64 * e]);
   __syncthreads();
-  const bool valid = lane < pn;
+  const bool valid = lane >= i0 && lane < pn;
   float dot[G];
 #pragma unroll
   for (int h = 0; h < G; h++) dot[h] = 0.0f;
   if (valid) {
-    const uint16_t *kr = kc + (size_t)(p0 + lane) * kvd + g * kHD;
-    for (int d0 = 0; d0 < kHD; d0 += 8) {
+    const uint16_t *kr = kc + (size_t)(p0 + lane) * kvd + g * HD;
+    for (int d0 = 0; d0 < HD; d0 += 8) {
       const uint4 k8 = *reinterpret_cast<const uint4 *>(kr + d0);
       const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
 #pragma unroll
@@ -61,68 +72,83 @@ __global__ __launch_bounds__(64) void attn_split_kernel(const uint16_t *__restri
   float m[G], l[G];
 #pragma unroll
   for (int h = 0; h < G; h++) {
-    const float s = valid ? dot[h] * scale : -__builtin_inff();
-    m[h] = wave_max(s);
-    const float e = valid ? expf_pq(s - m[h]) : 0.0f;
+    const float sc = valid ? dot[h] * scale : -__builtin_inff();
+    m[h] = wave_max(sc);
+    const float e = valid ? expf_pq(sc - m[h]) : 0.0f;
     l[h] = wave_pairwise_sum(e);
     es[h][lane] = e;
   }
   __syncthreads();
-  float o[G];
+  float o[G][E];
 #pragma unroll
-  for (int h = 0; h < G; h++) o[h] = 0.0f;
-  for (int p = 0; p < pn; p++) {
-    const float v = h2f(vc[(size_t)(p0 + p) * kvd + g * kHD + lane]);
+  for (int h = 0; h < G; h++)
 #pragma unroll
-    for (int h = 0; h < G; h++) o[h] = __builtin_fmaf(es[h][p], v, o[h]);
+    for (int e = 0; e < E; e++) o[h][e] = 0.0f;
+  for (int p = i0; p < pn; p++) {
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      const float v = h2f(vc[(size_t)(p0 + p) * kvd + g * HD + lane + 64 * e]);
+#pragma unroll
+      for (int h = 0; h < G; h++) o[h][e] = __builtin_fmaf(es[h][p], v, o[h][e]);
+    }
   }
 #pragma unroll
   for (int h = 0; h < G; h++) {
-    float *pp = part + (((size_t)t * nh + g * G + h) * nsplit_max + j) * kPart;
-    pp[lane] = o[h];
+    float *pp = part + (((size_t)t * nh + g * G + h) * nsplit_max + j) * PART;
+#pragma unroll
+    for (int e = 0; e < E; e++) pp[lane + 64 * e] = o[h][e];
     if (lane == 0) {
-      pp[kHD] = m[h];
-      pp[kHD + 1] = l[h];
+      pp[HD] = m[h];
+      pp[HD + 1] = l[h];
     }
   }
 }
 
-// One wave per (head, query); lane d = dimension d.
+// One wave per (head, query); lane l = dimensions l + 64e. The window's
+// splits merge in ascending order.
+template <int HD>
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ part, int pos0, int nh,
                                                          int nsplit_max, const uint16_t *__restrict__ gate,
                                                          int gate_stride, uint16_t *__restrict__ out, int out_stride,
-                                                         int8_t *__restrict__ qx, float *__restrict__ dx) {
+                                                         int8_t *__restrict__ qx, float *__restrict__ dx, int win) {
+  constexpr int E = HD / 64, PART = HD + 2;
   const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
   const int npos = pos0 + t + 1;
+  const int j0 = window_lo(npos, win) / kSplit;
   const int ns = (npos + kSplit - 1) / kSplit;
-  const float *pp = part + ((size_t)t * nh + h) * nsplit_max * kPart;
+  const float *pp = part + ((size_t)t * nh + h) * nsplit_max * PART;
   float M = -__builtin_inff();
-  for (int j = 0; j < ns; j++) M = fmaxf(M, pp[j * kPart + kHD]);
-  float L = 0.0f, O = 0.0f;
-  for (int j = 0; j < ns; j++) {
-    const float w = expf_pq(pp[j * kPart + kHD] - M);
-    L = __builtin_fmaf(pp[j * kPart + kHD + 1], w, L);
-    O = __builtin_fmaf(pp[j * kPart + d], w, O);
-  }
-  uint16_t r = f2bf(O / L);
-  if (gate != nullptr) {
-    const float s = 1.0f / (1.0f + expf_pq(-bf2f(gate[(size_t)t * gate_stride + h])));
-    r = f2bf(bf2f(r) * s);
-  }
-  if (out != nullptr) out[(size_t)t * out_stride + h * kHD + d] = r;
-  if (qx != nullptr) {
-    const float v = bf2f(r);
-    float a = fabsf(v);
+  for (int j = j0; j < ns; j++) M = fmaxf(M, pp[j * PART + HD]);
+  float L = 0.0f, O[E];
 #pragma unroll
-    for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-    const float dq = a / 127.0f;
-    // d = 0 only when every |x| of the block is below 127 * 2^-149: dividing
-    // by 1 then gives q = 0 as the zero-block rule does, with no branch
-    int qv = (int)__builtin_rintf(v / (dq != 0.0f ? dq : 1.0f));
-    qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
-    const size_t K = (size_t)nh * kHD;
-    qx[(size_t)t * K + h * kHD + d] = (int8_t)qv;
-    if ((d & 31) == 0) dx[(size_t)t * (K / 32) + (h * kHD + d) / 32] = dq;
+  for (int e = 0; e < E; e++) O[e] = 0.0f;
+  for (int j = j0; j < ns; j++) {
+    const float w = expf_pq(pp[j * PART + HD] - M);
+    L = __builtin_fmaf(pp[j * PART + HD + 1], w, L);
+#pragma unroll
+    for (int e = 0; e < E; e++) O[e] = __builtin_fmaf(pp[j * PART + d + 64 * e], w, O[e]);
+  }
+  const float gs = gate != nullptr ? 1.0f / (1.0f + expf_pq(-bf2f(gate[(size_t)t * gate_stride + h]))) : 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    uint16_t r = f2bf(O[e] / L);
+    if (gate != nullptr) r = f2bf(bf2f(r) * gs);
+    const int dd = d + 64 * e;
+    if (out != nullptr) out[(size_t)t * out_stride + h * HD + dd] = r;
+    if (qx != nullptr) {
+      const float v = bf2f(r);
+      float a = fabsf(v);
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+      const float dq = a / 127.0f;
+      // d = 0 only when every |x| of the block is below 127 * 2^-149: dividing
+      // by 1 then gives q = 0 as the zero-block rule does, with no branch
+      int qv = (int)__builtin_rintf(v / (dq != 0.0f ? dq : 1.0f));
+      qv = qv > 127 ? 127 : (qv < -127 ? -127 : qv);
+      const size_t K = (size_t)nh * HD;
+      qx[(size_t)t * K + h * HD + dd] = (int8_t)qv;
+      if ((d & 31) == 0) dx[(size_t)t * (K / 32) + (h * HD + dd) / 32] = dq;
+    }
   }
 }
 
@@ -130,40 +156,52 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict_
 
 using namespace pq;
 
-extern "C" size_t pq_attn_workspace_bytes(int nh, int max_pos, int T) {
-  if (nh <= 0 || max_pos <= 0 || T <= 0) return 0;
+extern "C" size_t pq_attn_workspace_bytes(int nh, int hd, int max_pos, int T) {
+  if (nh <= 0 || (hd != 64 && hd != 128) || max_pos <= 0 || T <= 0) return 0;
   const size_t ns = (size_t)(max_pos + kSplit - 1) / kSplit;
-  return (size_t)T * nh * ns * kPart * sizeof(float);
+  return (size_t)T * nh * ns * (hd + 2) * sizeof(float);
 }
 
-extern "C" int pq_attn_decode(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
-                              const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int8_t *qx,
-                              float *dx, int pos0, int nh, int nkv, int hd, int T, float scale, void *ws,
-                              size_t ws_bytes, void *stream) {
-  PQ_REQUIRE(q && kcache && vcache && (out || qx) && (!qx || dx), PQ_ERR_ARG, "pq_attn_decode: null pointer");
-  PQ_REQUIRE(hd == kHD, PQ_ERR_ARG, "pq_attn_decode: head_dim %d (this build: 64)", hd);
-  PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && T > 0 && pos0 >= 0, PQ_ERR_ARG,
-             "pq_attn_decode: nh=%d nkv=%d T=%d pos0=%d", nh, nkv, T, pos0);
-  PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "pq_attn_decode: KV cache must be 16-byte aligned");
-  const int max_pos = pos0 + T;
-  const int nsplit = (max_pos + kSplit - 1) / kSplit;
-  const size_t need = pq_attn_workspace_bytes(nh, max_pos, T);
-  PQ_REQUIRE(ws && ws_bytes >= need, PQ_ERR_WORKSPACE, "pq_attn_decode: workspace of %zu bytes needed (got %zu)", need,
-             ws_bytes);
-  hipStream_t st = as_stream(stream);
+template <int HD>
+static int attn_launch(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                       const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int8_t *qx, float *dx,
+                       int pos0, int nh, int nkv, int T, float scale, int win, float *part, int nsplit,
+                       hipStream_t st) {
   const int G = nh / nkv;
   const dim3 g1(nkv, nsplit, T), b1(64);
-  float *part = reinterpret_cast<float *>(ws);
   switch (G) {
-    case 1: launch(attn_split_kernel<1>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale); break;
-    case 2: launch(attn_split_kernel<2>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale); break;
-    case 4: launch(attn_split_kernel<4>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale); break;
-    case 8: launch(attn_split_kernel<8>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale); break;
+    case 1: launch(attn_split_kernel<1, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
+    case 2: launch(attn_split_kernel<2, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
+    case 4: launch(attn_split_kernel<4, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
+    case 8: launch(attn_split_kernel<8, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
     default: return fail(PQ_ERR_ARG, "pq_attn_decode: %d q heads per kv head (1, 2, 4 or 8)", G);
   }
   int rc = check_launch("pq_attn_decode split");
   if (rc) return rc;
-  launch(attn_merge_kernel, dim3(nh, T), dim3(64), 0, st, part, pos0, nh, nsplit, gate, gate_stride, out, out_stride,
-         qx, dx);
+  launch(attn_merge_kernel<HD>, dim3(nh, T), dim3(64), 0, st, part, pos0, nh, nsplit, gate, gate_stride, out,
+         out_stride, qx, dx, win);
   return check_launch("pq_attn_decode merge");
+}
+
+extern "C" int pq_attn_decode(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                              const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int8_t *qx,
+                              float *dx, int pos0, int nh, int nkv, int hd, int T, float scale, int win, void *ws,
+                              size_t ws_bytes, void *stream) {
+  PQ_REQUIRE(q && kcache && vcache && (out || qx) && (!qx || dx), PQ_ERR_ARG, "pq_attn_decode: null pointer");
+  PQ_REQUIRE(hd == 64 || hd == 128, PQ_ERR_ARG, "pq_attn_decode: head_dim %d (64 or 128)", hd);
+  PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && T > 0 && pos0 >= 0 && win >= 0, PQ_ERR_ARG,
+             "pq_attn_decode: nh=%d nkv=%d T=%d pos0=%d win=%d", nh, nkv, T, pos0, win);
+  PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "pq_attn_decode: KV cache must be 16-byte aligned");
+  const int max_pos = pos0 + T;
+  const int nsplit = (max_pos + kSplit - 1) / kSplit;
+  const size_t need = pq_attn_workspace_bytes(nh, hd, max_pos, T);
+  PQ_REQUIRE(ws && ws_bytes >= need, PQ_ERR_WORKSPACE, "pq_attn_decode: workspace of %zu bytes needed (got %zu)", need,
+             ws_bytes);
+  float *part = reinterpret_cast<float *>(ws);
+  hipStream_t st = as_stream(stream);
+  if (hd == 64)
+    return attn_launch<64>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, pos0, nh, nkv, T,
+                           scale, win, part, nsplit, st);
+  return attn_launch<128>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, pos0, nh, nkv, T,
+                          scale, win, part, nsplit, st);
 }

@@ -42,7 +42,7 @@ struct Q8Dev {
 };
 
 struct LayerDev {
-  int attn = 0;
+  int attn = 0, slide = 0;   // slide: sliding-window attention (its own RoPE table, rot and window)
   Q8Dev in, out, ug, down;
   float *op_norm = nullptr, *post_op_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
   float *q_norm = nullptr, *k_norm = nullptr, *taps = nullptr;
@@ -57,7 +57,7 @@ struct Engine {
   hipStream_t st = nullptr;
   std::vector<LayerDev> L;
   Q8Dev emb;
-  float *final_norm = nullptr, *rope = nullptr;
+  float *final_norm = nullptr, *rope = nullptr, *rope_slide = nullptr;
   int pos = 0, tmax = 0, qd = 0, kvd = 0, nin = 0, last_t = 1;
   bool fused = false;             // T=1 steps through the fused kernels (when supported)
   bool graph = true;              // fused steps replay as captured HIP graphs
@@ -139,6 +139,7 @@ static int create(Engine &E, const pq_model_cfg &c) {
   for (int l = 0; l < c.nlayers; l++) {
     LayerDev &D = E.L[l];
     D.attn = (int)((c.attn_mask >> l) & 1u);
+    D.slide = D.attn && ((c.slide_mask >> l) & 1u);
     if (D.attn) {
       PQ_TRY(alloc_q8(E, D.in, E.nin, H));
       PQ_TRY(alloc_q8(E, D.out, H, E.qd));
@@ -164,6 +165,7 @@ static int create(Engine &E, const pq_model_cfg &c) {
   PQ_TRY(alloc_q8(E, E.emb, c.vocab, H));
   PQ_TRY(E.dalloc(&E.final_norm, H));
   PQ_TRY(E.dalloc(&E.rope, (size_t)c.ctx * (c.rot / 2) * 2 + 2));
+  if (c.slide_mask) PQ_TRY(E.dalloc(&E.rope_slide, (size_t)c.ctx * (c.slide_rot / 2) * 2 + 2));
   const int T = E.tmax;
   const int wide = std::max(std::max(3 * H, 2 * F), E.nin);
   const int kmax = std::max(std::max(H, F), E.qd);
@@ -187,7 +189,7 @@ static int create(Engine &E, const pq_model_cfg &c) {
   E.max_ids = c.ctx + 1;
   PQ_TRY(E.dalloc(&E.ids, (size_t)E.max_ids));
   PQ_TRY(E.dalloc(&E.ctr, 2));
-  E.attn_ws_bytes = pq_attn_workspace_bytes(c.nh, c.ctx, T);
+  E.attn_ws_bytes = pq_attn_workspace_bytes(c.nh, c.hd, c.ctx, T);
   PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.attn_ws), E.attn_ws_bytes));
   // the split-K GEMM workspace: the largest of the layer shapes at tmax positions
   const int shapes[6][2] = {{E.nin, H}, {3 * H, H}, {H, E.qd}, {H, H}, {2 * F, H}, {H, F}};
@@ -398,11 +400,22 @@ static int load_synthetic(Engine &E) {
   return PQ_OK;
 }
 
+// One table per attention layer type: full attention (theta, rot) and, with
+// sliding layers, their own (slide_theta, slide_rot) -- the reference's
+// invf_full / invf_slide (lfm3_nanode.cu:5486-5487).
 static int upload_rope(Engine &E) {
   std::vector<float> cs;
   rope_table(cs, E.c.ctx, E.c.hd, E.c.rot, E.c.theta);
-  return upload_f32(E, E.rope, cs.data(), cs.size());
+  PQ_TRY(upload_f32(E, E.rope, cs.data(), cs.size()));
+  if (!E.rope_slide) return PQ_OK;
+  rope_table(cs, E.c.ctx, E.c.hd, E.c.slide_rot, E.c.slide_theta);
+  return upload_f32(E, E.rope_slide, cs.data(), cs.size());
 }
+
+// The attention layer's RoPE table, rotated dims and window.
+static const float *layer_rope(const Engine &E, const LayerDev &D) { return D.slide ? E.rope_slide : E.rope; }
+static int layer_rot(const Engine &E, const LayerDev &D) { return D.slide ? E.c.slide_rot : E.c.rot; }
+static int layer_win(const Engine &E, const LayerDev &D) { return D.slide ? E.c.slide_win : 0; }
 
 // Zero KV caches and conv rings with a kernel-free copy of a zero host buffer
 // (allocated once per reset; reset is not on the decode path).
@@ -463,10 +476,10 @@ static int forward(Engine &E, const int32_t *toks, int n, int32_t *next) {
       float *din = E.din + (size_t)c0 * (H / 32);
       PQ_TRY(gemm_T(E, D.in, qin, din, E.Wd, T));
       if (D.attn) {
-        PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, pos0, c.nh, c.nkv, c.hd, c.rot, T,
-                          c.eps, E.st));
+        PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pos0, c.nh, c.nkv, c.hd,
+                          layer_rot(E, D), T, c.eps, E.st));
         PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, nullptr, 0, E.qx, E.dx, pos0,
-                              c.nh, c.nkv, c.hd, T, scale, E.attn_ws, E.attn_ws_bytes, E.st));
+                              c.nh, c.nkv, c.hd, T, scale, layer_win(E, D), E.attn_ws, E.attn_ws_bytes, E.st));
       } else {
         PQ_TRY(pq_conv(D.ring(), D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
         PQ_TRY(pq_q8_quant_bf16(E.A, E.qx, E.dx, H, T, E.st));
@@ -514,10 +527,10 @@ static int forward_r2(Engine &E, const int32_t *toks, int n, int32_t *next) {
       uint16_t *xin = E.xin + (size_t)c0 * H;
       PQ_TRY(gemm_r2(E, D.in, xin, E.Wd, PQ_DTYPE_BF16, T));
       if (D.attn) {
-        PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, pos0, c.nh, c.nkv, c.hd, c.rot, T,
-                          c.eps, E.st));
+        PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pos0, c.nh, c.nkv, c.hd,
+                          layer_rot(E, D), T, c.eps, E.st));
         PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr, nullptr,
-                              pos0, c.nh, c.nkv, c.hd, T, scale, E.attn_ws, E.attn_ws_bytes, E.st));
+                              pos0, c.nh, c.nkv, c.hd, T, scale, layer_win(E, D), E.attn_ws, E.attn_ws_bytes, E.st));
       } else {
         PQ_TRY(pq_conv(D.ring(), D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
       }
@@ -554,6 +567,7 @@ static bool fused_supported(const pq_model_cfg &c, const char **why) {
   if (c.numerics == PQ_NUMERICS_REF) *why = "the reference-numerics mode runs unfused steps";
   else if (!pow2(c.hidden) || !pow2(c.ffn)) *why = "hidden and ffn must be powers of two in 1024..8192";
   else if (conv && c.ntaps != 3) *why = "the fused conv prologue takes 3 taps";
+  else if (attn && c.slide_mask) *why = "the fused attention mixer has no sliding window";
   else if (attn) {
     const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
     const size_t ns = ((size_t)c.ctx + 63) / 64;
@@ -737,13 +751,18 @@ extern "C" void *pq_engine_create(const pq_model_cfg *cfg) {
   if (!cfg) { fail(PQ_ERR_ARG, "pq_engine_create: null config"); return nullptr; }
   const pq_model_cfg &c = *cfg;
   const bool ok = c.hidden >= 256 && (c.hidden & (c.hidden - 1)) == 0 && c.hidden <= 8192 && c.ffn % 256 == 0 &&
-                  c.ffn > 0 && c.vocab > 0 && c.nlayers > 0 && c.nlayers <= 32 && c.hd == 64 && c.nkv > 0 &&
+                  c.ffn > 0 && c.vocab > 0 && c.nlayers > 0 && c.nlayers <= 32 && (c.hd == 64 || c.hd == 128) &&
+                  c.nkv > 0 &&
                   c.nh % c.nkv == 0 && c.nh * c.hd % 64 == 0 && c.rot >= 0 && c.rot <= c.hd && c.rot % 2 == 0 &&
                   (c.ntaps == 2 || c.ntaps == 3 || c.ntaps == 4 || c.ntaps == 7) && c.ctx > 0 &&
                   c.prefill_chunk > 0 && c.prefill_chunk <= 512 &&
                   (c.numerics == PQ_NUMERICS_Q8 || c.numerics == PQ_NUMERICS_REF);
   if (!ok) { fail(PQ_ERR_ARG, "pq_engine_create: unsupported configuration"); return nullptr; }
-  if (c.slide_mask != 0) { fail(PQ_ERR_ARG, "pq_engine_create: sliding-window layers are not supported"); return nullptr; }
+  if (c.slide_mask != 0 && ((c.slide_mask & ~c.attn_mask) != 0 || c.slide_win <= 0 || c.slide_rot < 0 ||
+                            c.slide_rot > c.hd || c.slide_rot % 2 != 0 || !(c.slide_theta > 0.0f))) {
+    fail(PQ_ERR_ARG, "pq_engine_create: sliding layers must be attention layers with a window, rot and theta");
+    return nullptr;
+  }
   auto E = std::make_unique<Engine>();
   if (create(*E, c) != PQ_OK) return nullptr;
   if (upload_rope(*E) != PQ_OK || reset(*E) != PQ_OK) return nullptr;
@@ -808,12 +827,31 @@ struct BlobTarget {
 // attention layer's input GEMV, w1 (gate) and w3 (up) into gate/up. The fp32
 // weight scales stay fp32 under PQ_NUMERICS_REF; under PQ_NUMERICS_Q8 they
 // must be fp16 values (a blob written from fp16 scales), else the load is
-// refused with a count of the scales fp16 cannot hold.
+// refused with a count of the scales fp16 cannot hold. The blob's layer_types
+// must match the engine's layer kinds.
 static int load_blob(Engine &E, void *blob) {
   const pq_model_cfg &c = E.c;
   const long long H = c.hidden, F = c.ffn;
-  PQ_REQUIRE(!strstr(pq_blob_config(blob), "\"sliding_attention\""), PQ_ERR_ARG,
-             "pq_engine_load_blob: the blob has sliding-window attention layers, which this engine does not run");
+  // the header's layer_types (conv / full_attention / sliding_attention, as
+  // the reference reads them, lfm3_nanode.cu:5404-5424) must be the engine's
+  {
+    const char *js = pq_blob_config(blob);
+    const char *lt = strstr(js, "\"layer_types\":[");
+    if (lt) {
+      const char *q = lt + strlen("\"layer_types\":[");
+      for (int l = 0; l < c.nlayers; l++) {
+        const char *a = strchr(q, '"');
+        const char *b = a ? strchr(a + 1, '"') : nullptr;
+        PQ_REQUIRE(a && b, PQ_ERR_ARG, "pq_engine_load_blob: layer_types has fewer than %d entries", c.nlayers);
+        const std::string ty(a + 1, b);
+        const LayerDev &D = E.L[l];
+        const char *want = !D.attn ? "conv" : D.slide ? "sliding_attention" : "full_attention";
+        PQ_REQUIRE(ty == want, PQ_ERR_ARG, "pq_engine_load_blob: layer %d is %s in the blob, %s in the engine", l,
+                   ty.c_str(), want);
+        q = b + 1;
+      }
+    }
+  }
   auto LN = [](int l, const char *suf) { return "lfm.model.layers." + std::to_string(l) + "." + suf; };
   std::vector<BlobTarget> T;
   T.push_back({-1, 0, true, {{"lfm.model.embed_tokens.weight", c.vocab, H}}});

@@ -113,45 +113,72 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ x, 
 }
 
 // ------------------------------------------------- q/k norm, RoPE, KV write
-// One wave per (head, position); lane d holds dimension d (hd == 64). Heads
-// [0, nh) are q (norm + rope, in place), [nh, nh+nkv) k (norm + rope, then
-// written to the fp16 cache), [nh+nkv, nh+2nkv) v (written to the cache).
+// One wave per (head, position); lane l holds dimensions l + 64e, e < HD/64
+// (HD = 64 or 128). Heads [0, nh) are q (norm + rope, in place), [nh, nh+nkv)
+// k (norm + rope, then written to the fp16 cache), [nh+nkv, nh+2nkv) v
+// (written to the cache). The sum of squares is the pairwise tree over the
+// head in natural order: the wave's pairwise sum of each 64-dim slice, the
+// slices added pairwise. RoPE pairs (i, i + HD/2) for i < rot/2 (k_rope,
+// lfm3_nanode.cu:483-498): a lane-pair exchange at HD = 64, the lane's own two
+// values at HD = 128. cs is the layer's [pos][rot/2][cos, sin] table.
+template <int HD>
 __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv, int row_stride,
                                                       const float *__restrict__ qn, const float *__restrict__ kn,
                                                       const float *__restrict__ cs, uint16_t *__restrict__ kc,
                                                       uint16_t *__restrict__ vc, int pos0, int nh, int nkv, int rot,
                                                       float eps) {
-  constexpr int hd = 64;
-  const int head = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  constexpr int E = HD / 64;
+  const int head = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
   const int pos = pos0 + t;
   uint16_t *row = qkv + (size_t)t * row_stride;
-  const int kvd = nkv * hd;
+  const int kvd = nkv * HD;
   if (head >= nh + nkv) {  // v: straight to the cache
     const int g = head - nh - nkv;
-    vc[(size_t)pos * kvd + g * hd + d] = f2h(bf2f(row[nh * hd + kvd + g * hd + d]));
+#pragma unroll
+    for (int e = 0; e < E; e++)
+      vc[(size_t)pos * kvd + g * HD + l + 64 * e] = f2h(bf2f(row[nh * HD + kvd + g * HD + l + 64 * e]));
     return;
   }
   const bool isq = head < nh;
-  uint16_t *xr = isq ? row + head * hd : row + nh * hd + (head - nh) * hd;
+  uint16_t *xr = isq ? row + head * HD : row + nh * HD + (head - nh) * HD;
   const float *w = isq ? qn : kn;
-  const float x = bf2f(xr[d]);
-  const float ss = wave_pairwise_sum(x * x);
-  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)hd) + eps);
-  float v = bf2f(f2bf(w[d] * bf2f(f2bf(x * rs))));
-  const int half = rot / 2;
-  const float up = __shfl_down(v, hd / 2, 64);     // partner for d < hd/2
-  const float dn = __shfl_up(v, hd / 2, 64);       // partner for d >= hd/2
-  if (d < hd / 2 && d < half) {
-    const float c = cs[((size_t)pos * half + d) * 2], s = cs[((size_t)pos * half + d) * 2 + 1];
-    v = v * c - up * s;
-  } else if (d >= hd / 2 && d - hd / 2 < half) {
-    const int i = d - hd / 2;
-    const float c = cs[((size_t)pos * half + i) * 2], s = cs[((size_t)pos * half + i) * 2 + 1];
-    v = v * c + dn * s;
+  float x[E], v[E];
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    x[e] = bf2f(xr[l + 64 * e]);
+    const float part = wave_pairwise_sum(x[e] * x[e]);
+    ss = e == 0 ? part : ss + part;
   }
-  const uint16_t vb = f2bf(v);
-  if (isq) xr[d] = vb;
-  else kc[(size_t)pos * kvd + (head - nh) * hd + d] = f2h(bf2f(vb));
+  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)HD) + eps);
+#pragma unroll
+  for (int e = 0; e < E; e++) v[e] = bf2f(f2bf(w[l + 64 * e] * bf2f(f2bf(x[e] * rs))));
+  const int half = rot / 2;
+  float r[E];
+  if constexpr (HD == 64) {
+    const float up = __shfl_down(v[0], 32, 64);     // partner for d < 32
+    const float dn = __shfl_up(v[0], 32, 64);       // partner for d >= 32
+    const int i = l & 31;
+    r[0] = v[0];
+    if (i < half) {
+      const float c = cs[((size_t)pos * half + i) * 2], sn = cs[((size_t)pos * half + i) * 2 + 1];
+      r[0] = l < 32 ? v[0] * c - up * sn : v[0] * c + dn * sn;
+    }
+  } else {   // HD = 128: the pair (l, l + 64) is the lane's own
+    r[0] = v[0];
+    r[1] = v[1];
+    if (l < half) {
+      const float c = cs[((size_t)pos * half + l) * 2], sn = cs[((size_t)pos * half + l) * 2 + 1];
+      r[0] = v[0] * c - v[1] * sn;
+      r[1] = v[1] * c + v[0] * sn;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    const uint16_t vb = f2bf(r[e]);
+    if (isq) xr[l + 64 * e] = vb;
+    else kc[(size_t)pos * kvd + (head - nh) * HD + l + 64 * e] = f2h(bf2f(vb));
+  }
 }
 
 // ------------------------------------------------------------ short conv
@@ -338,12 +365,16 @@ extern "C" int pq_qk_prep(uint16_t *qkv, int row_stride, const float *q_norm, co
                           uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv, int hd, int rot, int T,
                           float eps, void *stream) {
   PQ_REQUIRE(qkv && q_norm && k_norm && rope_cs && kcache && vcache, PQ_ERR_ARG, "pq_qk_prep: null pointer");
-  PQ_REQUIRE(hd == 64, PQ_ERR_ARG, "pq_qk_prep: head_dim %d (this build: 64)", hd);
+  PQ_REQUIRE(hd == 64 || hd == 128, PQ_ERR_ARG, "pq_qk_prep: head_dim %d (64 or 128)", hd);
   PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && rot >= 0 && rot <= hd && rot % 2 == 0 && T > 0 && pos0 >= 0,
              PQ_ERR_ARG, "pq_qk_prep: nh=%d nkv=%d rot=%d T=%d pos0=%d", nh, nkv, rot, T, pos0);
   PQ_REQUIRE(row_stride >= (nh + 2 * nkv) * hd, PQ_ERR_ARG, "pq_qk_prep: row stride %d too small", row_stride);
-  launch(qk_prep_kernel, dim3(nh + 2 * nkv, T), dim3(64), 0, as_stream(stream), qkv, row_stride, q_norm, k_norm,
-         rope_cs, kcache, vcache, pos0, nh, nkv, rot, eps);
+  if (hd == 64)
+    launch(qk_prep_kernel<64>, dim3(nh + 2 * nkv, T), dim3(64), 0, as_stream(stream), qkv, row_stride, q_norm, k_norm,
+           rope_cs, kcache, vcache, pos0, nh, nkv, rot, eps);
+  else
+    launch(qk_prep_kernel<128>, dim3(nh + 2 * nkv, T), dim3(64), 0, as_stream(stream), qkv, row_stride, q_norm,
+           k_norm, rope_cs, kcache, vcache, pos0, nh, nkv, rot, eps);
   return check_launch("pq_qk_prep");
 }
 

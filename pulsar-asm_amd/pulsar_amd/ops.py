@@ -185,15 +185,15 @@ def qk_prep(qkv, row_stride, q_norm, k_norm, rope_cs, kc, vc, pos0, nh, nkv, hd,
 
 
 def attn_decode(q, q_stride, kc, vc, pos0, nh, nkv, hd, T, scale, gate=None, gate_stride=0, out=None,
-                out_stride=0, qx=None, dx=None, ws=None):
+                out_stride=0, qx=None, dx=None, ws=None, win=0):
     L = lib()
-    need = L.pq_attn_workspace_bytes(nh, pos0 + T, T)
+    need = L.pq_attn_workspace_bytes(nh, hd, pos0 + T, T)
     if ws is None:
         ws = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
     check(L.pq_attn_decode(_bits16(q), q_stride, _bits16(kc), _bits16(vc),
                            _bits16(gate) if gate is not None else None, gate_stride,
                            _bits16(out) if out is not None else None, out_stride, _ptr(qx), _ptr(dx), pos0, nh, nkv,
-                           hd, T, scale, ws.data_ptr(), ws.numel(), stream_ptr()), "pq_attn_decode")
+                           hd, T, scale, win, ws.data_ptr(), ws.numel(), stream_ptr()), "pq_attn_decode")
 
 
 def conv(ring, taps, bcx, out, H, T, ntaps):

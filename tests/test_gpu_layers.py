@@ -55,10 +55,16 @@ def _qkv_case(orc, nh, nkv, hd, T, ctx, seed):
     return nin, rows, qn, kn, cs
 
 
-@pytest.mark.parametrize("pos0,T", [(0, 1), (77, 1), (100, 9), (2000, 3)])
-def test_qk_prep(orc, pq, dev, pos0, T):
-    nh, nkv, hd, ctx = 32, 8, 64, 2048
-    nin, rows, qn, kn, cs = _qkv_case(orc, nh, nkv, hd, T, ctx, SEED + pos0)
+@pytest.mark.parametrize("pos0,T,hd,rot,theta", [(0, 1, 64, 32, 1e6), (77, 1, 64, 32, 1e6), (100, 9, 64, 32, 1e6),
+                                                  (2000, 3, 64, 32, 1e6),
+                                                  # head_dim 128: full attention (half rotated, theta 1e6)
+                                                  # and sliding attention (all rotated, theta 1e4)
+                                                  (0, 1, 128, 64, 1e6), (300, 5, 128, 64, 1e6),
+                                                  (257, 3, 128, 128, 1e4), (4000, 2, 128, 128, 1e4)])
+def test_qk_prep(orc, pq, dev, pos0, T, hd, rot, theta):
+    nh, nkv, ctx = (32, 8, 2048) if hd == 64 else (16, 4, 4096)
+    nin, rows, qn, kn, _ = _qkv_case(orc, nh, nkv, hd, T, 2, SEED + pos0)
+    cs = orc.rope_table(ctx, hd, rot, theta)
     kvd = nkv * hd
     want_rows = rows.copy()
     kc_r = np.zeros((ctx, kvd), np.uint16)
@@ -67,8 +73,8 @@ def test_qk_prep(orc, pq, dev, pos0, T):
         r = want_rows[t]
         q = orc.headnorm(r[:nh * hd], qn, nh, hd)
         k = orc.headnorm(r[nh * hd:nh * hd + kvd], kn, nkv, hd)
-        q = orc.rope(q, cs, pos0 + t, nh, hd, 32)
-        k = orc.rope(k, cs, pos0 + t, nkv, hd, 32)
+        q = orc.rope(q, cs, pos0 + t, nh, hd, rot)
+        k = orc.rope(k, cs, pos0 + t, nkv, hd, rot)
         r[:nh * hd] = q
         kc_r[pos0 + t] = orc.bf2f(k).astype(np.float16).view(np.uint16)
         vc_r[pos0 + t] = orc.bf2f(r[nh * hd + kvd:nh * hd + 2 * kvd]).astype(np.float16).view(np.uint16)
@@ -76,16 +82,20 @@ def test_qk_prep(orc, pq, dev, pos0, T):
     kc = torch.zeros((ctx, kvd), dtype=torch.int16, device=dev)
     vc = torch.zeros((ctx, kvd), dtype=torch.int16, device=dev)
     pq.qk_prep(qkv, nin, torch.from_numpy(qn).to(dev), torch.from_numpy(kn).to(dev), torch.from_numpy(cs).to(dev),
-               kc, vc, pos0, nh, nkv, hd, 32, T)
+               kc, vc, pos0, nh, nkv, hd, rot, T)
     got = _u16(qkv)
     assert np.array_equal(got[:, :nh * hd], want_rows[:, :nh * hd])
     assert np.array_equal(_u16(kc), kc_r) and np.array_equal(_u16(vc), vc_r)
 
 
-@pytest.mark.parametrize("npos_last,T,nh,nkv", [(1, 1, 32, 8), (64, 1, 32, 8), (65, 1, 32, 8), (300, 1, 32, 8),
-                                                (2048, 1, 32, 8), (40, 33, 32, 8), (130, 7, 8, 8), (70, 2, 16, 2)])
-def test_attention(orc, pq, dev, npos_last, T, nh, nkv):
-    hd = 64
+@pytest.mark.parametrize("npos_last,T,nh,nkv,hd,win", [
+    (1, 1, 32, 8, 64, 0), (64, 1, 32, 8, 64, 0), (65, 1, 32, 8, 64, 0), (300, 1, 32, 8, 64, 0),
+    (2048, 1, 32, 8, 64, 0), (40, 33, 32, 8, 64, 0), (130, 7, 8, 8, 64, 0), (70, 2, 16, 2, 64, 0),
+    # head_dim 128 (16 q / 4 kv heads), full and sliding-window (256) layers
+    (1, 1, 16, 4, 128, 0), (300, 1, 16, 4, 128, 0), (129, 40, 16, 4, 128, 0),
+    (300, 1, 16, 4, 128, 256), (257, 1, 16, 4, 128, 256), (2000, 1, 16, 4, 128, 256),
+    (330, 90, 16, 4, 128, 256), (200, 20, 8, 8, 64, 100), (90, 5, 16, 4, 128, 1)])
+def test_attention(orc, pq, dev, npos_last, T, nh, nkv, hd, win):
     pos0 = npos_last - T
     kvd = nkv * hd
     q = orc.f2bf(orc.gen_normal(SEED + 9 * npos_last, T * nh * hd).reshape(T, nh * hd) * 2)
@@ -93,13 +103,13 @@ def test_attention(orc, pq, dev, npos_last, T, nh, nkv):
     kc = (orc.gen_normal(SEED + 9 * npos_last + 2, npos_last * kvd) * 2).astype(np.float16).view(np.uint16)
     vc = (orc.gen_normal(SEED + 9 * npos_last + 3, npos_last * kvd) * 5).astype(np.float16).view(np.uint16)
     scale = 0.125
-    want = np.stack([orc.sigmoid_gate(gate[t], orc.attn(q[t], kc, vc, pos0 + t + 1, nh, nkv, hd, scale), nh, hd)
+    want = np.stack([orc.sigmoid_gate(gate[t], orc.attn(q[t], kc, vc, pos0 + t + 1, nh, nkv, hd, scale, win), nh, hd)
                      for t in range(T)])
     out = torch.zeros((T, nh * hd), dtype=torch.int16, device=dev)
     qx = torch.empty((T, nh * hd), dtype=torch.int8, device=dev)
     dx = torch.empty((T, nh * hd // 32), dtype=torch.float32, device=dev)
     pq.attn_decode(_t16(q, dev), nh * hd, _t16(kc, dev), _t16(vc, dev), pos0, nh, nkv, hd, T, scale,
-                   gate=_t16(gate, dev), gate_stride=nh, out=out, out_stride=nh * hd, qx=qx, dx=dx)
+                   gate=_t16(gate, dev), gate_stride=nh, out=out, out_stride=nh * hd, qx=qx, dx=dx, win=win)
     got = _u16(out)
     bad = np.argwhere(got != want)
     assert bad.shape[0] == 0, f"{bad.shape[0]} differ, first {bad[:4].tolist()}"

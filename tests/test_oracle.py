@@ -295,6 +295,35 @@ def test_attention_vs_two_pass(orc):
             assert np.array_equal(orc.attn(q, Kc, Vc, 1, nh, nkv, hd, 0.125), want)
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_attention_window(orc, hd):
+    """Sliding-window layers (k_attn_head's lo = npos - win when npos > win,
+    lfm3_nanode.cu:515): against the double-precision two-pass softmax over the
+    same keys [lo, npos); win = 1 gives the newest value row itself; a window
+    at least npos wide is the full attention, bit for bit; a key outside the
+    window cannot move the output."""
+    nh, nkv = 8, 2
+    for npos, win in ((300, 256), (300, 100), (70, 64), (65, 1), (200, 17), (5, 256)):
+        q = orc.f2bf(orc.gen_normal(80 + npos + win, nh * hd))
+        Kc = orc.gen_normal(81 + npos, npos * nkv * hd).astype(np.float16).view(np.uint16)
+        Vc = orc.gen_normal(82 + npos, npos * nkv * hd).astype(np.float16).view(np.uint16)
+        a = orc.attn(q, Kc, Vc, npos, nh, nkv, hd, 0.125, win)
+        b = orc.attn_twopass(q, Kc, Vc, npos, nh, nkv, hd, 0.125, win)
+        assert np.abs(orc.bf2f(a) - b).max() <= np.abs(b).max() * 2 ** -7, (npos, win)
+        if win >= npos:
+            assert np.array_equal(a, orc.attn(q, Kc, Vc, npos, nh, nkv, hd, 0.125))
+        else:
+            assert not np.allclose(orc.bf2f(a), orc.attn_twopass(q, Kc, Vc, npos, nh, nkv, hd, 0.125), atol=1e-3)
+            lo = npos - win
+            K2, V2 = Kc.copy(), Vc.copy()
+            K2.reshape(npos, -1)[lo - 1] ^= 0x0400        # perturb the key and value just outside
+            V2.reshape(npos, -1)[lo - 1] ^= 0x0400
+            assert np.array_equal(a, orc.attn(q, K2, V2, npos, nh, nkv, hd, 0.125, win))
+        if win == 1:
+            vlast = Vc.view(np.float16).astype(np.float32).reshape(npos, nkv, hd)[-1]
+            assert np.array_equal(a, orc.f2bf(np.repeat(vlast, nh // nkv, axis=0).reshape(-1)))
+
+
 def test_conv_impulse_response(orc):
     H, nt = 64, 3
     taps = orc.gen_normal(60, H * nt)
