@@ -401,7 +401,11 @@ static int silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int 
   PQ_REQUIRE(gu && (y || qx) && (!qx || dx), PQ_ERR_ARG, "%s: null pointer", who);
   PQ_REQUIRE(F > 0 && F % 256 == 0 && T > 0, PQ_ERR_ARG, "%s: F=%d (a multiple of 256)", who, F);
   constexpr int E = 8;
-  const int threads = F / E < 256 ? F / E : 256;
+  // threads per workgroup: the largest of 256, 128, 64, 32 that divides the
+  // F/E thread count (F % 256 == 0 makes 32 always one), so the grid covers F
+  // exactly -- F = 7680 (the LFM3 FFN) runs 15 workgroups of 64
+  int threads = 256;
+  while ((F / E) % threads != 0) threads >>= 1;
   if (il)
     launch(silu_mul_kernel<E, true>, dim3(F / E / threads, T), dim3(threads), 0, as_stream(stream), gu, y, qx, dx, F);
   else

@@ -1,6 +1,6 @@
 """Writes the golden fixtures of tests/golden/ from the CPU oracle.
 
-    python tests/golden/make_golden.py [kernels] [tiny] [full] [full_ref]
+    python tests/golden/make_golden.py [kernels] [tiny] [full] [full_ref] [real]
 
 lfm3_synth_greedy.json  the synthetic 24-layer LFM3-style backbone (hidden 2048,
                         FFN 8192, vocab 65536, layers 0-15 gated conv, 16-23 GQA
@@ -8,6 +8,9 @@ lfm3_synth_greedy.json  the synthetic 24-layer LFM3-style backbone (hidden 2048,
                         prompt and the 64 greedy ids the oracle decodes from it
 lfm3_synth_greedy_ref.json  the same model and prompt with every GEMV in the
                         reference's own order (numerics = 1: bf16 x, fp32 scales)
+lfm3_real_shapes_greedy.json  the real LFM3 backbone's shapes and layer pattern (13 conv,
+                        6 full and 5 sliding-window attention layers, head_dim 128,
+                        FFN 7680, vocab 128000, 7-tap conv) with synthetic weights
 tiny_greedy.json        a 4-layer, hidden-256 model: prompt, ids, last logits digest
 kernels.npz             small kernel vectors (Q8_0 GEMV / GEMM, ternary GEMV,
                         attention) with their oracle outputs
@@ -30,6 +33,16 @@ FULL = dict(hidden=2048, ffn=8192, vocab=65536, nlayers=24, nh=32, nkv=8, hd=64,
             eps=1e-5, theta=1e6, seed=20261201, attn_mask=0xFF0000)
 TINY = dict(hidden=256, ffn=512, vocab=1000, nlayers=4, nh=4, nkv=2, hd=64, rot=32, ntaps=3, ctx=256,
             eps=1e-5, theta=1e6, seed=20261201, attn_mask=0b1010)
+# The real LFM3 backbone's shapes and layer pattern (the reference's model:
+# hidden 2048, FFN 7680, vocab 128000, 16 q / 4 kv heads of dim 128, 7-tap
+# conv; layers 0, 1, 3, 5, ..., 23 conv, 2, 6, ..., 22 full attention (theta 1e6,
+# half the dims rotated), 4, 8, ..., 20 sliding-window attention (window 256,
+# theta 1e4, all dims rotated)), with synthetic weights.
+REAL_ATTN = sum(1 << l for l in range(2, 24, 2))
+REAL_SLIDE = sum(1 << l for l in range(4, 24, 4))
+REAL = dict(hidden=2048, ffn=7680, vocab=128000, nlayers=24, nh=16, nkv=4, hd=128, rot=64, ntaps=7, ctx=2048,
+            eps=1e-5, theta=1e6, seed=20261201, attn_mask=REAL_ATTN, slide_mask=REAL_SLIDE, slide_win=256,
+            slide_rot=128, slide_theta=1e4)
 PROMPT_SEED = 20261201 + 4 * 5000
 
 
@@ -73,12 +86,14 @@ def kernel_fixture(path):
 
 
 if __name__ == "__main__":
-    which = sys.argv[1:] or ["kernels", "tiny", "full", "full_ref"]
+    which = sys.argv[1:] or ["kernels", "tiny", "full", "full_ref", "real"]
     if "kernels" in which:
         kernel_fixture(os.path.join(HERE, "kernels.npz"))
     if "tiny" in which:
         greedy_fixture(TINY, 40, 16, os.path.join(HERE, "tiny_greedy.json"))
     if "full" in which:
         greedy_fixture(FULL, 256, 64, os.path.join(HERE, "lfm3_synth_greedy.json"))
+    if "real" in which:
+        greedy_fixture(REAL, 256, 64, os.path.join(HERE, "lfm3_real_shapes_greedy.json"))
     if "full_ref" in which:
         greedy_fixture(dict(FULL, numerics=1), 256, 64, os.path.join(HERE, "lfm3_synth_greedy_ref.json"))

@@ -137,7 +137,12 @@ def _model_blob(orc, cfg, path):
         for slot, nm in ((4, "operator_norm"), (5, "post_operator_norm"), (6, "ffn_norm"), (7, "post_ffn_norm")):
             ts.append((P + nm + ".weight", np.array(m.tensor(l, slot))))
     ts.append(("lfm.model.embedding_norm.weight", np.array(m.tensor(-1, 1))))
-    layer_types = ["full_attention" if (cfg["attn_mask"] >> l) & 1 else "conv" for l in range(cfg["nlayers"])]
+    def kind(l):
+        if not (cfg["attn_mask"] >> l) & 1:
+            return "conv"
+        return "sliding_attention" if (cfg.get("slide_mask", 0) >> l) & 1 else "full_attention"
+
+    layer_types = [kind(l) for l in range(cfg["nlayers"])]
     write_blob(path, {"hidden_size": H, "vocab_size": cfg["vocab"], "layer_types": layer_types}, ts)
     m.close()
 
@@ -270,3 +275,60 @@ def test_blob_scales_fp16_or_ref_numerics(orc, pq, dev, tmp_path):
     ids = e.greedy(prompt, 4)
     assert len(ids) == 4
     e.close()
+
+
+# ------------------------------------------------- the real LFM3 backbone's shapes
+# hidden 2048, FFN 7680, vocab 128000, 16 q / 4 kv heads of dim 128, 7-tap conv,
+# full attention (theta 1e6, 64 of 128 dims rotated) and sliding-window
+# attention (theta 1e4, all dims rotated); four layers, the window cut to 40 so
+# a 100-token prompt crosses it inside and across 32-position chunks
+REAL4 = dict(hidden=2048, ffn=7680, vocab=128000, nlayers=4, nh=16, nkv=4, hd=128, rot=64, ntaps=7, ctx=256,
+             eps=1e-5, theta=1e6, seed=77, attn_mask=0b1010, slide_mask=0b1000, slide_win=40, slide_rot=128,
+             slide_theta=1e4)
+
+
+@pytest.mark.parametrize("numerics", [0, 1])
+def test_real_widths_match_oracle(orc, pq, dev, numerics):
+    cfg = dict(REAL4, numerics=numerics)
+    e = _engine(pq, cfg)
+    m = orc.Model(**cfg)
+    prompt = orc.gen_tokens(8, 100, cfg["vocab"])
+    r_e, lg_e = e.feed(prompt, True)
+    r_o, lg_o = m.feed(prompt, True)
+    assert np.array_equal(e.hidden(), m.hidden())
+    assert r_e == r_o and np.array_equal(lg_e.view(np.uint32), lg_o.view(np.uint32))
+    for step in range(4):
+        r_e, lg_e = e.feed(np.array([r_e], np.int32), True)
+        r_o, lg_o = m.feed(np.array([r_o], np.int32), True)
+        assert r_e == r_o and np.array_equal(lg_e.view(np.uint32), lg_o.view(np.uint32)), step
+    e.close()
+    m.close()
+
+
+def test_real_lfm3_blob_greedy_64(orc, pq, dev, tmp_path):
+    """The real LFM3 backbone's shapes and layer pattern (13 conv, 6 full and 5
+    sliding-window attention layers, interleaved as the reference's model):
+    the oracle's synthetic model written as an .lfm3q8 file under the
+    reference's tensor names and layer_types, loaded through
+    pq_engine_load_blob; a 256-token prompt and 64 greedy ids (positions past
+    the 256-key window) equal to tests/golden/lfm3_real_shapes_greedy.json."""
+    from pulsar_amd.engine import Engine
+    g = json.load(open(os.path.join(GOLDEN, "lfm3_real_shapes_greedy.json")))
+    cfg = dict(g["cfg"])
+    p = tmp_path / "lfm3_real_shapes.lfm3q8"
+    t0 = time.time()
+    _model_blob(orc, cfg, p)
+    t1 = time.time()
+    e = Engine(**cfg, prefill_chunk=256)
+    e.load_blob(p)
+    t2 = time.time()
+    prompt = np.array(g["prompt"], np.int32)
+    ids = e.greedy(prompt, 64)
+    print(f"blob write {t1 - t0:.1f}s ({os.path.getsize(p) / 1e9:.2f} GB), load {t2 - t1:.1f}s")
+    assert ids.tolist() == g["ids"], f"first mismatch at step {int(np.argmax(ids != np.array(g['ids'])))}"
+    e.reset()
+    _, lg = e.feed(prompt, True)
+    import hashlib
+    assert hashlib.sha256(lg.tobytes()).hexdigest() == g["prompt_logits_sha256"]
+    e.close()
+    os.remove(p)

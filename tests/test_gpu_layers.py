@@ -134,7 +134,7 @@ def test_conv(orc, pq, dev, ntaps, T):
     assert np.array_equal(_u16(rd), ring)
 
 
-@pytest.mark.parametrize("F,T", [(8192, 1), (8192, 4), (512, 2)])
+@pytest.mark.parametrize("F,T", [(8192, 1), (8192, 4), (512, 2), (7680, 3), (768, 2)])
 def test_silu_mul(orc, pq, dev, F, T):
     gu = orc.f2bf(orc.gen_normal(SEED + F + T, T * 2 * F).reshape(T, 2 * F) * 20)
     want = np.stack([orc.silu_mul(gu[t, :F], gu[t, F:]) for t in range(T)])

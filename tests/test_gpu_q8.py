@@ -115,7 +115,11 @@ def test_gemv_repeat_and_inplace(orc, pq, dev):
 @pytest.mark.parametrize("N,K,T", [(64, 2048, 1), (97, 96, 5), (130, 288, 33), (3104, 2048, 32),
                                    (2048, 8192, 32), (16384, 2048, 64), (2048, 2048, 77),
                                    (16384, 2048, 100), (16416, 2048, 40), (16384, 4096, 48),
-                                   (16384, 2048, 512), (65536, 2048, 96)])
+                                   (16384, 2048, 512), (65536, 2048, 96),
+                                   # the LFM3 shapes: FFN 7680 (gate+up 15360 rows, down K = 7680),
+                                   # q|k|v|gate 3088 rows, vocab 128000
+                                   (15360, 2048, 32), (2048, 7680, 32), (2048, 7680, 256), (3088, 2048, 100),
+                                   (128000, 2048, 32)])
 def test_gemm_bitexact(orc, pq, dev, N, K, T):
     print(f"gemm N={N} K={K} T={T}", flush=True)
     W, S, w = _weights(orc, pq, dev, N, K, SEED + 11 * N + K)
