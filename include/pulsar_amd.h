@@ -295,7 +295,7 @@ int pq_embed_rows(const int8_t *codes, const float *scales, const int32_t *token
  *   PQ_PRO_SILU     x = silu(gu[0:K]) * gu[K:2K]
  *   PQ_PRO_CONV     gated short conv of bcx [B|C|x] with ring_in -> ring_out
  *                   (the shifted ring, written once; a ping-pong pair);
- *                   ntaps must be 3, taps f32 [K][3] 16-byte aligned
+ *                   ntaps 3 or 7, taps f32 [K][ntaps] 16-byte aligned
  *   PQ_PRO_F32      x = xf, fp32 [K] (16-byte aligned), quantized in-kernel
  *                   exactly as pq_q8_quant_f32
  * K is the GEMV's K (a power of two, 1024..8192). argmax_parts (optional,

@@ -16,6 +16,7 @@
 // the same bits. The GQA head map h -> h / (nh/nkv) is lfm3_nanode.cu:520.
 #include "pq_device.h"
 #include "pq_host.h"
+#include "pq_internal.h"
 
 namespace pq {
 
@@ -35,12 +36,12 @@ __global__ __launch_bounds__(64) void attn_split_kernel(const uint16_t *__restri
                                                          const uint16_t *__restrict__ kc,
                                                          const uint16_t *__restrict__ vc, float *__restrict__ part,
                                                          int pos0, int nh, int nkv, int nsplit_max, float scale,
-                                                         int win) {
+                                                         int win, const int32_t *__restrict__ pos_dev) {
   constexpr int E = HD / 64, PART = HD + 2;
   __shared__ __align__(16) float qs[G][HD];
   __shared__ float es[G][kSplit];
   const int g = blockIdx.x, j = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
-  const int npos = pos0 + t + 1;
+  const int npos = (pos_dev != nullptr ? *pos_dev : pos0) + t + 1;
   const int lo = window_lo(npos, win);
   const int p0 = j * kSplit;
   if (p0 >= npos || p0 + kSplit <= lo) return;
@@ -110,10 +111,11 @@ template <int HD>
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float *__restrict__ part, int pos0, int nh,
                                                          int nsplit_max, const uint16_t *__restrict__ gate,
                                                          int gate_stride, uint16_t *__restrict__ out, int out_stride,
-                                                         int8_t *__restrict__ qx, float *__restrict__ dx, int win) {
+                                                         int8_t *__restrict__ qx, float *__restrict__ dx, int win,
+                                                         const int32_t *__restrict__ pos_dev) {
   constexpr int E = HD / 64, PART = HD + 2;
   const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-  const int npos = pos0 + t + 1;
+  const int npos = (pos_dev != nullptr ? *pos_dev : pos0) + t + 1;
   const int j0 = window_lo(npos, win) / kSplit;
   const int ns = (npos + kSplit - 1) / kSplit;
   const float *pp = part + ((size_t)t * nh + h) * nsplit_max * PART;
@@ -165,21 +167,21 @@ extern "C" size_t pq_attn_workspace_bytes(int nh, int hd, int max_pos, int T) {
 template <int HD>
 static int attn_launch(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
                        const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int8_t *qx, float *dx,
-                       int pos0, int nh, int nkv, int T, float scale, int win, float *part, int nsplit,
-                       hipStream_t st) {
+                       int pos0, const int32_t *pos_dev, int nh, int nkv, int T, float scale, int win, float *part,
+                       int nsplit, hipStream_t st) {
   const int G = nh / nkv;
   const dim3 g1(nkv, nsplit, T), b1(64);
   switch (G) {
-    case 1: launch(attn_split_kernel<1, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
-    case 2: launch(attn_split_kernel<2, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
-    case 4: launch(attn_split_kernel<4, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
-    case 8: launch(attn_split_kernel<8, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win); break;
+    case 1: launch(attn_split_kernel<1, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win, pos_dev); break;
+    case 2: launch(attn_split_kernel<2, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win, pos_dev); break;
+    case 4: launch(attn_split_kernel<4, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win, pos_dev); break;
+    case 8: launch(attn_split_kernel<8, HD>, g1, b1, 0, st, q, q_stride, kcache, vcache, part, pos0, nh, nkv, nsplit, scale, win, pos_dev); break;
     default: return fail(PQ_ERR_ARG, "pq_attn_decode: %d q heads per kv head (1, 2, 4 or 8)", G);
   }
   int rc = check_launch("pq_attn_decode split");
   if (rc) return rc;
   launch(attn_merge_kernel<HD>, dim3(nh, T), dim3(64), 0, st, part, pos0, nh, nsplit, gate, gate_stride, out,
-         out_stride, qx, dx, win);
+         out_stride, qx, dx, win, pos_dev);
   return check_launch("pq_attn_decode merge");
 }
 
@@ -200,8 +202,31 @@ extern "C" int pq_attn_decode(const uint16_t *q, int q_stride, const uint16_t *k
   float *part = reinterpret_cast<float *>(ws);
   hipStream_t st = as_stream(stream);
   if (hd == 64)
-    return attn_launch<64>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, pos0, nh, nkv, T,
-                           scale, win, part, nsplit, st);
-  return attn_launch<128>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, pos0, nh, nkv, T,
-                          scale, win, part, nsplit, st);
+    return attn_launch<64>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, pos0, nullptr, nh,
+                           nkv, T, scale, win, part, nsplit, st);
+  return attn_launch<128>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, pos0, nullptr, nh,
+                          nkv, T, scale, win, part, nsplit, st);
 }
+
+namespace pq {
+// One query (T = 1) at the position *pos_dev holds: the split grid and the
+// workspace cover positions below ctx, and the splits past the position
+// return at once, so a captured launch replays for any position.
+int attn_decode_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                    const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int8_t *qx, float *dx,
+                    const int32_t *pos_dev, int ctx, int nh, int nkv, int hd, float scale, int win, void *ws,
+                    size_t ws_bytes, hipStream_t st) {
+  PQ_REQUIRE(q && kcache && vcache && pos_dev && (out || qx) && (!qx || dx) && ctx > 0, PQ_ERR_ARG,
+             "attn_decode_dev: bad arguments");
+  PQ_REQUIRE(hd == 64 || hd == 128, PQ_ERR_ARG, "attn_decode_dev: head_dim %d", hd);
+  const int nsplit = (ctx + kSplit - 1) / kSplit;
+  PQ_REQUIRE(ws && ws_bytes >= pq_attn_workspace_bytes(nh, hd, ctx, 1), PQ_ERR_WORKSPACE,
+             "attn_decode_dev: workspace too small");
+  float *part = reinterpret_cast<float *>(ws);
+  if (hd == 64)
+    return attn_launch<64>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, 0, pos_dev, nh,
+                           nkv, 1, scale, win, part, nsplit, st);
+  return attn_launch<128>(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, qx, dx, 0, pos_dev, nh,
+                          nkv, 1, scale, win, part, nsplit, st);
+}
+}  // namespace pq

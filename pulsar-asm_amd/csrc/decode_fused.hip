@@ -143,20 +143,26 @@ __device__ __forceinline__ void quant_lds(const float *v, int e0, int8_t *xs, fl
 // Phase 1 (pro_load) issues every global load of the thread's E elements, raw;
 // the GEMV then issues its weight loads; phase 2 (pro_compute) does the math
 // with LDS-only barriers and leaves the Q8_0 x in LDS.
-constexpr int kFusedTaps = 3;  // the fused conv prologue's tap count
+// The CONV prologue comes in two tap counts (3: the synthetic backbone; 7:
+// LFM3's conv_L_cache): the template kind kProConv7 is PQ_PRO_CONV with 7 taps.
+constexpr int kProConv7 = 0x100 | PQ_PRO_CONV;
+constexpr int pro_base(int pro) { return pro & 0xff; }
+constexpr int conv_taps(int pro) { return pro == kProConv7 ? 7 : 3; }
 
-template <int E>
+template <int E, int NT>
 struct ProRegs {
   uint32_t u0[E / 2], u1[E / 2], u2[E / 2];
-  uint32_t ring[kFusedTaps - 1][E / 2];
+  uint32_t ring[NT - 1][E / 2];
   float f0[E], f1[E];
-  float taps[E * kFusedTaps];
+  float taps[E * NT];
   uint32_t emb_c[E / 4];
   uint16_t emb_s;
 };
 
 template <int PRO, int E>
-__device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int K, ProRegs<E> &r) {
+__device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int K,
+                                         ProRegs<E, conv_taps(PRO)> &r) {
+  constexpr int NT = conv_taps(PRO);
   if constexpr (PRO == PQ_PRO_Q8) {
 #pragma unroll
     for (int i = 0; i < E / 4; i++) r.emb_c[i] = reinterpret_cast<const uint32_t *>(p.qx + e0)[i];
@@ -187,19 +193,20 @@ __device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int 
   } else if constexpr (PRO == PQ_PRO_SILU) {
     ld_raw<E>(p.gu + e0, r.u0);
     ld_raw<E>(p.gu + K + e0, r.u1);
-  } else if constexpr (PRO == PQ_PRO_CONV) {
+  } else if constexpr (pro_base(PRO) == PQ_PRO_CONV) {
     ld_raw<E>(p.bcx + e0, r.u0);          // B
     ld_raw<E>(p.bcx + K + e0, r.u1);      // C
     ld_raw<E>(p.bcx + 2 * K + e0, r.u2);  // x
 #pragma unroll
-    for (int k = 1; k < kFusedTaps; k++) ld_raw<E>(p.ring_in + (size_t)k * K + e0, r.ring[k - 1]);
-    ld_f32<E * kFusedTaps>(p.taps + (size_t)e0 * kFusedTaps, r.taps);
+    for (int k = 1; k < NT; k++) ld_raw<E>(p.ring_in + (size_t)k * K + e0, r.ring[k - 1]);
+    ld_f32<E * NT>(p.taps + (size_t)e0 * NT, r.taps);
   }
 }
 
 template <int PRO, int E>
-__device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, int K, ProRegs<E> &r, float *red,
-                                            int8_t *xs, float *dxs) {
+__device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, int K, ProRegs<E, conv_taps(PRO)> &r,
+                                            float *red, int8_t *xs, float *dxs) {
+  constexpr int NT = conv_taps(PRO);
   const bool writer = blockIdx.x == 0;
   float v[E];
   if constexpr (PRO == PQ_PRO_Q8) {
@@ -251,7 +258,7 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
     }
 #pragma unroll
     for (int i = 0; i < E; i += 2) bfr2(v[i], v[i + 1]);
-  } else if constexpr (PRO == PQ_PRO_CONV) {
+  } else if constexpr (pro_base(PRO) == PQ_PRO_CONV) {
     // the shifted ring keeps the stored bf16 bits; its new entry is bx = bf16(B*x)
     uint32_t bxw[E / 2];
 #pragma unroll
@@ -263,8 +270,8 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
     for (int i = 0; i < E; i++) {
       float acc = 0.0f;
 #pragma unroll
-      for (int k = 0; k < kFusedTaps; k++)
-        acc = acc + r.taps[i * kFusedTaps + k] * bf_at(k + 1 < kFusedTaps ? r.ring[k] : bxw, i);
+      for (int k = 0; k < NT; k++)
+        acc = acc + r.taps[i * NT + k] * bf_at(k + 1 < NT ? r.ring[k] : bxw, i);
       v[i] = acc;
     }
 #pragma unroll
@@ -276,8 +283,8 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
     }
     if (writer) {
 #pragma unroll
-      for (int k = 0; k + 1 < kFusedTaps; k++) st_bf16w<E>(p.ring_out + (size_t)k * K + e0, r.ring[k]);
-      st_bf16w<E>(p.ring_out + (size_t)(kFusedTaps - 1) * K + e0, bxw);
+      for (int k = 0; k + 1 < NT; k++) st_bf16w<E>(p.ring_out + (size_t)k * K + e0, r.ring[k]);
+      st_bf16w<E>(p.ring_out + (size_t)(NT - 1) * K + e0, bxw);
     }
   }
   quant_lds<E>(v, e0, xs, dxs);
@@ -360,7 +367,7 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
   if (threadIdx.x >= W && threadIdx.x < 8) red[threadIdx.x] = red[8 + threadIdx.x] = 0.0f;
   // 1. the prologue's global loads, then round 0's weight loads, then the
   //    prologue math: its waits leave the weight loads in flight
-  ProRegs<E> pr;
+  ProRegs<E, conv_taps(PRO)> pr;
   pro_load<PRO, E>(p, e0, K, pr);
   const TileRsrc tr = tile_rsrc(pc, ps, tile, nb, nch);
   int c = slot;
@@ -704,8 +711,8 @@ static int check_fused_args(const int8_t *pcodes, const uint16_t *pscales, const
       break;
     case PQ_PRO_CONV:
       PQ_REQUIRE(p.bcx && p.ring_in && p.ring_out && p.taps && p.ring_in != p.ring_out &&
-                     p.ntaps == kFusedTaps && aligned(p.taps, 16),
-                 PQ_ERR_ARG, "%s: CONV needs bcx, taps, distinct ring_in / ring_out, ntaps 3", who);
+                     (p.ntaps == 3 || p.ntaps == 7) && aligned(p.taps, 16),
+                 PQ_ERR_ARG, "%s: CONV needs bcx, taps, distinct ring_in / ring_out, ntaps 3 or 7", who);
       break;
     default:
       return fail(PQ_ERR_ARG, "%s: prologue kind %d", who, p.kind);
@@ -796,7 +803,10 @@ static int launch_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_
     case PQ_PRO_EMBED: PQ_FUSED(PQ_PRO_EMBED); break;
     case PQ_PRO_SILU: PQ_FUSED(PQ_PRO_SILU); break;
     case PQ_PRO_F32: PQ_FUSED(PQ_PRO_F32); break;
-    default: PQ_FUSED(PQ_PRO_CONV); break;
+    default:
+      if (p.ntaps == 7) PQ_FUSED(kProConv7);
+      else PQ_FUSED(PQ_PRO_CONV);
+      break;
   }
 #undef PQ_FUSED
   return check_launch(who);

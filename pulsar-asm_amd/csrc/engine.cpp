@@ -555,26 +555,34 @@ static int forward_any(Engine &E, const int32_t *toks, int n, int32_t *next) {
   return ref_numerics(E) ? forward_r2(E, toks, n, next) : forward(E, toks, n, next);
 }
 
-// Whether the fused decode kernels take this configuration: power-of-two
-// hidden and FFN widths of 1024..8192 (the fused GEMV prologue), 3 conv taps,
-// head_dim 64 with a GQA group of 1, 2 or 4 and the attention mixer's LDS at
-// the full context.
+static bool pow2_range(int v) { return v >= 1024 && v <= 8192 && (v & (v - 1)) == 0; }
+
+// Whether an attention layer's decode mixer is the one-launch kernel: head_dim
+// 64, no window, a GQA group of 1, 2 or 4 and its LDS at the full context;
+// other layers take q/k prep + the split-K attention.
+static bool mixer_fused_cfg(const pq_model_cfg &c, bool slide) {
+  const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
+  const size_t ns = ((size_t)c.ctx + 63) / 64;
+  return !slide && c.hd == 64 && (G == 1 || G == 2 || G == 4) &&
+         (64 + 8 * 64 + ns * 66) * 4 + (2 * 64 + 8 * 64 * 72) * 2 <= 160 * 1024;
+}
+static bool mixer_fused(const Engine &E, const LayerDev &D) { return mixer_fused_cfg(E.c, D.slide != 0); }
+
+// Whether the fused decode kernels take this configuration: a power-of-two
+// hidden width of 1024..8192 (the fused GEMV prologues), an FFN width that is
+// a multiple of 32 (the SwiGLU epilogue's 32-row groups; a width that is not
+// a power of two runs its down projection as the plain Q8_0 GEMV), 3 or 7
+// conv taps, and attention the split-K kernels can run (GQA group 1..8).
 static bool fused_supported(const pq_model_cfg &c, const char **why) {
-  auto pow2 = [](int v) { return v >= 1024 && v <= 8192 && (v & (v - 1)) == 0; };
   bool conv = false, attn = false;
   for (int l = 0; l < c.nlayers; l++) ((c.attn_mask >> l) & 1u ? attn : conv) = true;
+  const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
   *why = nullptr;
   if (c.numerics == PQ_NUMERICS_REF) *why = "the reference-numerics mode runs unfused steps";
-  else if (!pow2(c.hidden) || !pow2(c.ffn)) *why = "hidden and ffn must be powers of two in 1024..8192";
-  else if (conv && c.ntaps != 3) *why = "the fused conv prologue takes 3 taps";
-  else if (attn && c.slide_mask) *why = "the fused attention mixer has no sliding window";
-  else if (attn) {
-    const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
-    const size_t ns = ((size_t)c.ctx + 63) / 64;
-    if (c.hd != 64 || (G != 1 && G != 2 && G != 4)) *why = "the fused attention mixer takes head_dim 64, GQA group 1, 2 or 4";
-    else if ((64 + 8 * 64 + ns * 66) * 4 + (2 * 64 + 8 * 64 * 72) * 2 > 160 * 1024)
-      *why = "context too long for the fused attention mixer";
-  }
+  else if (!pow2_range(c.hidden)) *why = "hidden must be a power of two in 1024..8192";
+  else if (c.ffn % 32 != 0) *why = "ffn must be a multiple of 32";
+  else if (conv && c.ntaps != 3 && c.ntaps != 7) *why = "the fused conv prologue takes 3 or 7 taps";
+  else if (attn && G != 1 && G != 2 && G != 4 && G != 8) *why = "GQA group 1, 2, 4 or 8";
   return *why == nullptr;
 }
 
@@ -622,13 +630,27 @@ static int forward_decode(Engine &E, bool dev) {
     }
     PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
     p = pq_gemv_prologue{};
-    if (D.attn) {
+    if (D.attn && mixer_fused(E, D)) {
       if (dev)
-        PQ_TRY(attn_layer_decode_dev(E.Wd, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.ctr + 1, c.ctx, c.nh, c.nkv,
-                                     c.hd, c.rot, c.eps, scale, nullptr, E.qx, E.dx, E.st));
+        PQ_TRY(attn_layer_decode_dev(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.ctr + 1, c.ctx, c.nh,
+                                     c.nkv, c.hd, layer_rot(E, D), c.eps, scale, nullptr, E.qx, E.dx, E.st));
       else
-        PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, E.rope, D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd, c.rot,
-                                    c.eps, scale, nullptr, E.qx, E.dx, E.st));
+        PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd,
+                                    layer_rot(E, D), c.eps, scale, nullptr, E.qx, E.dx, E.st));
+    } else if (D.attn) {
+      // head_dim 128 or a sliding window: q/k prep and the split-K attention
+      // (two launches), the position read on the device in the captured step
+      const int32_t *pd = dev ? E.ctr + 1 : nullptr;
+      PQ_TRY(qk_prep_launch(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, pd, c.nh, c.nkv,
+                            c.hd, layer_rot(E, D), 1, c.eps, E.st));
+      if (dev)
+        PQ_TRY(attn_decode_dev(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, nullptr, 0, E.qx, E.dx, pd,
+                               c.ctx, c.nh, c.nkv, c.hd, scale, layer_win(E, D), E.attn_ws, E.attn_ws_bytes, E.st));
+      else
+        PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, nullptr, 0, E.qx, E.dx, E.pos,
+                              c.nh, c.nkv, c.hd, 1, scale, layer_win(E, D), E.attn_ws, E.attn_ws_bytes, E.st));
+    }
+    if (D.attn) {
       p.kind = PQ_PRO_Q8;
       p.qx = E.qx;
       p.dx = E.dx;
@@ -644,11 +666,15 @@ static int forward_decode(Engine &E, bool dev) {
     PQ_TRY(gemv(D.out, E.Hb, PQ_DTYPE_BF16, nullptr));
     resnorm(D.post_op_norm, D.ffn_norm);
     PQ_TRY(pq_q8_gemv_fused_swiglu(D.ug.pc, D.ug.ps, &p, E.qx, E.dx, c.ffn, H, E.st));
-    p = pq_gemv_prologue{};
-    p.kind = PQ_PRO_Q8;
-    p.qx = E.qx;
-    p.dx = E.dx;
-    PQ_TRY(gemv(D.down, E.Hb, PQ_DTYPE_BF16, nullptr));
+    if (pow2_range(D.down.K)) {
+      p = pq_gemv_prologue{};
+      p.kind = PQ_PRO_Q8;
+      p.qx = E.qx;
+      p.dx = E.dx;
+      PQ_TRY(gemv(D.down, E.Hb, PQ_DTYPE_BF16, nullptr));
+    } else {   // FFN widths that are not powers of two (LFM3: 7680): the Q8_0 GEMV, the same bits
+      PQ_TRY(pq_q8_gemv(D.down.pc, D.down.ps, E.qx, E.dx, E.Hb, PQ_DTYPE_BF16, D.down.N, D.down.K, E.st));
+    }
   }
   resnorm(E.L[c.nlayers - 1].post_ffn_norm, E.final_norm);
   PQ_TRY(gemv(E.emb, E.logits, PQ_DTYPE_F32, E.parts));

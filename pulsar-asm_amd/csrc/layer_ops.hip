@@ -9,6 +9,7 @@
 // pq::expf_pq, 1/sqrt is the correctly rounded 1.0f / sqrtf.
 #include "pq_device.h"
 #include "pq_host.h"
+#include "pq_internal.h"
 
 namespace pq {
 
@@ -126,10 +127,10 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv,
                                                       const float *__restrict__ qn, const float *__restrict__ kn,
                                                       const float *__restrict__ cs, uint16_t *__restrict__ kc,
                                                       uint16_t *__restrict__ vc, int pos0, int nh, int nkv, int rot,
-                                                      float eps) {
+                                                      float eps, const int32_t *__restrict__ pos_dev) {
   constexpr int E = HD / 64;
   const int head = blockIdx.x, t = blockIdx.y, l = threadIdx.x;
-  const int pos = pos0 + t;
+  const int pos = (pos_dev != nullptr ? *pos_dev : pos0) + t;
   uint16_t *row = qkv + (size_t)t * row_stride;
   const int kvd = nkv * HD;
   if (head >= nh + nkv) {  // v: straight to the cache
@@ -369,14 +370,23 @@ extern "C" int pq_qk_prep(uint16_t *qkv, int row_stride, const float *q_norm, co
   PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && rot >= 0 && rot <= hd && rot % 2 == 0 && T > 0 && pos0 >= 0,
              PQ_ERR_ARG, "pq_qk_prep: nh=%d nkv=%d rot=%d T=%d pos0=%d", nh, nkv, rot, T, pos0);
   PQ_REQUIRE(row_stride >= (nh + 2 * nkv) * hd, PQ_ERR_ARG, "pq_qk_prep: row stride %d too small", row_stride);
+  return qk_prep_launch(qkv, row_stride, q_norm, k_norm, rope_cs, kcache, vcache, pos0, nullptr, nh, nkv, hd, rot, T,
+                        eps, as_stream(stream));
+}
+
+namespace pq {
+int qk_prep_launch(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm, const float *rope_cs,
+                   uint16_t *kcache, uint16_t *vcache, int pos0, const int32_t *pos_dev, int nh, int nkv, int hd,
+                   int rot, int T, float eps, hipStream_t st) {
   if (hd == 64)
-    launch(qk_prep_kernel<64>, dim3(nh + 2 * nkv, T), dim3(64), 0, as_stream(stream), qkv, row_stride, q_norm, k_norm,
-           rope_cs, kcache, vcache, pos0, nh, nkv, rot, eps);
+    launch(qk_prep_kernel<64>, dim3(nh + 2 * nkv, T), dim3(64), 0, st, qkv, row_stride, q_norm, k_norm, rope_cs,
+           kcache, vcache, pos0, nh, nkv, rot, eps, pos_dev);
   else
-    launch(qk_prep_kernel<128>, dim3(nh + 2 * nkv, T), dim3(64), 0, as_stream(stream), qkv, row_stride, q_norm,
-           k_norm, rope_cs, kcache, vcache, pos0, nh, nkv, rot, eps);
+    launch(qk_prep_kernel<128>, dim3(nh + 2 * nkv, T), dim3(64), 0, st, qkv, row_stride, q_norm, k_norm, rope_cs,
+           kcache, vcache, pos0, nh, nkv, rot, eps, pos_dev);
   return check_launch("pq_qk_prep");
 }
+}  // namespace pq
 
 extern "C" int pq_conv(uint16_t *ring, const float *taps, const uint16_t *bcx, uint16_t *out, int H, int T, int ntaps,
                        void *stream) {

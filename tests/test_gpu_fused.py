@@ -80,8 +80,9 @@ def test_silu_prologue(orc, pq, dev):
     assert np.array_equal(_u16(y), _ref_gemv(orc, W, S, orc.silu_mul(gu[:F], gu[F:])))
 
 
-def test_conv_prologue(orc, pq, dev):
-    H, N, nt = 2048, 2048, 3
+@pytest.mark.parametrize("nt", [3, 7])
+def test_conv_prologue(orc, pq, dev, nt):
+    H, N = 2048, 2048
     W, S, w = _w(orc, pq, dev, N, H, SEED + 30)
     taps = orc.gen_affine(SEED + 31, H * nt, 0.0, 0.5)
     ring = orc.f2bf(orc.gen_normal(SEED + 32, nt * H) * 3)
@@ -148,14 +149,28 @@ def test_attn_layer_decode(orc, pq, dev, pos):
     assert torch.equal(qx1, qx2) and torch.equal(dx1.view(torch.int32), dx2.view(torch.int32))
 
 
-def test_engine_fused_equals_unfused(orc, pq, dev):
+# the synthetic backbone's layer shapes (head_dim 64, 3 taps: the one-launch
+# attention mixer), and the real LFM3 widths (head_dim 128, FFN 7680, 7 taps,
+# a full and a sliding-window attention layer with the window cut to 40: the
+# q/k prep + split-K attention pair, the 7-tap CONV prologue and the plain
+# Q8_0 GEMV for the K = 7680 down projection)
+FUSED_CFGS = {
+    "synth": dict(hidden=2048, ffn=8192, vocab=65536, nlayers=3, nh=32, nkv=8, hd=64, rot=32, ntaps=3, ctx=512,
+                  eps=1e-5, theta=1e6, seed=77, attn_mask=0b010),
+    "lfm3": dict(hidden=2048, ffn=7680, vocab=128000, nlayers=4, nh=16, nkv=4, hd=128, rot=64, ntaps=7, ctx=256,
+                 eps=1e-5, theta=1e6, seed=78, attn_mask=0b1010, slide_mask=0b1000, slide_win=40, slide_rot=128,
+                 slide_theta=1e4),
+}
+
+
+@pytest.mark.parametrize("which", list(FUSED_CFGS))
+def test_engine_fused_equals_unfused(orc, pq, dev, which):
     """Fused steps replayed as captured graphs, fused steps launched one by one,
     and the unfused op sequence give the oracle's ids; graph replays are split
     into several decode calls with eager work (state reads, a non-graph step)
     between them."""
     from pulsar_amd.engine import Engine
-    cfg = dict(hidden=2048, ffn=8192, vocab=65536, nlayers=3, nh=32, nkv=8, hd=64, rot=32, ntaps=3, ctx=512,
-               eps=1e-5, theta=1e6, seed=77, attn_mask=0b010)
+    cfg = FUSED_CFGS[which]
     prompt = orc.gen_tokens(9, 70, cfg["vocab"])
     m = orc.Model(**{k: v for k, v in cfg.items()})
     ref = m.greedy(prompt, 12)
