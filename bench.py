@@ -11,10 +11,11 @@ its own pool of >= 300 MB of distinct copies, rotated launch by launch, so no
 launch finds its weights in the 256 MB Infinity Cache.
 
 Prints ONE JSON line. value = algorithmic bytes per step / time per step (GB/s;
-the K steps are one captured graph, the median of 5 timed replays). roofline =
-the GEMV kernel's algorithmic bytes / its mean launch duration, each launch
-timed by HIP events attached to its own dispatch (the quantity rocprofv3's
-kernel trace reports), against 8 TB/s. cpu_baseline = the reference's own CPU
+the K steps are one captured graph, the median of 5 timed replays, HIP events
+on the launch stream). roofline = the GEMV kernel's algorithmic bytes per
+launch / its average launch duration over that timed region (the region's
+time / its 5K launches; every launch of the step is q8_gemv_fused_kernel),
+against 8 TB/s, with each shape's back-to-back launch period beside it. cpu_baseline = the reference's own CPU
 GEMV (.auto/lfm3/q8_gemv_cpu.c gemv_q8, compiled into oracle/_ref) on the host
 cores over a bounded sample of the same shapes. The other keys are the single
 8192x2048 GEMV, the 24-layer backbone decode and its prompt prefill, the prefill
@@ -95,23 +96,6 @@ def period_ms(torch, launch, n, stream):
     ms = timed_replay(torch, g, stream) / n
     del g
     return ms
-
-
-def dispatch_ms(pq, torch, launch, n, warm=3):
-    """Mean and median duration of n eager launches (launch(i), rotating weights),
-    each timed by two HIP events attached to its own dispatch
-    (pq_time_next_launch): the kernel's own start-to-end, as rocprofv3 reports it."""
-    from pulsar_amd.hiptime import Event
-    for i in range(warm):
-        launch(i)
-    torch.cuda.synchronize()
-    ev = [(Event(), Event()) for _ in range(n)]
-    for i in range(n):
-        pq.check(pq.lib().pq_time_next_launch(ev[i][0].h, ev[i][1].h), "pq_time_next_launch")
-        launch(warm + i)
-    torch.cuda.synchronize()
-    d = [a.elapsed_ms(b) for a, b in ev]
-    return statistics.fmean(d), statistics.median(d)
 
 
 def copies_for(nbytes, min_mb=ROTATE_MB):
@@ -276,7 +260,7 @@ def cpu_backbone(cfg, n_prompt=8, n_steps=12):
 
 
 # ------------------------------------------------------------------ GPU side
-def config1_bench(pq, torch, dev, g, stream, n=40):
+def config1_bench(pq, torch, dev, g, stream, n=100):
     """The single Q8_0 GEMV, 8192x2048, fp32 x quantized in the prologue, fp32 y."""
     N, K = 8192, 2048
     pool, per = q8_pool(pq, torch, dev, g, N, K)
@@ -286,15 +270,14 @@ def config1_bench(pq, torch, dev, g, stream, n=40):
     def launch(i):
         pq.gemv_fused(pool[i % len(pool)], pq.PRO_F32, out_dtype=pq.DT_F32, out=y, xf=x)
 
-    mean, med = dispatch_ms(pq, torch, launch, n)
-    per_ms = period_ms(torch, launch, 60, stream)
+    per_ms = period_ms(torch, launch, n, stream)
     nb = gemv_bytes(N, K, "f32")
     ncopy = len(pool)
     del pool
     torch.cuda.empty_cache()
-    return {"gemv": f"{N}x{K}", "bytes": nb, "us": round(mean * 1e3, 2), "us_median": round(med * 1e3, 2),
-            "GB/s": round(nb / (mean * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "period_us": round(per_ms * 1e3, 2), "period_GB/s": round(nb / (per_ms * 1e-3) / 1e9, 1),
+    return {"gemv": f"{N}x{K}", "bytes": nb, "us": round(per_ms * 1e3, 2),
+            "GB/s": round(nb / (per_ms * 1e-3) / 1e9, 1), "hbm_frac": round(nb / (per_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "timed": f"{n} back-to-back launches in one graph, median of 5 replays",
             "weight_copies_rotated": ncopy, "rotated_MB": round(ncopy * per / 1e6, 1)}
 
 
@@ -349,6 +332,48 @@ def decode_bench(pq, n_steps=64, n_prompt=256, reps=3):
             "prefill_ms_256": round(prefill_ms, 2), "prefill_tok_s": round(n_prompt / (prefill_ms * 1e-3), 1),
             "prefill_chunk": LFM3_SYNTH["prefill_chunk"], "prefill_order": "layer-major",
             "prefill_ms_256_chunk32": round(prefill32_ms, 2)}
+
+
+# the real LFM3 backbone's shapes and layer pattern (synthetic weights): 13
+# conv layers, 6 full and 5 sliding-window attention layers, head_dim 128,
+# FFN 7680, vocab 128000, 7-tap conv
+LFM3_REAL = dict(hidden=2048, ffn=7680, vocab=128000, nlayers=24, nh=16, nkv=4, hd=128, rot=64, ntaps=7, ctx=2048,
+                 eps=1e-5, theta=1e6, seed=20261201, attn_mask=sum(1 << l for l in range(2, 24, 2)),
+                 slide_mask=sum(1 << l for l in range(4, 24, 4)), slide_win=256, slide_rot=128, slide_theta=1e4,
+                 prefill_chunk=256)
+
+
+def decode_variant(pq, cfg, n_steps=32, n_prompt=256):
+    """tok/s of n_steps greedy steps after a 256-token prompt (median of 3 runs)
+    for another engine configuration."""
+    from pulsar_amd.engine import Engine, synth_fill
+    from pulsar_amd.hiptime import Event
+    e = Engine(**cfg)
+    e.load_synthetic()
+    prompt = synth_fill(5, cfg["seed"] + 4 * 5000, n_prompt, float(cfg["vocab"]))
+    st = e.stream()
+    e.reset()
+    e.feed(prompt)
+    e.decode(2, want_ids=False)
+    e.sync()
+    pre, dec = [], []
+    for _ in range(3):
+        a, b, c = Event(), Event(), Event()
+        e.reset()
+        a.record(st)
+        e.feed(prompt)
+        b.record(st)
+        e.decode(n_steps, want_ids=False)
+        c.record(st)
+        e.sync()
+        pre.append(a.elapsed_ms(b))
+        dec.append(b.elapsed_ms(c) / n_steps)
+    ms = statistics.median(dec)
+    wbytes = e.weight_bytes()
+    e.close()
+    return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4), "weight_bytes": wbytes,
+            "GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "prefill_ms_256": round(statistics.median(pre), 2), "steps": n_steps}
 
 
 def prefill_gemm_bench(pq, torch, dev, g, stream, gpu, T=512, chunk=32):
@@ -453,15 +478,14 @@ def prefill_profile_workload(pq, torch, dev, reps=3):
 
 
 def _per_shape(pq, torch, stream, shapes, launch_of, nbytes_of, n=30):
-    """Per shape: mean dispatch duration and launch period over its rotated pool."""
+    """Per shape: the launch period of n back-to-back launches over its rotated
+    pool (one graph, HIP events on the launch stream)."""
     per = {}
     for s in shapes:
         name = s[0]
-        mean, _ = dispatch_ms(pq, torch, launch_of(s), n)
         prd = period_ms(torch, launch_of(s), n, stream)
         nb = nbytes_of(s)
-        per[name] = {"us": round(mean * 1e3, 2), "period_us": round(prd * 1e3, 2),
-                     "GB/s": round(nb / (mean * 1e-3) / 1e9, 1)}
+        per[name] = {"us": round(prd * 1e3, 2), "GB/s": round(nb / (prd * 1e-3) / 1e9, 1)}
     return per
 
 
@@ -501,7 +525,7 @@ def ref_numerics_bench(pq, torch, dev, g, stream, reps=20):
     torch.cuda.empty_cache()
     return {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "kernel_us": round(kern, 2), "kernel_hbm_frac": round(nbytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "period_us_sum": round(kern, 2), "period_hbm_frac": round(nbytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "per_shape": per, "rotated_MB_per_shape": ROTATE_MB}
 
 
@@ -545,8 +569,8 @@ def qlow_bench(pq, torch, dev, g, stream, reps=20):
         res[f"q{bits}"] = {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
                            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                           "kernel_us": round(kern, 2),
-                           "kernel_hbm_frac": round(nbytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                           "period_us_sum": round(kern, 2),
+                           "period_hbm_frac": round(nbytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                            "per_shape": per, "rotated_MB_per_shape": ROTATE_MB}
     return res
 
@@ -594,7 +618,7 @@ def ternary_bench(pq, torch, dev, g, stream, reps=20):
     return {"shapes": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "us_per_step": round(ms * 1e3, 2),
             "bytes_per_step": step_bytes, "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "kernel_us": round(kern, 2), "kernel_hbm_frac": round(step_bytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "period_us_sum": round(kern, 2), "period_hbm_frac": round(step_bytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "per_shape": per, "rotated_MB_per_shape": ROTATE_MB}
 
 
@@ -653,13 +677,14 @@ def main():
     ms_per_step = timed_replay(torch, g_steps, stream) / args.steps
     del g_steps
 
-    # the GEMV kernel's launch duration per shape (dispatch events, rotating
-    # pool), and its back-to-back launch period
+    # each shape's back-to-back launch period (rotating pool)
     per = _per_shape(pq, torch, stream, SHAPES, launch_of, lambda s: gemv_bytes(*s[1:]), n=40)
     step_bytes = sum(gemv_bytes(N, K, o) for (_, N, K, o) in SHAPES)
-    kern_ms = sum(p["us"] for p in per.values()) * 1e-3
-    achieved = step_bytes / (kern_ms * 1e-3) / 1e9
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    # the roofline kernel: every launch of the timed region is q8_gemv_fused_kernel,
+    # so its average launch moves step_bytes / 5 in ms_per_step / 5
+    launch_us = ms_per_step * 1e3 / len(SHAPES)
+    achieved = (step_bytes / len(SHAPES)) / (launch_us * 1e-6) / 1e9
     gpu = gpu_desc(torch, pq)
 
     line = {
@@ -683,8 +708,9 @@ def main():
                    "rotated_MB_per_shape": {n: round(len(pools[n]) * per_copy[n] / 1e6, 1) for n in pools}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "q8_gemv_fused_kernel (5 shapes, mean dispatch duration)",
-                     "kernel_us_per_step": round(kern_ms * 1e3, 2), "per_shape": per,
+                     "kernel": "q8_gemv_fused_kernel: the timed region's 5 x steps launches",
+                     "launches": len(SHAPES) * args.steps, "avg_launch_us": round(launch_us, 3),
+                     "bytes_per_launch": step_bytes // len(SHAPES), "per_shape_period": per,
                      "lm_head_frac": round(per["lm_head"]["GB/s"] / HBM_PEAK_GBS, 4)},
         "cpu_baseline": None,
     }
@@ -700,6 +726,9 @@ def main():
     if not args.no_extra:
         line["config1_gemv"] = config1_bench(pq, torch, dev, g, stream)
         line["decode"] = decode_bench(pq)
+        line["decode_lfm3_real_shapes"] = decode_variant(pq, LFM3_REAL)
+        from pulsar_amd.engine import LFM3_SYNTH
+        line["decode_ref_numerics"] = decode_variant(pq, dict(LFM3_SYNTH, numerics=1))
         line["prefill_gemm"] = prefill_gemm_bench(pq, torch, dev, g, stream, gpu)
         line["ternary_gemv"] = ternary_bench(pq, torch, dev, g, stream)
         line["ref_numerics_gemv"] = ref_numerics_bench(pq, torch, dev, g, stream)

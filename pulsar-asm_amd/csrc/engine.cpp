@@ -191,9 +191,13 @@ static int create(Engine &E, const pq_model_cfg &c) {
   PQ_TRY(E.dalloc(&E.ctr, 2));
   E.attn_ws_bytes = pq_attn_workspace_bytes(c.nh, c.hd, c.ctx, T);
   PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.attn_ws), E.attn_ws_bytes));
-  // the split-K GEMM workspace: the largest of the layer shapes at tmax positions
+  // the split-K GEMM workspace: the largest of the layer shapes at any chunk
+  // size up to tmax (pq_engine_set_chunk may shrink the chunk, and the small
+  // chunks are the ones that split K)
   const int shapes[6][2] = {{E.nin, H}, {3 * H, H}, {H, E.qd}, {H, H}, {2 * F, H}, {H, F}};
-  for (const auto &nk : shapes) E.gemm_ws_bytes = std::max(E.gemm_ws_bytes, pq_q8_gemm_workspace_bytes(nk[0], nk[1], T));
+  for (int t = 1; t <= T; t++)
+    for (const auto &nk : shapes)
+      E.gemm_ws_bytes = std::max(E.gemm_ws_bytes, pq_q8_gemm_workspace_bytes(nk[0], nk[1], t));
   if (E.gemm_ws_bytes) PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.gemm_ws), E.gemm_ws_bytes));
   return PQ_OK;
 }
