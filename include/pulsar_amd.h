@@ -339,16 +339,17 @@ int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream);
 int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
                             int8_t *qx, float *dx, int F, int K, void *stream);
 /* The attention mixer of one decode step (T=1, position pos) in one launch:
- * q/k norm + RoPE, fp16 KV write at pos, every 64-position split, the ordered
- * merge, the sigmoid gate, and the Q8_0 row (qx, dx) of o_proj's input; out
- * (bf16, optional) gets the gated attention output. qkvg is the fused
- * [q | k | v | gate] GEMV row. Same numerics as pq_qk_prep + pq_attn_decode.
+ * q/k norm + RoPE, fp16 KV write at pos, every 64-position split of the
+ * window (win as in pq_attn_decode; 0 = full attention), the ordered merge,
+ * the sigmoid gate, and the Q8_0 row (qx, dx) of o_proj's input and/or out
+ * (bf16) with the gated attention output. qkvg is the fused [q | k | v | gate]
+ * GEMV row; head_dim 64 or 128. Same numerics as pq_qk_prep + pq_attn_decode.
  * Replaces k_headnorm, k_rope, the KV write, k_attn_head and k_sigmoid_gate of
  * layer_body (lfm3_nanode.cu:3749-3786). */
 int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float *k_norm,
                          const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos, int nh,
-                         int nkv, int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx,
-                         float *dx, void *stream);
+                         int nkv, int hd, int rot, int win, float eps, float scale, uint16_t *out,
+                         int8_t *qx, float *dx, void *stream);
 
 /* ======================================================= ternary GEMV
  * PQ2_0 x Q8_K, the Bonsai ternary path. codes u8 [N][K/4] (weight i of a

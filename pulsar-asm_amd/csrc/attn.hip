@@ -22,10 +22,6 @@ namespace pq {
 
 constexpr int kSplit = 64;
 
-// Keys a query at npos - 1 sees: [lo, npos), lo = npos - win for a sliding
-// layer whose window the context has outgrown (k_attn_head, lfm3_nanode.cu:515).
-__device__ __forceinline__ int window_lo(int npos, int win) { return (win > 0 && npos > win) ? npos - win : 0; }
-
 // One wave per (kv head g, split j, query t); lane p = position 64j + p for the
 // scores, lane l = dimensions l + 64e (e < HD/64) for the value sums; the G
 // heads of the group share every K and V load. Splits with no key in the

@@ -22,6 +22,8 @@
 // The attention mixer of a decode step is one kernel per layer
 // (attn_layer_kernel): q/k norm, RoPE, KV write, every split, the ordered
 // merge, the sigmoid gate and the Q8_0 output for o_proj.
+#include <type_traits>
+
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
@@ -669,6 +671,198 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
   }
 }
 
+// ------------------------------------- attention mixer, head_dim 64 or 128
+// The one-launch decode mixer for the shapes attn_head_kernel does not take
+// (head_dim 128, sliding windows): the arithmetic of qk_prep_kernel +
+// attn_split_kernel + attn_merge_kernel in one workgroup of 8 waves per q
+// head. Waves 0-2 form q (norm + RoPE from the layer's table), k (norm + RoPE,
+// fp16, written to the cache by the group's first workgroup) and v; wave w
+// then owns the splits j0 + w, j0 + w + 8, ... of the window. Per split lane p
+// loads key row p (whole cache lines) and every lane loads its E = HD/64
+// adjacent value dims of all 64 positions up front, so a split waits on
+// memory about once; the row at pos, which this launch writes, comes from LDS.
+// Wave 0 merges the splits in ascending order, gates, and writes the head's
+// bf16 output and/or its Q8_0 blocks.
+template <int HD>
+__device__ __forceinline__ void mixer_norm_rope(const float *x, const float *__restrict__ w,
+                                                const float *__restrict__ cs, int pos, int rot, float eps, int lane,
+                                                float *r) {
+  constexpr int E = HD / 64;
+  float ss = 0.0f, v[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    const float part = wave_pairwise_sum(x[e] * x[e]);
+    ss = e == 0 ? part : ss + part;
+  }
+  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)HD) + eps);
+#pragma unroll
+  for (int e = 0; e < E; e++) v[e] = bf2f(f2bf(w[lane + 64 * e] * bf2f(f2bf(x[e] * rs))));
+  const int half = rot / 2;
+  if constexpr (HD == 64) {
+    const float up = __shfl_down(v[0], 32, 64);
+    const float dn = __shfl_up(v[0], 32, 64);
+    const int i = lane & 31;
+    r[0] = v[0];
+    if (i < half) {
+      const float c = cs[((size_t)pos * half + i) * 2], sn = cs[((size_t)pos * half + i) * 2 + 1];
+      r[0] = lane < 32 ? v[0] * c - up * sn : v[0] * c + dn * sn;
+    }
+  } else {
+    r[0] = v[0];
+    r[1] = v[1];
+    if (lane < half) {
+      const float c = cs[((size_t)pos * half + lane) * 2], sn = cs[((size_t)pos * half + lane) * 2 + 1];
+      r[0] = v[0] * c - v[1] * sn;
+      r[1] = v[1] * c + v[0] * sn;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; e++) r[e] = bf2f(f2bf(r[e]));
+}
+
+template <int HD>
+__global__ __launch_bounds__(512) void attn_mixer_kernel(const uint16_t *__restrict__ qkvg, const float *__restrict__ qn,
+                                                          const float *__restrict__ kn, const float *__restrict__ cs,
+                                                          uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+                                                          int pos_arg, const int32_t *__restrict__ pos_dev, int nh,
+                                                          int nkv, int rot, int win, float eps, float scale,
+                                                          uint16_t *__restrict__ out, int8_t *__restrict__ qx,
+                                                          float *__restrict__ dx) {
+  constexpr int E = HD / 64, PART = HD + 2;
+  using VT = typename std::conditional<E == 2, uint32_t, uint16_t>::type;   // a lane's E adjacent fp16
+  extern __shared__ __align__(16) unsigned char smem[];
+  float *qs = reinterpret_cast<float *>(smem);                      // [HD] q
+  float *ew = qs + HD;                                               // [8 waves][64] e
+  uint16_t *kvnew = reinterpret_cast<uint16_t *>(ew + 8 * kSplitF);  // [2][HD] fp16 k, v at pos
+  float *st = reinterpret_cast<float *>(kvnew + 2 * HD);            // [nsplit][HD + 2]
+  const int pos = pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_arg;
+  const int hq = blockIdx.x, G = nh / nkv, g = hq / G;
+  const bool writer = hq % G == 0;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int kvd = nkv * HD;
+  const int npos = pos + 1;
+  const int lo = window_lo(npos, win);
+  const int j0 = lo / kSplitF, ns = (npos + kSplitF - 1) / kSplitF;
+  // 1. q, k (norm + RoPE) and v of position pos
+  if (wave < 3) {
+    const int base = wave == 0 ? hq * HD : wave == 1 ? nh * HD + g * HD : nh * HD + kvd + g * HD;
+    float x[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) x[e] = bf2f(qkvg[base + lane + 64 * e]);
+    if (wave == 2) {
+#pragma unroll
+      for (int e = 0; e < E; e++) {
+        const uint16_t v = f2h(x[e]);
+        kvnew[HD + lane + 64 * e] = v;
+        if (writer) vc[(size_t)pos * kvd + g * HD + lane + 64 * e] = v;
+      }
+    } else {
+      float r[E];
+      mixer_norm_rope<HD>(x, wave == 0 ? qn : kn, cs, pos, rot, eps, lane, r);
+#pragma unroll
+      for (int e = 0; e < E; e++) {
+        if (wave == 0) {
+          qs[lane + 64 * e] = r[e];
+        } else {
+          const uint16_t k = f2h(r[e]);
+          kvnew[lane + 64 * e] = k;
+          if (writer) kc[(size_t)pos * kvd + g * HD + lane + 64 * e] = k;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // 2. the window's splits
+  float *eww = ew + wave * kSplitF;
+  for (int j = j0 + wave; j < ns; j += 8) {
+    const int p0 = j * kSplitF;
+    const int pn = npos - p0 < kSplitF ? npos - p0 : kSplitF;
+    const int i0 = lo > p0 ? lo - p0 : 0;
+    const bool valid = lane >= i0 && lane < pn;
+    VT vr[kSplitF];
+    {
+      const VT *vb = reinterpret_cast<const VT *>(vc + (size_t)p0 * kvd + g * HD) + lane;
+#pragma unroll
+      for (int p = 0; p < kSplitF; p++)
+        vr[p] = p >= i0 && p < pn && p0 + p != pos ? vb[(size_t)p * (kvd / E)] : (VT)0;
+    }
+    uint4 k8[HD / 8];
+    {
+      const bool from_cache = valid && p0 + lane != pos;
+      const uint4 *kr = from_cache ? reinterpret_cast<const uint4 *>(kc + (size_t)(p0 + lane) * kvd + g * HD)
+                                   : reinterpret_cast<const uint4 *>(kvnew);
+#pragma unroll
+      for (int i = 0; i < HD / 8; i++) k8[i] = kr[i];
+    }
+    float d = 0.0f;
+#pragma unroll
+    for (int i = 0; i < HD / 8; i++) {
+      const uint32_t kw[4] = {k8[i].x, k8[i].y, k8[i].z, k8[i].w};
+#pragma unroll
+      for (int u = 0; u < 8; u++) d = __builtin_fmaf(qs[8 * i + u], h2f((uint16_t)(kw[u >> 1] >> (16 * (u & 1)))), d);
+    }
+    const float sc = valid ? d * scale : -__builtin_inff();
+    const float m = wave_max(sc);
+    const float e = valid ? expf_pq(sc - m) : 0.0f;
+    const float l = wave_pairwise_sum(e);
+    eww[lane] = e;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float o[E];
+#pragma unroll
+    for (int k = 0; k < E; k++) o[k] = 0.0f;
+    const VT vpos = reinterpret_cast<const VT *>(kvnew + HD)[lane];
+#pragma unroll
+    for (int p = 0; p < kSplitF; p++)
+      if (p >= i0 && p < pn) {
+        const uint32_t bits = (uint32_t)(p0 + p == pos ? vpos : vr[p]);
+        const float ep = eww[p];
+#pragma unroll
+        for (int k = 0; k < E; k++) o[k] = __builtin_fmaf(ep, h2f((uint16_t)(bits >> (16 * k))), o[k]);
+      }
+    float *sj = st + (size_t)j * PART;
+#pragma unroll
+    for (int k = 0; k < E; k++) sj[E * lane + k] = o[k];
+    if (lane == 0) {
+      sj[HD] = m;
+      sj[HD + 1] = l;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  // 3. ordered merge, gate, outputs
+  if (wave == 0) {
+    float M = -__builtin_inff();
+    for (int j = j0; j < ns; j++) M = fmaxf(M, st[(size_t)j * PART + HD]);
+    float L = 0.0f, O[E];
+#pragma unroll
+    for (int k = 0; k < E; k++) O[k] = 0.0f;
+    for (int j = j0; j < ns; j++) {
+      const float w = expf_pq(st[(size_t)j * PART + HD] - M);
+      L = __builtin_fmaf(st[(size_t)j * PART + HD + 1], w, L);
+#pragma unroll
+      for (int k = 0; k < E; k++) O[k] = __builtin_fmaf(st[(size_t)j * PART + lane + 64 * k], w, O[k]);
+    }
+    const float gs = 1.0f / (1.0f + expf_pq(-bf2f(qkvg[nh * HD + 2 * kvd + hq])));
+#pragma unroll
+    for (int k = 0; k < E; k++) {
+      const int dd = hq * HD + lane + 64 * k;
+      const uint16_t rb = f2bf(bf2f(f2bf(O[k] / L)) * gs);
+      if (out != nullptr) out[dd] = rb;
+      if (qx != nullptr) {
+        const float v = bf2f(rb);
+        float a = fabsf(v);
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+        const float dq = a / 127.0f;
+        qx[dd] = (int8_t)q8_code(Q8Div(dq).div(v));
+        if ((lane & 31) == 0) dx[dd / 32] = dq;
+      }
+    }
+  }
+}
+
 }  // namespace pq
 
 using namespace pq;
@@ -849,37 +1043,52 @@ int argmax_parts_step(const float *parts, int nparts, int32_t *out, int32_t *ids
 
 static int attn_layer(const uint16_t *qkvg, const float *q_norm, const float *k_norm, const float *rope_cs,
                       uint16_t *kcache, uint16_t *vcache, int pos, const int32_t *pos_dev, int ctx, int nh, int nkv,
-                      int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx, hipStream_t st) {
-  PQ_REQUIRE(qkvg && q_norm && k_norm && rope_cs && kcache && vcache && qx && dx, PQ_ERR_ARG,
+                      int hd, int rot, int win, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
+                      hipStream_t st) {
+  PQ_REQUIRE(qkvg && q_norm && k_norm && rope_cs && kcache && vcache && (qx || out) && (!qx || dx), PQ_ERR_ARG,
              "pq_attn_layer_decode: null pointer");
-  PQ_REQUIRE(hd == kHDf && nh > 0 && nkv > 0 && nh % nkv == 0 && pos >= 0 && rot >= 0 && rot <= hd, PQ_ERR_ARG,
-             "pq_attn_layer_decode: hd=%d nh=%d nkv=%d pos=%d", hd, nh, nkv, pos);
+  PQ_REQUIRE((hd == 64 || hd == 128) && nh > 0 && nkv > 0 && nh % nkv == 0 && pos >= 0 && rot >= 0 && rot <= hd &&
+                 win >= 0,
+             PQ_ERR_ARG, "pq_attn_layer_decode: hd=%d nh=%d nkv=%d pos=%d win=%d", hd, nh, nkv, pos, win);
   PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "pq_attn_layer_decode: cache alignment");
   const int G = nh / nkv;
   const int ns = (ctx + kSplitF - 1) / kSplitF;   // LDS for the splits of positions 0..ctx-1
-  const size_t lds = ((size_t)kHDf + 8 * (size_t)kSplitF + (size_t)ns * kPartf) * 4 +
-                     (2 * (size_t)kHDf + 8 * (size_t)kSplitF * kVRow) * 2;
-  PQ_REQUIRE(G == 1 || G == 2 || G == 4, PQ_ERR_ARG, "pq_attn_layer_decode: %d q heads per kv head (1, 2 or 4)", G);
+  if (hd == kHDf && win == 0 && (G == 1 || G == 2 || G == 4)) {
+    // head_dim 64, full attention: the K/V blocks pass through LDS (attn_head_kernel)
+    const size_t lds = ((size_t)kHDf + 8 * (size_t)kSplitF + (size_t)ns * kPartf) * 4 +
+                       (2 * (size_t)kHDf + 8 * (size_t)kSplitF * kVRow) * 2;
+    if (lds <= kMaxLds) {
+      launch(attn_head_kernel, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos,
+             pos_dev, nh, nkv, rot, eps, scale, out, qx, dx);
+      return check_launch("pq_attn_layer_decode");
+    }
+  }
+  const size_t lds = ((size_t)hd + 8 * (size_t)kSplitF + (size_t)ns * (hd + 2)) * 4 + 2 * (size_t)hd * 2;
   PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_attn_layer_decode: %d positions need %zu B of LDS", ctx, lds);
-  launch(attn_head_kernel, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, pos_dev,
-         nh, nkv, rot, eps, scale, out, qx, dx);
+  if (hd == 64)
+    launch(attn_mixer_kernel<64>, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos,
+           pos_dev, nh, nkv, rot, win, eps, scale, out, qx, dx);
+  else
+    launch(attn_mixer_kernel<128>, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos,
+           pos_dev, nh, nkv, rot, win, eps, scale, out, qx, dx);
   return check_launch("pq_attn_layer_decode");
 }
 
 extern "C" int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float *k_norm,
                                     const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos, int nh, int nkv,
-                                    int hd, int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
-                                    void *stream) {
-  return attn_layer(qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nullptr, pos + 1, nh, nkv, hd, rot, eps, scale,
-                    out, qx, dx, as_stream(stream));
+                                    int hd, int rot, int win, float eps, float scale, uint16_t *out, int8_t *qx,
+                                    float *dx, void *stream) {
+  return attn_layer(qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos, nullptr, pos + 1, nh, nkv, hd, rot, win, eps,
+                    scale, out, qx, dx, as_stream(stream));
 }
 
 namespace pq {
 int attn_layer_decode_dev(const uint16_t *qkvg, const float *q_norm, const float *k_norm, const float *rope_cs,
                           uint16_t *kcache, uint16_t *vcache, const int32_t *pos_dev, int ctx, int nh, int nkv, int hd,
-                          int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx, hipStream_t st) {
+                          int rot, int win, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
+                          hipStream_t st) {
   PQ_REQUIRE(pos_dev && ctx > 0, PQ_ERR_ARG, "attn_layer_decode_dev: bad arguments");
-  return attn_layer(qkvg, q_norm, k_norm, rope_cs, kcache, vcache, 0, pos_dev, ctx, nh, nkv, hd, rot, eps, scale, out,
-                    qx, dx, st);
+  return attn_layer(qkvg, q_norm, k_norm, rope_cs, kcache, vcache, 0, pos_dev, ctx, nh, nkv, hd, rot, win, eps, scale,
+                    out, qx, dx, st);
 }
 }  // namespace pq

@@ -561,14 +561,14 @@ static int forward_any(Engine &E, const int32_t *toks, int n, int32_t *next) {
 
 static bool pow2_range(int v) { return v >= 1024 && v <= 8192 && (v & (v - 1)) == 0; }
 
-// Whether an attention layer's decode mixer is the one-launch kernel: head_dim
-// 64, no window, a GQA group of 1, 2 or 4 and its LDS at the full context;
-// other layers take q/k prep + the split-K attention.
+// Whether an attention layer's decode mixer is one launch (pq_attn_layer_decode:
+// head_dim 64 or 128, any window) -- its LDS holds the split partials of the
+// whole context; otherwise q/k prep + the split-K attention pair.
 static bool mixer_fused_cfg(const pq_model_cfg &c, bool slide) {
-  const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
+  (void)slide;
   const size_t ns = ((size_t)c.ctx + 63) / 64;
-  return !slide && c.hd == 64 && (G == 1 || G == 2 || G == 4) &&
-         (64 + 8 * 64 + ns * 66) * 4 + (2 * 64 + 8 * 64 * 72) * 2 <= 160 * 1024;
+  return (c.hd == 64 || c.hd == 128) && ((size_t)c.hd + 8 * 64 + ns * (c.hd + 2)) * 4 + 2 * (size_t)c.hd * 2 <=
+                                            160 * 1024;
 }
 static bool mixer_fused(const Engine &E, const LayerDev &D) { return mixer_fused_cfg(E.c, D.slide != 0); }
 
@@ -637,10 +637,11 @@ static int forward_decode(Engine &E, bool dev) {
     if (D.attn && mixer_fused(E, D)) {
       if (dev)
         PQ_TRY(attn_layer_decode_dev(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.ctr + 1, c.ctx, c.nh,
-                                     c.nkv, c.hd, layer_rot(E, D), c.eps, scale, nullptr, E.qx, E.dx, E.st));
+                                     c.nkv, c.hd, layer_rot(E, D), layer_win(E, D), c.eps, scale, nullptr, E.qx, E.dx,
+                                     E.st));
       else
         PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, c.nh, c.nkv, c.hd,
-                                    layer_rot(E, D), c.eps, scale, nullptr, E.qx, E.dx, E.st));
+                                    layer_rot(E, D), layer_win(E, D), c.eps, scale, nullptr, E.qx, E.dx, E.st));
     } else if (D.attn) {
       // head_dim 128 or a sliding window: q/k prep and the split-K attention
       // (two launches), the position read on the device in the captured step

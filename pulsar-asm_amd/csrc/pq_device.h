@@ -189,4 +189,8 @@ __device__ __forceinline__ lds_ptr<T> lds_base(const T *p) {
   return (lds_ptr<T>)(size_t)a;
 }
 
+// Keys a query at npos - 1 sees: [lo, npos), lo = npos - win for a sliding
+// layer whose window the context has outgrown (k_attn_head, lfm3_nanode.cu:515).
+__device__ __forceinline__ int window_lo(int npos, int win) { return (win > 0 && npos > win) ? npos - win : 0; }
+
 }  // namespace pq

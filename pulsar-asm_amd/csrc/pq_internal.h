@@ -15,7 +15,8 @@ namespace pq {
 // sized for any position below ctx.
 int attn_layer_decode_dev(const uint16_t *qkvg, const float *q_norm, const float *k_norm, const float *rope_cs,
                           uint16_t *kcache, uint16_t *vcache, const int32_t *pos_dev, int ctx, int nh, int nkv, int hd,
-                          int rot, float eps, float scale, uint16_t *out, int8_t *qx, float *dx, hipStream_t st);
+                          int rot, int win, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
+                          hipStream_t st);
 
 // pq_qk_prep with the launch stream given; pos_dev (if not NULL) holds the
 // position of row 0 on the device instead of pos0.

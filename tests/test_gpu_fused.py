@@ -115,16 +115,25 @@ def test_q8_prologue(orc, pq, dev):
     assert torch.equal(y.view(torch.int16), pq.q8_gemv(w, qx, dx, out_dtype=pq.DT_BF16).view(torch.int16))
 
 
-@pytest.mark.parametrize("pos", [0, 63, 64, 300, 2047, 4500])
-def test_attn_layer_decode(orc, pq, dev, pos):
-    nh, nkv, hd, rot = 32, 8, 64, 32
+# (pos, hd, nh, nkv, rot, theta, win): head_dim 64 full attention (the K/V-through-LDS
+# mixer), then head_dim 128 full / sliding and head_dim 64 sliding (the generic mixer)
+MIXER_CASES = [(0, 64, 32, 8, 32, 1e6, 0), (63, 64, 32, 8, 32, 1e6, 0), (64, 64, 32, 8, 32, 1e6, 0),
+               (300, 64, 32, 8, 32, 1e6, 0), (2047, 64, 32, 8, 32, 1e6, 0), (4500, 64, 32, 8, 32, 1e6, 0),
+               (0, 128, 16, 4, 64, 1e6, 0), (300, 128, 16, 4, 64, 1e6, 0), (2047, 128, 16, 4, 64, 1e6, 0),
+               (300, 128, 16, 4, 128, 1e4, 256), (256, 128, 16, 4, 128, 1e4, 256), (1000, 128, 16, 4, 128, 1e4, 256),
+               (130, 64, 32, 8, 32, 1e6, 100), (40, 128, 16, 4, 128, 1e4, 1)]
+
+
+@pytest.mark.parametrize("pos,hd,nh,nkv,rot,theta,win", MIXER_CASES)
+def test_attn_layer_decode(orc, pq, dev, pos, hd, nh, nkv, rot, theta, win):
+    print(f"mixer pos={pos} hd={hd} win={win}", flush=True)
     ctx = max(2048, pos + 1)
     nin = nh * hd + 2 * nkv * hd + nh
     kvd = nkv * hd
     row = orc.f2bf(orc.gen_normal(SEED + pos, nin) * 30)
     qn = orc.gen_affine(SEED + 50, hd, 1.0, 0.1)
     kn = orc.gen_affine(SEED + 51, hd, 1.0, 0.1)
-    cs = orc.rope_table(ctx, hd, rot, 1e6)
+    cs = orc.rope_table(ctx, hd, rot, theta)
     kc0 = np.zeros((ctx, kvd), np.float16)
     vc0 = np.zeros((ctx, kvd), np.float16)
     kc0[:pos] = orc.gen_normal(SEED + 52, pos * kvd).reshape(pos, kvd) * 2
@@ -138,12 +147,12 @@ def test_attn_layer_decode(orc, pq, dev, pos):
     qx1 = torch.empty(nh * hd, dtype=torch.int8, device=dev)
     dx1 = torch.empty(nh * hd // 32, dtype=torch.float32, device=dev)
     pq.attn_decode(r1, nin, kc1, vc1, pos, nh, nkv, hd, 1, 0.125, gate=r1[nh * hd + 2 * kvd:], gate_stride=nin,
-                   out=out1, out_stride=nh * hd, qx=qx1, dx=dx1)
+                   out=out1, out_stride=nh * hd, qx=qx1, dx=dx1, win=win)
     # fused
     r2 = _t16(row, dev)
     kc2, vc2 = _t16(kc0.view(np.uint16), dev), _t16(vc0.view(np.uint16), dev)
     out2 = torch.empty(nh * hd, dtype=torch.int16, device=dev)
-    qx2, dx2 = pq.attn_layer_decode(r2, *args, kc2, vc2, pos, nh, nkv, hd, rot, 0.125, out=out2)
+    qx2, dx2 = pq.attn_layer_decode(r2, *args, kc2, vc2, pos, nh, nkv, hd, rot, 0.125, out=out2, win=win)
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     assert torch.equal(out1, out2)
     assert torch.equal(qx1, qx2) and torch.equal(dx1.view(torch.int32), dx2.view(torch.int32))
