@@ -366,7 +366,7 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
   g0.ok = true;
   item(blockIdx.x, g0);
   GemmCur g1 = next(g0);
-  GemmW w0, w1;
+  GemmW wa, wb, wc;   // the three chunk buffers of the pipeline, rotated by name (see below)
   int seg_k = -1, seg_c1 = 0, seg_p = -1;   // staged chunks [seg_k, min(seg_k + 8, seg_c1)), position block
   float yv[16];
 #pragma unroll
@@ -375,8 +375,11 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
   // a new segment's activations first, then (first step only) the weights of
   // chunks 0 and 1, then the weights two chunks ahead -- so staging waits only
   // on the activations. The first step is a separate copy (FIRST) so every
-  // wait the compiler places stays exact.
-  auto step = [&](auto FIRST) -> bool {
+  // wait the compiler places stays exact. w0 holds the weights of the chunk
+  // computed, w1 and w2 those of the next two; the loop below passes the three
+  // buffers in rotated order instead of copying them, since a copy of a
+  // register that a load is still filling waits for that load.
+  auto step = [&](auto FIRST, GemmW &w0, GemmW &w1, GemmW &w2) -> bool {
     const int c = g0.c;
     // activations and dx: the 8 chunks from c of position block p0 (uniform:
     // every wave of the workgroup walks the same chunk sequence)
@@ -426,7 +429,6 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
       lds_barrier();
     };
     GemmCur g2;
-    GemmW w2;
     if constexpr (decltype(FIRST)::value) {
       // first step: only chunk 0's weights go out with the activations (a
       // deeper prefetch from every CU queues ahead of them in memory)
@@ -475,12 +477,11 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
     if (!g1.ok) return false;
     g0 = g1;
     g1 = g2;
-    w0 = w1;
-    w1 = w2;
     return true;
   };
-  if (step(std::integral_constant<bool, true>{}))
-    while (step(std::integral_constant<bool, false>{})) {
+  const std::integral_constant<bool, false> rest;
+  if (step(std::integral_constant<bool, true>{}, wa, wb, wc))
+    while (step(rest, wb, wc, wa) && step(rest, wc, wa, wb) && step(rest, wa, wb, wc)) {
     }
 }
 
@@ -494,12 +495,14 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(const int8_t *__r
 // for two workgroups per CU). Same numerics as the walking form.
 // PH = 16 gives a workgroup 16 positions (the A operand's other 16 rows read
 // zeros and their outputs are neither folded nor written): twice the
-// workgroups and half the fold per wave, for GEMMs with few slices.
+// workgroups and half the fold per wave, for GEMMs with few slices. AUX is the
+// weight loads' cache policy: nontemporal, or cached where many position
+// blocks' workgroups re-read the same weights.
 constexpr int kTileSlots = 8;
 constexpr size_t kTileActBytes = 32 * (size_t)kGemmARow;
 constexpr size_t kTileLds = kTileActBytes + (size_t)kTileSlots * kCB * 32 * 4;
 
-template <int S, bool PIPE, int PH = 32>
+template <int S, bool PIPE, int PH = 32, int AUX = kAuxNT>
 __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const int8_t *__restrict__ pc,
                                                                         const uint16_t *__restrict__ ps,
                                                                         const int8_t *__restrict__ qx,
@@ -557,7 +560,7 @@ __global__ __launch_bounds__(64 * kTileSlots * S) void q8_gemm_tile_kernel(const
     v4i wv[kCB];
     const int oc = valid ? c * kCB * kSlab + (h * kTR + jt) * 16 : kRsrcOob;
 #pragma unroll
-    for (int i = 0; i < kCB; i++) wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, oc + i * kSlab, 0, kAuxNT);
+    for (int i = 0; i < kCB; i++) wv[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, oc + i * kSlab, 0, AUX);
     const v4i sv = __builtin_amdgcn_raw_buffer_load_b128(rs, valid ? (c * kTR + jt) * 16 : kRsrcOob, 0, 0);
     if (rd > 0) lds_barrier();   // the previous round's fold reads of the partials are done
 #pragma unroll
@@ -761,9 +764,14 @@ extern "C" int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, cons
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
   hipStream_t st = as_stream(stream);
   const int form = gemm_form(N, K, T);
-  if (form == kFormTile) {
-    launch(q8_gemm_tile_kernel<2, false>, dim3((unsigned)ntiles(N), 1, (unsigned)((T + 31) / 32)), dim3(64 * kTileSlots * 2),
-           kTileLds, st, pcodes, pscales, qx, dx, y, yb, N, K, T);
+  if (form == kFormTile) {   // with 8+ position blocks the weights' re-reads are served from cache (measured)
+    const dim3 grid((unsigned)ntiles(N), 1, (unsigned)((T + 31) / 32));
+    if (grid.z >= 8)
+      launch(q8_gemm_tile_kernel<2, false, 32, 0>, grid, dim3(64 * kTileSlots * 2), kTileLds, st, pcodes, pscales, qx,
+             dx, y, yb, N, K, T);
+    else
+      launch(q8_gemm_tile_kernel<2, false>, grid, dim3(64 * kTileSlots * 2), kTileLds, st, pcodes, pscales, qx, dx, y,
+             yb, N, K, T);
     return check_launch("pq_q8_gemm");
   }
   if (form == kFormSlice) {
