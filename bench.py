@@ -489,6 +489,32 @@ def _per_shape(pq, torch, stream, shapes, launch_of, nbytes_of, n=30):
     return per
 
 
+def read_floor(pq, torch, dev, stream, named_bytes, n=40):
+    """Per shape: the launch period of pq_stream_read over the same number of
+    bytes (a plain streaming read, 1024 x 512 threads, no arithmetic), n
+    back-to-back launches at rotating offsets of a 1 GiB buffer, one graph.
+    It is the practical ceiling of one launch that reads that many bytes (the
+    launch and first-byte latency included), which the GEMV periods are read
+    against."""
+    pool = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    pool.fill_(1)
+    sink = torch.zeros(1, dtype=torch.float32, device=dev)
+    out = {}
+    for name, nb in named_bytes:
+        nb16 = nb // 16 * 16
+        span = (nb16 + 4095) // 4096 * 4096
+        nslots = max(1, pool.numel() // span)
+
+        def launch(i, nb16=nb16, span=span, nslots=nslots):
+            pq.check(pq.lib().pq_stream_read(pool.data_ptr() + (i % nslots) * span, nb16, sink.data_ptr(),
+                                             pq.stream_ptr()), "pq_stream_read")
+        prd = period_ms(torch, launch, n, stream)
+        out[name] = {"us": round(prd * 1e3, 2), "GB/s": round(nb16 / (prd * 1e-3) / 1e9, 1)}
+    del pool
+    torch.cuda.empty_cache()
+    return out
+
+
 def ref_numerics_bench(pq, torch, dev, g, stream, reps=20):
     """The config-2 step through the reference-numerics GEMV (pq_q8r_gemv: the
     reference's own order, bf16 x, fp32 weight scales, row-major codes), each
@@ -566,7 +592,10 @@ def qlow_bench(pq, torch, dev, g, stream, reps=20):
         kern = sum(p["us"] for p in per.values())
         del pools
         torch.cuda.empty_cache()
+        floor = read_floor(pq, torch, dev, stream, [(s[0], nb[s[0]]) for s in shapes])
         res[f"q{bits}"] = {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
+                           "stream_read_floor": {"per_shape": floor,
+                                                 "step_us": round(sum(v["us"] for v in floor.values()), 2)},
                            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                            "period_us_sum": round(kern, 2),
@@ -615,7 +644,9 @@ def ternary_bench(pq, torch, dev, g, stream, reps=20):
     kern = sum(p["us"] for p in per.values())
     del pools
     torch.cuda.empty_cache()
+    floor = read_floor(pq, torch, dev, stream, [(n, nb[n]) for (n, N, K) in shapes])
     return {"shapes": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "us_per_step": round(ms * 1e3, 2),
+            "stream_read_floor": {"per_shape": floor, "step_us": round(sum(v["us"] for v in floor.values()), 2)},
             "bytes_per_step": step_bytes, "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "period_us_sum": round(kern, 2), "period_hbm_frac": round(step_bytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
@@ -686,6 +717,8 @@ def main():
     launch_us = ms_per_step * 1e3 / len(SHAPES)
     achieved = (step_bytes / len(SHAPES)) / (launch_us * 1e-6) / 1e9
     gpu = gpu_desc(torch, pq)
+    floor = read_floor(pq, torch, dev, stream, [(s[0], gemv_bytes(*s[1:])) for s in SHAPES])
+    floor_us = sum(v["us"] for v in floor.values())
 
     line = {
         "metric": "Q8 GEMV HBM GB/s (% of peak); backbone decode tok/s on 1 MI355X",
@@ -711,7 +744,12 @@ def main():
                      "kernel": "q8_gemv_fused_kernel: the timed region's 5 x steps launches",
                      "launches": len(SHAPES) * args.steps, "avg_launch_us": round(launch_us, 3),
                      "bytes_per_launch": step_bytes // len(SHAPES), "per_shape_period": per,
-                     "lm_head_frac": round(per["lm_head"]["GB/s"] / HBM_PEAK_GBS, 4)},
+                     "lm_head_frac": round(per["lm_head"]["GB/s"] / HBM_PEAK_GBS, 4),
+                     "stream_read_floor": {"per_shape": floor, "step_us": round(floor_us, 2),
+                                           "GB/s": round(step_bytes / (floor_us * 1e-6) / 1e9, 1),
+                                           "gemv_step_over_floor": round(floor_us / (ms_per_step * 1e3), 4),
+                                           "what": "pq_stream_read over each shape's algorithmic bytes, launch "
+                                                   "periods: a plain read of the same bytes in the same launches"}},
         "cpu_baseline": None,
     }
     del pools

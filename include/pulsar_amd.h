@@ -63,6 +63,12 @@ int pq_check_quant_div(uint32_t *counts, uint32_t *first, uint32_t seed, void *s
  * against the 100 MHz real-time counter). out: 2 floats of device memory,
  * out[0] = MHz. No counterpart in the reference. */
 int pq_clock_mhz(float *out, void *stream);
+/* A plain streaming read of `bytes` (a multiple of 16) from p: 1024 x 512
+ * threads, one nontemporal 16-byte load per lane per grid-stride step, no
+ * arithmetic. Its launch period is the practical ceiling of any kernel that
+ * reads that many bytes in one launch; sink (one float of device memory) is
+ * never written for real data. No counterpart in the reference. */
+int pq_stream_read(const void *p, size_t bytes, float *sink, void *stream);
 
 /* --------------------------------------------------------- Q8_0 activations
  * x [T][K] -> qx [T][K] int8, dx [T][K/32] fp32. Per 32-block:

@@ -139,7 +139,32 @@ __global__ __launch_bounds__(64) void clock_probe_kernel(float *__restrict__ out
   }
 }
 
+// A plain streaming read of n16 16-byte pieces: 1024 workgroups of 512
+// threads, one nontemporal 16-byte load per lane per grid-stride step and no
+// arithmetic beyond an xor, so its launch period is what a kernel that only
+// streams the same bytes achieves -- the practical ceiling a GEMV launch of
+// that size is read against. sink is written only if the xor of the data hits
+// a value it cannot for the caller's buffers (the loads stay live).
+typedef int piece16 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(512) void stream_read_kernel(const piece16 *__restrict__ p, long long n16,
+                                                          float *__restrict__ sink) {
+  int acc = 0;
+  for (long long i = (long long)blockIdx.x * 512 + threadIdx.x; i < n16; i += (long long)gridDim.x * 512) {
+    const piece16 v = __builtin_nontemporal_load(p + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x7eadbeef) sink[0] = (float)acc;
+}
+
 }  // namespace pq
+
+extern "C" int pq_stream_read(const void *p, size_t bytes, float *sink, void *stream) {
+  PQ_REQUIRE(p && sink && bytes % 16 == 0, PQ_ERR_ARG, "pq_stream_read: p, sink and a multiple of 16 bytes");
+  PQ_REQUIRE(pq::aligned(p, 16), PQ_ERR_ALIGN, "pq_stream_read: p must be 16-byte aligned");
+  pq::launch(pq::stream_read_kernel, dim3(1024), dim3(512), 0, pq::as_stream(stream),
+             static_cast<const pq::piece16 *>(p), (long long)(bytes / 16), sink);
+  return pq::check_launch("pq_stream_read");
+}
 
 extern "C" int pq_clock_mhz(float *out, void *stream) {
   PQ_REQUIRE(out, PQ_ERR_ARG, "pq_clock_mhz: null pointer");

@@ -40,6 +40,7 @@ SIGNATURES = {
     "pq_check_bf16_cvt": (I, [P, P, P]),
     "pq_check_quant_div": (I, [P, P, C.c_uint32, P]),
     "pq_clock_mhz": (I, [P, P]),
+    "pq_stream_read": (I, [P, Z, P, P]),
     "pq_q8_quant_f32": (I, [P, P, P, I, I, P]),
     "pq_q8_quant_bf16": (I, [P, P, P, I, I, P]),
     "pq_q8_packed_codes_bytes": (Z, [I, I]),

@@ -41,6 +41,8 @@ def test_loads_and_rejects_bad_args():
     assert L.pq_q8_quant_f32(8, 8, 8, 33, 1, None) == -1          # K not a multiple of 32
     assert b"multiple of 32" in L.pq_last_error()
     assert L.pq_time_next_launch(None, 8) == -1
+    assert L.pq_stream_read(16, 24, 16, None) == -1               # not a multiple of 16 bytes
+    assert b"multiple of 16" in L.pq_last_error()
 
 
 def test_python_wrappers_exported():

@@ -58,3 +58,14 @@ def test_clock_probe(pq, dev):
     pq.check(pq.lib().pq_clock_mhz(out.data_ptr(), pq.stream_ptr()), "pq_clock_mhz")
     torch.cuda.synchronize()
     assert 500.0 < float(out[0]) < 3000.0
+
+
+def test_stream_read(pq, dev):
+    """pq_stream_read (the bench's read ceiling) runs over a buffer and a tail
+    shorter than one grid step, and leaves its sink alone for real data."""
+    buf = torch.ones(3 << 20, dtype=torch.uint8, device=dev)
+    sink = torch.full((1,), 5.0, dtype=torch.float32, device=dev)
+    for nb in (buf.numel(), 16, 4096 + 16):
+        pq.check(pq.lib().pq_stream_read(buf.data_ptr(), nb, sink.data_ptr(), pq.stream_ptr()), "pq_stream_read")
+    torch.cuda.synchronize()
+    assert float(sink[0]) == 5.0
