@@ -187,47 +187,52 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv,
 // window of the last NT bx values (the ring holds the NT before the chunk,
 // newest last); acc = sum_k fl(tap_k * bx_{t-NT+1+k}) ascending from 0;
 // cy = bf16(acc); out = bf16(C*cy). The positions are independent once bx is
-// known, so a workgroup owns 64 channels and its waves take positions t = w,
-// w + W, ...; each thread forms the bx values of its window itself (the same
-// bf16 products), reading the ring for positions before the chunk. The new
-// ring (the last NT bx values) is written after a workgroup barrier, so every
-// read of the old ring has happened: a channel's ring is touched by its own
-// workgroup only, which makes the in-place update safe.
+// known, so a workgroup owns 64 channels x kConvTP positions [t0, t0 + TP):
+// its threads first form the bx values the tile's windows need (positions
+// t0 - NT + 1 .. t0 + TP - 1, each once, from the ring before the chunk) into
+// LDS, then each output from LDS. The new ring (the last NT bx values) is
+// written by the tile at t0 = 0, after a workgroup barrier: it is the only
+// tile that reads the old ring, so the in-place update cannot race.
+constexpr int kConvTP = 32;   // positions per workgroup
+
 template <int NT>
 __global__ __launch_bounds__(512) void conv_kernel(uint16_t *__restrict__ ring, const float *__restrict__ taps,
                                                     const uint16_t *__restrict__ bcx, uint16_t *__restrict__ out,
                                                     int H, int T) {
-  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+  constexpr int NW = kConvTP + NT - 1;   // window positions of the tile
+  __shared__ uint16_t sbx[NW][64];
+  const int lc = threadIdx.x & 63, c = blockIdx.x * 64 + lc;
   const int w = threadIdx.x >> 6, W = blockDim.x >> 6;
+  const int t0 = blockIdx.y * kConvTP;
   const bool live = c < H;
-  float tp[NT];
-  uint16_t old[NT];
-#pragma unroll
-  for (int k = 0; k < NT; k++) {
-    tp[k] = live ? taps[(size_t)c * NT + k] : 0.0f;
-    old[k] = live ? ring[(size_t)k * H + c] : (uint16_t)0;
-  }
   auto bx = [&](int tau) -> uint16_t {   // tau < 0: the ring (tau = -1 is its newest entry)
-    if (tau < 0) return old[NT + tau];
+    if (tau < 0) return ring[(size_t)(NT + tau) * H + c];
     const uint16_t *row = bcx + (size_t)tau * 3 * H;
     return f2bf(bf2f(row[c]) * bf2f(row[2 * H + c]));
   };
-  if (live) {
-    for (int t = w; t < T; t += W) {
-      float acc = 0.0f;
+  const int tend = T - t0 < kConvTP ? T - t0 : kConvTP;   // positions of this tile
+  if (live)
+    for (int i = w; i < tend + NT - 1; i += W) sbx[i][lc] = bx(t0 - (NT - 1) + i);
+  float tp[NT];
 #pragma unroll
-      for (int k = 0; k < NT; k++) acc = acc + tp[k] * bf2f(bx(t - (NT - 1) + k));
-      const uint16_t cy = f2bf(acc);
-      out[(size_t)t * H + c] = f2bf(bf2f(bcx[(size_t)t * 3 * H + H + c]) * bf2f(cy));
-    }
-  }
+  for (int k = 0; k < NT; k++) tp[k] = live ? taps[(size_t)c * NT + k] : 0.0f;
   uint16_t nr[NT];
-  if (live && w == 0) {
+  if (blockIdx.y == 0 && live && w == 0) {   // the new ring, from the old one where T < NT
 #pragma unroll
     for (int k = 0; k < NT; k++) nr[k] = bx(T - NT + k);
   }
-  __syncthreads();   // every thread's reads of the old ring are done
-  if (live && w == 0) {
+  __syncthreads();   // the window is in LDS; every read of the old ring is done
+  if (live) {
+    for (int i = w; i < tend; i += W) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NT; k++) acc = acc + tp[k] * bf2f(sbx[i + k][lc]);
+      const uint16_t cy = f2bf(acc);
+      const int t = t0 + i;
+      out[(size_t)t * H + c] = f2bf(bf2f(bcx[(size_t)t * 3 * H + H + c]) * bf2f(cy));
+    }
+  }
+  if (blockIdx.y == 0 && live && w == 0) {
 #pragma unroll
     for (int k = 0; k < NT; k++) ring[(size_t)k * H + c] = nr[k];
   }
@@ -392,9 +397,9 @@ extern "C" int pq_conv(uint16_t *ring, const float *taps, const uint16_t *bcx, u
                        void *stream) {
   PQ_REQUIRE(ring && taps && bcx && out, PQ_ERR_ARG, "pq_conv: null pointer");
   PQ_REQUIRE(H > 0 && T > 0, PQ_ERR_ARG, "pq_conv: H=%d T=%d", H, T);
-  // 64 channels per workgroup; up to 8 waves over the positions
+  // 64 channels x 32 positions per workgroup; up to 8 waves over the positions
   const int waves = T < 8 ? T : 8;
-  const dim3 grid((H + 63) / 64), block(64 * waves);
+  const dim3 grid((H + 63) / 64, (T + kConvTP - 1) / kConvTP), block(64 * waves);
   hipStream_t st = as_stream(stream);
   switch (ntaps) {
     case 2: launch(conv_kernel<2>, grid, block, 0, st, ring, taps, bcx, out, H, T); break;

@@ -116,9 +116,12 @@ def test_attention(orc, pq, dev, npos_last, T, nh, nkv, hd, win):
     assert np.array_equal(qx.cpu().numpy(), orc.q8_quant_bf16(want)[0])
 
 
-@pytest.mark.parametrize("ntaps,T", [(3, 1), (3, 32), (7, 5)])
-def test_conv(orc, pq, dev, ntaps, T):
-    H = 2048
+# T past one 32-position tile (33, 100, 256: the tile at 0 alone reads and then
+# rewrites the ring), T below the tap count (7, 3), a channel count that is not
+# a multiple of 64
+@pytest.mark.parametrize("ntaps,T,H", [(3, 1, 2048), (3, 32, 2048), (7, 5, 2048), (3, 33, 2048), (3, 100, 2048),
+                                       (7, 256, 2048), (7, 3, 2048), (7, 70, 1000)])
+def test_conv(orc, pq, dev, ntaps, T, H):
     taps = orc.gen_affine(SEED + 20, H * ntaps, 0.0, 0.5)
     ring0 = orc.f2bf(orc.gen_normal(SEED + 21, ntaps * H) * 3)
     bcx = orc.f2bf(orc.gen_normal(SEED + 22, T * 3 * H).reshape(T, 3 * H) * 10)
