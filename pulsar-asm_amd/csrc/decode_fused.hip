@@ -656,18 +656,20 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
     const float gs = 1.0f / (1.0f + expf_pq(-bf2f(graw)));
     rb = f2bf(bf2f(rb) * gs);
     if (out != nullptr) out[hq * kHDf + lane] = rb;
-    const float v = bf2f(rb);
-    // amax over each 32-lane half (one Q8_0 block): DPP within 16-lane rows,
-    // then the row-pair swap
-    float a = fabsf(v);
-    a = fmaxf(a, dpp_f<kDppXor1>(a));
-    a = fmaxf(a, dpp_f<kDppXor2>(a));
-    a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
-    a = fmaxf(a, dpp_f<kDppMirror>(a));
-    a = max_row_pair(a);
-    const float dq = a / 127.0f;
-    qx[hq * kHDf + lane] = (int8_t)q8_code(Q8Div(dq).div(v));
-    if ((lane & 31) == 0) dx[(hq * kHDf + lane) / 32] = dq;
+    if (qx != nullptr) {   // the Q8_0 blocks of o_proj's input (a caller may ask for bf16 only)
+      const float v = bf2f(rb);
+      // amax over each 32-lane half (one Q8_0 block): DPP within 16-lane rows,
+      // then the row-pair swap
+      float a = fabsf(v);
+      a = fmaxf(a, dpp_f<kDppXor1>(a));
+      a = fmaxf(a, dpp_f<kDppXor2>(a));
+      a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
+      a = fmaxf(a, dpp_f<kDppMirror>(a));
+      a = max_row_pair(a);
+      const float dq = a / 127.0f;
+      qx[hq * kHDf + lane] = (int8_t)q8_code(Q8Div(dq).div(v));
+      if ((lane & 31) == 0) dx[(hq * kHDf + lane) / 32] = dq;
+    }
   }
 }
 

@@ -506,6 +506,17 @@ static int forward(Engine &E, const int32_t *toks, int n, int32_t *next) {
   return PQ_OK;
 }
 
+// Whether an attention layer's decode mixer is one launch (pq_attn_layer_decode:
+// head_dim 64 or 128, any window) -- its LDS holds the split partials of the
+// whole context; otherwise q/k prep + the split-K attention pair.
+static bool mixer_fused_cfg(const pq_model_cfg &c, bool slide) {
+  (void)slide;
+  const size_t ns = ((size_t)c.ctx + 63) / 64;
+  return (c.hd == 64 || c.hd == 128) && ((size_t)c.hd + 8 * 64 + ns * (c.hd + 2)) * 4 + 2 * (size_t)c.hd * 2 <=
+                                            160 * 1024;
+}
+static bool mixer_fused(const Engine &E, const LayerDev &D) { return mixer_fused_cfg(E.c, D.slide != 0); }
+
 // The same layer sequence under PQ_NUMERICS_REF: every GEMV is pq_q8r_gemv
 // (the reference's own order on bf16 activations and fp32 scales, row-major
 // codes) and the activations between ops stay bf16, as in layer_body; the
@@ -530,7 +541,10 @@ static int forward_r2(Engine &E, const int32_t *toks, int n, int32_t *next) {
       uint16_t *Xc = E.X + (size_t)c0 * H;
       uint16_t *xin = E.xin + (size_t)c0 * H;
       PQ_TRY(gemm_r2(E, D.in, xin, E.Wd, PQ_DTYPE_BF16, T));
-      if (D.attn) {
+      if (D.attn && T == 1 && mixer_fused(E, D)) {   // one launch, the same bits (bf16 out for o_proj)
+        PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pos0, c.nh, c.nkv, c.hd,
+                                    layer_rot(E, D), layer_win(E, D), c.eps, scale, E.A, nullptr, nullptr, E.st));
+      } else if (D.attn) {
         PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pos0, c.nh, c.nkv, c.hd,
                           layer_rot(E, D), T, c.eps, E.st));
         PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr, nullptr,
@@ -561,16 +575,6 @@ static int forward_any(Engine &E, const int32_t *toks, int n, int32_t *next) {
 
 static bool pow2_range(int v) { return v >= 1024 && v <= 8192 && (v & (v - 1)) == 0; }
 
-// Whether an attention layer's decode mixer is one launch (pq_attn_layer_decode:
-// head_dim 64 or 128, any window) -- its LDS holds the split partials of the
-// whole context; otherwise q/k prep + the split-K attention pair.
-static bool mixer_fused_cfg(const pq_model_cfg &c, bool slide) {
-  (void)slide;
-  const size_t ns = ((size_t)c.ctx + 63) / 64;
-  return (c.hd == 64 || c.hd == 128) && ((size_t)c.hd + 8 * 64 + ns * (c.hd + 2)) * 4 + 2 * (size_t)c.hd * 2 <=
-                                            160 * 1024;
-}
-static bool mixer_fused(const Engine &E, const LayerDev &D) { return mixer_fused_cfg(E.c, D.slide != 0); }
 
 // Whether the fused decode kernels take this configuration: a power-of-two
 // hidden width of 1024..8192 (the fused GEMV prologues), an FFN width that is

@@ -296,11 +296,15 @@ def argmax_parts(parts, nparts):
 
 
 def attn_layer_decode(qkvg, q_norm, k_norm, rope_cs, kc, vc, pos, nh, nkv, hd, rot, scale, eps=1e-5, out=None,
-                      win=0):
-    qx = torch.empty(nh * hd, dtype=torch.int8, device=qkvg.device)
-    dx = torch.empty(nh * hd // 32, dtype=torch.float32, device=qkvg.device)
+                      win=0, quant=True):
+    """The one-launch attention mixer; returns o_proj's Q8_0 input (qx, dx), or
+    (None, None) with quant=False (then out, the bf16 output, is required)."""
+    if not quant and out is None:
+        raise ValueError("quant=False needs out")
+    qx = torch.empty(nh * hd, dtype=torch.int8, device=qkvg.device) if quant else None
+    dx = torch.empty(nh * hd // 32, dtype=torch.float32, device=qkvg.device) if quant else None
     check(lib().pq_attn_layer_decode(_bits16(qkvg), q_norm.data_ptr(), k_norm.data_ptr(), rope_cs.data_ptr(),
                                      _bits16(kc), _bits16(vc), pos, nh, nkv, hd, rot, win, eps, scale,
-                                     _bits16(out) if out is not None else None, qx.data_ptr(), dx.data_ptr(),
+                                     _bits16(out) if out is not None else None, _ptr(qx), _ptr(dx),
                                      stream_ptr()), "pq_attn_layer_decode")
     return qx, dx

@@ -124,9 +124,14 @@ MIXER_CASES = [(0, 64, 32, 8, 32, 1e6, 0), (63, 64, 32, 8, 32, 1e6, 0), (64, 64,
                (130, 64, 32, 8, 32, 1e6, 100), (40, 128, 16, 4, 128, 1e4, 1)]
 
 
-@pytest.mark.parametrize("pos,hd,nh,nkv,rot,theta,win", MIXER_CASES)
-def test_attn_layer_decode(orc, pq, dev, pos, hd, nh, nkv, rot, theta, win):
-    print(f"mixer pos={pos} hd={hd} win={win}", flush=True)
+# quant: o_proj's Q8_0 input as well as the bf16 output, or the bf16 output
+# alone (the reference-numerics engine's o_proj reads bf16); the small-head
+# cases (4 q / 2 kv heads) are the tiny test model's shapes
+@pytest.mark.parametrize("quant", [True, False], ids=["q8", "bf16"])
+@pytest.mark.parametrize("pos,hd,nh,nkv,rot,theta,win", MIXER_CASES + [(37, 64, 4, 2, 32, 1e6, 0),
+                                                                     (37, 128, 4, 2, 64, 1e6, 0)])
+def test_attn_layer_decode(orc, pq, dev, pos, hd, nh, nkv, rot, theta, win, quant):
+    print(f"mixer pos={pos} hd={hd} nh={nh} win={win} quant={quant}", flush=True)
     ctx = max(2048, pos + 1)
     nin = nh * hd + 2 * nkv * hd + nh
     kvd = nkv * hd
@@ -152,10 +157,11 @@ def test_attn_layer_decode(orc, pq, dev, pos, hd, nh, nkv, rot, theta, win):
     r2 = _t16(row, dev)
     kc2, vc2 = _t16(kc0.view(np.uint16), dev), _t16(vc0.view(np.uint16), dev)
     out2 = torch.empty(nh * hd, dtype=torch.int16, device=dev)
-    qx2, dx2 = pq.attn_layer_decode(r2, *args, kc2, vc2, pos, nh, nkv, hd, rot, 0.125, out=out2, win=win)
+    qx2, dx2 = pq.attn_layer_decode(r2, *args, kc2, vc2, pos, nh, nkv, hd, rot, 0.125, out=out2, win=win, quant=quant)
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     assert torch.equal(out1, out2)
-    assert torch.equal(qx1, qx2) and torch.equal(dx1.view(torch.int32), dx2.view(torch.int32))
+    if quant:
+        assert torch.equal(qx1, qx2) and torch.equal(dx1.view(torch.int32), dx2.view(torch.int32))
 
 
 # the synthetic backbone's layer shapes (head_dim 64, 3 taps: the one-launch
