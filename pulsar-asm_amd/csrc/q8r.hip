@@ -19,6 +19,8 @@
 // fp32 in LDS with each 32-element block padded to 36 floats, so the 16-byte
 // reads of any 8 consecutive lanes cover all 32 banks. A lane's weight loads
 // for a chunk are issued before the previous chunk's arithmetic.
+#include <algorithm>
+
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
@@ -130,6 +132,110 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_kernel(const int8_t *__res
   }
 }
 
+// The T-wide form (T > 1): the same per-output arithmetic, with each weight
+// load serving many positions. A workgroup takes 8 rows x up to kRTPW
+// positions; per chunk of K its lanes load their leaves' blocks once (CVT:
+// codes widened to fp32 once, for up to 2 blocks per leaf), then the
+// positions' x of that chunk are staged in LDS tp at a time (bf16 widened to
+// fp32, 36-float padded blocks) and every position runs the leaf chains and
+// the tree of the single-position kernel. The chunk partials of a (position,
+// row) go to an LDS running sum in chunk order, y = ((0 + p_0) + p_1) + ...
+constexpr int kRTPW = 32;      // positions per workgroup
+
+template <int BPL, bool CVT>
+__global__ __launch_bounds__(kRThreads) void q8r_gemm_kernel(const int8_t *__restrict__ codes,
+                                                             const float *__restrict__ scales,
+                                                             const uint16_t *__restrict__ x, void *__restrict__ y,
+                                                             int y_bf16, int N, int K, int T, int tp) {
+  extern __shared__ __align__(16) float rsm[];
+  const int nb = K / kQ, KC = q8r_chunk(K), nbc = KC / kQ, nch = K / KC;
+  float *ysum = rsm;                                   // [kRTPW][kRRows] running sums
+  float *xs = rsm + kRTPW * kRRows;                    // [tp][nbc][kRXStride]
+  const int wr = threadIdx.x >> 5, L = threadIdx.x & 31;
+  const int row = blockIdx.x * kRRows + wr;
+  const int t0 = blockIdx.y * kRTPW, tn = T - t0 < kRTPW ? T - t0 : kRTPW;
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(codes), (short)0, N * K, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scales), (short)0, N * nb * 4, kRsrcWord3);
+  for (int i = threadIdx.x; i < kRTPW * kRRows; i += kRThreads) ysum[i] = 0.0f;
+  for (int c = 0; c < nch; c++) {
+    RBlocks B;
+    q8r_load<BPL>(B, rc, rs, row, N, K, nb, nbc, c, L);
+    float cf[CVT ? BPL : 1][32];
+    if constexpr (CVT) {
+#pragma unroll
+      for (int i = 0; i < BPL; i++) {
+        const uint32_t w[8] = {(uint32_t)B.c[2 * i].x,     (uint32_t)B.c[2 * i].y,     (uint32_t)B.c[2 * i].z,
+                               (uint32_t)B.c[2 * i].w,     (uint32_t)B.c[2 * i + 1].x, (uint32_t)B.c[2 * i + 1].y,
+                               (uint32_t)B.c[2 * i + 1].z, (uint32_t)B.c[2 * i + 1].w};
+#pragma unroll
+        for (int k = 0; k < 32; k++) cf[i][k] = (float)(int8_t)((w[k >> 2] >> (8 * (k & 3))) & 0xffu);
+      }
+    }
+    for (int tt = 0; tt < tn; tt += tp) {
+      const int np = tn - tt < tp ? tn - tt : tp;
+      __syncthreads();   // the previous tile's reads of xs are done (and ysum is zeroed)
+      // x of positions t0+tt .. +np, chunk c: 8 bf16 per thread per step
+      for (int e = threadIdx.x * 8; e < np * KC; e += kRThreads * 8) {
+        const int p = e / KC, k = e % KC;
+        const uint4 u = *reinterpret_cast<const uint4 *>(x + (size_t)(t0 + tt + p) * K + (size_t)c * KC + k);
+        const uint32_t v[4] = {u.x, u.y, u.z, u.w};
+        float f[8];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          f[2 * q] = __uint_as_float(v[q] << 16);
+          f[2 * q + 1] = __uint_as_float(v[q] & 0xffff0000u);
+        }
+        float *d = xs + ((size_t)p * nbc + (k >> 5)) * kRXStride + (k & 31);
+        *reinterpret_cast<float4 *>(d) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4 *>(d + 4) = make_float4(f[4], f[5], f[6], f[7]);
+      }
+      __syncthreads();
+      for (int p = 0; p < np; p++) {
+        const float *xp = xs + (size_t)p * nbc * kRXStride;
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < BPL; i++) {
+          const int b = L + 32 * i;
+          // a block past the chunk has zero codes and scale: fmaf(0, 0, acc) = acc
+          const float *xb = xp + (size_t)(b < nbc ? b : 0) * kRXStride;
+          float dot = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 8; q++) {
+            const float4 x4 = *reinterpret_cast<const float4 *>(xb + 4 * q);
+            if constexpr (CVT) {
+              dot = __builtin_fmaf(cf[i][4 * q], x4.x, dot);
+              dot = __builtin_fmaf(cf[i][4 * q + 1], x4.y, dot);
+              dot = __builtin_fmaf(cf[i][4 * q + 2], x4.z, dot);
+              dot = __builtin_fmaf(cf[i][4 * q + 3], x4.w, dot);
+            } else {
+              const uint32_t w = (uint32_t)(q < 4 ? B.c[2 * i][q] : B.c[2 * i + 1][q - 4]);
+              dot = __builtin_fmaf((float)(int8_t)(w & 0xffu), x4.x, dot);
+              dot = __builtin_fmaf((float)(int8_t)((w >> 8) & 0xffu), x4.y, dot);
+              dot = __builtin_fmaf((float)(int8_t)((w >> 16) & 0xffu), x4.z, dot);
+              dot = __builtin_fmaf((float)(int8_t)(w >> 24), x4.w, dot);
+            }
+          }
+          acc = __builtin_fmaf(B.s[i], dot, acc);
+        }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) acc = acc + __shfl_down(acc, o, 32);
+        if (L == 0) ysum[(tt + p) * kRRows + wr] += acc;
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < tn * kRRows; i += kRThreads) {
+    const int t = i / kRRows, r = blockIdx.x * kRRows + i % kRRows;
+    if (r < N) {
+      const float v = ysum[i];
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)(t0 + t) * N + r] = f2bf(v);
+      else reinterpret_cast<float *>(y)[(size_t)(t0 + t) * N + r] = v;
+    }
+  }
+}
+
 }  // namespace pq
 
 using namespace pq;
@@ -147,9 +253,27 @@ extern "C" int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint1
   PQ_REQUIRE((long long)N * K < (1ll << 31), PQ_ERR_ARG, "pq_q8r_gemv: N=%d K=%d too large", N, K);
   const size_t lds = (size_t)(K / kQ) * kRXStride * sizeof(float);
   PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_q8r_gemv: K=%d too large for LDS", K);
-  const dim3 grid((unsigned)((N + kRRows - 1) / kRRows), (unsigned)T), block(kRThreads);
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
   hipStream_t st = as_stream(stream);
+  static const int env_t = env_int("PQ_Q8R_POSWISE");   // 1: one position per workgroup row at any T
+  if (T > 1 && env_t != 1) {   // the T-wide form: each weight load serves up to 32 positions
+    // positions per LDS tile: as many 36-float padded chunks as fit 18 KB, at most 8 (small tiles keep
+    // several workgroups per CU: a 256-token prompt through 24 layers of hidden 2048 / FFN 8192 takes
+    // 41 ms with 72 KB tiles, 25 ms with 18 KB)
+    const size_t per = (size_t)(KC / kQ) * kRXStride * sizeof(float);
+    static const int env_kb = env_int("PQ_Q8R_TILE_KB");
+    const size_t budget = (size_t)(env_kb > 0 ? env_kb : 18) * 1024;
+    const int tp = (int)std::min<size_t>(8, std::max<size_t>(1, budget / per));
+    const size_t lds_t = (size_t)kRTPW * kRRows * sizeof(float) + (size_t)tp * per;
+    PQ_REQUIRE(lds_t <= kMaxLds, PQ_ERR_ARG, "pq_q8r_gemv: K=%d too large for LDS", K);
+    const dim3 gt((unsigned)((N + kRRows - 1) / kRRows), (unsigned)((T + kRTPW - 1) / kRTPW)), bt(kRThreads);
+    if (bpl <= 1) launch(q8r_gemm_kernel<1, true>, gt, bt, lds_t, st, codes, scales, x, y, yb, N, K, T, tp);
+    else if (bpl <= 2) launch(q8r_gemm_kernel<2, true>, gt, bt, lds_t, st, codes, scales, x, y, yb, N, K, T, tp);
+    else if (bpl <= 4) launch(q8r_gemm_kernel<4, false>, gt, bt, lds_t, st, codes, scales, x, y, yb, N, K, T, tp);
+    else launch(q8r_gemm_kernel<8, false>, gt, bt, lds_t, st, codes, scales, x, y, yb, N, K, T, tp);
+    return check_launch("pq_q8r_gemv");
+  }
+  const dim3 grid((unsigned)((N + kRRows - 1) / kRRows), (unsigned)T), block(kRThreads);
   if (bpl <= 1) launch(q8r_gemv_kernel<1>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
   else if (bpl <= 2) launch(q8r_gemv_kernel<2>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
   else if (bpl <= 4) launch(q8r_gemv_kernel<4>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
