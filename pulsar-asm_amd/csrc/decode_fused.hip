@@ -446,236 +446,310 @@ __global__ __launch_bounds__(1024) void argmax_parts_kernel(const float *__restr
 
 // --------------------------------------------------------- attention mixer
 // One workgroup of 8 waves per q head hq (kv head g = hq / G) at T=1, position
-// pos (keys 0..pos). Wave w owns splits w, w+8, ... (64 positions each).
-// Every global load a wave needs for its first split is issued before
-// anything waits: the step-1 inputs, then the K and V blocks of its split,
-// 8 lanes per 128-byte row (whole cache lines per load), through buffer
+// pos (keys lo..pos, lo = pos + 1 - win for a sliding window). Wave w owns the
+// splits j0 + w, j0 + w + 8, ... (64 positions each, j0 = lo / 64). Every
+// global load a wave needs for its first split is issued before anything
+// waits: the step-1 inputs, the gate, then the K and V blocks of its split, 8
+// lanes per 128-byte row slice (whole cache lines per load), through buffer
 // resources that end at position pos (rows >= pos read zeros, no branch).
 //  1. wave 0 norms + ropes q into LDS; wave 1 norms + ropes k, wave 2 rounds
 //     v, both into LDS as fp16 bits and (workgroup G*g only) to the cache.
-//  2. per split: K goes through LDS so lane p holds key p: s = q.k (fmaf
-//     chain over d), m, e, l as attn_split_kernel; then V goes through the same
-//     LDS buffer so lane d runs the fmaf chain over positions for o.
+//  2. per split, per 64-dim slice of the head: the K slice goes through LDS
+//     so lane p holds key p (s = q.k, one fmaf chain over d ascending), then
+//     m, e, l; each V slice goes through the same LDS buffer so lane d runs
+//     the fmaf chain over positions for o of dim d (+ 64 per slice).
 //  3. wave 0 merges the splits in ascending order, applies the sigmoid gate
-//     and writes the head's Q8_0 blocks of o_proj's input.
-constexpr int kHDf = 64;
-constexpr int kPartf = kHDf + 2;
-constexpr int kSplitF = 64;       // positions per attention split
-constexpr int kVRow = kHDf + 8;   // padded fp16 row of a K/V block in LDS
+//     and writes the head's bf16 output and/or o_proj's Q8_0 blocks.
+constexpr int kSplitF = 64;   // positions per attention split
+constexpr int kVRow = 64 + 8;  // padded fp16 row of a 64-dim K/V block slice in LDS
 
-// q/k head norm + RoPE of one head (lane d holds x_d, its norm weight wd and
-// the RoPE (cos, sin) of its pair index d mod 32), the arithmetic of
-// qk_prep_kernel.
-__device__ __forceinline__ float qk_norm_rope(float x, float wd, float2 csv, int rot, float eps, int d) {
-  const float ss = wave_pairwise_sum(x * x);
-  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)kHDf) + eps);
-  float v = bf2f(f2bf(wd * bf2f(f2bf(x * rs))));
-  const int half = rot / 2;
-  const float up = __shfl_down(v, kHDf / 2, 64);
-  const float dn = __shfl_up(v, kHDf / 2, 64);
-  if (d < kHDf / 2 && d < half) {
-    v = v * csv.x - up * csv.y;
-  } else if (d >= kHDf / 2 && d - kHDf / 2 < half) {
-    v = v * csv.x + dn * csv.y;
+// q/k head norm + RoPE from preloaded inputs: x[e] and wv[e] are element
+// lane + 64e of the head and of its norm weight, (c, sn) the cos/sin of the
+// lane's RoPE pair: pair lane & 31 for head_dim 64 (elements i and i + 32
+// sit in lanes i and i + 32), pair lane for head_dim 128 (elements lane and
+// lane + 64 in one lane). The arithmetic of qk_prep_kernel.
+template <int HD>
+__device__ __forceinline__ void norm_rope(const float *x, const float *wv, float c, float sn, int rot, float eps,
+                                          int lane, float *r) {
+  constexpr int E = HD / 64;
+  float ss = 0.0f, v[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    const float part = wave_pairwise_sum(x[e] * x[e]);
+    ss = e == 0 ? part : ss + part;
   }
-  return bf2f(f2bf(v));
+  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)HD) + eps);
+#pragma unroll
+  for (int e = 0; e < E; e++) v[e] = bf2f(f2bf(wv[e] * bf2f(f2bf(x[e] * rs))));
+  const int half = rot / 2;
+  if constexpr (HD == 64) {
+    const float up = __shfl_down(v[0], 32, 64);
+    const float dn = __shfl_up(v[0], 32, 64);
+    r[0] = v[0];
+    if ((lane & 31) < half) r[0] = lane < 32 ? v[0] * c - up * sn : v[0] * c + dn * sn;
+  } else {
+    r[0] = v[0];
+    r[1] = v[1];
+    if (lane < half) {
+      r[0] = v[0] * c - v[1] * sn;
+      r[1] = v[1] * c + v[0] * sn;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; e++) r[e] = bf2f(f2bf(r[e]));
 }
 
+// the amax of each 32-lane half of a wave (one Q8_0 block): DPP within
+// 16-lane rows, then the row-pair swap
+__device__ __forceinline__ float block_amax(float v) {
+  float a = fabsf(v);
+  a = fmaxf(a, dpp_f<kDppXor1>(a));
+  a = fmaxf(a, dpp_f<kDppXor2>(a));
+  a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
+  a = fmaxf(a, dpp_f<kDppMirror>(a));
+  return max_row_pair(a);
+}
+
+template <int HD>
 __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restrict__ qkvg, const float *__restrict__ qn,
                                                          const float *__restrict__ kn, const float *__restrict__ cs,
                                                          uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
                                                          int pos_arg, const int32_t *__restrict__ pos_dev, int nh,
-                                                         int nkv, int rot, float eps, float scale,
+                                                         int nkv, int rot, int win, float eps, float scale,
                                                          uint16_t *__restrict__ out, int8_t *__restrict__ qx,
                                                          float *__restrict__ dx) {
+  constexpr int E = HD / 64, PART = HD + 2;
   extern __shared__ __align__(16) unsigned char smem[];
-  float *qs = reinterpret_cast<float *>(smem);                    // [64] q
-  float *ew = qs + kHDf;                                           // [8 waves][64] e
-  uint16_t *kvnew = reinterpret_cast<uint16_t *>(ew + 8 * kSplitF);  // [2][64] fp16 k, v at pos
-  uint16_t *blk = kvnew + 2 * kHDf;                                // [8 waves][64][kVRow] K, then V
-  float *st = reinterpret_cast<float *>(blk + 8 * kSplitF * kVRow);  // [nsplit][66]
+  float *qs = reinterpret_cast<float *>(smem);                      // [HD] q
+  float *ew = qs + HD;                                               // [8 waves][64] e
+  uint16_t *kvnew = reinterpret_cast<uint16_t *>(ew + 8 * kSplitF);  // [2][HD] fp16 k, v at pos
+  uint16_t *blk = kvnew + 2 * HD;                                    // [8 waves][64][kVRow] K, then V slices
+  float *st = reinterpret_cast<float *>(blk + 8 * kSplitF * kVRow);  // [nsplit][HD + 2]
   const int pos = pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_arg;
   const int hq = blockIdx.x, G = nh / nkv, g = hq / G;
   const bool writer = hq % G == 0;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int kvd = nkv * kHDf;
+  const int kvd = nkv * HD;
   const int npos = pos + 1;
-  const int ns = (npos + kSplitF - 1) / kSplitF;
+  const int lo = window_lo(npos, win);
+  const int j0 = lo / kSplitF, ns = (npos + kSplitF - 1) / kSplitF;
   const int half = rot / 2;
   // step-1 and step-3 inputs: wave 0 q, wave 1 k, others v (valid addresses)
-  const int xoff = wave == 0 ? hq * kHDf : wave == 1 ? nh * kHDf + g * kHDf : nh * kHDf + kvd + g * kHDf;
-  const uint16_t xraw = qkvg[xoff + lane];
-  const float wd = (wave == 1 ? kn : qn)[lane];
+  const int xoff = wave == 0 ? hq * HD : wave == 1 ? nh * HD + g * HD : nh * HD + kvd + g * HD;
+  uint16_t xraw[E];
+  float wv[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    xraw[e] = qkvg[xoff + lane + 64 * e];
+    wv[e] = (wave == 1 ? kn : qn)[lane + 64 * e];
+  }
+  const int pair = HD == 64 ? (lane & 31) : lane;
   const __amdgpu_buffer_rsrc_t rcs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(cs), (short)0, (pos + 1) * half * 8, kRsrcWord3);
-  const v2i csw = __builtin_amdgcn_raw_buffer_load_b64(
-      rcs, (pos * half + max(0, min(lane & (kHDf / 2 - 1), half - 1))) * 8, 0, 0);
-  const float2 csv = make_float2(__int_as_float(csw.x), __int_as_float(csw.y));
-  const uint16_t graw = qkvg[nh * kHDf + 2 * kvd + hq];
-  // K, V blocks of split J: lane l loads 16 B (chunk l%8) of rows 8i + l/8
+  const v2i csw = __builtin_amdgcn_raw_buffer_load_b64(rcs, (pos * half + max(0, min(pair, half - 1))) * 8, 0, 0);
+  const uint16_t graw = qkvg[nh * HD + 2 * kvd + hq];
+  // K, V blocks of split J: slice h, lane l loads 16 B (chunk l%8) of rows 8i + l/8
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kc, (short)0, pos * kvd * 2, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vc, (short)0, pos * kvd * 2, kRsrcWord3);
   const int lr = lane >> 3, lc = lane & 7;
-  v4i kr[8], vr[8];
-#define PQ_LOAD_BLOCKS(J)                                                                              \
-  {                                                                                                    \
-    const int off_ = (((J) * kSplitF + lr) * kvd + g * kHDf) * 2 + lc * 16;                          \
-    _Pragma("unroll") for (int i = 0; i < 8; i++) kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off_ + i * 8 * kvd * 2, 0, 0); \
-    _Pragma("unroll") for (int i = 0; i < 8; i++) vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off_ + i * 8 * kvd * 2, 0, 0); \
-  }
-  PQ_LOAD_BLOCKS(wave)
-  // 1. q/k norm + rope, KV write
-  const float x1 = bf2f(xraw);
+  v4i kr[E][8], vr[E][8];
+  auto load_blocks = [&](int J) {
+    const int off = ((J * kSplitF + lr) * kvd + g * HD) * 2 + lc * 16;
+#pragma unroll
+    for (int h = 0; h < E; h++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) kr[h][i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off + h * 128 + i * 8 * kvd * 2, 0, 0);
+#pragma unroll
+    for (int h = 0; h < E; h++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) vr[h][i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off + h * 128 + i * 8 * kvd * 2, 0, 0);
+  };
+  __builtin_amdgcn_sched_barrier(0);   // the step-1 inputs' loads first,
+  load_blocks(j0 + wave);
+  __builtin_amdgcn_sched_barrier(0);   // and every load is issued before anything waits
+  // 1. q/k norm + rope, KV write. The empty asm uses the norm weights and
+  //    the RoPE pair in every wave, so that their loads stay ahead of the K/V
+  //    loads in issue order (a wait for them leaves the K/V loads in flight).
+#pragma unroll
+  for (int e = 0; e < E; e++) asm volatile("" ::"v"(wv[e]));
+  asm volatile("" ::"v"(csw.x), "v"(csw.y));
+  float x1[E], r[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) x1[e] = bf2f(xraw[e]);
+  if (wave < 2) norm_rope<HD>(x1, wv, __int_as_float(csw.x), __int_as_float(csw.y), rot, eps, lane, r);
   if (wave == 0) {
-    qs[lane] = qk_norm_rope(x1, wd, csv, rot, eps, lane);
+#pragma unroll
+    for (int e = 0; e < E; e++) qs[lane + 64 * e] = r[e];
   } else if (wave == 1) {
-    const uint16_t k = f2h(qk_norm_rope(x1, wd, csv, rot, eps, lane));
-    if (writer) kc[(size_t)pos * kvd + g * kHDf + lane] = k;
-    kvnew[lane] = k;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      const uint16_t k = f2h(r[e]);
+      if (writer) kc[(size_t)pos * kvd + g * HD + lane + 64 * e] = k;
+      kvnew[lane + 64 * e] = k;
+    }
   } else if (wave == 2) {
-    const uint16_t v = f2h(x1);
-    if (writer) vc[(size_t)pos * kvd + g * kHDf + lane] = v;
-    kvnew[kHDf + lane] = v;
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+      const uint16_t v = f2h(x1[e]);
+      if (writer) vc[(size_t)pos * kvd + g * HD + lane + 64 * e] = v;
+      kvnew[HD + lane + 64 * e] = v;
+    }
   }
   lds_barrier();
   // 2. splits
   float *eww = ew + wave * kSplitF;
   uint16_t *bw = blk + wave * kSplitF * kVRow;
-  for (int j = wave; j < ns; j += 8) {
-    if (j != wave) PQ_LOAD_BLOCKS(j)
+  for (int j = j0 + wave; j < ns; j += 8) {
+    if (j != j0 + wave) load_blocks(j);
     const int p0 = j * kSplitF;
     const int pn = npos - p0 < kSplitF ? npos - p0 : kSplitF;
-    const bool valid = lane < pn;
-    // K block -> LDS -> lane p's row (the row at pos from kvnew)
-#pragma unroll
-    for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = kr[i];
-    const uint16_t *krow = p0 + lane == pos ? kvnew : bw + lane * kVRow;
-    float kf[kHDf];
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-      const v4i w4 = *reinterpret_cast<const v4i *>(krow + 8 * q);
-      const uint32_t kw[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
-#pragma unroll
-      for (int i = 0; i < 8; i++) kf[8 * q + i] = h2f((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
-    }
-    float4 q4[kHDf / 4];
-#pragma unroll
-    for (int i = 0; i < kHDf / 4; i++) q4[i] = reinterpret_cast<const float4 *>(qs)[i];
+    const int i0 = lo > p0 ? lo - p0 : 0;
+    const bool valid = lane >= i0 && lane < pn;
+    // K slices -> LDS -> lane p's row (the row at pos from kvnew); one chain over d
     float d = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kHDf / 4; i++) {
-      d = __builtin_fmaf(q4[i].x, kf[4 * i], d);
-      d = __builtin_fmaf(q4[i].y, kf[4 * i + 1], d);
-      d = __builtin_fmaf(q4[i].z, kf[4 * i + 2], d);
-      d = __builtin_fmaf(q4[i].w, kf[4 * i + 3], d);
+    for (int h = 0; h < E; h++) {
+      if (h > 0) {   // the previous slice's reads precede this slice's writes
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = kr[h][i];
+      const uint16_t *krow = p0 + lane == pos ? kvnew + 64 * h : bw + lane * kVRow;
+      float kf[64];
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const v4i w4 = *reinterpret_cast<const v4i *>(krow + 8 * q);
+        const uint32_t kw[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) kf[8 * q + i] = h2f((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
+      }
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float4 q4 = reinterpret_cast<const float4 *>(qs + 64 * h)[i];
+        d = __builtin_fmaf(q4.x, kf[4 * i], d);
+        d = __builtin_fmaf(q4.y, kf[4 * i + 1], d);
+        d = __builtin_fmaf(q4.z, kf[4 * i + 2], d);
+        d = __builtin_fmaf(q4.w, kf[4 * i + 3], d);
+      }
     }
     const float sc = valid ? d * scale : -__builtin_inff();
     const float m = wave_max(sc);
     const float e = valid ? expf_pq(sc - m) : 0.0f;
     const float l = wave_pairwise_sum(e);
     eww[lane] = e;
-    // V block -> the same LDS buffer (this wave's K reads precede it in LDS
-    // order); the row at pos from kvnew
+    float *sj = st + (size_t)j * PART;
 #pragma unroll
-    for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = vr[i];
-    if (pos - p0 < kSplitF && lane < 8)
-      *reinterpret_cast<v4i *>(bw + (pos - p0) * kVRow + lane * 8) = reinterpret_cast<const v4i *>(kvnew + kHDf)[lane];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    // o = sum_p e[p] v[p][lane] (fmaf chain over p < pn), 16 positions per
-    // batch, the next batch's LDS reads issued before this batch's fmafs (rows
-    // past pn are read but not used; e[p] = 0 there)
-    float o = 0.0f;
-    {
-      uint16_t vb[16];
-      float4 e4[4];
+    for (int h = 0; h < E; h++) {
+      // V slice h -> the same LDS buffer (this wave's earlier reads of it
+      // precede it in LDS order); the row at pos from kvnew
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int i = 0; i < 16; i++) vb[i] = bw[i * kVRow + lane];
+      for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = vr[h][i];
+      if (pos - p0 < kSplitF && lane < 8)
+        *reinterpret_cast<v4i *>(bw + (pos - p0) * kVRow + lane * 8) =
+            reinterpret_cast<const v4i *>(kvnew + HD + 64 * h)[lane];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      // o = sum_p e[p] v[p][64h + lane] (fmaf chain over i0 <= p < pn), 16
+      // positions per batch, the next batch's LDS reads issued before this
+      // batch's fmafs. Rows past pos read as zeros (the buffer bound) with
+      // e = 0, and fmaf(0, +0, o) = o, so the last batch runs whole; rows
+      // below i0 (the window's first split) are skipped, a cache row there
+      // may hold an fp16 infinity
+      auto vchain = [&](auto FULL) {
+        float o = 0.0f;
+        uint16_t vb[16];
+        float4 e4[4];
 #pragma unroll
-      for (int k = 0; k < 4; k++) e4[k] = reinterpret_cast<const float4 *>(eww)[k];
-      for (int b0 = 0; b0 < pn; b0 += 16) {
-        const int nb0 = b0 + 16 < kSplitF ? b0 + 16 : b0;
-        uint16_t vn[16];
-        float4 en[4];
+        for (int i = 0; i < 16; i++) vb[i] = bw[i * kVRow + lane];
 #pragma unroll
-        for (int i = 0; i < 16; i++) vn[i] = bw[(nb0 + i) * kVRow + lane];
+        for (int k = 0; k < 4; k++) e4[k] = reinterpret_cast<const float4 *>(eww)[k];
+        for (int b0 = 0; b0 < pn; b0 += 16) {
+          const int nb0 = b0 + 16 < kSplitF ? b0 + 16 : b0;
+          uint16_t vn[16];
+          float4 en[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) en[k] = reinterpret_cast<const float4 *>(eww + nb0)[k];
+          for (int i = 0; i < 16; i++) vn[i] = bw[(nb0 + i) * kVRow + lane];
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-          if (b0 + i < pn) {
-            const float4 &q = e4[i >> 2];
-            const float ei = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
-            o = __builtin_fmaf(ei, h2f(vb[i]), o);
-          }
+          for (int k = 0; k < 4; k++) en[k] = reinterpret_cast<const float4 *>(eww + nb0)[k];
 #pragma unroll
-        for (int i = 0; i < 16; i++) vb[i] = vn[i];
+          for (int i = 0; i < 16; i++)
+            if (FULL || b0 + i >= i0) {
+              const float4 &q = e4[i >> 2];
+              const float ei = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+              o = __builtin_fmaf(ei, h2f(vb[i]), o);
+            }
 #pragma unroll
-        for (int k = 0; k < 4; k++) e4[k] = en[k];
-      }
+          for (int i = 0; i < 16; i++) vb[i] = vn[i];
+#pragma unroll
+          for (int k = 0; k < 4; k++) e4[k] = en[k];
+        }
+        return o;
+      };
+      const float o = i0 == 0 ? vchain(std::true_type{}) : vchain(std::false_type{});
+      sj[64 * h + lane] = o;
     }
-    float *sj = st + (size_t)j * kPartf;
-    sj[lane] = o;
     if (lane == 0) {
-      sj[kHDf] = m;
-      sj[kHDf + 1] = l;
+      sj[HD] = m;
+      sj[HD + 1] = l;
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
   }
-#undef PQ_LOAD_BLOCKS
   lds_barrier();
-  // 3. merge, gate, Q8_0 out
+  // 3. merge, gate, outputs
   if (wave == 0) {
     // M = max m_j; w_j = e^(m_j - M) for 64 splits at a time, one per lane;
     // then L and O as fmaf chains over j ascending (w_j, l_j by v_readlane)
     float M = -__builtin_inff();
-    for (int j0 = 0; j0 < ns; j0 += 64)
-      M = fmaxf(M, wave_max(j0 + lane < ns ? st[(size_t)(j0 + lane) * kPartf + kHDf] : -__builtin_inff()));
-    float L = 0.0f, O = 0.0f;
-    for (int j0 = 0; j0 < ns; j0 += 64) {
-      const int jl = j0 + lane < ns ? j0 + lane : ns - 1;
-      const float w = expf_pq(st[(size_t)jl * kPartf + kHDf] - M);
-      const float lj = st[(size_t)jl * kPartf + kHDf + 1];
-      const int n = ns - j0 < 64 ? ns - j0 : 64;
-      for (int b = 0; b < n; b += 8) {
-        float oj[8];
+    for (int jb = j0; jb < ns; jb += 64)
+      M = fmaxf(M, wave_max(jb + lane < ns ? st[(size_t)(jb + lane) * PART + HD] : -__builtin_inff()));
+    float L = 0.0f, O[E];
 #pragma unroll
-        for (int i = 0; i < 8; i++) oj[i] = st[(size_t)(j0 + (b + i < n ? b + i : 0)) * kPartf + lane];
+    for (int h = 0; h < E; h++) O[h] = 0.0f;
+    for (int jb = j0; jb < ns; jb += 64) {
+      const int jl = jb + lane < ns ? jb + lane : ns - 1;
+      const float w = expf_pq(st[(size_t)jl * PART + HD] - M);
+      const float lj = st[(size_t)jl * PART + HD + 1];
+      const int n = ns - jb < 64 ? ns - jb : 64;
+      for (int b = 0; b < n; b += 8) {
+        float oj[8][E];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+          for (int h = 0; h < E; h++) oj[i][h] = st[(size_t)(jb + (b + i < n ? b + i : 0)) * PART + 64 * h + lane];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 8; i++)
           if (b + i < n) {
             const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b + i));
             L = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj), b + i)), wi, L);
-            O = __builtin_fmaf(oj[i], wi, O);
+#pragma unroll
+            for (int h = 0; h < E; h++) O[h] = __builtin_fmaf(oj[i][h], wi, O[h]);
           }
       }
     }
-    uint16_t rb = f2bf(O / L);
     const float gs = 1.0f / (1.0f + expf_pq(-bf2f(graw)));
-    rb = f2bf(bf2f(rb) * gs);
-    if (out != nullptr) out[hq * kHDf + lane] = rb;
-    if (qx != nullptr) {   // the Q8_0 blocks of o_proj's input (a caller may ask for bf16 only)
-      const float v = bf2f(rb);
-      // amax over each 32-lane half (one Q8_0 block): DPP within 16-lane rows,
-      // then the row-pair swap
-      float a = fabsf(v);
-      a = fmaxf(a, dpp_f<kDppXor1>(a));
-      a = fmaxf(a, dpp_f<kDppXor2>(a));
-      a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
-      a = fmaxf(a, dpp_f<kDppMirror>(a));
-      a = max_row_pair(a);
-      const float dq = a / 127.0f;
-      qx[hq * kHDf + lane] = (int8_t)q8_code(Q8Div(dq).div(v));
-      if ((lane & 31) == 0) dx[(hq * kHDf + lane) / 32] = dq;
+#pragma unroll
+    for (int h = 0; h < E; h++) {
+      const int dd = hq * HD + 64 * h + lane;
+      const uint16_t rb = f2bf(bf2f(f2bf(O[h] / L)) * gs);
+      if (out != nullptr) out[dd] = rb;
+      if (qx != nullptr) {   // the Q8_0 blocks of o_proj's input (a caller may ask for bf16 only)
+        const float v = bf2f(rb);
+        const float dq = block_amax(v) / 127.0f;
+        qx[dd] = (int8_t)q8_code(Q8Div(dq).div(v));
+        if ((lane & 31) == 0) dx[dd / 32] = dq;
+      }
     }
   }
 }
 
 // ------------------------------------- attention mixer, head_dim 64 or 128
 // The one-launch decode mixer for the shapes attn_head_kernel does not take
-// (head_dim 128, sliding windows): the arithmetic of qk_prep_kernel +
+// (GQA group 8, or contexts whose splits overflow its LDS): the arithmetic of qk_prep_kernel +
 // attn_split_kernel + attn_merge_kernel in one workgroup of 8 waves per q
 // head. Waves 0-2 form q (norm + RoPE from the layer's table), k (norm + RoPE,
 // fp16, written to the cache by the group's first workgroup) and v; wave w
@@ -690,36 +764,16 @@ __device__ __forceinline__ void mixer_norm_rope(const float *x, const float *__r
                                                 const float *__restrict__ cs, int pos, int rot, float eps, int lane,
                                                 float *r) {
   constexpr int E = HD / 64;
-  float ss = 0.0f, v[E];
+  float wv[E];
 #pragma unroll
-  for (int e = 0; e < E; e++) {
-    const float part = wave_pairwise_sum(x[e] * x[e]);
-    ss = e == 0 ? part : ss + part;
+  for (int e = 0; e < E; e++) wv[e] = w[lane + 64 * e];
+  const int half = rot / 2, pair = HD == 64 ? (lane & 31) : lane;
+  float c = 0.0f, sn = 0.0f;
+  if (pair < half) {
+    c = cs[((size_t)pos * half + pair) * 2];
+    sn = cs[((size_t)pos * half + pair) * 2 + 1];
   }
-  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)HD) + eps);
-#pragma unroll
-  for (int e = 0; e < E; e++) v[e] = bf2f(f2bf(w[lane + 64 * e] * bf2f(f2bf(x[e] * rs))));
-  const int half = rot / 2;
-  if constexpr (HD == 64) {
-    const float up = __shfl_down(v[0], 32, 64);
-    const float dn = __shfl_up(v[0], 32, 64);
-    const int i = lane & 31;
-    r[0] = v[0];
-    if (i < half) {
-      const float c = cs[((size_t)pos * half + i) * 2], sn = cs[((size_t)pos * half + i) * 2 + 1];
-      r[0] = lane < 32 ? v[0] * c - up * sn : v[0] * c + dn * sn;
-    }
-  } else {
-    r[0] = v[0];
-    r[1] = v[1];
-    if (lane < half) {
-      const float c = cs[((size_t)pos * half + lane) * 2], sn = cs[((size_t)pos * half + lane) * 2 + 1];
-      r[0] = v[0] * c - v[1] * sn;
-      r[1] = v[1] * c + v[0] * sn;
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < E; e++) r[e] = bf2f(f2bf(r[e]));
+  norm_rope<HD>(x, wv, c, sn, rot, eps, lane, r);
 }
 
 template <int HD>
@@ -1055,13 +1109,17 @@ static int attn_layer(const uint16_t *qkvg, const float *q_norm, const float *k_
   PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "pq_attn_layer_decode: cache alignment");
   const int G = nh / nkv;
   const int ns = (ctx + kSplitF - 1) / kSplitF;   // LDS for the splits of positions 0..ctx-1
-  if (hd == kHDf && win == 0 && (G == 1 || G == 2 || G == 4)) {
-    // head_dim 64, full attention: the K/V blocks pass through LDS (attn_head_kernel)
-    const size_t lds = ((size_t)kHDf + 8 * (size_t)kSplitF + (size_t)ns * kPartf) * 4 +
-                       (2 * (size_t)kHDf + 8 * (size_t)kSplitF * kVRow) * 2;
+  if (G == 1 || G == 2 || G == 4) {
+    // the K/V blocks pass through LDS (attn_head_kernel)
+    const size_t lds = ((size_t)hd + 8 * (size_t)kSplitF + (size_t)ns * (hd + 2)) * 4 +
+                       (2 * (size_t)hd + 8 * (size_t)kSplitF * kVRow) * 2;
     if (lds <= kMaxLds) {
-      launch(attn_head_kernel, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos,
-             pos_dev, nh, nkv, rot, eps, scale, out, qx, dx);
+      if (hd == 64)
+        launch(attn_head_kernel<64>, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache, pos,
+               pos_dev, nh, nkv, rot, win, eps, scale, out, qx, dx);
+      else
+        launch(attn_head_kernel<128>, dim3(nh), dim3(512), lds, st, qkvg, q_norm, k_norm, rope_cs, kcache, vcache,
+               pos, pos_dev, nh, nkv, rot, win, eps, scale, out, qx, dx);
       return check_launch("pq_attn_layer_decode");
     }
   }
