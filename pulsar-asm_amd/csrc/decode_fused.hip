@@ -120,6 +120,18 @@ __device__ __forceinline__ void store_q8_lds(const uint32_t *w, int e0, int8_t *
   }
 }
 
+// The max over each aligned group of L lanes (L a power of two, 1..32), by
+// DPP within 16-lane rows and the row-pair swap (all 64 lanes active).
+template <int L>
+__device__ __forceinline__ float group_max(float a) {
+  if constexpr (L >= 2) a = fmaxf(a, dpp_f<kDppXor1>(a));
+  if constexpr (L >= 4) a = fmaxf(a, dpp_f<kDppXor2>(a));
+  if constexpr (L >= 8) a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
+  if constexpr (L >= 16) a = fmaxf(a, dpp_f<kDppMirror>(a));
+  if constexpr (L >= 32) a = max_row_pair(a);
+  return a;
+}
+
 // Q8_0 of the thread's E values (elements e0 .. e0+E-1) into the staged-x
 // layout in LDS (chunk c at c*kXStride, block i of the chunk at i*32) and dxs:
 // amax over the block's 32/E threads, d = amax/127, q = rne(x/d) clamped.
@@ -128,8 +140,7 @@ __device__ __forceinline__ void quant_lds(const float *v, int e0, int8_t *xs, fl
   float a = 0.0f;
 #pragma unroll
   for (int i = 0; i < E; i++) a = fmaxf(a, fabsf(v[i]));
-#pragma unroll
-  for (int o = 1; o < 32 / E; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  a = group_max<32 / E>(a);
   const float d = a / 127.0f;
   const Q8Div qd(d);
   uint32_t w[E / 4];
