@@ -130,6 +130,7 @@ __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+constexpr int kDppRowShr1 = 0x111;   // lane i takes lane i - 1 of its 16-lane row
 
 // v + (the value of the other 16-lane row of the pair), rows uniform
 __device__ __forceinline__ float add_row_pair(float v) {

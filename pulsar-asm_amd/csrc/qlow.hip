@@ -153,34 +153,35 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
     sr[k] = __builtin_amdgcn_raw_buffer_load_b128(
         rsc, i < G * HQ ? ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4 : kRsrcOob, 0, 0);
   }
-  // x widened into LDS, then each group's sum of x in order
+  // x widened into LDS, and each group's sum of x in order from 0: a group's
+  // 32 elements are the 8-element pieces of 4 adjacent lanes (K is a multiple
+  // of 256), so lane j of the 4 continues the chain of lane j - 1 (a row shift
+  // by one lane) and the group's last lane holds the sum
 #pragma unroll
   for (int it = 0; it < kXLoads; it++) {
     const int e = tid * 8 + it * NT * 8;
-    if (e < K) {
-      const uint32_t vv[4] = {xr[it].x, xr[it].y, xr[it].z, xr[it].w};
-      float f[8];
+    const uint32_t vv[4] = {xr[it].x, xr[it].y, xr[it].z, xr[it].w};
+    float f[8];
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        f[2 * k] = __uint_as_float(vv[k] << 16);
-        f[2 * k + 1] = __uint_as_float(vv[k] & 0xffff0000u);
-      }
+    for (int k = 0; k < 4; k++) {
+      f[2 * k] = __uint_as_float(vv[k] << 16);
+      f[2 * k + 1] = __uint_as_float(vv[k] & 0xffff0000u);
+    }
+    if (e < K) {
       *reinterpret_cast<float4 *>(xs + e) = make_float4(f[0], f[1], f[2], f[3]);
       *reinterpret_cast<float4 *>(xs + e + 4) = make_float4(f[4], f[5], f[6], f[7]);
     }
-  }
-  __syncthreads();
-  for (int g = tid; g < G; g += NT) {
-    float xv[kQ];
+    float c = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kQ; k += 4) {
-      const float4 q = *reinterpret_cast<const float4 *>(xs + g * kQ + k);
-      xv[k] = q.x; xv[k + 1] = q.y; xv[k + 2] = q.z; xv[k + 3] = q.w;
+    for (int k = 0; k < 8; k++) c = c + f[k];
+#pragma unroll
+    for (int j = 1; j < 4; j++) {
+      float cj = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), kDppRowShr1, 0xf, 0xf, false));
+#pragma unroll
+      for (int k = 0; k < 8; k++) cj = cj + f[k];
+      if ((tid & 3) == j) c = cj;
     }
-    float t = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kQ; k++) t += xv[k];
-    sx[g] = t;
+    if ((tid & 3) == 3 && e < K) sx[e / kQ] = c;
   }
   __syncthreads();
   // group partials acc - sg, PF groups of loads in flight
