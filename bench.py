@@ -242,7 +242,7 @@ def cpu_ternary(shapes, seconds):
 
 
 def cpu_backbone(cfg, n_prompt=8, n_steps=12):
-    """The oracle's 24-layer backbone (this build's C restatement, OpenMP over
+    """The oracle's 24-layer backbone (the C restatement, OpenMP over
     GEMV rows): decode tok/s after a short prompt. A port, not the reference's
     code: the reference's x86 LFM3 engine is a stub."""
     import numpy as np

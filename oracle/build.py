@@ -8,7 +8,7 @@ Outputs:
                                  the reference sources where they lie:
                                  .auto/lfm3/q8_gemv_cpu.c (needs _Float16 -> ROCm clang)
                                  pulsar_arm/bonsai2/pq2_host.c
-Both directories are git-ignored and travel with the tree to the GPU box.
+Both directories are git-ignored and travel with the tree to a GPU machine.
 """
 import os
 import subprocess
@@ -39,7 +39,7 @@ def build_oracle():
 
 def build_ref():
     """Compile the reference's CPU routines; returns the path or None when the
-    reference tree is absent (the GPU box uses the prebuilt file)."""
+    reference tree is absent (a machine without it uses the prebuilt file)."""
     q8 = os.path.join(REF_ROOT, ".auto/lfm3/q8_gemv_cpu.c")
     pq2 = os.path.join(REF_ROOT, "pulsar_arm/bonsai2/pq2_host.c")
     if not (os.path.exists(q8) and os.path.exists(pq2)):

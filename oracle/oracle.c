@@ -1,7 +1,7 @@
 /* oracle.c -- CPU restatement of the PULSAR-ASM hot path (test infrastructure).
  *
  * ONLY tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load this library, and only as the checker / CPU baseline. The product
+ * load this library, and only as the test reference / CPU baseline. The product
  * (pulsar-asm_amd/) never links or calls it.
  *
  * Citations are relative to the PULSAR-ASM tree. The orders the build defines
@@ -509,8 +509,8 @@ float orc_pairwise(const float *v, int n) {
  *   ss = pairwise(x_i^2), v = fl(fl(ss / n) + eps), rs = fl(1 / fl(sqrt(v)))
  *   y_i = bf16(fl(w_i * bf16(fl(x_i * rs))))   -- round BEFORE the weight
  * The reference's per-thread-then-warp-tree sum (383-440) and the NEON
- * 8-accumulator order (lfm3_elem_test.c:35-45) are both fixed trees; this build
- * fixes the pairwise tree, which wave64 butterflies produce exactly. The
+ * 8-accumulator order (lfm3_elem_test.c:35-45) are both fixed trees; the GPU
+ * path and this restatement fix the pairwise tree, which wave64 butterflies produce exactly. The
  * reference uses rsqrtf on the device and 1/sqrtf on the CPU (lfm3_elem_test.c:
  * 45); both sides here use the correctly rounded 1/sqrtf. n is a power of two. */
 void orc_rmsnorm(const uint16_t *x, const float *w, uint16_t *y, int n, float eps) {
@@ -724,7 +724,7 @@ void orc_sigmoid_gate(const uint16_t *g, uint16_t *attn, int nh, int hd) {
 
 /* Greedy argmax: the LOWEST index among the maxima (strict > scan). The
  * reference's k_argmax (lfm3_nanode.cu:942-964) breaks ties by thread slot;
- * this build fixes the lowest index on both sides. */
+ * the GPU path and this restatement both take the lowest index. */
 int orc_argmax(const float *v, int n) {
   int bi = 0;
   float bv = v[0];

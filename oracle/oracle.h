@@ -1,6 +1,6 @@
 /* oracle.h -- CPU restatement of the PULSAR-ASM LFM3/Bonsai hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP path:
+ * TEST INFRASTRUCTURE ONLY. This library is the test reference for the HIP path:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
  * it. The product library never links, calls or falls back to it.
  *
