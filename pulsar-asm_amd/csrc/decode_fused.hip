@@ -537,7 +537,11 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
   uint16_t *blk = kvnew + 2 * HD;                                    // [8 waves][64][kVRow] K, then V slices
   float *st = reinterpret_cast<float *>(blk + 8 * kSplitF * kVRow);  // [nsplit][HD + 2]
   const int pos = pos_dev != nullptr ? __builtin_amdgcn_readfirstlane(*pos_dev) : pos_arg;
-  const int hq = blockIdx.x, G = nh / nkv, g = hq / G;
+  // workgroups go round-robin over the 8 XCDs (XCD = id % 8): with nh a
+  // multiple of 8, XCD x takes q heads x*nh/8 .. +nh/8, so the q heads of a kv
+  // group share an L2 (or two) and their K/V blocks come from HBM once per L2
+  const int hq = nh % 8 == 0 ? (int)(blockIdx.x % 8) * (nh / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  const int G = nh / nkv, g = hq / G;
   const bool writer = hq % G == 0;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int kvd = nkv * HD;
