@@ -521,6 +521,169 @@ __device__ __forceinline__ float block_amax(float v) {
   return max_row_pair(a);
 }
 
+// One 64-position split j of a q head, by one wave: the K slices go through
+// the wave's LDS buffer bw so lane p holds key p (s = q.k, one fmaf chain over
+// d ascending), then m, e, l; each V slice goes through the same buffer so
+// lane d runs the fmaf chain over positions for o of dim d (+ 64 per slice).
+// kr/vr hold the split's K and V blocks (lane l: 16-byte chunk l%8 of rows
+// 8i + l/8, slice h), rows at and past pos zero; the row at pos comes from
+// kvnew. Writes (o[HD], m, l) to sj (LDS or global).
+template <int HD>
+__device__ __forceinline__ void split_partial(const v4i (&kr)[HD / 64][8], const v4i (&vr)[HD / 64][8],
+                                              const float *qs, const uint16_t *kvnew, uint16_t *bw, float *eww, int pos,
+                                              int npos, int lo, int j, int lane, float scale, float *sj) {
+  constexpr int E = HD / 64;
+  const int lr = lane >> 3, lc = lane & 7;
+  const int p0 = j * kSplitF;
+  const int pn = npos - p0 < kSplitF ? npos - p0 : kSplitF;
+  const int i0 = lo > p0 ? lo - p0 : 0;
+  const bool valid = lane >= i0 && lane < pn;
+  // K slices -> LDS -> lane p's row (the row at pos from kvnew); one chain over d
+  float d = 0.0f;
+#pragma unroll
+  for (int h = 0; h < E; h++) {
+    if (h > 0) {   // the previous slice's reads precede this slice's writes
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = kr[h][i];
+    const uint16_t *krow = p0 + lane == pos ? kvnew + 64 * h : bw + lane * kVRow;
+    float kf[64];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const v4i w4 = *reinterpret_cast<const v4i *>(krow + 8 * q);
+      const uint32_t kw[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) kf[8 * q + i] = h2f((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float4 q4 = reinterpret_cast<const float4 *>(qs + 64 * h)[i];
+      d = __builtin_fmaf(q4.x, kf[4 * i], d);
+      d = __builtin_fmaf(q4.y, kf[4 * i + 1], d);
+      d = __builtin_fmaf(q4.z, kf[4 * i + 2], d);
+      d = __builtin_fmaf(q4.w, kf[4 * i + 3], d);
+    }
+  }
+  const float sc = valid ? d * scale : -__builtin_inff();
+  const float m = wave_max(sc);
+  const float e = valid ? expf_pq(sc - m) : 0.0f;
+  const float l = wave_pairwise_sum(e);
+  eww[lane] = e;
+#pragma unroll
+  for (int h = 0; h < E; h++) {
+    // V slice h -> the same LDS buffer (this wave's earlier reads of it
+    // precede it in LDS order); the row at pos from kvnew
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = vr[h][i];
+    if (pos - p0 < kSplitF && lane < 8)
+      *reinterpret_cast<v4i *>(bw + (pos - p0) * kVRow + lane * 8) =
+          reinterpret_cast<const v4i *>(kvnew + HD + 64 * h)[lane];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // o = sum_p e[p] v[p][64h + lane] (fmaf chain over i0 <= p < pn), 16
+    // positions per batch, the next batch's LDS reads issued before this
+    // batch's fmafs. Rows past pos read as zeros (the buffer bound) with
+    // e = 0, and fmaf(0, +0, o) = o, so the last batch runs whole; rows
+    // below i0 (the window's first split) are skipped, a cache row there
+    // may hold an fp16 infinity
+    auto vchain = [&](auto FULL) {
+      float o = 0.0f;
+      uint16_t vb[16];
+      float4 e4[4];
+#pragma unroll
+      for (int i = 0; i < 16; i++) vb[i] = bw[i * kVRow + lane];
+#pragma unroll
+      for (int k = 0; k < 4; k++) e4[k] = reinterpret_cast<const float4 *>(eww)[k];
+      for (int b0 = 0; b0 < pn; b0 += 16) {
+        const int nb0 = b0 + 16 < kSplitF ? b0 + 16 : b0;
+        uint16_t vn[16];
+        float4 en[4];
+#pragma unroll
+        for (int i = 0; i < 16; i++) vn[i] = bw[(nb0 + i) * kVRow + lane];
+#pragma unroll
+        for (int k = 0; k < 4; k++) en[k] = reinterpret_cast<const float4 *>(eww + nb0)[k];
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+          if (FULL || b0 + i >= i0) {
+            const float4 &q = e4[i >> 2];
+            const float ei = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+            o = __builtin_fmaf(ei, h2f(vb[i]), o);
+          }
+#pragma unroll
+        for (int i = 0; i < 16; i++) vb[i] = vn[i];
+#pragma unroll
+        for (int k = 0; k < 4; k++) e4[k] = en[k];
+      }
+      return o;
+    };
+    const float o = i0 == 0 ? vchain(std::true_type{}) : vchain(std::false_type{});
+    sj[64 * h + lane] = o;
+  }
+  if (lane == 0) {
+    sj[HD] = m;
+    sj[HD + 1] = l;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Merge the splits j0 .. ns-1 of q head hq (partials (o[HD], m, l) at st, PART
+// floats apart) by one wave, in ascending order; then the sigmoid gate, the
+// bf16 output and/or the Q8_0 blocks of o_proj's input.
+template <int HD>
+__device__ __forceinline__ void merge_splits(const float *st, int j0, int ns, int lane, uint16_t graw, int hq,
+                                             uint16_t *__restrict__ out, int8_t *__restrict__ qx,
+                                             float *__restrict__ dx) {
+  constexpr int E = HD / 64, PART = HD + 2;
+  // M = max m_j; w_j = e^(m_j - M) for 64 splits at a time, one per lane;
+  // then L and O as fmaf chains over j ascending (w_j, l_j by v_readlane)
+  float M = -__builtin_inff();
+  for (int jb = j0; jb < ns; jb += 64)
+    M = fmaxf(M, wave_max(jb + lane < ns ? st[(size_t)(jb + lane) * PART + HD] : -__builtin_inff()));
+  float L = 0.0f, O[E];
+#pragma unroll
+  for (int h = 0; h < E; h++) O[h] = 0.0f;
+  for (int jb = j0; jb < ns; jb += 64) {
+    const int jl = jb + lane < ns ? jb + lane : ns - 1;
+    const float w = expf_pq(st[(size_t)jl * PART + HD] - M);
+    const float lj = st[(size_t)jl * PART + HD + 1];
+    const int n = ns - jb < 64 ? ns - jb : 64;
+    for (int b = 0; b < n; b += 8) {
+      float oj[8][E];
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int h = 0; h < E; h++) oj[i][h] = st[(size_t)(jb + (b + i < n ? b + i : 0)) * PART + 64 * h + lane];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (b + i < n) {
+          const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b + i));
+          L = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj), b + i)), wi, L);
+#pragma unroll
+          for (int h = 0; h < E; h++) O[h] = __builtin_fmaf(oj[i][h], wi, O[h]);
+        }
+    }
+  }
+  const float gs = 1.0f / (1.0f + expf_pq(-bf2f(graw)));
+#pragma unroll
+  for (int h = 0; h < E; h++) {
+    const int dd = hq * HD + 64 * h + lane;
+    const uint16_t rb = f2bf(bf2f(f2bf(O[h] / L)) * gs);
+    if (out != nullptr) out[dd] = rb;
+    if (qx != nullptr) {   // the Q8_0 blocks of o_proj's input (a caller may ask for bf16 only)
+      const float v = bf2f(rb);
+      const float dq = block_amax(v) / 127.0f;
+      qx[dd] = (int8_t)q8_code(Q8Div(dq).div(v));
+      if ((lane & 31) == 0) dx[dd / 32] = dq;
+    }
+  }
+}
+
 template <int HD>
 __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restrict__ qkvg, const float *__restrict__ qn,
                                                          const float *__restrict__ kn, const float *__restrict__ cs,
@@ -612,154 +775,16 @@ __global__ __launch_bounds__(512) void attn_head_kernel(const uint16_t *__restri
   }
   lds_barrier();
   // 2. splits
-  float *eww = ew + wave * kSplitF;
   uint16_t *bw = blk + wave * kSplitF * kVRow;
   for (int j = j0 + wave; j < ns; j += 8) {
     if (j != j0 + wave) load_blocks(j);
-    const int p0 = j * kSplitF;
-    const int pn = npos - p0 < kSplitF ? npos - p0 : kSplitF;
-    const int i0 = lo > p0 ? lo - p0 : 0;
-    const bool valid = lane >= i0 && lane < pn;
-    // K slices -> LDS -> lane p's row (the row at pos from kvnew); one chain over d
-    float d = 0.0f;
-#pragma unroll
-    for (int h = 0; h < E; h++) {
-      if (h > 0) {   // the previous slice's reads precede this slice's writes
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-      }
-#pragma unroll
-      for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = kr[h][i];
-      const uint16_t *krow = p0 + lane == pos ? kvnew + 64 * h : bw + lane * kVRow;
-      float kf[64];
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const v4i w4 = *reinterpret_cast<const v4i *>(krow + 8 * q);
-        const uint32_t kw[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) kf[8 * q + i] = h2f((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
-      }
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const float4 q4 = reinterpret_cast<const float4 *>(qs + 64 * h)[i];
-        d = __builtin_fmaf(q4.x, kf[4 * i], d);
-        d = __builtin_fmaf(q4.y, kf[4 * i + 1], d);
-        d = __builtin_fmaf(q4.z, kf[4 * i + 2], d);
-        d = __builtin_fmaf(q4.w, kf[4 * i + 3], d);
-      }
-    }
-    const float sc = valid ? d * scale : -__builtin_inff();
-    const float m = wave_max(sc);
-    const float e = valid ? expf_pq(sc - m) : 0.0f;
-    const float l = wave_pairwise_sum(e);
-    eww[lane] = e;
-    float *sj = st + (size_t)j * PART;
-#pragma unroll
-    for (int h = 0; h < E; h++) {
-      // V slice h -> the same LDS buffer (this wave's earlier reads of it
-      // precede it in LDS order); the row at pos from kvnew
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int i = 0; i < 8; i++) *reinterpret_cast<v4i *>(bw + (8 * i + lr) * kVRow + lc * 8) = vr[h][i];
-      if (pos - p0 < kSplitF && lane < 8)
-        *reinterpret_cast<v4i *>(bw + (pos - p0) * kVRow + lane * 8) =
-            reinterpret_cast<const v4i *>(kvnew + HD + 64 * h)[lane];
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      // o = sum_p e[p] v[p][64h + lane] (fmaf chain over i0 <= p < pn), 16
-      // positions per batch, the next batch's LDS reads issued before this
-      // batch's fmafs. Rows past pos read as zeros (the buffer bound) with
-      // e = 0, and fmaf(0, +0, o) = o, so the last batch runs whole; rows
-      // below i0 (the window's first split) are skipped, a cache row there
-      // may hold an fp16 infinity
-      auto vchain = [&](auto FULL) {
-        float o = 0.0f;
-        uint16_t vb[16];
-        float4 e4[4];
-#pragma unroll
-        for (int i = 0; i < 16; i++) vb[i] = bw[i * kVRow + lane];
-#pragma unroll
-        for (int k = 0; k < 4; k++) e4[k] = reinterpret_cast<const float4 *>(eww)[k];
-        for (int b0 = 0; b0 < pn; b0 += 16) {
-          const int nb0 = b0 + 16 < kSplitF ? b0 + 16 : b0;
-          uint16_t vn[16];
-          float4 en[4];
-#pragma unroll
-          for (int i = 0; i < 16; i++) vn[i] = bw[(nb0 + i) * kVRow + lane];
-#pragma unroll
-          for (int k = 0; k < 4; k++) en[k] = reinterpret_cast<const float4 *>(eww + nb0)[k];
-#pragma unroll
-          for (int i = 0; i < 16; i++)
-            if (FULL || b0 + i >= i0) {
-              const float4 &q = e4[i >> 2];
-              const float ei = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
-              o = __builtin_fmaf(ei, h2f(vb[i]), o);
-            }
-#pragma unroll
-          for (int i = 0; i < 16; i++) vb[i] = vn[i];
-#pragma unroll
-          for (int k = 0; k < 4; k++) e4[k] = en[k];
-        }
-        return o;
-      };
-      const float o = i0 == 0 ? vchain(std::true_type{}) : vchain(std::false_type{});
-      sj[64 * h + lane] = o;
-    }
-    if (lane == 0) {
-      sj[HD] = m;
-      sj[HD + 1] = l;
-    }
+    split_partial<HD>(kr, vr, qs, kvnew, bw, ew + wave * kSplitF, pos, npos, lo, j, lane, scale, st + (size_t)j * PART);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
   }
   lds_barrier();
   // 3. merge, gate, outputs
-  if (wave == 0) {
-    // M = max m_j; w_j = e^(m_j - M) for 64 splits at a time, one per lane;
-    // then L and O as fmaf chains over j ascending (w_j, l_j by v_readlane)
-    float M = -__builtin_inff();
-    for (int jb = j0; jb < ns; jb += 64)
-      M = fmaxf(M, wave_max(jb + lane < ns ? st[(size_t)(jb + lane) * PART + HD] : -__builtin_inff()));
-    float L = 0.0f, O[E];
-#pragma unroll
-    for (int h = 0; h < E; h++) O[h] = 0.0f;
-    for (int jb = j0; jb < ns; jb += 64) {
-      const int jl = jb + lane < ns ? jb + lane : ns - 1;
-      const float w = expf_pq(st[(size_t)jl * PART + HD] - M);
-      const float lj = st[(size_t)jl * PART + HD + 1];
-      const int n = ns - jb < 64 ? ns - jb : 64;
-      for (int b = 0; b < n; b += 8) {
-        float oj[8][E];
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-#pragma unroll
-          for (int h = 0; h < E; h++) oj[i][h] = st[(size_t)(jb + (b + i < n ? b + i : 0)) * PART + 64 * h + lane];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-          if (b + i < n) {
-            const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), b + i));
-            L = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj), b + i)), wi, L);
-#pragma unroll
-            for (int h = 0; h < E; h++) O[h] = __builtin_fmaf(oj[i][h], wi, O[h]);
-          }
-      }
-    }
-    const float gs = 1.0f / (1.0f + expf_pq(-bf2f(graw)));
-#pragma unroll
-    for (int h = 0; h < E; h++) {
-      const int dd = hq * HD + 64 * h + lane;
-      const uint16_t rb = f2bf(bf2f(f2bf(O[h] / L)) * gs);
-      if (out != nullptr) out[dd] = rb;
-      if (qx != nullptr) {   // the Q8_0 blocks of o_proj's input (a caller may ask for bf16 only)
-        const float v = bf2f(rb);
-        const float dq = block_amax(v) / 127.0f;
-        qx[dd] = (int8_t)q8_code(Q8Div(dq).div(v));
-        if ((lane & 31) == 0) dx[dd / 32] = dq;
-      }
-    }
-  }
+  if (wave == 0) merge_splits<HD>(st, j0, ns, lane, graw, hq, out, qx, dx);
 }
 
 // ------------------------------------- attention mixer, head_dim 64 or 128
