@@ -55,6 +55,19 @@ __device__ __forceinline__ void q8r_load(RBlocks &B, __amdgpu_buffer_rsrc_t rc, 
   }
 }
 
+// The reference's leaf tree over each 32-lane half of a wave: offsets 16, 8,
+// 4, 2, 1, v_i = v_i + v_{i+o}; lanes 0 and 32 end with their half's sum. The
+// 16-step crosses 16-lane rows (the row-pair swap: the sum is commutative, so
+// both rows get v_i + v_{i+16}); the others are DPP row shifts (lane i reads
+// lane i + o of its row), in place of cross-lane permutes through LDS.
+__device__ __forceinline__ float leaf_tree32(float v) {
+  v = add_row_pair(v);
+  v = v + dpp_f<0x108>(v);   // row_shl:8
+  v = v + dpp_f<0x104>(v);   // row_shl:4
+  v = v + dpp_f<0x102>(v);   // row_shl:2
+  return v + dpp_f<0x101>(v);   // row_shl:1
+}
+
 template <int BPL>
 __device__ __forceinline__ float q8r_leaf(const RBlocks &B, const float *__restrict__ xs, int nbc, int c, int L) {
   float acc = 0.0f;
@@ -81,12 +94,14 @@ __device__ __forceinline__ float q8r_leaf(const RBlocks &B, const float *__restr
   return acc;
 }
 
-// BPL = blocks per leaf per chunk (ceil(chunk blocks / 32)).
-template <int BPL>
+// BPL = blocks per leaf per chunk (ceil(chunk blocks / 32)); MC: K holds
+// several chunks (a second block set in flight; with one chunk the kernel
+// keeps the registers, and the occupancy, of one).
+template <int BPL, bool MC>
 __global__ __launch_bounds__(kRThreads) void q8r_gemv_kernel(const int8_t *__restrict__ codes,
-                                                             const float *__restrict__ scales,
-                                                             const uint16_t *__restrict__ x, void *__restrict__ y,
-                                                             int y_bf16, int N, int K) {
+                                                           const float *__restrict__ scales,
+                                                           const uint16_t *__restrict__ x, void *__restrict__ y,
+                                                           int y_bf16, int N, int K) {
   extern __shared__ __align__(16) float xs[];   // [nb][kRXStride]
   const int t = blockIdx.y;
   const int nb = K / kQ, KC = q8r_chunk(K), nbc = KC / kQ, nch = K / KC;
@@ -98,8 +113,8 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_kernel(const int8_t *__res
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(codes), (short)0, N * K, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scales), (short)0, N * nb * 4, kRsrcWord3);
-  RBlocks B;
-  q8r_load<BPL>(B, rc, rs, row, N, K, nb, nbc, 0, L);
+  RBlocks Ba, Bb;
+  q8r_load<BPL>(Ba, rc, rs, row, N, K, nb, nbc, 0, L);
   // x of position t: 8 bf16 per thread per step, widened into the padded blocks
   const uint16_t *xt = x + (size_t)t * K;
   for (int e = threadIdx.x * 8; e < K; e += kRThreads * 8) {
@@ -116,15 +131,24 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_kernel(const int8_t *__res
     *reinterpret_cast<float4 *>(d + 4) = make_float4(f[4], f[5], f[6], f[7]);
   }
   __syncthreads();
+  // chunks in order, the next chunk's blocks in flight during this one's
+  // arithmetic; the two block sets alternate by name (a register copy of a
+  // set still being loaded would wait for its loads)
   float yv = 0.0f;
-  for (int c = 0; c < nch; c++) {
-    RBlocks Bn;
-    if (c + 1 < nch) q8r_load<BPL>(Bn, rc, rs, row, N, K, nb, nbc, c + 1, L);
-    float acc = q8r_leaf<BPL>(B, xs, nbc, c, L);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) acc = acc + __shfl_down(acc, o, 32);
+  auto chunk = [&](const RBlocks &B, int c) {
+    const float acc = leaf_tree32(q8r_leaf<BPL>(B, xs, nbc, c, L));
     yv = yv + acc;   // lane L = 0 holds the chunk partial
-    if (c + 1 < nch) B = Bn;
+  };
+  if constexpr (!MC) {
+    chunk(Ba, 0);
+  } else {
+    for (int c = 0; c < nch; c += 2) {
+      if (c + 1 < nch) q8r_load<BPL>(Bb, rc, rs, row, N, K, nb, nbc, c + 1, L);
+      chunk(Ba, c);
+      if (c + 1 >= nch) break;
+      if (c + 2 < nch) q8r_load<BPL>(Ba, rc, rs, row, N, K, nb, nbc, c + 2, L);
+      chunk(Bb, c + 1);
+    }
   }
   if (L == 0 && row < N) {
     if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)t * N + row] = f2bf(yv);
@@ -219,8 +243,7 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemm_kernel(const int8_t *__res
           }
           acc = __builtin_fmaf(B.s[i], dot, acc);
         }
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) acc = acc + __shfl_down(acc, o, 32);
+        acc = leaf_tree32(acc);
         if (L == 0) ysum[(tt + p) * kRRows + wr] += acc;
       }
     }
@@ -274,9 +297,16 @@ extern "C" int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint1
     return check_launch("pq_q8r_gemv");
   }
   const dim3 grid((unsigned)((N + kRRows - 1) / kRRows), (unsigned)T), block(kRThreads);
-  if (bpl <= 1) launch(q8r_gemv_kernel<1>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
-  else if (bpl <= 2) launch(q8r_gemv_kernel<2>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
-  else if (bpl <= 4) launch(q8r_gemv_kernel<4>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
-  else launch(q8r_gemv_kernel<8>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  const bool mc = K / KC > 1;
+#define PQ_Q8R_V(BB)                                                                                           \
+  do {                                                                                                         \
+    if (mc) launch(q8r_gemv_kernel<BB, true>, grid, block, lds, st, codes, scales, x, y, yb, N, K);            \
+    else launch(q8r_gemv_kernel<BB, false>, grid, block, lds, st, codes, scales, x, y, yb, N, K);              \
+  } while (0)
+  if (bpl <= 1) PQ_Q8R_V(1);
+  else if (bpl <= 2) PQ_Q8R_V(2);
+  else if (bpl <= 4) PQ_Q8R_V(4);
+  else PQ_Q8R_V(8);
+#undef PQ_Q8R_V
   return check_launch("pq_q8r_gemv");
 }
