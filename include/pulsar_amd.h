@@ -337,6 +337,24 @@ int pq_q8_gemv_parts(int N, int K);
 int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
                      void *y, int y_dtype, int N, int K, float *argmax_parts, void *stream);
 int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream);
+/* pq_q8r_gemv at T = 1 (the reference's own GEMV order on row-major codes and
+ * fp32 scales) with x from a prologue: RESNORM, NORM, SILU or CONV (K <= 4096
+ * for CONV), computed exactly as the kinds above and handed to the GEMV as the
+ * bf16 values the unfused op would store. K is 1024, 2048, 4096 or 8192; y
+ * bf16 or fp32; argmax_parts as for pq_q8_gemv_fused. Replaces the rmsnorm_body / k_silu_mul_bf / k_conv7 + gemv
+ * pairs of layer_body (lfm3_nanode.cu:3739-3856) under the reference numerics. */
+int pq_q8r_gemv_fused(const int8_t *codes, const float *scales, const pq_gemv_prologue *pro, void *y,
+                      int y_dtype, int N, int K, float *argmax_parts, void *stream);
+/* Workgroups of pq_q8r_gemv_fused for N rows: the (value, index) pairs it
+ * writes to argmax_parts (if not NULL) for pq_argmax_parts. */
+int pq_q8r_gemv_parts(int N);
+/* The FFN's gate/up GEMV under the reference numerics: codes [2F][K] (gate
+ * rows 0..F-1, up rows F..2F-1, row-major), fp32 scales, x from a RESNORM or
+ * NORM prologue, and y [F] bf16 = silu_mul of the bf16 gate and up outputs --
+ * the gemv + k_silu_mul_bf pair (lfm3_nanode.cu:821-829) of layer_body
+ * (3739-3856) in one launch, the same bits. F a multiple of 4. */
+int pq_q8r_gemv_fused_swiglu(const int8_t *codes, const float *scales, const pq_gemv_prologue *pro,
+                             uint16_t *y, int F, int K, void *stream);
 /* The FFN's gate/up GEMV (weights from pq_q8_pack_gate_up, N = 2F) with the
  * prologue pro and silu(gate) * up as its epilogue: writes the Q8_0 row
  * (qx [F], dx [F/32]) that the down projection reads (PQ_PRO_Q8) -- the

@@ -27,6 +27,7 @@
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
+#include "q8r_common.h"
 #include "pq_internal.h"
 
 namespace pq {
@@ -216,18 +217,15 @@ __device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int 
   }
 }
 
+// The prologue's x values for the thread's E elements (every kind but Q8),
+// bf16-rounded where the unfused op rounds; the vectors it writes once
+// (x_out, ring_out) are written by workgroup 0.
 template <int PRO, int E>
-__device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, int K, ProRegs<E, conv_taps(PRO)> &r,
-                                            float *red, int8_t *xs, float *dxs) {
+__device__ __forceinline__ void pro_values(const pq_gemv_prologue &p, int e0, int K, ProRegs<E, conv_taps(PRO)> &r,
+                                           float *red, float *v) {
   constexpr int NT = conv_taps(PRO);
-  const bool writer = blockIdx.x == 0;
-  float v[E];
-  if constexpr (PRO == PQ_PRO_Q8) {
-    store_q8_lds<E>(r.emb_c, e0, xs);
-    if ((e0 & 31) == 0) dxs[e0 >> 5] = r.f0[0];
-    lds_barrier();
-    return;
-  } else if constexpr (PRO == PQ_PRO_RESNORM) {
+  const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+  if constexpr (PRO == PQ_PRO_RESNORM) {
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
     const float ss = wg_pairwise_sq<E>(v, red);
@@ -300,8 +298,21 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
       st_bf16w<E>(p.ring_out + (size_t)(NT - 1) * K + e0, bxw);
     }
   }
-  quant_lds<E>(v, e0, xs, dxs);
-  lds_barrier();
+}
+
+template <int PRO, int E>
+__device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, int K, ProRegs<E, conv_taps(PRO)> &r,
+                                            float *red, int8_t *xs, float *dxs) {
+  if constexpr (PRO == PQ_PRO_Q8) {
+    store_q8_lds<E>(r.emb_c, e0, xs);
+    if ((e0 & 31) == 0) dxs[e0 >> 5] = r.f0[0];
+    lds_barrier();
+  } else {
+    float v[E];
+    pro_values<PRO, E>(p, e0, K, r, red, v);
+    quant_lds<E>(v, e0, xs, dxs);
+    lds_barrier();
+  }
 }
 
 // The fused GEMV's outputs from wave 0 (lane l < R holds row tile*64 + l's
@@ -416,6 +427,120 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
     if (rd + 1 < nrounds) __syncthreads();
   }
   if (wave == 0) fused_epilogue<R>(yv, lane, tile, row, (int)blockIdx.x, y, y_bf16, N, parts, qo, dqo);
+}
+
+// ------------------------------------ the reference-numerics fused GEMV
+// q8r_gemv_kernel at T = 1 with x from a prologue. The prologue's E = K/256
+// values per thread (bf16-rounded where the unfused op rounds them) go to LDS
+// as fp32 in the 36-float padded blocks the leaf chains read -- the same
+// values the unfused op writes as bf16 and the plain kernel widens -- once
+// per workgroup: the workgroup then walks row tiles blockIdx.x, + gridDim.x,
+// ... (ntiles in all), each tile's 2048-wide chunks in order, the next
+// (tile, chunk)'s blocks loading while the current one folds. TWO: two block
+// sets rotated by name (a workgroup with more than one (tile, chunk)); else
+// the one (tile, chunk) of a single-tile, single-chunk workgroup.
+// SWI: the tile is 4 gate rows t*4 + r and their up rows F + t*4 + r (codes
+// [2F][K], F = N/2); its 4 outputs are silu_mul_kernel's of the bf16 gate
+// and up values. Else, with parts: the workgroup's (largest y, its row; the
+// lowest row on ties) at parts[2 * blockIdx.x].
+template <int BPL, int PRO, int E, bool TWO, bool SWI>
+__global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t *__restrict__ codes,
+                                                                   const float *__restrict__ scales,
+                                                                   pq_gemv_prologue p, void *__restrict__ y,
+                                                                   int y_bf16, int N, int K, int ntiles,
+                                                                   float *__restrict__ parts) {
+  constexpr int W = kRThreads / 64;
+  extern __shared__ __align__(16) float rxs[];   // [nb][kRXStride]
+  __shared__ float red[16];
+  __shared__ float sw[2][kRRows];
+  const int nb = K / kQ, KC = q8r_chunk(K), nbc = KC / kQ, nch = K / KC;
+  const int r = threadIdx.x >> 5, L = threadIdx.x & 31, F = N >> 1;
+  auto row_of = [&](int t) { return SWI ? (r < kRRows / 2 ? t * (kRRows / 2) + r : F + t * (kRRows / 2) + r - kRRows / 2)
+                                        : t * kRRows + r; };
+  if (threadIdx.x >= W && threadIdx.x < 8) red[threadIdx.x] = red[8 + threadIdx.x] = 0.0f;
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(codes), (short)0, N * K, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scales), (short)0, N * nb * 4, kRsrcWord3);
+  const int e0 = threadIdx.x * E;
+  int t = blockIdx.x, c = 0, k = 0;
+  ProRegs<E, conv_taps(PRO)> pr;
+  pro_load<PRO, E>(p, e0, K, pr);
+  RBlocks Ba, Bb;
+  q8r_load<BPL>(Ba, rc, rs, row_of(t), N, K, nb, nbc, 0, L);
+  {
+    float v[E];
+    pro_values<PRO, E>(p, e0, K, pr, red, v);
+    float *d = rxs + (size_t)(e0 >> 5) * kRXStride + (e0 & 31);   // E divides 32: one block
+#pragma unroll
+    for (int i = 0; i < E; i += 4) *reinterpret_cast<float4 *>(d + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+  }
+  lds_barrier();
+  float yv = 0.0f, best = -__builtin_inff();
+  int bidx = 0x7fffffff;
+  // fold chunk cc of tile tt (lane L = 0 of each row holds the partial); the
+  // tile's last chunk writes its outputs
+  auto step = [&](const RBlocks &B, int tt, int cc) {
+    yv = yv + leaf_tree32(q8r_leaf<BPL>(B, rxs, nbc, cc, L));
+    if (cc + 1 < nch) return;
+    if constexpr (SWI) {
+      if (L == 0) sw[k & 1][r] = bf2f(f2bf(yv));
+      lds_barrier();   // sw alternates per tile: its reads end before the next tile's barrier
+      if (threadIdx.x < kRRows / 2) {
+        const float a = sw[k & 1][threadIdx.x], u = sw[k & 1][kRRows / 2 + threadIdx.x];
+        const float sg = 1.0f / (1.0f + expf_pq(-a));
+        reinterpret_cast<uint16_t *>(y)[tt * (kRRows / 2) + threadIdx.x] = f2bf((a * sg) * u);
+      }
+      k++;
+    } else {
+      const int row = tt * kRRows + r;
+      if (L == 0 && row < N) {
+        if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yv);
+        else reinterpret_cast<float *>(y)[row] = yv;
+        if (yv > best || (yv == best && row < bidx)) { best = yv; bidx = row; }
+      }
+    }
+    yv = 0.0f;
+  };
+  if constexpr (!TWO) {
+    step(Ba, t, 0);
+  } else {
+    auto advance = [&](int &tn, int &cn) {
+      tn = t;
+      cn = c + 1;
+      if (cn == nch) { cn = 0; tn += gridDim.x; }
+      return tn < ntiles;
+    };
+    for (;;) {
+      int tn, cn;
+      bool more = advance(tn, cn);
+      if (more) q8r_load<BPL>(Bb, rc, rs, row_of(tn), N, K, nb, nbc, cn, L);
+      step(Ba, t, c);
+      if (!more) break;
+      t = tn;
+      c = cn;
+      more = advance(tn, cn);
+      if (more) q8r_load<BPL>(Ba, rc, rs, row_of(tn), N, K, nb, nbc, cn, L);
+      step(Bb, t, c);
+      if (!more) break;
+      t = tn;
+      c = cn;
+    }
+  }
+  if constexpr (!SWI) {
+    if (parts != nullptr) {   // uniform: every thread reaches the barrier
+      __shared__ float pb[kRRows];
+      __shared__ int pi[kRRows];
+      if (L == 0) { pb[r] = best; pi[r] = bidx; }
+      lds_barrier();
+      if (threadIdx.x == 0) {
+        for (int i = 1; i < kRRows; i++)
+          if (pb[i] > best || (pb[i] == best && pi[i] < bidx)) { best = pb[i]; bidx = pi[i]; }
+        parts[2 * blockIdx.x] = best;
+        parts[2 * blockIdx.x + 1] = __int_as_float(bidx);
+      }
+    }
+  }
 }
 
 // (value, index) partials -> the lowest index among the maxima.
@@ -1121,6 +1246,87 @@ extern "C" int pq_q8_gemv_fused_swiglu(const int8_t *pcodes, const uint16_t *psc
   if (rc) return rc;
   return launch_fused(pcodes, pscales, *pro, nullptr, 0, 2 * F, K, nullptr, qx, dx, 64, as_stream(stream),
                       "pq_q8_gemv_fused_swiglu");
+}
+
+// Workgroups of the fused reference-numerics GEMV: ntiles row tiles over at
+// most 512 workgroups (two per CU), so a large N pays its prologue once per
+// workgroup, not once per 8 rows (512 measured faster than 1024 and 2048 for
+// the 16384- and 65536-row shapes).
+static int q8r_fused_grid(int ntiles) {
+  static const int cap = [] {
+    const char *e = getenv("PQ_Q8RF_GRID");
+    const int v = e ? atoi(e) : 0;
+    return v >= 64 ? v : 512;
+  }();
+  return std::min(ntiles, cap);
+}
+
+template <int PRO, bool SWI>
+static void launch_q8r_fused(int K, int ntiles, size_t lds, hipStream_t st, const int8_t *codes, const float *scales,
+                             const pq_gemv_prologue &p, void *y, int yb, int N, float *parts) {
+  const int G = q8r_fused_grid(ntiles);
+  const bool two = G < ntiles || K > 2048;
+  const dim3 grid((unsigned)G), blk(kRThreads);
+  // K = 256 E; chunks of 2048 (one for K <= 2048): BPL = 1 at K = 1024, else 2
+#define PQ_Q8RF(BPL, E, TWO) \
+  launch(q8r_gemv_fused_kernel<BPL, PRO, E, TWO, SWI>, grid, blk, lds, st, codes, scales, p, y, yb, N, K, ntiles, \
+         parts)
+  switch (K) {
+    case 1024: if (two) PQ_Q8RF(1, 4, true); else PQ_Q8RF(1, 4, false); break;
+    case 2048: if (two) PQ_Q8RF(2, 8, true); else PQ_Q8RF(2, 8, false); break;
+    case 4096: PQ_Q8RF(2, 16, true); break;
+    default:
+      if constexpr (pro_base(PRO) != PQ_PRO_CONV) PQ_Q8RF(2, 32, true);
+      break;
+  }
+#undef PQ_Q8RF
+}
+
+template <bool SWI>
+static int q8r_fused_entry(const int8_t *codes, const float *scales, const pq_gemv_prologue *pro, void *y, int y_dtype,
+                           int N, int K, float *parts, void *stream, const char *who) {
+  PQ_REQUIRE(codes && scales && pro && y, PQ_ERR_ARG, "%s: null pointer", who);
+  PQ_REQUIRE(N > 0 && (K == 1024 || K == 2048 || K == 4096 || K == 8192), PQ_ERR_ARG,
+             "%s: N=%d K=%d (K 1024, 2048, 4096 or 8192)", who, N, K);
+  PQ_REQUIRE((long long)N * K < (1ll << 31), PQ_ERR_ARG, "%s: N=%d K=%d too large", who, N, K);
+  PQ_REQUIRE(aligned(codes, 16) && aligned(scales, 16), PQ_ERR_ALIGN, "%s: codes, scales alignment", who);
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "%s: y_dtype %d", who, y_dtype);
+  const pq_gemv_prologue &p = *pro;
+  PQ_REQUIRE(p.kind == PQ_PRO_RESNORM || p.kind == PQ_PRO_NORM || (!SWI && (p.kind == PQ_PRO_SILU || p.kind == PQ_PRO_CONV)),
+             PQ_ERR_ARG, "%s: prologue kind %d (RESNORM, NORM%s)", who, p.kind, SWI ? "" : ", SILU or CONV");
+  PQ_REQUIRE(p.kind != PQ_PRO_CONV || K <= 4096, PQ_ERR_ARG, "%s: the CONV prologue takes K <= 4096", who);
+  const int rc = check_fused_args(codes, reinterpret_cast<const uint16_t *>(scales), pro, y, N, K, who);
+  if (rc) return rc;
+  const size_t lds = (size_t)(K / kQ) * kRXStride * sizeof(float);
+  const int ntiles = SWI ? N / kRRows : (N + kRRows - 1) / kRRows;
+  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  hipStream_t st = as_stream(stream);
+  switch (p.kind) {
+    case PQ_PRO_RESNORM: launch_q8r_fused<PQ_PRO_RESNORM, SWI>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts); break;
+    case PQ_PRO_NORM: launch_q8r_fused<PQ_PRO_NORM, SWI>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts); break;
+    default:
+      if constexpr (!SWI) {
+        if (p.kind == PQ_PRO_SILU) launch_q8r_fused<PQ_PRO_SILU, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
+        else if (p.ntaps == 7) launch_q8r_fused<kProConv7, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
+        else launch_q8r_fused<PQ_PRO_CONV, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
+      }
+      break;
+  }
+  return check_launch(who);
+}
+
+extern "C" int pq_q8r_gemv_parts(int N) { return N > 0 ? q8r_fused_grid((N + kRRows - 1) / kRRows) : 0; }
+
+extern "C" int pq_q8r_gemv_fused(const int8_t *codes, const float *scales, const pq_gemv_prologue *pro, void *y,
+                                 int y_dtype, int N, int K, float *argmax_parts, void *stream) {
+  return q8r_fused_entry<false>(codes, scales, pro, y, y_dtype, N, K, argmax_parts, stream, "pq_q8r_gemv_fused");
+}
+
+extern "C" int pq_q8r_gemv_fused_swiglu(const int8_t *codes, const float *scales, const pq_gemv_prologue *pro,
+                                        uint16_t *y, int F, int K, void *stream) {
+  PQ_REQUIRE(F > 0 && F % (kRRows / 2) == 0, PQ_ERR_ARG, "pq_q8r_gemv_fused_swiglu: F=%d (a multiple of 4)", F);
+  return q8r_fused_entry<true>(codes, scales, pro, y, PQ_DTYPE_BF16, 2 * F, K, nullptr, stream,
+                               "pq_q8r_gemv_fused_swiglu");
 }
 
 extern "C" int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream) {

@@ -177,7 +177,7 @@ static int create(Engine &E, const pq_model_cfg &c) {
   if (ref_numerics(E)) PQ_TRY(E.dalloc(&E.xin, npos * H));
   PQ_TRY(E.dalloc(&E.Xd[0], (size_t)H));
   PQ_TRY(E.dalloc(&E.Xd[1], (size_t)H));
-  E.nparts = pq_q8_gemv_parts(c.vocab, H);
+  E.nparts = ref_numerics(E) ? pq_q8r_gemv_parts(c.vocab) : pq_q8_gemv_parts(c.vocab, H);
   PQ_TRY(E.dalloc(&E.parts, (size_t)E.nparts * 2));
   PQ_TRY(E.dalloc(&E.Hb, (size_t)T * H));
   PQ_TRY(E.dalloc(&E.Wd, (size_t)T * wide));
@@ -581,18 +581,23 @@ static bool pow2_range(int v) { return v >= 1024 && v <= 8192 && (v & (v - 1)) =
 // a multiple of 32 (the SwiGLU epilogue's 32-row groups; a width that is not
 // a power of two runs its down projection as the plain Q8_0 GEMV), 3 or 7
 // conv taps, and attention the split-K kernels can run (GQA group 1..8).
+// Under PQ_NUMERICS_REF the same holds, and the conv prologue (conv layers)
+// takes hidden <= 4096.
 static bool fused_supported(const pq_model_cfg &c, const char **why) {
   bool conv = false, attn = false;
   for (int l = 0; l < c.nlayers; l++) ((c.attn_mask >> l) & 1u ? attn : conv) = true;
   const int G = c.nkv > 0 ? c.nh / c.nkv : 0;
   *why = nullptr;
-  if (c.numerics == PQ_NUMERICS_REF) *why = "the reference-numerics mode runs unfused steps";
-  else if (!pow2_range(c.hidden)) *why = "hidden must be a power of two in 1024..8192";
+  if (!pow2_range(c.hidden)) *why = "hidden must be a power of two in 1024..8192";
   else if (c.ffn % 32 != 0) *why = "ffn must be a multiple of 32";
   else if (conv && c.ntaps != 3 && c.ntaps != 7) *why = "the fused conv prologue takes 3 or 7 taps";
+  else if (conv && c.numerics == PQ_NUMERICS_REF && c.hidden > 4096)
+    *why = "the reference-numerics conv prologue takes hidden <= 4096";
   else if (attn && G != 1 && G != 2 && G != 4 && G != 8) *why = "GQA group 1, 2, 4 or 8";
   return *why == nullptr;
 }
+
+static int forward_decode_r2(Engine &E, bool dev);
 
 // One T=1 decode step through the fused kernels: four GEMV launches per conv
 // layer, five per attention layer (incl. the attention mixer), the LM head with
@@ -601,6 +606,7 @@ static bool fused_supported(const pq_model_cfg &c, const char **why) {
 // dev: the position comes from E.ctr[1] and the id is appended at E.ids[E.ctr[0]]
 // on the device (the form captured for replay); otherwise E.pos is passed.
 static int forward_decode(Engine &E, bool dev) {
+  if (ref_numerics(E)) return forward_decode_r2(E, dev);
   const pq_model_cfg &c = E.c;
   const int H = c.hidden;
   if (E.pos + 1 > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + 1 > %d", E.pos, c.ctx);
@@ -693,6 +699,102 @@ static int forward_decode(Engine &E, bool dev) {
   E.last_t = 1;
   E.last_resid = xa;
   (void)H;
+  return PQ_OK;
+}
+
+// forward_r2's T=1 step through the fused reference-numerics kernels, the
+// same bits: the norm + residual pairs and the conv run as the prologues of
+// the GEMVs that read them, silu(gate) * up as the gate/up GEMV's epilogue,
+// and the LM head writes per-workgroup argmax pairs: per attention layer the
+// in GEMV, the attention mixer, o_proj, gate/up and down (five launches), per
+// conv layer four (the conv is the out GEMV's prologue), plus the embedding
+// row, the LM head and the argmax. The position and id slot as in
+// forward_decode (dev: on the device, so the step can be captured and
+// replayed).
+static int forward_decode_r2(Engine &E, bool dev) {
+  const pq_model_cfg &c = E.c;
+  const int H = c.hidden;
+  if (E.pos + 1 > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + 1 > %d", E.pos, c.ctx);
+  uint16_t *xa = E.Xd[0], *xb = E.Xd[1];
+  pq_gemv_prologue p;
+  auto resnorm = [&](const float *w0, const float *w1) {
+    p = pq_gemv_prologue{};
+    p.kind = PQ_PRO_RESNORM;
+    p.h = E.Hb;
+    p.x_in = xa;
+    p.x_out = xb;
+    p.w0 = w0;
+    p.w1 = w1;
+    p.eps = c.eps;
+    std::swap(xa, xb);
+  };
+  auto gemv = [&](const Q8Dev &w, void *y, int dt, float *parts) {
+    return pq_q8r_gemv_fused(w.pc, w.sf, &p, y, dt, w.N, w.K, parts, E.st);
+  };
+  auto plain = [&](const Q8Dev &w, const uint16_t *x, uint16_t *y) {
+    return pq_q8r_gemv(w.pc, w.sf, x, y, PQ_DTYPE_BF16, w.N, w.K, 1, E.st);
+  };
+  const float scale = 1.0f / sqrtf((float)c.hd);
+  // the token's embedding row (bf16); layer 0's in GEMV normalizes it
+  PQ_TRY(pq_embed_rows(E.emb.pc, E.emb.sf, E.tok, xa, H, c.vocab, 1, E.st));
+  for (int l = 0; l < c.nlayers; l++) {
+    LayerDev &D = E.L[l];
+    if (l == 0) {
+      p = pq_gemv_prologue{};
+      p.kind = PQ_PRO_NORM;
+      p.x_in = xa;
+      p.w0 = D.op_norm;
+      p.eps = c.eps;
+    } else {
+      resnorm(E.L[l - 1].post_ffn_norm, D.op_norm);
+    }
+    PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
+    if (D.attn) {
+      const int32_t *pd = dev ? E.ctr + 1 : nullptr;
+      if (mixer_fused(E, D)) {
+        if (dev)
+          PQ_TRY(attn_layer_decode_dev(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pd, c.ctx, c.nh, c.nkv,
+                                       c.hd, layer_rot(E, D), layer_win(E, D), c.eps, scale, E.A, nullptr, nullptr,
+                                       E.st));
+        else
+          PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, c.nh, c.nkv,
+                                      c.hd, layer_rot(E, D), layer_win(E, D), c.eps, scale, E.A, nullptr, nullptr,
+                                      E.st));
+      } else {
+        PQ_TRY(qk_prep_launch(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, pd, c.nh, c.nkv,
+                              c.hd, layer_rot(E, D), 1, c.eps, E.st));
+        if (dev)
+          PQ_TRY(attn_decode_dev(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr,
+                                 nullptr, pd, c.ctx, c.nh, c.nkv, c.hd, scale, layer_win(E, D), E.attn_ws,
+                                 E.attn_ws_bytes, E.st));
+        else
+          PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr, nullptr,
+                                E.pos, c.nh, c.nkv, c.hd, 1, scale, layer_win(E, D), E.attn_ws, E.attn_ws_bytes,
+                                E.st));
+      }
+      PQ_TRY(plain(D.out, E.A, E.Hb));
+    } else {
+      p = pq_gemv_prologue{};
+      p.kind = PQ_PRO_CONV;
+      p.bcx = E.Wd;
+      p.ring_in = D.rings[D.rc];
+      p.ring_out = D.rings[1 - D.rc];
+      p.taps = D.taps;
+      p.ntaps = c.ntaps;
+      D.rc = 1 - D.rc;
+      PQ_TRY(gemv(D.out, E.Hb, PQ_DTYPE_BF16, nullptr));
+    }
+    resnorm(D.post_op_norm, D.ffn_norm);
+    PQ_TRY(pq_q8r_gemv_fused_swiglu(D.ug.pc, D.ug.sf, &p, E.A, c.ffn, H, E.st));
+    PQ_TRY(plain(D.down, E.A, E.Hb));
+  }
+  resnorm(E.L[c.nlayers - 1].post_ffn_norm, E.final_norm);
+  PQ_TRY(gemv(E.emb, E.logits, PQ_DTYPE_F32, E.parts));
+  if (dev) PQ_TRY(argmax_parts_step(E.parts, E.nparts, E.tok, E.ids, E.ctr, E.st));
+  else PQ_TRY(pq_argmax_parts(E.parts, E.nparts, E.tok, E.st));
+  E.pos += 1;
+  E.last_t = 1;
+  E.last_resid = xa;
   return PQ_OK;
 }
 

@@ -8,10 +8,10 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "QlowWeight", "qlow_gemv", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "gemv_fused",
            "gemv_fused_swiglu",
-           "argmax_parts", "attn_layer_decode", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
+           "argmax_parts", "attn_layer_decode", "q8r_gemv_fused_swiglu", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
            "PRO_CONV", "PRO_F32"]
 
 PRO_Q8, PRO_RESNORM, PRO_NORM, PRO_EMBED, PRO_SILU, PRO_CONV, PRO_F32 = 0, 1, 2, 3, 4, 5, 6
@@ -271,6 +271,39 @@ def gemv_fused(w, kind, out_dtype=DT_BF16, out=None, parts=None, eps=1e-5, **ptr
         out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=w.pcodes.device)
     check(lib().pq_q8_gemv_fused(w.pcodes.data_ptr(), w.pscales.data_ptr(), C.byref(p), out.data_ptr(), out_dtype,
                                  w.N, w.K, _ptr(parts), stream_ptr()), "pq_q8_gemv_fused")
+    return out
+
+
+def q8r_gemv_fused(codes, scales, kind, out_dtype=DT_BF16, out=None, parts=None, eps=1e-5, **ptrs):
+    """The reference-numerics GEMV (codes int8 [N][K], fp32 scales [N][K/32])
+    at T = 1 with x from a prologue (pq_q8r_gemv_fused): kind RESNORM, NORM,
+    SILU or CONV, ptrs as for gemv_fused; parts (fp32, 2 * pq_q8r_gemv_parts(N))
+    receives the per-workgroup argmax pairs."""
+    import ctypes as C
+    N, K = codes.shape
+    if scales.shape != (N, K // 32) or scales.dtype != torch.float32:
+        raise ValueError("scales must be fp32 [N][K/32]")
+    p = _prologue(kind, eps, ptrs)
+    if out is None:
+        out = torch.empty(N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=codes.device)
+    check(lib().pq_q8r_gemv_fused(codes.data_ptr(), scales.data_ptr(), C.byref(p), out.data_ptr(), out_dtype, N, K,
+                                  _ptr(parts), stream_ptr()), "pq_q8r_gemv_fused")
+    return out
+
+
+def q8r_gemv_fused_swiglu(codes, scales, kind, out=None, eps=1e-5, **ptrs):
+    """The reference-numerics gate/up GEMV (codes int8 [2F][K]: gate rows, then
+    up rows) with a RESNORM or NORM prologue and the silu(gate) * up epilogue
+    (pq_q8r_gemv_fused_swiglu): returns y bf16 [F]."""
+    import ctypes as C
+    N, K = codes.shape
+    if scales.shape != (N, K // 32) or scales.dtype != torch.float32:
+        raise ValueError("scales must be fp32 [N][K/32]")
+    p = _prologue(kind, eps, ptrs)
+    if out is None:
+        out = torch.empty(N // 2, dtype=torch.bfloat16, device=codes.device)
+    check(lib().pq_q8r_gemv_fused_swiglu(codes.data_ptr(), scales.data_ptr(), C.byref(p), out.data_ptr(), N // 2, K,
+                                         stream_ptr()), "pq_q8r_gemv_fused_swiglu")
     return out
 
 

@@ -178,26 +178,30 @@ FUSED_CFGS = {
 }
 
 
+@pytest.mark.parametrize("numerics", [0, 1], ids=["q8", "ref"])
 @pytest.mark.parametrize("which", list(FUSED_CFGS))
-def test_engine_fused_equals_unfused(orc, pq, dev, which):
+def test_engine_fused_equals_unfused(orc, pq, dev, which, numerics):
     """Fused steps replayed as captured graphs, fused steps launched one by one,
-    and the unfused op sequence give the oracle's ids; graph replays are split
-    into several decode calls with eager work (state reads, a non-graph step)
-    between them."""
+    and the unfused op sequence give the oracle's ids and the same final
+    residual, under both GEMV numerics; graph replays are split into several
+    decode calls with eager work (state reads, a non-graph step) between them."""
     from pulsar_amd.engine import Engine
-    cfg = FUSED_CFGS[which]
+    cfg = dict(FUSED_CFGS[which], numerics=numerics)
     prompt = orc.gen_tokens(9, 70, cfg["vocab"])
     m = orc.Model(**{k: v for k, v in cfg.items()})
     ref = m.greedy(prompt, 12)
     m.close()
+    resid = []
     for fused, graph in ((True, True), (True, False), (False, False)):
         e = Engine(**cfg)
         e.load_synthetic()
         e.set_fused(fused)
         e.set_graph(graph)
         ids = e.greedy(prompt, 12)
+        resid.append(e.hidden())
         e.close()
         assert np.array_equal(ids, ref), (fused, graph)
+    assert np.array_equal(resid[0], resid[2]) and np.array_equal(resid[1], resid[2])
     e = Engine(**cfg)
     e.load_synthetic()
     assert e.feed(prompt) == ref[0]

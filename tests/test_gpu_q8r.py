@@ -64,3 +64,98 @@ def test_q8r_rejects_bad_args(pq, dev):
     x = torch.zeros(K, dtype=torch.bfloat16, device=dev)
     with pytest.raises(RuntimeError):
         pq.q8r_gemv(W, S, x)
+
+
+# The T = 1 reference-numerics GEMV with x from a prologue equals the unfused
+# op (pq_rmsnorm / pq_silu_mul / pq_conv, each pinned to the oracle elsewhere)
+# followed by pq_q8r_gemv, bit for bit, with the vectors the prologue writes
+# once (the residual, the shifted conv ring) equal too.
+@pytest.mark.parametrize("kind,N,K", [("resnorm", 3104, 2048), ("resnorm", 65536, 2048), ("resnorm", 300, 4096),
+                                      ("norm", 6144, 2048), ("norm", 77, 1024), ("silu", 2048, 8192),
+                                      ("silu", 2048, 4096), ("silu", 130, 2048), ("conv3", 2048, 2048),
+                                      ("conv7", 2048, 2048), ("conv3", 1000, 4096)])
+def test_q8r_gemv_fused(pq, dev, kind, N, K):
+    print(f"q8r fused {kind} N={N} K={K}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(N * 7 + K)
+    codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    scales = torch.rand((N, K // 32), device=dev, generator=g) * 0.02
+    bf = lambda *shape, s=1.0: (torch.randn(shape, device=dev, generator=g) * s).to(torch.bfloat16)
+    out_dt = pq.DT_F32 if N == 65536 else pq.DT_BF16
+    if kind == "resnorm":
+        h, x = bf(K, s=30.0), bf(K, s=4.0)
+        w0, w1 = torch.rand(K, device=dev, generator=g) + 0.5, torch.rand(K, device=dev, generator=g) + 0.5
+        x1 = x.clone()
+        xin, _, _ = pq.rmsnorm(x1, w0, h=h, w1=w1)
+        want = pq.q8r_gemv(codes, scales, xin, out_dtype=out_dt)
+        xo = torch.empty(K, dtype=torch.int16, device=dev)
+        nparts = pq.lib().pq_q8r_gemv_parts(N)
+        parts = torch.empty(2 * nparts, dtype=torch.float32, device=dev)
+        y = pq.q8r_gemv_fused(codes, scales, pq.PRO_RESNORM, out_dtype=out_dt, parts=parts, h=h.view(torch.int16),
+                              x_in=x.view(torch.int16), x_out=xo, w0=w0, w1=w1)
+        assert torch.equal(xo, x1.view(torch.int16))
+        if out_dt == pq.DT_F32:   # the per-workgroup pairs give pq_argmax's id over the fp32 outputs
+            assert int(pq.argmax_parts(parts, nparts).item()) == int(pq.argmax(want).item())
+    elif kind == "norm":
+        x = bf(K, s=3.0)
+        w0 = torch.rand(K, device=dev, generator=g) + 0.5
+        xin, _, _ = pq.rmsnorm(x.clone(), w0)
+        want = pq.q8r_gemv(codes, scales, xin, out_dtype=out_dt)
+        y = pq.q8r_gemv_fused(codes, scales, pq.PRO_NORM, out_dtype=out_dt, x_in=x.view(torch.int16), w0=w0)
+    elif kind == "silu":
+        gu = bf(2 * K, s=3.0)
+        xin, _, _ = pq.silu_mul(gu, K, 1)
+        want = pq.q8r_gemv(codes, scales, xin.reshape(K), out_dtype=out_dt)
+        y = pq.q8r_gemv_fused(codes, scales, pq.PRO_SILU, out_dtype=out_dt, gu=gu.view(torch.int16))
+    else:
+        nt = 7 if kind == "conv7" else 3
+        bcx, ring = bf(3 * K, s=2.0), bf(nt * K, s=2.0)
+        taps = torch.randn(K, nt, device=dev, generator=g) * 0.5
+        ring1 = ring.clone()
+        xin = torch.empty(K, dtype=torch.bfloat16, device=dev)
+        pq.conv(ring1, taps, bcx, xin, K, 1, nt)
+        want = pq.q8r_gemv(codes, scales, xin, out_dtype=out_dt)
+        ring_out = torch.empty_like(ring)
+        y = pq.q8r_gemv_fused(codes, scales, pq.PRO_CONV, out_dtype=out_dt, bcx=bcx.view(torch.int16),
+                              ring_in=ring.view(torch.int16), ring_out=ring_out.view(torch.int16), taps=taps,
+                              ntaps=nt)
+        assert torch.equal(ring_out.view(torch.int16), ring1.view(torch.int16))
+    torch.cuda.synchronize()
+    if out_dt == pq.DT_F32:
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+    else:
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+
+
+# The gate/up GEMV with the SwiGLU epilogue equals the unfused gate/up GEMV
+# (bf16 out) followed by pq_silu_mul, bit for bit; F = 4 exercises a single
+# tile, 8192 the tile walk over many row tiles per workgroup.
+@pytest.mark.parametrize("kind,F,K", [("resnorm", 8192, 2048), ("resnorm", 7680, 2048), ("norm", 4, 2048),
+                                      ("resnorm", 2052, 1024), ("resnorm", 2048, 8192), ("norm", 1000, 4096)])
+def test_q8r_gemv_fused_swiglu(pq, dev, kind, F, K):
+    print(f"q8r fused swiglu {kind} F={F} K={K}", flush=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(F * 3 + K)
+    codes = torch.randint(-127, 128, (2 * F, K), dtype=torch.int8, device=dev, generator=g)
+    scales = torch.rand((2 * F, K // 32), device=dev, generator=g) * 0.02
+    bf = lambda n, s: (torch.randn(n, device=dev, generator=g) * s).to(torch.bfloat16)
+    w0, w1 = torch.rand(K, device=dev, generator=g) + 0.5, torch.rand(K, device=dev, generator=g) + 0.5
+    x = bf(K, 4.0)
+    if kind == "resnorm":
+        h = bf(K, 30.0)
+        x1 = x.clone()
+        xin, _, _ = pq.rmsnorm(x1, w0, h=h, w1=w1)
+        xo = torch.empty(K, dtype=torch.int16, device=dev)
+        y = pq.q8r_gemv_fused_swiglu(codes, scales, pq.PRO_RESNORM, h=h, x_in=x, x_out=xo, w0=w0, w1=w1)
+    else:
+        xin, _, _ = pq.rmsnorm(x.clone(), w0)
+        y = pq.q8r_gemv_fused_swiglu(codes, scales, pq.PRO_NORM, x_in=x, w0=w0)
+    gu = pq.q8r_gemv(codes, scales, xin)
+    Fp = (F + 255) // 256 * 256   # pq_silu_mul takes F a multiple of 256: zero-pad gate and up
+    gup = torch.zeros(2 * Fp, dtype=torch.bfloat16, device=dev)
+    gup[:F], gup[Fp:Fp + F] = gu[:F], gu[F:]
+    want, _, _ = pq.silu_mul(gup, Fp, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), want.reshape(Fp)[:F].view(torch.int16))
+    if kind == "resnorm":
+        assert torch.equal(xo, x1.view(torch.int16))
