@@ -435,15 +435,16 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
 // as fp32 in the 36-float padded blocks the leaf chains read -- the same
 // values the unfused op writes as bf16 and the plain kernel widens -- once
 // per workgroup: the workgroup then walks row tiles blockIdx.x, + gridDim.x,
-// ... (ntiles in all), each tile's 2048-wide chunks in order, the next
-// (tile, chunk)'s blocks loading while the current one folds. TWO: two block
-// sets rotated by name (a workgroup with more than one (tile, chunk)); else
-// the one (tile, chunk) of a single-tile, single-chunk workgroup.
+// ... (ntiles in all), each tile's 2048-wide chunks in order: its units
+// (tile, chunk) u = 0, 1, ... With NS = 2 block sets rotated by name, unit
+// u + 1 loads while unit u folds (unit 0 before the prologue; a third set,
+// two units ahead, measured slower in the decode step: 0.712 against 0.687
+// ms); NS = 1 is the one unit of a single-tile, single-chunk workgroup.
 // SWI: the tile is 4 gate rows t*4 + r and their up rows F + t*4 + r (codes
 // [2F][K], F = N/2); its 4 outputs are silu_mul_kernel's of the bf16 gate
 // and up values. Else, with parts: the workgroup's (largest y, its row; the
 // lowest row on ties) at parts[2 * blockIdx.x].
-template <int BPL, int PRO, int E, bool TWO, bool SWI>
+template <int BPL, int PRO, int E, int NS, bool SWI>
 __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t *__restrict__ codes,
                                                                    const float *__restrict__ scales,
                                                                    pq_gemv_prologue p, void *__restrict__ y,
@@ -463,11 +464,15 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scales), (short)0, N * nb * 4, kRsrcWord3);
   const int e0 = threadIdx.x * E;
-  int t = blockIdx.x, c = 0, k = 0;
+  int k = 0;   // tiles done (SWI's LDS slot)
+  const int nu = nch * ((ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x);   // units
+  auto load_u = [&](RBlocks &B, int u) {
+    q8r_load<BPL>(B, rc, rs, row_of((int)blockIdx.x + (u / nch) * (int)gridDim.x), N, K, nb, nbc, u % nch, L);
+  };
   ProRegs<E, conv_taps(PRO)> pr;
   pro_load<PRO, E>(p, e0, K, pr);
   RBlocks Ba, Bb;
-  q8r_load<BPL>(Ba, rc, rs, row_of(t), N, K, nb, nbc, 0, L);
+  load_u(Ba, 0);
   {
     float v[E];
     pro_values<PRO, E>(p, e0, K, pr, red, v);
@@ -502,29 +507,16 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
     }
     yv = 0.0f;
   };
-  if constexpr (!TWO) {
-    step(Ba, t, 0);
+  auto step_u = [&](const RBlocks &B, int u) { step(B, (int)blockIdx.x + (u / nch) * (int)gridDim.x, u % nch); };
+  if constexpr (NS == 1) {
+    step_u(Ba, 0);
   } else {
-    auto advance = [&](int &tn, int &cn) {
-      tn = t;
-      cn = c + 1;
-      if (cn == nch) { cn = 0; tn += gridDim.x; }
-      return tn < ntiles;
-    };
-    for (;;) {
-      int tn, cn;
-      bool more = advance(tn, cn);
-      if (more) q8r_load<BPL>(Bb, rc, rs, row_of(tn), N, K, nb, nbc, cn, L);
-      step(Ba, t, c);
-      if (!more) break;
-      t = tn;
-      c = cn;
-      more = advance(tn, cn);
-      if (more) q8r_load<BPL>(Ba, rc, rs, row_of(tn), N, K, nb, nbc, cn, L);
-      step(Bb, t, c);
-      if (!more) break;
-      t = tn;
-      c = cn;
+    for (int u = 0; u < nu; u += 2) {
+      if (u + 1 < nu) load_u(Bb, u + 1);
+      step_u(Ba, u);
+      if (u + 1 >= nu) break;
+      if (u + 2 < nu) load_u(Ba, u + 2);
+      step_u(Bb, u + 1);
     }
   }
   if constexpr (!SWI) {
@@ -1265,20 +1257,26 @@ template <int PRO, bool SWI>
 static void launch_q8r_fused(int K, int ntiles, size_t lds, hipStream_t st, const int8_t *codes, const float *scales,
                              const pq_gemv_prologue &p, void *y, int yb, int N, float *parts) {
   const int G = q8r_fused_grid(ntiles);
-  const bool two = G < ntiles || K > 2048;
+  const bool one = G == ntiles && K <= 2048;   // one unit per workgroup
   const dim3 grid((unsigned)G), blk(kRThreads);
   // K = 256 E; chunks of 2048 (one for K <= 2048): BPL = 1 at K = 1024, else 2
-#define PQ_Q8RF(BPL, E, TWO) \
-  launch(q8r_gemv_fused_kernel<BPL, PRO, E, TWO, SWI>, grid, blk, lds, st, codes, scales, p, y, yb, N, K, ntiles, \
+#define PQ_Q8RF(BPL, E, NS) \
+  launch(q8r_gemv_fused_kernel<BPL, PRO, E, NS, SWI>, grid, blk, lds, st, codes, scales, p, y, yb, N, K, ntiles, \
          parts)
+#define PQ_Q8RF_W(BPL, E)        \
+  do {                           \
+    if (one) PQ_Q8RF(BPL, E, 1); \
+    else PQ_Q8RF(BPL, E, 2);     \
+  } while (0)
   switch (K) {
-    case 1024: if (two) PQ_Q8RF(1, 4, true); else PQ_Q8RF(1, 4, false); break;
-    case 2048: if (two) PQ_Q8RF(2, 8, true); else PQ_Q8RF(2, 8, false); break;
-    case 4096: PQ_Q8RF(2, 16, true); break;
+    case 1024: PQ_Q8RF_W(1, 4); break;
+    case 2048: PQ_Q8RF_W(2, 8); break;
+    case 4096: PQ_Q8RF(2, 16, 2); break;
     default:
-      if constexpr (pro_base(PRO) != PQ_PRO_CONV) PQ_Q8RF(2, 32, true);
+      if constexpr (pro_base(PRO) != PQ_PRO_CONV) PQ_Q8RF(2, 32, 2);
       break;
   }
+#undef PQ_Q8RF_W
 #undef PQ_Q8RF
 }
 

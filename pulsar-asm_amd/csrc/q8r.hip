@@ -90,6 +90,68 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_kernel(const int8_t *__res
   }
 }
 
+// q8r_gemv_kernel for rows of several 2048-wide chunks when N alone gives too
+// few workgroups (down, K = 8192: N/8 workgroups of one CU each): CW half-waves
+// per row, half-wave g taking chunks g, g + CW, ... (the next one loading while
+// this one folds), each chunk's partial (lane 0 after the tree) into LDS; then
+// one thread per row adds them in chunk order from 0, y = ((0 + p0) + p1) + ...
+// as the single-walker kernel does. x is staged once per 8 rows as there.
+template <int CW>
+__global__ __launch_bounds__(kRThreads * CW) void q8r_gemv_kc_kernel(const int8_t *__restrict__ codes,
+                                                                    const float *__restrict__ scales,
+                                                                    const uint16_t *__restrict__ x,
+                                                                    void *__restrict__ y, int y_bf16, int N, int K) {
+  constexpr int BPL = 2;   // 2048-wide chunks: 64 blocks over 32 lanes
+  extern __shared__ __align__(16) float xs[];   // [nb][kRXStride]
+  __shared__ float pp[kRRows][kRMaxChunks];
+  const int t = blockIdx.y;
+  const int nb = K / kQ, nbc = 2048 / kQ, nch = K / 2048;
+  const int hw = threadIdx.x >> 5, L = threadIdx.x & 31, r = hw / CW, g = hw % CW;
+  const int row = blockIdx.x * kRRows + r;
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(codes), (short)0, N * K, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scales), (short)0, N * nb * 4, kRsrcWord3);
+  RBlocks Ba, Bb;
+  q8r_load<BPL>(Ba, rc, rs, row, N, K, nb, nbc, g, L);
+  const uint16_t *xt = x + (size_t)t * K;
+  for (int e = threadIdx.x * 8; e < K; e += kRThreads * CW * 8) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(xt + e);
+    const uint32_t v[4] = {u.x, u.y, u.z, u.w};
+    float f[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      f[2 * k] = __uint_as_float(v[k] << 16);
+      f[2 * k + 1] = __uint_as_float(v[k] & 0xffff0000u);
+    }
+    float *d = xs + (size_t)(e >> 5) * kRXStride + (e & 31);
+    *reinterpret_cast<float4 *>(d) = make_float4(f[0], f[1], f[2], f[3]);
+    *reinterpret_cast<float4 *>(d + 4) = make_float4(f[4], f[5], f[6], f[7]);
+  }
+  __syncthreads();
+  auto chunk = [&](const RBlocks &B, int c) {
+    const float acc = leaf_tree32(q8r_leaf<BPL>(B, xs, nbc, c, L));
+    if (L == 0) pp[r][c] = acc;
+  };
+  for (int c = g; c < nch; c += 2 * CW) {
+    if (c + CW < nch) q8r_load<BPL>(Bb, rc, rs, row, N, K, nb, nbc, c + CW, L);
+    chunk(Ba, c);
+    if (c + CW >= nch) break;
+    if (c + 2 * CW < nch) q8r_load<BPL>(Ba, rc, rs, row, N, K, nb, nbc, c + 2 * CW, L);
+    chunk(Bb, c + CW);
+  }
+  lds_barrier();
+  if (threadIdx.x < kRRows) {
+    const int rw = blockIdx.x * kRRows + threadIdx.x;
+    float yv = 0.0f;
+    for (int c = 0; c < nch; c++) yv = yv + pp[threadIdx.x][c];
+    if (rw < N) {
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)t * N + rw] = f2bf(yv);
+      else reinterpret_cast<float *>(y)[(size_t)t * N + rw] = yv;
+    }
+  }
+}
+
 // The T-wide form (T > 1): the same per-output arithmetic, with each weight
 // load serving many positions. A workgroup takes 8 rows x up to kRTPW
 // positions; per chunk of K its lanes load their leaves' blocks once (CVT:
@@ -232,6 +294,19 @@ extern "C" int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint1
   }
   const dim3 grid((unsigned)((N + kRRows - 1) / kRRows), (unsigned)T), block(kRThreads);
   const bool mc = K / KC > 1;
+  // rows of 2..8 chunks on fewer than 1024 workgroups: CW = 2 half-waves per row (PQ_Q8R_CW: 1, 2 or
+  // 4). Measured per launch with cold weights: down 2048 x 8192 7.53 / 6.75 / 6.78 us at CW = 1 / 2 /
+  // 4, 4096 x 12288 13.5 / 12.6 / 15.9 us, 2048 x 4096 5.0 / 4.7 / 4.7 us
+  static const int env_cw = env_int("PQ_Q8R_CW");
+  const int nch = K / KC;
+  int cw = env_cw > 0 ? env_cw : (mc && nch <= kRMaxChunks && grid.x * T < 1024 ? 2 : 1);
+  if (nch < 4) cw = std::min(cw, 2);   // no idle half-waves
+  if (mc && nch <= kRMaxChunks && cw > 1) {
+    const dim3 bk(kRThreads * cw);
+    if (cw == 2) launch(q8r_gemv_kc_kernel<2>, grid, bk, lds, st, codes, scales, x, y, yb, N, K);
+    else launch(q8r_gemv_kc_kernel<4>, grid, bk, lds, st, codes, scales, x, y, yb, N, K);
+    return check_launch("pq_q8r_gemv");
+  }
 #define PQ_Q8R_V(BB)                                                                                           \
   do {                                                                                                         \
     if (mc) launch(q8r_gemv_kernel<BB, true>, grid, block, lds, st, codes, scales, x, y, yb, N, K);            \

@@ -13,6 +13,7 @@ namespace pq {
 constexpr int kRRows = 8;        // rows per workgroup
 constexpr int kRThreads = 32 * kRRows;
 constexpr int kRXStride = 36;    // LDS floats per staged 32-block of x
+constexpr int kRMaxChunks = 8;   // 2048-wide chunks a row may hold in the chunk-split form
 
 __host__ __device__ inline int q8r_chunk(int K) { return (K >= 2048 && K % 2048 == 0) ? 2048 : K; }
 
