@@ -230,7 +230,11 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemm_kernel(const int8_t *__res
               dot = __builtin_fmaf(cf[i][4 * q + 2], x4.z, dot);
               dot = __builtin_fmaf(cf[i][4 * q + 3], x4.w, dot);
             } else {
-              const uint32_t w = (uint32_t)(q < 4 ? B.c[2 * i][q] : B.c[2 * i + 1][q - 4]);
+              // the code word passes through an empty asm per position: otherwise the converts,
+              // invariant in p, are hoisted out of the position loop and their 32 * BPL
+              // values held (BPL = 8: 256 VGPRs, one wave per SIMD; with this 105, four)
+              uint32_t w = (uint32_t)(q < 4 ? B.c[2 * i][q] : B.c[2 * i + 1][q - 4]);
+              asm volatile("" : "+v"(w));
               dot = __builtin_fmaf((float)(int8_t)(w & 0xffu), x4.x, dot);
               dot = __builtin_fmaf((float)(int8_t)((w >> 8) & 0xffu), x4.y, dot);
               dot = __builtin_fmaf((float)(int8_t)((w >> 16) & 0xffu), x4.z, dot);
