@@ -638,6 +638,21 @@ def ternary_bench(pq, torch, dev, g, stream, reps=20):
     gr = graph_of(torch, lambda: [step(i) for i in range(reps)])
     ms = timed_replay(torch, gr, stream) / reps
     del gr
+
+    # gate and up read the same activations: one batched launch for both, as the
+    # reference's engine calls them (gemvP_multi), then down
+    def gate_up(i):
+        a, b = pools["gate"][i % len(pools["gate"])], pools["up"][i % len(pools["up"])]
+        pq.tq2_gemv_batch([a, b], x4, 4096, outs=[outs["gate"], outs["up"]])
+
+    def step_b(i):
+        gate_up(i)
+        launch_of(shapes[2])(i)
+
+    gr = graph_of(torch, lambda: [step_b(i) for i in range(reps)])
+    ms_b = timed_replay(torch, gr, stream) / reps
+    del gr
+    gu_us = period_ms(torch, gate_up, 3 * len(pools["gate"]), stream) * 1e3
     nb = {n: N * K // 4 + N * K // 128 * 2 + K // 256 * 292 + N * 4 for (n, N, K) in shapes}
     per = _per_shape(pq, torch, stream, shapes, launch_of, lambda s: nb[s[0]])
     step_bytes = sum(nb.values())
@@ -650,7 +665,10 @@ def ternary_bench(pq, torch, dev, g, stream, reps=20):
             "bytes_per_step": step_bytes, "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "period_us_sum": round(kern, 2), "period_hbm_frac": round(step_bytes / (kern * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "per_shape": per, "rotated_MB_per_shape": ROTATE_MB}
+            "per_shape": per, "rotated_MB_per_shape": ROTATE_MB,
+            "batched_gate_up": {"us_per_step": round(ms_b * 1e3, 2), "gate_up_launch_us": round(gu_us, 2),
+                                "GB/s": round(step_bytes / (ms_b * 1e-3) / 1e9, 1),
+                                "hbm_frac": round(step_bytes / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
 def main():

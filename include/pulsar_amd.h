@@ -387,6 +387,16 @@ int pq_attn_layer_decode(const uint16_t *qkvg, const float *q_norm, const float 
  * of a negative status on error. */
 int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int K,
                 int N, void *stream);
+/* n = 1..3 ternary tensors of the same K over the same xq in one launch
+ * (codes[i], scales[i], ys[i]: device pointers in host arrays; rows[i] rows
+ * each), every output the bits pq_tq2_gemv gives it: the gate and up
+ * projections of an FFN, or q, k and v. Replaces the batched launch the
+ * reference's engine makes for projections that read one activation
+ * (pq2_gemv_batch, pq2_fwd8_shim.h:16, called from gemvP_multi, fwd8.c:303-310
+ * and 857-861; the device form is pq1_gemv_batch_launch,
+ * pq1_swar_sm53.cu:1480-1680). */
+int pq_tq2_gemv_batch(const uint8_t *const *codes, const uint16_t *const *scales, const uint8_t *xq,
+                      float *const *ys, int K, const int *rows, int n, void *stream);
 /* x [T][K] fp32 -> Q8_K blocks (quantize_row_q8_K_ref as restated in
  * fwd8.c:61-137); K a multiple of 256. */
 int pq_q8k_quant(const float *x, uint8_t *out, int K, int T, void *stream);

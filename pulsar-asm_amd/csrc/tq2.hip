@@ -88,6 +88,19 @@ __device__ __forceinline__ void tq2_store_x(const TqX<XR> &t, int K, int *xperm,
   }
 }
 
+// Up to three tensors of one K over the same activations in one launch (the
+// reference's batched launch for projections that read the same vector): the
+// workgroups of tensor i are wg0[i] .. wg0[i+1]-1, so each workgroup's rows
+// are one tensor's and every row runs the single-tensor arithmetic.
+constexpr int kTqBatch = 3;
+struct TqBatch {
+  const uint8_t *codes[kTqBatch];
+  const uint16_t *scales[kTqBatch];
+  float *y[kTqBatch];
+  int rows[kTqBatch];
+  int wg0[kTqBatch + 1];
+};
+
 // LPR lanes per row (16, 32 or 64), NT/LPR rows per workgroup of NT threads. Lane gs of a row
 // reads the row's 16-byte pieces gs, gs + LPR, ... (a row's lanes cover
 // 16*LPR contiguous bytes per load, whole cache lines): piece p is half p % 2 of group p / 2, so lanes
@@ -95,10 +108,7 @@ __device__ __forceinline__ void tq2_store_x(const TqX<XR> &t, int K, int *xperm,
 // half-dots add across the pair, and the even lane forms the group partial.
 // PPL pieces per lane per round (LPR*PPL pieces = 64*LPR*PPL of K).
 template <int LPR, int PPL, int XR, int NT>
-__global__ __launch_bounds__(NT) void tq2_gemv_kernel(const uint8_t *__restrict__ codes,
-                                                        const uint16_t *__restrict__ scales,
-                                                        const uint8_t *__restrict__ xq, float *__restrict__ y, int N,
-                                                        int K) {
+__global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t *__restrict__ xq, int K) {
   static_assert(64 % LPR == 0, "a row's lanes must sit in one wave");
   extern __shared__ __align__(16) unsigned char smem[];
   const int ng = K / kTqGroup, npc = 2 * ng;                 // groups, 16-byte pieces per row
@@ -108,7 +118,12 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(const uint8_t *__restrict_
   float *pg = db + ng;                                         // [NT/LPR rows][ng] group partials
   const int tid = threadIdx.x;
   const int r = tid / LPR, gs = tid % LPR;
-  const int row = blockIdx.x * (NT / LPR) + r;
+  const int ti = (int)blockIdx.x >= bt.wg0[2] ? 2 : (int)blockIdx.x >= bt.wg0[1] ? 1 : 0;   // workgroup-uniform
+  const uint8_t *__restrict__ codes = bt.codes[ti];
+  const uint16_t *__restrict__ scales = bt.scales[ti];
+  float *__restrict__ y = bt.y[ti];
+  const int N = bt.rows[ti];
+  const int row = ((int)blockIdx.x - bt.wg0[ti]) * (NT / LPR) + r;
   const bool live = row < N;
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(codes + (size_t)(live ? row : 0) * (K / 4)), (short)0, live ? K / 4 : 0, kRsrcWord3);
@@ -230,14 +245,9 @@ extern "C" int pq_q8k_quant(const float *x, uint8_t *out, int K, int T, void *st
   return check_launch("pq_q8k_quant");
 }
 
-extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int K, int N,
-                           void *stream) {
-  PQ_REQUIRE(codes && scales && xq && y, PQ_ERR_ARG, "pq_tq2_gemv: null pointer");
-  PQ_REQUIRE(N > 0 && K > 0 && K % kQ8K == 0 && K <= 32768, PQ_ERR_ARG,
-             "pq_tq2_gemv: N=%d K=%d (K a multiple of 256, at most 32768)", N, K);
-  PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
+// The launch for a batch of n tensors (rows and pointers checked by the caller).
+static int tq2_launch(TqBatch bt, int n, const uint8_t *xq, int K, hipStream_t st, const char *who) {
   const int ng = K / kTqGroup;
-  hipStream_t st = as_stream(stream);
   // lanes per row by row length: 64 from 192 pieces (K = 12288), 32 from 64
   // pieces (K = 4096), else 16 (measured at 256 and at 512 threads); PPL
   // covers a row in one round up to K = 12288
@@ -252,10 +262,13 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   const int nt = envt == 256 || envt == 512 || envt == 1024 ? envt : 512;
   const int rows = nt / lpr;
   const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)rows * ng * 4;
-  const dim3 grid((unsigned)((N + rows - 1) / rows)), block(nt);
+  bt.wg0[0] = 0;
+  for (int i = 0; i < kTqBatch; i++) bt.wg0[i + 1] = bt.wg0[i] + (i < n ? (bt.rows[i] + rows - 1) / rows : 0);
+  for (int i = n; i < kTqBatch; i++) bt.wg0[i + 1] = 0x7fffffff;   // never selected
+  const dim3 grid((unsigned)bt.wg0[n]), block(nt);
   // 16-qs runs of x per thread (K/16 runs over nt threads)
   const int runs = (K / 16 + nt - 1) / nt, xr = runs <= 1 ? 1 : runs <= 2 ? 2 : runs <= 4 ? 4 : 8;
-#define PQ_TQ2_X(L, P, X, T) launch(tq2_gemv_kernel<L, P, X, T>, grid, block, lds, st, codes, scales, xq, y, N, K)
+#define PQ_TQ2_X(L, P, X, T) launch(tq2_gemv_kernel<L, P, X, T>, grid, block, lds, st, bt, xq, K)
 #define PQ_TQ2_T(L, P)                                             \
   do {                                                             \
     if (nt == 1024) {                                              \
@@ -287,5 +300,42 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   }
 #undef PQ_TQ2_T
 #undef PQ_TQ2_X
-  return check_launch("pq_tq2_gemv");
+  return check_launch(who);
+}
+
+extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const uint8_t *xq, float *y, int K, int N,
+                           void *stream) {
+  PQ_REQUIRE(codes && scales && xq && y, PQ_ERR_ARG, "pq_tq2_gemv: null pointer");
+  PQ_REQUIRE(N > 0 && K > 0 && K % kQ8K == 0 && K <= 32768, PQ_ERR_ARG,
+             "pq_tq2_gemv: N=%d K=%d (K a multiple of 256, at most 32768)", N, K);
+  PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
+  TqBatch bt{};
+  bt.codes[0] = codes;
+  bt.scales[0] = scales;
+  bt.y[0] = y;
+  bt.rows[0] = N;
+  return tq2_launch(bt, 1, xq, K, as_stream(stream), "pq_tq2_gemv");
+}
+
+extern "C" int pq_tq2_gemv_batch(const uint8_t *const *codes, const uint16_t *const *scales, const uint8_t *xq,
+                                 float *const *ys, int K, const int *rows, int n, void *stream) {
+  PQ_REQUIRE(codes && scales && xq && ys && rows && n >= 1 && n <= kTqBatch, PQ_ERR_ARG,
+             "pq_tq2_gemv_batch: null pointer or n=%d (1..3)", n);
+  PQ_REQUIRE(K > 0 && K % kQ8K == 0 && K <= 32768, PQ_ERR_ARG,
+             "pq_tq2_gemv_batch: K=%d (a multiple of 256, at most 32768)", K);
+  PQ_REQUIRE(aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv_batch: xq alignment");
+  TqBatch bt{};
+  long long wgs = 0;
+  for (int i = 0; i < n; i++) {
+    PQ_REQUIRE(codes[i] && scales[i] && ys[i] && rows[i] > 0, PQ_ERR_ARG,
+               "pq_tq2_gemv_batch: tensor %d: null pointer or rows=%d", i, rows[i]);
+    PQ_REQUIRE(aligned(codes[i], 16), PQ_ERR_ALIGN, "pq_tq2_gemv_batch: tensor %d codes must be 16-byte aligned", i);
+    bt.codes[i] = codes[i];
+    bt.scales[i] = scales[i];
+    bt.y[i] = ys[i];
+    bt.rows[i] = rows[i];
+    wgs += rows[i];
+  }
+  PQ_REQUIRE(wgs < (1ll << 30), PQ_ERR_ARG, "pq_tq2_gemv_batch: %lld rows in all", wgs);
+  return tq2_launch(bt, n, xq, K, as_stream(stream), "pq_tq2_gemv_batch");
 }

@@ -78,6 +78,7 @@ SIGNATURES = {
     "pq_q8_gemv_fused_swiglu": (I, [P, P, C.POINTER(GemvPrologue), P, P, I, I, P]),
     "pq_attn_layer_decode": (I, [P, P, P, P, P, P, I, I, I, I, I, I, F, F, P, P, P, P]),
     "pq_tq2_gemv": (I, [P, P, P, P, I, I, P]),
+    "pq_tq2_gemv_batch": (I, [P, P, P, P, I, P, I, P]),
     "pq_q8_gemm_scratch_bytes": (Z, []),
     "pq_q8_gemm_noalloc": (I, [P, P, P, P, P, I, I, I, I, P]),
     "pq_q8k_quant": (I, [P, P, I, I, P]),

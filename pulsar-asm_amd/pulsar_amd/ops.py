@@ -9,7 +9,7 @@ import torch
 from . import check, lib
 
 __all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
-           "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "gemv_fused",
+           "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "tq2_gemv_batch", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "q8r_gemv_fused_swiglu", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
            "PRO_CONV", "PRO_F32"]
@@ -243,6 +243,22 @@ def tq2_gemv(codes, scales, xq, K, N, out=None):
     check(lib().pq_tq2_gemv(codes.data_ptr(), scales.data_ptr(), xq.data_ptr(), out.data_ptr(), K, N, stream_ptr()),
           "pq_tq2_gemv")
     return out
+
+
+def tq2_gemv_batch(tensors, xq, K, outs=None):
+    """1..3 ternary tensors [(codes, scales), ...] of one K over the same Q8_K
+    xq in one launch (pq_tq2_gemv_batch) -> [y fp32 [N_i], ...]."""
+    import ctypes as C
+    n = len(tensors)
+    rows = [int(c.shape[0]) for c, _ in tensors]
+    if outs is None:
+        outs = [torch.empty(r, dtype=torch.float32, device=xq.device) for r in rows]
+    cp = (C.c_void_p * n)(*[c.data_ptr() for c, _ in tensors])
+    sp = (C.c_void_p * n)(*[s.data_ptr() for _, s in tensors])
+    yp = (C.c_void_p * n)(*[o.data_ptr() for o in outs])
+    rp = (C.c_int * n)(*rows)
+    check(lib().pq_tq2_gemv_batch(cp, sp, xq.data_ptr(), yp, K, rp, n, stream_ptr()), "pq_tq2_gemv_batch")
+    return outs
 
 
 # ------------------------------------------------------- fused decode path

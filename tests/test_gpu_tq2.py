@@ -71,3 +71,25 @@ def test_tq2_reference_call_order(orc, pq, dev, N, K):
     # K that is not a multiple of 256 is refused with a negative status
     assert pq.lib().pq_tq2_gemv(ctypes.c_void_p(d_cd.data_ptr()), ctypes.c_void_p(d_sc.data_ptr()),
                                 ctypes.c_void_p(d_xq.data_ptr()), ctypes.c_void_p(d_y.data_ptr()), 100, rows, None) < 0
+
+
+# one launch over several tensors of one K: each tensor's rows give the oracle's
+# bits (row counts that do and do not fill whole workgroups, one to three tensors)
+@pytest.mark.parametrize("rows,K", [((12288, 12288), 4096), ((2048, 512, 512), 4096), ((61, 1001, 37), 2560),
+                                    ((4096,), 12288), ((3, 5), 256)])
+def test_tq2_gemv_batch(orc, pq, dev, rows, K):
+    print(f"tq2 batch rows={rows} K={K}", flush=True)
+    x = orc.gen_normal(K + 7, K)
+    xq = orc.q8k_quant(x)
+    xqd = pq.q8k_quant(torch.from_numpy(x).to(dev))
+    host, dev_t = [], []
+    for i, N in enumerate(rows):
+        codes = orc.gen_ternary(N + K + 11 * i, N * K // 4).reshape(N, K // 4)
+        S = orc.gen_scales(N + K + 11 * i + 1, N * K // 128).reshape(N, K // 128)
+        host.append((codes, S, N))
+        dev_t.append((torch.from_numpy(codes).to(dev), torch.from_numpy(S.view(np.int16)).to(dev)))
+    ys = pq.tq2_gemv_batch(dev_t, xqd, K)
+    torch.cuda.synchronize()
+    for (codes, S, N), y in zip(host, ys):
+        want = orc.tq2_gemv(codes, S, xq, N, K)
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32)), N
