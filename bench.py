@@ -785,6 +785,7 @@ def main():
         line["decode_lfm3_real_shapes"] = decode_variant(pq, LFM3_REAL)
         from pulsar_amd.engine import LFM3_SYNTH
         line["decode_ref_numerics"] = decode_variant(pq, dict(LFM3_SYNTH, numerics=1))
+        line["decode_ref_numerics_real_shapes"] = decode_variant(pq, dict(LFM3_REAL, numerics=1))
         line["prefill_gemm"] = prefill_gemm_bench(pq, torch, dev, g, stream, gpu)
         line["ternary_gemv"] = ternary_bench(pq, torch, dev, g, stream)
         line["ref_numerics_gemv"] = ref_numerics_bench(pq, torch, dev, g, stream)
