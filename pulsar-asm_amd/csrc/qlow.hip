@@ -90,7 +90,7 @@ __device__ __forceinline__ void qlow_place(int b, int ntiles, int &tile, int &su
 // With ws (the split form): workgroup (slice of rows, s) covers only K slice
 // s = blockIdx.y and writes its y_s to ws[s][N]; qlow_combine_kernel adds the
 // slices in order. Without ws: all K slices in one workgroup.
-template <int B, int RS, int XL, int NT>
+template <int B, int RS, int XL, int NT, int PF>
 __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict__ pc,
                                                               const uint32_t *__restrict__ ps,
                                                               const uint16_t *__restrict__ x, void *__restrict__ y,
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   // lane's first PF groups' codes, then the slice's scale pairs (4 rows per
   // 16-byte load, up to kScl loads per thread; any more come after the
   // partials).
-  constexpr int kXLoads = XL, PF = 4, kScl = 4;
+  constexpr int kXLoads = XL, kScl = 4;
   constexpr int HQ = RS / 4;
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, K * 2, kRsrcWord3);
@@ -403,8 +403,17 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   const uint32_t *ps32 = reinterpret_cast<const uint32_t *>(pscales);
   // x loads per thread for the K one workgroup covers (NT threads x 8)
   const int xl = (G * kQ + 8 * NT - 1) / (8 * NT), XL = xl <= 1 ? 1 : xl <= 2 ? 2 : xl <= 4 ? 4 : 8;
-#define PQ_QLOW(BB, RR, XX, TT) \
-  launch(qlow_gemv_kernel<BB, RR, XX, TT>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf)
+  // PF groups of loads in flight per slot: 2 (the partials of one round overlap the next
+  // round's loads); per config-2 step Q4 22.9 / 21.9 / 22.4 us at PF = 4 / 2 / 1, Q5 24.2 / 23.5 /
+  // 23.9 us (PQ_QLOW_PF: 1, 2 or 4)
+  static const int env_pf = env_int("PQ_QLOW_PF");
+  const int pf = env_pf == 1 || env_pf == 4 ? env_pf : 2;
+#define PQ_QLOW(BB, RR, XX, TT)                                                                            \
+  do {                                                                                                     \
+    if (pf == 1) launch(qlow_gemv_kernel<BB, RR, XX, TT, 1>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf); \
+    else if (pf == 2) launch(qlow_gemv_kernel<BB, RR, XX, TT, 2>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf); \
+    else launch(qlow_gemv_kernel<BB, RR, XX, TT, 4>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf); \
+  } while (0)
 #define PQ_QLOW_X(BB, RR)                                  \
   if (NT == 512) {                                         \
     switch (XL) {                                          \
