@@ -682,6 +682,9 @@ def main():
                     help="also run a plain elementwise kernel over 256 MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill-profile", action="store_true",
                     help="only run the prefill GEMMs (3 launches each at T=512 and T=32) for counter runs; no JSON")
+    ap.add_argument("--decode-profile", choices=["synth", "real", "synth-ref", "real-ref"],
+                    help="only run one backbone's decode measurement (the synthetic or the real LFM3 shapes, "
+                         "-ref: the reference's GEMV numerics) for kernel traces; prints its result")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: there is no multi-GPU path (the GEMV would shard by rows, with an "
@@ -694,6 +697,13 @@ def main():
     dev = torch.device("cuda:0")
     if args.prefill_profile:
         prefill_profile_workload(pq, torch, dev)
+        return
+    if args.decode_profile:
+        from pulsar_amd.engine import LFM3_SYNTH
+        cfg = dict(LFM3_SYNTH if args.decode_profile.startswith("synth") else LFM3_REAL)
+        if args.decode_profile.endswith("-ref"):
+            cfg["numerics"] = 1
+        print(json.dumps({"decode_profile": args.decode_profile, **decode_variant(pq, cfg)}))
         return
     torch.manual_seed(20261201)
     g = torch.Generator(device=dev)
