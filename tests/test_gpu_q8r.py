@@ -31,12 +31,13 @@ def _run(pq, dev, W, S, xb, dt):
 # 12288 fold several 2048-wide chunks, K = 7680 and 2560 are one chunk of 240
 # and 80 blocks (leaves with several blocks, codes widened per use); at T = 1
 # rows of 2..8 chunks on few workgroups split their chunks over half-waves
-# (K = 4096, 6144: two per row; 8192, 12288, 16384: four)
+# (K = 4096, 6144: two per row; 8192, 12288, 16384: four); K = 5120, 7680
+# and 8160 are one chunk of 5..8 blocks per lane
 @pytest.mark.parametrize("N,K,T", [(8192, 2048, 1), (3072, 2048, 1), (2048, 8192, 1), (97, 7680, 2),
                                    (61, 512, 1), (37, 1024, 3), (13, 32, 1), (65, 12288, 1), (45, 2560, 2),
                                    (2048, 2048, 4), (300, 2048, 40), (77, 8192, 33), (97, 7680, 9),
                                    (64, 12288, 5), (45, 2560, 17), (300, 4096, 1), (33, 16384, 1),
-                                   (7, 6144, 1)])
+                                   (7, 6144, 1), (2048, 7680, 1), (131, 5120, 1), (40, 8160, 1)])
 def test_q8r_gemv_bitexact(orc, pq, dev, N, K, T):
     print(f"q8r N={N} K={K} T={T}", flush=True)
     W, S, xb = _case(orc, N, K, T, SEED + N + K, signed_scales=(N % 2 == 1))
