@@ -8,6 +8,9 @@ Outputs:
                                  the reference sources where they lie:
                                  .auto/lfm3/q8_gemv_cpu.c (needs _Float16 -> ROCm clang)
                                  pulsar_arm/bonsai2/pq2_host.c
+                                 pulsar_arm/bonsai2/bq1_cpu.c (its bq1_quant_row_i8: the
+                                 Q8_K block rule, NEON-free, where fwd8.c's copy needs
+                                 arm_neon.h)
 Both directories are git-ignored and travel with the tree to a GPU machine.
 """
 import os
@@ -42,7 +45,8 @@ def build_ref():
     reference tree is absent (a machine without it uses the prebuilt file)."""
     q8 = os.path.join(REF_ROOT, ".auto/lfm3/q8_gemv_cpu.c")
     pq2 = os.path.join(REF_ROOT, "pulsar_arm/bonsai2/pq2_host.c")
-    if not (os.path.exists(q8) and os.path.exists(pq2)):
+    bq1 = os.path.join(REF_ROOT, "pulsar_arm/bonsai2/bq1_cpu.c")
+    if not (os.path.exists(q8) and os.path.exists(pq2) and os.path.exists(bq1)):
         return None
     out_dir = os.path.join(HERE, "_ref")
     os.makedirs(out_dir, exist_ok=True)
@@ -51,7 +55,7 @@ def build_ref():
     omp_lib = "/opt/rocm/llvm/lib"
     _run([CLANG, *FLAGS, "-fopenmp", "-w", f'-DREF_Q8_CPU="{q8}"',
           "-I", os.path.dirname(pq2), "-o", tmp,
-          os.path.join(HERE, "ref_shim.c"), pq2,
+          os.path.join(HERE, "ref_shim.c"), pq2, bq1,
           "-L", omp_lib, f"-Wl,-rpath,{omp_lib}", "-lomp", "-lm"])
     os.replace(tmp, out)
     return out

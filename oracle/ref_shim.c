@@ -7,7 +7,9 @@
  *   ref_q8_gemv   -> gemv_q8   (.auto/lfm3/q8_gemv_cpu.c:29-58)
  *   ref_q8_quant  -> quant_row (.auto/lfm3/q8_gemv_cpu.c:63-81)
  *   ref_set_threads / ref_max_threads -> the OpenMP team size
- *   pq2_gemv_cpu / pq2_h2f are exported by pulsar_arm/bonsai2/pq2_host.c itself.
+ *   pq2_gemv_cpu / pq2_h2f are exported by pulsar_arm/bonsai2/pq2_host.c itself;
+ *   bq1_quant_row_i8 by pulsar_arm/bonsai2/bq1_cpu.c itself (bq1_cpu.c:40-54,
+ *   the Q8_K rule of fwd8.c:72-137 over one block of K values).
  */
 #include <omp.h>
 

@@ -160,6 +160,41 @@ def test_q8k_quant_properties(orc):
         assert np.abs(qs * np.float64(d) - xb).max() <= abs(d) * 0.5000001
 
 
+def test_q8k_quant_is_reference_code(orc):
+    """orc_q8k_quant's d and qs equal the reference's own Q8_K block rule run on
+    each 256-block: bq1_quant_row_i8 (bq1_cpu.c:40-54, oracle/_ref), which the
+    reference states is fwd8.c's q8_K_quant rule (fwd8.c:72-137: first index
+    reaching |x|max, iscale = -127/max, the 1.5*2^23 round, min(127, .),
+    d = 1/iscale; an all-zero block gives d = 0 and qs = 0). bsums are the
+    exact sums of 16 qs (fwd8.c leaves an all-zero block's bsums stale; the
+    oracle writes zeros there)."""
+    ref = orc.ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    import ctypes as C
+    ref.bq1_quant_row_i8.restype = C.c_float
+    ref.bq1_quant_row_i8.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+    rng = np.random.default_rng(29)
+    nb = 64
+    x = (rng.standard_normal(nb * 256) * rng.choice([1e-30, 1e-3, 1.0, 40.0, 3e4], nb * 256)).astype(np.float32)
+    x[256:512] = 0.0                                    # all-zero block
+    x[512:768] = np.clip(x[512:768], -4.0, 4.0)         # ties for |x|max: the first index (-9) wins
+    x[512 + 7] = -9.0
+    x[512 + 100] = x[512 + 200] = 9.0
+    x[768:1024] = np.float32(0.5) * rng.integers(-300, 300, 256).astype(np.float32)   # exact halves: ties to even
+    x[1024:1280] = 0.0
+    x[1024 + 255] = -1e-41                              # a lone subnormal
+    out = orc.q8k_quant(x)
+    for b in range(nb):
+        xb = np.ascontiguousarray(x[b * 256:(b + 1) * 256])
+        qr = np.empty(256, np.int8)
+        dr = ref.bq1_quant_row_i8(xb.ctypes.data_as(C.c_void_p), qr.ctypes.data_as(C.c_void_p), 256)
+        blk = out[b * 292:(b + 1) * 292]
+        assert blk[:4].view(np.uint32)[0] == np.float32(dr).view(np.uint32), b
+        assert np.array_equal(blk[4:260].view(np.int8), qr), b
+        assert np.array_equal(blk[260:292].view(np.int16), qr.astype(np.int32).reshape(16, 16).sum(1)), b
+
+
 # ------------------------------------------------------------------- GEMVs
 def _q8_case(orc, seed, N, K):
     W, S = orc.q8_weights(seed, N, K)
