@@ -77,7 +77,9 @@ def test_q8r_rejects_bad_args(pq, dev):
 @pytest.mark.parametrize("kind,N,K", [("resnorm", 3104, 2048), ("resnorm", 65536, 2048), ("resnorm", 300, 4096),
                                       ("norm", 6144, 2048), ("norm", 77, 1024), ("silu", 2048, 8192),
                                       ("silu", 2048, 4096), ("silu", 130, 2048), ("conv3", 2048, 2048),
-                                      ("conv7", 2048, 2048), ("conv3", 1000, 4096)])
+                                      ("conv7", 2048, 2048), ("conv3", 1000, 4096), ("conv7", 1000, 4096),
+                                      ("resnorm", 2052, 8192), ("norm", 4100, 8192), ("silu", 513, 1024),
+                                      ("resnorm", 7, 1024)])
 def test_q8r_gemv_fused(pq, dev, kind, N, K):
     print(f"q8r fused {kind} N={N} K={K}", flush=True)
     g = torch.Generator(device=dev)
