@@ -440,9 +440,10 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
 // u + 1 loads while unit u folds (unit 0 before the prologue; a third set,
 // two units ahead, measured slower in the decode step: 0.712 against 0.687
 // ms); NS = 1 is the one unit of a single-tile, single-chunk workgroup.
-// SWI: the tile is 4 gate rows t*4 + r and their up rows F + t*4 + r (codes
-// [2F][K], F = N/2); its 4 outputs are silu_mul_kernel's of the bf16 gate
-// and up values. Else, with parts: the workgroup's (largest y, its row; the
+// SWI: the tile is 4 gate rows t*4 + w and their up rows F + t*4 + w (codes
+// [2F][K], F = N/2), wave w holding gate row t*4 + w in lanes 0-31 and its up
+// row in lanes 32-63; lane 0 forms silu_mul_kernel's output from the bf16
+// gate and up values (no barrier per tile). Else, with parts: the workgroup's (largest y, its row; the
 // lowest row on ties) at parts[2 * blockIdx.x].
 template <int BPL, int PRO, int E, int NS, bool SWI>
 __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t *__restrict__ codes,
@@ -453,18 +454,15 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
   constexpr int W = kRThreads / 64;
   extern __shared__ __align__(16) float rxs[];   // [nb][kRXStride]
   __shared__ float red[16];
-  __shared__ float sw[2][kRRows];
   const int nb = K / kQ, KC = q8r_chunk(K), nbc = KC / kQ, nch = K / KC;
   const int r = threadIdx.x >> 5, L = threadIdx.x & 31, F = N >> 1;
-  auto row_of = [&](int t) { return SWI ? (r < kRRows / 2 ? t * (kRRows / 2) + r : F + t * (kRRows / 2) + r - kRRows / 2)
-                                        : t * kRRows + r; };
+  auto row_of = [&](int t) { return SWI ? ((r & 1) ? F : 0) + t * (kRRows / 2) + (r >> 1) : t * kRRows + r; };
   if (threadIdx.x >= W && threadIdx.x < 8) red[threadIdx.x] = red[8 + threadIdx.x] = 0.0f;
   const __amdgpu_buffer_rsrc_t rc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(codes), (short)0, N * K, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(scales), (short)0, N * nb * 4, kRsrcWord3);
   const int e0 = threadIdx.x * E;
-  int k = 0;   // tiles done (SWI's LDS slot)
   const int nu = nch * ((ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x);   // units
   auto load_u = [&](RBlocks &B, int u) {
     q8r_load<BPL>(B, rc, rs, row_of((int)blockIdx.x + (u / nch) * (int)gridDim.x), N, K, nb, nbc, u % nch, L);
@@ -489,14 +487,12 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
     yv = yv + leaf_tree32(q8r_leaf<BPL>(B, rxs, nbc, cc, L));
     if (cc + 1 < nch) return;
     if constexpr (SWI) {
-      if (L == 0) sw[k & 1][r] = bf2f(f2bf(yv));
-      lds_barrier();   // sw alternates per tile: its reads end before the next tile's barrier
-      if (threadIdx.x < kRRows / 2) {
-        const float a = sw[k & 1][threadIdx.x], u = sw[k & 1][kRRows / 2 + threadIdx.x];
+      const float u = bf2f(f2bf(__shfl_down(yv, 32, 64)));   // the up row's sum, from lane 32
+      if ((threadIdx.x & 63) == 0) {
+        const float a = bf2f(f2bf(yv));
         const float sg = 1.0f / (1.0f + expf_pq(-a));
-        reinterpret_cast<uint16_t *>(y)[tt * (kRRows / 2) + threadIdx.x] = f2bf((a * sg) * u);
+        reinterpret_cast<uint16_t *>(y)[tt * (kRRows / 2) + (threadIdx.x >> 6)] = f2bf((a * sg) * u);
       }
-      k++;
     } else {
       const int row = tt * kRRows + r;
       if (L == 0 && row < N) {
