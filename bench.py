@@ -721,6 +721,12 @@ def main():
         prefill_profile_workload(pq, torch, dev)
         return
     if args.decode_profile:
+        if args.calib:   # the counter calibration of the traffic runs: 256 MiB read + 256 MiB written
+            src = torch.randn(64 << 20, device=dev)
+            dst = torch.empty_like(src)
+            torch.neg(src, out=dst)
+            torch.cuda.synchronize()
+            del src, dst
         from pulsar_amd.engine import LFM3_SYNTH
         cfg = dict(LFM3_SYNTH if args.decode_profile.startswith("synth") else LFM3_REAL)
         if args.decode_profile.endswith("-ref"):
