@@ -46,7 +46,7 @@ SHAPES = [  # name, N, K, output dtype
 
 
 def measured_traffic():
-    """HBM bytes per step of the 5 GEMV launches, from the two rocprofv3 --pmc
+    """HBM bytes of one step's 5 GEMV launches, from the two rocprofv3 --pmc
     passes summarised in profiles/q8_gemv_hbm_traffic.md (None if absent)."""
     import re
     path = os.path.join(ROOT, "profiles", "q8_gemv_hbm_traffic.md")
@@ -796,7 +796,10 @@ def main():
                    "weight_copies_rotated": {n: len(p) for n, p in pools.items()},
                    "rotated_MB_per_shape": {n: round(len(pools[n]) * per_copy[n] / 1e6, 1) for n in pools}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     # per launch like achieved: the step's measured bytes over its 5 launches
+                     "traffic": (lambda t: t // len(SHAPES) if t else None)(measured_traffic()),
+                     "traffic_per_step": measured_traffic(),
                      "kernel": "q8_gemv_fused_kernel: the timed region's 5 x steps launches",
                      "launches": len(SHAPES) * args.steps, "avg_launch_us": round(launch_us, 3),
                      "bytes_per_launch": step_bytes // len(SHAPES), "per_shape_period": per,
