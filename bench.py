@@ -787,7 +787,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 x int8 -> int32 block dots; fp16 weight scales, fp32 activation scales, fp32 accumulate",
+        "dtype": "int8",
+        "dtype_detail": "int8 x int8 -> int32 block dots; fp16 weight scales, fp32 activation scales, fp32 accumulate",
         "data": "synthetic (seeded uniform int8 codes, |N(0,1)|*0.01 fp16 scales, N(0,1) fp32 x)",
         "config": {"workload": "one LFM-style layer's T=1 Q8_0 GEMVs + LM head (hidden 2048)",
                    "gpu": gpu,
