@@ -311,15 +311,11 @@ extern "C" int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint1
     else launch(q8r_gemv_kc_kernel<4>, grid, bk, lds, st, codes, scales, x, y, yb, N, K);
     return check_launch("pq_q8r_gemv");
   }
-#define PQ_Q8R_V(BB)                                                                                           \
-  do {                                                                                                         \
-    if (mc) launch(q8r_gemv_kernel<BB, true>, grid, block, lds, st, codes, scales, x, y, yb, N, K);            \
-    else launch(q8r_gemv_kernel<BB, false>, grid, block, lds, st, codes, scales, x, y, yb, N, K);              \
-  } while (0)
-  if (bpl <= 1) PQ_Q8R_V(1);
-  else if (bpl <= 2) PQ_Q8R_V(2);
-  else if (bpl <= 4) PQ_Q8R_V(4);
-  else PQ_Q8R_V(8);
-#undef PQ_Q8R_V
+  // several chunks only with 2048-wide chunks, i.e. 2 blocks per lane
+  if (mc) launch(q8r_gemv_kernel<2, true>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  else if (bpl <= 1) launch(q8r_gemv_kernel<1, false>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  else if (bpl <= 2) launch(q8r_gemv_kernel<2, false>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  else if (bpl <= 4) launch(q8r_gemv_kernel<4, false>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
+  else launch(q8r_gemv_kernel<8, false>, grid, block, lds, st, codes, scales, x, y, yb, N, K);
   return check_launch("pq_q8r_gemv");
 }
