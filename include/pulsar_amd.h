@@ -332,6 +332,7 @@ typedef struct pq_gemv_prologue {
   const int32_t *tok;
   int vocab;
   const float *xf;
+  const float *emb_sf;   /* PQ_PRO_EMBED under pq_q8r_gemv_fused: the row-major table's fp32 scales */
 } pq_gemv_prologue;
 int pq_q8_gemv_parts(int N, int K);
 int pq_q8_gemv_fused(const int8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
@@ -343,6 +344,10 @@ int pq_argmax_parts(const float *parts, int nparts, int32_t *out, void *stream);
  * bf16 values the unfused op would store. K is 1024, 2048, 4096 or 8192; y
  * bf16 or fp32; argmax_parts as for pq_q8_gemv_fused. Replaces the rmsnorm_body / k_silu_mul_bf / k_conv7 + gemv
  * pairs of layer_body (lfm3_nanode.cu:3739-3856) under the reference numerics. */
+/* (PQ_PRO_EMBED here reads the row-major .lfm3q8 table, emb_pc codes
+ * [vocab][K] and emb_sf fp32 scales [vocab][K/32]: x_out = bf16(code * scale)
+ * of row *tok, zeros for an id outside [0, vocab), as pq_embed_rows;
+ * k_dequant_row, lfm3_nanode.cu:138-142.) */
 int pq_q8r_gemv_fused(const int8_t *codes, const float *scales, const pq_gemv_prologue *pro, void *y,
                       int y_dtype, int N, int K, float *argmax_parts, void *stream);
 /* Workgroups of pq_q8r_gemv_fused for N rows: the (value, index) pairs it

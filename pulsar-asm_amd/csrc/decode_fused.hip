@@ -160,6 +160,7 @@ __device__ __forceinline__ void quant_lds(const float *v, int e0, int8_t *xs, fl
 // The CONV prologue comes in two tap counts (3: the synthetic backbone; 7:
 // LFM3's conv_L_cache): the template kind kProConv7 is PQ_PRO_CONV with 7 taps.
 constexpr int kProConv7 = 0x100 | PQ_PRO_CONV;
+constexpr int kProEmbedR = 0x100 | PQ_PRO_EMBED;   // EMBED on the row-major table (the R2 GEMV)
 constexpr int pro_base(int pro) { return pro & 0xff; }
 constexpr int conv_taps(int pro) { return pro == kProConv7 ? 7 : 3; }
 
@@ -171,6 +172,7 @@ struct ProRegs {
   float taps[E * NT];
   uint32_t emb_c[E / 4];
   uint16_t emb_s;
+  float emb_f;
 };
 
 template <int PRO, int E>
@@ -203,6 +205,14 @@ __device__ __forceinline__ void pro_load(const pq_gemv_prologue &p, int e0, int 
       r.emb_c[i] = ok ? *reinterpret_cast<const uint32_t *>(src) : 0u;
     }
     r.emb_s = ok ? p.emb_ps[(((size_t)tile * nch + b / kCB) * kTR + rr) * kCB + (b % kCB)] : (uint16_t)0;
+    ld_f32<E>(p.w0 + e0, r.f0);
+  } else if constexpr (PRO == kProEmbedR) {
+    const int id = *p.tok;
+    const bool ok = id >= 0 && id < p.vocab;   // an id outside the table gives a zero row
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(p.emb_pc + (size_t)(ok ? id : 0) * K + e0);
+#pragma unroll
+    for (int i = 0; i < E / 4; i++) r.emb_c[i] = ok ? src[i] : 0u;
+    r.emb_f = ok ? p.emb_sf[(size_t)id * (K / kQ) + e0 / kQ] : 0.0f;   // E <= 32: one block
     ld_f32<E>(p.w0 + e0, r.f0);
   } else if constexpr (PRO == PQ_PRO_SILU) {
     ld_raw<E>(p.gu + e0, r.u0);
@@ -256,6 +266,14 @@ __device__ __forceinline__ void pro_values(const pq_gemv_prologue &p, int e0, in
     uint32_t xb[E / 2];
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = (float)(int8_t)((r.emb_c[i >> 2] >> (8 * (i & 3))) & 0xffu) * sc;
+#pragma unroll
+    for (int i = 0; i < E; i += 2) xb[i >> 1] = bfr2(v[i], v[i + 1]);
+    if (writer) st_bf16w<E>(p.x_out + e0, xb);
+    norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
+  } else if constexpr (PRO == kProEmbedR) {   // pq_embed_rows' bf16(code * scale), then the norm
+    uint32_t xb[E / 2];
+#pragma unroll
+    for (int i = 0; i < E; i++) v[i] = (float)(int8_t)((r.emb_c[i >> 2] >> (8 * (i & 3))) & 0xffu) * r.emb_f;
 #pragma unroll
     for (int i = 0; i < E; i += 2) xb[i >> 1] = bfr2(v[i], v[i + 1]);
     if (writer) st_bf16w<E>(p.x_out + e0, xb);
@@ -1286,11 +1304,17 @@ static int q8r_fused_entry(const int8_t *codes, const float *scales, const pq_ge
   PQ_REQUIRE(aligned(codes, 16) && aligned(scales, 16), PQ_ERR_ALIGN, "%s: codes, scales alignment", who);
   PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "%s: y_dtype %d", who, y_dtype);
   const pq_gemv_prologue &p = *pro;
-  PQ_REQUIRE(p.kind == PQ_PRO_RESNORM || p.kind == PQ_PRO_NORM || (!SWI && (p.kind == PQ_PRO_SILU || p.kind == PQ_PRO_CONV)),
-             PQ_ERR_ARG, "%s: prologue kind %d (RESNORM, NORM%s)", who, p.kind, SWI ? "" : ", SILU or CONV");
+  PQ_REQUIRE(p.kind == PQ_PRO_RESNORM || p.kind == PQ_PRO_NORM ||
+                 (!SWI && (p.kind == PQ_PRO_SILU || p.kind == PQ_PRO_CONV || p.kind == PQ_PRO_EMBED)),
+             PQ_ERR_ARG, "%s: prologue kind %d (RESNORM, NORM%s)", who, p.kind, SWI ? "" : ", SILU, CONV or EMBED");
   PQ_REQUIRE(p.kind != PQ_PRO_CONV || K <= 4096, PQ_ERR_ARG, "%s: the CONV prologue takes K <= 4096", who);
-  const int rc = check_fused_args(codes, reinterpret_cast<const uint16_t *>(scales), pro, y, N, K, who);
-  if (rc) return rc;
+  if (p.kind == PQ_PRO_EMBED) {   // the row-major table (emb_pc codes, emb_sf fp32 scales)
+    PQ_REQUIRE(p.tok && p.emb_pc && p.emb_sf && p.x_out && p.w0 && p.vocab > 0 && aligned(p.emb_pc, 4), PQ_ERR_ARG,
+               "%s: EMBED needs tok, emb_pc (4-byte aligned), emb_sf, x_out, w0 and vocab", who);
+  } else {
+    const int rc = check_fused_args(codes, reinterpret_cast<const uint16_t *>(scales), pro, y, N, K, who);
+    if (rc) return rc;
+  }
   const size_t lds = (size_t)(K / kQ) * kRXStride * sizeof(float);
   const int ntiles = SWI ? N / kRRows : (N + kRRows - 1) / kRRows;
   const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
@@ -1300,7 +1324,8 @@ static int q8r_fused_entry(const int8_t *codes, const float *scales, const pq_ge
     case PQ_PRO_NORM: launch_q8r_fused<PQ_PRO_NORM, SWI>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts); break;
     default:
       if constexpr (!SWI) {
-        if (p.kind == PQ_PRO_SILU) launch_q8r_fused<PQ_PRO_SILU, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
+        if (p.kind == PQ_PRO_EMBED) launch_q8r_fused<kProEmbedR, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
+        else if (p.kind == PQ_PRO_SILU) launch_q8r_fused<PQ_PRO_SILU, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
         else if (p.ntaps == 7) launch_q8r_fused<kProConv7, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
         else launch_q8r_fused<PQ_PRO_CONV, false>(K, ntiles, lds, st, codes, scales, p, y, yb, N, parts);
       }

@@ -703,12 +703,12 @@ static int forward_decode(Engine &E, bool dev) {
 }
 
 // forward_r2's T=1 step through the fused reference-numerics kernels, the
-// same bits: the norm + residual pairs and the conv run as the prologues of
-// the GEMVs that read them, silu(gate) * up as the gate/up GEMV's epilogue,
-// and the LM head writes per-workgroup argmax pairs: per attention layer the
-// in GEMV, the attention mixer, o_proj, gate/up and down (five launches), per
-// conv layer four (the conv is the out GEMV's prologue), plus the embedding
-// row, the LM head and the argmax. The position and id slot as in
+// same bits: the embedding row, the norm + residual pairs and the conv run as
+// the prologues of the GEMVs that read them, silu(gate) * up as the gate/up
+// GEMV's epilogue, and the LM head writes per-workgroup argmax pairs: per
+// attention layer the in GEMV, the attention mixer, o_proj, gate/up and down
+// (five launches), per conv layer four (the conv is the out GEMV's
+// prologue), plus the LM head and the argmax. The position and id slot as in
 // forward_decode (dev: on the device, so the step can be captured and
 // replayed).
 static int forward_decode_r2(Engine &E, bool dev) {
@@ -735,14 +735,16 @@ static int forward_decode_r2(Engine &E, bool dev) {
     return pq_q8r_gemv(w.pc, w.sf, x, y, PQ_DTYPE_BF16, w.N, w.K, 1, E.st);
   };
   const float scale = 1.0f / sqrtf((float)c.hd);
-  // the token's embedding row (bf16); layer 0's in GEMV normalizes it
-  PQ_TRY(pq_embed_rows(E.emb.pc, E.emb.sf, E.tok, xa, H, c.vocab, 1, E.st));
   for (int l = 0; l < c.nlayers; l++) {
     LayerDev &D = E.L[l];
-    if (l == 0) {
+    if (l == 0) {   // the token's embedding row (written once to xa), normalized
       p = pq_gemv_prologue{};
-      p.kind = PQ_PRO_NORM;
-      p.x_in = xa;
+      p.kind = PQ_PRO_EMBED;
+      p.tok = E.tok;
+      p.emb_pc = E.emb.pc;
+      p.emb_sf = E.emb.sf;
+      p.vocab = c.vocab;
+      p.x_out = xa;
       p.w0 = D.op_norm;
       p.eps = c.eps;
     } else {

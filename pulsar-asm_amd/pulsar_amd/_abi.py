@@ -30,7 +30,7 @@ class GemvPrologue(C.Structure):
                 ("x_out", C.c_void_p), ("w0", C.c_void_p), ("w1", C.c_void_p), ("eps", C.c_float),
                 ("gu", C.c_void_p), ("bcx", C.c_void_p), ("ring_in", C.c_void_p), ("ring_out", C.c_void_p),
                 ("taps", C.c_void_p), ("ntaps", C.c_int), ("emb_pc", C.c_void_p), ("emb_ps", C.c_void_p),
-                ("tok", C.c_void_p), ("vocab", C.c_int), ("xf", C.c_void_p)]
+                ("tok", C.c_void_p), ("vocab", C.c_int), ("xf", C.c_void_p), ("emb_sf", C.c_void_p)]
 
 
 SIGNATURES = {

@@ -270,6 +270,8 @@ def _prologue(kind, eps, ptrs):
     for k, v in ptrs.items():
         if k == "emb":
             p.emb_pc, p.emb_ps = v.pcodes.data_ptr(), v.pscales.data_ptr()
+        elif k == "emb_rows":   # (codes int8 [vocab][K], fp32 scales [vocab][K/32]): the row-major table
+            p.emb_pc, p.emb_sf = v[0].data_ptr(), v[1].data_ptr()
         elif k in ("ntaps", "vocab"):
             setattr(p, k, int(v))
         else:

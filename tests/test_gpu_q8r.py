@@ -165,3 +165,33 @@ def test_q8r_gemv_fused_swiglu(pq, dev, kind, F, K):
     assert torch.equal(y.view(torch.int16), want.reshape(Fp)[:F].view(torch.int16))
     if kind == "resnorm":
         assert torch.equal(xo, x1.view(torch.int16))
+
+
+# The EMBED prologue on the row-major table (the R2 decode step's layer 0):
+# x_out = pq_embed_rows' row of *tok (zeros for an id outside the table) and the
+# GEMV of its RMSNorm, bit for bit against pq_embed_rows + pq_rmsnorm + pq_q8r_gemv.
+@pytest.mark.parametrize("K", [2048, 1024])
+def test_q8r_gemv_fused_embed(pq, dev, K):
+    import ctypes as C
+    g = torch.Generator(device=dev)
+    g.manual_seed(K + 5)
+    N, vocab = 3000, 1000
+    codes = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    scales = torch.rand((N, K // 32), device=dev, generator=g) * 0.02
+    ec = torch.randint(-127, 128, (vocab, K), dtype=torch.int8, device=dev, generator=g)
+    es = torch.rand((vocab, K // 32), device=dev, generator=g) * 0.05
+    w0 = torch.rand(K, device=dev, generator=g) + 0.5
+    for tok in (0, vocab - 1, 123, -1, vocab):
+        print(f"q8r fused embed K={K} tok={tok}", flush=True)
+        t = torch.tensor([tok], dtype=torch.int32, device=dev)
+        row = torch.empty(K, dtype=torch.int16, device=dev)
+        pq.check(pq.lib().pq_embed_rows(C.c_void_p(ec.data_ptr()), C.c_void_p(es.data_ptr()), C.c_void_p(t.data_ptr()),
+                                        C.c_void_p(row.data_ptr()), K, vocab, 1, C.c_void_p(pq.stream_ptr())),
+                 "pq_embed_rows")
+        xin, _, _ = pq.rmsnorm(row.view(torch.bfloat16).clone(), w0)
+        want = pq.q8r_gemv(codes, scales, xin)
+        xo = torch.full((K,), 0x7fff, dtype=torch.int16, device=dev)
+        y = pq.q8r_gemv_fused(codes, scales, pq.PRO_EMBED, tok=t, emb_rows=(ec, es), x_out=xo, w0=w0, vocab=vocab)
+        torch.cuda.synchronize()
+        assert torch.equal(xo, row), tok
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16)), tok
