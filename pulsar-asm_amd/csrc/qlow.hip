@@ -387,9 +387,14 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   // the split form (one workgroup per (8 rows, K slice), then the ordered
   // combine): for long rows on too few row slices to fill the chip, or when
   // a whole row's staging exceeds LDS
+  // PQ_QLOW_SPLIT=1 takes the split form whenever the workspace allows, 2 only
+  // when a whole row's staging exceeds LDS
+  static const int env_split = env_int("PQ_QLOW_SPLIT");
   const bool whole_fits = lds_of(K / kQ, KS) <= kMaxLds;
-  const bool split = ws != nullptr && ws_bytes >= pq_qlow_workspace_bytes(N, K, bits) &&
-                     ((N / RS < 128 && K >= 4096) || !whole_fits);
+  const bool want_split = env_split == 1   ? true
+                          : env_split == 2 ? !whole_fits
+                                           : (N / RS < 128 && K >= 4096) || !whole_fits;
+  const bool split = ws != nullptr && ws_bytes >= pq_qlow_workspace_bytes(N, K, bits) && want_split;
   PQ_REQUIRE(!split || aligned(ws, 4), PQ_ERR_ALIGN, "pq_qlow_gemv: workspace alignment");
   const int G = split ? K / kQ / KS : K / kQ, KSW = split ? 1 : KS;
   const size_t lds = lds_of(G, KSW);
