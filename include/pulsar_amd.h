@@ -137,8 +137,11 @@ int pq_q8_gemm_ws(const int8_t *pcodes, const uint16_t *pscales, const int8_t *q
  * needs more than the array (pq_q8_gemm_workspace_bytes > the array) are
  * refused with PQ_ERR_WORKSPACE. Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race
- * and must be serialized by the caller. The stream must belong to the
- * current device. Same bits as pq_q8_gemm_ws. */
+ * and must be serialized by the caller (one stream per GPU). The stream must
+ * belong to the current device. The first call on each device looks up the
+ * array's device address (hipGetSymbolAddress) and must be made outside
+ * stream capture (under capture it is refused with PQ_ERR_ARG); later calls
+ * may be captured into a graph. Same bits as pq_q8_gemm_ws. */
 size_t pq_q8_gemm_scratch_bytes(void);
 int pq_q8_gemm_noalloc(const int8_t *pcodes, const uint16_t *pscales, const int8_t *qx, const float *dx,
                        void *y, int y_dtype, int N, int K, int T, void *stream);

@@ -837,6 +837,14 @@ static int scratch_address(hipStream_t st, void **out) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    // the lookup is a runtime call that a stream capture must not record or
+    // refuse halfway: it is made on a call outside capture
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (st != nullptr && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(PQ_ERR_ARG,
+                  "pq_q8_gemm_noalloc: the first call on device %d is under stream capture; make one call "
+                  "outside capture first (it looks up the scratch array's address)",
+                  dev);
     void *p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)

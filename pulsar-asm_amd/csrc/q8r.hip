@@ -303,7 +303,8 @@ extern "C" int pq_q8r_gemv(const int8_t *codes, const float *scales, const uint1
   // 4, 4096 x 12288 13.5 / 12.6 / 15.9 us, 2048 x 4096 5.0 / 4.7 / 4.7 us
   static const int env_cw = env_int("PQ_Q8R_CW");
   const int nch = K / KC;
-  int cw = env_cw > 0 ? env_cw : (mc && nch <= kRMaxChunks && grid.x * T < 1024 ? 2 : 1);
+  const bool cw_ok = env_cw == 1 || env_cw == 2 || env_cw == 4;   // any other value: the default
+  int cw = cw_ok ? env_cw : (mc && nch <= kRMaxChunks && grid.x * T < 1024 ? 2 : 1);
   if (nch < 4) cw = std::min(cw, 2);   // no idle half-waves
   if (mc && nch <= kRMaxChunks && cw > 1) {
     const dim3 bk(kRThreads * cw);

@@ -111,6 +111,25 @@ def q8_gemm(w, qx, dx, out_dtype=DT_F32, out=None, split=True, ws=None):
     return out
 
 
+def q8_gemm_noalloc(w, qx, dx, out_dtype=DT_F32, out=None):
+    """q8_gemm through pq_q8_gemm_noalloc: the split-K partials go to the
+    library's own 16 MiB device array (one per GPU), so the call allocates
+    nothing when out is given. Every call on one GPU shares that array: calls
+    that could overlap on one GPU (two streams, two threads) race and must be
+    serialized by the caller -- use one stream per GPU. The first call on each
+    GPU looks up the array's address and must be made outside graph capture;
+    later calls may be captured."""
+    T = qx.shape[0]
+    if qx.shape[1] != w.K or dx.shape != (T, w.K // 32):
+        raise ValueError("x does not match K")
+    if out is None:
+        out = torch.empty((T, w.N), dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16,
+                          device=qx.device)
+    check(lib().pq_q8_gemm_noalloc(w.pcodes.data_ptr(), w.pscales.data_ptr(), qx.data_ptr(), dx.data_ptr(),
+                                   out.data_ptr(), out_dtype, w.N, w.K, T, stream_ptr()), "pq_q8_gemm_noalloc")
+    return out
+
+
 def q8r_gemv(codes, scales, x, out_dtype=DT_BF16, out=None):
     """The reference's own GEMV numerics (pq_q8r_gemv): codes int8 [N][K],
     fp32 scales [N][K/32], x bf16 [K] or [T][K] -> y [N] or [T][N]."""

@@ -106,6 +106,67 @@ def test_f32_prologue(orc, pq, dev, N, K):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32))
 
 
+@pytest.mark.parametrize("nt", [3, 7])
+def test_conv_prologue_closed_forms(orc, pq, dev, nt):
+    """The CONV prologue on the hand-built channels of tests/conv_cases.py (ascending
+    unfused tap sum, bx and cy rounded to bf16): the shifted ring it writes, and the
+    GEMV of its conv output, equal the closed forms."""
+    import conv_cases as cc
+    H = N = 2048
+    W, S, w = _w(orc, pq, dev, N, H, SEED + 35)
+    rb, taps, bcx, _ = cc.build(H, nt)
+    want_out, want_ring = cc.expected(H, nt)
+    rout = torch.zeros(nt * H, dtype=torch.int16, device=dev)
+    y = pq.gemv_fused(w, pq.PRO_CONV, bcx=_t16(bcx, dev), ring_in=_t16(rb.reshape(-1), dev), ring_out=rout,
+                      taps=torch.from_numpy(taps.reshape(-1)).to(dev), ntaps=nt)
+    assert np.array_equal(_u16(rout).reshape(nt, H), want_ring)
+    assert np.array_equal(_u16(y), _ref_gemv(orc, W, S, want_out))
+
+
+def test_f32_prologue_quant_ties(orc, pq, dev):
+    """The F32 prologue's quantizer (and pq_q8_quant) on blocks of exact halves
+    (tests/quant_cases.py): codes rounded half to even, as lrintf in the
+    reference's quant_row, then the GEMV over them."""
+    import quant_cases as qc
+    K, N = 2048, 2048
+    x = qc.tie_blocks(seed=31, reps=10)[:K]
+    qx_r, dx_r = orc.q8_quant(x)
+    assert np.array_equal(qx_r, qc.rne_codes(x))
+    qx, dx = pq.q8_quant(torch.from_numpy(x).to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(qx.cpu().numpy().reshape(-1), qx_r)
+    assert np.array_equal(dx.cpu().numpy().reshape(-1).view(np.uint32), dx_r.view(np.uint32))
+    W, S, w = _w(orc, pq, dev, N, K, SEED + 36)
+    y = pq.gemv_fused(w, pq.PRO_F32, out_dtype=pq.DT_F32, xf=torch.from_numpy(x).to(dev))
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), orc.q8_gemv(W, S, qx_r, dx_r).view(np.uint32))
+
+
+def _bench_shapes():
+    import bench
+    return bench.SHAPES
+
+
+@pytest.mark.parametrize("name,N,K,o", _bench_shapes(), ids=[s[0] for s in _bench_shapes()])
+def test_f32_prologue_bench_step(orc, pq, dev, name, N, K, o):
+    """The launch bench.py times, in the form it times it: q8_gemv_fused_kernel with
+    the F32 prologue on each GEMV of its step, with the output dtype it writes
+    (bf16 for the layer GEMVs, fp32 logits for the LM head), twice in a row into
+    the same output, against the oracle's R1 GEMV."""
+    W, S, w = _w(orc, pq, dev, N, K, SEED + 170 + N + K)
+    dt = pq.DT_F32 if o == "f32" else pq.DT_BF16
+    out = torch.empty(N, dtype=torch.float32 if o == "f32" else torch.bfloat16, device=dev)
+    for rep in range(2):
+        x = orc.gen_normal(SEED + 171 + rep + K, K)
+        qx, dx = orc.q8_quant(x)
+        yr = orc.q8_gemv(W, S, qx, dx)
+        y = pq.gemv_fused(w, pq.PRO_F32, out_dtype=dt, out=out, xf=torch.from_numpy(x).to(dev))
+        torch.cuda.synchronize()
+        if o == "f32":
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32)), (name, rep)
+        else:
+            assert np.array_equal(_u16(y), orc.f2bf(yr)), (name, rep)
+
+
 def test_q8_prologue(orc, pq, dev):
     N, K = 2048, 2048
     W, S, w = _w(orc, pq, dev, N, K, SEED + 40)

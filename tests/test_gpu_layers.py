@@ -173,3 +173,20 @@ def test_expf_on_device_matches_host(orc, pq, dev):
     gu = np.concatenate([a, b])[None, :]
     y, _, _ = pq.silu_mul(_t16(gu, dev), 8192, 1)
     assert np.array_equal(_u16(y)[0], orc.silu_mul(a, b))
+
+
+@pytest.mark.parametrize("nt", [3, 7])
+def test_conv_closed_forms(orc, pq, dev, nt):
+    """The conv kernel on the hand-built channels of tests/conv_cases.py: the
+    ascending unfused tap sum, bx = bf16(B*x) and cy = bf16(acc) before C, each
+    of which a departure would change (the oracle's closed-form test shows which)."""
+    import conv_cases as cc
+    H = 256
+    rb, taps, bcx, _ = cc.build(H, nt)
+    want_out, want_ring = cc.expected(H, nt)
+    rd = _t16(rb.reshape(-1), dev)
+    out = torch.empty((1, H), dtype=torch.int16, device=dev)
+    pq.conv(rd, torch.from_numpy(taps.reshape(-1)).to(dev), _t16(bcx, dev), out, H, 1, nt)
+    torch.cuda.synchronize()
+    assert np.array_equal(_u16(out)[0], want_out)
+    assert np.array_equal(_u16(rd).reshape(nt, H), want_ring)

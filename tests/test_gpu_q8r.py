@@ -170,7 +170,7 @@ def test_q8r_gemv_fused_swiglu(pq, dev, kind, F, K):
 # The EMBED prologue on the row-major table (the R2 decode step's layer 0):
 # x_out = pq_embed_rows' row of *tok (zeros for an id outside the table) and the
 # GEMV of its RMSNorm, bit for bit against pq_embed_rows + pq_rmsnorm + pq_q8r_gemv.
-@pytest.mark.parametrize("K", [2048, 1024])
+@pytest.mark.parametrize("K", [2048, 1024, 4096, 8192])
 def test_q8r_gemv_fused_embed(pq, dev, K):
     import ctypes as C
     g = torch.Generator(device=dev)

@@ -376,6 +376,57 @@ def test_conv_impulse_response(orc):
     assert not outs[nt].any()
 
 
+@pytest.mark.parametrize("nt", [3, 7])
+def test_conv_step_closed_forms(orc, nt):
+    """orc_conv_step follows k_conv7 / k_conv_chunk (lfm3_nanode.cu:901-941): the
+    taps summed in ascending order with each product rounded before its add,
+    bx = bf16(B*x) shifted in as the newest slot, cy = bf16(acc) before C
+    multiplies it. Channels built by hand (tests/conv_cases.py) separate each of
+    a descending sum, an fma chain, an unrounded B*x and an unrounded cy from the
+    reference's order: each departure changes its own channels' outputs."""
+    import conv_cases as cc
+    H = 64
+    rb, taps, bcx, kinds = cc.build(H, nt)
+    want_out, want_ring = cc.expected(H, nt)
+    dep = cc.departures(H, nt)
+    assert np.array_equal(dep["reference"], want_out)
+    for name, kind in (("descending", cc.ORDER), ("fused", cc.FUSED), ("bx unrounded", cc.BX),
+                       ("cy unrounded", cc.CY)):
+        differs = dep[name] != want_out
+        assert differs[kinds == kind].all() and not differs[kinds != kind].any(), name
+    out, ring = orc.conv_step(rb.reshape(-1), taps.reshape(-1), bcx, H, nt)
+    assert np.array_equal(out, want_out)
+    assert np.array_equal(ring.reshape(nt, H), want_ring)
+
+
+def test_q8_quant_ties_are_reference_code(orc):
+    """Where amax/127 is an fp16 value, the reference's quant_row
+    (q8_gemv_cpu.c:63-81: sc16 = (float)(_Float16)(amax/127), q = lrintf(x/sc16),
+    clamp +-127) and orc_q8_quant (d = amax/127 in fp32, q = rne(x/d)) divide by
+    the same d, so their codes must agree bit for bit. Blocks with amax = 127*m*2^k
+    (m an fp16 significand) full of exact halves n*d + d/2 pin the ties to even:
+    ties away from zero or truncation fail them."""
+    import ctypes as C
+    import quant_cases as qc
+    ref = orc.ref()
+    x = qc.tie_blocks()
+    q, dx = orc.q8_quant(x)
+    xb = x.reshape(-1, 32).astype(np.float64)
+    dd = np.repeat(dx.astype(np.float64), 32).reshape(-1, 32)
+    assert (xb / dd * 2 % 2 == 1).sum() >= 4 * len(qc.SCALES)     # the ties are really there
+    want = qc.rne_codes(x)
+    assert np.array_equal(q, want)
+    assert (qc.away_codes(x) != want).any()
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    qr = np.empty(x.size, np.int8)
+    sr = np.empty(x.size // 32, np.float32)
+    ref.ref_q8_quant(x.ctypes.data_as(C.c_void_p), C.c_int(x.size), qr.ctypes.data_as(C.c_void_p),
+                     sr.ctypes.data_as(C.c_void_p))
+    assert np.array_equal(f32bits(sr), f32bits(dx))
+    assert np.array_equal(qr, q)
+
+
 def test_silu_and_gate(orc):
     rng = np.random.default_rng(23)
     a = orc.f2bf(rng.standard_normal(4096).astype(np.float32) * 8)

@@ -74,3 +74,38 @@ def test_noalloc_refuses_what_does_not_fit(orc, pq, dev):
     rc = L.pq_q8_gemm_noalloc(p, p, p, p, p, pq.DT_F32, N, K, T, None)
     assert rc == PQ_ERR_WORKSPACE
     assert b"scratch" in L.pq_last_error()
+
+
+def test_noalloc_under_graph_capture(orc, pq, dev):
+    """Calls captured into a HIP graph after one eager call on the device (which
+    looks up the scratch array's address): two split shapes back to back in one
+    graph, replayed three times with eager work between the replays, each replay
+    bit-equal to pq_q8_gemm_ws."""
+    L = pq.lib()
+    cases = [(2048, 8192, 32, 31), (2048, 4096, 8, 32)]
+    data = [_case(orc, pq, dev, N, K, T, seed) for (N, K, T, seed) in cases]
+    refs = [_with_ws(pq, w, qx, dx, N, K, T)[1] for (w, qx, dx), (N, K, T, _) in zip(data, cases)]
+    rc, _ = _noalloc(pq, *data[0], *cases[0][:3])   # outside capture: resolves the address
+    assert rc == 0, L.pq_last_error()
+    ys = [torch.full((T, N), float("nan"), dtype=torch.float32, device=dev) for (N, K, T, _) in cases]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(g):
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for (w, qx, dx), (N, K, T, _), y in zip(data, cases, ys):
+            rcs.append(L.pq_q8_gemm_noalloc(_ptr(w.pcodes), _ptr(w.pscales), _ptr(qx), _ptr(dx), _ptr(y), pq.DT_F32,
+                                            N, K, T, stream))
+    assert rcs == [0, 0], L.pq_last_error()
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        for y in ys:
+            y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for y, r in zip(ys, refs):
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), r.cpu().numpy().view(np.uint32)), rep
+        # eager work between replays, on the same scratch array
+        rc, _ = _noalloc(pq, *data[1], *cases[1][:3])
+        assert rc == 0, L.pq_last_error()
+        torch.cuda.synchronize()
