@@ -447,6 +447,34 @@ void orc_qlow_gemv(const uint8_t *Q, const uint16_t *S, const uint16_t *x, float
   free(sx);
 }
 
+/* The bf16-table LM head (k_gemv_bf16, lfm3_nanode.cu:3504-3534, as
+ * lm_head_bf16 launches it, 3536-3573): W bf16 [N][K], x bf16 [K] widened to
+ * fp32. Per row, leaf L = 0..31 sums k = L, L+32, L+64, ... ascending from 0,
+ * each product rounded before its add (__fmul_rn, __fadd_rn); the 32 leaves
+ * then combine as the shfl_down tree 16, 8, 4, 2, 1 (leaf i += leaf i+o for
+ * i < o). y fp32. */
+void orc_bf16_gemv(const uint16_t *W, const uint16_t *x, float *y, int N, int K) {
+  float *xf = (float *)malloc(sizeof(float) * (size_t)K);
+  for (int i = 0; i < K; i++) xf[i] = orc_bf2f(x[i]);
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < N; r++) {
+    const uint16_t *wr = W + (size_t)r * K;
+    float leaf[32];
+    for (int L = 0; L < 32; L++) {
+      float s = 0.0f;
+      for (int k = L; k < K; k += 32) {
+        const float p = orc_bf2f(wr[k]) * xf[k];
+        s = s + p;
+      }
+      leaf[L] = s;
+    }
+    for (int o = 16; o > 0; o >>= 1)
+      for (int i = 0; i < o; i++) leaf[i] = leaf[i] + leaf[i + o];
+    y[r] = leaf[0];
+  }
+  free(xf);
+}
+
 /* Exact value of the quantized product, sum_b (S_b*dx_b as real) * isum_b, in
  * double (every term is exact in double: S_b and dx_b have 11 and 24 bit
  * mantissas, isum_b < 2^20; the sum rounds at most nb times at 2^-53). */

@@ -64,6 +64,7 @@ void orc_q8_gemv_a11(const int8_t *W, const float *S, const float *x, float *y, 
 void orc_q8r_gemm(const int8_t *W, const float *S, const uint16_t *x, float *y, int N, int K, int T);
 /* Q4/Q5 low-bit GEMV in the reference's order; Q [N][K] one code per byte, S [N][K/32][2] fp16 (d', mn) */
 void orc_qlow_gemv(const uint8_t *Q, const uint16_t *S, const uint16_t *x, float *y, int N, int K);
+void orc_bf16_gemv(const uint16_t *W, const uint16_t *x, float *y, int N, int K);
 void orc_q8_gemv_exact(const int8_t *W, const uint16_t *S, const int8_t *qx, const float *dx,
                        double *y, int N, int K);
 void orc_tq2_gemv(const uint8_t *codes, const uint16_t *S, const uint8_t *xq, float *y,
@@ -105,6 +106,11 @@ typedef struct orc_cfg {
   int slide_win;             /* keys a sliding layer sees (the last slide_win)  */
   int slide_rot;             /* rotated dims of a sliding layer                */
   float slide_theta;         /* RoPE base of a sliding layer                   */
+  int emb_bf16;              /* 1: the tied table is bf16 (the exporter's --emb-bf16):
+                                embedding rows copied, LM head orc_bf16_gemv   */
+  int lowbit;                /* 0, 4 or 5: the bits of the low-bit tensors      */
+  uint32_t lowbit_mask;      /* bit L set -> layer L's linears are low-bit (all
+                                but the attention gate_proj); needs numerics 1 */
 } orc_cfg;
 
 typedef struct orc_model orc_model;
@@ -123,6 +129,14 @@ void orc_model_greedy(orc_model *m, const int32_t *prompt, int n_prompt, int n_s
 int orc_model_tensor(orc_model *m, int layer, int slot, const void **p0, const void **p1,
                      int *N, int *K);
 int orc_model_debug_hidden(orc_model *m, uint16_t *out);   /* residual of last position */
+/* The source tensors of a slot (0 mixer in, 1 mixer out, 2 gate/up, 3 down) as
+ * the .lfm3q8 file lists them: up to 4 (row offset, rows, bits: 8 = Q8, 4 / 5 =
+ * low-bit). Returns their count, or -1. */
+int orc_model_parts(orc_model *m, int layer, int slot, int *r0, int *n, int *bits);
+/* A slot's low-bit codes (uint8 [N][K], one per byte) and scales ([N][K/32][2]
+ * fp16: d' = 128 d, mn), for every row (the low-bit parts' rows are the ones
+ * used); -1 if the slot has no low-bit part. */
+int orc_model_lowbit(orc_model *m, int layer, int slot, const uint8_t **q, const uint16_t **s, int *N, int *K);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,11 @@ typedef struct {
   uint16_t *s;   /* fp16 scales (the R1 GEMV)                          */
   float *sf;     /* the same scales widened to fp32 (the R2 GEMV)      */
   int N, K;
+  /* the slot's source tensors (row offset, rows, bits: 8 = Q8, 4 / 5 =
+   * low-bit) and, when one is low-bit, its codes / scales for every row */
+  int np, pr0[4], pn[4], pbits[4];
+  uint8_t *lq;     /* [N][K], one code per byte                          */
+  uint16_t *ls;    /* [N][K/32][2] fp16: d' = 128 d, mn                  */
 } q8t;
 
 typedef struct {
@@ -52,6 +57,7 @@ struct orc_model {
   orc_cfg c;
   layer_t *L;
   q8t emb;
+  uint16_t *emb16;   /* emb_bf16: the tied table as bf16 [vocab][H] */
   float *final_norm;
   float *rope, *rope_slide;   /* cos/sin tables: full-attention and sliding layers */
   int pos;
@@ -70,6 +76,45 @@ static void q8_make(q8t *q, const orc_cfg *c, int t, int N, int K) {
   for (size_t i = 0; i < (size_t)N * (K / ORC_QBLK); i++) q->sf[i] = orc_h2f(q->s[i]);
 }
 
+/* The slot's source tensors (the .lfm3q8 names, in row order): nsrc of them
+ * with the given row counts. A source is low-bit (cfg.lowbit bits) when its
+ * layer is in lowbit_mask, its rows are a multiple of 32 and K of 256 (the
+ * exporter's dtype 6 / 7 rule, lfm3_nanode.cu:1494-1496) and it is not the
+ * attention gate_proj (skip: its index, or -1), which stays Q8 as in the real
+ * LFM3 shapes (16 rows). The low-bit parameters of tensor t come from their
+ * own streams (t + 5000): codes uniform in [0, 2^B), d' = f16(|z| * 2560 / 2^B)
+ * (so w = d q + mn spreads like the Q8 weights), mn = f16(-(2^B - 1)/2 * d'/128
+ * + 0.02 z), centring w. */
+static void parts_make(q8t *q, const orc_cfg *c, int t, int layer, const int *rows, int nsrc, int skip) {
+  const int low = c->lowbit && ((c->lowbit_mask >> layer) & 1u);
+  int r0 = 0, any = 0;
+  q->np = nsrc;
+  for (int i = 0; i < nsrc; i++) {
+    q->pr0[i] = r0;
+    q->pn[i] = rows[i];
+    q->pbits[i] = (low && i != skip && rows[i] % 32 == 0 && q->K % 256 == 0) ? c->lowbit : 8;
+    any |= q->pbits[i] != 8;
+    r0 += rows[i];
+  }
+  if (!any) return;
+  const int B = c->lowbit, G = q->K / ORC_QBLK;
+  const size_t n = (size_t)q->N * q->K, ng = (size_t)q->N * G;
+  q->lq = (uint8_t *)malloc(n);
+  q->ls = (uint16_t *)malloc(ng * 4);
+  const uint64_t sq = tseed(c, 5000 + t, 0), sd = tseed(c, 5000 + t, 1), sm = tseed(c, 5000 + t, 2);
+  for (size_t i = 0; i < n; i++) q->lq[i] = (uint8_t)(orc_sm64_at(sq, i) >> (64 - B));
+  uint16_t *dp = (uint16_t *)malloc(ng * 2);
+  float *z = (float *)malloc(sizeof(float) * ng);
+  orc_gen_scales(sd, dp, ng, 2560.0f / (float)(1 << B));
+  orc_gen_normal(sm, z, ng);
+  for (size_t g = 0; g < ng; g++) {
+    q->ls[2 * g] = dp[g];
+    q->ls[2 * g + 1] = orc_f2h(-(float)((1 << B) - 1) * 0.5f * orc_h2f(dp[g]) / 128.0f + 0.02f * z[g]);
+  }
+  free(dp);
+  free(z);
+}
+
 static float *vec_make(const orc_cfg *c, int t, int n, float a, float b) {
   float *v = (float *)malloc(sizeof(float) * (size_t)n);
   orc_gen_affine(tseed(c, t, 2), v, (size_t)n, a, b);
@@ -77,6 +122,10 @@ static float *vec_make(const orc_cfg *c, int t, int n, float a, float b) {
 }
 
 orc_model *orc_model_create(const orc_cfg *cfg) {
+  /* the bf16 table and low-bit tensors take bf16 activations: the reference's
+   * own GEMV numerics (numerics 1) */
+  if ((cfg->emb_bf16 || cfg->lowbit) && cfg->numerics != 1) return NULL;
+  if (cfg->lowbit != 0 && cfg->lowbit != 4 && cfg->lowbit != 5) return NULL;
   orc_model *m = (orc_model *)calloc(1, sizeof(orc_model));
   m->c = *cfg;
   const orc_cfg *c = &m->c;
@@ -88,26 +137,39 @@ orc_model *orc_model_create(const orc_cfg *cfg) {
     L->attn = (int)((c->attn_mask >> l) & 1u);
     L->slide = L->attn && ((c->slide_mask >> l) & 1u);
     if (L->attn) {
+      const int rin[4] = {qd, kvd, kvd, c->nh};
       q8_make(&L->in, c, t0 + 0, qd + 2 * kvd + c->nh, H);
+      parts_make(&L->in, c, t0 + 0, l, rin, 4, 3);
       q8_make(&L->out, c, t0 + 1, H, qd);
+      parts_make(&L->out, c, t0 + 1, l, &H, 1, -1);
       L->q_norm = vec_make(c, t0 + 8, c->hd, 1.0f, 0.1f);
       L->k_norm = vec_make(c, t0 + 9, c->hd, 1.0f, 0.1f);
       L->kc = (uint16_t *)calloc((size_t)c->ctx * kvd, 2);
       L->vc = (uint16_t *)calloc((size_t)c->ctx * kvd, 2);
     } else {
+      const int rin = 3 * H;
       q8_make(&L->in, c, t0 + 0, 3 * H, H);
+      parts_make(&L->in, c, t0 + 0, l, &rin, 1, -1);
       q8_make(&L->out, c, t0 + 1, H, H);
+      parts_make(&L->out, c, t0 + 1, l, &H, 1, -1);
       L->taps = vec_make(c, t0 + 10, H * c->ntaps, 0.0f, 0.5f);
       L->ring = (uint16_t *)calloc((size_t)c->ntaps * H, 2);
     }
+    const int rug[2] = {F, F};
     q8_make(&L->ug, c, t0 + 2, 2 * F, H);
+    parts_make(&L->ug, c, t0 + 2, l, rug, 2, -1);
     q8_make(&L->down, c, t0 + 3, H, F);
+    parts_make(&L->down, c, t0 + 3, l, &H, 1, -1);
     L->op_norm = vec_make(c, t0 + 4, H, 1.0f, 0.1f);
     L->post_op_norm = vec_make(c, t0 + 5, H, 4.0f, 0.4f);
     L->ffn_norm = vec_make(c, t0 + 6, H, 1.0f, 0.1f);
     L->post_ffn_norm = vec_make(c, t0 + 7, H, 4.0f, 0.4f);
   }
   q8_make(&m->emb, c, 4000, c->vocab, H);
+  if (c->emb_bf16) {   /* the bf16 table: each row is the Q8 table's embedding row */
+    m->emb16 = (uint16_t *)malloc((size_t)c->vocab * H * 2);
+    for (int v = 0; v < c->vocab; v++) orc_embed_row(m->emb.w, m->emb.s, v, H, m->emb16 + (size_t)v * H);
+  }
   m->final_norm = vec_make(c, 4001, H, 1.0f, 0.1f);
   m->rope = (float *)malloc(sizeof(float) * (size_t)c->ctx * (c->rot / 2) * 2 + 8);
   orc_rope_table(m->rope, c->ctx, c->hd, c->rot, c->theta);
@@ -134,7 +196,7 @@ void orc_model_reset(orc_model *m) {
   m->pos = 0;
 }
 
-static void q8_free(q8t *q) { free(q->w); free(q->s); free(q->sf); }
+static void q8_free(q8t *q) { free(q->w); free(q->s); free(q->sf); free(q->lq); free(q->ls); }
 
 void orc_model_free(orc_model *m) {
   if (!m) return;
@@ -146,6 +208,7 @@ void orc_model_free(orc_model *m) {
   }
   free(m->L);
   q8_free(&m->emb);
+  free(m->emb16);
   free(m->final_norm); free(m->rope); free(m->rope_slide); free(m->last_hidden);
   free(m);
 }
@@ -156,6 +219,7 @@ int orc_model_tensor(orc_model *m, int layer, int slot, const void **p0, const v
     if (slot == 0) { *p0 = m->emb.w; *p1 = m->emb.s; *N = m->emb.N; *K = m->emb.K; return 0; }
     if (slot == 1) { *p0 = m->final_norm; *p1 = NULL; *N = 1; *K = m->c.hidden; return 0; }
     if (slot == 2) { *p0 = m->rope; *p1 = NULL; *N = m->c.ctx; *K = m->c.rot; return 0; }
+    if (slot == 3 && m->emb16) { *p0 = m->emb16; *p1 = NULL; *N = m->c.vocab; *K = m->c.hidden; return 0; }
     return -1;
   }
   if (layer < 0 || layer >= m->c.nlayers) return -1;
@@ -183,6 +247,32 @@ int orc_model_tensor(orc_model *m, int layer, int slot, const void **p0, const v
   return 0;
 }
 
+static q8t *slot_q8(orc_model *m, int layer, int slot) {
+  if (layer < 0 || layer >= m->c.nlayers) return NULL;
+  layer_t *L = &m->L[layer];
+  switch (slot) {
+    case 0: return &L->in;
+    case 1: return &L->out;
+    case 2: return &L->ug;
+    case 3: return &L->down;
+    default: return NULL;
+  }
+}
+
+int orc_model_parts(orc_model *m, int layer, int slot, int *r0, int *n, int *bits) {
+  const q8t *q = slot_q8(m, layer, slot);
+  if (!q) return -1;
+  for (int i = 0; i < q->np; i++) { r0[i] = q->pr0[i]; n[i] = q->pn[i]; bits[i] = q->pbits[i]; }
+  return q->np;
+}
+
+int orc_model_lowbit(orc_model *m, int layer, int slot, const uint8_t **qq, const uint16_t **ss, int *N, int *K) {
+  const q8t *q = slot_q8(m, layer, slot);
+  if (!q || !q->lq) return -1;
+  *qq = q->lq; *ss = q->ls; *N = q->N; *K = q->K;
+  return 0;
+}
+
 int orc_model_debug_hidden(orc_model *m, uint16_t *out) {
   memcpy(out, m->last_hidden, (size_t)m->c.hidden * 2);
   return 0;
@@ -194,6 +284,25 @@ int orc_model_debug_hidden(orc_model *m, uint16_t *out) {
 static int g_numerics;   /* set per feed from the model's configuration */
 static void gemm_f32(const q8t *W, const uint16_t *x, float *y, int T, int8_t *qx, float *dx) {
   const int K = W->K, N = W->N, nb = K / ORC_QBLK;
+  if (g_numerics == 1 && W->lq) {
+    /* per source tensor (gemv per name, layer_body 3739-3856): a Q8 part in
+     * the R2 order, a low-bit part one position at a time (pf_gemv_T,
+     * lfm3_nanode.cu:4846-4848) in the Q4 / Q5 order */
+    float *tmp = (float *)malloc(sizeof(float) * (size_t)T * N);
+    for (int i = 0; i < W->np; i++) {
+      const int r0 = W->pr0[i], n = W->pn[i];
+      if (W->pbits[i] == 8) {
+        orc_q8r_gemm(W->w + (size_t)r0 * K, W->sf + (size_t)r0 * nb, x, tmp, n, K, T);
+      } else {
+        for (int t = 0; t < T; t++)
+          orc_qlow_gemv(W->lq + (size_t)r0 * K, W->ls + (size_t)r0 * nb * 2, x + (size_t)t * K, tmp + (size_t)t * n,
+                        n, K);
+      }
+      for (int t = 0; t < T; t++) memcpy(y + (size_t)t * N + r0, tmp + (size_t)t * n, sizeof(float) * (size_t)n);
+    }
+    free(tmp);
+    return;
+  }
   if (g_numerics == 1) {
     orc_q8r_gemm(W->w, W->sf, x, y, N, K, T);
     return;
@@ -228,7 +337,14 @@ int orc_model_feed(orc_model *m, const int32_t *tok, int T, float *logits_out) {
   int8_t *qx = (int8_t *)malloc((size_t)T * kmax);
   float *dx = (float *)malloc(sizeof(float) * (size_t)T * (kmax / ORC_QBLK));
 
-  for (int t = 0; t < T; t++) orc_embed_row(m->emb.w, m->emb.s, tok[t], H, X + (size_t)t * H);
+  for (int t = 0; t < T; t++) {
+    if (m->emb16) {   /* the bf16 row as stored (lfm3_nanode.cu:6062-6076); an id off the table: zeros */
+      if (tok[t] >= 0 && tok[t] < c->vocab) memcpy(X + (size_t)t * H, m->emb16 + (size_t)tok[t] * H, (size_t)H * 2);
+      else memset(X + (size_t)t * H, 0, (size_t)H * 2);
+    } else {
+      orc_embed_row(m->emb.w, m->emb.s, tok[t], H, X + (size_t)t * H);
+    }
+  }
 
   for (int l = 0; l < c->nlayers; l++) {
     layer_t *L = &m->L[l];
@@ -281,7 +397,8 @@ int orc_model_feed(orc_model *m, const int32_t *tok, int T, float *logits_out) {
   const uint16_t *xl = X + (size_t)(T - 1) * H;
   memcpy(m->last_hidden, xl, (size_t)H * 2);
   orc_rmsnorm(xl, m->final_norm, H1, H, c->eps);
-  gemm_f32(&m->emb, H1, yf, 1, qx, dx);
+  if (m->emb16) orc_bf16_gemv(m->emb16, H1, yf, c->vocab, H);   /* lm_head_bf16 (3536-3573) */
+  else gemm_f32(&m->emb, H1, yf, 1, qx, dx);
   const int id = orc_argmax(yf, c->vocab);
   if (logits_out) memcpy(logits_out, yf, sizeof(float) * (size_t)c->vocab);
   m->pos += T;

@@ -195,6 +195,16 @@ def qlow_gemv(Q, S, xb):
     return y
 
 
+def bf16_gemv(W, xb):
+    """The bf16-table LM head (k_gemv_bf16 order): W bf16 bits [N][K], x bf16
+    bits [K] -> y fp32 [N]."""
+    N, K = W.shape
+    y = np.empty(N, np.float32)
+    lib().orc_bf16_gemv(_p(np.ascontiguousarray(W, np.uint16)), _p(np.ascontiguousarray(xb, np.uint16)), _p(y),
+                        C.c_int(N), C.c_int(K))
+    return y
+
+
 def q8_gemv_exact(W, S, qx, dx):
     N, K = W.shape
     y = np.empty(N, np.float64)
@@ -333,7 +343,8 @@ class Cfg(C.Structure):
                 ("ntaps", C.c_int), ("ctx", C.c_int), ("eps", C.c_float), ("theta", C.c_float),
                 ("seed", C.c_uint64), ("attn_mask", C.c_uint32), ("numerics", C.c_int),
                 ("slide_mask", C.c_uint32), ("slide_win", C.c_int), ("slide_rot", C.c_int),
-                ("slide_theta", C.c_float)]
+                ("slide_theta", C.c_float), ("emb_bf16", C.c_int), ("lowbit", C.c_int),
+                ("lowbit_mask", C.c_uint32)]
 
 
 class Model:
@@ -343,6 +354,8 @@ class Model:
         self.cfg = dict(cfg)
         self._c = Cfg(**cfg)
         self._h = lib().orc_model_create(C.byref(self._c))
+        if not self._h:
+            raise ValueError("orc_model_create refused the configuration")
 
     def close(self):
         if self._h:
@@ -371,6 +384,25 @@ class Model:
                                C.c_int(n_steps), _p(ids))
         return ids
 
+    def parts(self, layer, slot):
+        """The slot's source tensors: [(row offset, rows, bits)], bits 8 = Q8, 4 / 5 = low-bit."""
+        r0, n, b = (C.c_int * 4)(), (C.c_int * 4)(), (C.c_int * 4)()
+        k = lib().orc_model_parts(C.c_void_p(self._h), C.c_int(layer), C.c_int(slot), r0, n, b)
+        if k < 0:
+            raise KeyError((layer, slot))
+        return [(r0[i], n[i], b[i]) for i in range(k)]
+
+    def lowbit(self, layer, slot):
+        """The slot's low-bit codes uint8 [N][K] and scales fp16 bits [N][K/32][2], or None."""
+        q, sc = C.c_void_p(), C.c_void_p()
+        n, k = C.c_int(), C.c_int()
+        if lib().orc_model_lowbit(C.c_void_p(self._h), C.c_int(layer), C.c_int(slot), C.byref(q), C.byref(sc),
+                                  C.byref(n), C.byref(k)) != 0:
+            return None
+        N, K = n.value, k.value
+        return (np.ctypeslib.as_array(C.cast(q, C.POINTER(C.c_uint8)), shape=(N, K)),
+                np.ctypeslib.as_array(C.cast(sc, C.POINTER(C.c_uint16)), shape=(N, K // QBLK, 2)))
+
     def hidden(self):
         out = np.empty(self.cfg["hidden"], np.uint16)
         lib().orc_model_debug_hidden(C.c_void_p(self._h), _p(out))
@@ -390,4 +422,6 @@ class Model:
             return w, s
         if layer == -1 and slot == 2:
             return np.ctypeslib.as_array(C.cast(p0, C.POINTER(C.c_float)), shape=(N * (K // 2) * 2,))
+        if layer == -1 and slot == 3:   # the bf16 table
+            return np.ctypeslib.as_array(C.cast(p0, C.POINTER(C.c_uint16)), shape=(N, K))
         return np.ctypeslib.as_array(C.cast(p0, C.POINTER(C.c_float)), shape=(K,))

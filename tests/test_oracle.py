@@ -850,3 +850,154 @@ def test_qlow_vs_exact(orc, bits, N, K):
     den = (np.abs(dp) * ((1 + q / 128) * np.abs(x)).sum(-1) + np.abs(m) * np.abs(x).sum(-1)).sum(-1)
     y = orc.qlow_gemv(Q, S, xb).astype(np.float64)
     assert (np.abs(y - exact) / den).max() <= 1e-5
+
+
+# ------------------------------------------- the bf16-table LM head (k_gemv_bf16)
+def _bf16_head_case(K, vals):
+    """One row of ones and x = vals at the given element indices (exact in bf16)."""
+    W = np.full((1, K), 0x3F80, np.uint16)
+    x = np.zeros(K, np.float32)
+    for k, v in vals.items():
+        x[k] = v
+    return W, _bf16(x)
+
+
+def test_bf16_head_leaves_stride_32(orc):
+    """orc_bf16_gemv follows k_gemv_bf16 (lfm3_nanode.cu:3517-3534): leaf L sums
+    elements L, L+32, L+64, ... in order, rounding each add; the leaves combine as
+    the shfl_down tree 16, 8, 4, 2, 1. Closed forms by hand (2^24 + 1 ties to 2^24):
+      A: x[0] = x[32] = 1, x[1] = 2^24 -- leaf 0 = 2, leaf 1 = 2^24, tree 2^24 + 2;
+         a sequential sum over k, or lanes holding contiguous pairs, give 2^24;
+      B: x[0] = 2^24, x[32] = x[64] = 1 -- leaf 0 in order: 2^24; a pairwise
+         leaf (x0 + (x32 + x64)) gives 2^24 + 2;
+      C: x[0] = x[16] = 1, x[1] = 2^24 -- the tree adds leaves 0 and 16 first
+         (2), then leaf 1: 2^24 + 2; a sequential fold over the leaves gives 2^24."""
+    big = float(2 ** 24)
+
+    def sequential(x):   # one fp32 chain over k, the departure cases A and C rule out
+        s = np.float32(0)
+        for v in orc.bf2f(x):
+            s = np.float32(s + v)
+        return s
+
+    W, x = _bf16_head_case(64, {0: 1.0, 32: 1.0, 1: big})
+    assert orc.bf16_gemv(W, x)[0] == np.float32(big + 2) and sequential(x) == np.float32(big)
+    W, x = _bf16_head_case(96, {0: big, 32: 1.0, 64: 1.0})
+    assert orc.bf16_gemv(W, x)[0] == np.float32(big)
+    W, x = _bf16_head_case(64, {0: 1.0, 16: 1.0, 1: big})
+    assert orc.bf16_gemv(W, x)[0] == np.float32(big + 2) and sequential(x) == np.float32(big)
+
+
+def test_bf16_head_vs_exact(orc):
+    """Random bf16 rows and x: within 1e-6 of sum |w x| of the exact double sum
+    (the products are exact in fp32, only the adds round); rows are independent."""
+    rng = np.random.default_rng(71)
+    N, K = 37, 2048
+    W = orc.f2bf(rng.standard_normal(N * K).astype(np.float32)).reshape(N, K)
+    x = orc.f2bf(rng.standard_normal(K).astype(np.float32) * 3)
+    y = orc.bf16_gemv(W, x).astype(np.float64)
+    t = orc.bf2f(W).astype(np.float64) * orc.bf2f(x).astype(np.float64)
+    assert (np.abs(y - t.sum(1)) / np.abs(t).sum(1)).max() <= 1e-6
+    assert np.array_equal(f32bits(orc.bf16_gemv(W[5:9], x)), f32bits(orc.bf16_gemv(W, x)[5:9]))
+
+
+# ------------------------------- the low-bit backbone and the bf16 table (numerics 1)
+LOWQ = dict(TINY, numerics=1, lowbit=4, lowbit_mask=0b0110, emb_bf16=1)
+
+
+def test_model_lowbit_parts(orc):
+    """Layers in lowbit_mask list their source tensors as low-bit (all but the
+    attention gate_proj, which stays Q8); others all Q8. An R1 model refuses
+    low-bit tensors and the bf16 table (they take bf16 activations)."""
+    m = orc.Model(**LOWQ)
+    H, F = TINY["hidden"], TINY["ffn"]
+    assert m.parts(1, 0) == [(0, 256, 4), (256, 128, 4), (384, 128, 4), (512, 4, 8)]
+    assert m.parts(2, 0) == [(0, 3 * H, 4)] and m.parts(2, 2) == [(0, F, 4), (F, F, 4)]
+    assert m.parts(0, 0) == [(0, 3 * H, 8)] and m.lowbit(0, 0) is None
+    Q, S = m.lowbit(1, 3)
+    assert Q.shape == (H, F) and Q.max() == 15 and S.shape == (H, F // 32, 2)
+    m.close()
+    for bad in (dict(LOWQ, numerics=0), dict(TINY, emb_bf16=1), dict(LOWQ, lowbit=3)):
+        with pytest.raises(ValueError):
+            orc.Model(**bad)
+
+
+@pytest.mark.parametrize("bits", [4, 5])
+def test_model_lowbit_batched_equals_sequential(orc, bits):
+    m = orc.Model(**dict(LOWQ, lowbit=bits))
+    prompt = orc.gen_tokens(5, 33, TINY["vocab"])
+    r1, lg1 = m.feed(prompt, True)
+    h1 = m.hidden()
+    m.reset()
+    for t in prompt[:-1]:
+        m.feed(np.array([t], np.int32))
+    r2, lg2 = m.feed(prompt[-1:], True)
+    assert r1 == r2 and np.array_equal(f32bits(lg1), f32bits(lg2)) and np.array_equal(h1, m.hidden())
+    assert len(set(m.greedy(prompt, 16).tolist())) >= 6
+    m.close()
+
+
+def _layer_by_hand(orc, m, cfg, tok):
+    """One position through a one-layer model, restated from layer_body
+    (lfm3_nanode.cu:3739-3856) with the pinned primitives, every GEMV per
+    source tensor (gemv per name, 1916-1923: low-bit -> qlow_gemv, Q8 -> the R2
+    GEMV), the bf16 table's row and head (6062-6076, 3536-3573)."""
+    H, F, hd, nh, nkv = cfg["hidden"], cfg["ffn"], cfg["hd"], cfg["nh"], cfg["nkv"]
+
+    def gemv(slot, x):
+        W, S = m.tensor(0, slot)
+        low = m.lowbit(0, slot)
+        y = np.empty(W.shape[0], np.float32)
+        for r0, n, bits in m.parts(0, slot):
+            if bits == 8:
+                y[r0:r0 + n] = orc.q8r_gemm(W[r0:r0 + n], S[r0:r0 + n].view(np.float16).astype(np.float32), x)
+            else:
+                y[r0:r0 + n] = orc.qlow_gemv(low[0][r0:r0 + n], low[1][r0:r0 + n], x)
+        return orc.f2bf(y)
+
+    if cfg.get("emb_bf16"):
+        x = np.array(m.tensor(-1, 3)[tok])
+    else:
+        x = orc.embed_row(*m.tensor(-1, 0), tok)
+    h1 = orc.rmsnorm(x, m.tensor(0, 4))
+    if cfg["attn_mask"] & 1:
+        qd, kd = nh * hd, nkv * hd
+        w = gemv(0, h1)
+        q = orc.headnorm(w[:qd], m.tensor(0, 8), nh, hd)
+        k = orc.headnorm(w[qd:qd + kd], m.tensor(0, 9), nkv, hd)
+        cs = orc.rope_table(cfg["ctx"], hd, cfg["rot"], cfg["theta"])
+        q, k = orc.rope(q, cs, 0, nh, hd, cfg["rot"]), orc.rope(k, cs, 0, nkv, hd, cfg["rot"])
+        kc = orc.bf2f(k).astype(np.float16).view(np.uint16)
+        vc = orc.bf2f(w[qd + kd:qd + 2 * kd]).astype(np.float16).view(np.uint16)
+        a = orc.attn(q, kc, vc, 1, nh, nkv, hd, 1.0 / np.sqrt(np.float32(hd)))
+        a = orc.sigmoid_gate(w[qd + 2 * kd:], a, nh, hd)
+        h2 = gemv(1, a)
+    else:
+        bcx = gemv(0, h1)
+        out, _ = orc.conv_step(np.zeros(cfg["ntaps"] * H, np.uint16), m.tensor(0, 10), bcx, H, cfg["ntaps"])
+        h2 = gemv(1, out)
+    x = orc.add(x, orc.rmsnorm(h2, m.tensor(0, 5)))
+    gu = gemv(2, orc.rmsnorm(x, m.tensor(0, 6)))
+    d = gemv(3, orc.silu_mul(gu[:F], gu[F:]))
+    x = orc.add(x, orc.rmsnorm(d, m.tensor(0, 7)))
+    h = orc.rmsnorm(x, m.tensor(-1, 1))
+    if cfg.get("emb_bf16"):
+        return orc.bf16_gemv(m.tensor(-1, 3), h)
+    E, ES = m.tensor(-1, 0)
+    return orc.q8r_gemm(E, ES.view(np.float16).astype(np.float32), h)
+
+
+@pytest.mark.parametrize("kind", ["conv", "attn"])
+@pytest.mark.parametrize("low", [(0, 0), (4, 0), (5, 1)], ids=["q8-table", "q4-table", "q5-bf16"])
+def test_model_layer_composition(orc, kind, low):
+    """The oracle's layer and head composition against a second restatement of
+    layer_body built from the separately pinned primitives: which norm weight
+    goes where, the residual adds, the per-tensor GEMV dispatch of a low-bit
+    layer, the embedding row and tied head of a Q8 or bf16 table."""
+    bits, emb16 = low
+    cfg = dict(TINY, nlayers=1, attn_mask=1 if kind == "attn" else 0, numerics=1, lowbit=bits,
+               lowbit_mask=1 if bits else 0, emb_bf16=emb16)
+    m = orc.Model(**cfg)
+    _, lg = m.feed(np.array([417], np.int32), True)
+    assert np.array_equal(f32bits(_layer_by_hand(orc, m, cfg, 417)), f32bits(lg))
+    m.close()
