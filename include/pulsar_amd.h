@@ -199,7 +199,9 @@ int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, const uint16
  * bytes. Host-side only: no GPU is needed to open or read one. */
 typedef struct pq_blob_tensor {
   char name[128];
-  int dtype;          /* 1 Q8 (codes + fp32 scales), 2 fp32, 3 bf16 */
+  int dtype;          /* 1 Q8 (codes + fp32 scales), 2 fp32, 3 bf16, 6 / 7 Q4 / Q5 (the
+                         exporter's pre-tiled payload, pq_qlow_pack's layout: codes, then
+                         (d', mn) fp16 scales; N a multiple of 32, K of 256) */
   int ndim;
   long long ne[4];    /* shape, as the table lists it ([N][K] for a Linear) */
   long long ncodes;   /* payload bytes: codes (or the fp32 / bf16 values) */
@@ -288,6 +290,22 @@ int pq_embed(const int8_t *pcodes, const uint16_t *pscales, const int32_t *token
  * (138-142) on the blob's tensor, as the reference runs it. */
 int pq_embed_rows(const int8_t *codes, const float *scales, const int32_t *tokens, uint16_t *out, int H,
                   int vocab, int T, void *stream);
+
+/* The tied table kept as bf16 [vocab][H] (the exporter's --emb-bf16, dtype 3).
+ * pq_embed_bf16: rows of T token ids (device) copied as stored, zero rows for
+ * ids outside [0, vocab) -- the reference's bf16 row copy (lfm3_nanode.cu:
+ * 6062-6076). pq_bf16_gemv: y [N] fp32 = W . x for x bf16 [K] (K a multiple
+ * of 32, at most 16384), in k_gemv_bf16's order (3517-3534, as lm_head_bf16
+ * launches it, 3536-3573): per row, leaf L = 0..31 sums the products of
+ * elements L, L+32, ... in order, each rounded before its add, then the
+ * shfl_down tree 16, 8, 4, 2, 1 over the leaves. argmax_parts (NULL or
+ * 2 * pq_bf16_gemv_parts(N) floats) receives each workgroup's (largest y, its
+ * row; the lowest row on ties) for pq_argmax_parts. */
+int pq_embed_bf16(const uint16_t *table, const int32_t *tokens, uint16_t *out, int H, int vocab, int T,
+                  void *stream);
+int pq_bf16_gemv_parts(int N);
+int pq_bf16_gemv(const uint16_t *W, const uint16_t *x, float *y, int N, int K, float *argmax_parts,
+                 void *stream);
 
 
 /* ================================================== fused decode kernels

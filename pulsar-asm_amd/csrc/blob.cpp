@@ -8,7 +8,9 @@
 //   "data_bytes", "table": [{"name", "dtype", "ne", "off", "ncodes", "nscales",
 //   "crc"}, ...]}; then the payloads, tensor i at (12 + n) + off_i: ncodes
 //   bytes (int8 codes for dtype 1, f32 for 2, bf16 for 3) followed by nscales
-//   bytes of fp32 scales (one per 32 codes, dtype 1 only). crc is the zlib
+//   bytes of fp32 scales (one per 32 codes, dtype 1 only); dtype 6 / 7 are the
+//   Q4 / Q5 tensors .auto/lfm3/export_qlow.py writes, pre-tiled in 32-row tiles
+//   (16 / 20 code bytes per 32-group, then 4 bytes of (d', mn) fp16). crc is the zlib
 //   crc32 of the payload (codes then scales), recomputed here on the bytes
 //   read, as the reference's loader does (1358-1362).
 #include <fcntl.h>
@@ -302,8 +304,9 @@ static Blob *blob_open(const char *path) {
     e.dtype = (int)dt->num;
     e.crc = (uint32_t)crc;
     e.ndim = (int)ne->arr.size();
-    // every size is bounded by the file's: an element count past fsize (or a
-    // product that would overflow on the way there) cannot be a real tensor
+    // every size is bounded by the file's: an element count past 2 * fsize (Q4
+    // stores 0.625 bytes per element; or a product that would overflow on the
+    // way there) cannot be a real tensor
     uint64_t elems = 1;
     for (int d = 0; d < e.ndim; d++) {
       if (ne->arr[d].kind != Json::Num || ne->arr[d].num < 1 || ne->arr[d].num > 1e12) {
@@ -311,16 +314,19 @@ static Blob *blob_open(const char *path) {
         return nullptr;
       }
       e.ne[d] = (long long)ne->arr[d].num;
-      if (__builtin_mul_overflow(elems, (uint64_t)e.ne[d], &elems) || elems > B->fsize) {
-        fail(PQ_ERR_ARG, "blob: %s has more elements than the file has bytes", e.name.c_str());
+      if (__builtin_mul_overflow(elems, (uint64_t)e.ne[d], &elems) || elems > 2 * (uint64_t)B->fsize) {
+        fail(PQ_ERR_ARG, "blob: %s has more elements than the file can hold", e.name.c_str());
         return nullptr;
       }
     }
     // the payload must be what the shape and dtype say (export_lfm3_q8.py:132-155)
     bool ok = false;
     if (e.dtype == 1) ok = e.ndim == 2 && e.ne[1] % 32 == 0 && e.ncodes == elems && e.nscales == elems / 8;
-    else if (e.dtype == 2) ok = e.ncodes == elems * 4 && e.nscales == 0;      // elems <= fsize: no overflow
+    else if (e.dtype == 2) ok = e.ncodes == elems * 4 && e.nscales == 0;      // elems <= 2 fsize: no overflow
     else if (e.dtype == 3) ok = e.ncodes == elems * 2 && e.nscales == 0;
+    else if (e.dtype == 6 || e.dtype == 7)   // Q4 / Q5, pre-tiled (lfm3_nanode.cu:1494-1500)
+      ok = e.ndim == 2 && e.ne[0] % 32 == 0 && e.ne[1] % 256 == 0 &&
+           e.ncodes == elems / 32 * (e.dtype == 6 ? 16 : 20) && e.nscales == elems / 32 * 4;
     if (!ok) {
       fail(PQ_ERR_ARG, "blob: %s: dtype %d with %llu + %llu payload bytes does not match its shape", e.name.c_str(),
            e.dtype, (unsigned long long)e.ncodes, (unsigned long long)e.nscales);

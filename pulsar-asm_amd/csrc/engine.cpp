@@ -30,6 +30,17 @@
 
 namespace pq {
 
+// A source tensor of a slot as the .lfm3q8 file lists it (layer_body runs one
+// gemv per name, 3739-3856): rows r0 .. r0 + n of the slot; bits 8 = Q8 (the
+// slot's own row-major arrays), 4 / 5 = the exporter's pre-tiled Q4 / Q5
+// payload (dtype 6 / 7, pc and ps on the device), which gemv hands to
+// qlow_gemv (1916-1923).
+struct Part {
+  int r0 = 0, n = 0, bits = 8;
+  uint8_t *pc = nullptr;
+  uint16_t *ps = nullptr;
+};
+
 // A Q8 weight on the device. PQ_NUMERICS_Q8: packed tiles (pc) and fp16
 // scales (ps). PQ_NUMERICS_REF: row-major codes (pc) and fp32 scales (sf), as
 // the .lfm3q8 file stores them.
@@ -39,6 +50,8 @@ struct Q8Dev {
   float *sf = nullptr;
   int N = 0, K = 0;
   bool gate_up = false;  // Q8: packed by pq_q8_pack_gate_up (rows interleaved in groups of 32)
+  std::vector<Part> parts;   // non-empty when a source is low-bit: each part runs its own GEMV
+  bool split() const { return !parts.empty(); }
 };
 
 struct LayerDev {
@@ -82,6 +95,15 @@ struct Engine {
   size_t attn_ws_bytes = 0;
   void *gemm_ws = nullptr;
   size_t gemm_ws_bytes = 0;
+  // from a blob (PQ_NUMERICS_REF only): the tied table as bf16 [vocab][H]
+  // (dtype 3; null for a Q8 table), the Q4 / Q5 GEMV workspace and the
+  // [tmax][wide] staging of a part's rows at T > 1
+  uint16_t *emb16 = nullptr;
+  bool emb_bf16 = false;
+  void *qlow_ws = nullptr;
+  size_t qlow_ws_bytes = 0;
+  char *ptmp = nullptr;
+  int nparts16 = 0;
   std::vector<void *> allocs;
   bool loaded = false;
 
@@ -91,6 +113,17 @@ struct Engine {
       if (g) hipGraphExecDestroy(g);
     for (void *p : allocs) hipFree(p);
     if (st) hipStreamDestroy(st);
+  }
+
+  // frees an allocation dalloc made (null: nothing)
+  void dfree(void *p) {
+    if (!p) return;
+    for (size_t i = 0; i < allocs.size(); i++)
+      if (allocs[i] == p) {
+        hipFree(p);
+        allocs.erase(allocs.begin() + (long)i);
+        return;
+      }
   }
 
   template <typename T>
@@ -178,7 +211,8 @@ static int create(Engine &E, const pq_model_cfg &c) {
   PQ_TRY(E.dalloc(&E.Xd[0], (size_t)H));
   PQ_TRY(E.dalloc(&E.Xd[1], (size_t)H));
   E.nparts = ref_numerics(E) ? pq_q8r_gemv_parts(c.vocab) : pq_q8_gemv_parts(c.vocab, H);
-  PQ_TRY(E.dalloc(&E.parts, (size_t)E.nparts * 2));
+  E.nparts16 = pq_bf16_gemv_parts(c.vocab);
+  PQ_TRY(E.dalloc(&E.parts, (size_t)std::max(E.nparts, E.nparts16) * 2));
   PQ_TRY(E.dalloc(&E.Hb, (size_t)T * H));
   PQ_TRY(E.dalloc(&E.Wd, (size_t)T * wide));
   PQ_TRY(E.dalloc(&E.A, (size_t)T * kmax));
@@ -522,14 +556,47 @@ static bool mixer_fused(const Engine &E, const LayerDev &D) { return mixer_fused
 // codes) and the activations between ops stay bf16, as in layer_body; the
 // bf16 layer input xin holds every position (the Q8_0 qin's counterpart).
 static int gemm_r2(Engine &E, const Q8Dev &w, const uint16_t *x, void *y, int y_dtype, int T) {
-  return pq_q8r_gemv(w.pc, w.sf, x, y, y_dtype, w.N, w.K, T, E.st);
+  if (!w.split()) return pq_q8r_gemv(w.pc, w.sf, x, y, y_dtype, w.N, w.K, T, E.st);
+  // one GEMV per source tensor (gemv per name): a Q8 part over its rows of the
+  // slot's arrays, a Q4 / Q5 part one position at a time as pf_gemv_T runs it
+  // (4846-4848); at T > 1 a part's [T][n] rows go through ptmp into y's
+  // [T][N] rows by one strided copy
+  const size_t es = y_dtype == PQ_DTYPE_F32 ? 4 : 2;
+  for (const Part &p : w.parts) {
+    char *dst = T == 1 ? static_cast<char *>(y) + (size_t)p.r0 * es : E.ptmp;
+    if (p.bits == 8) {
+      PQ_TRY(pq_q8r_gemv(w.pc + (size_t)p.r0 * w.K, w.sf + (size_t)p.r0 * (w.K / 32), x, dst, y_dtype, p.n, w.K, T,
+                         E.st));
+    } else {
+      for (int t = 0; t < T; t++)
+        PQ_TRY(pq_qlow_gemv_ws(p.pc, p.ps, x + (size_t)t * w.K, dst + (size_t)t * p.n * es, y_dtype, p.n, w.K,
+                               p.bits, E.qlow_ws, E.qlow_ws_bytes, E.st));
+    }
+    if (T > 1 && hipMemcpy2DAsync(static_cast<char *>(y) + (size_t)p.r0 * es, (size_t)w.N * es, dst,
+                                  (size_t)p.n * es, (size_t)p.n * es, (size_t)T, hipMemcpyDeviceToDevice,
+                                  E.st) != hipSuccess)
+      return fail(PQ_ERR_LAUNCH, "part copy failed");
+  }
+  return PQ_OK;
+}
+
+// The embedding rows of n device token ids and the tied head on one final-normed
+// row, from the Q8 table or the bf16 one.
+static int embed_r2(Engine &E, const int32_t *toks, uint16_t *out, int n) {
+  if (E.emb_bf16) return pq_embed_bf16(E.emb16, toks, out, E.c.hidden, E.c.vocab, n, E.st);
+  return pq_embed_rows(E.emb.pc, E.emb.sf, toks, out, E.c.hidden, E.c.vocab, n, E.st);
+}
+static int head_r2(Engine &E, const uint16_t *x, float *parts) {
+  if (E.emb_bf16) return pq_bf16_gemv(E.emb16, x, E.logits, E.c.vocab, E.c.hidden, parts, E.st);   // lm_head_bf16
+  if (parts) return fail(PQ_ERR_ARG, "head_r2: argmax parts come from the fused GEMV");
+  return gemm_r2(E, E.emb, x, E.logits, PQ_DTYPE_F32, 1);
 }
 
 static int forward_r2(Engine &E, const int32_t *toks, int n, int32_t *next) {
   const pq_model_cfg &c = E.c;
   const int H = c.hidden, F = c.ffn;
   if (n <= 0 || E.pos + n > c.ctx) return fail(PQ_ERR_STATE, "context full: %d + %d > %d", E.pos, n, c.ctx);
-  PQ_TRY(pq_embed_rows(E.emb.pc, E.emb.sf, toks, E.X, H, c.vocab, n, E.st));
+  PQ_TRY(embed_r2(E, toks, E.X, n));
   PQ_TRY(pq_rmsnorm(E.X, nullptr, E.L[0].op_norm, nullptr, E.xin, nullptr, nullptr, H, n, c.eps, E.st));
   const float scale = 1.0f / sqrtf((float)c.hd);
   for (int l = 0; l < c.nlayers; l++) {
@@ -560,8 +627,9 @@ static int forward_r2(Engine &E, const int32_t *toks, int n, int32_t *next) {
       PQ_TRY(pq_rmsnorm(Xc, E.Hb, D.post_ffn_norm, next_norm, xin, nullptr, nullptr, H, T, c.eps, E.st));
     }
   }
-  // tied LM head (gemv_f: fp32 logits) on the last position's final-normed row
-  PQ_TRY(gemm_r2(E, E.emb, E.xin + (size_t)(n - 1) * H, E.logits, PQ_DTYPE_F32, 1));
+  // tied LM head (gemv_f, or lm_head_bf16 for a bf16 table: fp32 logits) on
+  // the last position's final-normed row
+  PQ_TRY(head_r2(E, E.xin + (size_t)(n - 1) * H, nullptr));
   PQ_TRY(pq_argmax(E.logits, c.vocab, next, E.st));
   E.pos += n;
   E.last_t = n;
@@ -708,9 +776,12 @@ static int forward_decode(Engine &E, bool dev) {
 // GEMV's epilogue, and the LM head writes per-workgroup argmax pairs: per
 // attention layer the in GEMV, the attention mixer, o_proj, gate/up and down
 // (five launches), per conv layer four (the conv is the out GEMV's
-// prologue), plus the LM head and the argmax. The position and id slot as in
-// forward_decode (dev: on the device, so the step can be captured and
-// replayed).
+// prologue), plus the LM head and the argmax. A slot with a low-bit source
+// tensor (a Q4 / Q5 blob) runs its parts' GEMVs on the op's bf16 output
+// instead (pq_rmsnorm's residual form, pq_conv on a copy of the ring,
+// pq_silu_mul: the same values), and a bf16 table takes the row copy and
+// pq_bf16_gemv. The position and id slot as in forward_decode (dev: on the
+// device, so the step can be captured and replayed).
 static int forward_decode_r2(Engine &E, bool dev) {
   const pq_model_cfg &c = E.c;
   const int H = c.hidden;
@@ -728,16 +799,34 @@ static int forward_decode_r2(Engine &E, bool dev) {
     p.eps = c.eps;
     std::swap(xa, xb);
   };
+  // the unfused "rms1 -> eadd -> rms1" triple: xa += rmsnorm(Hb, w0) in place,
+  // y = rmsnorm(xa, w1) as bf16
+  auto resnorm_to = [&](const float *w0, const float *w1, uint16_t *y) {
+    return pq_rmsnorm(xa, E.Hb, w0, w1, y, nullptr, nullptr, H, 1, c.eps, E.st);
+  };
   auto gemv = [&](const Q8Dev &w, void *y, int dt, float *parts) {
     return pq_q8r_gemv_fused(w.pc, w.sf, &p, y, dt, w.N, w.K, parts, E.st);
   };
   auto plain = [&](const Q8Dev &w, const uint16_t *x, uint16_t *y) {
-    return pq_q8r_gemv(w.pc, w.sf, x, y, PQ_DTYPE_BF16, w.N, w.K, 1, E.st);
+    return gemm_r2(E, w, x, y, PQ_DTYPE_BF16, 1);
   };
   const float scale = 1.0f / sqrtf((float)c.hd);
   for (int l = 0; l < c.nlayers; l++) {
     LayerDev &D = E.L[l];
-    if (l == 0) {   // the token's embedding row (written once to xa), normalized
+    if (l == 0 && (E.emb_bf16 || D.in.split())) {   // the row into xa, then its norm
+      PQ_TRY(embed_r2(E, E.tok, xa, 1));
+      if (D.in.split()) {
+        PQ_TRY(pq_rmsnorm(xa, nullptr, D.op_norm, nullptr, E.A, nullptr, nullptr, H, 1, c.eps, E.st));
+        PQ_TRY(plain(D.in, E.A, E.Wd));
+      } else {
+        p = pq_gemv_prologue{};
+        p.kind = PQ_PRO_NORM;
+        p.x_in = xa;
+        p.w0 = D.op_norm;
+        p.eps = c.eps;
+        PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
+      }
+    } else if (l == 0) {   // the token's embedding row (written once to xa), normalized
       p = pq_gemv_prologue{};
       p.kind = PQ_PRO_EMBED;
       p.tok = E.tok;
@@ -747,10 +836,14 @@ static int forward_decode_r2(Engine &E, bool dev) {
       p.x_out = xa;
       p.w0 = D.op_norm;
       p.eps = c.eps;
+      PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
+    } else if (D.in.split()) {
+      PQ_TRY(resnorm_to(E.L[l - 1].post_ffn_norm, D.op_norm, E.A));
+      PQ_TRY(plain(D.in, E.A, E.Wd));
     } else {
       resnorm(E.L[l - 1].post_ffn_norm, D.op_norm);
+      PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
     }
-    PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
     if (D.attn) {
       const int32_t *pd = dev ? E.ctr + 1 : nullptr;
       if (mixer_fused(E, D)) {
@@ -775,6 +868,15 @@ static int forward_decode_r2(Engine &E, bool dev) {
                                 E.st));
       }
       PQ_TRY(plain(D.out, E.A, E.Hb));
+    } else if (D.out.split()) {
+      // the ring ping-pong as the CONV prologue keeps it: the shifted ring goes
+      // to the other buffer (a copy, then the conv updates it in place)
+      const size_t rb = (size_t)c.ntaps * H * 2;
+      if (hipMemcpyAsync(D.rings[1 - D.rc], D.rings[D.rc], rb, hipMemcpyDeviceToDevice, E.st) != hipSuccess)
+        return fail(PQ_ERR_LAUNCH, "ring copy failed");
+      D.rc = 1 - D.rc;
+      PQ_TRY(pq_conv(D.rings[D.rc], D.taps, E.Wd, E.A, H, 1, c.ntaps, E.st));
+      PQ_TRY(plain(D.out, E.A, E.Hb));
     } else {
       p = pq_gemv_prologue{};
       p.kind = PQ_PRO_CONV;
@@ -786,14 +888,28 @@ static int forward_decode_r2(Engine &E, bool dev) {
       D.rc = 1 - D.rc;
       PQ_TRY(gemv(D.out, E.Hb, PQ_DTYPE_BF16, nullptr));
     }
-    resnorm(D.post_op_norm, D.ffn_norm);
-    PQ_TRY(pq_q8r_gemv_fused_swiglu(D.ug.pc, D.ug.sf, &p, E.A, c.ffn, H, E.st));
+    if (D.ug.split()) {
+      PQ_TRY(resnorm_to(D.post_op_norm, D.ffn_norm, E.A));
+      PQ_TRY(plain(D.ug, E.A, E.Wd));                               // [gate | up] rows
+      PQ_TRY(pq_silu_mul(E.Wd, E.A, nullptr, nullptr, c.ffn, 1, E.st));
+    } else {
+      resnorm(D.post_op_norm, D.ffn_norm);
+      PQ_TRY(pq_q8r_gemv_fused_swiglu(D.ug.pc, D.ug.sf, &p, E.A, c.ffn, H, E.st));
+    }
     PQ_TRY(plain(D.down, E.A, E.Hb));
   }
-  resnorm(E.L[c.nlayers - 1].post_ffn_norm, E.final_norm);
-  PQ_TRY(gemv(E.emb, E.logits, PQ_DTYPE_F32, E.parts));
-  if (dev) PQ_TRY(argmax_parts_step(E.parts, E.nparts, E.tok, E.ids, E.ctr, E.st));
-  else PQ_TRY(pq_argmax_parts(E.parts, E.nparts, E.tok, E.st));
+  const float *last_post = E.L[c.nlayers - 1].post_ffn_norm;
+  int nparts = E.nparts;
+  if (E.emb_bf16) {
+    PQ_TRY(resnorm_to(last_post, E.final_norm, E.A));
+    PQ_TRY(head_r2(E, E.A, E.parts));
+    nparts = E.nparts16;
+  } else {
+    resnorm(last_post, E.final_norm);
+    PQ_TRY(gemv(E.emb, E.logits, PQ_DTYPE_F32, E.parts));
+  }
+  if (dev) PQ_TRY(argmax_parts_step(E.parts, nparts, E.tok, E.ids, E.ctr, E.st));
+  else PQ_TRY(pq_argmax_parts(E.parts, nparts, E.tok, E.st));
   E.pos += 1;
   E.last_t = 1;
   E.last_resid = xa;
@@ -886,6 +1002,10 @@ static int decode(Engine &E, int n, int first_slot) {
 
 using namespace pq;
 
+static void drop_graphs(Engine &E);
+static void clear_blob_extras(Engine &E);
+static void clear_parts(Engine &E, Q8Dev &q);
+
 extern "C" void *pq_engine_create(const pq_model_cfg *cfg) {
   if (!cfg) { fail(PQ_ERR_ARG, "pq_engine_create: null config"); return nullptr; }
   const pq_model_cfg &c = *cfg;
@@ -918,6 +1038,8 @@ extern "C" int pq_engine_destroy(void *h) {
 extern "C" int pq_engine_load_synthetic(void *h) {
   PQ_REQUIRE(h, PQ_ERR_ARG, "null engine");
   Engine &E = *static_cast<Engine *>(h);
+  drop_graphs(E);
+  clear_blob_extras(E);
   PQ_TRY(load_synthetic(E));
   E.loaded = true;
   return PQ_OK;
@@ -928,6 +1050,8 @@ extern "C" int pq_engine_set_q8(void *h, int layer, int slot, const int8_t *code
   Engine &E = *static_cast<Engine *>(h);
   Q8Dev *q = q8_slot(E, layer, slot);
   PQ_REQUIRE(q, PQ_ERR_ARG, "pq_engine_set_q8: no Q8 tensor at layer %d slot %d", layer, slot);
+  drop_graphs(E);
+  clear_parts(E, *q);
   return upload_q8(E, *q, codes, scales, nullptr);
 }
 
@@ -936,6 +1060,8 @@ extern "C" int pq_engine_set_q8_f32(void *h, int layer, int slot, const int8_t *
   Engine &E = *static_cast<Engine *>(h);
   Q8Dev *q = q8_slot(E, layer, slot);
   PQ_REQUIRE(q, PQ_ERR_ARG, "pq_engine_set_q8_f32: no Q8 tensor at layer %d slot %d", layer, slot);
+  drop_graphs(E);
+  clear_parts(E, *q);
   return upload_q8(E, *q, codes, nullptr, scales);
 }
 
@@ -960,6 +1086,43 @@ struct BlobTarget {
   std::vector<BlobSrc> src;
 };
 }  // namespace
+
+// Discards the captured decode steps (they hold the weights' addresses); the
+// next decode captures them again.
+static void drop_graphs(Engine &E) {
+  if (E.st) hipStreamSynchronize(E.st);
+  for (hipGraphExec_t &g : E.gexec)
+    if (g) {
+      hipGraphExecDestroy(g);
+      g = nullptr;
+    }
+}
+
+// Frees what a blob load adds beyond the create-time arenas: low-bit parts,
+// the bf16 table, their workspaces; the slots are plain Q8 again.
+static void clear_parts(Engine &E, Q8Dev &q) {
+  if (q.parts.empty()) return;
+  if (E.st) hipStreamSynchronize(E.st);
+  for (const Part &pt : q.parts) {
+    E.dfree(pt.pc);
+    E.dfree(pt.ps);
+  }
+  q.parts.clear();
+}
+
+static void clear_blob_extras(Engine &E) {
+  if (E.st) hipStreamSynchronize(E.st);
+  for (LayerDev &D : E.L)
+    for (Q8Dev *q : {&D.in, &D.out, &D.ug, &D.down}) clear_parts(E, *q);
+  E.dfree(E.emb16);
+  E.emb16 = nullptr;
+  E.emb_bf16 = false;
+  E.dfree(E.qlow_ws);
+  E.qlow_ws = nullptr;
+  E.qlow_ws_bytes = 0;
+  E.dfree(E.ptmp);
+  E.ptmp = nullptr;
+}
 
 // The reference's tensor names (layer_body, lfm3_nanode.cu:3739-3856; the
 // exporter's table) onto the engine's slots: q|k|v|gate_proj stack into the
@@ -1016,8 +1179,10 @@ static int load_blob(Engine &E, void *blob) {
     T.push_back({l, 7, false, {{LN(l, "post_ffn_norm.weight"), H, 0}}});
   }
   T.push_back({-1, 1, false, {{"lfm.model.embedding_norm.weight", H, 0}}});
-  // every source present, with the dtype and shape its slot needs
-  std::vector<int> order;
+  // every source present, with the dtype and shape its slot needs: a linear is
+  // Q8 (dtype 1) or, under the reference numerics, Q4 / Q5 (6 / 7); the tied
+  // table Q8 or, under the reference numerics, bf16 (3)
+  std::vector<int> order, dtypes;
   for (const BlobTarget &t : T)
     for (const BlobSrc &s : t.src) {
       const int i = pq::blob_find(blob, s.name.c_str());
@@ -1027,23 +1192,39 @@ static int load_blob(Engine &E, void *blob) {
       long long elems = 1;
       for (int d = 0; d < ti.ndim; d++) elems *= ti.ne[d];
       if (t.q8) {
-        PQ_REQUIRE(ti.dtype == 1 && ti.ndim == 2 && ti.ne[0] == s.n0 && ti.ne[1] == s.n1, PQ_ERR_ARG,
-                   "pq_engine_load_blob: %s is dtype %d [%lld x %lld], the engine needs Q8 [%lld x %lld]",
-                   s.name.c_str(), ti.dtype, ti.ne[0], ti.ndim > 1 ? ti.ne[1] : 0, s.n0, s.n1);
+        const bool emb = t.layer == -1, low = ti.dtype == 6 || ti.dtype == 7;
+        PQ_REQUIRE((ti.dtype == 1 || (low && !emb) || (ti.dtype == 3 && emb)) && ti.ndim == 2 && ti.ne[0] == s.n0 &&
+                       ti.ne[1] == s.n1,
+                   PQ_ERR_ARG,
+                   "pq_engine_load_blob: %s is dtype %d [%lld x %lld], the engine needs [%lld x %lld] as Q8 (dtype 1)"
+                   "%s",
+                   s.name.c_str(), ti.dtype, ti.ne[0], ti.ndim > 1 ? ti.ne[1] : 0, s.n0, s.n1,
+                   emb ? " or bf16 (dtype 3)" : " or Q4 / Q5 (dtype 6 / 7)");
+        PQ_REQUIRE(ti.dtype == 1 || ref_numerics(E), PQ_ERR_ARG,
+                   "pq_engine_load_blob: %s is %s, which is not supported under the Q8_0 numerics (its GEMV takes "
+                   "bf16 activations): load it into an engine created with PQ_NUMERICS_REF",
+                   s.name.c_str(), low ? "a Q4 / Q5 tensor (dtype 6 / 7)" : "the bf16 table (dtype 3)");
       } else {
         PQ_REQUIRE(ti.dtype == 2 && elems == s.n0, PQ_ERR_ARG,
                    "pq_engine_load_blob: %s is dtype %d with %lld values, the engine needs %lld fp32", s.name.c_str(),
                    ti.dtype, elems, s.n0);
       }
       order.push_back(i);
+      dtypes.push_back(ti.dtype);
     }
+  // a new load replaces what an earlier one set up (the captured steps hold
+  // the old parts' addresses)
+  drop_graphs(E);
+  clear_blob_extras(E);
   // read ahead on a thread of its own while the tensors before convert and upload
   pq::BlobReader rd(blob, order, 2);
   std::vector<char> buf;
   std::vector<int8_t> codes;
   std::vector<float> sc32;
+  size_t si = 0;   // index of the next source in order / dtypes
   for (const BlobTarget &t : T) {
     if (!t.q8) {
+      si++;
       PQ_TRY(rd.take(buf));
       size_t n = 0;
       float *dst = vec_slot(E, t.layer, t.slot, &n);
@@ -1058,16 +1239,53 @@ static int load_blob(Engine &E, void *blob) {
     PQ_REQUIRE(q && q->N == rows && q->K == t.src[0].n1, PQ_ERR_ARG,
                "pq_engine_load_blob: slot %d of layer %d holds [%d x %d]", t.slot, t.layer, q ? q->N : 0,
                q ? q->K : 0);
-    codes.resize((size_t)rows * q->K);
-    sc32.resize((size_t)rows * (q->K / 32));
+    if (t.layer == -1 && dtypes[si] == 3) {   // the bf16 table, as stored
+      si++;
+      PQ_TRY(rd.take(buf));
+      if (!E.emb16) PQ_TRY(E.dalloc(&E.emb16, (size_t)c.vocab * H));
+      if (hipMemcpyAsync(E.emb16, buf.data(), buf.size(), hipMemcpyHostToDevice, E.st) != hipSuccess ||
+          hipStreamSynchronize(E.st) != hipSuccess)
+        return fail(PQ_ERR_LAUNCH, "bf16 table upload failed");
+      E.emb_bf16 = true;
+      continue;
+    }
+    // Q8 sources into the slot's row-major arrays (rows of low-bit sources stay
+    // zero there, unused), low-bit sources onto the device as the exporter laid
+    // them out
+    codes.assign((size_t)rows * q->K, 0);
+    sc32.assign((size_t)rows * (q->K / 32), 0.0f);
+    std::vector<Part> parts;
+    bool low = false;
     size_t r0 = 0;
     for (const BlobSrc &s : t.src) {
+      const int dt = dtypes[si++];
       PQ_TRY(rd.take(buf));
       const size_t nc = (size_t)s.n0 * s.n1, ns = nc / 32;
-      memcpy(codes.data() + r0 * q->K, buf.data(), nc);
-      memcpy(sc32.data() + r0 * (q->K / 32), buf.data() + nc, ns * 4);
+      Part pt;
+      pt.r0 = (int)r0;
+      pt.n = (int)s.n0;
+      if (dt == 1) {
+        memcpy(codes.data() + r0 * q->K, buf.data(), nc);
+        memcpy(sc32.data() + r0 * (q->K / 32), buf.data() + nc, ns * 4);
+      } else {
+        pt.bits = dt == 6 ? 4 : 5;
+        const size_t pcb = pq_qlow_packed_codes_bytes((int)s.n0, (int)s.n1, pt.bits);
+        const size_t psb = pq_qlow_packed_scales_bytes((int)s.n0, (int)s.n1, pt.bits);
+        PQ_REQUIRE(pcb + psb == buf.size(), PQ_ERR_ARG, "pq_engine_load_blob: %s: %zu payload bytes, want %zu",
+                   s.name.c_str(), buf.size(), pcb + psb);
+        PQ_TRY(E.dalloc(&pt.pc, pcb));
+        PQ_TRY(E.dalloc(&pt.ps, psb / 2));
+        if (hipMemcpyAsync(pt.pc, buf.data(), pcb, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+            hipMemcpyAsync(pt.ps, buf.data() + pcb, psb, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+            hipStreamSynchronize(E.st) != hipSuccess)
+          return fail(PQ_ERR_LAUNCH, "low-bit upload failed");
+        low = true;
+        E.qlow_ws_bytes = std::max(E.qlow_ws_bytes, pq_qlow_workspace_bytes(pt.n, (int)s.n1, pt.bits));
+      }
+      parts.push_back(pt);
       r0 += (size_t)s.n0;
     }
+    if (low) q->parts = std::move(parts);
     const int rc = upload_q8(E, *q, codes.data(), nullptr, sc32.data());
     if (rc != PQ_OK) {
       if (rc == PQ_ERR_DATA) {   // name the tensor in the message
@@ -1076,6 +1294,14 @@ static int load_blob(Engine &E, void *blob) {
       }
       return rc;
     }
+  }
+  // the low-bit GEMV workspace and the staging of a part's rows at T > 1
+  bool split = false;
+  for (const LayerDev &D : E.L) split = split || D.in.split() || D.out.split() || D.ug.split() || D.down.split();
+  if (split) {
+    PQ_TRY(E.dalloc(reinterpret_cast<char **>(&E.qlow_ws), std::max<size_t>(E.qlow_ws_bytes, 16)));
+    const size_t wide = (size_t)std::max(std::max(3 * H, 2 * F), (long long)E.nin);
+    PQ_TRY(E.dalloc(&E.ptmp, (size_t)E.tmax * wide * 4));
   }
   return PQ_OK;
 }

@@ -68,6 +68,9 @@ SIGNATURES = {
     "pq_argmax": (I, [P, I, P, P]),
     "pq_embed": (I, [P, P, P, P, I, I, I, P]),
     "pq_embed_rows": (I, [P, P, P, P, I, I, I, P]),
+    "pq_embed_bf16": (I, [P, P, P, I, I, I, P]),
+    "pq_bf16_gemv_parts": (I, [I]),
+    "pq_bf16_gemv": (I, [P, P, P, I, I, P, P]),
     "pq_engine_set_q8_f32": (I, [P, I, I, P, P]),
     "pq_q8_gemv_parts": (I, [I, I]),
     "pq_q8_gemv_fused": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, I, P, P]),

@@ -14,7 +14,7 @@ from . import PQError, check, lib
 from ._abi import BlobTensor
 
 MAGIC = b"LFM3Q8\x01\x00"
-T_Q8, T_F32, T_BF16 = 1, 2, 3
+T_Q8, T_F32, T_BF16, T_Q4, T_Q5 = 1, 2, 3, 6, 7
 
 
 class Blob:
@@ -64,16 +64,29 @@ class Blob:
         if t["dtype"] == T_Q8:
             N, K = t["ne"]
             return codes.view(np.int8).reshape(N, K), scales[:t["nscales"]].view(np.float32).reshape(N, K // 32)
+        if t["dtype"] in (T_Q4, T_Q5):   # the pre-tiled payload as stored: code bytes, (d', mn) fp16 bits
+            return codes, scales[:t["nscales"]].view(np.uint16)
         dt = np.float32 if t["dtype"] == T_F32 else np.uint16
         return codes.view(dt).reshape(t["ne"])
 
 
 def write_blob(path, cfg, tensors):
     """tensors: list of (name, value) with value (codes int8 [N][K], scales
-    fp32 [N][K/32]) for Q8, an fp32 array, or ("bf16", uint16 array)."""
+    fp32 [N][K/32]) for Q8, an fp32 array, ("bf16", uint16 array), or
+    ("qlow", bits, N, K, code bytes, scale bits) for a Q4 / Q5 tensor already
+    in the exporter's tiled payload (dtype 6 / 7, .auto/lfm3/export_qlow.py)."""
     entries, blobs, off = [], [], 0
     for name, v in tensors:
-        if isinstance(v, tuple) and len(v) == 2 and not isinstance(v[0], str):
+        if isinstance(v, tuple) and isinstance(v[0], str) and v[0] == "qlow":
+            _, bits, N, K, pc, ps = v
+            pc = np.ascontiguousarray(pc, np.uint8)
+            ps = np.ascontiguousarray(ps, np.uint16)
+            assert bits in (4, 5) and N % 32 == 0 and K % 256 == 0
+            assert pc.nbytes == N * K // 32 * (16 if bits == 4 else 20) and ps.nbytes == N * K // 32 * 4
+            payload = [pc.tobytes(), ps.tobytes()]
+            e = dict(name=name, dtype=T_Q4 if bits == 4 else T_Q5, ne=[N, K], off=off, ncodes=pc.nbytes,
+                     nscales=ps.nbytes)
+        elif isinstance(v, tuple) and len(v) == 2 and not isinstance(v[0], str):
             codes = np.ascontiguousarray(v[0], np.int8)
             scales = np.ascontiguousarray(v[1], np.float32)
             assert codes.ndim == 2 and scales.shape == (codes.shape[0], codes.shape[1] // 32)

@@ -8,6 +8,9 @@ lfm3_synth_greedy.json  the synthetic 24-layer LFM3-style backbone (hidden 2048,
                         prompt and the 64 greedy ids the oracle decodes from it
 lfm3_synth_greedy_ref.json  the same model and prompt with every GEMV in the
                         reference's own order (numerics = 1: bf16 x, fp32 scales)
+lfm3_synth_q4_greedy.json  the same model, prompt and GEMV order with every layer's
+                        linears Q4 (all but the attention gate_proj, which stays Q8;
+                        the exporter's dtype 6 tensors, .auto/lfm3/export_qlow.py)
 lfm3_real_shapes_greedy.json  the real LFM3 backbone's shapes and layer pattern (13 conv,
                         6 full and 5 sliding-window attention layers, head_dim 128,
                         FFN 7680, vocab 128000, 7-tap conv) with synthetic weights
@@ -86,7 +89,7 @@ def kernel_fixture(path):
 
 
 if __name__ == "__main__":
-    which = sys.argv[1:] or ["kernels", "tiny", "full", "full_ref", "real"]
+    which = sys.argv[1:] or ["kernels", "tiny", "full", "full_ref", "real", "full_q4"]
     if "kernels" in which:
         kernel_fixture(os.path.join(HERE, "kernels.npz"))
     if "tiny" in which:
@@ -97,3 +100,6 @@ if __name__ == "__main__":
         greedy_fixture(REAL, 256, 64, os.path.join(HERE, "lfm3_real_shapes_greedy.json"))
     if "full_ref" in which:
         greedy_fixture(dict(FULL, numerics=1), 256, 64, os.path.join(HERE, "lfm3_synth_greedy_ref.json"))
+    if "full_q4" in which:
+        greedy_fixture(dict(FULL, numerics=1, lowbit=4, lowbit_mask=0xFFFFFF), 256, 64,
+                       os.path.join(HERE, "lfm3_synth_q4_greedy.json"))

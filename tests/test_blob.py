@@ -139,3 +139,47 @@ def test_oversized_sizes_are_refused(tmp_path):
         q.write_bytes(_rewrite_entry(raw, 1, **f))
         with pytest.raises(PQError):
             Blob(q)
+
+
+def _raw_blob(path, entries, payloads):
+    """A file with a hand-written table (for sizes write_blob would refuse)."""
+    import json
+    hj = json.dumps(dict(magic=MAGIC.decode(), cfg={}, n_tensors=len(entries), table=entries)).encode()
+    with open(path, "wb") as fh:
+        fh.write(MAGIC)
+        fh.write(struct.pack("<I", len(hj)))
+        fh.write(hj)
+        for b in payloads:
+            fh.write(b)
+
+
+@pytest.mark.parametrize("bits", [4, 5])
+def test_lowbit_tensors(tmp_path, bits):
+    """Q4 / Q5 tensors (dtype 6 / 7, the pre-tiled payload of
+    .auto/lfm3/export_qlow.py): N a multiple of 32, K of 256, N*K/32 groups of
+    16 (Q4) or 20 (Q5) code bytes, then 4 bytes of (d', mn) per group, as the
+    reference's loader checks them (lfm3_nanode.cu:1494-1500). The payload reads
+    back as stored; a size or shape off that rule is refused."""
+    rng = np.random.default_rng(bits)
+    N, K = 64, 512
+    G = N * K // 32
+    pc = rng.integers(0, 256, G * (16 if bits == 4 else 20)).astype(np.uint8)
+    ps = rng.integers(0, 65536, G * 2).astype(np.uint16)
+    p = tmp_path / "q.lfm3q8"
+    write_blob(p, {}, [("lfm.model.layers.0.feed_forward.w2.weight", ("qlow", bits, N, K, pc, ps))])
+    b = Blob(p)
+    t = b.info(0)
+    assert t["dtype"] == (6 if bits == 4 else 7) and t["ne"] == [N, K]
+    c, s = b.read(0)
+    assert np.array_equal(c, pc) and np.array_equal(s, ps)
+    b.close()
+    dt = 6 if bits == 4 else 7
+    for (n, k, nc, ns) in ((N, K, pc.nbytes - 16, ps.nbytes), (N, K, pc.nbytes, ps.nbytes + 4),
+                           (40, K, 40 * K // 32 * (pc.nbytes // G), 40 * K // 32 * 4),
+                           (N, 480, N * 15 * (pc.nbytes // G), N * 15 * 4)):
+        q = tmp_path / "bad.lfm3q8"
+        payload = bytes(nc + ns)
+        _raw_blob(q, [dict(name="w", dtype=dt, ne=[n, k], off=0, ncodes=nc, nscales=ns,
+                           crc=zlib.crc32(payload) & 0xFFFFFFFF)], [payload])
+        with pytest.raises(PQError, match="does not match its shape"):
+            Blob(q)

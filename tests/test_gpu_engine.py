@@ -104,47 +104,8 @@ def test_lfm3_synth_greedy_64(orc, pq, dev):
 
 
 def _model_blob(orc, cfg, path):
-    """The oracle's synthetic model written as an .lfm3q8 file under the
-    reference's tensor names (fp16 scales widened to fp32, exact)."""
-    from pulsar_amd.blob import write_blob
-    m = orc.Model(**cfg)
-    H, F = cfg["hidden"], cfg["ffn"]
-    qd, kd = cfg["nh"] * cfg["hd"], cfg["nkv"] * cfg["hd"]
-
-    def q8(layer, slot):
-        w, s = m.tensor(layer, slot)
-        return np.array(w), np.array(s).view(np.float16).astype(np.float32)
-
-    ts = [("lfm.model.embed_tokens.weight", q8(-1, 0))]
-    for l in range(cfg["nlayers"]):
-        P = f"lfm.model.layers.{l}."
-        if (cfg["attn_mask"] >> l) & 1:
-            w, s = q8(l, 0)
-            cuts = [0, qd, qd + kd, qd + 2 * kd, qd + 2 * kd + cfg["nh"]]
-            for i, nm in enumerate(("q_proj", "k_proj", "v_proj", "gate_proj")):
-                ts.append((P + f"self_attn.{nm}.weight", (w[cuts[i]:cuts[i + 1]], s[cuts[i]:cuts[i + 1]])))
-            ts.append((P + "self_attn.o_proj.weight", q8(l, 1)))
-            ts.append((P + "self_attn.q_norm.weight", np.array(m.tensor(l, 8))))
-            ts.append((P + "self_attn.k_norm.weight", np.array(m.tensor(l, 9))))
-        else:
-            ts.append((P + "conv.in_proj.weight", q8(l, 0)))
-            ts.append((P + "conv.out_proj.weight", q8(l, 1)))
-            ts.append((P + "conv.conv.weight", np.array(m.tensor(l, 10)).reshape(H, 1, cfg["ntaps"])))
-        w, s = q8(l, 2)
-        ts.append((P + "feed_forward.w1.weight", (w[:F], s[:F])))
-        ts.append((P + "feed_forward.w3.weight", (w[F:], s[F:])))
-        ts.append((P + "feed_forward.w2.weight", q8(l, 3)))
-        for slot, nm in ((4, "operator_norm"), (5, "post_operator_norm"), (6, "ffn_norm"), (7, "post_ffn_norm")):
-            ts.append((P + nm + ".weight", np.array(m.tensor(l, slot))))
-    ts.append(("lfm.model.embedding_norm.weight", np.array(m.tensor(-1, 1))))
-    def kind(l):
-        if not (cfg["attn_mask"] >> l) & 1:
-            return "conv"
-        return "sliding_attention" if (cfg.get("slide_mask", 0) >> l) & 1 else "full_attention"
-
-    layer_types = [kind(l) for l in range(cfg["nlayers"])]
-    write_blob(path, {"hidden_size": H, "vocab_size": cfg["vocab"], "layer_types": layer_types}, ts)
-    m.close()
+    from model_blob import model_blob
+    model_blob(orc, cfg, path)
 
 
 def test_blob_load_matches_synthetic(orc, pq, dev, tmp_path):
