@@ -10,15 +10,16 @@
 // where db_g is the d of Q8_K block g/2 and qs its half g%2.
 //
 // The int32 group dots run lane-parallel; the fp32 chain is sequential per row
-// over all groups, so each workgroup owns whole rows (8 rows of 32 lanes, or
-// 16 of 16 for short rows): the lanes compute the group partials p_g into
-// LDS, then one lane per row folds them in group order.
+// over all groups, so each workgroup owns whole rows (16 rows of 32 lanes, 8
+// of 64 for long rows): the lanes compute the group partials p_g into LDS,
+// then, after one barrier, lane i of wave 0 folds row i in group order.
 //
 // Group dot without unpacking the codes to bytes: for a code dword w (16
-// weights), d_k = (w >> 2k) & 0x03030303 holds the codes of weights
-// {k, k+4, k+8, k+12}; the activations are staged in LDS permuted the same
-// way (dword k of each 16 = x[k], x[k+4], x[k+8], x[k+12]), so
-// sum code*x = sum_k dot4(d_k, xperm_k), and isum = that - sum x over the group.
+// weights), w & 0x33333333 holds the even weights' codes in its nibbles and
+// (w >> 2) & 0x33333333 the odd ones'; each activation is split x = 16 h + l
+// (h the signed high nibble, l the unsigned low one) and staged in LDS as four
+// nibble-packed dwords per 16 weights, so sum code*x = 16 * (two v_dot8_i32_i4)
+// + (two v_dot8_u32_u4), exact, and isum = that - sum x over the group.
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
@@ -59,6 +60,46 @@ __device__ __forceinline__ void tq2_load_x(const uint8_t *__restrict__ xq, int K
   t.d = __builtin_amdgcn_raw_buffer_load_b32(rx, g < ng ? blk * kQ8KBytes : kRsrcOob, 0, 0);
 }
 
+// A run of 16 qs (bytes x0..x15 in dwords w0..w3) regrouped by byte permutes:
+// A = x0 x4 x8 x12, B = x2 x6 x10 x14, C = x1 x5 x9 x13, D = x3 x7 x11 x15
+// (the byte form's dwords k = 0, 2, 1, 3: byte j of dword k = x[k + 4j]).
+struct TqRun {
+  uint32_t A, B, C, D;
+};
+__device__ __forceinline__ TqRun tq2_regroup(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+  const uint32_t e01 = __builtin_amdgcn_perm(w1, w0, 0x06020400u);   // x0 x4 x2 x6
+  const uint32_t e23 = __builtin_amdgcn_perm(w3, w2, 0x06020400u);   // x8 x12 x10 x14
+  const uint32_t o01 = __builtin_amdgcn_perm(w1, w0, 0x07030501u);   // x1 x5 x3 x7
+  const uint32_t o23 = __builtin_amdgcn_perm(w3, w2, 0x07030501u);   // x9 x13 x11 x15
+  TqRun r;
+  r.A = __builtin_amdgcn_perm(e23, e01, 0x05040100u);
+  r.B = __builtin_amdgcn_perm(e23, e01, 0x07060302u);
+  r.C = __builtin_amdgcn_perm(o23, o01, 0x05040100u);
+  r.D = __builtin_amdgcn_perm(o23, o01, 0x07060302u);
+  return r;
+}
+
+// The D8 form of a run: each x = 16 h + l with h = x >> 4 (a signed nibble,
+// -8..7) and l = x & 15 (an unsigned one), packed as the nibbles of the code
+// masks w & 0x33333333 (nibble n = code 2n) and (w >> 2) & 0x33333333 (code
+// 2n + 1) line up: dword 0 = h of x0, x2, ..., x14 (nibble 2k from A, 2k + 1
+// from B); 1 = h of the odd x (C, D); 2, 3 = l of the even and the odd x.
+__device__ __forceinline__ int4 tq2_d8_run(const TqRun &r) {
+  const uint32_t he = ((r.A >> 4) & 0x0f0f0f0fu) | (r.B & 0xf0f0f0f0u);
+  const uint32_t ho = ((r.C >> 4) & 0x0f0f0f0fu) | (r.D & 0xf0f0f0f0u);
+  const uint32_t le = (r.A & 0x0f0f0f0fu) | ((r.B & 0x0f0f0f0fu) << 4);
+  const uint32_t lo = (r.C & 0x0f0f0f0fu) | ((r.D & 0x0f0f0f0fu) << 4);
+  return make_int4((int)he, (int)ho, (int)le, (int)lo);
+}
+
+// The staged x in LDS: the 4 runs of a 64-weight piece (16 dwords) at a piece
+// stride of kXPieceDw dwords, so the pieces that consecutive lanes read start
+// on different banks (a 16-dword stride put every even piece on the same four
+// banks: 16-way conflicts).
+constexpr int kXPieceDw = 20;
+__host__ __device__ constexpr int tq2_xbytes(int K) { return K / 64 * kXPieceDw * 4; }
+__device__ __forceinline__ int tq2_run_dw(int m) { return (m >> 2) * kXPieceDw + (m & 3) * 4; }
+
 template <int XR, int NT>
 __device__ __forceinline__ void tq2_store_x(const TqX<XR> &t, int K, int *xperm, int *gsum, float *db) {
   const int ng = K / kTqGroup, nrun = K / 16;
@@ -66,15 +107,8 @@ __device__ __forceinline__ void tq2_store_x(const TqX<XR> &t, int K, int *xperm,
   for (int i = 0; i < XR; i++) {
     const int m = threadIdx.x + i * NT;
     if (m < nrun) {
-      const uint32_t w0 = t.run[i].x, w1 = t.run[i].y, w2 = t.run[i].z, w3 = t.run[i].w;
-      int4 o;
-      o.x = (int)((w0 & 0xffu) | ((w1 & 0xffu) << 8) | ((w2 & 0xffu) << 16) | ((w3 & 0xffu) << 24));
-      o.y = (int)(((w0 >> 8) & 0xffu) | (((w1 >> 8) & 0xffu) << 8) | (((w2 >> 8) & 0xffu) << 16) |
-                  (((w3 >> 8) & 0xffu) << 24));
-      o.z = (int)(((w0 >> 16) & 0xffu) | (((w1 >> 16) & 0xffu) << 8) | (((w2 >> 16) & 0xffu) << 16) |
-                  (((w3 >> 16) & 0xffu) << 24));
-      o.w = (int)((w0 >> 24) | ((w1 >> 24) << 8) | ((w2 >> 24) << 16) | ((w3 >> 24) << 24));
-      reinterpret_cast<int4 *>(xperm)[m] = o;
+      const TqRun rr = tq2_regroup(t.run[i].x, t.run[i].y, t.run[i].z, t.run[i].w);
+      *reinterpret_cast<int4 *>(xperm + tq2_run_dw(m)) = tq2_d8_run(rr);
     }
   }
   const int g = threadIdx.x;
@@ -107,13 +141,17 @@ struct TqBatch {
 // gs and gs ^ 1 hold the two halves of the same groups; their exact int32
 // half-dots add across the pair, and the even lane forms the group partial.
 // PPL pieces per lane per round (LPR*PPL pieces = 64*LPR*PPL of K).
+// The group dots are nibble dots (v_dot8: codes w & 0x33333333 and
+// (w >> 2) & 0x33333333 against x's signed high and unsigned low nibbles,
+// sum code*x = 16 sum code*h + sum code*l: 7 VALU per 16 weights, against 11
+// for four byte masks and sdot4). The codes load nontemporal.
 template <int LPR, int PPL, int XR, int NT>
 __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t *__restrict__ xq, int K) {
   static_assert(64 % LPR == 0, "a row's lanes must sit in one wave");
   extern __shared__ __align__(16) unsigned char smem[];
   const int ng = K / kTqGroup, npc = 2 * ng;                 // groups, 16-byte pieces per row
-  int *xperm = reinterpret_cast<int *>(smem);                  // K bytes, permuted
-  int *gsum = reinterpret_cast<int *>(smem + K);               // [ng] sum of qs over the group
+  int *xperm = reinterpret_cast<int *>(smem);                  // tq2_xbytes(K): K bytes, permuted, padded
+  int *gsum = reinterpret_cast<int *>(smem + tq2_xbytes(K));   // [ng] sum of qs over the group
   float *db = reinterpret_cast<float *>(gsum + ng);            // [ng] Q8_K d of the group's block
   float *pg = db + ng;                                         // [NT/LPR rows][ng] group partials
   const int tid = threadIdx.x;
@@ -125,10 +163,13 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
   const int N = bt.rows[ti];
   const int row = ((int)blockIdx.x - bt.wg0[ti]) * (NT / LPR) + r;
   const bool live = row < N;
+  // one resource per tensor (workgroup-uniform: scalar registers, no per-row
+  // waterfall); a row past N reads at an offset past num_records: zeros
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t *>(codes + (size_t)(live ? row : 0) * (K / 4)), (short)0, live ? K / 4 : 0, kRsrcWord3);
+      const_cast<uint8_t *>(codes), (short)0, (int)((size_t)N * (K / 4)), kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t *>(scales + (size_t)(live ? row : 0) * ng), (short)0, live ? ng * 2 : 0, kRsrcWord3);
+      const_cast<uint16_t *>(scales), (short)0, (int)((size_t)N * ng * 2), kRsrcWord3);
+  const int crow = live ? row * (K / 4) : kRsrcOob, srow = live ? row * ng * 2 : kRsrcOob;
   TqX<XR> xt;
   tq2_load_x<XR, NT>(xq, K, xt);
   for (int p0 = 0; p0 < npc; p0 += LPR * PPL) {
@@ -139,8 +180,10 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
 #pragma unroll
     for (int j = 0; j < PPL; j++) {
       const int pc = p0 + j * LPR + gs, g = pc >> 1;
-      c[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, pc < npc ? pc * 16 : kRsrcOob, 0, 0);
-      sc[j] = (gs & 1) == 0 ? __builtin_amdgcn_raw_buffer_load_b32(rsc, pc < npc ? (g & ~1) * 2 : kRsrcOob, 0, 0) : 0u;
+      c[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, pc < npc && live ? crow + pc * 16 : kRsrcOob, 0, kAuxNT);
+      // every lane loads (the odd lane of a pair discards it): no branch, so
+      // the waits on the earlier x loads count exactly
+      sc[j] = __builtin_amdgcn_raw_buffer_load_b32(rsc, pc < npc && live ? srow + (g & ~1) * 2 : kRsrcOob, 0, 0);
     }
     if (p0 == 0) {
       tq2_store_x<XR, NT>(xt, K, xperm, gsum, db);
@@ -150,17 +193,20 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
     for (int j = 0; j < PPL; j++) {
       const int pc = p0 + j * LPR + gs, g = pc >> 1;
       const uint32_t w[4] = {(uint32_t)c[j].x, (uint32_t)c[j].y, (uint32_t)c[j].z, (uint32_t)c[j].w};
-      const int *xp = xperm + (pc < npc ? pc : 0) * 16;
-      int sacc = 0;
+      const int *xp = xperm + (pc < npc ? pc : 0) * kXPieceDw;
+      int ah = 0;
+      uint32_t al = 0;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * q);
-        sacc = __builtin_amdgcn_sdot4((int)(w[q] & 0x03030303u), xv.x, sacc, false);
-        sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 2) & 0x03030303u), xv.y, sacc, false);
-        sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 4) & 0x03030303u), xv.z, sacc, false);
-        sacc = __builtin_amdgcn_sdot4((int)((w[q] >> 6) & 0x03030303u), xv.w, sacc, false);
+        const int m0 = (int)(w[q] & 0x33333333u), m1 = (int)((w[q] >> 2) & 0x33333333u);
+        ah = __builtin_amdgcn_sdot8(m0, xv.x, ah, false);
+        ah = __builtin_amdgcn_sdot8(m1, xv.y, ah, false);
+        al = __builtin_amdgcn_udot8(m0, xv.z, al, false);
+        al = __builtin_amdgcn_udot8(m1, xv.w, al, false);
       }
-      sacc += __shfl_xor(sacc, 1, 64);   // the group's two halves
+      int sacc = 16 * ah + (int)al;
+      sacc += __builtin_amdgcn_update_dpp(0, sacc, kDppXor1, 0xf, 0xf, false);   // the group's two halves
       if ((gs & 1) == 0 && pc < npc) {
         const int isum = sacc - gsum[g];
         const float t = h2f((uint16_t)(sc[j] >> (16 * (g & 1)))) * db[g];
@@ -168,13 +214,14 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
       }
     }
   }
-  // a row's LPR lanes sit in one wave (64 % LPR == 0), so its partials need
-  // only this wave's LDS writes to land
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  if (gs == 0 && live) {   // groups ascending; partials read 8 at a time
+  // after one workgroup barrier, lane i of wave 0 folds row i: every row of
+  // the workgroup in one wave's instruction stream (a fold per wave, with 2 of
+  // its lanes busy, measured 0.1-0.3 us slower per launch)
+  __syncthreads();
+  const int fr = tid, frow = ((int)blockIdx.x - bt.wg0[ti]) * (NT / LPR) + tid;
+  if (tid < NT / LPR && frow < N) {   // groups ascending; partials read 8 at a time
     float acc = 0.0f;
-    const float *pr = pg + r * ng;
+    const float *pr = pg + fr * ng;
     const int ng8 = (ng & 7) == 0 ? ng : 0;   // 16-byte aligned rows when ng % 8 == 0
     for (int g = ng8; g < ng; g++) acc = acc + pr[g];
     for (int g = 0; g < ng8; g += 8) {
@@ -183,7 +230,7 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
       acc = acc + a4.x; acc = acc + a4.y; acc = acc + a4.z; acc = acc + a4.w;
       acc = acc + b4.x; acc = acc + b4.y; acc = acc + b4.z; acc = acc + b4.w;
     }
-    y[row] = acc;
+    y[frow] = acc;
   }
 }
 
@@ -261,7 +308,7 @@ static int tq2_launch(TqBatch bt, int n, const uint8_t *xq, int K, hipStream_t s
   // 4096x12288 6.0 against 6.8 and 6.7)
   const int nt = envt == 256 || envt == 512 || envt == 1024 ? envt : 512;
   const int rows = nt / lpr;
-  const size_t lds = (size_t)K + (size_t)ng * 8 + (size_t)rows * ng * 4;
+  const size_t lds = (size_t)tq2_xbytes(K) + (size_t)ng * 8 + (size_t)rows * ng * 4;
   bt.wg0[0] = 0;
   for (int i = 0; i < kTqBatch; i++) bt.wg0[i + 1] = bt.wg0[i] + (i < n ? (bt.rows[i] + rows - 1) / rows : 0);
   for (int i = n; i < kTqBatch; i++) bt.wg0[i + 1] = 0x7fffffff;   // never selected
@@ -309,6 +356,7 @@ extern "C" int pq_tq2_gemv(const uint8_t *codes, const uint16_t *scales, const u
   PQ_REQUIRE(N > 0 && K > 0 && K % kQ8K == 0 && K <= 32768, PQ_ERR_ARG,
              "pq_tq2_gemv: N=%d K=%d (K a multiple of 256, at most 32768)", N, K);
   PQ_REQUIRE(aligned(codes, 16) && aligned(xq, 4), PQ_ERR_ALIGN, "pq_tq2_gemv: codes must be 16-byte aligned");
+  PQ_REQUIRE((long long)N * (K / 4) < kRsrcOob, PQ_ERR_ARG, "pq_tq2_gemv: N=%d K=%d: codes beyond 1 GiB", N, K);
   TqBatch bt{};
   bt.codes[0] = codes;
   bt.scales[0] = scales;
@@ -330,6 +378,8 @@ extern "C" int pq_tq2_gemv_batch(const uint8_t *const *codes, const uint16_t *co
     PQ_REQUIRE(codes[i] && scales[i] && ys[i] && rows[i] > 0, PQ_ERR_ARG,
                "pq_tq2_gemv_batch: tensor %d: null pointer or rows=%d", i, rows[i]);
     PQ_REQUIRE(aligned(codes[i], 16), PQ_ERR_ALIGN, "pq_tq2_gemv_batch: tensor %d codes must be 16-byte aligned", i);
+    PQ_REQUIRE((long long)rows[i] * (K / 4) < kRsrcOob, PQ_ERR_ARG, "pq_tq2_gemv_batch: tensor %d: codes beyond 1 GiB",
+               i);
     bt.codes[i] = codes[i];
     bt.scales[i] = scales[i];
     bt.y[i] = ys[i];
