@@ -343,13 +343,16 @@ LFM3_REAL = dict(hidden=2048, ffn=7680, vocab=128000, nlayers=24, nh=16, nkv=4, 
                  prefill_chunk=256)
 
 
-def decode_variant(pq, cfg, n_steps=32, n_prompt=256):
+def decode_variant(pq, cfg, n_steps=32, n_prompt=256, blob=None):
     """tok/s of n_steps greedy steps after a 256-token prompt (median of 3 runs)
-    for another engine configuration."""
+    for another engine configuration (synthetic weights, or those of a blob)."""
     from pulsar_amd.engine import Engine, synth_fill
     from pulsar_amd.hiptime import Event
     e = Engine(**cfg)
-    e.load_synthetic()
+    if blob:
+        e.load_blob(blob)
+    else:
+        e.load_synthetic()
     prompt = synth_fill(5, cfg["seed"] + 4 * 5000, n_prompt, float(cfg["vocab"]))
     st = e.stream()
     e.reset()
@@ -374,6 +377,70 @@ def decode_variant(pq, cfg, n_steps=32, n_prompt=256):
     return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4), "weight_bytes": wbytes,
             "GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "prefill_ms_256": round(statistics.median(pre), 2), "steps": n_steps}
+
+
+def lowbit_blob(pq, torch, dev, g, cfg, bits, path):
+    """An .lfm3q8 file of the synthetic backbone's shapes with random weights,
+    written with the product's own blob writer: every layer's linears Q4 / Q5
+    (dtype 6 / 7, packed on the GPU by pq_qlow_pack into the exporter's tiled
+    payload) but the attention gate_proj (16 or 32 rows), which stays Q8 as in
+    the real LFM3 shapes; the tied table Q8; the norms and conv taps fp32."""
+    import numpy as np
+    from pulsar_amd.blob import write_blob
+    H, F = cfg["hidden"], cfg["ffn"]
+    qd, kd = cfg["nh"] * cfg["hd"], cfg["nkv"] * cfg["hd"]
+
+    def q8(N, K):
+        c = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+        s = (torch.randn((N, K // 32), device=dev, generator=g).abs() * 0.01).half().float()
+        return c.cpu().numpy(), s.cpu().numpy()
+
+    def low(N, K):
+        c = torch.randint(0, 2 ** bits, (N, K), dtype=torch.uint8, device=dev, generator=g)
+        dp = (torch.randn((N, K // 32), device=dev, generator=g).abs() * (2560.0 / 2 ** bits)).half()
+        mn = (-(2 ** bits - 1) * 0.5 * dp.float() / 128.0).half()
+        w = pq.QlowWeight(c, torch.stack([dp, mn], -1).view(torch.int16).contiguous(), bits)
+        return ("qlow", bits, N, K, w.pcodes.cpu().numpy(), w.pscales.cpu().numpy().view(np.uint16))
+
+    def vec(n, a, b):
+        return (a + b * torch.randn(n, device=dev, generator=g)).cpu().numpy().astype(np.float32)
+
+    ts = [("lfm.model.embed_tokens.weight", q8(cfg["vocab"], H))]
+    for l in range(cfg["nlayers"]):
+        P = f"lfm.model.layers.{l}."
+        if (cfg["attn_mask"] >> l) & 1:
+            ts += [(P + "self_attn.q_proj.weight", low(qd, H)), (P + "self_attn.k_proj.weight", low(kd, H)),
+                   (P + "self_attn.v_proj.weight", low(kd, H)), (P + "self_attn.gate_proj.weight", q8(cfg["nh"], H)),
+                   (P + "self_attn.o_proj.weight", low(H, qd)),
+                   (P + "self_attn.q_norm.weight", vec(cfg["hd"], 1.0, 0.1)),
+                   (P + "self_attn.k_norm.weight", vec(cfg["hd"], 1.0, 0.1))]
+        else:
+            ts += [(P + "conv.in_proj.weight", low(3 * H, H)), (P + "conv.out_proj.weight", low(H, H)),
+                   (P + "conv.conv.weight", vec(H * cfg["ntaps"], 0.0, 0.5).reshape(H, 1, cfg["ntaps"]))]
+        ts += [(P + "feed_forward.w1.weight", low(F, H)), (P + "feed_forward.w3.weight", low(F, H)),
+               (P + "feed_forward.w2.weight", low(H, F))]
+        for nm, a, b in (("operator_norm", 1.0, 0.1), ("post_operator_norm", 4.0, 0.4), ("ffn_norm", 1.0, 0.1),
+                         ("post_ffn_norm", 4.0, 0.4)):
+            ts.append((P + nm + ".weight", vec(H, a, b)))
+    ts.append(("lfm.model.embedding_norm.weight", vec(H, 1.0, 0.1)))
+    kinds = ["full_attention" if (cfg["attn_mask"] >> l) & 1 else "conv" for l in range(cfg["nlayers"])]
+    write_blob(path, {"hidden_size": H, "vocab_size": cfg["vocab"], "layer_types": kinds}, ts)
+
+
+def decode_lowbit(pq, torch, dev, g, bits=4, n_steps=32, n_prompt=256):
+    """The synthetic 24-layer backbone with Q4 (or Q5) linears from an .lfm3q8
+    file, under the reference numerics (bf16 activations, as the reference runs
+    its low-bit tensors): decode tok/s after a 256-token prompt, the bytes a step
+    reads (the packed low-bit payloads) and their rate."""
+    import tempfile
+    from pulsar_amd.engine import LFM3_SYNTH
+    cfg = dict(LFM3_SYNTH, numerics=1)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, f"q{bits}.lfm3q8")
+        lowbit_blob(pq, torch, dev, g, cfg, bits, path)
+        out = decode_variant(pq, cfg, n_steps=n_steps, n_prompt=n_prompt, blob=path)
+    out["weights"] = f"Q{bits} linears (gate_proj Q8), Q8 table"
+    return out
 
 
 def prefill_gemm_bench(pq, torch, dev, g, stream, gpu, T=512, chunk=32):
@@ -704,9 +771,10 @@ def main():
                     help="also run a plain elementwise kernel over 256 MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill-profile", action="store_true",
                     help="only run the prefill GEMMs (3 launches each at T=512 and T=32) for counter runs; no JSON")
-    ap.add_argument("--decode-profile", choices=["synth", "real", "synth-ref", "real-ref"],
+    ap.add_argument("--decode-profile", choices=["synth", "real", "synth-ref", "real-ref", "synth-q4"],
                     help="only run one backbone's decode measurement (the synthetic or the real LFM3 shapes, "
-                         "-ref: the reference's GEMV numerics) for kernel traces; prints its result")
+                         "-ref: the reference's GEMV numerics, -q4: Q4 linears from a blob) for kernel traces; "
+                         "prints its result")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: there is no multi-GPU path (the GEMV would shard by rows, with an "
@@ -728,6 +796,11 @@ def main():
             torch.cuda.synchronize()
             del src, dst
         from pulsar_amd.engine import LFM3_SYNTH
+        if args.decode_profile == "synth-q4":
+            g = torch.Generator(device=dev)
+            g.manual_seed(20261201)
+            print(json.dumps({"decode_profile": args.decode_profile, **decode_lowbit(pq, torch, dev, g, 4)}))
+            return
         cfg = dict(LFM3_SYNTH if args.decode_profile.startswith("synth") else LFM3_REAL)
         if args.decode_profile.endswith("-ref"):
             cfg["numerics"] = 1
@@ -832,6 +905,7 @@ def main():
         line["ternary_gemv"] = ternary_bench(pq, torch, dev, g, stream)
         line["ref_numerics_gemv"] = ref_numerics_bench(pq, torch, dev, g, stream)
         line["qlow_gemv"] = qlow_bench(pq, torch, dev, g, stream)
+        line["decode_q4"] = decode_lowbit(pq, torch, dev, g, 4)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_q8_gemv([(N, K) for (_, N, K, _) in SHAPES], 10.0)
         if not args.no_extra:

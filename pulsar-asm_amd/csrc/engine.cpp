@@ -1251,38 +1251,62 @@ static int load_blob(Engine &E, void *blob) {
     }
     // Q8 sources into the slot's row-major arrays (rows of low-bit sources stay
     // zero there, unused), low-bit sources onto the device as the exporter laid
-    // them out
+    // them out. Adjacent low-bit sources of one width share a part (their
+    // 32-row tiles are stored tile after tile, so one payload holds both):
+    // q|k|v_proj or w1|w3 run as one GEMV.
     codes.assign((size_t)rows * q->K, 0);
     sc32.assign((size_t)rows * (q->K / 32), 0.0f);
     std::vector<Part> parts;
+    std::vector<int> part_of;   // the part of each source
+    {
+      size_t rr = 0;
+      for (size_t k = 0; k < t.src.size(); k++) {
+        const int dt = dtypes[si + k], bits = dt == 1 ? 8 : dt == 6 ? 4 : 5;
+        if (bits != 8 && !parts.empty() && parts.back().bits == bits) {
+          parts.back().n += (int)t.src[k].n0;
+        } else {
+          Part pt;
+          pt.r0 = (int)rr;
+          pt.n = (int)t.src[k].n0;
+          pt.bits = bits;
+          parts.push_back(pt);
+        }
+        part_of.push_back((int)parts.size() - 1);
+        rr += (size_t)t.src[k].n0;
+      }
+    }
     bool low = false;
+    for (Part &pt : parts)
+      if (pt.bits != 8) {
+        PQ_TRY(E.dalloc(&pt.pc, pq_qlow_packed_codes_bytes(pt.n, q->K, pt.bits)));
+        PQ_TRY(E.dalloc(&pt.ps, pq_qlow_packed_scales_bytes(pt.n, q->K, pt.bits) / 2));
+        E.qlow_ws_bytes = std::max(E.qlow_ws_bytes, pq_qlow_workspace_bytes(pt.n, q->K, pt.bits));
+        low = true;
+      }
     size_t r0 = 0;
-    for (const BlobSrc &s : t.src) {
+    for (size_t k = 0; k < t.src.size(); k++) {
+      const BlobSrc &s = t.src[k];
       const int dt = dtypes[si++];
       PQ_TRY(rd.take(buf));
       const size_t nc = (size_t)s.n0 * s.n1, ns = nc / 32;
-      Part pt;
-      pt.r0 = (int)r0;
-      pt.n = (int)s.n0;
       if (dt == 1) {
         memcpy(codes.data() + r0 * q->K, buf.data(), nc);
         memcpy(sc32.data() + r0 * (q->K / 32), buf.data() + nc, ns * 4);
       } else {
-        pt.bits = dt == 6 ? 4 : 5;
+        const Part &pt = parts[(size_t)part_of[k]];
         const size_t pcb = pq_qlow_packed_codes_bytes((int)s.n0, (int)s.n1, pt.bits);
         const size_t psb = pq_qlow_packed_scales_bytes((int)s.n0, (int)s.n1, pt.bits);
         PQ_REQUIRE(pcb + psb == buf.size(), PQ_ERR_ARG, "pq_engine_load_blob: %s: %zu payload bytes, want %zu",
                    s.name.c_str(), buf.size(), pcb + psb);
-        PQ_TRY(E.dalloc(&pt.pc, pcb));
-        PQ_TRY(E.dalloc(&pt.ps, psb / 2));
-        if (hipMemcpyAsync(pt.pc, buf.data(), pcb, hipMemcpyHostToDevice, E.st) != hipSuccess ||
-            hipMemcpyAsync(pt.ps, buf.data() + pcb, psb, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+        // the source's tiles follow those of the part's earlier sources
+        const size_t t0 = (r0 - (size_t)pt.r0) / 32;
+        const size_t ct = pq_qlow_packed_codes_bytes(32, q->K, pt.bits), st = pq_qlow_packed_scales_bytes(32, q->K, pt.bits);
+        if (hipMemcpyAsync(pt.pc + t0 * ct, buf.data(), pcb, hipMemcpyHostToDevice, E.st) != hipSuccess ||
+            hipMemcpyAsync(reinterpret_cast<char *>(pt.ps) + t0 * st, buf.data() + pcb, psb, hipMemcpyHostToDevice,
+                           E.st) != hipSuccess ||
             hipStreamSynchronize(E.st) != hipSuccess)
           return fail(PQ_ERR_LAUNCH, "low-bit upload failed");
-        low = true;
-        E.qlow_ws_bytes = std::max(E.qlow_ws_bytes, pq_qlow_workspace_bytes(pt.n, (int)s.n1, pt.bits));
       }
-      parts.push_back(pt);
       r0 += (size_t)s.n0;
     }
     if (low) q->parts = std::move(parts);
@@ -1429,10 +1453,20 @@ extern "C" size_t pq_engine_weight_bytes(void *h) {
   Engine &E = *static_cast<Engine *>(h);
   size_t b = 0;
   const size_t sb = ref_numerics(E) ? 4 : 2;   // fp32 or fp16 scale per 32
-  auto q8 = [&](const Q8Dev &q) { b += (size_t)q.N * q.K + (size_t)q.N * (q.K / 32) * sb; };
+  // the bytes a decode step reads: each part's own (a low-bit part its packed
+  // payload), the bf16 table at 2 bytes per weight
+  auto rows = [&](int n, int K, int bits) {
+    if (bits == 8) return (size_t)n * K + (size_t)n * (K / 32) * sb;
+    return pq_qlow_packed_codes_bytes(n, K, bits) + pq_qlow_packed_scales_bytes(n, K, bits);
+  };
+  auto q8 = [&](const Q8Dev &q) {
+    if (!q.split()) b += rows(q.N, q.K, 8);
+    for (const Part &pt : q.parts) b += rows(pt.n, q.K, pt.bits);
+  };
   for (const LayerDev &D : E.L) {
     q8(D.in); q8(D.out); q8(D.ug); q8(D.down);
   }
-  q8(E.emb);
+  if (E.emb_bf16) b += (size_t)E.c.vocab * E.c.hidden * 2;
+  else q8(E.emb);
   return b;
 }
