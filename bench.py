@@ -56,6 +56,25 @@ def measured_traffic():
     return int(float(m.group(1)) * 1e6) if m else None
 
 
+def profile_traffic(fname):
+    """Measured HBM bytes per launch from a counter summary under profiles/
+    (tables `| shape | kernel | grid | algorithmic MB | FETCH_SIZE KiB |
+    WRITE_SIZE KiB | measured HBM MB | ratio |`, one per `## ` section):
+    {section: {shape: bytes}} ({} if the file is absent)."""
+    import re
+    path = os.path.join(ROOT, "profiles", fname)
+    if not os.path.exists(path):
+        return {}
+    out, sec = {}, ""
+    for line in open(path):
+        if line.startswith("## "):
+            sec = line[3:].strip()
+        m = re.match(r"\| ([^|`]+) \| `[^`]+` \| \d+ \| [0-9.]+ \| [0-9.]+ \| [0-9.]+ \| ([0-9.]+) \| [0-9.]+ \|", line)
+        if m:
+            out.setdefault(sec, {})[m.group(1).strip()] = int(float(m.group(2)) * 1e6)
+    return out
+
+
 def graph_of(torch, fn):
     """fn's launches (on torch's current stream) captured into one HIP graph,
     after one eager run on a side stream: the timed regions replay graphs so the
@@ -682,7 +701,13 @@ def qlow_bench(pq, torch, dev, g, stream, reps=20):
         del pools
         torch.cuda.empty_cache()
         floor = read_floor(pq, torch, dev, stream, [(s[0], nb[s[0]]) for s in shapes])
+        tr = profile_traffic("qlow_gemv_counters.md").get(f"Q{bits}", {})
+        traffic = {s_[0]: tr.get(s_[0].replace("gate_up", "gate+up")) for s_ in shapes}
         res[f"q{bits}"] = {"us_per_step": round(ms * 1e3, 2), "bytes_per_step": nbytes,
+                           "traffic": {"per_shape": traffic,
+                                       "per_step": sum(traffic.values()) if all(traffic.values()) else None,
+                                       "source": "profiles/qlow_gemv_counters.md (HBM bytes per launch, rocprofv3 "
+                                                 "FETCH_SIZE / WRITE_SIZE scaled by the calibration kernel)"},
                            "stream_read_floor": {"per_shape": floor,
                                                  "step_us": round(sum(v["us"] for v in floor.values()), 2)},
                            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -749,7 +774,13 @@ def ternary_bench(pq, torch, dev, g, stream, reps=20):
     del pools
     torch.cuda.empty_cache()
     floor = read_floor(pq, torch, dev, stream, [(n, nb[n]) for (n, N, K) in shapes])
+    tr = profile_traffic("ternary_gemv_counters.md").get("", {})
+    traffic = {n: tr.get(n) for (n, N, K) in shapes}
     return {"shapes": [f"{n}:{N}x{K}" for (n, N, K) in shapes], "us_per_step": round(ms * 1e3, 2),
+            "traffic": {"per_shape": traffic, "per_step": sum(traffic.values()) if all(traffic.values()) else None,
+                        "batched_gate_up": tr.get("gate+up batched"),
+                        "source": "profiles/ternary_gemv_counters.md (HBM bytes per launch, rocprofv3 FETCH_SIZE / "
+                                  "WRITE_SIZE scaled by the calibration kernel)"},
             "stream_read_floor": {"per_shape": floor, "step_us": round(sum(v["us"] for v in floor.values()), 2)},
             "bytes_per_step": step_bytes, "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -758,6 +789,54 @@ def ternary_bench(pq, torch, dev, g, stream, reps=20):
             "batched_gate_up": {"us_per_step": round(ms_b * 1e3, 2), "gate_up_launch_us": round(gu_us, 2),
                                 "GB/s": round(step_bytes / (ms_b * 1e-3) / 1e9, 1),
                                 "hbm_frac": round(step_bytes / (ms_b * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+
+
+def gemv_profile_workload(pq, torch, dev, which, copies=3):
+    """Eager launches for counter runs (rocprofv3 --pmc): each shape of the
+    ternary FFN (gate, up, down, then the batched gate+up launch) or of the
+    Q4 / Q5 layer GEMVs (q|k|v, o_proj, gate+up, down) `copies` times, each
+    launch on its own weight copy so no launch finds its weights in a cache
+    the one before filled. Prints each shape's algorithmic bytes."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    out = {}
+    if which == "ternary":
+        shapes = [("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+        xs = {K: pq.q8k_quant(torch.randn(K, device=dev, generator=g)) for K in (4096, 12288)}
+        w = {name: [(ternary_codes(torch, N, K, dev, g),
+                     (torch.randn((N, K // 128), device=dev, generator=g).abs() * 0.01).half().view(torch.int16))
+                    for _ in range(copies)] for (name, N, K) in shapes}
+        ys = {name: torch.empty(N, dtype=torch.float32, device=dev) for (name, N, K) in shapes}
+        for (name, N, K) in shapes:
+            for c in range(copies):
+                pq.tq2_gemv(w[name][c][0], w[name][c][1], xs[K], K, N, out=ys[name])
+            torch.cuda.synchronize()
+            out[name] = N * K // 4 + N * K // 128 * 2 + K // 256 * 292 + N * 4
+        for c in range(copies):   # the batched gate+up launch, on copies not used above in this order
+            pq.tq2_gemv_batch([w["gate"][(c + 1) % copies], w["up"][(c + 2) % copies]], xs[4096], 4096,
+                              outs=[ys["gate"], ys["up"]])
+        torch.cuda.synchronize()
+        out["gate_up_batched"] = out["gate"] + out["up"] - 4096 // 256 * 292
+    else:
+        bits = 4 if which == "q4" else 5
+        xs = {K: torch.randn(K, device=dev, generator=g).to(torch.bfloat16) for K in (2048, 8192)}
+        for (name, N, K, _) in [s_ for s_ in SHAPES if s_[0] != "lm_head"]:
+            ws = []
+            for _ in range(copies):
+                qc = torch.randint(0, 2 ** bits, (N, K), dtype=torch.uint8, device=dev, generator=g)
+                sc = torch.randn((N, K // 32, 2), device=dev, generator=g).abs().mul(0.01).half().view(torch.int16)
+                ws.append(pq.QlowWeight(qc, sc, bits))
+                del qc, sc
+            torch.cuda.synchronize()
+            y = torch.empty(N, dtype=torch.bfloat16, device=dev)
+            for c in range(copies):
+                pq.qlow_gemv(ws[c], xs[K], out=y)
+            torch.cuda.synchronize()
+            out[name] = (pq.lib().pq_qlow_packed_codes_bytes(N, K, bits) + pq.lib().pq_qlow_packed_scales_bytes(N, K, bits)
+                         + 2 * K + 2 * N)
+            del ws
+            torch.cuda.empty_cache()
+    print(json.dumps({"gemv_profile": which, "algorithmic_bytes": out}), flush=True)
 
 
 def main():
@@ -771,6 +850,9 @@ def main():
                     help="also run a plain elementwise kernel over 256 MiB (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--prefill-profile", action="store_true",
                     help="only run the prefill GEMMs (3 launches each at T=512 and T=32) for counter runs; no JSON")
+    ap.add_argument("--gemv-profile", choices=["ternary", "q4", "q5"],
+                    help="only run eager launches of the ternary FFN GEMVs or the Q4 / Q5 layer GEMVs (3 weight "
+                         "copies per shape) for counter runs; prints their algorithmic bytes")
     ap.add_argument("--decode-profile", choices=["synth", "real", "synth-ref", "real-ref", "synth-q4"],
                     help="only run one backbone's decode measurement (the synthetic or the real LFM3 shapes, "
                          "-ref: the reference's GEMV numerics, -q4: Q4 linears from a blob) for kernel traces; "
@@ -787,6 +869,15 @@ def main():
     dev = torch.device("cuda:0")
     if args.prefill_profile:
         prefill_profile_workload(pq, torch, dev)
+        return
+    if args.gemv_profile:
+        if args.calib:   # the counter calibration of the traffic runs: 256 MiB read + 256 MiB written
+            src = torch.randn(64 << 20, device=dev)
+            dst = torch.empty_like(src)
+            torch.neg(src, out=dst)
+            torch.cuda.synchronize()
+            del src, dst
+        gemv_profile_workload(pq, torch, dev, args.gemv_profile)
         return
     if args.decode_profile:
         if args.calib:   # the counter calibration of the traffic runs: 256 MiB read + 256 MiB written

@@ -21,10 +21,12 @@
 // slice, slot j takes groups j, j + NT/RS, ... (a slot's
 // lanes read 16*RS contiguous bytes of the tile-group, whole 128-byte lines),
 // and computes acc - sg into LDS; then one lane per (row, slice of K) runs
-// that slice's fmaf chain, and the K slices add in order. The slices of a tile
-// run on one XCD (workgroups go round-robin over the 8 XCDs), so the tile's
-// scale and bit-4 plane lines, which all of them read, are fetched into one
-// L2. The code bytes become floats by one byte permute each.
+// that slice's fmaf chain, and the K slices add in order (through lane reads
+// when all chain lanes are wave 0's). The slices of a tile run on one XCD
+// (workgroups go round-robin over the 8 XCDs), so the tile's scale and bit-4
+// plane lines, which all of them read, are fetched into one L2. Two codes
+// become two fp16 values 1 + q/128 by one byte permute, which the FMA widens
+// exactly (v_fma_mix_f32).
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
@@ -35,11 +37,20 @@ namespace pq {
 __host__ __device__ inline int qlow_ks(int K) { return K >= 4096 ? 4 : 2; }
 __host__ __device__ inline int qlow_gw(int B) { return B == 4 ? 32 : 40; }   // 16-byte units per tile-group
 
-// The code q (< 128) as the float 1 + q/128: bits 0x3F800000 | q << 16. mm
-// holds four codes, one per byte, each with 0x80 (the mantissa's top bit of
-// 1.0's byte 2) or'ed in; one byte permute builds [0x3F, 0x80 | q, 0, 0].
-__device__ __forceinline__ float qlow_f(uint32_t mm, int b) {
-  return __uint_as_float(__builtin_amdgcn_perm(mm, 0x3F3F3F3Fu, ((uint32_t)(4 + b) << 16) | 0x0C0Cu));
+// LDS row stride (floats) of the per-row partials and scale pairs: rows
+// 64/RS banks apart (16-byte aligned: 4 for RS >= 16), so the 64/RS group
+// slots of a wave, which store to adjacent columns of RS rows at once, and the
+// scale stores hit 64 distinct banks.
+__host__ __device__ inline int qlow_gp(int G, int RS) { return (G + 63) / 64 * 64 + (RS == 8 ? 8 : 4); }
+
+// The code q (< 128) as the fp16 1 + q/128, bits 0x3C00 | q << 3: mq holds
+// four codes at bits 3-6 (and 7) of its bytes; one byte permute interleaves
+// bytes 2j and 2j + 1 with 0x3C into two such halves. An FMA with an fp16
+// operand (v_fma_mix_f32) widens it exactly, so fmaf(1 + q/128, x, a) is the
+// fp32 fmaf of the code's float.
+typedef _Float16 qh2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ qh2 qlow_h2(uint32_t mq, int j) {
+  return __builtin_bit_cast(qh2, __builtin_amdgcn_perm(0x3C3C3C3Cu, mq, j ? 0x04030402u : 0x04010400u));
 }
 
 template <int B>
@@ -50,17 +61,18 @@ __device__ __forceinline__ float qlow_acc(v4i w4, uint32_t hp, const float *__re
   for (int i = 0; i < 4; i++) {
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
-      uint32_t m = ((hf ? (w[i] >> 4) : w[i]) & 0x0F0F0F0Fu) | 0x80808080u;
-      if constexpr (B == 5) {   // bit 4 of quad p's four codes from the plane's bits p, 8+p, 16+p, 24+p
+      // quad p = 2i + hf: codes of weights 8i + 4hf + b (b = 0..3) at bits 3-6 of byte b
+      uint32_t m = (hf ? (w[i] >> 1) : (w[i] << 3)) & 0x78787878u;
+      if constexpr (B == 5) {   // bit 4 of quad p's codes: the plane's bits 8b + p, to bit 7 of byte b
         const int p = 2 * i + hf;
-        const uint32_t hs = p <= 4 ? (hp << (4 - p)) : (hp >> (p - 4));
-        m |= hs & 0x10101010u;
+        m |= (hp << (7 - p)) & 0x80808080u;
       }
       const float4 xv = *reinterpret_cast<const float4 *>(xg + 8 * i + 4 * hf);
-      a0 = __builtin_fmaf(qlow_f(m, 0), xv.x, a0);
-      a1 = __builtin_fmaf(qlow_f(m, 1), xv.y, a1);
-      a2 = __builtin_fmaf(qlow_f(m, 2), xv.z, a2);
-      a3 = __builtin_fmaf(qlow_f(m, 3), xv.w, a3);
+      const qh2 q01 = qlow_h2(m, 0), q23 = qlow_h2(m, 1);
+      a0 = __builtin_fmaf((float)q01.x, xv.x, a0);
+      a1 = __builtin_fmaf((float)q01.y, xv.y, a1);
+      a2 = __builtin_fmaf((float)q23.x, xv.z, a2);
+      a3 = __builtin_fmaf((float)q23.y, xv.w, a3);
     }
   }
   return (a0 + a1) + (a2 + a3);
@@ -71,6 +83,75 @@ __device__ __forceinline__ float qlow_acc(v4i w4, uint32_t hp, const float *__re
 __device__ __forceinline__ float qlow_step(float y, float u, float sg, uint32_t sc) {
   const float dp = h2f((uint16_t)(sc & 0xffffu)), mn = h2f((uint16_t)(sc >> 16));
   return __builtin_fmaf(dp, u, __builtin_fmaf(mn, sg, y));
+}
+
+// A slice's chain from 0 over its GL groups in order: per group the partial
+// up[g] = acc - sg, the scale pair cp[g] and the group sum sp[g] (16-byte
+// aligned LDS). With GL a multiple of 16 the operands come in blocks of 8
+// groups held in two register sets, each block's reads issued 8 steps before
+// its first use (the chain's two dependent FMAs per step then never wait on
+// LDS); otherwise two groups per read, one read ahead.
+__device__ __forceinline__ float qlow_chain(const float *__restrict__ up, const uint32_t *__restrict__ cp,
+                                            const float *__restrict__ sp, int GL) {
+  float yv = 0.0f;
+  if (GL % 16 == 0) {
+    struct Blk {
+      float4 u0, u1, s0, s1;
+      uint4 c0, c1;
+    };
+    auto ld = [&](Blk &k, int i) {
+      k.u0 = *reinterpret_cast<const float4 *>(up + 8 * i);
+      k.u1 = *reinterpret_cast<const float4 *>(up + 8 * i + 4);
+      k.s0 = *reinterpret_cast<const float4 *>(sp + 8 * i);
+      k.s1 = *reinterpret_cast<const float4 *>(sp + 8 * i + 4);
+      k.c0 = *reinterpret_cast<const uint4 *>(cp + 8 * i);
+      k.c1 = *reinterpret_cast<const uint4 *>(cp + 8 * i + 4);
+    };
+    auto run = [&](const Blk &k) {
+      yv = qlow_step(yv, k.u0.x, k.s0.x, k.c0.x);
+      yv = qlow_step(yv, k.u0.y, k.s0.y, k.c0.y);
+      yv = qlow_step(yv, k.u0.z, k.s0.z, k.c0.z);
+      yv = qlow_step(yv, k.u0.w, k.s0.w, k.c0.w);
+      yv = qlow_step(yv, k.u1.x, k.s1.x, k.c1.x);
+      yv = qlow_step(yv, k.u1.y, k.s1.y, k.c1.y);
+      yv = qlow_step(yv, k.u1.z, k.s1.z, k.c1.z);
+      yv = qlow_step(yv, k.u1.w, k.s1.w, k.c1.w);
+    };
+    // The empty asm statements with a memory clobber pin each block's reads
+    // where they stand: without them the compiler turns a register set
+    // carried round the loop into reads at the top of the next iteration,
+    // right before their use.
+    const int n = GL / 8;   // even
+    Blk A, B;
+    ld(A, 0);
+    ld(B, 1);
+    asm volatile("" ::: "memory");
+    for (int i = 0; i < n; i += 2) {
+      // the reads past the slice's last block repeat it (unconditional reads
+      // keep the LDS wait counts exact)
+      run(A);
+      ld(A, i + 2 < n ? i + 2 : n - 2);
+      asm volatile("" ::: "memory");
+      run(B);
+      ld(B, i + 3 < n ? i + 3 : n - 1);
+      asm volatile("" ::: "memory");
+    }
+    return yv;
+  }
+  const int n = GL / 2;   // G is a multiple of 8 and KS of 2 or 4: GL is even
+  float2 uq = *reinterpret_cast<const float2 *>(up), sq = *reinterpret_cast<const float2 *>(sp);
+  uint2 cq = *reinterpret_cast<const uint2 *>(cp);
+  for (int it = 0; it < n; it++) {
+    const int nx = (it + 1 < n ? it + 1 : it) * 2;
+    const float2 un = *reinterpret_cast<const float2 *>(up + nx), sn = *reinterpret_cast<const float2 *>(sp + nx);
+    const uint2 cn = *reinterpret_cast<const uint2 *>(cp + nx);
+    yv = qlow_step(yv, uq.x, sq.x, cq.x);
+    yv = qlow_step(yv, uq.y, sq.y, cq.y);
+    uq = un;
+    sq = sn;
+    cq = cn;
+  }
+  return yv;
 }
 
 // Workgroup b -> (tile, RS-row slice of it): with a multiple of 8 tiles, the
@@ -99,10 +180,9 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   const int GA = K / kQ, KSA = qlow_ks(K), GW = qlow_gw(B);
   // the groups this workgroup covers: [gb, gb + G), in KS slices of GL
   const int KS = ws ? 1 : KSA, G = ws ? GA / KSA : GA, GL = G / KS, gb = ws ? (int)blockIdx.y * G : 0;
-  // per row, the groups' partials and scale pairs at a padded stride GP
-  // (16-byte aligned rows, rows 4 banks apart)
+  // per row, the groups' partials and scale pairs at the padded stride GP
   constexpr int kLoSlots = NT / RS;   // group slots per round (NT threads: NT/RS slots of RS rows)
-  const int GP = G + 4;
+  const int GP = qlow_gp(G, RS);
   float *xs = lsm;                      // [G*32]
   float *sx = xs + G * kQ;              // [G]
   float *u = sx + G;                    // [8 rows][GP]: acc - sg
@@ -124,7 +204,8 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   // x (8 bf16 per 16-byte load, XL loads per thread: K <= 2048 XL), this
   // lane's first PF groups' codes, then the slice's scale pairs (4 rows per
   // 16-byte load, up to kScl loads per thread; any more come after the
-  // partials).
+  // partials). Codes and scales load nontemporal (read once per launch; the
+  // scale lines a tile's slices share are read close together in time).
   constexpr int kXLoads = XL, kScl = 4;
   constexpr int HQ = RS / 4;
   const __amdgpu_buffer_rsrc_t rx =
@@ -151,7 +232,7 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   for (int k = 0; k < kScl; k++) {
     const int i = tid + k * NT;
     sr[k] = __builtin_amdgcn_raw_buffer_load_b128(
-        rsc, i < G * HQ ? ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4 : kRsrcOob, 0, 0);
+        rsc, i < G * HQ ? ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4 : kRsrcOob, 0, kAuxNT);
   }
   // x widened into LDS, and each group's sum of x in order from 0: a group's
   // 32 elements are the 8-element pieces of 4 adjacent lanes (K is a multiple
@@ -221,54 +302,39 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   for (int k = 0; k < kScl; k++)
     if (tid + k * NT < G * HQ) put_scales(tid + k * NT, sr[k]);
   for (int i = tid + kScl * NT; i < G * HQ; i += NT)
-    put_scales(i, __builtin_amdgcn_raw_buffer_load_b128(rsc, ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4, 0, 0));
+    put_scales(i, __builtin_amdgcn_raw_buffer_load_b128(rsc, ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4, 0,
+                                                        kAuxNT));
   __syncthreads();
-  // per (row, K slice): the slice's chain over its groups in order. Its LDS
-  // operands come 4 groups per 16-byte read (2 where the slice length is not
-  // a multiple of 4), the next reads issued before the current steps.
+  // per (row, K slice): the slice's chain over its groups in order, one lane
+  // each. With at most 64 such lanes (every shape but 32-row slices of K >=
+  // 4096) they are wave 0's, and the slices add in order through lane reads:
+  // no barrier and no LDS pass
+  const int row = tile * 32 + sub * RS + tid % RS;
+  if (RS * KS <= 64) {
+    if (tid >= 64) return;
+    float yv = 0.0f;
+    if (tid < RS * KS) {
+      const int s = tid / RS, rr = tid % RS;
+      yv = qlow_chain(u + rr * GP + s * GL, scl + rr * GP + s * GL, sx + s * GL, GL);
+    }
+    if (ws) {   // one K slice per workgroup
+      if (tid < RS && row < N) ws[(size_t)blockIdx.y * N + row] = yv;
+      return;
+    }
+    float yt = 0.0f;
+    for (int s = 0; s < KS; s++) yt = yt + __shfl(yv, s * RS + tid % RS, 64);
+    if (tid < RS && row < N) {
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yt);
+      else reinterpret_cast<float *>(y)[row] = yt;
+    }
+    return;
+  }
   if (tid < RS * KS) {
     const int s = tid / RS, rr = tid % RS;
-    const int gs = s * GL;
-    const float *up = u + rr * GP + gs;
-    const uint32_t *cp = scl + rr * GP + gs;
-    const float *sp = sx + gs;
-    float yv = 0.0f;
-    if (GL % 4 == 0) {
-      const int n = GL / 4;
-      float4 uq = *reinterpret_cast<const float4 *>(up), sq = *reinterpret_cast<const float4 *>(sp);
-      uint4 cq = *reinterpret_cast<const uint4 *>(cp);
-      for (int it = 0; it < n; it++) {
-        const int nx = (it + 1 < n ? it + 1 : it) * 4;
-        const float4 un = *reinterpret_cast<const float4 *>(up + nx), sn = *reinterpret_cast<const float4 *>(sp + nx);
-        const uint4 cn = *reinterpret_cast<const uint4 *>(cp + nx);
-        yv = qlow_step(yv, uq.x, sq.x, cq.x);
-        yv = qlow_step(yv, uq.y, sq.y, cq.y);
-        yv = qlow_step(yv, uq.z, sq.z, cq.z);
-        yv = qlow_step(yv, uq.w, sq.w, cq.w);
-        uq = un;
-        sq = sn;
-        cq = cn;
-      }
-    } else {
-      const int n = GL / 2;   // G is a multiple of 8 and KS of 2 or 4: GL is even
-      float2 uq = *reinterpret_cast<const float2 *>(up), sq = *reinterpret_cast<const float2 *>(sp);
-      uint2 cq = *reinterpret_cast<const uint2 *>(cp);
-      for (int it = 0; it < n; it++) {
-        const int nx = (it + 1 < n ? it + 1 : it) * 2;
-        const float2 un = *reinterpret_cast<const float2 *>(up + nx), sn = *reinterpret_cast<const float2 *>(sp + nx);
-        const uint2 cn = *reinterpret_cast<const uint2 *>(cp + nx);
-        yv = qlow_step(yv, uq.x, sq.x, cq.x);
-        yv = qlow_step(yv, uq.y, sq.y, cq.y);
-        uq = un;
-        sq = sn;
-        cq = cn;
-      }
-    }
-    ys[s * RS + rr] = yv;
+    ys[s * RS + rr] = qlow_chain(u + rr * GP + s * GL, scl + rr * GP + s * GL, sx + s * GL, GL);
   }
   __syncthreads();
   if (tid < RS) {
-    const int row = tile * 32 + sub * RS + tid;
     if (ws) {
       if (row < N) ws[(size_t)blockIdx.y * N + row] = ys[tid];
       return;
@@ -382,7 +448,7 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   const int KS = qlow_ks(K);
   const int RS = qlow_rows(N);
   auto lds_of = [&](int G, int ks) {
-    return ((size_t)G * kQ + G + 2 * RS * (size_t)(G + 4) + (size_t)ks * RS) * sizeof(float);
+    return ((size_t)G * kQ + G + 2 * RS * (size_t)qlow_gp(G, RS) + (size_t)ks * RS) * sizeof(float);
   };
   // the split form (one workgroup per (8 rows, K slice), then the ordered
   // combine): for long rows on too few row slices to fill the chip, or when
