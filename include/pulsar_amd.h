@@ -381,6 +381,15 @@ int pq_q8r_gemv_parts(int N);
  * (3739-3856) in one launch, the same bits. F a multiple of 4. */
 int pq_q8r_gemv_fused_swiglu(const int8_t *codes, const float *scales, const pq_gemv_prologue *pro,
                              uint16_t *y, int F, int K, void *stream);
+/* The Q4 / Q5 GEMV (pq_qlow_gemv's payload and order) at T = 1 with x from a
+ * prologue: RESNORM, NORM, SILU or CONV (3 or 7 taps, K <= 4096), computed
+ * as the kinds above and handed to the GEMV as the bf16 values the unfused op
+ * would store. K is 2048, 4096 or 8192 (whole rows per workgroup, no K split);
+ * y bf16 or fp32. Replaces the rmsnorm_body / k_silu_mul_bf / k_conv7 +
+ * qlow_gemv pairs of layer_body (lfm3_nanode.cu:3739-3856, qlow_gemv
+ * 1894-1915) for a low-bit source tensor. */
+int pq_qlow_gemv_fused(const uint8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro, void *y,
+                       int y_dtype, int N, int K, int bits, void *stream);
 /* The FFN's gate/up GEMV (weights from pq_q8_pack_gate_up, N = 2F) with the
  * prologue pro and silu(gate) * up as its epilogue: writes the Q8_0 row
  * (qx [F], dx [F/32]) that the down projection reads (PQ_PRO_Q8) -- the

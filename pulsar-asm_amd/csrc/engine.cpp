@@ -782,6 +782,27 @@ static int forward_decode(Engine &E, bool dev) {
 // pq_silu_mul: the same values), and a bf16 table takes the row copy and
 // pq_bf16_gemv. The position and id slot as in forward_decode (dev: on the
 // device, so the step can be captured and replayed).
+// Whether a split slot's parts take a prologue (pq_qlow_gemv_fused for the
+// low-bit parts, pq_q8r_gemv_fused for the Q8 ones): K of 2048, 4096 or 8192,
+// K <= 4096 for CONV.
+static bool parts_fusable(const Q8Dev &w, int kind) {
+  return (w.K == 2048 || w.K == 4096 || w.K == 8192) && (kind != PQ_PRO_CONV || w.K <= 4096);
+}
+
+// A split slot's GEMVs at T = 1 with the prologue pro, each part writing its
+// rows of y (bf16). Every launch runs the prologue; the vectors it writes once
+// (x_out, ring_out) get the same values from each, from unchanged inputs.
+static int parts_fused(Engine &E, const Q8Dev &w, const pq_gemv_prologue &pro, uint16_t *y) {
+  for (const Part &p : w.parts) {
+    if (p.bits == 8)
+      PQ_TRY(pq_q8r_gemv_fused(w.pc + (size_t)p.r0 * w.K, w.sf + (size_t)p.r0 * (w.K / 32), &pro, y + p.r0,
+                               PQ_DTYPE_BF16, p.n, w.K, nullptr, E.st));
+    else
+      PQ_TRY(pq_qlow_gemv_fused(p.pc, p.ps, &pro, y + p.r0, PQ_DTYPE_BF16, p.n, w.K, p.bits, E.st));
+  }
+  return PQ_OK;
+}
+
 static int forward_decode_r2(Engine &E, bool dev) {
   const pq_model_cfg &c = E.c;
   const int H = c.hidden;
@@ -837,6 +858,9 @@ static int forward_decode_r2(Engine &E, bool dev) {
       p.w0 = D.op_norm;
       p.eps = c.eps;
       PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
+    } else if (D.in.split() && parts_fusable(D.in, PQ_PRO_RESNORM)) {
+      resnorm(E.L[l - 1].post_ffn_norm, D.op_norm);
+      PQ_TRY(parts_fused(E, D.in, p, E.Wd));
     } else if (D.in.split()) {
       PQ_TRY(resnorm_to(E.L[l - 1].post_ffn_norm, D.op_norm, E.A));
       PQ_TRY(plain(D.in, E.A, E.Wd));
@@ -868,6 +892,16 @@ static int forward_decode_r2(Engine &E, bool dev) {
                                 E.st));
       }
       PQ_TRY(plain(D.out, E.A, E.Hb));
+    } else if (D.out.split() && parts_fusable(D.out, PQ_PRO_CONV)) {
+      p = pq_gemv_prologue{};
+      p.kind = PQ_PRO_CONV;
+      p.bcx = E.Wd;
+      p.ring_in = D.rings[D.rc];
+      p.ring_out = D.rings[1 - D.rc];
+      p.taps = D.taps;
+      p.ntaps = c.ntaps;
+      D.rc = 1 - D.rc;
+      PQ_TRY(parts_fused(E, D.out, p, E.Hb));
     } else if (D.out.split()) {
       // the ring ping-pong as the CONV prologue keeps it: the shifted ring goes
       // to the other buffer (a copy, then the conv updates it in place)
@@ -887,6 +921,19 @@ static int forward_decode_r2(Engine &E, bool dev) {
       p.ntaps = c.ntaps;
       D.rc = 1 - D.rc;
       PQ_TRY(gemv(D.out, E.Hb, PQ_DTYPE_BF16, nullptr));
+    }
+    // a split gate/up slot: its parts with the RESNORM prologue write the
+    // [gate | up] rows, and down takes silu(gate) * up as its SILU prologue
+    const bool down_silu = D.down.split() ? parts_fusable(D.down, PQ_PRO_SILU) : pow2_range(D.down.K);
+    if (D.ug.split() && parts_fusable(D.ug, PQ_PRO_RESNORM) && down_silu) {
+      resnorm(D.post_op_norm, D.ffn_norm);
+      PQ_TRY(parts_fused(E, D.ug, p, E.Wd));                        // [gate | up] rows
+      p = pq_gemv_prologue{};
+      p.kind = PQ_PRO_SILU;
+      p.gu = E.Wd;
+      if (D.down.split()) PQ_TRY(parts_fused(E, D.down, p, E.Hb));
+      else PQ_TRY(gemv(D.down, E.Hb, PQ_DTYPE_BF16, nullptr));
+      continue;
     }
     if (D.ug.split()) {
       PQ_TRY(resnorm_to(D.post_op_norm, D.ffn_norm, E.A));

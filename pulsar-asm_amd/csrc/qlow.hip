@@ -30,6 +30,7 @@
 #include "pq_device.h"
 #include "pq_host.h"
 #include "q8_common.h"
+#include "pq_prologue.h"
 
 namespace pq {
 
@@ -171,12 +172,23 @@ __device__ __forceinline__ void qlow_place(int b, int ntiles, int &tile, int &su
 // With ws (the split form): workgroup (slice of rows, s) covers only K slice
 // s = blockIdx.y and writes its y_s to ws[s][N]; qlow_combine_kernel adds the
 // slices in order. Without ws: all K slices in one workgroup.
-template <int B, int RS, int XL, int NT, int PF>
+//
+// PRO: x is the bf16 vector x (kProPlain), or comes from a fused prologue
+// (pq_prologue.h: RESNORM, NORM, SILU, CONV; whole rows only, K = NT * E):
+// thread t computes elements tE .. tE + E - 1 as the bf16 values the unfused
+// op would store, which the staging below then widens and sums exactly as it
+// does x.
+constexpr int kProPlain = -1;
+
+template <int B, int RS, int XL, int NT, int PF, int PRO = kProPlain, int E = 8>
 __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict__ pc,
                                                               const uint32_t *__restrict__ ps,
                                                               const uint16_t *__restrict__ x, void *__restrict__ y,
-                                                              int y_bf16, int N, int K, float *__restrict__ ws) {
+                                                              int y_bf16, int N, int K, float *__restrict__ ws,
+                                                              pq_gemv_prologue p) {
+  constexpr bool kPro = PRO != kProPlain;
   extern __shared__ __align__(16) float lsm[];
+  __shared__ float red[16];   // the prologue's workgroup reductions
   const int GA = K / kQ, KSA = qlow_ks(K), GW = qlow_gw(B);
   // the groups this workgroup covers: [gb, gb + G), in KS slices of GL
   const int KS = ws ? 1 : KSA, G = ws ? GA / KSA : GA, GL = G / KS, gb = ws ? (int)blockIdx.y * G : 0;
@@ -206,16 +218,21 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   // 16-byte load, up to kScl loads per thread; any more come after the
   // partials). Codes and scales load nontemporal (read once per launch; the
   // scale lines a tile's slices share are read close together in time).
-  constexpr int kXLoads = XL, kScl = 4;
+  constexpr int kXLoads = kPro ? 1 : XL, kScl = 4;
   constexpr int HQ = RS / 4;
-  const __amdgpu_buffer_rsrc_t rx =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, K * 2, kRsrcWord3);
   uint4 xr[kXLoads];
+  ProRegs<E, conv_taps(PRO)> pr;
+  if constexpr (kPro) {
+    pro_load<PRO, E>(p, tid * E, K, pr);   // the prologue's global loads
+  } else {
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, K * 2, kRsrcWord3);
 #pragma unroll
-  for (int it = 0; it < kXLoads; it++) {
-    const int e = tid * 8 + it * NT * 8;
-    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, e < K ? e * 2 : kRsrcOob, 0, 0);
-    xr[it] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+    for (int it = 0; it < kXLoads; it++) {
+      const int e = tid * 8 + it * NT * 8;
+      const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rx, e < K ? e * 2 : kRsrcOob, 0, 0);
+      xr[it] = make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+    }
   }
   v4i w[PF];
   uint32_t hpl[PF];
@@ -237,9 +254,30 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   // x widened into LDS, and each group's sum of x in order from 0: a group's
   // 32 elements are the 8-element pieces of 4 adjacent lanes (K is a multiple
   // of 256), so lane j of the 4 continues the chain of lane j - 1 (a row shift
-  // by one lane) and the group's last lane holds the sum
+  // by one lane) and the group's last lane holds the sum. From a prologue: the
+  // E-element pieces of 32/E adjacent lanes, chained the same way.
+  if constexpr (kPro) {
+    float v[E];
+    pro_values<PRO, E>(p, tid * E, K, pr, red, v);
+    const int e0 = tid * E;
+    constexpr int LG = 32 / E;
 #pragma unroll
-  for (int it = 0; it < kXLoads; it++) {
+    for (int i = 0; i < E / 4; i++)
+      *reinterpret_cast<float4 *>(xs + e0 + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    float c = 0.0f;
+#pragma unroll
+    for (int k = 0; k < E; k++) c = c + v[k];
+#pragma unroll
+    for (int j = 1; j < LG; j++) {
+      float cj = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), kDppRowShr1, 0xf, 0xf, false));
+#pragma unroll
+      for (int k = 0; k < E; k++) cj = cj + v[k];
+      if ((tid & (LG - 1)) == j) c = cj;
+    }
+    if ((tid & (LG - 1)) == LG - 1) sx[e0 / kQ] = c;
+  }
+#pragma unroll
+  for (int it = 0; it < (kPro ? 0 : kXLoads); it++) {
     const int e = tid * 8 + it * NT * 8;
     const uint32_t vv[4] = {xr[it].x, xr[it].y, xr[it].z, xr[it].w};
     float f[8];
@@ -472,6 +510,7 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   float *wsf = split ? static_cast<float *>(ws) : nullptr;
   hipStream_t st = as_stream(stream);
   const uint32_t *ps32 = reinterpret_cast<const uint32_t *>(pscales);
+  const pq_gemv_prologue np0{};   // no prologue: x given
   // x loads per thread for the K one workgroup covers (NT threads x 8)
   const int xl = (G * kQ + 8 * NT - 1) / (8 * NT), XL = xl <= 1 ? 1 : xl <= 2 ? 2 : xl <= 4 ? 4 : 8;
   // PF groups of loads in flight per slot: 2 (the partials of one round overlap the next
@@ -481,9 +520,9 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   const int pf = env_pf == 1 || env_pf == 4 ? env_pf : 2;
 #define PQ_QLOW(BB, RR, XX, TT)                                                                            \
   do {                                                                                                     \
-    if (pf == 1) launch(qlow_gemv_kernel<BB, RR, XX, TT, 1>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf); \
-    else if (pf == 2) launch(qlow_gemv_kernel<BB, RR, XX, TT, 2>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf); \
-    else launch(qlow_gemv_kernel<BB, RR, XX, TT, 4>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf); \
+    if (pf == 1) launch(qlow_gemv_kernel<BB, RR, XX, TT, 1>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf, np0); \
+    else if (pf == 2) launch(qlow_gemv_kernel<BB, RR, XX, TT, 2>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf, np0); \
+    else launch(qlow_gemv_kernel<BB, RR, XX, TT, 4>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, wsf, np0); \
   } while (0)
 #define PQ_QLOW_X(BB, RR)                                  \
   if (NT == 512) {                                         \
@@ -515,4 +554,93 @@ extern "C" int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, c
   if (rc || !split) return rc;
   launch(qlow_combine_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, wsf, y, yb, N, KS);
   return check_launch("pq_qlow_gemv combine");
+}
+
+// The Q4 / Q5 GEMV with x from a prologue (RESNORM, NORM, SILU, CONV), whole
+// rows per workgroup (no K split): K = 512 * E for E = 4, 8 or 16, CONV with
+// K <= 4096.
+extern "C" int pq_qlow_gemv_fused(const uint8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
+                                  void *y, int y_dtype, int N, int K, int bits, void *stream) {
+  PQ_REQUIRE(pcodes && pscales && pro && y, PQ_ERR_ARG, "pq_qlow_gemv_fused: null pointer");
+  PQ_REQUIRE(qlow_shape(N, K, bits) && (K == 2048 || K == 4096 || K == 8192), PQ_ERR_ARG,
+             "pq_qlow_gemv_fused: N=%d K=%d bits=%d (N %% 32, K 2048, 4096 or 8192, bits 4 or 5)", N, K, bits);
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_qlow_gemv_fused: y_dtype %d",
+             y_dtype);
+  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 4), PQ_ERR_ALIGN,
+             "pq_qlow_gemv_fused: packed codes must be 16-byte aligned");
+  const pq_gemv_prologue &p = *pro;
+  switch (p.kind) {
+    case PQ_PRO_RESNORM:
+      PQ_REQUIRE(p.h && p.x_in && p.x_out && p.w0 && p.w1 && p.x_in != p.x_out, PQ_ERR_ARG,
+                 "pq_qlow_gemv_fused: RESNORM needs h, x_in, x_out (distinct), w0, w1");
+      PQ_REQUIRE(aligned(p.h, 16) && aligned(p.x_in, 16) && aligned(p.x_out, 16) && aligned(p.w0, 16) &&
+                     aligned(p.w1, 16),
+                 PQ_ERR_ALIGN, "pq_qlow_gemv_fused: RESNORM vectors must be 16-byte aligned");
+      break;
+    case PQ_PRO_NORM:
+      PQ_REQUIRE(p.x_in && p.w0, PQ_ERR_ARG, "pq_qlow_gemv_fused: NORM needs x_in, w0");
+      PQ_REQUIRE(aligned(p.x_in, 16) && aligned(p.w0, 16), PQ_ERR_ALIGN,
+                 "pq_qlow_gemv_fused: NORM vectors must be 16-byte aligned");
+      break;
+    case PQ_PRO_SILU:
+      PQ_REQUIRE(p.gu && aligned(p.gu, 16), PQ_ERR_ARG, "pq_qlow_gemv_fused: SILU needs a 16-byte aligned gu");
+      break;
+    case PQ_PRO_CONV:
+      PQ_REQUIRE(p.bcx && p.ring_in && p.ring_out && p.taps && p.ring_in != p.ring_out &&
+                     (p.ntaps == 3 || p.ntaps == 7) && K <= 4096,
+                 PQ_ERR_ARG, "pq_qlow_gemv_fused: CONV needs bcx, taps, distinct ring_in / ring_out, ntaps 3 or 7, "
+                             "K <= 4096");
+      PQ_REQUIRE(aligned(p.bcx, 16) && aligned(p.ring_in, 16) && aligned(p.ring_out, 16) && aligned(p.taps, 16),
+                 PQ_ERR_ALIGN, "pq_qlow_gemv_fused: CONV vectors must be 16-byte aligned");
+      break;
+    default:
+      return fail(PQ_ERR_ARG, "pq_qlow_gemv_fused: prologue kind %d (RESNORM, NORM, SILU or CONV)", p.kind);
+  }
+  const int RS = qlow_rows(N), G = K / kQ, KS = qlow_ks(K);
+  const size_t lds = ((size_t)G * kQ + G + 2 * RS * (size_t)qlow_gp(G, RS) + (size_t)KS * RS) * sizeof(float);
+  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_qlow_gemv_fused: K=%d exceeds the workgroup's LDS", K);
+  const dim3 grid((unsigned)(N / RS)), block(512);
+  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  hipStream_t st = as_stream(stream);
+  const uint32_t *ps32 = reinterpret_cast<const uint32_t *>(pscales);
+  const int kind = p.kind == PQ_PRO_CONV && p.ntaps == 7 ? kProConv7 : p.kind;
+  // one instantiation per (bits, rows per workgroup, prologue, E = K / 512)
+#define PQ_QLF(BB, RR, PP, EE) \
+  launch(qlow_gemv_kernel<BB, RR, 1, 512, 2, PP, EE>, grid, block, lds, st, pcodes, ps32, nullptr, y, yb, N, K, \
+         (float *)nullptr, p)
+#define PQ_QLF_E(BB, RR, PP)                  \
+  do {                                        \
+    if (K == 2048) PQ_QLF(BB, RR, PP, 4);     \
+    else if (K == 4096) PQ_QLF(BB, RR, PP, 8); \
+    else PQ_QLF(BB, RR, PP, 16);              \
+  } while (0)
+#define PQ_QLF_CONV(BB, RR, PP)               \
+  do {                                        \
+    if (K == 2048) PQ_QLF(BB, RR, PP, 4);     \
+    else PQ_QLF(BB, RR, PP, 8);               \
+  } while (0)
+#define PQ_QLF_P(BB, RR)                                                \
+  do {                                                                  \
+    switch (kind) {                                                     \
+      case PQ_PRO_RESNORM: PQ_QLF_E(BB, RR, PQ_PRO_RESNORM); break;     \
+      case PQ_PRO_NORM: PQ_QLF_E(BB, RR, PQ_PRO_NORM); break;           \
+      case PQ_PRO_SILU: PQ_QLF_E(BB, RR, PQ_PRO_SILU); break;           \
+      case kProConv7: PQ_QLF_CONV(BB, RR, kProConv7); break;            \
+      default: PQ_QLF_CONV(BB, RR, PQ_PRO_CONV); break;                 \
+    }                                                                   \
+  } while (0)
+  if (bits == 4) {
+    if (RS == 32) PQ_QLF_P(4, 32);
+    else if (RS == 16) PQ_QLF_P(4, 16);
+    else PQ_QLF_P(4, 8);
+  } else {
+    if (RS == 32) PQ_QLF_P(5, 32);
+    else if (RS == 16) PQ_QLF_P(5, 16);
+    else PQ_QLF_P(5, 8);
+  }
+#undef PQ_QLF_P
+#undef PQ_QLF_CONV
+#undef PQ_QLF_E
+#undef PQ_QLF
+  return check_launch("pq_qlow_gemv_fused");
 }

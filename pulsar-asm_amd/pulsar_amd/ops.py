@@ -8,7 +8,7 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "qlow_gemv_fused", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "tq2_gemv_batch", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "q8r_gemv_fused_swiglu", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
@@ -174,6 +174,18 @@ def qlow_gemv(w, x, out_dtype=DT_BF16, out=None, split=True, ws=None):
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     check(lib().pq_qlow_gemv_ws(w.pcodes.data_ptr(), w.pscales.data_ptr(), _bits16(x), out.data_ptr(), out_dtype,
                                 w.N, w.K, w.bits, _ptr(ws) if nbytes else None, nbytes, stream_ptr()), "pq_qlow_gemv")
+    return out
+
+
+def qlow_gemv_fused(w, kind, out_dtype=DT_BF16, out=None, eps=1e-5, **ptrs):
+    """The Q4/Q5 GEMV at T = 1 with x from a prologue (pq_qlow_gemv_fused):
+    kind RESNORM, NORM, SILU or CONV, ptrs as for gemv_fused."""
+    import ctypes as C
+    p = _prologue(kind, eps, ptrs)
+    if out is None:
+        out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=w.pcodes.device)
+    check(lib().pq_qlow_gemv_fused(w.pcodes.data_ptr(), w.pscales.data_ptr(), C.byref(p), out.data_ptr(), out_dtype,
+                                   w.N, w.K, w.bits, stream_ptr()), "pq_qlow_gemv_fused")
     return out
 
 

@@ -64,3 +64,80 @@ def test_qlow_rejects_bad_shapes(pq, dev):
     with pytest.raises(ValueError):
         pq.QlowWeight(torch.zeros((40, 256), dtype=torch.uint8, device=dev),
                       torch.zeros((40, 8, 2), dtype=torch.int16, device=dev), 4)
+
+
+# The Q4 / Q5 GEMV with x from a prologue equals the unfused op (pq_rmsnorm /
+# pq_silu_mul / pq_conv, each pinned to the oracle elsewhere) followed by
+# pq_qlow_gemv, bit for bit, with the vectors the prologue writes once (the
+# residual, the shifted conv ring) equal too. The shapes cover the three
+# per-thread widths (K = 2048, 4096, 8192) and the three rows-per-workgroup
+# slices (N = 16384, 3072, 2048).
+@pytest.mark.parametrize("kind,bits,N,K", [("resnorm", 4, 3072, 2048), ("resnorm", 5, 16384, 2048),
+                                           ("resnorm", 4, 2048, 8192), ("norm", 5, 2048, 2048),
+                                           ("norm", 4, 4096, 4096), ("silu", 4, 2048, 8192),
+                                           ("silu", 5, 3072, 4096), ("conv3", 4, 2048, 2048),
+                                           ("conv7", 5, 2048, 2048), ("conv3", 5, 1024, 4096),
+                                           ("conv7", 4, 3072, 4096)])
+def test_qlow_gemv_fused(orc, pq, dev, kind, bits, N, K):
+    print(f"qlow fused {kind} bits={bits} N={N} K={K}", flush=True)
+    Q, S, _ = _case(orc, N, K, bits, 31 * N + K + bits)
+    w = pq.QlowWeight(torch.from_numpy(Q).to(dev), torch.from_numpy(S.view(np.int16)).to(dev), bits)
+    g = torch.Generator(device=dev)
+    g.manual_seed(N + 3 * K + bits)
+    bf = lambda *shape, s=1.0: (torch.randn(shape, device=dev, generator=g) * s).to(torch.bfloat16)
+    out_dt = pq.DT_F32 if N == 16384 else pq.DT_BF16
+    if kind == "resnorm":
+        h, x = bf(K, s=30.0), bf(K, s=4.0)
+        w0, w1 = torch.rand(K, device=dev, generator=g) + 0.5, torch.rand(K, device=dev, generator=g) + 0.5
+        x1 = x.clone()
+        xin, _, _ = pq.rmsnorm(x1, w0, h=h, w1=w1)
+        want = pq.qlow_gemv(w, xin, out_dtype=out_dt)
+        xo = torch.empty(K, dtype=torch.int16, device=dev)
+        y = pq.qlow_gemv_fused(w, pq.PRO_RESNORM, out_dtype=out_dt, h=h.view(torch.int16), x_in=x.view(torch.int16),
+                               x_out=xo, w0=w0, w1=w1)
+        torch.cuda.synchronize()
+        assert torch.equal(xo, x1.view(torch.int16))
+    elif kind == "norm":
+        x = bf(K, s=3.0)
+        w0 = torch.rand(K, device=dev, generator=g) + 0.5
+        xin, _, _ = pq.rmsnorm(x.clone(), w0)
+        want = pq.qlow_gemv(w, xin, out_dtype=out_dt)
+        y = pq.qlow_gemv_fused(w, pq.PRO_NORM, out_dtype=out_dt, x_in=x.view(torch.int16), w0=w0)
+    elif kind == "silu":
+        gu = bf(2 * K, s=3.0)
+        xin, _, _ = pq.silu_mul(gu, K, 1)
+        want = pq.qlow_gemv(w, xin.reshape(K), out_dtype=out_dt)
+        y = pq.qlow_gemv_fused(w, pq.PRO_SILU, out_dtype=out_dt, gu=gu.view(torch.int16))
+    else:
+        nt = 7 if kind == "conv7" else 3
+        bcx, ring = bf(3 * K, s=2.0), bf(nt * K, s=2.0)
+        taps = torch.randn(K, nt, device=dev, generator=g) * 0.5
+        ring1 = ring.clone()
+        xin = torch.empty(K, dtype=torch.bfloat16, device=dev)
+        pq.conv(ring1, taps, bcx, xin, K, 1, nt)
+        want = pq.qlow_gemv(w, xin, out_dtype=out_dt)
+        ring_out = torch.empty_like(ring)
+        y = pq.qlow_gemv_fused(w, pq.PRO_CONV, out_dtype=out_dt, bcx=bcx.view(torch.int16),
+                               ring_in=ring.view(torch.int16), ring_out=ring_out.view(torch.int16), taps=taps,
+                               ntaps=nt)
+        torch.cuda.synchronize()
+        assert torch.equal(ring_out.view(torch.int16), ring1.view(torch.int16))
+    torch.cuda.synchronize()
+    if out_dt == pq.DT_F32:
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+    else:
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+
+
+def test_qlow_gemv_fused_rejects(pq, dev):
+    """Shapes and kinds the fused form does not take fail with an error."""
+    w = pq.QlowWeight(torch.zeros((64, 1024), dtype=torch.uint8, device=dev),
+                      torch.zeros((64, 32, 2), dtype=torch.int16, device=dev), 4)
+    x = torch.zeros(1024, dtype=torch.int16, device=dev)
+    w0 = torch.ones(1024, device=dev)
+    with pytest.raises(pq.PQError, match="K 2048, 4096 or 8192"):
+        pq.qlow_gemv_fused(w, pq.PRO_NORM, x_in=x, w0=w0)
+    w2 = pq.QlowWeight(torch.zeros((64, 2048), dtype=torch.uint8, device=dev),
+                       torch.zeros((64, 64, 2), dtype=torch.int16, device=dev), 4)
+    with pytest.raises(pq.PQError, match="prologue kind"):
+        pq.qlow_gemv_fused(w2, pq.PRO_F32, xf=torch.zeros(2048, device=dev))
