@@ -30,6 +30,11 @@ constexpr int kTqGroup = 128;
 constexpr int kQ8K = 256;
 constexpr int kQ8KBytes = 292;
 
+// Row stride (floats) of the group partials in LDS: rows 4 banks apart, so the
+// fold's lanes (one row each, reading 16 bytes at a time) spread over the banks
+// instead of all reading the same four (rows of 32 or 96 floats).
+__host__ __device__ inline int tq2_pgs(int ng) { return ng + 4; }
+
 // The activations' Q8_K row staged once per workgroup: permuted qs (dword k of
 // each 16 = x[k], x[k+4], x[k+8], x[k+12]), per-group sums from the bsums
 // (exact int16 sums of 16), and each group's block scale d. Split in two: the
@@ -153,7 +158,8 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
   int *xperm = reinterpret_cast<int *>(smem);                  // tq2_xbytes(K): K bytes, permuted, padded
   int *gsum = reinterpret_cast<int *>(smem + tq2_xbytes(K));   // [ng] sum of qs over the group
   float *db = reinterpret_cast<float *>(gsum + ng);            // [ng] Q8_K d of the group's block
-  float *pg = db + ng;                                         // [NT/LPR rows][ng] group partials
+  const int pgs = tq2_pgs(ng);                                 // padded row stride of the partials
+  float *pg = db + ng;                                         // [NT/LPR rows][pgs] group partials
   const int tid = threadIdx.x;
   const int r = tid / LPR, gs = tid % LPR;
   const int ti = (int)blockIdx.x >= bt.wg0[2] ? 2 : (int)blockIdx.x >= bt.wg0[1] ? 1 : 0;   // workgroup-uniform
@@ -210,7 +216,7 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
       if ((gs & 1) == 0 && pc < npc) {
         const int isum = sacc - gsum[g];
         const float t = h2f((uint16_t)(sc[j] >> (16 * (g & 1)))) * db[g];
-        pg[r * ng + g] = t * (float)isum;
+        pg[r * pgs + g] = t * (float)isum;
       }
     }
   }
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
   const int fr = tid, frow = ((int)blockIdx.x - bt.wg0[ti]) * (NT / LPR) + tid;
   if (tid < NT / LPR && frow < N) {   // groups ascending; partials read 8 at a time
     float acc = 0.0f;
-    const float *pr = pg + fr * ng;
+    const float *pr = pg + fr * pgs;
     const int ng8 = (ng & 7) == 0 ? ng : 0;   // 16-byte aligned rows when ng % 8 == 0
     for (int g = ng8; g < ng; g++) acc = acc + pr[g];
     for (int g = 0; g < ng8; g += 8) {
@@ -308,7 +314,7 @@ static int tq2_launch(TqBatch bt, int n, const uint8_t *xq, int K, hipStream_t s
   // 4096x12288 6.0 against 6.8 and 6.7)
   const int nt = envt == 256 || envt == 512 || envt == 1024 ? envt : 512;
   const int rows = nt / lpr;
-  const size_t lds = (size_t)tq2_xbytes(K) + (size_t)ng * 8 + (size_t)rows * ng * 4;
+  const size_t lds = (size_t)tq2_xbytes(K) + (size_t)ng * 8 + (size_t)rows * tq2_pgs(ng) * 4;
   bt.wg0[0] = 0;
   for (int i = 0; i < kTqBatch; i++) bt.wg0[i + 1] = bt.wg0[i] + (i < n ? (bt.rows[i] + rows - 1) / rows : 0);
   for (int i = n; i < kTqBatch; i++) bt.wg0[i + 1] = 0x7fffffff;   // never selected
