@@ -189,6 +189,12 @@ int pq_qlow_gemv(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t 
 size_t pq_qlow_workspace_bytes(int N, int K, int bits);
 int pq_qlow_gemv_ws(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y, int y_dtype,
                     int N, int K, int bits, void *ws, size_t ws_bytes, void *stream);
+/* pq_qlow_gemv of T positions in one launch: x [T][K] bf16 (16-byte aligned),
+ * y row t at y + t * ldy (ldy >= N, y_dtype fp32 or bf16), each row equal to
+ * pq_qlow_gemv of x[t] bit for bit. Replaces the per-position qlow_gemv calls
+ * of pf_gemv_T for a low-bit source tensor (lfm3_nanode.cu:4846-4848). */
+int pq_qlow_gemm(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y, int y_dtype, int N,
+                 int K, int T, int ldy, int bits, void *stream);
 
 /* ============================================================ weight blob
  * The .lfm3q8 file the reference's exporter writes (export_lfm3_q8.py) and

@@ -558,20 +558,23 @@ static bool mixer_fused(const Engine &E, const LayerDev &D) { return mixer_fused
 static int gemm_r2(Engine &E, const Q8Dev &w, const uint16_t *x, void *y, int y_dtype, int T) {
   if (!w.split()) return pq_q8r_gemv(w.pc, w.sf, x, y, y_dtype, w.N, w.K, T, E.st);
   // one GEMV per source tensor (gemv per name): a Q8 part over its rows of the
-  // slot's arrays, a Q4 / Q5 part one position at a time as pf_gemv_T runs it
-  // (4846-4848); at T > 1 a part's [T][n] rows go through ptmp into y's
-  // [T][N] rows by one strided copy
+  // slot's arrays; a Q4 / Q5 part, which pf_gemv_T runs one position at a
+  // time (4846-4848), as one pq_qlow_gemm over the T positions (the same bits
+  // per position) writing y's [T][N] rows in place; at T > 1 a Q8 part's
+  // [T][n] rows go through ptmp into y's rows by one strided copy
   const size_t es = y_dtype == PQ_DTYPE_F32 ? 4 : 2;
   for (const Part &p : w.parts) {
     char *dst = T == 1 ? static_cast<char *>(y) + (size_t)p.r0 * es : E.ptmp;
-    if (p.bits == 8) {
-      PQ_TRY(pq_q8r_gemv(w.pc + (size_t)p.r0 * w.K, w.sf + (size_t)p.r0 * (w.K / 32), x, dst, y_dtype, p.n, w.K, T,
-                         E.st));
-    } else {
-      for (int t = 0; t < T; t++)
-        PQ_TRY(pq_qlow_gemv_ws(p.pc, p.ps, x + (size_t)t * w.K, dst + (size_t)t * p.n * es, y_dtype, p.n, w.K,
-                               p.bits, E.qlow_ws, E.qlow_ws_bytes, E.st));
+    if (p.bits != 8) {
+      if (T == 1)
+        PQ_TRY(pq_qlow_gemv_ws(p.pc, p.ps, x, dst, y_dtype, p.n, w.K, p.bits, E.qlow_ws, E.qlow_ws_bytes, E.st));
+      else
+        PQ_TRY(pq_qlow_gemm(p.pc, p.ps, x, static_cast<char *>(y) + (size_t)p.r0 * es, y_dtype, p.n, w.K, T, w.N,
+                            p.bits, E.st));
+      continue;
     }
+    PQ_TRY(pq_q8r_gemv(w.pc + (size_t)p.r0 * w.K, w.sf + (size_t)p.r0 * (w.K / 32), x, dst, y_dtype, p.n, w.K, T,
+                       E.st));
     if (T > 1 && hipMemcpy2DAsync(static_cast<char *>(y) + (size_t)p.r0 * es, (size_t)w.N * es, dst,
                                   (size_t)p.n * es, (size_t)p.n * es, (size_t)T, hipMemcpyDeviceToDevice,
                                   E.st) != hipSuccess)

@@ -385,6 +385,201 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   }
 }
 
+// ---------------------------------------------------------- T positions
+// The GEMV of TB positions per workgroup, one position block per blockIdx.y
+// (a prompt's low-bit linears, which the reference runs one position at a
+// time): every position's arithmetic is the single-position kernel's, in the
+// same order, so y[t] equals pq_qlow_gemv of x[t] bit for bit. A group's codes
+// become their 16 fp16 pairs once and serve the TB positions. LDS: TB
+// positions' x and group sums, TB x RS rows of partials, RS rows of scales.
+
+// The 32 codes of a group as 16 fp16 pairs 1 + q/128 (quads in qlow_acc's
+// order: pair 2p + j holds codes 4p + 2j and 4p + 2j + 1 of quad p).
+template <int B>
+__device__ __forceinline__ void qlow_codes(v4i w4, uint32_t hp, qh2 *q) {
+  const uint32_t w[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      uint32_t m = (hf ? (w[i] >> 1) : (w[i] << 3)) & 0x78787878u;
+      if constexpr (B == 5) {
+        const int pq = 2 * i + hf;
+        m |= (hp << (7 - pq)) & 0x80808080u;
+      }
+      q[4 * i + 2 * hf] = qlow_h2(m, 0);
+      q[4 * i + 2 * hf + 1] = qlow_h2(m, 1);
+    }
+  }
+}
+
+// acc of one position from the group's pairs: qlow_acc's four chains.
+__device__ __forceinline__ float qlow_dot(const qh2 *q, const float *__restrict__ xg) {
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      const float4 xv = *reinterpret_cast<const float4 *>(xg + 8 * i + 4 * hf);
+      const qh2 q01 = q[4 * i + 2 * hf], q23 = q[4 * i + 2 * hf + 1];
+      a0 = __builtin_fmaf((float)q01.x, xv.x, a0);
+      a1 = __builtin_fmaf((float)q01.y, xv.y, a1);
+      a2 = __builtin_fmaf((float)q23.x, xv.z, a2);
+      a3 = __builtin_fmaf((float)q23.y, xv.w, a3);
+    }
+  }
+  return (a0 + a1) + (a2 + a3);
+}
+
+constexpr int kQgNT = 512;   // threads per workgroup of the T-position form
+
+template <int B, int RS, int TB, int XL>
+__global__ __launch_bounds__(kQgNT) void qlow_gemm_kernel(const uint8_t *__restrict__ pc,
+                                                           const uint32_t *__restrict__ ps,
+                                                           const uint16_t *__restrict__ x, void *__restrict__ y,
+                                                           int y_bf16, int N, int K, int T, int ldy) {
+  constexpr int NT = kQgNT, kLoSlots = NT / RS, HQ = RS / 4, kScl = 4;
+  extern __shared__ __align__(16) float lsm[];
+  const int G = K / kQ, KS = qlow_ks(K), GL = G / KS, GW = qlow_gw(B), GP = qlow_gp(G, RS);
+  float *xs = lsm;                                             // [TB][G*32]
+  float *sx = xs + TB * G * kQ;                                // [TB][G]
+  float *u = sx + TB * G;                                      // [TB][RS][GP]: acc - sg
+  uint32_t *scl = reinterpret_cast<uint32_t *>(u + TB * RS * GP);   // [RS][GP]
+  float *ys = reinterpret_cast<float *>(scl + RS * GP);              // [TB][KS][RS] (slices across waves)
+  const int tid = threadIdx.x;
+  int tile, sub;
+  qlow_place<RS>(blockIdx.x, N / 32, tile, sub);
+  const int r = tid % RS, slot = tid / RS, tr = sub * RS + r;
+  const int t0 = (int)blockIdx.y * TB, nt = T - t0 < TB ? T - t0 : TB;   // positions of this block
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(pc + (size_t)tile * G * GW * 16), (short)0, G * GW * 16, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t *>(ps + (size_t)tile * G * 32), (short)0, G * 32 * 4, kRsrcWord3);
+  // Loads in the order their data is needed: the block's x rows (positions
+  // past T read zeros; 8 bf16 per 16-byte load, XL per thread and position),
+  // the lane's first group of codes, the scale pairs.
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(x + (size_t)t0 * K), (short)0, nt * K * 2, kRsrcWord3);
+  v4i xr[TB][XL];
+#pragma unroll
+  for (int t = 0; t < TB; t++)
+#pragma unroll
+    for (int it = 0; it < XL; it++) {
+      const int e = tid * 8 + it * NT * 8;
+      xr[t][it] = __builtin_amdgcn_raw_buffer_load_b128(rx, e < K ? (t * K + e) * 2 : kRsrcOob, 0, 0);
+    }
+  int g = slot;
+  v4i wc = __builtin_amdgcn_raw_buffer_load_b128(rc, g < G ? (g * GW + tr) * 16 : kRsrcOob, 0, kAuxNT);
+  uint32_t hc = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rc, g < G ? (g * GW + 32) * 16 + tr * 4
+                                                                                : kRsrcOob, 0, kAuxNT)
+                       : 0u;
+  v4i sr[kScl];
+#pragma unroll
+  for (int k = 0; k < kScl; k++) {
+    const int i = tid + k * NT;
+    sr[k] = __builtin_amdgcn_raw_buffer_load_b128(
+        rsc, i < G * HQ ? ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4 : kRsrcOob, 0, kAuxNT);
+  }
+  // staging, position by position: x widened into LDS and its group sums in
+  // order from 0 (a group's 32 elements are the 8-element pieces of 4
+  // adjacent lanes; lane j continues lane j - 1's chain by a DPP row shift)
+#pragma unroll
+  for (int t = 0; t < TB; t++)
+#pragma unroll
+    for (int it = 0; it < XL; it++) {
+      const int e = tid * 8 + it * NT * 8;
+      const uint32_t vv[4] = {(uint32_t)xr[t][it].x, (uint32_t)xr[t][it].y, (uint32_t)xr[t][it].z,
+                              (uint32_t)xr[t][it].w};
+      float f[8];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        f[2 * k] = __uint_as_float(vv[k] << 16);
+        f[2 * k + 1] = __uint_as_float(vv[k] & 0xffff0000u);
+      }
+      float *xt = xs + t * G * kQ;
+      if (e < K) {
+        *reinterpret_cast<float4 *>(xt + e) = make_float4(f[0], f[1], f[2], f[3]);
+        *reinterpret_cast<float4 *>(xt + e + 4) = make_float4(f[4], f[5], f[6], f[7]);
+      }
+      float c = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; k++) c = c + f[k];
+#pragma unroll
+      for (int j = 1; j < 4; j++) {
+        float cj = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), kDppRowShr1, 0xf, 0xf, false));
+#pragma unroll
+        for (int k = 0; k < 8; k++) cj = cj + f[k];
+        if ((tid & 3) == j) c = cj;
+      }
+      if ((tid & 3) == 3 && e < K) sx[t * G + e / kQ] = c;
+    }
+  // the scale pairs, each row's to its row
+  auto put_scales = [&](int i, v4i v) {
+    const int gg = i / HQ, h = i % HQ;
+    scl[(4 * h) * GP + gg] = (uint32_t)v.x;
+    scl[(4 * h + 1) * GP + gg] = (uint32_t)v.y;
+    scl[(4 * h + 2) * GP + gg] = (uint32_t)v.z;
+    scl[(4 * h + 3) * GP + gg] = (uint32_t)v.w;
+  };
+#pragma unroll
+  for (int k = 0; k < kScl; k++)
+    if (tid + k * NT < G * HQ) put_scales(tid + k * NT, sr[k]);
+  for (int i = tid + kScl * NT; i < G * HQ; i += NT)
+    put_scales(i, __builtin_amdgcn_raw_buffer_load_b128(rsc, ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4, 0,
+                                                        kAuxNT));
+  __syncthreads();
+  // group partials: each (row, group) of the lane converts its codes once,
+  // then forms acc - sg for the block's positions; the next group's codes
+  // load before this one's arithmetic
+  for (; g < G; g += kLoSlots) {
+    const int gn = g + kLoSlots;
+    const v4i wn = __builtin_amdgcn_raw_buffer_load_b128(rc, gn < G ? (gn * GW + tr) * 16 : kRsrcOob, 0, kAuxNT);
+    const uint32_t hn = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                                     rc, gn < G ? (gn * GW + 32) * 16 + tr * 4 : kRsrcOob, 0, kAuxNT)
+                               : 0u;
+    qh2 q[16];
+    qlow_codes<B>(wc, hc, q);
+#pragma unroll
+    for (int t = 0; t < TB; t++)
+      u[(t * RS + r) * GP + g] = qlow_dot(q, xs + t * G * kQ + g * kQ) - sx[t * G + g];
+    wc = wn;
+    hc = hn;
+  }
+  __syncthreads();
+  // per (position, K slice, row): the slice's chain; lane ((t * KS + s) * RS + rr)
+  const int nl = TB * KS * RS;
+  float yv = 0.0f;
+  int tt = 0, ss = 0, rr = 0;
+  if (tid < nl) {
+    rr = tid % RS;
+    ss = (tid / RS) % KS;
+    tt = tid / (RS * KS);
+    yv = qlow_chain(u + (tt * RS + rr) * GP + ss * GL, scl + rr * GP + ss * GL, sx + tt * G + ss * GL, GL);
+  }
+  const int row = tile * 32 + sub * RS + rr;
+  auto put = [&](float yt) {
+    if (tt < nt && row < N) {
+      const size_t o = (size_t)(t0 + tt) * ldy + row;
+      if (y_bf16) reinterpret_cast<uint16_t *>(y)[o] = f2bf(yt);
+      else reinterpret_cast<float *>(y)[o] = yt;
+    }
+  };
+  if (KS * RS <= 64) {   // a (position, row)'s slices sit in one wave: they add in order by lane reads
+    float yt = 0.0f;
+    const int base = tid - ss * RS;
+    for (int s = 0; s < KS; s++) yt = yt + __shfl(yv, base + s * RS, 64);
+    if (tid < nl && ss == 0) put(yt);
+    return;
+  }
+  if (tid < nl) ys[(tt * KS + ss) * RS + rr] = yv;
+  __syncthreads();
+  if (tid < nl && ss == 0) {
+    float yt = 0.0f;
+    for (int s = 0; s < KS; s++) yt = yt + ys[(tt * KS + s) * RS + rr];
+    put(yt);
+  }
+}
+
 // y = ((0 + ws[0]) + ws[1]) + ... (k_qlow_combine, lfm3_qlow.cuh:107-113).
 __global__ __launch_bounds__(256) void qlow_combine_kernel(const float *__restrict__ ws, void *__restrict__ y,
                                                             int y_bf16, int N, int KS) {
@@ -642,4 +837,78 @@ extern "C" int pq_qlow_gemv_fused(const uint8_t *pcodes, const uint16_t *pscales
 #undef PQ_QLF_E
 #undef PQ_QLF
   return check_launch("pq_qlow_gemv_fused");
+}
+
+// The T-position form's shape: rows per workgroup RS and positions per
+// workgroup TB, the most positions first (x staged once per position block
+// serves RS rows; TB positions share each group's code conversion), then the
+// longest row slice, within the LDS and with TB * KS * RS chain lanes <= 512.
+static size_t qlow_gemm_lds(int G, int RS, int TB) {
+  return ((size_t)TB * G * kQ + (size_t)TB * G + (size_t)TB * RS * qlow_gp(G, RS) + (size_t)RS * qlow_gp(G, RS) +
+          (size_t)TB * qlow_ks(G * kQ) * RS) * sizeof(float);
+}
+static void qlow_gemm_shape(int N, int K, int T, int &RS, int &TB) {
+  const int G = K / kQ, KS = qlow_ks(K), XL = (K / 8 + kQgNT - 1) / kQgNT;
+  const int tbmax = XL == 1 ? 8 : XL == 2 ? 2 : 1;   // the instantiated (TB, XL) pairs
+  RS = 8;
+  TB = 1;
+  for (int tb = tbmax; tb >= 1; tb >>= 1) {
+    if (tb > 1 && tb > T) continue;
+    for (int rs = 32; rs >= 8; rs >>= 1)
+      if (tb * KS * rs <= kQgNT && qlow_gemm_lds(G, rs, tb) <= kMaxLds && (rs == 8 || N / rs >= 64)) {
+        RS = rs;
+        TB = tb;
+        return;
+      }
+  }
+}
+
+extern "C" int pq_qlow_gemm(const uint8_t *pcodes, const uint16_t *pscales, const uint16_t *x, void *y,
+                            int y_dtype, int N, int K, int T, int ldy, int bits, void *stream) {
+  PQ_REQUIRE(pcodes && pscales && x && y, PQ_ERR_ARG, "pq_qlow_gemm: null pointer");
+  PQ_REQUIRE(qlow_shape(N, K, bits) && T > 0 && ldy >= N, PQ_ERR_ARG,
+             "pq_qlow_gemm: N=%d K=%d T=%d ldy=%d bits=%d (N %% 32, K %% 256, K <= 16384, ldy >= N, bits 4 or 5)", N, K,
+             T, ldy, bits);
+  PQ_REQUIRE((long long)T * K < (1ll << 30) && (long long)T * ldy < (1ll << 31), PQ_ERR_ARG,
+             "pq_qlow_gemm: T=%d too large", T);
+  PQ_REQUIRE(y_dtype == PQ_DTYPE_F32 || y_dtype == PQ_DTYPE_BF16, PQ_ERR_ARG, "pq_qlow_gemm: y_dtype %d", y_dtype);
+  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 4) && aligned(x, 16), PQ_ERR_ALIGN,
+             "pq_qlow_gemm: packed codes and x must be 16-byte aligned");
+  int RS, TB;
+  qlow_gemm_shape(N, K, T, RS, TB);
+  const int G = K / kQ, XL = (K / 8 + kQgNT - 1) / kQgNT;
+  const size_t lds = qlow_gemm_lds(G, RS, TB);
+  PQ_REQUIRE(lds <= kMaxLds && TB * XL <= 8, PQ_ERR_ARG, "pq_qlow_gemm: K=%d exceeds the workgroup's LDS", K);
+  const dim3 grid((unsigned)(N / RS), (unsigned)((T + TB - 1) / TB)), block(kQgNT);
+  const int yb = y_dtype == PQ_DTYPE_BF16 ? 1 : 0;
+  hipStream_t st = as_stream(stream);
+  const uint32_t *ps32 = reinterpret_cast<const uint32_t *>(pscales);
+#define PQ_QG(BB, RR, TT, XX) \
+  launch(qlow_gemm_kernel<BB, RR, TT, XX>, grid, block, lds, st, pcodes, ps32, x, y, yb, N, K, T, ldy)
+#define PQ_QG_T(BB, RR)                                  \
+  do {                                                   \
+    if (XL == 1) {                                       \
+      if (TB == 8) PQ_QG(BB, RR, 8, 1);                  \
+      else if (TB == 4) PQ_QG(BB, RR, 4, 1);             \
+      else if (TB == 2) PQ_QG(BB, RR, 2, 1);             \
+      else PQ_QG(BB, RR, 1, 1);                          \
+    } else if (XL == 2) {                                \
+      if (TB >= 2) PQ_QG(BB, RR, 2, 2);                  \
+      else PQ_QG(BB, RR, 1, 2);                          \
+    } else {                                             \
+      PQ_QG(BB, RR, 1, 4);                               \
+    }                                                    \
+  } while (0)
+  if (bits == 4) {
+    if (RS == 32) PQ_QG_T(4, 32);
+    else if (RS == 16) PQ_QG_T(4, 16);
+    else PQ_QG_T(4, 8);
+  } else {
+    if (RS == 32) PQ_QG_T(5, 32);
+    else if (RS == 16) PQ_QG_T(5, 16);
+    else PQ_QG_T(5, 8);
+  }
+#undef PQ_QG_T
+#undef PQ_QG
+  return check_launch("pq_qlow_gemm");
 }

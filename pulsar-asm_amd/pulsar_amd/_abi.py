@@ -58,6 +58,7 @@ SIGNATURES = {
     "pq_qlow_gemv": (I, [P, P, P, P, I, I, I, I, P]),
     "pq_qlow_workspace_bytes": (Z, [I, I, I]),
     "pq_qlow_gemv_ws": (I, [P, P, P, P, I, I, I, I, P, Z, P]),
+    "pq_qlow_gemm": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "pq_rmsnorm": (I, [P, P, P, P, P, P, P, I, I, F, P]),
     "pq_qk_prep": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, F, P]),
     "pq_attn_workspace_bytes": (Z, [I, I, I, I]),

@@ -8,7 +8,7 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "qlow_gemv_fused", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "qlow_gemv_fused", "qlow_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "tq2_gemv_batch", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "q8r_gemv_fused_swiglu", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
@@ -174,6 +174,21 @@ def qlow_gemv(w, x, out_dtype=DT_BF16, out=None, split=True, ws=None):
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     check(lib().pq_qlow_gemv_ws(w.pcodes.data_ptr(), w.pscales.data_ptr(), _bits16(x), out.data_ptr(), out_dtype,
                                 w.N, w.K, w.bits, _ptr(ws) if nbytes else None, nbytes, stream_ptr()), "pq_qlow_gemv")
+    return out
+
+
+def qlow_gemm(w, x, out_dtype=DT_BF16, out=None):
+    """y [T][N] = the reference's Q4/Q5 GEMV of each row of x (bf16 [T][K]) in
+    one launch (pq_qlow_gemm), each row bit for bit as qlow_gemv."""
+    T = x.shape[0]
+    if x.shape != (T, w.K) or not x.is_contiguous():
+        raise ValueError("x must be a contiguous [T][K] tensor")
+    if out is None:
+        out = torch.empty((T, w.N), dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=x.device)
+    if out.shape != (T, w.N) or out.stride(1) != 1:
+        raise ValueError("out must be [T][N] with unit column stride")
+    check(lib().pq_qlow_gemm(w.pcodes.data_ptr(), w.pscales.data_ptr(), _bits16(x), out.data_ptr(), out_dtype,
+                             w.N, w.K, T, out.stride(0), w.bits, stream_ptr()), "pq_qlow_gemm")
     return out
 
 

@@ -141,3 +141,33 @@ def test_qlow_gemv_fused_rejects(pq, dev):
                        torch.zeros((64, 64, 2), dtype=torch.int16, device=dev), 4)
     with pytest.raises(pq.PQError, match="prologue kind"):
         pq.qlow_gemv_fused(w2, pq.PRO_F32, xf=torch.zeros(2048, device=dev))
+
+
+# T positions in one launch equal the per-position GEMV row by row, bit for
+# bit: every position-block size (T = 1, 3, 8, 33, 100) and the three K forms
+# (2048: 8 positions per workgroup, 4096: 4, 8192: 2), with the outputs
+# written at a row stride wider than N.
+@pytest.mark.parametrize("bits,N,K,T", [(4, 3072, 2048, 33), (5, 16384, 2048, 8), (4, 2048, 8192, 100),
+                                        (5, 2048, 4096, 3), (4, 96, 256, 40), (5, 2048, 2048, 1),
+                                        (4, 64, 16384, 5)])
+def test_qlow_gemm_equals_gemv(orc, pq, dev, bits, N, K, T):
+    print(f"qlow gemm bits={bits} N={N} K={K} T={T}", flush=True)
+    Q, S, _ = _case(orc, N, K, bits, 5 * N + K + T + bits)
+    w = pq.QlowWeight(torch.from_numpy(Q).to(dev), torch.from_numpy(S.view(np.int16)).to(dev), bits)
+    g = torch.Generator(device=dev)
+    g.manual_seed(N + K + T)
+    X = (torch.randn((T, K), device=dev, generator=g) * 2.0).to(torch.bfloat16)
+    X[T // 2] = 0.0                                   # a zero row
+    wide = torch.full((T, N + 40), float("nan"), dtype=torch.float32, device=dev)
+    y = pq.qlow_gemm(w, X, out_dtype=pq.DT_F32, out=wide[:, :N])
+    yb = pq.qlow_gemm(w, X)
+    torch.cuda.synchronize()
+    for t in range(T):
+        want = pq.qlow_gemv(w, X[t], out_dtype=pq.DT_F32)
+        assert torch.equal(y[t].view(torch.int32), want.view(torch.int32)), t
+        assert torch.equal(yb[t].view(torch.int16), pq.qlow_gemv(w, X[t]).view(torch.int16)), t
+    assert torch.isnan(wide[:, N:]).all()            # nothing written past N in a row
+    if T <= 8:   # the oracle on the first rows
+        for t in range(T):
+            xb = X[t].view(torch.int16).cpu().numpy().view(np.uint16)
+            assert np.array_equal(y[t].cpu().numpy().view(np.uint32), orc.qlow_gemv(Q, S, xb).view(np.uint32))
