@@ -302,29 +302,42 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
     if ((tid & 3) == 3 && e < K) sx[e / kQ] = c;
   }
   __syncthreads();
-  // group partials acc - sg, PF groups of loads in flight
-  for (int g0 = 0; g0 < G; g0 += kLoSlots * PF) {
-    v4i wn[PF];
-    uint32_t hn[PF];
-    const bool more = g0 + kLoSlots * PF < G;
-    if (more) {
-#pragma unroll
-      for (int k = 0; k < PF; k++) {
-        const int g = g0 + kLoSlots * PF + slot + kLoSlots * k;
-        wn[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, g < G ? (g * GW + tr) * 16 : kRsrcOob, 0, kAuxNT);
-        hn[k] = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-                             rc, g < G ? (g * GW + 32) * 16 + tr * 4 : kRsrcOob, 0, kAuxNT)
-                       : 0u;
-      }
-    }
+  // group partials acc - sg, PF groups of loads in flight: the rounds
+  // alternate between two register sets passed by name (w / hpl, then wb /
+  // hb), each round's loads issued before the round before it is computed and
+  // unconditionally (groups past G read zeros through the resource bound), so
+  // no copy of a register still being filled waits for its load
+  auto ld_round = [&](v4i *wr, uint32_t *hr, int g0) {
 #pragma unroll
     for (int k = 0; k < PF; k++) {
       const int g = g0 + slot + kLoSlots * k;
-      if (g < G) u[r * GP + g] = qlow_acc<B>(w[k], hpl[k], xs + g * kQ) - sx[g];
+      wr[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, g < G ? (g * GW + tr) * 16 : kRsrcOob, 0, kAuxNT);
+      hr[k] = B == 5 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                           rc, g < G ? (g * GW + 32) * 16 + tr * 4 : kRsrcOob, 0, kAuxNT)
+                     : 0u;
     }
-    if (more) {
+  };
+  auto do_round = [&](const v4i *wr, const uint32_t *hr, int g0) {
 #pragma unroll
-      for (int k = 0; k < PF; k++) { w[k] = wn[k]; hpl[k] = hn[k]; }
+    for (int k = 0; k < PF; k++) {
+      const int g = g0 + slot + kLoSlots * k;
+      if (g < G) u[r * GP + g] = qlow_acc<B>(wr[k], hr[k], xs + g * kQ) - sx[g];
+    }
+  };
+  constexpr int kRound = kLoSlots * PF;   // groups per round
+  v4i wb[PF];
+  uint32_t hb[PF];
+  if (G <= 2 * kRound) {   // one or two rounds (every decode shape): straight-line code, exact waits
+    ld_round(wb, hb, kRound);
+    do_round(w, hpl, 0);
+    do_round(wb, hb, kRound);
+  } else {
+    for (int g0 = 0; g0 < G; g0 += 2 * kRound) {
+      ld_round(wb, hb, g0 + kRound);
+      do_round(w, hpl, g0);
+      if (g0 + kRound >= G) break;
+      ld_round(w, hpl, g0 + 2 * kRound);
+      do_round(wb, hb, g0 + kRound);
     }
   }
   // the scale pairs, each row's to its row
