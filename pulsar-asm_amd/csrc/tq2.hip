@@ -150,84 +150,99 @@ struct TqBatch {
 // (w >> 2) & 0x33333333 against x's signed high and unsigned low nibbles,
 // sum code*x = 16 sum code*h + sum code*l: 7 VALU per 16 weights, against 11
 // for four byte masks and sdot4). The codes load nontemporal.
-template <int LPR, int PPL, int XR, int NT>
+// NB > 1: the batch's NB tensors have the same row count and a workgroup
+// takes the same row block of each (x staged once for all of them, and the
+// launch holds a third of the workgroups of one per tensor and row block);
+// NB = 1: a workgroup's rows are one tensor's, selected from the workgroup id.
+template <int LPR, int PPL, int XR, int NT, int NB>
 __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t *__restrict__ xq, int K) {
   static_assert(64 % LPR == 0, "a row's lanes must sit in one wave");
+  constexpr int kRows = NT / LPR;   // rows per workgroup and tensor
   extern __shared__ __align__(16) unsigned char smem[];
   const int ng = K / kTqGroup, npc = 2 * ng;                 // groups, 16-byte pieces per row
   int *xperm = reinterpret_cast<int *>(smem);                  // tq2_xbytes(K): K bytes, permuted, padded
   int *gsum = reinterpret_cast<int *>(smem + tq2_xbytes(K));   // [ng] sum of qs over the group
   float *db = reinterpret_cast<float *>(gsum + ng);            // [ng] Q8_K d of the group's block
   const int pgs = tq2_pgs(ng);                                 // padded row stride of the partials
-  float *pg = db + ng;                                         // [NT/LPR rows][pgs] group partials
+  float *pg = db + ng;                                         // [NB][kRows][pgs] group partials
   const int tid = threadIdx.x;
   const int r = tid / LPR, gs = tid % LPR;
-  const int ti = (int)blockIdx.x >= bt.wg0[2] ? 2 : (int)blockIdx.x >= bt.wg0[1] ? 1 : 0;   // workgroup-uniform
-  const uint8_t *__restrict__ codes = bt.codes[ti];
-  const uint16_t *__restrict__ scales = bt.scales[ti];
-  float *__restrict__ y = bt.y[ti];
-  const int N = bt.rows[ti];
-  const int row = ((int)blockIdx.x - bt.wg0[ti]) * (NT / LPR) + r;
+  // the first tensor and the row block (workgroup-uniform)
+  const int t0 = NB > 1 ? 0 : (int)blockIdx.x >= bt.wg0[2] ? 2 : (int)blockIdx.x >= bt.wg0[1] ? 1 : 0;
+  const int rb = (int)blockIdx.x - (NB > 1 ? 0 : bt.wg0[t0]);
+  const int N = bt.rows[t0];   // every tensor's when NB > 1
+  const int row = rb * kRows + r;
   const bool live = row < N;
   // one resource per tensor (workgroup-uniform: scalar registers, no per-row
   // waterfall); a row past N reads at an offset past num_records: zeros
-  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t *>(codes), (short)0, (int)((size_t)N * (K / 4)), kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t *>(scales), (short)0, (int)((size_t)N * ng * 2), kRsrcWord3);
+  __amdgpu_buffer_rsrc_t rc[NB], rsc[NB];
+#pragma unroll
+  for (int i = 0; i < NB; i++) {
+    rc[i] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(bt.codes[t0 + i]), (short)0,
+                                              (int)((size_t)N * (K / 4)), kRsrcWord3);
+    rsc[i] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(bt.scales[t0 + i]), (short)0,
+                                               (int)((size_t)N * ng * 2), kRsrcWord3);
+  }
   const int crow = live ? row * (K / 4) : kRsrcOob, srow = live ? row * ng * 2 : kRsrcOob;
   TqX<XR> xt;
   tq2_load_x<XR, NT>(xq, K, xt);
   for (int p0 = 0; p0 < npc; p0 += LPR * PPL) {
     // this round's codes (16 B per piece) and, on even lanes, the scale pair
-    // of each piece's group, before anything waits
-    v4i c[PPL];
-    uint32_t sc[PPL];
+    // of each piece's group, for every tensor, before anything waits
+    v4i c[NB][PPL];
+    uint32_t sc[NB][PPL];
 #pragma unroll
-    for (int j = 0; j < PPL; j++) {
-      const int pc = p0 + j * LPR + gs, g = pc >> 1;
-      c[j] = __builtin_amdgcn_raw_buffer_load_b128(rc, pc < npc && live ? crow + pc * 16 : kRsrcOob, 0, kAuxNT);
-      // every lane loads (the odd lane of a pair discards it): no branch, so
-      // the waits on the earlier x loads count exactly
-      sc[j] = __builtin_amdgcn_raw_buffer_load_b32(rsc, pc < npc && live ? srow + (g & ~1) * 2 : kRsrcOob, 0, 0);
-    }
+    for (int i = 0; i < NB; i++)
+#pragma unroll
+      for (int j = 0; j < PPL; j++) {
+        const int pc = p0 + j * LPR + gs, g = pc >> 1;
+        c[i][j] = __builtin_amdgcn_raw_buffer_load_b128(rc[i], pc < npc && live ? crow + pc * 16 : kRsrcOob, 0,
+                                                        kAuxNT);
+        // every lane loads (the odd lane of a pair discards it): no branch, so
+        // the waits on the earlier x loads count exactly
+        sc[i][j] = __builtin_amdgcn_raw_buffer_load_b32(rsc[i], pc < npc && live ? srow + (g & ~1) * 2 : kRsrcOob, 0,
+                                                        0);
+      }
     if (p0 == 0) {
       tq2_store_x<XR, NT>(xt, K, xperm, gsum, db);
       __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < PPL; j++) {
-      const int pc = p0 + j * LPR + gs, g = pc >> 1;
-      const uint32_t w[4] = {(uint32_t)c[j].x, (uint32_t)c[j].y, (uint32_t)c[j].z, (uint32_t)c[j].w};
-      const int *xp = xperm + (pc < npc ? pc : 0) * kXPieceDw;
-      int ah = 0;
-      uint32_t al = 0;
+    for (int i = 0; i < NB; i++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * q);
-        const int m0 = (int)(w[q] & 0x33333333u), m1 = (int)((w[q] >> 2) & 0x33333333u);
-        ah = __builtin_amdgcn_sdot8(m0, xv.x, ah, false);
-        ah = __builtin_amdgcn_sdot8(m1, xv.y, ah, false);
-        al = __builtin_amdgcn_udot8(m0, xv.z, al, false);
-        al = __builtin_amdgcn_udot8(m1, xv.w, al, false);
+      for (int j = 0; j < PPL; j++) {
+        const int pc = p0 + j * LPR + gs, g = pc >> 1;
+        const uint32_t w[4] = {(uint32_t)c[i][j].x, (uint32_t)c[i][j].y, (uint32_t)c[i][j].z, (uint32_t)c[i][j].w};
+        const int *xp = xperm + (pc < npc ? pc : 0) * kXPieceDw;
+        int ah = 0;
+        uint32_t al = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int4 xv = *reinterpret_cast<const int4 *>(xp + 4 * q);
+          const int m0 = (int)(w[q] & 0x33333333u), m1 = (int)((w[q] >> 2) & 0x33333333u);
+          ah = __builtin_amdgcn_sdot8(m0, xv.x, ah, false);
+          ah = __builtin_amdgcn_sdot8(m1, xv.y, ah, false);
+          al = __builtin_amdgcn_udot8(m0, xv.z, al, false);
+          al = __builtin_amdgcn_udot8(m1, xv.w, al, false);
+        }
+        int sacc = 16 * ah + (int)al;
+        sacc += __builtin_amdgcn_update_dpp(0, sacc, kDppXor1, 0xf, 0xf, false);   // the group's two halves
+        if ((gs & 1) == 0 && pc < npc) {
+          const int isum = sacc - gsum[g];
+          const float t = h2f((uint16_t)(sc[i][j] >> (16 * (g & 1)))) * db[g];
+          pg[(i * kRows + r) * pgs + g] = t * (float)isum;
+        }
       }
-      int sacc = 16 * ah + (int)al;
-      sacc += __builtin_amdgcn_update_dpp(0, sacc, kDppXor1, 0xf, 0xf, false);   // the group's two halves
-      if ((gs & 1) == 0 && pc < npc) {
-        const int isum = sacc - gsum[g];
-        const float t = h2f((uint16_t)(sc[j] >> (16 * (g & 1)))) * db[g];
-        pg[r * pgs + g] = t * (float)isum;
-      }
-    }
   }
-  // after one workgroup barrier, lane i of wave 0 folds row i: every row of
-  // the workgroup in one wave's instruction stream (a fold per wave, with 2 of
-  // its lanes busy, measured 0.1-0.3 us slower per launch)
+  // after one workgroup barrier, lane l of wave 0 folds row l % kRows of
+  // tensor l / kRows: every row of the workgroup in one wave's instruction
+  // stream (a fold per wave, with 2 of its lanes busy, measured 0.1-0.3 us
+  // slower per launch)
   __syncthreads();
-  const int fr = tid, frow = ((int)blockIdx.x - bt.wg0[ti]) * (NT / LPR) + tid;
-  if (tid < NT / LPR && frow < N) {   // groups ascending; partials read 8 at a time
+  const int fi = tid / kRows, fr = tid % kRows, frow = rb * kRows + fr;
+  if (tid < NB * kRows && frow < N) {   // groups ascending; partials read 8 at a time
     float acc = 0.0f;
-    const float *pr = pg + fr * pgs;
+    const float *pr = pg + (fi * kRows + fr) * pgs;
     const int ng8 = (ng & 7) == 0 ? ng : 0;   // 16-byte aligned rows when ng % 8 == 0
     for (int g = ng8; g < ng; g++) acc = acc + pr[g];
     for (int g = 0; g < ng8; g += 8) {
@@ -236,7 +251,7 @@ __global__ __launch_bounds__(NT) void tq2_gemv_kernel(TqBatch bt, const uint8_t 
       acc = acc + a4.x; acc = acc + a4.y; acc = acc + a4.z; acc = acc + a4.w;
       acc = acc + b4.x; acc = acc + b4.y; acc = acc + b4.z; acc = acc + b4.w;
     }
-    y[frow] = acc;
+    bt.y[t0 + fi][frow] = acc;
   }
 }
 
@@ -314,28 +329,42 @@ static int tq2_launch(TqBatch bt, int n, const uint8_t *xq, int K, hipStream_t s
   // 4096x12288 6.0 against 6.8 and 6.7)
   const int nt = envt == 256 || envt == 512 || envt == 1024 ? envt : 512;
   const int rows = nt / lpr;
-  const size_t lds = (size_t)tq2_xbytes(K) + (size_t)ng * 8 + (size_t)rows * tq2_pgs(ng) * 4;
+  // tensors of equal row count share workgroups: each takes the same row
+  // block of all of them (x staged once; gate+up 12288x4096 as one batch:
+  // 768 workgroups, all resident at once, instead of 1536); PQ_TQ2_NB1=1
+  // keeps one tensor per workgroup
+  static const int env_nb1 = env_int("PQ_TQ2_NB1");
+  bool same = n > 1 && env_nb1 != 1 && nt == 512;   // (instantiated at 512 threads)
+  for (int i = 1; i < n; i++) same = same && bt.rows[i] == bt.rows[0];
+  const int nb = same ? n : 1;
+  const size_t lds = (size_t)tq2_xbytes(K) + (size_t)ng * 8 + (size_t)nb * rows * tq2_pgs(ng) * 4;
   bt.wg0[0] = 0;
   for (int i = 0; i < kTqBatch; i++) bt.wg0[i + 1] = bt.wg0[i] + (i < n ? (bt.rows[i] + rows - 1) / rows : 0);
   for (int i = n; i < kTqBatch; i++) bt.wg0[i + 1] = 0x7fffffff;   // never selected
-  const dim3 grid((unsigned)bt.wg0[n]), block(nt);
+  const dim3 grid((unsigned)(same ? (bt.rows[0] + rows - 1) / rows : bt.wg0[n])), block(nt);
   // 16-qs runs of x per thread (K/16 runs over nt threads)
   const int runs = (K / 16 + nt - 1) / nt, xr = runs <= 1 ? 1 : runs <= 2 ? 2 : runs <= 4 ? 4 : 8;
-#define PQ_TQ2_X(L, P, X, T) launch(tq2_gemv_kernel<L, P, X, T>, grid, block, lds, st, bt, xq, K)
+#define PQ_TQ2_X1(L, P, X, T) launch(tq2_gemv_kernel<L, P, X, T, 1>, grid, block, lds, st, bt, xq, K)
+#define PQ_TQ2_X(L, P, X, T)                                                                \
+  do {                                                                                      \
+    if (nb == 2) launch(tq2_gemv_kernel<L, P, X, T, 2>, grid, block, lds, st, bt, xq, K);   \
+    else if (nb == 3) launch(tq2_gemv_kernel<L, P, X, T, 3>, grid, block, lds, st, bt, xq, K); \
+    else PQ_TQ2_X1(L, P, X, T);                                                             \
+  } while (0)
 #define PQ_TQ2_T(L, P)                                             \
   do {                                                             \
     if (nt == 1024) {                                              \
-      if (xr <= 1) PQ_TQ2_X(L, P, 1, 1024);                        \
-      else PQ_TQ2_X(L, P, 2, 1024);                                \
+      if (xr <= 1) PQ_TQ2_X1(L, P, 1, 1024);                       \
+      else PQ_TQ2_X1(L, P, 2, 1024);                               \
     } else if (nt == 512) {                                        \
       if (xr <= 1) PQ_TQ2_X(L, P, 1, 512);                         \
       else if (xr <= 2) PQ_TQ2_X(L, P, 2, 512);                    \
       else PQ_TQ2_X(L, P, 4, 512);                                 \
     } else {                                                       \
-      if (xr <= 1) PQ_TQ2_X(L, P, 1, 256);                         \
-      else if (xr <= 2) PQ_TQ2_X(L, P, 2, 256);                    \
-      else if (xr <= 4) PQ_TQ2_X(L, P, 4, 256);                    \
-      else PQ_TQ2_X(L, P, 8, 256);                                 \
+      if (xr <= 1) PQ_TQ2_X1(L, P, 1, 256);                        \
+      else if (xr <= 2) PQ_TQ2_X1(L, P, 2, 256);                   \
+      else if (xr <= 4) PQ_TQ2_X1(L, P, 4, 256);                   \
+      else PQ_TQ2_X1(L, P, 8, 256);                                \
     }                                                              \
   } while (0)
   if (lpr == 16) {
@@ -353,6 +382,7 @@ static int tq2_launch(TqBatch bt, int n, const uint8_t *xq, int K, hipStream_t s
   }
 #undef PQ_TQ2_T
 #undef PQ_TQ2_X
+#undef PQ_TQ2_X1
   return check_launch(who);
 }
 

@@ -74,9 +74,11 @@ def test_tq2_reference_call_order(orc, pq, dev, N, K):
 
 
 # one launch over several tensors of one K: each tensor's rows give the oracle's
-# bits (row counts that do and do not fill whole workgroups, one to three tensors)
+# bits (row counts that do and do not fill whole workgroups, one to three
+# tensors; tensors of equal row count share workgroups, the others do not)
 @pytest.mark.parametrize("rows,K", [((12288, 12288), 4096), ((2048, 512, 512), 4096), ((61, 1001, 37), 2560),
-                                    ((4096,), 12288), ((3, 5), 256)])
+                                    ((4096,), 12288), ((3, 5), 256), ((1000, 1000, 1000), 4096),
+                                    ((77, 77), 12288), ((33, 33), 256), ((500, 500, 500), 2560)])
 def test_tq2_gemv_batch(orc, pq, dev, rows, K):
     print(f"tq2 batch rows={rows} K={K}", flush=True)
     x = orc.gen_normal(K + 7, K)
