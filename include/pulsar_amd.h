@@ -396,6 +396,14 @@ int pq_q8r_gemv_fused_swiglu(const int8_t *codes, const float *scales, const pq_
  * 1894-1915) for a low-bit source tensor. */
 int pq_qlow_gemv_fused(const uint8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro, void *y,
                        int y_dtype, int N, int K, int bits, void *stream);
+/* The FFN's gate/up GEMV on a low-bit [w1 | w3] payload (pq_qlow_pack of the
+ * 2F rows, gate rows first) with a RESNORM or NORM prologue and y [F] bf16 =
+ * silu_mul of the bf16 gate and up outputs: the qlow_gemv (1894-1915) +
+ * k_silu_mul_bf (821-829) pair of layer_body (lfm3_nanode.cu:3830-3833) in
+ * one launch, the same bits as pq_qlow_gemv_fused (N = 2F, bf16) followed by
+ * pq_silu_mul. F a multiple of 32; K 2048, 4096 or 8192. */
+int pq_qlow_gemv_fused_swiglu(const uint8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
+                              uint16_t *y, int F, int K, int bits, void *stream);
 /* The FFN's gate/up GEMV (weights from pq_q8_pack_gate_up, N = 2F) with the
  * prologue pro and silu(gate) * up as its epilogue: writes the Q8_0 row
  * (qx [F], dx [F/32]) that the down projection reads (PQ_PRO_Q8) -- the

@@ -806,6 +806,18 @@ static int parts_fused(Engine &E, const Q8Dev &w, const pq_gemv_prologue &pro, u
   return PQ_OK;
 }
 
+// A gate/up slot whose [gate | up] rows are one low-bit part (w1 | w3 of one
+// width, tile after tile): pq_qlow_gemv_fused_swiglu writes silu(gate) * up
+// directly (PQ_QLOW_SWIGLU=0: the GEMV, then down's SILU prologue).
+static bool qlow_swiglu(const Q8Dev &w) {
+  static const bool off = [] {
+    const char *e = getenv("PQ_QLOW_SWIGLU");
+    return e != nullptr && atoi(e) == 0;
+  }();
+  return !off && w.parts.size() == 1 && w.parts[0].bits != 8 && w.parts[0].n == w.N && (w.N / 2) % 32 == 0 &&
+         parts_fusable(w, PQ_PRO_RESNORM);
+}
+
 static int forward_decode_r2(Engine &E, bool dev) {
   const pq_model_cfg &c = E.c;
   const int H = c.hidden;
@@ -928,6 +940,13 @@ static int forward_decode_r2(Engine &E, bool dev) {
     // a split gate/up slot: its parts with the RESNORM prologue write the
     // [gate | up] rows, and down takes silu(gate) * up as its SILU prologue
     const bool down_silu = D.down.split() ? parts_fusable(D.down, PQ_PRO_SILU) : pow2_range(D.down.K);
+    if (qlow_swiglu(D.ug)) {
+      resnorm(D.post_op_norm, D.ffn_norm);
+      const Part &pu = D.ug.parts[0];
+      PQ_TRY(pq_qlow_gemv_fused_swiglu(pu.pc, pu.ps, &p, E.A, c.ffn, H, pu.bits, E.st));
+      PQ_TRY(plain(D.down, E.A, E.Hb));
+      continue;
+    }
     if (D.ug.split() && parts_fusable(D.ug, PQ_PRO_RESNORM) && down_silu) {
       resnorm(D.post_op_norm, D.ffn_norm);
       PQ_TRY(parts_fused(E, D.ug, p, E.Wd));                        // [gate | up] rows

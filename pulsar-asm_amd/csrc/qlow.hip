@@ -179,7 +179,12 @@ __device__ __forceinline__ void qlow_place(int b, int ntiles, int &tile, int &su
 // does x.
 constexpr int kProPlain = -1;
 
-template <int B, int RS, int XL, int NT, int PF, int PRO = kProPlain, int E = 8>
+// SWI: the FFN's gate/up GEMV with the SwiGLU epilogue. The tensor's N = 2F
+// rows are [gate | up]; a workgroup takes RS rows of a gate tile with its first
+// NT/2 threads and the same rows of the up tile (F/32 tiles on) with the
+// others, and writes y = bf16(silu(bf16 g) * bf16 u) for its RS rows [F]: the
+// GEMV, bf16 outputs and pq_silu_mul in one launch, the same bits.
+template <int B, int RS, int XL, int NT, int PF, int PRO = kProPlain, int E = 8, bool SWI = false>
 __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict__ pc,
                                                               const uint32_t *__restrict__ ps,
                                                               const uint16_t *__restrict__ x, void *__restrict__ y,
@@ -192,17 +197,21 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   // the groups this workgroup covers: [gb, gb + G), in KS slices of GL
   const int KS = ws ? 1 : KSA, G = ws ? GA / KSA : GA, GL = G / KS, gb = ws ? (int)blockIdx.y * G : 0;
   // per row, the groups' partials and scale pairs at the padded stride GP
-  constexpr int kLoSlots = NT / RS;   // group slots per round (NT threads: NT/RS slots of RS rows)
+  constexpr int kHalf = SWI ? NT / 2 : NT;   // threads per row set (SWI: the gate rows', then the up rows')
+  constexpr int kLoSlots = kHalf / RS;       // group slots per round (kHalf/RS slots of RS rows)
+  constexpr int kRows = SWI ? 2 * RS : RS;   // rows staged in LDS
   const int GP = qlow_gp(G, RS);
   float *xs = lsm;                      // [G*32]
   float *sx = xs + G * kQ;              // [G]
-  float *u = sx + G;                    // [8 rows][GP]: acc - sg
-  uint32_t *scl = reinterpret_cast<uint32_t *>(u + RS * GP);   // [8 rows][GP] half2 (d', mn)
-  float *ys = reinterpret_cast<float *>(scl + RS * GP);          // [KS][8]
+  float *u = sx + G;                    // [kRows][GP]: acc - sg
+  uint32_t *scl = reinterpret_cast<uint32_t *>(u + kRows * GP);   // [kRows][GP] half2 (d', mn)
+  float *ys = reinterpret_cast<float *>(scl + kRows * GP);          // [KS][RS] (SWI: [RS] up outputs)
   const int tid = threadIdx.x;
+  const int half = SWI ? tid / kHalf : 0, tih = SWI ? tid % kHalf : tid;   // wave-uniform half
   int tile, sub;
-  qlow_place<RS>(blockIdx.x, N / 32, tile, sub);
-  const int r = tid % RS, slot = tid / RS;
+  qlow_place<RS>(blockIdx.x, (SWI ? N / 2 : N) / 32, tile, sub);
+  if (SWI && half) tile += N / 64;      // the up rows' tile
+  const int r = tih % RS, slot = tih / RS;
   const int tr = sub * RS + r;          // this lane's row within the tile
   // the tile's codes and scales from group gb (wave-uniform resources)
   const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
@@ -246,7 +255,7 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   v4i sr[kScl];
 #pragma unroll
   for (int k = 0; k < kScl; k++) {
-    const int i = tid + k * NT;
+    const int i = tih + k * kHalf;
     sr[k] = __builtin_amdgcn_raw_buffer_load_b128(
         rsc, i < G * HQ ? ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4 : kRsrcOob, 0, kAuxNT);
   }
@@ -321,7 +330,7 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
 #pragma unroll
     for (int k = 0; k < PF; k++) {
       const int g = g0 + slot + kLoSlots * k;
-      if (g < G) u[r * GP + g] = qlow_acc<B>(wr[k], hr[k], xs + g * kQ) - sx[g];
+      if (g < G) u[(half * RS + r) * GP + g] = qlow_acc<B>(wr[k], hr[k], xs + g * kQ) - sx[g];
     }
   };
   constexpr int kRound = kLoSlots * PF;   // groups per round
@@ -342,16 +351,16 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   }
   // the scale pairs, each row's to its row
   auto put_scales = [&](int i, v4i v) {
-    const int g = i / HQ, h = i % HQ;
-    scl[(4 * h) * GP + g] = (uint32_t)v.x;
-    scl[(4 * h + 1) * GP + g] = (uint32_t)v.y;
-    scl[(4 * h + 2) * GP + g] = (uint32_t)v.z;
-    scl[(4 * h + 3) * GP + g] = (uint32_t)v.w;
+    const int g = i / HQ, h = half * RS + 4 * (i % HQ);
+    scl[h * GP + g] = (uint32_t)v.x;
+    scl[(h + 1) * GP + g] = (uint32_t)v.y;
+    scl[(h + 2) * GP + g] = (uint32_t)v.z;
+    scl[(h + 3) * GP + g] = (uint32_t)v.w;
   };
 #pragma unroll
   for (int k = 0; k < kScl; k++)
-    if (tid + k * NT < G * HQ) put_scales(tid + k * NT, sr[k]);
-  for (int i = tid + kScl * NT; i < G * HQ; i += NT)
+    if (tih + k * kHalf < G * HQ) put_scales(tih + k * kHalf, sr[k]);
+  for (int i = tih + kScl * kHalf; i < G * HQ; i += kHalf)
     put_scales(i, __builtin_amdgcn_raw_buffer_load_b128(rsc, ((i / HQ) * 32 + sub * RS + 4 * (i % HQ)) * 4, 0,
                                                         kAuxNT));
   __syncthreads();
@@ -359,6 +368,24 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
   // each. With at most 64 such lanes (every shape but 32-row slices of K >=
   // 4096) they are wave 0's, and the slices add in order through lane reads:
   // no barrier and no LDS pass
+  if constexpr (SWI) {   // wave 0: the gate rows' chains, wave 1 the up rows' (RS * KS <= 64 each)
+    const int wv = tid >> 6, ln = tid & 63;
+    float yv = 0.0f, yt = 0.0f;
+    if (wv < 2 && ln < RS * KS) {
+      const int s = ln / RS, rr = ln % RS;
+      yv = qlow_chain(u + (wv * RS + rr) * GP + s * GL, scl + (wv * RS + rr) * GP + s * GL, sx + s * GL, GL);
+    }
+    if (wv < 2)
+      for (int s = 0; s < KS; s++) yt = yt + __shfl(yv, s * RS + ln % RS, 64);
+    if (wv == 1 && ln < RS) ys[ln] = yt;
+    __syncthreads();
+    if (wv == 0 && ln < RS) {   // silu_mul of the two bf16 outputs (silu_mul_kernel's arithmetic)
+      const float a = bf2f(f2bf(yt)), uu = bf2f(f2bf(ys[ln]));
+      const float sg = 1.0f / (1.0f + expf_pq(-a));
+      reinterpret_cast<uint16_t *>(y)[tile * 32 + sub * RS + ln] = f2bf((a * sg) * uu);
+    }
+    return;
+  }
   const int row = tile * 32 + sub * RS + tid % RS;
   if (RS * KS <= 64) {
     if (tid >= 64) return;
@@ -924,4 +951,68 @@ extern "C" int pq_qlow_gemm(const uint8_t *pcodes, const uint16_t *pscales, cons
 #undef PQ_QG_T
 #undef PQ_QG
   return check_launch("pq_qlow_gemm");
+}
+
+// The FFN's gate/up GEMV on a low-bit [gate | up] tensor (N = 2F rows) with a
+// RESNORM or NORM prologue and the SwiGLU epilogue: y bf16 [F] = silu(gate) *
+// up as pq_silu_mul forms it from the bf16 outputs.
+extern "C" int pq_qlow_gemv_fused_swiglu(const uint8_t *pcodes, const uint16_t *pscales, const pq_gemv_prologue *pro,
+                                         uint16_t *y, int F, int K, int bits, void *stream) {
+  PQ_REQUIRE(pcodes && pscales && pro && y, PQ_ERR_ARG, "pq_qlow_gemv_fused_swiglu: null pointer");
+  PQ_REQUIRE(F > 0 && F % 32 == 0 && qlow_shape(2 * F, K, bits) && (K == 2048 || K == 4096 || K == 8192), PQ_ERR_ARG,
+             "pq_qlow_gemv_fused_swiglu: F=%d K=%d bits=%d (F %% 32, K 2048, 4096 or 8192, bits 4 or 5)", F, K, bits);
+  PQ_REQUIRE(aligned(pcodes, 16) && aligned(pscales, 4), PQ_ERR_ALIGN,
+             "pq_qlow_gemv_fused_swiglu: packed codes must be 16-byte aligned");
+  const pq_gemv_prologue &p = *pro;
+  if (p.kind == PQ_PRO_RESNORM) {
+    PQ_REQUIRE(p.h && p.x_in && p.x_out && p.w0 && p.w1 && p.x_in != p.x_out, PQ_ERR_ARG,
+               "pq_qlow_gemv_fused_swiglu: RESNORM needs h, x_in, x_out (distinct), w0, w1");
+    PQ_REQUIRE(aligned(p.h, 16) && aligned(p.x_in, 16) && aligned(p.x_out, 16) && aligned(p.w0, 16) &&
+                   aligned(p.w1, 16),
+               PQ_ERR_ALIGN, "pq_qlow_gemv_fused_swiglu: RESNORM vectors must be 16-byte aligned");
+  } else if (p.kind == PQ_PRO_NORM) {
+    PQ_REQUIRE(p.x_in && p.w0 && aligned(p.x_in, 16) && aligned(p.w0, 16), PQ_ERR_ARG,
+               "pq_qlow_gemv_fused_swiglu: NORM needs 16-byte aligned x_in, w0");
+  } else {
+    return fail(PQ_ERR_ARG, "pq_qlow_gemv_fused_swiglu: prologue kind %d (RESNORM or NORM)", p.kind);
+  }
+  const int G = K / kQ, KS = qlow_ks(K);
+  // rows of each half per workgroup: qlow_rows of the 2F rows, at most 64 / KS
+  // (a half's slice chains sit in one wave). Measured, Q4 F = 8192, K = 2048:
+  // 32 rows a half (256 workgroups) 8.03 us, as the plain gate/up GEMV's 8.06,
+  // against 8.87 at 16 and 12.0 at 8.
+  int RS = qlow_rows(2 * F);
+  while (RS * KS > 64) RS >>= 1;
+  const size_t lds = ((size_t)G * kQ + G + 2 * 2 * RS * (size_t)qlow_gp(G, RS) + (size_t)KS * RS) * sizeof(float);
+  PQ_REQUIRE(lds <= kMaxLds, PQ_ERR_ARG, "pq_qlow_gemv_fused_swiglu: K=%d exceeds the workgroup's LDS", K);
+  const dim3 grid((unsigned)(F / RS)), block(512);
+  hipStream_t st = as_stream(stream);
+  const uint32_t *ps32 = reinterpret_cast<const uint32_t *>(pscales);
+#define PQ_QSW(BB, RR, PP, EE)                                                                                  \
+  launch(qlow_gemv_kernel<BB, RR, 1, 512, 2, PP, EE, true>, grid, block, lds, st, pcodes, ps32, nullptr, y, 1, \
+         2 * F, K, (float *)nullptr, p)
+#define PQ_QSW_E(BB, RR, PP)                  \
+  do {                                        \
+    if (K == 2048) PQ_QSW(BB, RR, PP, 4);     \
+    else if (K == 4096) PQ_QSW(BB, RR, PP, 8); \
+    else PQ_QSW(BB, RR, PP, 16);              \
+  } while (0)
+#define PQ_QSW_P(BB, RR)                                                          \
+  do {                                                                            \
+    if (p.kind == PQ_PRO_RESNORM) PQ_QSW_E(BB, RR, PQ_PRO_RESNORM);               \
+    else PQ_QSW_E(BB, RR, PQ_PRO_NORM);                                           \
+  } while (0)
+  if (bits == 4) {
+    if (RS == 32) PQ_QSW_P(4, 32);
+    else if (RS == 16) PQ_QSW_P(4, 16);
+    else PQ_QSW_P(4, 8);
+  } else {
+    if (RS == 32) PQ_QSW_P(5, 32);
+    else if (RS == 16) PQ_QSW_P(5, 16);
+    else PQ_QSW_P(5, 8);
+  }
+#undef PQ_QSW_P
+#undef PQ_QSW_E
+#undef PQ_QSW
+  return check_launch("pq_qlow_gemv_fused_swiglu");
 }

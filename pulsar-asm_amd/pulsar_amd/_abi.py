@@ -78,6 +78,7 @@ SIGNATURES = {
     "pq_argmax_parts": (I, [P, I, P, P]),
     "pq_q8r_gemv_fused": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, I, P, P]),
     "pq_qlow_gemv_fused": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, I, I, P]),
+    "pq_qlow_gemv_fused_swiglu": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, I, P]),
     "pq_q8r_gemv_parts": (I, [I]),
     "pq_q8r_gemv_fused_swiglu": (I, [P, P, C.POINTER(GemvPrologue), P, I, I, P]),
     "pq_q8_gemv_fused_swiglu": (I, [P, P, C.POINTER(GemvPrologue), P, P, I, I, P]),

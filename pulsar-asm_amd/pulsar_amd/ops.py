@@ -8,7 +8,7 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "qlow_gemv_fused", "qlow_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "qlow_gemv_fused", "qlow_gemv_fused_swiglu", "qlow_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "tq2_gemv_batch", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "q8r_gemv_fused_swiglu", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
@@ -201,6 +201,20 @@ def qlow_gemv_fused(w, kind, out_dtype=DT_BF16, out=None, eps=1e-5, **ptrs):
         out = torch.empty(w.N, dtype=torch.float32 if out_dtype == DT_F32 else torch.bfloat16, device=w.pcodes.device)
     check(lib().pq_qlow_gemv_fused(w.pcodes.data_ptr(), w.pscales.data_ptr(), C.byref(p), out.data_ptr(), out_dtype,
                                    w.N, w.K, w.bits, stream_ptr()), "pq_qlow_gemv_fused")
+    return out
+
+
+def qlow_gemv_fused_swiglu(w, kind, out=None, eps=1e-5, **ptrs):
+    """The FFN's gate/up GEMV on a low-bit [gate | up] tensor (w.N = 2F rows)
+    with a RESNORM or NORM prologue and the SwiGLU epilogue
+    (pq_qlow_gemv_fused_swiglu): bf16 [F] = silu(gate) * up."""
+    import ctypes as C
+    p = _prologue(kind, eps, ptrs)
+    F = w.N // 2
+    if out is None:
+        out = torch.empty(F, dtype=torch.bfloat16, device=w.pcodes.device)
+    check(lib().pq_qlow_gemv_fused_swiglu(w.pcodes.data_ptr(), w.pscales.data_ptr(), C.byref(p), _bits16(out), F,
+                                          w.K, w.bits, stream_ptr()), "pq_qlow_gemv_fused_swiglu")
     return out
 
 

@@ -129,6 +129,46 @@ def test_qlow_gemv_fused(orc, pq, dev, kind, bits, N, K):
         assert torch.equal(y.view(torch.int16), want.view(torch.int16))
 
 
+# The gate/up GEMV with the SwiGLU epilogue equals pq_rmsnorm, pq_qlow_gemv of
+# the 2F rows (bf16) and pq_silu_mul, bit for bit. F covers the three rows per
+# half (8: F=1024 and 1056, 16: F=3072, 32: F=8192 and 16384 at K=2048, halved
+# to 16 at K=4096), a tile count that is not a multiple of 8 (F=1056), both K
+# slice counts and the three per-thread prologue widths.
+@pytest.mark.parametrize("kind,bits,F,K", [("resnorm", 4, 8192, 2048), ("resnorm", 5, 1024, 4096),
+                                           ("norm", 4, 3072, 8192), ("norm", 5, 16384, 2048),
+                                           ("resnorm", 4, 16384, 4096), ("norm", 4, 1056, 2048)])
+def test_qlow_gemv_fused_swiglu(orc, pq, dev, kind, bits, F, K):
+    print(f"qlow swiglu {kind} bits={bits} F={F} K={K}", flush=True)
+    Q, S, _ = _case(orc, 2 * F, K, bits, 7 * F + K + bits)
+    w = pq.QlowWeight(torch.from_numpy(Q).to(dev), torch.from_numpy(S.view(np.int16)).to(dev), bits)
+    g = torch.Generator(device=dev)
+    g.manual_seed(F + 5 * K + bits)
+    bf = lambda *shape, s=1.0: (torch.randn(shape, device=dev, generator=g) * s).to(torch.bfloat16)
+    x = bf(K, s=4.0)
+    w0, w1 = torch.rand(K, device=dev, generator=g) + 0.5, torch.rand(K, device=dev, generator=g) + 0.5
+    if kind == "resnorm":
+        h = bf(K, s=30.0)
+        x1 = x.clone()
+        xin, _, _ = pq.rmsnorm(x1, w0, h=h, w1=w1)
+        xo = torch.empty(K, dtype=torch.int16, device=dev)
+        y = pq.qlow_gemv_fused_swiglu(w, pq.PRO_RESNORM, h=h.view(torch.int16), x_in=x.view(torch.int16), x_out=xo,
+                                      w0=w0, w1=w1)
+        torch.cuda.synchronize()
+        assert torch.equal(xo, x1.view(torch.int16))
+    else:
+        xin, _, _ = pq.rmsnorm(x.clone(), w0)
+        y = pq.qlow_gemv_fused_swiglu(w, pq.PRO_NORM, x_in=x.view(torch.int16), w0=w0)
+    gu = pq.qlow_gemv(w, xin, out_dtype=pq.DT_BF16)
+    # pq_silu_mul takes F a multiple of 256: gate and up each padded with zeros
+    # (an elementwise op; the first F outputs are the ones wanted)
+    Fp = -(-F // 256) * 256
+    gp = torch.zeros(2 * Fp, dtype=torch.bfloat16, device=dev)
+    gp[:F], gp[Fp:Fp + F] = gu[:F], gu[F:]
+    want, _, _ = pq.silu_mul(gp, Fp, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), want.reshape(Fp)[:F].view(torch.int16))
+
+
 def test_qlow_gemv_fused_rejects(pq, dev):
     """Shapes and kinds the fused form does not take fail with an error."""
     w = pq.QlowWeight(torch.zeros((64, 1024), dtype=torch.uint8, device=dev),
@@ -141,6 +181,8 @@ def test_qlow_gemv_fused_rejects(pq, dev):
                        torch.zeros((64, 64, 2), dtype=torch.int16, device=dev), 4)
     with pytest.raises(pq.PQError, match="prologue kind"):
         pq.qlow_gemv_fused(w2, pq.PRO_F32, xf=torch.zeros(2048, device=dev))
+    with pytest.raises(pq.PQError, match="RESNORM or NORM"):
+        pq.qlow_gemv_fused_swiglu(w2, pq.PRO_SILU, gu=torch.zeros(4096, dtype=torch.int16, device=dev))
 
 
 # T positions in one launch equal the per-position GEMV row by row, bit for
