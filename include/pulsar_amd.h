@@ -232,8 +232,11 @@ unsigned pq_crc32(unsigned crc, const void *data, size_t n);
  * stride (position-first). Each op rounds once to bf16 where the reference's
  * kernel does (lfm3_nanode.cu:383-498, 811-941). */
 
-/* RMSNorm of T rows of H (a power of two, 64..8192), sum of squares as a
- * pairwise tree, rs = 1/sqrtf(ss/H + eps), y = bf16(w * bf16(x * rs)).
+/* RMSNorm of T rows of H (a power of two, 256..8192), the sum of squares in
+ * rmsnorm_body's order (threads of 8 consecutive elements summed pairwise,
+ * the shfl_down tree over 32 threads, the partials of each 256 elements in
+ * order), rs = 1/sqrtf(ss * (1/H) + eps), y = bf16(w * bf16(x * rs)) (the
+ * reference's rsqrtf is the one step taken correctly rounded instead).
  * Residual form (h != NULL): h3 = rmsnorm(h, w0); x = bf16(x + h3) (x is
  * updated in place); out = rmsnorm(x, w1) -- one call for layer_body's
  * "rms1(post_norm) -> eadd -> rms1(next_norm)" triple (3819-3851). The
@@ -247,8 +250,10 @@ int pq_rmsnorm(uint16_t *x, const uint16_t *h, const float *w0, const float *w1,
  * qkv rows hold [q (nh*hd) | k (nkv*hd) | v (nkv*hd) | ...] with row_stride
  * elements; q is updated in place. head_dim 64 or 128; the table and rot are
  * the layer type's (full attention: partial rotation, theta 1e6; sliding:
- * full rotation, theta 1e4 -- lfm3_nanode.cu:3756-3765). Replaces k_headnorm,
- * k_rope and the KV write (460-498, 157-162, 3749-3778). */
+ * full rotation, theta 1e4 -- lfm3_nanode.cu:3756-3765). The head norm's sum
+ * of squares is k_headnorm's: 32 threads of hd/32 consecutive elements summed
+ * pairwise, then the shfl_down tree. Replaces k_headnorm, k_rope and the KV
+ * write (460-498, 157-162, 3749-3778). */
 int pq_qk_prep(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm,
                const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv,
                int hd, int rot, int T, float eps, void *stream);
@@ -282,8 +287,10 @@ int pq_silu_mul(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, i
 int pq_silu_mul_interleaved(const uint16_t *gu, uint16_t *y, int8_t *qx, float *dx, int F, int T,
                             void *stream);
 
-/* Greedy id: the lowest index among the maxima of v[n]. Replaces k_argmax
- * (942-964; the reference breaks ties by thread slot). */
+/* Greedy id: k_argmax's pick among v[n] (942-964): the largest value above
+ * -1e30, ties in its order -- the smallest (bitrev3(i/32 mod 8), bitrev5(i mod
+ * 32)), then the smallest i -- and -1 when no value exceeds -1e30. Replaces
+ * k_argmax. */
 int pq_argmax(const float *v, int n, int32_t *out, void *stream);
 
 /* Embedding rows of T token ids (device) from the packed tied Q8_0 table:
@@ -305,8 +312,8 @@ int pq_embed_rows(const int8_t *codes, const float *scales, const int32_t *token
  * launches it, 3536-3573): per row, leaf L = 0..31 sums the products of
  * elements L, L+32, ... in order, each rounded before its add, then the
  * shfl_down tree 16, 8, 4, 2, 1 over the leaves. argmax_parts (NULL or
- * 2 * pq_bf16_gemv_parts(N) floats) receives each workgroup's (largest y, its
- * row; the lowest row on ties) for pq_argmax_parts. */
+ * 2 * pq_bf16_gemv_parts(N) floats) receives each workgroup's (y, row) pick
+ * in pq_argmax's order for pq_argmax_parts. */
 int pq_embed_bf16(const uint16_t *table, const int32_t *tokens, uint16_t *out, int H, int vocab, int T,
                   void *stream);
 int pq_bf16_gemv_parts(int N);
@@ -333,7 +340,8 @@ int pq_bf16_gemv(const uint16_t *W, const uint16_t *x, float *y, int N, int K, f
  *                   exactly as pq_q8_quant_f32
  * K is the GEMV's K (a power of two, 1024..8192). argmax_parts (optional,
  * 2 floats per workgroup, pq_q8_gemv_parts(N, K) of them) receives each
- * workgroup's (max, index) for pq_argmax_parts -- the LM head + k_argmax. */
+ * workgroup's (value, index) pick in pq_argmax's order for pq_argmax_parts --
+ * the LM head + k_argmax. The norms' sums of squares are pq_rmsnorm's. */
 #define PQ_PRO_Q8 0
 #define PQ_PRO_RESNORM 1
 #define PQ_PRO_NORM 2

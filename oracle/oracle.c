@@ -526,39 +526,87 @@ void orc_tq2_gemv(const uint8_t *codes, const uint16_t *S, const uint8_t *xq, fl
 
 /* Pairwise (balanced binary) sum in natural order: n == 1 -> v[0], else
  * fl(pw(first floor(n/2)) + pw(rest)). For n a power of two this is exactly
- * the xor-butterfly across lanes the kernels use. */
+ * the xor-butterfly across lanes the attention kernels use for a split's
+ * softmax denominator. */
 float orc_pairwise(const float *v, int n) {
   if (n == 1) return v[0];
   const int h = n / 2;
   return orc_pairwise(v, h) + orc_pairwise(v + h, n - h);
 }
 
+/* The shfl_down tree of a 32-thread warp (lfm3_nanode.cu:398, 470): at
+ * offset o = 16, 8, 4, 2, 1 thread l < o adds thread l + o's value; thread 0
+ * ends with the warp's sum. */
+static float orc_warp_tree(float *s) {
+  for (int o = 16; o > 0; o >>= 1)
+    for (int l = 0; l < o; l++) s[l] = s[l] + s[l + o];
+  return s[0];
+}
+
+/* The sum of squares of rmsnorm_body (lfm3_nanode.cu:383-440): thread l of
+ * warp w holds elements 256w + 8l .. 256w + 8l + 7 and sums their squares
+ * pairwise, the warp's 32 sums go through the shfl_down tree, and the n/256
+ * warp partials add in order from warp 0. n a multiple of 256 (the reference
+ * runs n = 2048: 256 threads, 8 warps). */
+float orc_rms_sumsq(const uint16_t *x, int n) {
+  float tot = 0.0f;
+  for (int w = 0; w < n / 256; w++) {
+    float s[32];
+    for (int l = 0; l < 32; l++) {
+      float q[8];
+      for (int j = 0; j < 8; j++) {
+        const float v = orc_bf2f(x[256 * w + 8 * l + j]);
+        q[j] = v * v;
+      }
+      s[l] = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+    }
+    const float p = orc_warp_tree(s);
+    tot = w == 0 ? p : tot + p;
+  }
+  return tot;
+}
+
 /* RMSNorm, bf16 in/out, fp32 weight (lfm3_nanode.cu:383-440 rmsnorm_body):
- *   ss = pairwise(x_i^2), v = fl(fl(ss / n) + eps), rs = fl(1 / fl(sqrt(v)))
+ *   ss = orc_rms_sumsq(x), v = fl(fl(ss * fl(1/n)) + eps), rs = fl(1 / fl(sqrt(v)))
  *   y_i = bf16(fl(w_i * bf16(fl(x_i * rs))))   -- round BEFORE the weight
- * The reference's per-thread-then-warp-tree sum (383-440) and the NEON
- * 8-accumulator order (lfm3_elem_test.c:35-45) are both fixed trees; the GPU
- * path and this restatement fix the pairwise tree, which wave64 butterflies produce exactly. The
- * reference uses rsqrtf on the device and 1/sqrtf on the CPU (lfm3_elem_test.c:
- * 45); both sides here use the correctly rounded 1/sqrtf. n is a power of two. */
+ * The reference takes rs = rsqrtf(v) on the device (an approximation CUDA
+ * does not specify bit for bit) and 1/sqrtf on the CPU (lfm3_elem_test.c:45);
+ * both sides here use the correctly rounded 1/sqrtf. n a multiple of 256. */
 void orc_rmsnorm(const uint16_t *x, const float *w, uint16_t *y, int n, float eps) {
-  float *sq = (float *)malloc((size_t)n * sizeof(float));
-  for (int i = 0; i < n; i++) { const float v = orc_bf2f(x[i]); sq[i] = v * v; }
-  const float ss = orc_pairwise(sq, n);
-  free(sq);
-  const float rs = 1.0f / sqrtf(ss / (float)n + eps);
+  const float ss = orc_rms_sumsq(x, n);
+  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)n) + eps);
   for (int i = 0; i < n; i++) {
     const float rounded = orc_bf2f(orc_f2bf(orc_bf2f(x[i]) * rs));
     y[i] = orc_f2bf(w[i] * rounded);
   }
 }
 
-/* Per-head RMSNorm over head_dim, in place (lfm3_nanode.cu:460-479 k_headnorm). */
+/* The sum of squares of k_headnorm (lfm3_nanode.cu:460-479) over one head:
+ * 32 threads of e = hd/32 consecutive elements (4 at hd = 128, the
+ * reference's; 2 at hd = 64, which it does not run), their squares summed
+ * pairwise (the reference's trailing + 0 leaves a sum of squares unchanged),
+ * then the shfl_down tree. */
+float orc_head_sumsq(const uint16_t *x, int hd) {
+  const int e = hd / 32;
+  float s[32];
+  for (int l = 0; l < 32; l++) {
+    float q[4];
+    for (int j = 0; j < e; j++) {
+      const float v = orc_bf2f(x[e * l + j]);
+      q[j] = v * v;
+    }
+    s[l] = e == 4 ? (q[0] + q[1]) + (q[2] + q[3]) : q[0] + q[1];
+  }
+  return orc_warp_tree(s);
+}
+
+/* Per-head RMSNorm over head_dim, in place (k_headnorm): orc_head_sumsq, then
+ * the rounding steps of orc_rmsnorm with n = hd. */
 void orc_headnorm(uint16_t *x, const float *w, int nheads, int hd, float eps) {
-  uint16_t tmp[1024];
   for (int h = 0; h < nheads; h++) {
-    orc_rmsnorm(x + (size_t)h * hd, w, tmp, hd, eps);
-    memcpy(x + (size_t)h * hd, tmp, (size_t)hd * 2);
+    uint16_t *xr = x + (size_t)h * hd;
+    const float rs = 1.0f / sqrtf(orc_head_sumsq(xr, hd) * (1.0f / (float)hd) + eps);
+    for (int i = 0; i < hd; i++) xr[i] = orc_f2bf(w[i] * orc_bf2f(orc_f2bf(orc_bf2f(xr[i]) * rs)));
   }
 }
 
@@ -750,14 +798,36 @@ void orc_sigmoid_gate(const uint16_t *g, uint16_t *attn, int nh, int hd) {
   }
 }
 
-/* Greedy argmax: the LOWEST index among the maxima (strict > scan). The
- * reference's k_argmax (lfm3_nanode.cu:942-964) breaks ties by thread slot;
- * the GPU path and this restatement both take the lowest index. */
+/* Greedy argmax as k_argmax (lfm3_nanode.cu:942-964) picks it: thread t of
+ * 256 scans i = t, t + 256, ... keeping the first value strictly above its
+ * best (from -1e30, index -1); the 32 lanes of each warp then fold with the
+ * shfl_down tree, lane l < o taking lane l + o's pair only when its value is
+ * strictly larger, and the 8 warp pairs fold the same way. -1 when no value
+ * exceeds -1e30. */
 int orc_argmax(const float *v, int n) {
-  int bi = 0;
-  float bv = v[0];
-  for (int i = 1; i < n; i++) if (v[i] > bv) { bv = v[i]; bi = i; }
-  return bi;
+  float bv[256];
+  int bi[256];
+  for (int t = 0; t < 256; t++) {
+    bv[t] = -1e30f;
+    bi[t] = -1;
+    for (int i = t; i < n; i += 256)
+      if (v[i] > bv[t]) { bv[t] = v[i]; bi[t] = i; }
+  }
+  float wv[8];
+  int wi[8];
+  for (int w = 0; w < 8; w++) {
+    float *sv = bv + 32 * w;
+    int *si = bi + 32 * w;
+    for (int o = 16; o > 0; o >>= 1)
+      for (int l = 0; l < o; l++)
+        if (sv[l + o] > sv[l]) { sv[l] = sv[l + o]; si[l] = si[l + o]; }
+    wv[w] = sv[0];
+    wi[w] = si[0];
+  }
+  for (int o = 4; o > 0; o >>= 1)
+    for (int l = 0; l < o; l++)
+      if (wv[l + o] > wv[l]) { wv[l] = wv[l + o]; wi[l] = wi[l + o]; }
+  return wi[0];
 }
 
 /* Embedding row from the tied Q8 table: bf16(fl(code * scale)) (lfm3_nanode.cu:

@@ -72,6 +72,8 @@ void orc_tq2_gemv(const uint8_t *codes, const uint16_t *S, const uint8_t *xq, fl
 
 /* ------------------------------------------------------ layer primitives */
 float orc_pairwise(const float *v, int n);
+float orc_rms_sumsq(const uint16_t *x, int n);
+float orc_head_sumsq(const uint16_t *x, int hd);
 void orc_rmsnorm(const uint16_t *x, const float *w, uint16_t *y, int n, float eps);
 void orc_headnorm(uint16_t *x, const float *w, int nheads, int hd, float eps);
 int orc_max_threads(void);

@@ -44,6 +44,8 @@ def lib():
         L.orc_sm64_at.argtypes = [C.c_uint64, C.c_uint64]
         L.orc_argmax.restype = C.c_int
         L.orc_pairwise.restype = C.c_float
+        L.orc_rms_sumsq.restype = C.c_float
+        L.orc_head_sumsq.restype = C.c_float
         L.orc_model_create.restype = C.c_void_p
         L.orc_model_feed.restype = C.c_int
         L.orc_model_tensor.restype = C.c_int
@@ -245,6 +247,18 @@ def rmsnorm(x, w, eps=1e-5):
         lib().orc_rmsnorm(_p(xr[t]), _p(np.ascontiguousarray(w, np.float32)), _p(yr[t]),
                           C.c_int(n), C.c_float(eps))
     return y
+
+
+def rms_sumsq(x):
+    """RMSNorm's sum of squares of bf16 x in rmsnorm_body's order."""
+    x = np.ascontiguousarray(x, np.uint16)
+    return np.float32(lib().orc_rms_sumsq(_p(x), C.c_int(x.size)))
+
+
+def head_sumsq(x):
+    """A head norm's sum of squares of bf16 x [hd] in k_headnorm's order."""
+    x = np.ascontiguousarray(x, np.uint16)
+    return np.float32(lib().orc_head_sumsq(_p(x), C.c_int(x.size)))
 
 
 def headnorm(x, w, nheads, hd, eps=1e-5):

@@ -47,8 +47,8 @@ __device__ __forceinline__ void slice_load(SliceRegs &s, __amdgpu_buffer_rsrc_t 
   }
 }
 
-// Per workgroup: y for its rows and, with parts, (largest y, its row; the
-// lowest row on ties) at parts[2 * blockIdx.x].
+// Per workgroup: y for its rows and, with parts, the (y, row) of its rows'
+// pick in k_argmax's order (am_better) at parts[2 * blockIdx.x].
 __global__ __launch_bounds__(64 * kB16Waves) void bf16_gemv_kernel(const uint16_t *__restrict__ W,
                                                                      const uint16_t *__restrict__ x,
                                                                      float *__restrict__ y, int N, int K,
@@ -70,8 +70,8 @@ __global__ __launch_bounds__(64 * kB16Waves) void bf16_gemv_kernel(const uint16_
   slice_load(cur, wr, row0 + 2 * wave, N, K, 0, lane);
   for (int i = threadIdx.x; i < K; i += 64 * kB16Waves) xs[i] = bf2f(x[i]);
   __syncthreads();
-  float best = -__builtin_inff();
-  int besti = 0x7fffffff;
+  float best = kAmFloor;
+  int besti = -1;
   for (int pp = 0; pp < npairs; pp++) {
     const int ra = row0 + 2 * wave + 2 * kB16Waves * pp;   // this pass's row pair: ra, ra + 1
     float s = 0.0f;
@@ -101,15 +101,18 @@ __global__ __launch_bounds__(64 * kB16Waves) void bf16_gemv_kernel(const uint16_
     const int r = ra + half;
     if (leaf == 0 && r < N) {
       y[r] = s;
-      if (s > best || (s == best && r < besti)) { best = s; besti = r; }
+      float cv;
+      int ci;
+      am_leaf(s, r, cv, ci);
+      if (am_better(cv, ci, best, besti)) { best = cv; besti = ci; }
     }
   }
   if (parts == nullptr) return;
-  // (value, row) of the workgroup's largest output, the lowest row on ties
+  // (value, row) of the workgroup's pick in k_argmax's order (am_better)
   {
     const float ov = __shfl(best, 32, 64);
     const int oi = __shfl(besti, 32, 64);
-    if (ov > best || (ov == best && oi < besti)) { best = ov; besti = oi; }
+    if (am_better(ov, oi, best, besti)) { best = ov; besti = oi; }
   }
   if (lane == 0) { bv[wave] = best; bi[wave] = besti; }
   __syncthreads();
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(64 * kB16Waves) void bf16_gemv_kernel(const uint16_
     float v = bv[0];
     int idx = bi[0];
     for (int w = 1; w < kB16Waves; w++)
-      if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+      if (am_better(bv[w], bi[w], v, idx)) { v = bv[w]; idx = bi[w]; }
     parts[2 * blockIdx.x] = v;
     parts[2 * blockIdx.x + 1] = __int_as_float(idx);
   }

@@ -17,8 +17,9 @@
 //   Q8       y already quantized (qx, dx)
 //   F32      y = fp32 x, quantized here
 // then quantizes y to Q8_0 in LDS and runs the GEMV of q8.hip on it. Every op
-// keeps the unfused kernels' arithmetic and order (pairwise sums of squares,
-// the same roundings), so the fused step is bit-identical to the unfused one.
+// keeps the unfused kernels' arithmetic and order (the sums of squares in
+// rmsnorm_body's order, the same roundings), so the fused step is
+// bit-identical to the unfused one.
 // The attention mixer of a decode step is one kernel per layer
 // (attn_layer_kernel): q/k norm, RoPE, KV write, every split, the ordered
 // merge, the sigmoid gate and the Q8_0 output for o_proj.
@@ -104,7 +105,8 @@ __device__ __forceinline__ void pro_compute(const pq_gemv_prologue &p, int e0, i
 // pq_q8_pack_gate_up: lane l < 32 holds gate row 32*tile + l, lane l + 32 its
 // up row; writes the Q8_0 block tile of silu(gate) * up as silu_mul_kernel +
 // quant_store form it), else y (bf16 or fp32) and, with parts, the (value,
-// index) of the largest output (lowest index on ties) at parts[2*part].
+// index) of the pick among its outputs in k_argmax's order (am_better) at
+// parts[2*part].
 template <int R>
 __device__ __forceinline__ void fused_epilogue(float yv, int lane, int tile, int row, int part, void *__restrict__ y,
                                                int y_bf16, int N, float *__restrict__ parts, int8_t *__restrict__ qo,
@@ -129,13 +131,14 @@ __device__ __forceinline__ void fused_epilogue(float yv, int lane, int tile, int
     else reinterpret_cast<float *>(y)[row] = yv;
   }
   if (parts != nullptr) {
-    float v = (lane < R && row < N) ? yv : -__builtin_inff();
-    int idx = (lane < R && row < N) ? row : 0x7fffffff;
+    float v;
+    int idx;
+    am_leaf((lane < R && row < N) ? yv : kAmFloor, row, v, idx);
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const float ov = __shfl_xor(v, o, 64);
       const int oi = __shfl_xor(idx, o, 64);
-      if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+      if (am_better(ov, oi, v, idx)) { v = ov; idx = oi; }
     }
     if (lane == 0) {
       parts[2 * part] = v;
@@ -148,8 +151,8 @@ __device__ __forceinline__ void fused_epilogue(float yv, int lane, int tile, int
 // The GEMV of q8.hip (R rows per workgroup, chunk slots per lane, rounds with an
 // ordered LDS fold) with x from the prologue: 64*W threads, E = K/(64*W)
 // contiguous elements of the prologue per thread. Optional argmax partials:
-// each workgroup writes the (value, index) of the largest of its outputs
-// (lowest index on ties) for pq_argmax_parts.
+// each workgroup writes the (value, index) of its outputs' pick in
+// k_argmax's order (am_better) for pq_argmax_parts.
 template <int R, int PRO, int E>
 __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__restrict__ pc,
                                                              const uint16_t *__restrict__ ps, pq_gemv_prologue p,
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
                                                              float *__restrict__ dqo) {
   constexpr int C = 64 / R;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float red[16];
+  __shared__ __align__(16) float red[2 * kNormSlots];
   const int nb = K / kQ, nch = nchunks(K);  // K a power of two >= 1024: every chunk is full
   const int W = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -172,7 +175,6 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
   const int nrounds = (nch + per_round - 1) / per_round;
   const int slot = wave * C + cs;
   const int e0 = threadIdx.x * E;
-  if (threadIdx.x >= W && threadIdx.x < 8) red[threadIdx.x] = red[8 + threadIdx.x] = 0.0f;
   // 1. the prologue's global loads, then round 0's weight loads, then the
   //    prologue math: its waits leave the weight loads in flight
   ProRegs<E, conv_taps(PRO)> pr;
@@ -227,8 +229,8 @@ __global__ __launch_bounds__(512) void q8_gemv_fused_kernel(const int8_t *__rest
 // SWI: the tile is 4 gate rows t*4 + w and their up rows F + t*4 + w (codes
 // [2F][K], F = N/2), wave w holding gate row t*4 + w in lanes 0-31 and its up
 // row in lanes 32-63; lane 0 forms silu_mul_kernel's output from the bf16
-// gate and up values (no barrier per tile). Else, with parts: the workgroup's (largest y, its row; the
-// lowest row on ties) at parts[2 * blockIdx.x].
+// gate and up values (no barrier per tile). Else, with parts: the (y, row) of
+// the workgroup's pick in k_argmax's order (am_better) at parts[2 * blockIdx.x].
 template <int BPL, int PRO, int E, int NS, bool SWI>
 __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t *__restrict__ codes,
                                                                    const float *__restrict__ scales,
@@ -237,11 +239,10 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
                                                                    float *__restrict__ parts) {
   constexpr int W = kRThreads / 64;
   extern __shared__ __align__(16) float rxs[];   // [nb][kRXStride]
-  __shared__ float red[16];
+  __shared__ __align__(16) float red[2 * kNormSlots];
   const int nb = K / kQ, KC = q8r_chunk(K), nbc = KC / kQ, nch = K / KC;
   const int r = threadIdx.x >> 5, L = threadIdx.x & 31, F = N >> 1;
   auto row_of = [&](int t) { return SWI ? ((r & 1) ? F : 0) + t * (kRRows / 2) + (r >> 1) : t * kRRows + r; };
-  if (threadIdx.x >= W && threadIdx.x < 8) red[threadIdx.x] = red[8 + threadIdx.x] = 0.0f;
   const __amdgpu_buffer_rsrc_t rc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(codes), (short)0, N * K, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rs =
@@ -263,8 +264,8 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
     for (int i = 0; i < E; i += 4) *reinterpret_cast<float4 *>(d + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
   }
   lds_barrier();
-  float yv = 0.0f, best = -__builtin_inff();
-  int bidx = 0x7fffffff;
+  float yv = 0.0f, best = kAmFloor;
+  int bidx = -1;
   // fold chunk cc of tile tt (lane L = 0 of each row holds the partial); the
   // tile's last chunk writes its outputs
   auto step = [&](const RBlocks &B, int tt, int cc) {
@@ -282,7 +283,10 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
       if (L == 0 && row < N) {
         if (y_bf16) reinterpret_cast<uint16_t *>(y)[row] = f2bf(yv);
         else reinterpret_cast<float *>(y)[row] = yv;
-        if (yv > best || (yv == best && row < bidx)) { best = yv; bidx = row; }
+        float cv;
+        int ci;
+        am_leaf(yv, row, cv, ci);
+        if (am_better(cv, ci, best, bidx)) { best = cv; bidx = ci; }
       }
     }
     yv = 0.0f;
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
       lds_barrier();
       if (threadIdx.x == 0) {
         for (int i = 1; i < kRRows; i++)
-          if (pb[i] > best || (pb[i] == best && pi[i] < bidx)) { best = pb[i]; bidx = pi[i]; }
+          if (am_better(pb[i], pi[i], best, bidx)) { best = pb[i]; bidx = pi[i]; }
         parts[2 * blockIdx.x] = best;
         parts[2 * blockIdx.x + 1] = __int_as_float(bidx);
       }
@@ -315,7 +319,8 @@ __global__ __launch_bounds__(kRThreads) void q8r_gemv_fused_kernel(const int8_t 
   }
 }
 
-// (value, index) partials -> the lowest index among the maxima.
+// (value, index) partials -> the pick in k_argmax's order (am_better); -1
+// when no output exceeds kAmFloor.
 // With ctr (the engine's replayed decode step): also ids[ctr[0]++] = the id and
 // ctr[1]++ (the position).
 __global__ __launch_bounds__(1024) void argmax_parts_kernel(const float *__restrict__ parts, int n,
@@ -323,26 +328,26 @@ __global__ __launch_bounds__(1024) void argmax_parts_kernel(const float *__restr
                                                              int32_t *__restrict__ ctr) {
   __shared__ float bv[16];
   __shared__ int bi[16];
-  float best = -__builtin_inff();
-  int idx = 0x7fffffff;
+  float best = kAmFloor;
+  int idx = -1;
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const float v = parts[2 * i];
     const int j = __float_as_int(parts[2 * i + 1]);
-    if (v > best || (v == best && j < idx)) { best = v; idx = j; }
+    if (am_better(v, j, best, idx)) { best = v; idx = j; }
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const float ob = __shfl_xor(best, o, 64);
     const int oi = __shfl_xor(idx, o, 64);
-    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    if (am_better(ob, oi, best, idx)) { best = ob; idx = oi; }
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { bv[wave] = best; bi[wave] = idx; }
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < (int)(blockDim.x >> 6); w++)
-      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
-    const int id = idx == 0x7fffffff ? 0 : idx;
+      if (am_better(bv[w], bi[w], best, idx)) { best = bv[w]; idx = bi[w]; }
+    const int id = idx;
     *out = id;
     if (ctr != nullptr) {
       ids[ctr[0]] = id;
@@ -380,13 +385,8 @@ template <int HD>
 __device__ __forceinline__ void norm_rope(const float *x, const float *wv, float c, float sn, int rot, float eps,
                                           int lane, float *r) {
   constexpr int E = HD / 64;
-  float ss = 0.0f, v[E];
-#pragma unroll
-  for (int e = 0; e < E; e++) {
-    const float part = wave_pairwise_sum(x[e] * x[e]);
-    ss = e == 0 ? part : ss + part;
-  }
-  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)HD) + eps);
+  float v[E];
+  const float rs = 1.0f / sqrtf(head_sumsq<HD>(x) * (1.0f / (float)HD) + eps);
 #pragma unroll
   for (int e = 0; e < E; e++) v[e] = bf2f(f2bf(wv[e] * bf2f(f2bf(x[e] * rs))));
   const int half = rot / 2;

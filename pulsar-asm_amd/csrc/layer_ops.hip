@@ -4,9 +4,10 @@
 // gated short conv, silu(gate)*up, argmax and the embedding row lookup.
 //
 // Every op keeps the reference's rounding points (one bf16 round per op,
-// RMSNorm rounding before the weight multiply) and the build's fixed orders:
-// sums of squares are pairwise trees (the wave64 xor butterfly), e^x is
-// pq::expf_pq, 1/sqrt is the correctly rounded 1.0f / sqrtf.
+// RMSNorm rounding before the weight multiply) and its orders where they are
+// fixed ones: sums of squares as rmsnorm_body / k_headnorm add them, argmax
+// ties as k_argmax breaks them; e^x is pq::expf_pq, 1/sqrt the correctly
+// rounded 1.0f / sqrtf (the reference's rsqrtf is the one step not restated).
 #include "pq_device.h"
 #include "pq_host.h"
 #include "pq_internal.h"
@@ -14,35 +15,6 @@
 namespace pq {
 
 // ------------------------------------------------------------------ helpers
-// Pairwise sum over the workgroup: each thread passes the pairwise sum of its
-// E consecutive elements; wave butterfly; then a pairwise tree over the waves
-// (W a power of two). Every thread receives the total.
-__device__ __forceinline__ float block_pairwise(float v, float *red) {
-  v = wave_pairwise_sum(v);
-  const int W = blockDim.x >> 6, wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  for (int n = W; n > 1; n >>= 1) {
-    if ((int)threadIdx.x < n / 2) red[threadIdx.x] = red[2 * threadIdx.x] + red[2 * threadIdx.x + 1];
-    __syncthreads();
-  }
-  const float t = red[0];
-  __syncthreads();
-  return t;
-}
-
-template <int E>
-__device__ __forceinline__ float local_pairwise_sq(const float *v) {
-  float s[E];
-#pragma unroll
-  for (int i = 0; i < E; i++) s[i] = v[i] * v[i];
-#pragma unroll
-  for (int n = E; n > 1; n >>= 1)
-#pragma unroll
-    for (int i = 0; i < n / 2; i++) s[i] = s[2 * i] + s[2 * i + 1];
-  return s[0];
-}
-
 // Q8_0 quantization of a thread's E consecutive bf16 outputs (E <= 32, 32/E
 // threads per block): amax over the block's threads (xor butterfly of max),
 // d = amax/127, q = rne(v/d) clamped -- the same rule as q8_quant_kernel.
@@ -68,15 +40,18 @@ __device__ __forceinline__ void quant_store(const float *v, int8_t *qx, float *d
 }
 
 // ---------------------------------------------------------------- RMSNorm
-// One workgroup per row of H = 256*E... (blockDim * E == H). Optional
-// residual form: h3 = rmsnorm(h, w0); x = bf16(x + h3) (written back);
-// out = rmsnorm(x, w1). The output goes to y (bf16) and/or (qx, dx).
-template <int E, bool RESID>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ x, const uint16_t *__restrict__ h,
-                                                       const float *__restrict__ w0, const float *__restrict__ w1,
-                                                       uint16_t *__restrict__ y, int8_t *__restrict__ qx,
-                                                       float *__restrict__ dx, int H, float eps) {
-  __shared__ float red[8];
+// One workgroup per row of H = 8 * blockDim elements, thread t holding 8
+// consecutive ones as rmsnorm_body's threads do (H = 2048: its 256 threads).
+// Optional residual form: h3 = rmsnorm(h, w0); x = bf16(x + h3) (written
+// back); out = rmsnorm(x, w1). The output goes to y (bf16) and/or (qx, dx).
+template <bool RESID>
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(uint16_t *__restrict__ x, const uint16_t *__restrict__ h,
+                                                        const float *__restrict__ w0, const float *__restrict__ w1,
+                                                        uint16_t *__restrict__ y, int8_t *__restrict__ qx,
+                                                        float *__restrict__ dx, int H, float eps) {
+  constexpr int E = 8;
+  __shared__ __align__(16) float part[64];   // the warp partials of the two sums (H / 256 <= 32 each)
+  const int nparts = H / 256;
   const size_t row = blockIdx.x;
   const int e0 = threadIdx.x * E;
   float v[E];
@@ -85,7 +60,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ x, 
     float hv[E];
 #pragma unroll
     for (int i = 0; i < E; i++) hv[i] = bf2f(h[row * H + e0 + i]);
-    const float ss = block_pairwise(local_pairwise_sq<E>(hv), red);
+    const float ss = ref_sumsq<E, false>(hv, part, nparts);
     const float rs = 1.0f / sqrtf(ss * inv_n + eps);
 #pragma unroll
     for (int i = 0; i < E; i++) {
@@ -101,7 +76,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ x, 
     for (int i = 0; i < E; i++) v[i] = bf2f(x[row * H + e0 + i]);
   }
   const float *w = RESID ? w1 : w0;
-  const float ss = block_pairwise(local_pairwise_sq<E>(v), red);
+  const float ss = ref_sumsq<E, false>(v, part + 32, nparts);
   const float rs = 1.0f / sqrtf(ss * inv_n + eps);
   float o[E];
 #pragma unroll
@@ -117,9 +92,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(uint16_t *__restrict__ x, 
 // One wave per (head, position); lane l holds dimensions l + 64e, e < HD/64
 // (HD = 64 or 128). Heads [0, nh) are q (norm + rope, in place), [nh, nh+nkv)
 // k (norm + rope, then written to the fp16 cache), [nh+nkv, nh+2nkv) v
-// (written to the cache). The sum of squares is the pairwise tree over the
-// head in natural order: the wave's pairwise sum of each 64-dim slice, the
-// slices added pairwise. RoPE pairs (i, i + HD/2) for i < rot/2 (k_rope,
+// (written to the cache). The sum of squares is k_headnorm's (head_sumsq).
+// RoPE pairs (i, i + HD/2) for i < rot/2 (k_rope,
 // lfm3_nanode.cu:483-498): a lane-pair exchange at HD = 64, the lane's own two
 // values at HD = 128. cs is the layer's [pos][rot/2][cos, sin] table.
 template <int HD>
@@ -144,14 +118,9 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv,
   uint16_t *xr = isq ? row + head * HD : row + nh * HD + (head - nh) * HD;
   const float *w = isq ? qn : kn;
   float x[E], v[E];
-  float ss = 0.0f;
 #pragma unroll
-  for (int e = 0; e < E; e++) {
-    x[e] = bf2f(xr[l + 64 * e]);
-    const float part = wave_pairwise_sum(x[e] * x[e]);
-    ss = e == 0 ? part : ss + part;
-  }
-  const float rs = 1.0f / sqrtf(ss * (1.0f / (float)HD) + eps);
+  for (int e = 0; e < E; e++) x[e] = bf2f(xr[l + 64 * e]);
+  const float rs = 1.0f / sqrtf(head_sumsq<HD>(x) * (1.0f / (float)HD) + eps);
 #pragma unroll
   for (int e = 0; e < E; e++) v[e] = bf2f(f2bf(w[l + 64 * e] * bf2f(f2bf(x[e] * rs))));
   const int half = rot / 2;
@@ -267,30 +236,33 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restric
 }
 
 // ------------------------------------------------------------------ argmax
-// Lowest index among the maxima: strict > scans ascending per thread, then a
-// tree that keeps the larger value and, on ties, the smaller index.
+// The pick of k_argmax (am_better: the largest value above kAmFloor, ties in
+// its thread-slot order; -1 when there is none), by any tree: a scan per
+// thread, then the wave butterfly and the waves in order.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ v, int n, int32_t *__restrict__ out) {
   __shared__ float bv[16];
   __shared__ int bi[16];
-  float best = -__builtin_inff();
-  int idx = 0x7fffffff;
+  float best = kAmFloor;
+  int idx = -1;
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float x = v[i];
-    if (x > best) { best = x; idx = i; }
+    float cv;
+    int ci;
+    am_leaf(v[i], i, cv, ci);
+    if (am_better(cv, ci, best, idx)) { best = cv; idx = ci; }
   }
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const float ob = __shfl_xor(best, o, 64);
     const int oi = __shfl_xor(idx, o, 64);
-    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    if (am_better(ob, oi, best, idx)) { best = ob; idx = oi; }
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { bv[wave] = best; bi[wave] = idx; }
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < (int)(blockDim.x >> 6); w++)
-      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
-    *out = idx == 0x7fffffff ? 0 : idx;
+      if (am_better(bv[w], bi[w], best, idx)) { best = bv[w]; idx = bi[w]; }
+    *out = idx;
   }
 }
 
@@ -347,23 +319,12 @@ extern "C" int pq_rmsnorm(uint16_t *x, const uint16_t *h, const float *w0, const
   PQ_REQUIRE(x && w0 && (y || qx), PQ_ERR_ARG, "pq_rmsnorm: null pointer");
   PQ_REQUIRE(!h || w1, PQ_ERR_ARG, "pq_rmsnorm: the residual form needs w1");
   PQ_REQUIRE(!qx || dx, PQ_ERR_ARG, "pq_rmsnorm: qx without dx");
-  PQ_REQUIRE(pow2(H) && H >= 64 && H <= 8192 && T > 0, PQ_ERR_ARG, "pq_rmsnorm: H=%d (power of two, 64..8192)", H);
-  const int threads = H >= 256 ? 256 : H;
-  const int E = H / threads;
+  PQ_REQUIRE(pow2(H) && H >= 256 && H <= 8192 && T > 0, PQ_ERR_ARG, "pq_rmsnorm: H=%d (power of two, 256..8192)",
+             H);
   hipStream_t st = as_stream(stream);
-  const dim3 grid(T), block(threads);
-#define PQ_RMS(EE)                                                                                                 \
-  if (h) launch(rmsnorm_kernel<EE, true>, grid, block, 0, st, x, h, w0, w1, y, qx, dx, H, eps);                    \
-  else launch(rmsnorm_kernel<EE, false>, grid, block, 0, st, x, h, w0, w1, y, qx, dx, H, eps);
-  switch (E) {
-    case 1: PQ_RMS(1) break;
-    case 2: PQ_RMS(2) break;
-    case 4: PQ_RMS(4) break;
-    case 8: PQ_RMS(8) break;
-    case 16: PQ_RMS(16) break;
-    default: PQ_RMS(32) break;
-  }
-#undef PQ_RMS
+  const dim3 grid(T), block(H / 8);
+  if (h) launch(rmsnorm_kernel<true>, grid, block, 0, st, x, h, w0, w1, y, qx, dx, H, eps);
+  else launch(rmsnorm_kernel<false>, grid, block, 0, st, x, h, w0, w1, y, qx, dx, H, eps);
   return check_launch("pq_rmsnorm");
 }
 

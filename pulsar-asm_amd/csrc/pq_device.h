@@ -194,4 +194,165 @@ __device__ __forceinline__ lds_ptr<T> lds_base(const T *p) {
 // layer whose window the context has outgrown (k_attn_head, lfm3_nanode.cu:515).
 __device__ __forceinline__ int window_lo(int npos, int win) { return (win > 0 && npos > win) ? npos - win : 0; }
 
+// ------------------------------------------ the reference's reduction orders
+// v + (the value D lanes up), exact at every lane l with l mod 2D < D (the
+// lanes a shfl_down tree step reads on): D = 1, 2 by quad permutes, 4 and 8
+// by 16-lane row rotates (row_ror:n reads lane l - n mod 16), 16 and 32 by the
+// permlane row / half swaps (lane for lane).
+template <int D>
+__device__ __forceinline__ float add_down(float v) {
+  if constexpr (D == 1) return v + dpp_f<kDppXor1>(v);
+  else if constexpr (D == 2) return v + dpp_f<kDppXor2>(v);
+  else if constexpr (D == 4) return v + dpp_f<0x12c>(v);   // row_ror:12
+  else if constexpr (D == 8) return v + dpp_f<0x128>(v);   // row_ror:8
+  else if constexpr (D == 16) return add_row_pair(v);
+  else return add_half_pair(v);
+}
+
+// One step (offset O, in reference threads) of the shfl_down tree of
+// rmsnorm_body over a thread's t[R] (R reference threads per lane, or LPR
+// lanes per reference thread).
+template <int E, int O>
+__device__ __forceinline__ void ref_tree_step(float *t) {
+  constexpr int R = E >= 8 ? E / 8 : 1, LPR = E >= 8 ? 1 : 8 / E;
+  if constexpr (O >= R) {
+#pragma unroll
+    for (int j = 0; j < R; j++) t[j] = add_down<(O / R) * LPR>(t[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j + O < R; j++) t[j] = t[j] + t[j + O];
+  }
+}
+
+// ((p[0] + p[1]) + p[2]) + ... over NP values of LDS, all read first.
+template <int NP>
+__device__ __forceinline__ float ordered_sum_n(const float *p) {
+  float v[NP];
+  if constexpr (NP % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < NP / 4; i++) {
+      const float4 q = reinterpret_cast<const float4 *>(p)[i];
+      v[4 * i] = q.x;
+      v[4 * i + 1] = q.y;
+      v[4 * i + 2] = q.z;
+      v[4 * i + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NP; i++) v[i] = p[i];
+  }
+  float t = v[0];
+#pragma unroll
+  for (int i = 1; i < NP; i++) t = t + v[i];
+  return t;
+}
+// the same for n = 1, 2, 4, .. 32 (a uniform branch); p 16-byte aligned
+__device__ __forceinline__ float ordered_sum(const float *p, int n) {
+  switch (n) {
+    case 1: return p[0];
+    case 2: return ordered_sum_n<2>(p);
+    case 4: return ordered_sum_n<4>(p);
+    case 8: return ordered_sum_n<8>(p);
+    case 16: return ordered_sum_n<16>(p);
+    default: return ordered_sum_n<32>(p);
+  }
+}
+
+// The sum of squares of RMSNorm in the reference's order (rmsnorm_body,
+// lfm3_nanode.cu:383-440): a thread of 8 consecutive elements sums their
+// squares pairwise, a warp of 32 such threads folds them with the shfl_down
+// tree (offsets 16, 8, 4, 2, 1: s_l + s_{l+o}), and the warp partials (one per
+// 256 elements) add in order from the first. Here workgroup thread t holds
+// elements tE .. tE + E - 1 (E = 4 .. 32): a reference thread is a lane pair
+// (E = 4) or an 8-element piece of a lane, and the tree's offsets become lane
+// offsets or sums within the lane. part (16-byte aligned LDS) gets the
+// nparts = n/256 partials (1, 2, 4, .. 32; one barrier, LDS-only with LDSB);
+// every thread returns the total.
+template <int E, bool LDSB>
+__device__ __forceinline__ float ref_sumsq(const float *v, float *part, int nparts) {
+  static_assert(E == 4 || E == 8 || E == 16 || E == 32, "4 .. 32 elements per thread");
+  constexpr int R = E >= 8 ? E / 8 : 1, LPR = E >= 8 ? 1 : 8 / E;
+  float t[R];
+  if constexpr (E == 4) {
+    t[0] = add_down<1>((v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]));
+  } else {
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const float *e = v + 8 * j;
+      t[j] = ((e[0] * e[0] + e[1] * e[1]) + (e[2] * e[2] + e[3] * e[3])) +
+             ((e[4] * e[4] + e[5] * e[5]) + (e[6] * e[6] + e[7] * e[7]));
+    }
+  }
+  ref_tree_step<E, 16>(t);
+  ref_tree_step<E, 8>(t);
+  ref_tree_step<E, 4>(t);
+  ref_tree_step<E, 2>(t);
+  ref_tree_step<E, 1>(t);
+  constexpr int S = 32 * LPR / R;   // lanes per reference warp
+  const int lane = threadIdx.x & 63;
+  if ((lane & (S - 1)) == 0) part[(threadIdx.x >> 6) * (64 / S) + lane / S] = t[0];
+  if constexpr (LDSB) lds_barrier();
+  else __syncthreads();
+  return ordered_sum(part, nparts);
+}
+
+// The sum of squares of a head norm in the reference's order (k_headnorm,
+// lfm3_nanode.cu:460-479): 32 threads of HD/32 consecutive elements (4 at
+// HD = 128; HD = 64, which the reference does not run, takes 2), each summed
+// pairwise, then the shfl_down tree; the trailing + 0 of the reference leaves
+// a sum of squares unchanged. Lane l of the wave holds elements l and l + 64
+// (x[0], x[1]) at HD = 128, element l at HD = 64; every lane gets lane 0's
+// total.
+template <int HD>
+__device__ __forceinline__ float head_sumsq(const float *x) {
+  float s;
+  if constexpr (HD == 128) {   // thread m < 16: lanes 4m..4m+3 of x[0]; m >= 16: of x[1]
+    float a = x[0] * x[0], b = x[1] * x[1];
+    a = add_down<2>(add_down<1>(a));
+    b = add_down<2>(add_down<1>(b));
+    s = a + b;                 // offset 16: threads m and m + 16 share lane 4m
+    s = add_down<32>(s);       // 8
+    s = add_down<16>(s);       // 4
+    s = add_down<8>(s);        // 2
+    s = add_down<4>(s);        // 1
+  } else {                     // thread m: lanes 2m, 2m + 1
+    s = add_down<1>(x[0] * x[0]);
+    s = add_down<32>(s);
+    s = add_down<16>(s);
+    s = add_down<8>(s);
+    s = add_down<4>(s);
+    s = add_down<2>(s);
+  }
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+}
+
+// Greedy argmax in the reference's order (k_argmax, lfm3_nanode.cu:942-964):
+// its 256 threads scan i = tid, tid + 256, ... keeping the first strict
+// maximum above -1e30 (kAmFloor), then two shfl_down trees (the 32 lanes of a
+// warp, then the 8 warps) keep the lower lane's pair unless the other's value
+// is strictly larger. Among equal maxima the last tree step weighs most: the
+// pick has the smallest (bitrev3(warp), bitrev5(lane)) of its thread slot
+// i mod 256, then the smallest i. am_key orders indices that way (no index,
+// -1: the largest key); the pick is the largest value, then the smallest key,
+// a total order that any reduction tree reproduces. No value above kAmFloor
+// gives -1, as the reference's does.
+constexpr float kAmFloor = -1e30f;
+__device__ __forceinline__ uint32_t am_key(int i) {
+  if (i < 0) return 0xffffffffu;
+  const uint32_t s = (uint32_t)i & 255u, w = s >> 5, l = s & 31u;
+  const uint32_t bw = ((w & 1u) << 2) | (w & 2u) | (w >> 2);
+  const uint32_t bl = ((l & 1u) << 4) | ((l & 2u) << 2) | (l & 4u) | ((l >> 2) & 2u) | (l >> 4);
+  return (((bw << 5) | bl) << 24) | ((uint32_t)i >> 8);
+}
+// (v, i) picked over (bv, bi)
+__device__ __forceinline__ bool am_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && am_key(i) < am_key(bi));
+}
+// a candidate (v, i): itself when v > kAmFloor, else no index
+__device__ __forceinline__ void am_leaf(float v, int i, float &bv, int &bi) {
+  const bool ok = v > kAmFloor;
+  bv = ok ? v : kAmFloor;
+  bi = ok ? i : -1;
+}
+
 }  // namespace pq

@@ -2,7 +2,7 @@
 // small ops of a decode step (residual add + RMSNorm, RMSNorm, SiLU * up, the
 // gated short conv, the embedding row) computed by the GEMV that consumes
 // them, redundantly in every workgroup, with the unfused ops' arithmetic and
-// order (pairwise sums of squares, the same bf16 roundings), so a fused step is
+// order (sums of squares in rmsnorm_body's order, the same bf16 roundings), so a fused step is
 // bit-identical to the unfused one. Shared by the Q8_0, reference-numerics and
 // Q4 / Q5 GEMVs.
 #pragma once
@@ -54,24 +54,13 @@ __device__ __forceinline__ void st_bf16w(uint16_t *__restrict__ p, const uint32_
   }
 }
 
-// Pairwise sum of the squares of a thread's E values, then over the workgroup
-// (wave butterfly, then a pairwise tree over 8 wave slots): the pairwise tree
-// over all E*64*W elements in natural order. red holds 8 slots whose entries
-// for absent waves (W < 8) are zero, which leaves every sum of the tree exact.
-// Each call uses its own red slots, so one barrier suffices.
+// The sum of squares of a norm prologue over K = E * blockDim elements, in
+// rmsnorm_body's order (ref_sumsq); red holds kNormSlots partials per sum,
+// so the two sums of RESNORM take red and red + kNormSlots (K <= 8192).
+constexpr int kNormSlots = 32;
 template <int E>
-__device__ __forceinline__ float wg_pairwise_sq(const float *v, float *red) {
-  float s[E];
-#pragma unroll
-  for (int i = 0; i < E; i++) s[i] = v[i] * v[i];
-#pragma unroll
-  for (int n = E; n > 1; n >>= 1)
-#pragma unroll
-    for (int i = 0; i < n / 2; i++) s[i] = s[2 * i] + s[2 * i + 1];
-  const float t = wave_pairwise_sum(s[0]);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
-  lds_barrier();
-  return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+__device__ __forceinline__ float pro_sumsq(const float *v, float *red, int K) {
+  return ref_sumsq<E, true>(v, red, K / 256);
 }
 
 // y = bf16(w * bf16(x * rs)) for the thread's E values.
@@ -173,7 +162,7 @@ __device__ __forceinline__ void pro_values(const pq_gemv_prologue &p, int e0, in
   if constexpr (PRO == PQ_PRO_RESNORM) {
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
-    const float ss = wg_pairwise_sq<E>(v, red);
+    const float ss = pro_sumsq<E>(v, red, K);
     const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + p.eps);
     uint32_t xn[E / 2];
 #pragma unroll
@@ -188,14 +177,14 @@ __device__ __forceinline__ void pro_values(const pq_gemv_prologue &p, int e0, in
       xn[i >> 1] = bfr2(v[i], v[i + 1]);
     }
     if (writer) st_bf16w<E>(p.x_out + e0, xn);
-    norm_apply<E>(v, r.f1, wg_pairwise_sq<E>(v, red + 8), K, p.eps);
+    norm_apply<E>(v, r.f1, pro_sumsq<E>(v, red + kNormSlots, K), K, p.eps);
   } else if constexpr (PRO == PQ_PRO_F32) {
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = r.f0[i];
   } else if constexpr (PRO == PQ_PRO_NORM) {
 #pragma unroll
     for (int i = 0; i < E; i++) v[i] = bf_at(r.u0, i);
-    norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
+    norm_apply<E>(v, r.f0, pro_sumsq<E>(v, red, K), K, p.eps);
   } else if constexpr (PRO == PQ_PRO_EMBED) {
     const float sc = h2f(r.emb_s);
     uint32_t xb[E / 2];
@@ -204,7 +193,7 @@ __device__ __forceinline__ void pro_values(const pq_gemv_prologue &p, int e0, in
 #pragma unroll
     for (int i = 0; i < E; i += 2) xb[i >> 1] = bfr2(v[i], v[i + 1]);
     if (writer) st_bf16w<E>(p.x_out + e0, xb);
-    norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
+    norm_apply<E>(v, r.f0, pro_sumsq<E>(v, red, K), K, p.eps);
   } else if constexpr (PRO == kProEmbedR) {   // pq_embed_rows' bf16(code * scale), then the norm
     uint32_t xb[E / 2];
 #pragma unroll
@@ -212,7 +201,7 @@ __device__ __forceinline__ void pro_values(const pq_gemv_prologue &p, int e0, in
 #pragma unroll
     for (int i = 0; i < E; i += 2) xb[i >> 1] = bfr2(v[i], v[i + 1]);
     if (writer) st_bf16w<E>(p.x_out + e0, xb);
-    norm_apply<E>(v, r.f0, wg_pairwise_sq<E>(v, red), K, p.eps);
+    norm_apply<E>(v, r.f0, pro_sumsq<E>(v, red, K), K, p.eps);
   } else if constexpr (PRO == PQ_PRO_SILU) {
 #pragma unroll
     for (int i = 0; i < E; i++) {

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(NT) void qlow_gemv_kernel(const uint8_t *__restrict
                                                               pq_gemv_prologue p) {
   constexpr bool kPro = PRO != kProPlain;
   extern __shared__ __align__(16) float lsm[];
-  __shared__ float red[16];   // the prologue's workgroup reductions
+  __shared__ __align__(16) float red[2 * kNormSlots];   // the prologue's workgroup reductions
   const int GA = K / kQ, KSA = qlow_ks(K), GW = qlow_gw(B);
   // the groups this workgroup covers: [gb, gb + G), in KS slices of GL
   const int KS = ws ? 1 : KSA, G = ws ? GA / KSA : GA, GL = G / KS, gb = ws ? (int)blockIdx.y * G : 0;

@@ -106,6 +106,43 @@ def test_f32_prologue(orc, pq, dev, N, K):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32))
 
 
+# k_argmax's tie order through the argmax partials of the fused GEMVs: rows 1,
+# 2, 33, 64 and 300 hold the same codes and scales and give the largest
+# outputs, so they tie; k_argmax picks row 2 (lane 2 outranks lane 1, warp 0
+# outranks warps 1 and 2; the oracle's transcription agrees), where the lowest
+# index would be row 1.
+TIED = [1, 2, 33, 64, 300]
+
+
+def test_argmax_parts_tie_order(orc, pq, dev):
+    N, K = 3072, 2048
+    W, S = orc.q8_weights(SEED + 91, N, K)
+    W[TIED] = 127
+    S[TIED] = np.float16(0.01).view(np.uint16)
+    x = (np.abs(orc.gen_normal(SEED + 90, K)) + 0.5).astype(np.float32)
+    qx, dx = orc.q8_quant(x)
+    yr = orc.q8_gemv(W, S, qx, dx)
+    assert (yr[TIED] == yr.max()).all() and orc.argmax(yr) == 2
+    w = pq.Q8Weight(torch.from_numpy(W).to(dev), torch.from_numpy(S.view(np.int16)).to(dev))
+    nparts = pq.lib().pq_q8_gemv_parts(N, K)
+    parts = torch.empty(2 * nparts, dtype=torch.float32, device=dev)
+    y = pq.gemv_fused(w, pq.PRO_F32, out_dtype=pq.DT_F32, parts=parts, xf=torch.from_numpy(x).to(dev))
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32))
+    assert int(pq.argmax_parts(parts, nparts).item()) == 2
+    assert int(pq.argmax(y).item()) == 2
+    # the reference-numerics GEMV's pairs (row-major codes, fp32 scales)
+    codes = torch.from_numpy(W).to(dev)
+    scales = torch.from_numpy(S.view(np.float16).astype(np.float32)).to(dev)
+    w0 = torch.ones(K, device=dev)
+    xb = torch.from_numpy(orc.f2bf(x).view(np.int16)).to(dev)
+    nparts = pq.lib().pq_q8r_gemv_parts(N)
+    parts = torch.empty(2 * nparts, dtype=torch.float32, device=dev)
+    y2 = pq.q8r_gemv_fused(codes, scales, pq.PRO_NORM, out_dtype=pq.DT_F32, parts=parts, x_in=xb, w0=w0)
+    y2h = y2.cpu().numpy()
+    assert (y2h[TIED] == y2h.max()).all() and orc.argmax(y2h) == 2
+    assert int(pq.argmax_parts(parts, nparts).item()) == 2
+
+
 @pytest.mark.parametrize("nt", [3, 7])
 def test_conv_prologue_closed_forms(orc, pq, dev, nt):
     """The CONV prologue on the hand-built channels of tests/conv_cases.py (ascending

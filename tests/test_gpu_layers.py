@@ -152,6 +152,16 @@ def test_argmax_and_ties(orc, pq, dev):
     v2 = np.zeros(65536, np.float32)
     v2[[7, 300, 65535]] = 5.0
     assert int(pq.argmax(torch.from_numpy(v2).to(dev)).item()) == 7
+    # k_argmax's tie order (the oracle's transcription of its trees) where many
+    # values tie: rows 1 and 2 give 2, nothing above -1e30 gives -1
+    v3 = np.zeros(300, np.float32)
+    v3[[1, 2]] = 1.0
+    assert int(pq.argmax(torch.from_numpy(v3).to(dev)).item()) == 2
+    assert int(pq.argmax(torch.full((100,), -float("inf"), device=dev)).item()) == -1
+    rng = np.random.default_rng(SEED + 31)
+    for n in (5, 256, 300, 4099, 65536, 128000):
+        v4 = rng.integers(0, 3, n).astype(np.float32)
+        assert int(pq.argmax(torch.from_numpy(v4).to(dev)).item()) == orc.argmax(v4), n
 
 
 def test_embed(orc, pq, dev):

@@ -37,7 +37,7 @@ def test_bf16_gemv(orc, pq, dev, N, K):
     rng = np.random.default_rng(N + K)
     W = orc.f2bf(rng.standard_normal(N * K).astype(np.float32)).reshape(N, K)
     x = orc.f2bf(rng.standard_normal(K).astype(np.float32) * 2)
-    W[N // 3, :] = W[N // 5, :]            # a tie for the argmax: the lower row wins
+    W[N // 3, :] = W[N // 5, :]            # two equal rows
     want = orc.bf16_gemv(W, x)
     Wd = torch.from_numpy(W.view(np.int16)).to(dev)
     xd = torch.from_numpy(x.view(np.int16)).to(dev)
@@ -49,6 +49,28 @@ def test_bf16_gemv(orc, pq, dev, N, K):
     torch.cuda.synchronize()
     assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
     assert int(pq.argmax_parts(parts, nparts).item()) == orc.argmax(want)
+
+
+def test_bf16_gemv_tie_order(orc, pq, dev):
+    """Rows 1, 2, 33, 64 and 300 equal and largest: the argmax pairs give
+    k_argmax's pick, row 2 (the lowest index would be row 1)."""
+    N, K = 3000, 512
+    rng = np.random.default_rng(17)
+    W = orc.f2bf(rng.standard_normal(N * K).astype(np.float32) * 0.01).reshape(N, K)
+    W[[1, 2, 33, 64, 300]] = orc.f2bf(np.ones(K, np.float32))
+    x = orc.f2bf(np.ones(K, np.float32))
+    want = orc.bf16_gemv(W, x)
+    assert orc.argmax(want) == 2
+    Wd = torch.from_numpy(W.view(np.int16)).to(dev)
+    xd = torch.from_numpy(x.view(np.int16)).to(dev)
+    y = torch.empty(N, dtype=torch.float32, device=dev)
+    nparts = pq.lib().pq_bf16_gemv_parts(N)
+    parts = torch.empty(2 * nparts, dtype=torch.float32, device=dev)
+    pq.check(pq.lib().pq_bf16_gemv(_p(Wd), _p(xd), _p(y), N, K, _p(parts), C.c_void_p(pq.stream_ptr())),
+             "pq_bf16_gemv")
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert int(pq.argmax_parts(parts, nparts).item()) == 2
 
 
 def test_embed_bf16(orc, pq, dev):

@@ -441,9 +441,51 @@ def test_silu_and_gate(orc):
     assert (out[0] == 0.5).all() and (out[1] == 1.0).all() and (out[2] == 0.0).all()
 
 
-def test_argmax_lowest_index(orc):
-    v = np.array([1.0, 3.0, -2.0, 3.0, 3.0], np.float32)
-    assert orc.argmax(v) == 1
+def _argmax_by_key(v):
+    """k_argmax's pick written as a key (lfm3_nanode.cu:942-964): among the
+    values above -1e30 the largest; on ties the last tree step weighs most, so
+    thread slot s = i mod 256 (warp w = s // 32, lane l = s % 32) ranks by
+    (bitrev3(w), bitrev5(l)), then i; -1 when none."""
+    v = np.asarray(v, np.float32)
+    ok = v > np.float32(-1e30)
+    if not ok.any():
+        return -1
+    m = v[ok].max()
+    idx = np.flatnonzero(ok & (v == m))
+    s = idx & 255
+    br = lambda x, b: int(format(int(x), f"0{b}b")[::-1], 2)
+    keys = [(br(si >> 5, 3), br(si & 31, 5), int(i)) for si, i in zip(s, idx)]
+    return int(idx[min(range(len(idx)), key=lambda k: keys[k])])
+
+
+def test_argmax_reference_order(orc):
+    """k_argmax's tie order, hand-derived from its trees: a later (smaller)
+    shfl_down offset outranks an earlier one, so among equal maxima lane 2
+    beats lane 1 (offset 2 joins lane 0 to lane 2 before offset 1 meets lane
+    1), thread 0's index 256 beats thread 1's index 1, warp 2 beats warp 1
+    (64 over 32), and warp 0 beats warp 1 (1 over 32). No value above -1e30
+    gives -1; NaN never wins."""
+    def at(n, idx, val=3.0, fill=1.0):
+        v = np.full(n, fill, np.float32)
+        v[idx] = val
+        return v
+    assert orc.argmax(at(5, [1, 2])) == 2
+    assert orc.argmax(at(300, [1, 256])) == 256
+    assert orc.argmax(at(100, [32, 64])) == 64
+    assert orc.argmax(at(100, [1, 32])) == 1
+    assert orc.argmax(at(100, [0, 32])) == 0
+    assert orc.argmax(at(1000, [300, 44])) == 44          # one slot: the lower index
+    # ties at 1, 3, 4: offset 4 moves lane 4's pair into lane 0, offset 1 keeps it
+    assert orc.argmax(np.array([1.0, 3.0, -2.0, 3.0, 3.0], np.float32)) == 4
+    assert orc.argmax(np.full(7, -1e30, np.float32)) == -1
+    assert orc.argmax(np.full(7, -np.inf, np.float32)) == -1
+    assert orc.argmax(np.array([np.nan, 2.0, np.nan], np.float32)) == 1
+    assert orc.argmax(np.array([-1e30, -2e30, -9e29], np.float32)) == 2
+    rng = np.random.default_rng(41)
+    for n in (1, 7, 255, 256, 300, 1000, 4096, 65536):
+        for _ in range(8):
+            v = rng.integers(0, 4, n).astype(np.float32)
+            assert orc.argmax(v) == _argmax_by_key(v), n
 
 
 def _bf16_rne_exact(v):
@@ -485,16 +527,86 @@ def test_rmsnorm_rounds_before_weight(orc):
     assert np.all(orc.rmsnorm(x, w, 0.0) == 0x3F81)
 
 
-def test_headnorm_is_rmsnorm_per_head(orc):
-    """k_headnorm (lfm3_nanode.cu:460-479) is RMSNorm over each hd slice with the
-    shared [hd] weight."""
+def _f32(v):
+    return np.float32(v)
+
+
+def _sim_tree(s):
+    """The shfl_down tree over the last axis (32 lanes): lane l < o adds lane
+    l + o, o = 16 .. 1; lane 0's value."""
+    s = s.astype(np.float32).copy()
+    for o in (16, 8, 4, 2, 1):
+        s[..., :o] = s[..., :o] + s[..., o:2 * o]
+    return s[..., 0]
+
+
+def _sim_rms_sumsq(xb):
+    """rmsnorm_body's sum (lfm3_nanode.cu:393-405) vectorised: [warp][thread][8]."""
+    x = orc_bf2f_np(xb)
+    q = (x * x).reshape(-1, 32, 8)
+    t = ((q[..., 0] + q[..., 1]) + (q[..., 2] + q[..., 3])) + ((q[..., 4] + q[..., 5]) + (q[..., 6] + q[..., 7]))
+    p = _sim_tree(t)
+    tot = p[0]
+    for w in range(1, p.size):
+        tot = _f32(tot + p[w])
+    return tot
+
+
+def _sim_head_sumsq(xb):
+    x = orc_bf2f_np(xb)
+    q = (x * x).reshape(32, -1)
+    t = (q[:, 0] + q[:, 1]) + (q[:, 2] + q[:, 3]) if q.shape[1] == 4 else q[:, 0] + q[:, 1]
+    return _sim_tree(t)
+
+
+def orc_bf2f_np(xb):
+    return (np.asarray(xb, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _bits(n, vals):
+    """bf16 bits of a vector of n zeros with vals {index: value} set."""
+    x = np.zeros(n, np.float32)
+    for i, v in vals.items():
+        x[i] = v
+    return (x.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_rms_sumsq_reference_order(orc):
+    """rmsnorm_body's sum of squares, hand-derived cases where its order gives
+    another value than an adjacent pairwise tree or a sequential sum (4096^2 =
+    2^24 absorbs a lone 1): within a thread, pairwise (squares 2^24, 0, 1, 1:
+    2^24 + 2; sequential 2^24); thread 1 meets thread 17 before thread 0
+    (squares 2^24 at thread 0, 1 at threads 1 and 17: 2^24 + 2; an adjacent tree
+    2^24); the warp partials in order (2^24, 0, 1, 1: 2^24; pairwise 2^24 + 2).
+    Then random rows against the vectorised transcription."""
+    assert orc.rms_sumsq(_bits(256, {0: 4096.0, 2: 1.0, 3: 1.0})) == 2.0 ** 24 + 2
+    assert orc.rms_sumsq(_bits(256, {0: 4096.0, 8: 1.0, 136: 1.0})) == 2.0 ** 24 + 2
+    assert orc.rms_sumsq(_bits(1024, {0: 4096.0, 512: 1.0, 768: 1.0})) == 2.0 ** 24
+    rng = np.random.default_rng(43)
+    for n in (256, 2048, 8192):
+        for _ in range(4):
+            xb = orc.f2bf((rng.standard_normal(n) * np.exp(2 * rng.standard_normal(n))).astype(np.float32))
+            assert orc.rms_sumsq(xb) == _sim_rms_sumsq(xb), n
+
+
+def test_headnorm_reference_order(orc):
+    """k_headnorm (lfm3_nanode.cu:460-479): its sum of squares (32 threads of
+    4 at hd = 128: squares 2^24 at thread 0 and 1 at threads 1 and 17 give
+    2^24 + 2, an adjacent tree 2^24; hd = 64 in threads of 2), then RMSNorm's
+    rounding steps per head with the shared [hd] weight."""
+    assert orc.head_sumsq(_bits(128, {0: 4096.0, 4: 1.0, 68: 1.0})) == 2.0 ** 24 + 2
+    assert orc.head_sumsq(_bits(64, {0: 4096.0, 2: 1.0, 34: 1.0})) == 2.0 ** 24 + 2
     for nh, hd in ((4, 64), (3, 128)):
         x = orc.f2bf(orc.gen_normal(70 + hd, nh * hd) * 2)
         w = orc.gen_affine(71 + hd, hd, 1.0, 0.1)
         got = orc.headnorm(x, w, nh, hd)
-        want = np.concatenate([orc.rmsnorm(x[h * hd:(h + 1) * hd], w) for h in range(nh)])
-        assert np.array_equal(got, want)
-        assert not np.array_equal(got, orc.rmsnorm(x, np.tile(w, nh)))   # not one norm over all heads
+        for h in range(nh):
+            xh = x[h * hd:(h + 1) * hd]
+            ss = orc.head_sumsq(xh)
+            assert ss == _sim_head_sumsq(xh)
+            rs = _f32(1) / np.sqrt(_f32(ss * (_f32(1) / _f32(hd)) + _f32(1e-5)))
+            r = orc_bf2f_np(orc.f2bf(orc_bf2f_np(xh) * rs))
+            assert np.array_equal(got[h * hd:(h + 1) * hd], orc.f2bf(w * r))
 
 
 def test_embed_row_closed_form(orc):
