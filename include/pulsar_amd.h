@@ -273,6 +273,25 @@ int pq_attn_decode(const uint16_t *q, int q_stride, const uint16_t *kcache, cons
                    float *dx, int pos0, int nh, int nkv, int hd, int T, float scale, int win, void *ws,
                    size_t ws_bytes, void *stream);
 
+/* The reference-numerics arm's attention, in k_attn_head's own order
+ * (lfm3_nanode.cu:503-602), then k_sigmoid_gate (852-858): pq_qk_prep_ref is
+ * pq_qk_prep with the cache holding the bf16 k and v rows as k_kv_write copies
+ * them (157-162); pq_attn_ref attends query t (row t of q) at position pos0+t
+ * to keys lo..pos0+t of that bf16 cache (lo as in pq_attn_decode) with one
+ * 256-thread workgroup per (head, t), whose 8 32-lane warps keep the
+ * reference's places: each score a chain over the lane's hd/32 dims and the
+ * shfl_down tree; the softmax sum per thread over keys t, t+256, ..., the warp
+ * tree, the 8 warps' tree; the probabilities normalized before an 8-segment
+ * value sum added pairwise. e^x is the build's expf_pq where the reference
+ * calls CUDA's expf. head_dim 64 or 128; at most 32768 keys in a window;
+ * gate NULL for none; out bf16 [T] rows of stride out_stride. */
+int pq_qk_prep_ref(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm,
+                   const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv,
+                   int hd, int rot, int T, float eps, void *stream);
+int pq_attn_ref(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int pos0, int nh,
+                int nkv, int hd, int T, float scale, int win, void *stream);
+
 /* Gated short conv over T positions: bcx rows [B | C | x] (3H), ring
  * [ntaps][H] bf16 (newest last, updated), out [T][H] bf16 = bf16(C * conv(B*x)).
  * ntaps 2, 3, 4 or 7. Replaces k_shift_in + k_conv7 / k_conv_chunk (892-941). */

@@ -724,6 +724,63 @@ void orc_attn(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, uint16_
   free(m); free(l); free(o);
 }
 
+/* Attention in k_attn_head's order (lfm3_nanode.cu:503-602) over a bf16 cache
+ * [npos][nkv][hd], for the query at position npos - 1 (keys lo .. npos - 1, lo
+ * from win as in orc_attn). Per q head, the reference's 256 threads being 8
+ * warps of 32 lanes:
+ *  - key i's score: lane l's chain over dims e*l .. e*l + e - 1 (e = hd/32),
+ *    s = fl(s + fl(q_d * k_d)) from 0; the shfl_down tree over the 32 lanes;
+ *    fl(s * scale);
+ *  - m = the largest of -1e30 and the scores;
+ *  - e_i = orc_expf(s_i - m) (CUDA's expf in the reference); thread t sums
+ *    e_i over i = t, t + 256, ... in order, each warp's 32 sums go through the
+ *    shfl_down tree, the 8 warp sums through the tree of offsets 4, 2, 1;
+ *    inv = fl(1 / sum);
+ *  - per dim d, segment g of 8 sums fl(fl(e_i * inv) * v_id) over i = g,
+ *    g + 8, ... in order from 0, and out_d = bf16 of the segments added
+ *    pairwise, ((g0 + g1) + (g2 + g3)) + ((g4 + g5) + (g6 + g7)).
+ * i counts from lo. */
+void orc_attn_ref(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, uint16_t *out,
+                  int npos, int nh, int nkv, int hd, float scale, int win) {
+  const int grp = nh / nkv, e = hd / 32;
+  const int lo = (win > 0 && npos > win) ? npos - win : 0, np = npos - lo;
+  float *sl = (float *)malloc(sizeof(float) * (size_t)np);
+  for (int h = 0; h < nh; h++) {
+    const int g = h / grp;
+    const uint16_t *qh = q + (size_t)h * hd;
+    for (int i = 0; i < np; i++) {
+      const uint16_t *kr = Kc + ((size_t)(lo + i) * nkv + g) * hd;
+      float s[32];
+      for (int l = 0; l < 32; l++) {
+        float a = 0.0f;
+        for (int j = 0; j < e; j++) a = a + orc_bf2f(qh[e * l + j]) * orc_bf2f(kr[e * l + j]);
+        s[l] = a;
+      }
+      sl[i] = orc_warp_tree(s) * scale;
+    }
+    float m = -1e30f;
+    for (int i = 0; i < np; i++) m = fmaxf(m, sl[i]);
+    for (int i = 0; i < np; i++) sl[i] = orc_expf(sl[i] - m);
+    float th[256], ws[8];
+    for (int t = 0; t < 256; t++) {
+      th[t] = 0.0f;
+      for (int i = t; i < np; i += 256) th[t] = th[t] + sl[i];
+    }
+    for (int w = 0; w < 8; w++) ws[w] = orc_warp_tree(th + 32 * w);
+    const float inv = 1.0f / (((ws[0] + ws[4]) + (ws[2] + ws[6])) + ((ws[1] + ws[5]) + (ws[3] + ws[7])));
+    for (int d = 0; d < hd; d++) {
+      float sg[8];
+      for (int k = 0; k < 8; k++) {
+        float acc = 0.0f;
+        for (int i = k; i < np; i += 8) acc = acc + (sl[i] * inv) * orc_bf2f(Vc[((size_t)(lo + i) * nkv + g) * hd + d]);
+        sg[k] = acc;
+      }
+      out[(size_t)h * hd + d] = orc_f2bf(((sg[0] + sg[1]) + (sg[2] + sg[3])) + ((sg[4] + sg[5]) + (sg[6] + sg[7])));
+    }
+  }
+  free(sl);
+}
+
 /* Two-pass softmax attention in double (the structure of k_attn_head,
  * lfm3_nanode.cu:503-602, without its rounding steps): the referee for
  * orc_attn. out is fp32 [nh][hd]. */

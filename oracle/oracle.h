@@ -82,6 +82,8 @@ void orc_rope_table(float *cs, int maxpos, int hd, int rot, float theta);
 void orc_rope(uint16_t *x, const float *cs, int pos, int nheads, int hd, int rot);
 void orc_attn(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, uint16_t *out,
               int npos, int nh, int nkv, int hd, float scale, int win);
+void orc_attn_ref(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, uint16_t *out,
+                  int npos, int nh, int nkv, int hd, float scale, int win);
 void orc_attn_twopass(const uint16_t *q, const uint16_t *Kc, const uint16_t *Vc, float *out,
                       int npos, int nh, int nkv, int hd, float scale, int win);
 void orc_conv_step(uint16_t *ring, const float *taps, const uint16_t *bcx, uint16_t *out,

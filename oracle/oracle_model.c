@@ -3,8 +3,9 @@
  * The layer sequence restates layer_body (lfm3_nanode.cu:3739-3856) with the
  * hot-path numerics of oracle.c: Q8_0 x Q8_0 GEMVs (activations quantized per
  * 32-block; or, with numerics = 1, the reference's own GEMV order on bf16 x
- * and fp32 scales, orc_q8r_gemm), fp16 KV cache with split-K flash decode,
- * table RoPE, one expf.
+ * and fp32 scales, orc_q8r_gemm), fp16 KV cache with split-K flash decode (with
+ * numerics = 1: the bf16 cache and k_attn_head's order, orc_attn_ref), table
+ * RoPE, one expf.
  *   operator_norm -> {attention | gated conv} -> post_operator_norm -> +residual
  *   ffn_norm -> gate/up GEMV -> silu(gate)*up -> down GEMV -> post_ffn_norm -> +residual
  * Attention: fused [q | k | v | gate] GEMV (gate = one value per q head), per-head
@@ -49,7 +50,7 @@ typedef struct {
   int attn, slide;       /* slide: a sliding-window attention layer */
   q8t in, out, ug, down;
   float *op_norm, *post_op_norm, *ffn_norm, *post_ffn_norm, *q_norm, *k_norm, *taps;
-  uint16_t *kc, *vc;    /* fp16 [ctx][nkv][hd] */
+  uint16_t *kc, *vc;    /* fp16 (numerics 1: bf16) [ctx][nkv][hd] */
   uint16_t *ring;       /* bf16 [ntaps][H]      */
 } layer_t;
 
@@ -364,13 +365,19 @@ int orc_model_feed(orc_model *m, const int32_t *tok, int T, float *logits_out) {
         const int rot = L->slide ? c->slide_rot : c->rot;
         orc_rope(q, rt, pos, c->nh, c->hd, rot);
         orc_rope(k, rt, pos, c->nkv, c->hd, rot);
+        /* R1: fp16 cache, split-K flash decode; numerics 1: the bf16 rows as
+         * k_kv_write copies them and k_attn_head's order */
         for (int i = 0; i < kvd; i++) {
-          L->kc[(size_t)pos * kvd + i] = orc_f2h(orc_bf2f(k[i]));
-          L->vc[(size_t)pos * kvd + i] = orc_f2h(orc_bf2f(v[i]));
+          L->kc[(size_t)pos * kvd + i] = c->numerics == 1 ? k[i] : orc_f2h(orc_bf2f(k[i]));
+          L->vc[(size_t)pos * kvd + i] = c->numerics == 1 ? v[i] : orc_f2h(orc_bf2f(v[i]));
         }
         uint16_t *a = H2 + (size_t)t * qd;
-        orc_attn(q, L->kc, L->vc, a, pos + 1, c->nh, c->nkv, c->hd, 1.0f / sqrtf((float)c->hd),
-                 L->slide ? c->slide_win : 0);
+        if (c->numerics == 1)
+          orc_attn_ref(q, L->kc, L->vc, a, pos + 1, c->nh, c->nkv, c->hd, 1.0f / sqrtf((float)c->hd),
+                       L->slide ? c->slide_win : 0);
+        else
+          orc_attn(q, L->kc, L->vc, a, pos + 1, c->nh, c->nkv, c->hd, 1.0f / sqrtf((float)c->hd),
+                   L->slide ? c->slide_win : 0);
         orc_sigmoid_gate(g, a, c->nh, c->hd);
       }
       gemm_bf16(&L->out, H2, H1, T, yf, qx, dx);               /* [T][H] */

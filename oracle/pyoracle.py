@@ -295,6 +295,15 @@ def attn(q, Kc, Vc, npos, nh, nkv, hd, scale, win=0):
     return out
 
 
+def attn_ref(q, Kc, Vc, npos, nh, nkv, hd, scale, win=0):
+    """k_attn_head's order over a bf16 cache (orc_attn_ref); returns bf16 [nh*hd]."""
+    out = np.empty(nh * hd, np.uint16)
+    lib().orc_attn_ref(_p(np.ascontiguousarray(q, np.uint16)), _p(np.ascontiguousarray(Kc, np.uint16)),
+                       _p(np.ascontiguousarray(Vc, np.uint16)), _p(out), C.c_int(npos), C.c_int(nh), C.c_int(nkv),
+                       C.c_int(hd), C.c_float(scale), C.c_int(win))
+    return out
+
+
 def attn_twopass(q, Kc, Vc, npos, nh, nkv, hd, scale, win=0):
     out = np.empty(nh * hd, np.float32)
     lib().orc_attn_twopass(_p(np.ascontiguousarray(q, np.uint16)), _p(np.ascontiguousarray(Kc, np.uint16)),

@@ -1,0 +1,253 @@
+// attn_ref.hip -- the attention of the reference-numerics engine (gfx950), in
+// the reference's own order: k_attn_head (lfm3_nanode.cu:503-602) over a bf16
+// KV cache [pos][nkv][hd] (written by pq_qk_prep_ref, as k_kv_write copies the
+// bf16 rows, 157-162), then k_sigmoid_gate's gate (852-858).
+//
+// One 256-thread workgroup per (q head, query position t), as the reference
+// launches it (a block of 256 per head; blockIdx.y the chunk position). Its 8
+// warps of 32 are the 32-lane halves of the 4 waves (lane = tid & 31, warp =
+// tid >> 5), so every sum keeps its place:
+//   score p (warp p mod 8): lane l's chain s = fl(s + fl(q_d * k_d)) over its
+//     hd/32 dims from 0, the shfl_down tree over the 32 lanes, fl(s * scale);
+//   m = the largest score (a max: any order gives it);
+//   e_p = e^(s_p - m) by pq::expf_pq, the build's e^x, where the reference
+//     calls CUDA's expf (not restated bit for bit); thread t sums e over
+//     p = t, t + 256, ... in order, the shfl_down tree per warp, the 8 warp
+//     sums by the tree of offsets 4, 2, 1; inv = 1 / sum;
+//   the value sum: warp g (segment g) accumulates fl(w_p * v_pd), w_p =
+//     fl(e_p * inv), over p = g, g + 8, ... in order for the lane's hd/32
+//     dims; out_d = bf16 of the 8 segments added pairwise.
+// p counts from the window's first key lo (the reference's i and p). head_dim
+// 128 is the reference's (4 dims a lane); 64 takes 2.
+#include "pq_device.h"
+#include "pq_host.h"
+#include "pq_internal.h"
+#include "q8_common.h"
+
+
+namespace pq {
+
+constexpr int kArRound = 8;          // keys a warp loads per round
+constexpr int kArMaxKeys = 32768;    // keys in one window (LDS: 4 bytes each)
+
+// the shfl_down tree of a 32-lane warp (offsets 16 .. 1): lane 0 of each half
+// of the wave ends with its warp's sum
+__device__ __forceinline__ float warp_tree32(float s) {
+  s = add_down<16>(s);
+  s = add_down<8>(s);
+  s = add_down<4>(s);
+  s = add_down<2>(s);
+  return add_down<1>(s);
+}
+
+// E consecutive bf16 values of a cache row: one 8-byte (E = 4) or 4-byte load
+template <int E>
+struct KVPiece {
+  using T = uint2;
+};
+template <>
+struct KVPiece<2> {
+  using T = uint32_t;
+};
+// the lane's piece at byte offset off of a cache resource (zeros past its end)
+template <int E>
+__device__ __forceinline__ typename KVPiece<E>::T kv_load(__amdgpu_buffer_rsrc_t r, int off) {
+  if constexpr (E == 4) {
+    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2((uint32_t)v.x, (uint32_t)v.y);
+  } else {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  }
+}
+template <int E>
+__device__ __forceinline__ void kv_unpack(const typename KVPiece<E>::T &w, float *f) {
+  if constexpr (E == 4) {
+    f[0] = __uint_as_float(w.x << 16);
+    f[1] = __uint_as_float(w.x & 0xffff0000u);
+    f[2] = __uint_as_float(w.y << 16);
+    f[3] = __uint_as_float(w.y & 0xffff0000u);
+  } else {
+    f[0] = __uint_as_float(w << 16);
+    f[1] = __uint_as_float(w & 0xffff0000u);
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_ref_kernel(const uint16_t *__restrict__ q, int q_stride,
+                                                        const uint16_t *__restrict__ kc,
+                                                        const uint16_t *__restrict__ vc,
+                                                        const uint16_t *__restrict__ gate, int gate_stride,
+                                                        uint16_t *__restrict__ out, int out_stride, int pos0,
+                                                        const int32_t *__restrict__ pos_dev, int nh, int nkv,
+                                                        float scale, int win) {
+  constexpr int E = HD / 32;
+  using KT = typename KVPiece<E>::T;
+  extern __shared__ __align__(16) float sl[];   // the window's scores, then their e
+  __shared__ float red[8];
+  __shared__ float seg[8][HD];
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 31, wid = tid >> 5;
+  const int npos = (pos_dev != nullptr ? *pos_dev : pos0) + t + 1;
+  const int lo = window_lo(npos, win), np = npos - lo;
+  const int kvd = nkv * HD;
+  const size_t kvo = (size_t)(h / (nh / nkv)) * HD + lane * E;   // the lane's dims within a cache row
+  float qv[E];
+#pragma unroll
+  for (int j = 0; j < E; j++) qv[j] = bf2f(q[(size_t)t * q_stride + (size_t)h * HD + lane * E + j]);
+  // the caches up to the query's position: keys past it read zeros
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kc), (short)0,
+                                                                      npos * kvd * 2, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vc), (short)0,
+                                                                      npos * kvd * 2, kRsrcWord3);
+  // warp w's keys (and value segment): lo + w + 8j, j < nk, in rounds of
+  // kArRound keys whose loads all go out before the round is computed; the
+  // first round of value rows is loaded before the softmax, which hides its
+  // latency. With one wave a SIMD the kernel is bound by instruction latency,
+  // so short rounds (the fewest key slots issued past the window) measured
+  // fastest: 290 keys 7.8 us at 8 a round, 8.4 at 16, 10.5 at 64 (head_dim 64).
+  constexpr int B = kArRound;
+  const int nk = np > wid ? (np - wid + 7) / 8 : 0;
+  auto key_off = [&](int j) { return (int)(((size_t)(lo + wid + 8 * j) * kvd + kvo) * 2); };
+  auto ld = [&](__amdgpu_buffer_rsrc_t r, KT *w, int j0) {
+#pragma unroll
+    for (int b = 0; b < B; b++) w[b] = kv_load<E>(r, key_off(j0 + b));
+  };
+  KT wk[B], wv[B];
+  for (int j0 = 0; j0 < nk; j0 += B) {
+    ld(rk, wk, j0);
+    float s[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+      float kf[E];
+      kv_unpack<E>(wk[b], kf);
+      s[b] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < E; j++) s[b] = s[b] + qv[j] * kf[j];
+    }
+    // the trees of the round's keys step by step (independent chains side by side)
+#pragma unroll
+    for (int b = 0; b < B; b++) s[b] = add_down<16>(s[b]);
+#pragma unroll
+    for (int b = 0; b < B; b++) s[b] = add_down<8>(s[b]);
+#pragma unroll
+    for (int b = 0; b < B; b++) s[b] = add_down<4>(s[b]);
+#pragma unroll
+    for (int b = 0; b < B; b++) s[b] = add_down<2>(s[b]);
+#pragma unroll
+    for (int b = 0; b < B; b++) s[b] = add_down<1>(s[b]);
+    if (lane == 0) {
+#pragma unroll
+      for (int b = 0; b < B; b++) {
+        const int i = wid + 8 * (j0 + b);
+        if (i < np) sl[i] = s[b] * scale;
+      }
+    }
+  }
+  ld(rv, wv, 0);
+  __syncthreads();
+  float mx = -1e30f;
+  for (int i = tid; i < np; i += 256) mx = fmaxf(mx, sl[i]);
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.0f;
+  for (int i = tid; i < np; i += 256) {
+    const float e = expf_pq(sl[i] - m);
+    sl[i] = e;
+    sum = sum + e;
+  }
+  sum = warp_tree32(sum);
+  if (lane == 0) red[wid] = sum;
+  __syncthreads();
+  const float inv = 1.0f / (((red[0] + red[4]) + (red[2] + red[6])) + ((red[1] + red[5]) + (red[3] + red[7])));
+  // the value sum of segment wid over keys wid, wid + 8, ... (from lo)
+  float acc[E];
+#pragma unroll
+  for (int j = 0; j < E; j++) acc[j] = 0.0f;
+  for (int j0 = 0; j0 < nk; j0 += B) {
+    if (j0 > 0) ld(rv, wv, j0);
+    // branch-free, so the round's weight reads from LDS go out together: keys
+    // past the window read a clamped slot and leave acc as it is (a select)
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+      const int i = wid + 8 * (j0 + b);
+      const float wt = sl[i < np ? i : np - 1] * inv;
+      float vf[E];
+      kv_unpack<E>(wv[b], vf);
+#pragma unroll
+      for (int j = 0; j < E; j++) {
+        const float a = acc[j] + wt * vf[j];
+        acc[j] = i < np ? a : acc[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < E; j++) seg[wid][lane * E + j] = acc[j];
+  __syncthreads();
+  if (tid < HD) {
+    const float o = ((seg[0][tid] + seg[1][tid]) + (seg[2][tid] + seg[3][tid])) +
+                    ((seg[4][tid] + seg[5][tid]) + (seg[6][tid] + seg[7][tid]));
+    uint16_t ob = f2bf(o);
+    if (gate != nullptr) {   // k_sigmoid_gate: bf16(out * 1 / (1 + e^-g))
+      const float sg = 1.0f / (1.0f + expf_pq(-bf2f(gate[(size_t)t * gate_stride + h])));
+      ob = f2bf(bf2f(ob) * sg);
+    }
+    out[(size_t)t * out_stride + (size_t)h * HD + tid] = ob;
+  }
+}
+
+static int attn_ref_launch(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                           const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int pos0,
+                           const int32_t *pos_dev, int keys, int nh, int nkv, int hd, int T, float scale, int win,
+                           hipStream_t st) {
+  const dim3 grid((unsigned)nh, (unsigned)T), block(256);
+  const size_t lds = (size_t)keys * sizeof(float);
+  if (hd == 64)
+    launch(attn_ref_kernel<64>, grid, block, lds, st, q, q_stride, kcache, vcache, gate, gate_stride, out,
+           out_stride, pos0, pos_dev, nh, nkv, scale, win);
+  else
+    launch(attn_ref_kernel<128>, grid, block, lds, st, q, q_stride, kcache, vcache, gate, gate_stride, out,
+           out_stride, pos0, pos_dev, nh, nkv, scale, win);
+  return check_launch("pq_attn_ref");
+}
+
+static int attn_ref_check(const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache, const uint16_t *out,
+                          int nh, int nkv, int hd, int T, int win, int keys, const char *who) {
+  PQ_REQUIRE(q && kcache && vcache && out, PQ_ERR_ARG, "%s: null pointer", who);
+  PQ_REQUIRE(hd == 64 || hd == 128, PQ_ERR_ARG, "%s: head_dim %d (64 or 128)", who, hd);
+  PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && T > 0 && win >= 0, PQ_ERR_ARG, "%s: nh=%d nkv=%d T=%d win=%d",
+             who, nh, nkv, T, win);
+  PQ_REQUIRE(aligned(kcache, 16) && aligned(vcache, 16), PQ_ERR_ALIGN, "%s: KV cache must be 16-byte aligned", who);
+  PQ_REQUIRE(keys <= kArMaxKeys, PQ_ERR_ARG, "%s: %d keys in a window (at most %d)", who, keys, kArMaxKeys);
+  return PQ_OK;
+}
+
+// pq_attn_ref at the device position *pos_dev: LDS for the keys of any
+// position below ctx.
+int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                 const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, const int32_t *pos_dev,
+                 int ctx, int nh, int nkv, int hd, float scale, int win, hipStream_t st) {
+  const int keys = win > 0 && win < ctx ? win : ctx;
+  PQ_REQUIRE(pos_dev && ctx > 0, PQ_ERR_ARG, "attn_ref_dev: no position");
+  const int rc = attn_ref_check(q, kcache, vcache, out, nh, nkv, hd, 1, win, keys, "attn_ref_dev");
+  if (rc) return rc;
+  return attn_ref_launch(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, 0, pos_dev, keys, nh, nkv,
+                         hd, 1, scale, win, st);
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" int pq_attn_ref(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                           const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int pos0, int nh,
+                           int nkv, int hd, int T, float scale, int win, void *stream) {
+  PQ_REQUIRE(pos0 >= 0, PQ_ERR_ARG, "pq_attn_ref: pos0=%d", pos0);
+  const int last = pos0 + T;   // keys of the chunk's last query
+  const int keys = win > 0 && win < last ? win : last;
+  const int rc = attn_ref_check(q, kcache, vcache, out, nh, nkv, hd, T, win, keys, "pq_attn_ref");
+  if (rc) return rc;
+  return attn_ref_launch(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, pos0, nullptr, keys, nh,
+                         nkv, hd, T, scale, win, as_stream(stream));
+}

@@ -611,14 +611,11 @@ static int forward_r2(Engine &E, const int32_t *toks, int n, int32_t *next) {
       uint16_t *Xc = E.X + (size_t)c0 * H;
       uint16_t *xin = E.xin + (size_t)c0 * H;
       PQ_TRY(gemm_r2(E, D.in, xin, E.Wd, PQ_DTYPE_BF16, T));
-      if (D.attn && T == 1 && mixer_fused(E, D)) {   // one launch, the same bits (bf16 out for o_proj)
-        PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pos0, c.nh, c.nkv, c.hd,
-                                    layer_rot(E, D), layer_win(E, D), c.eps, scale, E.A, nullptr, nullptr, E.st));
-      } else if (D.attn) {
-        PQ_TRY(pq_qk_prep(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pos0, c.nh, c.nkv, c.hd,
-                          layer_rot(E, D), T, c.eps, E.st));
-        PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr, nullptr,
-                              pos0, c.nh, c.nkv, c.hd, T, scale, layer_win(E, D), E.attn_ws, E.attn_ws_bytes, E.st));
+      if (D.attn) {   // k_attn_head's order over the bf16 cache
+        PQ_TRY(pq_qk_prep_ref(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pos0, c.nh, c.nkv, c.hd,
+                              layer_rot(E, D), T, c.eps, E.st));
+        PQ_TRY(pq_attn_ref(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, pos0, c.nh, c.nkv,
+                           c.hd, T, scale, layer_win(E, D), E.st));
       } else {
         PQ_TRY(pq_conv(D.ring(), D.taps, E.Wd, E.A, H, T, c.ntaps, E.st));
       }
@@ -883,29 +880,16 @@ static int forward_decode_r2(Engine &E, bool dev) {
       resnorm(E.L[l - 1].post_ffn_norm, D.op_norm);
       PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
     }
-    if (D.attn) {
+    if (D.attn) {   // k_attn_head's order over the bf16 cache
       const int32_t *pd = dev ? E.ctr + 1 : nullptr;
-      if (mixer_fused(E, D)) {
-        if (dev)
-          PQ_TRY(attn_layer_decode_dev(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, pd, c.ctx, c.nh, c.nkv,
-                                       c.hd, layer_rot(E, D), layer_win(E, D), c.eps, scale, E.A, nullptr, nullptr,
-                                       E.st));
-        else
-          PQ_TRY(pq_attn_layer_decode(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, c.nh, c.nkv,
-                                      c.hd, layer_rot(E, D), layer_win(E, D), c.eps, scale, E.A, nullptr, nullptr,
-                                      E.st));
-      } else {
-        PQ_TRY(qk_prep_launch(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, pd, c.nh, c.nkv,
-                              c.hd, layer_rot(E, D), 1, c.eps, E.st));
-        if (dev)
-          PQ_TRY(attn_decode_dev(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr,
-                                 nullptr, pd, c.ctx, c.nh, c.nkv, c.hd, scale, layer_win(E, D), E.attn_ws,
-                                 E.attn_ws_bytes, E.st));
-        else
-          PQ_TRY(pq_attn_decode(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, nullptr, nullptr,
-                                E.pos, c.nh, c.nkv, c.hd, 1, scale, layer_win(E, D), E.attn_ws, E.attn_ws_bytes,
-                                E.st));
-      }
+      PQ_TRY(qk_prep_launch(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, pd, c.nh, c.nkv,
+                            c.hd, layer_rot(E, D), 1, c.eps, E.st, true));
+      if (dev)
+        PQ_TRY(attn_ref_dev(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, pd, c.ctx, c.nh,
+                            c.nkv, c.hd, scale, layer_win(E, D), E.st));
+      else
+        PQ_TRY(pq_attn_ref(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, E.pos, c.nh, c.nkv,
+                           c.hd, 1, scale, layer_win(E, D), E.st));
       PQ_TRY(plain(D.out, E.A, E.Hb));
     } else if (D.out.split() && parts_fusable(D.out, PQ_PRO_CONV)) {
       p = pq_gemv_prologue{};

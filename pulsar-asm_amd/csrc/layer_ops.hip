@@ -95,8 +95,10 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(uint16_t *__restrict__ x,
 // (written to the cache). The sum of squares is k_headnorm's (head_sumsq).
 // RoPE pairs (i, i + HD/2) for i < rot/2 (k_rope,
 // lfm3_nanode.cu:483-498): a lane-pair exchange at HD = 64, the lane's own two
-// values at HD = 128. cs is the layer's [pos][rot/2][cos, sin] table.
-template <int HD>
+// values at HD = 128. cs is the layer's [pos][rot/2][cos, sin] table. KVB: the
+// cache holds the bf16 values as the reference's k_kv_write copies them
+// (157-162); else fp16 of them.
+template <int HD, bool KVB>
 __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv, int row_stride,
                                                       const float *__restrict__ qn, const float *__restrict__ kn,
                                                       const float *__restrict__ cs, uint16_t *__restrict__ kc,
@@ -110,8 +112,10 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv,
   if (head >= nh + nkv) {  // v: straight to the cache
     const int g = head - nh - nkv;
 #pragma unroll
-    for (int e = 0; e < E; e++)
-      vc[(size_t)pos * kvd + g * HD + l + 64 * e] = f2h(bf2f(row[nh * HD + kvd + g * HD + l + 64 * e]));
+    for (int e = 0; e < E; e++) {
+      const uint16_t vb = row[nh * HD + kvd + g * HD + l + 64 * e];
+      vc[(size_t)pos * kvd + g * HD + l + 64 * e] = KVB ? vb : f2h(bf2f(vb));
+    }
     return;
   }
   const bool isq = head < nh;
@@ -147,7 +151,7 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(uint16_t *__restrict__ qkv,
   for (int e = 0; e < E; e++) {
     const uint16_t vb = f2bf(r[e]);
     if (isq) xr[l + 64 * e] = vb;
-    else kc[(size_t)pos * kvd + (head - nh) * HD + l + 64 * e] = f2h(bf2f(vb));
+    else kc[(size_t)pos * kvd + (head - nh) * HD + l + 64 * e] = KVB ? vb : f2h(bf2f(vb));
   }
 }
 
@@ -328,28 +332,47 @@ extern "C" int pq_rmsnorm(uint16_t *x, const uint16_t *h, const float *w0, const
   return check_launch("pq_rmsnorm");
 }
 
+static int qk_prep_entry(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm,
+                         const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv, int hd,
+                         int rot, int T, float eps, void *stream, bool kv_bf16, const char *who) {
+  PQ_REQUIRE(qkv && q_norm && k_norm && rope_cs && kcache && vcache, PQ_ERR_ARG, "%s: null pointer", who);
+  PQ_REQUIRE(hd == 64 || hd == 128, PQ_ERR_ARG, "%s: head_dim %d (64 or 128)", who, hd);
+  PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && rot >= 0 && rot <= hd && rot % 2 == 0 && T > 0 && pos0 >= 0,
+             PQ_ERR_ARG, "%s: nh=%d nkv=%d rot=%d T=%d pos0=%d", who, nh, nkv, rot, T, pos0);
+  PQ_REQUIRE(row_stride >= (nh + 2 * nkv) * hd, PQ_ERR_ARG, "%s: row stride %d too small", who, row_stride);
+  return qk_prep_launch(qkv, row_stride, q_norm, k_norm, rope_cs, kcache, vcache, pos0, nullptr, nh, nkv, hd, rot, T,
+                        eps, as_stream(stream), kv_bf16);
+}
+
 extern "C" int pq_qk_prep(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm, const float *rope_cs,
                           uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv, int hd, int rot, int T,
                           float eps, void *stream) {
-  PQ_REQUIRE(qkv && q_norm && k_norm && rope_cs && kcache && vcache, PQ_ERR_ARG, "pq_qk_prep: null pointer");
-  PQ_REQUIRE(hd == 64 || hd == 128, PQ_ERR_ARG, "pq_qk_prep: head_dim %d (64 or 128)", hd);
-  PQ_REQUIRE(nh > 0 && nkv > 0 && nh % nkv == 0 && rot >= 0 && rot <= hd && rot % 2 == 0 && T > 0 && pos0 >= 0,
-             PQ_ERR_ARG, "pq_qk_prep: nh=%d nkv=%d rot=%d T=%d pos0=%d", nh, nkv, rot, T, pos0);
-  PQ_REQUIRE(row_stride >= (nh + 2 * nkv) * hd, PQ_ERR_ARG, "pq_qk_prep: row stride %d too small", row_stride);
-  return qk_prep_launch(qkv, row_stride, q_norm, k_norm, rope_cs, kcache, vcache, pos0, nullptr, nh, nkv, hd, rot, T,
-                        eps, as_stream(stream));
+  return qk_prep_entry(qkv, row_stride, q_norm, k_norm, rope_cs, kcache, vcache, pos0, nh, nkv, hd, rot, T, eps,
+                       stream, false, "pq_qk_prep");
+}
+
+extern "C" int pq_qk_prep_ref(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm,
+                              const float *rope_cs, uint16_t *kcache, uint16_t *vcache, int pos0, int nh, int nkv,
+                              int hd, int rot, int T, float eps, void *stream) {
+  return qk_prep_entry(qkv, row_stride, q_norm, k_norm, rope_cs, kcache, vcache, pos0, nh, nkv, hd, rot, T, eps,
+                       stream, true, "pq_qk_prep_ref");
 }
 
 namespace pq {
 int qk_prep_launch(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm, const float *rope_cs,
                    uint16_t *kcache, uint16_t *vcache, int pos0, const int32_t *pos_dev, int nh, int nkv, int hd,
-                   int rot, int T, float eps, hipStream_t st) {
-  if (hd == 64)
-    launch(qk_prep_kernel<64>, dim3(nh + 2 * nkv, T), dim3(64), 0, st, qkv, row_stride, q_norm, k_norm, rope_cs,
-           kcache, vcache, pos0, nh, nkv, rot, eps, pos_dev);
-  else
-    launch(qk_prep_kernel<128>, dim3(nh + 2 * nkv, T), dim3(64), 0, st, qkv, row_stride, q_norm, k_norm, rope_cs,
-           kcache, vcache, pos0, nh, nkv, rot, eps, pos_dev);
+                   int rot, int T, float eps, hipStream_t st, bool kv_bf16) {
+#define PQ_QKP(HH, KB)                                                                                             \
+  launch(qk_prep_kernel<HH, KB>, dim3(nh + 2 * nkv, T), dim3(64), 0, st, qkv, row_stride, q_norm, k_norm, rope_cs, \
+         kcache, vcache, pos0, nh, nkv, rot, eps, pos_dev)
+  if (hd == 64) {
+    if (kv_bf16) PQ_QKP(64, true);
+    else PQ_QKP(64, false);
+  } else {
+    if (kv_bf16) PQ_QKP(128, true);
+    else PQ_QKP(128, false);
+  }
+#undef PQ_QKP
   return check_launch("pq_qk_prep");
 }
 }  // namespace pq

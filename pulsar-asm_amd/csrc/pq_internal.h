@@ -18,11 +18,18 @@ int attn_layer_decode_dev(const uint16_t *qkvg, const float *q_norm, const float
                           int rot, int win, float eps, float scale, uint16_t *out, int8_t *qx, float *dx,
                           hipStream_t st);
 
-// pq_qk_prep with the launch stream given; pos_dev (if not NULL) holds the
-// position of row 0 on the device instead of pos0.
+// pq_qk_prep (pq_qk_prep_ref with kv_bf16) with the launch stream given;
+// pos_dev (if not NULL) holds the position of row 0 on the device instead of
+// pos0.
 int qk_prep_launch(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm, const float *rope_cs,
                    uint16_t *kcache, uint16_t *vcache, int pos0, const int32_t *pos_dev, int nh, int nkv, int hd,
-                   int rot, int T, float eps, hipStream_t st);
+                   int rot, int T, float eps, hipStream_t st, bool kv_bf16 = false);
+
+// pq_attn_ref for one query at the device position *pos_dev (keys up to it,
+// window win); LDS sized for positions below ctx.
+int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
+                 const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, const int32_t *pos_dev,
+                 int ctx, int nh, int nkv, int hd, float scale, int win, hipStream_t st);
 
 // pq_attn_decode for one query at the device position *pos_dev (keys up to
 // it, window win), sized for positions below ctx.

@@ -116,6 +116,70 @@ def test_attention(orc, pq, dev, npos_last, T, nh, nkv, hd, win):
     assert np.array_equal(qx.cpu().numpy(), orc.q8_quant_bf16(want)[0])
 
 
+def test_qk_prep_ref_bf16_cache(orc, pq, dev):
+    """pq_qk_prep_ref: q as pq_qk_prep leaves it, and the cache rows the bf16 k
+    (normed, rotated) and v as they are (k_kv_write's copy)."""
+    nh, nkv, hd, ctx, pos0, T, rot = 16, 4, 128, 512, 300, 5, 64
+    nin, rows, qn, kn, _ = _qkv_case(orc, nh, nkv, hd, T, 2, SEED + 77)
+    cs = orc.rope_table(ctx, hd, rot, 1e6)
+    kvd = nkv * hd
+    want = rows.copy()
+    kc_r = np.zeros((ctx, kvd), np.uint16)
+    vc_r = np.zeros((ctx, kvd), np.uint16)
+    for t in range(T):
+        r = want[t]
+        r[:nh * hd] = orc.rope(orc.headnorm(r[:nh * hd], qn, nh, hd), cs, pos0 + t, nh, hd, rot)
+        kc_r[pos0 + t] = orc.rope(orc.headnorm(r[nh * hd:nh * hd + kvd], kn, nkv, hd), cs, pos0 + t, nkv, hd, rot)
+        vc_r[pos0 + t] = r[nh * hd + kvd:nh * hd + 2 * kvd]
+    qkv = _t16(rows, dev)
+    kc = torch.zeros((ctx, kvd), dtype=torch.int16, device=dev)
+    vc = torch.zeros((ctx, kvd), dtype=torch.int16, device=dev)
+    pq.qk_prep_ref(qkv, nin, torch.from_numpy(qn).to(dev), torch.from_numpy(kn).to(dev),
+                   torch.from_numpy(cs).to(dev), kc, vc, pos0, nh, nkv, hd, rot, T)
+    assert np.array_equal(_u16(qkv)[:, :nh * hd], want[:, :nh * hd])
+    assert np.array_equal(_u16(kc), kc_r) and np.array_equal(_u16(vc), vc_r)
+
+
+# pq_attn_ref (k_attn_head's order over the bf16 cache) against the oracle's
+# orc_attn_ref + sigmoid gate, bit for bit: one key, one and several rounds of
+# the 256 threads' softmax sums, 2048 and 4500 keys, chunks of T queries,
+# head_dim 64 and 128, GQA groups 1, 4 and 8, windows 256, 100 and 1.
+@pytest.mark.parametrize("npos_last,T,nh,nkv,hd,win", [
+    (1, 1, 32, 8, 64, 0), (300, 1, 32, 8, 64, 0), (2048, 1, 32, 8, 64, 0), (40, 33, 32, 8, 64, 0),
+    (1, 1, 16, 4, 128, 0), (600, 1, 16, 4, 128, 0), (129, 40, 16, 4, 128, 0), (4500, 2, 16, 4, 128, 0),
+    (300, 1, 16, 4, 128, 256), (2000, 1, 16, 4, 128, 256), (330, 90, 16, 4, 128, 256),
+    (200, 20, 8, 8, 64, 100), (90, 5, 16, 4, 128, 1)])
+def test_attention_ref(orc, pq, dev, npos_last, T, nh, nkv, hd, win):
+    pos0 = npos_last - T
+    kvd = nkv * hd
+    q = orc.f2bf(orc.gen_normal(SEED + 7 * npos_last, T * nh * hd).reshape(T, nh * hd) * 2)
+    gate = orc.f2bf(orc.gen_normal(SEED + 7 * npos_last + 1, T * nh).reshape(T, nh) * 3)
+    kc = orc.f2bf(orc.gen_normal(SEED + 7 * npos_last + 2, npos_last * kvd) * 2)
+    vc = orc.f2bf(orc.gen_normal(SEED + 7 * npos_last + 3, npos_last * kvd) * 5)
+    scale = 0.125
+    want = np.stack([orc.sigmoid_gate(gate[t], orc.attn_ref(q[t], kc, vc, pos0 + t + 1, nh, nkv, hd, scale, win),
+                                      nh, hd) for t in range(T)])
+    out = torch.zeros((T, nh * hd), dtype=torch.int16, device=dev)
+    pq.attn_ref(_t16(q, dev), nh * hd, _t16(kc, dev), _t16(vc, dev), pos0, nh, nkv, hd, T, scale, out, nh * hd,
+                gate=_t16(gate, dev), gate_stride=nh, win=win)
+    got = _u16(out)
+    bad = np.argwhere(got != want)
+    assert bad.shape[0] == 0, f"{bad.shape[0]} differ, first {bad[:4].tolist()}"
+
+
+def test_attention_ref_segment_order(orc, pq, dev):
+    """The value segments add pairwise (the oracle's hand-derived case: 0x3f81
+    where a sequential sum gives 0x3f80), and no gate leaves the output as is."""
+    nh, nkv, hd = 4, 2, 128
+    bf = lambda a: orc.f2bf(np.asarray(a, np.float32))
+    v = np.zeros((16, nkv, hd), np.float32)
+    v[0], v[8], v[1:8] = 16.0, 2.0 ** -4, 2.0 ** -20
+    out = torch.zeros(nh * hd, dtype=torch.int16, device=dev)
+    pq.attn_ref(_t16(bf(np.zeros(nh * hd)), dev), nh * hd, _t16(bf(np.ones(16 * nkv * hd)), dev), _t16(bf(v), dev),
+                15, nh, nkv, hd, 1, 0.125, out, nh * hd)
+    assert (_u16(out) == 0x3F81).all()
+
+
 # T past one 32-position tile (33, 100, 256: the tile at 0 alone reads and then
 # rewrites the ring), T below the tap count (7, 3), a channel count that is not
 # a multiple of 64

@@ -330,6 +330,85 @@ def test_attention_vs_two_pass(orc):
             assert np.array_equal(orc.attn(q, Kc, Vc, 1, nh, nkv, hd, 0.125), want)
 
 
+def _twopass_bf16cache(q, Kc, Vc, npos, nh, nkv, hd, scale, win=0):
+    """Softmax attention in double over a bf16 cache (keys lo..npos-1)."""
+    lo = npos - win if win > 0 and npos > win else 0
+    qf = orc_bf2f_np(q).astype(np.float64).reshape(nh, hd)
+    K = orc_bf2f_np(Kc).astype(np.float64).reshape(npos, nkv, hd)[lo:]
+    V = orc_bf2f_np(Vc).astype(np.float64).reshape(npos, nkv, hd)[lo:]
+    out = np.empty((nh, hd))
+    for h in range(nh):
+        g = h // (nh // nkv)
+        s = K[:, g] @ qf[h] * scale
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ V[:, g]
+    return out.reshape(-1)
+
+
+def _sim_attn_ref(orc, q, Kc, Vc, npos, nh, nkv, hd, scale, win=0):
+    """k_attn_head (lfm3_nanode.cu:503-602) vectorised over keys: lane chains
+    [key][32 lanes], the shfl_down trees, thread sums [256 threads], warp
+    trees, the segment chains [8 segments] added pairwise."""
+    lo = npos - win if win > 0 and npos > win else 0
+    np_ = npos - lo
+    e = hd // 32
+    qf = orc_bf2f_np(q).reshape(nh, 32, e)
+    K = orc_bf2f_np(Kc).reshape(npos, nkv, 32, e)[lo:]
+    V = orc_bf2f_np(Vc).reshape(npos, nkv, hd)[lo:]
+    out = np.empty((nh, hd), np.uint16)
+    for h in range(nh):
+        g = h // (nh // nkv)
+        chain = np.zeros((np_, 32), np.float32)
+        for j in range(e):
+            chain = chain + qf[h, :, j] * K[:, g, :, j]
+        sc = _sim_tree(chain) * np.float32(scale)
+        m = np.float32(max(np.float32(-1e30), sc.max()))
+        ex = orc.expf(sc - m)
+        th = np.zeros(256, np.float32)
+        for i0 in range(0, np_, 256):
+            blk = ex[i0:i0 + 256]
+            th[:blk.size] = th[:blk.size] + blk
+        w = _sim_tree(th.reshape(8, 32))
+        tot = ((w[0] + w[4]) + (w[2] + w[6])) + ((w[1] + w[5]) + (w[3] + w[7]))
+        wt = ex * (np.float32(1) / tot)
+        sg = np.zeros((8, hd), np.float32)
+        for i in range(np_):
+            sg[i % 8] = sg[i % 8] + wt[i] * V[i, g]
+        o = ((sg[0] + sg[1]) + (sg[2] + sg[3])) + ((sg[4] + sg[5]) + (sg[6] + sg[7]))
+        out[h] = orc.f2bf(o)
+    return out.reshape(-1)
+
+
+def test_attention_reference_order(orc):
+    """orc_attn_ref, k_attn_head's order over a bf16 cache: one key gives its
+    value row exactly; the 8 value segments add pairwise (16 keys of equal
+    score, so every weight is 2^-4: segment 0 holds 1 + 2^-8, the seven others
+    2^-24 each; pairwise they sum to 1 + 2^-8 + 3 * 2^-23, above the bf16
+    midpoint, 0x3f81, where a sequential sum stays at the midpoint and rounds
+    to 0x3f80); against a double-precision softmax within bf16 rounding; and
+    against a vectorised transcription of the kernel, bit for bit."""
+    bf = lambda a: orc.f2bf(np.asarray(a, np.float32))
+    nh, nkv = 4, 2
+    for hd in (64, 128):
+        q = bf(orc.gen_normal(90 + hd, nh * hd))
+        Kc = bf(orc.gen_normal(91 + hd, nkv * hd))
+        Vc = bf(orc.gen_normal(92 + hd, nkv * hd) * 3)
+        want = np.repeat(Vc.reshape(nkv, hd), nh // nkv, axis=0).reshape(-1)
+        assert np.array_equal(orc.attn_ref(q, Kc, Vc, 1, nh, nkv, hd, 0.125), want)
+        v = np.zeros((16, nkv, hd), np.float32)
+        v[0], v[8], v[1:8] = 16.0, 2.0 ** -4, 2.0 ** -20
+        out = orc.attn_ref(bf(np.zeros(nh * hd)), bf(np.ones(16 * nkv * hd)), bf(v), 16, nh, nkv, hd, 0.125)
+        assert (out == 0x3F81).all()
+    for hd, npos, win in ((64, 300, 0), (128, 600, 0), (128, 300, 100), (64, 700, 256), (128, 5, 0)):
+        q = bf(orc.gen_normal(93 + npos, nh * hd))
+        Kc = bf(orc.gen_normal(94 + npos, npos * nkv * hd))
+        Vc = bf(orc.gen_normal(95 + npos, npos * nkv * hd))
+        a = orc.attn_ref(q, Kc, Vc, npos, nh, nkv, hd, 0.125, win)
+        b = _twopass_bf16cache(q, Kc, Vc, npos, nh, nkv, hd, 0.125, win)
+        assert np.abs(orc.bf2f(a) - b).max() <= np.abs(b).max() * 2 ** -7, (hd, npos, win)
+        assert np.array_equal(a, _sim_attn_ref(orc, q, Kc, Vc, npos, nh, nkv, hd, 0.125, win)), (hd, npos, win)
+
+
 @pytest.mark.parametrize("hd", [64, 128])
 def test_attention_window(orc, hd):
     """Sliding-window layers (k_attn_head's lo = npos - win when npos > win,
