@@ -3,11 +3,13 @@
 // KV cache [pos][nkv][hd] (written by pq_qk_prep_ref, as k_kv_write copies the
 // bf16 rows, 157-162), then k_sigmoid_gate's gate (852-858).
 //
-// One 256-thread workgroup per (q head, query position t), as the reference
-// launches it (a block of 256 per head; blockIdx.y the chunk position). Its 8
-// warps of 32 are the 32-lane halves of the 4 waves (lane = tid & 31, warp =
-// tid >> 5), so every sum keeps its place:
-//   score p (warp p mod 8): lane l's chain s = fl(s + fl(q_d * k_d)) over its
+// One workgroup per (q head, query position t), as the reference launches a
+// block of 256 per head (blockIdx.y the chunk position). Threads 0..255 are
+// the reference's: its 8 warps of 32 are the 32-lane halves of waves 0-3
+// (lane = tid & 31, warp = tid >> 5), so every sum keeps its place. The scores
+// do not depend on which warp forms them, so all 32 warps of the 1024 threads
+// share them (a quarter of the key rounds, four waves a SIMD to hide latency):
+//   score p (warp p mod 32): lane l's chain s = fl(s + fl(q_d * k_d)) over its
 //     hd/32 dims from 0, the shfl_down tree over the 32 lanes, fl(s * scale);
 //   m = the largest score (a max: any order gives it);
 //   e_p = e^(s_p - m) by pq::expf_pq, the build's e^x, where the reference
@@ -72,8 +74,10 @@ __device__ __forceinline__ void kv_unpack(const typename KVPiece<E>::T &w, float
   }
 }
 
+constexpr int kArThreads = 1024;     // 32 warps for the scores; the first 256 are the reference's
+
 template <int HD>
-__global__ __launch_bounds__(256) void attn_ref_kernel(const uint16_t *__restrict__ q, int q_stride,
+__global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__restrict__ q, int q_stride,
                                                         const uint16_t *__restrict__ kc,
                                                         const uint16_t *__restrict__ vc,
                                                         const uint16_t *__restrict__ gate, int gate_stride,
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(const uint16_t *__restric
   constexpr int E = HD / 32;
   using KT = typename KVPiece<E>::T;
   extern __shared__ __align__(16) float sl[];   // the window's scores, then their e
-  __shared__ float red[8];
+  __shared__ float red[kArThreads / 64];
   __shared__ float seg[8][HD];
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 31, wid = tid >> 5;
   const int npos = (pos_dev != nullptr ? *pos_dev : pos0) + t + 1;
@@ -98,22 +102,25 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(const uint16_t *__restric
                                                                       npos * kvd * 2, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vc), (short)0,
                                                                       npos * kvd * 2, kRsrcWord3);
-  // warp w's keys (and value segment): lo + w + 8j, j < nk, in rounds of
-  // kArRound keys whose loads all go out before the round is computed; the
-  // first round of value rows is loaded before the softmax, which hides its
-  // latency. With one wave a SIMD the kernel is bound by instruction latency,
-  // so short rounds (the fewest key slots issued past the window) measured
-  // fastest: 290 keys 7.8 us at 8 a round, 8.4 at 16, 10.5 at 64 (head_dim 64).
+  // score warp w's keys: lo + w + 32j; value segment w's (w < 8): lo + w + 8j.
+  // Rounds of kArRound keys whose loads all go out before the round is
+  // computed; the first round of value rows is loaded before the softmax,
+  // which hides its latency. The kernel is bound by instruction latency, so
+  // short rounds (the fewest key slots issued past the window) measured
+  // fastest: 290 keys at 256 threads 7.8 us at 8 a round, 8.4 at 16, 10.5 at 64
+  // (head_dim 64).
   constexpr int B = kArRound;
-  const int nk = np > wid ? (np - wid + 7) / 8 : 0;
-  auto key_off = [&](int j) { return (int)(((size_t)(lo + wid + 8 * j) * kvd + kvo) * 2); };
-  auto ld = [&](__amdgpu_buffer_rsrc_t r, KT *w, int j0) {
+  constexpr int W = kArThreads / 32;   // score warps
+  const int nks = np > wid ? (np - wid + W - 1) / W : 0;   // this warp's keys: lo + wid + W j
+  const int nk = np > wid ? (np - wid + 7) / 8 : 0;        // segment wid's keys (wid < 8): lo + wid + 8 j
+  auto ld = [&](__amdgpu_buffer_rsrc_t r, KT *w, int j0, int stride) {
 #pragma unroll
-    for (int b = 0; b < B; b++) w[b] = kv_load<E>(r, key_off(j0 + b));
+    for (int b = 0; b < B; b++)
+      w[b] = kv_load<E>(r, (int)(((size_t)(lo + wid + stride * (j0 + b)) * kvd + kvo) * 2));
   };
   KT wk[B], wv[B];
-  for (int j0 = 0; j0 < nk; j0 += B) {
-    ld(rk, wk, j0);
+  for (int j0 = 0; j0 < nks; j0 += B) {
+    ld(rk, wk, j0, W);
     float s[B];
 #pragma unroll
     for (int b = 0; b < B; b++) {
@@ -137,36 +144,40 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(const uint16_t *__restric
     if (lane == 0) {
 #pragma unroll
       for (int b = 0; b < B; b++) {
-        const int i = wid + 8 * (j0 + b);
+        const int i = wid + W * (j0 + b);
         if (i < np) sl[i] = s[b] * scale;
       }
     }
   }
-  ld(rv, wv, 0);
+  if (wid < 8) ld(rv, wv, 0, 8);
   __syncthreads();
   float mx = -1e30f;
-  for (int i = tid; i < np; i += 256) mx = fmaxf(mx, sl[i]);
+  for (int i = tid; i < np; i += kArThreads) mx = fmaxf(mx, sl[i]);
   mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
-  const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < kArThreads / 64; w++) m = fmaxf(m, red[w]);
   __syncthreads();
-  float sum = 0.0f;
-  for (int i = tid; i < np; i += 256) {
-    const float e = expf_pq(sl[i] - m);
-    sl[i] = e;
-    sum = sum + e;
+  if (tid < 256) {   // the reference's threads: e over keys tid, tid + 256, ..., then the warp trees
+    float sum = 0.0f;
+    for (int i = tid; i < np; i += 256) {
+      const float e = expf_pq(sl[i] - m);
+      sl[i] = e;
+      sum = sum + e;
+    }
+    sum = warp_tree32(sum);
+    if (lane == 0) red[wid] = sum;
   }
-  sum = warp_tree32(sum);
-  if (lane == 0) red[wid] = sum;
   __syncthreads();
   const float inv = 1.0f / (((red[0] + red[4]) + (red[2] + red[6])) + ((red[1] + red[5]) + (red[3] + red[7])));
   // the value sum of segment wid over keys wid, wid + 8, ... (from lo)
   float acc[E];
 #pragma unroll
   for (int j = 0; j < E; j++) acc[j] = 0.0f;
-  for (int j0 = 0; j0 < nk; j0 += B) {
-    if (j0 > 0) ld(rv, wv, j0);
+  for (int j0 = 0; j0 < (wid < 8 ? nk : 0); j0 += B) {
+    if (j0 > 0) ld(rv, wv, j0, 8);
     // branch-free, so the round's weight reads from LDS go out together: keys
     // past the window read a clamped slot and leave acc as it is (a select)
 #pragma unroll
@@ -182,8 +193,10 @@ __global__ __launch_bounds__(256) void attn_ref_kernel(const uint16_t *__restric
       }
     }
   }
+  if (wid < 8) {
 #pragma unroll
-  for (int j = 0; j < E; j++) seg[wid][lane * E + j] = acc[j];
+    for (int j = 0; j < E; j++) seg[wid][lane * E + j] = acc[j];
+  }
   __syncthreads();
   if (tid < HD) {
     const float o = ((seg[0][tid] + seg[1][tid]) + (seg[2][tid] + seg[3][tid])) +
@@ -201,7 +214,7 @@ static int attn_ref_launch(const uint16_t *q, int q_stride, const uint16_t *kcac
                            const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int pos0,
                            const int32_t *pos_dev, int keys, int nh, int nkv, int hd, int T, float scale, int win,
                            hipStream_t st) {
-  const dim3 grid((unsigned)nh, (unsigned)T), block(256);
+  const dim3 grid((unsigned)nh, (unsigned)T), block(kArThreads);
   const size_t lds = (size_t)keys * sizeof(float);
   if (hd == 64)
     launch(attn_ref_kernel<64>, grid, block, lds, st, q, q_stride, kcache, vcache, gate, gate_stride, out,
