@@ -278,11 +278,11 @@ int pq_attn_decode(const uint16_t *q, int q_stride, const uint16_t *kcache, cons
  * pq_qk_prep with the cache holding the bf16 k and v rows as k_kv_write copies
  * them (157-162); pq_attn_ref attends query t (row t of q) at position pos0+t
  * to keys lo..pos0+t of that bf16 cache (lo as in pq_attn_decode) with one
- * 256-thread workgroup per (head, t), whose 8 32-lane warps keep the
- * reference's places: each score a chain over the lane's hd/32 dims and the
- * shfl_down tree; the softmax sum per thread over keys t, t+256, ..., the warp
- * tree, the 8 warps' tree; the probabilities normalized before an 8-segment
- * value sum added pairwise. e^x is the build's expf_pq where the reference
+ * 1024-thread workgroup per (head, t): each score a chain over the lane's
+ * hd/32 dims and the shfl_down tree of a 32-lane warp (32 warps share the
+ * keys); then its first 256 threads keep the reference's places: the softmax
+ * sum per thread over keys t, t+256, ..., the warp tree, the 8 warps' tree;
+ * the probabilities normalized before an 8-segment value sum added pairwise. e^x is the build's expf_pq where the reference
  * calls CUDA's expf. head_dim 64 or 128; at most 32768 keys in a window;
  * gate NULL for none; out bf16 [T] rows of stride out_stride. */
 int pq_qk_prep_ref(uint16_t *qkv, int row_stride, const float *q_norm, const float *k_norm,
@@ -291,6 +291,20 @@ int pq_qk_prep_ref(uint16_t *qkv, int row_stride, const float *q_norm, const flo
 int pq_attn_ref(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
                 const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int pos0, int nh,
                 int nkv, int hd, int T, float scale, int win, void *stream);
+
+/* One decode token's pq_qk_prep_ref + pq_attn_ref in a single launch, with
+ * the same results (outputs and cache rows bit for bit): qkv is the token's
+ * projected row [q (nh hd) | k (nkv hd) | v (nkv hd)] (left unchanged; the
+ * rotated q stays on chip), the token at position pos; the k and v rows of pos
+ * go to the cache and into each workgroup's LDS, and its key and value are
+ * taken from there, so no workgroup waits on another's cache write. gate NULL
+ * for none (one bf16 per head); out bf16 [nh hd]. Replaces k_headnorm,
+ * k_rope, k_kv_write, k_attn_head and k_sigmoid_gate of one decode step
+ * (lfm3_nanode.cu:460-498, 157-162, 503-602, 852-858). */
+int pq_attn_decode_ref(const uint16_t *qkv, const float *q_norm, const float *k_norm,
+                       const float *rope_cs, uint16_t *kcache, uint16_t *vcache, const uint16_t *gate,
+                       uint16_t *out, int pos, int nh, int nkv, int hd, int rot, float eps, float scale,
+                       int win, void *stream);
 
 /* Gated short conv over T positions: bcx rows [B | C | x] (3H), ring
  * [ntaps][H] bf16 (newest last, updated), out [T][H] bf16 = bf16(C * conv(B*x)).

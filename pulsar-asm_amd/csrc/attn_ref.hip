@@ -76,32 +76,47 @@ __device__ __forceinline__ void kv_unpack(const typename KVPiece<E>::T &w, float
 
 constexpr int kArThreads = 1024;     // 32 warps for the scores; the first 256 are the reference's
 
-template <int HD>
+// The decode launch's own q/k prep (attn_ref_kernel<HD, true>): the inputs of
+// qk_prep_kernel for the token's q, k and v rows.
+struct AttnPrep {
+  const float *qn, *kn;   // q and k head-norm weights [hd]
+  const float *cs;        // RoPE (cos, sin) pairs [pos][rot / 2]
+  int rot;                // rotated dims
+  float eps;
+};
+
+// PREP (one decode token, T = 1): q is the token's projected row [q | k | v]
+// (nh, nkv, nkv heads), and the workgroup first forms the position's q, k and
+// v rows as qk_prep_kernel does (head norm and RoPE for q and k, v as it is):
+// q into qs, bf16 k and v into kvn, and the k and v rows into the cache by the
+// group's first q head. The cache reads stop before that row, which no
+// workgroup reads back; each workgroup takes the position's key and value from
+// kvn instead, as the last key of its score warp and of its value segment, so
+// every sum keeps the order of the unfused pair (pq_qk_prep_ref, then the
+// attention of this kernel without PREP).
+template <int HD, bool PREP>
 __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__restrict__ q, int q_stride,
-                                                        const uint16_t *__restrict__ kc,
-                                                        const uint16_t *__restrict__ vc,
+                                                        uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
                                                         const uint16_t *__restrict__ gate, int gate_stride,
                                                         uint16_t *__restrict__ out, int out_stride, int pos0,
                                                         const int32_t *__restrict__ pos_dev, int nh, int nkv,
-                                                        float scale, int win) {
+                                                        float scale, int win, AttnPrep pp) {
   constexpr int E = HD / 32;
   using KT = typename KVPiece<E>::T;
   extern __shared__ __align__(16) float sl[];   // the window's scores, then their e
   __shared__ float red[kArThreads / 64];
   __shared__ float seg[8][HD];
+  __shared__ float qs[PREP ? HD : 1];                      // PREP: the position's q
+  __shared__ __align__(16) uint16_t kvn[PREP ? 2 * HD : 2];   // PREP: its bf16 k, then v
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 31, wid = tid >> 5;
   const int npos = (pos_dev != nullptr ? *pos_dev : pos0) + t + 1;
   const int lo = window_lo(npos, win), np = npos - lo;
-  const int kvd = nkv * HD;
-  const size_t kvo = (size_t)(h / (nh / nkv)) * HD + lane * E;   // the lane's dims within a cache row
-  float qv[E];
-#pragma unroll
-  for (int j = 0; j < E; j++) qv[j] = bf2f(q[(size_t)t * q_stride + (size_t)h * HD + lane * E + j]);
-  // the caches up to the query's position: keys past it read zeros
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(kc), (short)0,
-                                                                      npos * kvd * 2, kRsrcWord3);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(vc), (short)0,
-                                                                      npos * kvd * 2, kRsrcWord3);
+  const int kvd = nkv * HD, kvh = h / (nh / nkv);
+  const size_t kvo = (size_t)kvh * HD + lane * E;   // the lane's dims within a cache row
+  // the caches up to the query's position (PREP: before it): keys past read zeros
+  const int nrow = PREP ? npos - 1 : npos;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kc, (short)0, nrow * kvd * 2, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vc, (short)0, nrow * kvd * 2, kRsrcWord3);
   // score warp w's keys: lo + w + 32j; value segment w's (w < 8): lo + w + 8j.
   // Rounds of kArRound keys whose loads all go out before the round is
   // computed; the first round of value rows is loaded before the softmax,
@@ -119,8 +134,58 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
       w[b] = kv_load<E>(r, (int)(((size_t)(lo + wid + stride * (j0 + b)) * kvd + kvo) * 2));
   };
   KT wk[B], wv[B];
+  if (nks > 0) ld(rk, wk, 0, W);   // the first round's keys load during the prep
+  float qv[E];
+  if constexpr (PREP) {
+    if (tid < 192) {   // wave 0: q, wave 1: k, wave 2: v
+      constexpr int EH = HD / 64;
+      const int l = tid & 63, part = tid >> 6, pos = npos - 1;
+      const uint16_t *src = q + (part == 0 ? h * HD : nh * HD + (part - 1) * kvd + kvh * HD);
+      uint16_t *dst = (part == 1 ? kc : vc) + (size_t)pos * kvd + kvh * HD;
+      const bool writer = h % (nh / nkv) == 0;
+      if (part == 2) {
+#pragma unroll
+        for (int e = 0; e < EH; e++) {
+          const uint16_t vb = src[l + 64 * e];
+          kvn[HD + l + 64 * e] = vb;
+          if (writer) dst[l + 64 * e] = vb;
+        }
+      } else {
+        const float *w = part == 0 ? pp.qn : pp.kn;
+        float x[EH], wn[EH], r[EH];
+#pragma unroll
+        for (int e = 0; e < EH; e++) {
+          x[e] = bf2f(src[l + 64 * e]);
+          wn[e] = w[l + 64 * e];
+        }
+        const int half = pp.rot / 2, pair = HD == 64 ? (l & 31) : l;
+        float c = 1.0f, sn = 0.0f;
+        if (pair < half) {
+          c = pp.cs[((size_t)pos * half + pair) * 2];
+          sn = pp.cs[((size_t)pos * half + pair) * 2 + 1];
+        }
+        norm_rope<HD>(x, wn, c, sn, pp.rot, pp.eps, l, r);
+#pragma unroll
+        for (int e = 0; e < EH; e++) {
+          if (part == 0) {
+            qs[l + 64 * e] = r[e];
+          } else {
+            const uint16_t kb = f2bf(r[e]);
+            kvn[l + 64 * e] = kb;
+            if (writer) dst[l + 64 * e] = kb;
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < E; j++) qv[j] = qs[lane * E + j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < E; j++) qv[j] = bf2f(q[(size_t)t * q_stride + (size_t)h * HD + lane * E + j]);
+  }
   for (int j0 = 0; j0 < nks; j0 += B) {
-    ld(rk, wk, j0, W);
+    if (j0 > 0) ld(rk, wk, j0, W);
     float s[B];
 #pragma unroll
     for (int b = 0; b < B; b++) {
@@ -149,6 +214,16 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
       }
     }
   }
+  if constexpr (PREP) {   // the position's own key (read as zeros above), from kvn
+    const int ws = (np - 1) % W;
+    if ((wid >> 1) == (ws >> 1)) {   // its whole wave, for the tree
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < E; j++) s = s + qv[j] * __uint_as_float((uint32_t)kvn[lane * E + j] << 16);
+      s = warp_tree32(s);
+      if (wid == ws && lane == 0) sl[np - 1] = s * scale;
+    }
+  }
   if (wid < 8) ld(rv, wv, 0, 8);
   __syncthreads();
   float mx = -1e30f;
@@ -172,7 +247,9 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
   }
   __syncthreads();
   const float inv = 1.0f / (((red[0] + red[4]) + (red[2] + red[6])) + ((red[1] + red[5]) + (red[3] + red[7])));
-  // the value sum of segment wid over keys wid, wid + 8, ... (from lo)
+  // the value sum of segment wid over keys wid, wid + 8, ... (from lo); PREP
+  // leaves the last key to the step after the loop
+  const int npv = PREP ? np - 1 : np;
   float acc[E];
 #pragma unroll
   for (int j = 0; j < E; j++) acc[j] = 0.0f;
@@ -189,8 +266,15 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
 #pragma unroll
       for (int j = 0; j < E; j++) {
         const float a = acc[j] + wt * vf[j];
-        acc[j] = i < np ? a : acc[j];
+        acc[j] = i < npv ? a : acc[j];
       }
+    }
+  }
+  if constexpr (PREP) {   // the position's own value row: its segment's last key
+    if (wid == (np - 1) % 8) {
+      const float wt = sl[np - 1] * inv;
+#pragma unroll
+      for (int j = 0; j < E; j++) acc[j] = acc[j] + wt * __uint_as_float((uint32_t)kvn[HD + lane * E + j] << 16);
     }
   }
   if (wid < 8) {
@@ -210,19 +294,27 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
   }
 }
 
+// pp non-null: the PREP kernel (T = 1)
 static int attn_ref_launch(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
                            const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int pos0,
                            const int32_t *pos_dev, int keys, int nh, int nkv, int hd, int T, float scale, int win,
-                           hipStream_t st) {
+                           const AttnPrep *pp, hipStream_t st) {
   const dim3 grid((unsigned)nh, (unsigned)T), block(kArThreads);
   const size_t lds = (size_t)keys * sizeof(float);
-  if (hd == 64)
-    launch(attn_ref_kernel<64>, grid, block, lds, st, q, q_stride, kcache, vcache, gate, gate_stride, out,
-           out_stride, pos0, pos_dev, nh, nkv, scale, win);
-  else
-    launch(attn_ref_kernel<128>, grid, block, lds, st, q, q_stride, kcache, vcache, gate, gate_stride, out,
-           out_stride, pos0, pos_dev, nh, nkv, scale, win);
-  return check_launch("pq_attn_ref");
+  uint16_t *kc = const_cast<uint16_t *>(kcache), *vc = const_cast<uint16_t *>(vcache);
+  const AttnPrep p = pp != nullptr ? *pp : AttnPrep{};
+#define PQ_AR(HH, PR)                                                                                              \
+  launch(attn_ref_kernel<HH, PR>, grid, block, lds, st, q, q_stride, kc, vc, gate, gate_stride, out, out_stride, \
+         pos0, pos_dev, nh, nkv, scale, win, p)
+  if (hd == 64) {
+    if (pp != nullptr) PQ_AR(64, true);
+    else PQ_AR(64, false);
+  } else {
+    if (pp != nullptr) PQ_AR(128, true);
+    else PQ_AR(128, false);
+  }
+#undef PQ_AR
+  return check_launch(pp != nullptr ? "pq_attn_decode_ref" : "pq_attn_ref");
 }
 
 static int attn_ref_check(const uint16_t *q, const uint16_t *kcache, const uint16_t *vcache, const uint16_t *out,
@@ -236,6 +328,13 @@ static int attn_ref_check(const uint16_t *q, const uint16_t *kcache, const uint1
   return PQ_OK;
 }
 
+static int attn_prep_check(const float *q_norm, const float *k_norm, const float *rope_cs, int hd, int rot,
+                           const char *who) {
+  PQ_REQUIRE(q_norm && k_norm && rope_cs, PQ_ERR_ARG, "%s: null pointer", who);
+  PQ_REQUIRE(rot >= 0 && rot <= hd && rot % 2 == 0, PQ_ERR_ARG, "%s: rot=%d (even, at most head_dim)", who, rot);
+  return PQ_OK;
+}
+
 // pq_attn_ref at the device position *pos_dev: LDS for the keys of any
 // position below ctx.
 int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
@@ -246,7 +345,25 @@ int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const 
   const int rc = attn_ref_check(q, kcache, vcache, out, nh, nkv, hd, 1, win, keys, "attn_ref_dev");
   if (rc) return rc;
   return attn_ref_launch(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, 0, pos_dev, keys, nh, nkv,
-                         hd, 1, scale, win, st);
+                         hd, 1, scale, win, nullptr, st);
+}
+
+// pq_attn_decode_ref at the device position *pos_dev (pos_dev null: pos):
+// LDS for the keys of any position below ctx.
+int attn_decode_ref_dev(const uint16_t *qkv, const float *q_norm, const float *k_norm, const float *rope_cs,
+                        uint16_t *kcache, uint16_t *vcache, const uint16_t *gate, uint16_t *out, int pos,
+                        const int32_t *pos_dev, int ctx, int nh, int nkv, int hd, int rot, float eps, float scale,
+                        int win, hipStream_t st) {
+  const int keys = win > 0 && win < ctx ? win : ctx;
+  PQ_REQUIRE(ctx > 0 && (pos_dev || (pos >= 0 && pos < ctx)), PQ_ERR_ARG, "pq_attn_decode_ref: pos=%d ctx=%d",
+             pos, ctx);
+  int rc = attn_ref_check(qkv, kcache, vcache, out, nh, nkv, hd, 1, win, keys, "pq_attn_decode_ref");
+  if (rc) return rc;
+  rc = attn_prep_check(q_norm, k_norm, rope_cs, hd, rot, "pq_attn_decode_ref");
+  if (rc) return rc;
+  const AttnPrep pp{q_norm, k_norm, rope_cs, rot, eps};
+  return attn_ref_launch(qkv, 0, kcache, vcache, gate, 0, out, 0, pos, pos_dev, keys, nh, nkv, hd, 1, scale, win,
+                         &pp, st);
 }
 
 }  // namespace pq
@@ -262,5 +379,13 @@ extern "C" int pq_attn_ref(const uint16_t *q, int q_stride, const uint16_t *kcac
   const int rc = attn_ref_check(q, kcache, vcache, out, nh, nkv, hd, T, win, keys, "pq_attn_ref");
   if (rc) return rc;
   return attn_ref_launch(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, pos0, nullptr, keys, nh,
-                         nkv, hd, T, scale, win, as_stream(stream));
+                         nkv, hd, T, scale, win, nullptr, as_stream(stream));
+}
+
+extern "C" int pq_attn_decode_ref(const uint16_t *qkv, const float *q_norm, const float *k_norm,
+                                  const float *rope_cs, uint16_t *kcache, uint16_t *vcache, const uint16_t *gate,
+                                  uint16_t *out, int pos, int nh, int nkv, int hd, int rot, float eps, float scale,
+                                  int win, void *stream) {
+  return attn_decode_ref_dev(qkv, q_norm, k_norm, rope_cs, kcache, vcache, gate, out, pos, nullptr, pos + 1, nh, nkv,
+                             hd, rot, eps, scale, win, as_stream(stream));
 }

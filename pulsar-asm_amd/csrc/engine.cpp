@@ -815,6 +815,16 @@ static bool qlow_swiglu(const Q8Dev &w) {
          parts_fusable(w, PQ_PRO_RESNORM);
 }
 
+// The decode token's q/k prep inside its attention launch
+// (PQ_ATTN_PREP=0: pq_qk_prep_ref's kernel, then the attention).
+static bool attn_prep_fused() {
+  static const bool off = [] {
+    const char *e = getenv("PQ_ATTN_PREP");
+    return e != nullptr && atoi(e) == 0;
+  }();
+  return !off;
+}
+
 static int forward_decode_r2(Engine &E, bool dev) {
   const pq_model_cfg &c = E.c;
   const int H = c.hidden;
@@ -882,14 +892,20 @@ static int forward_decode_r2(Engine &E, bool dev) {
     }
     if (D.attn) {   // k_attn_head's order over the bf16 cache
       const int32_t *pd = dev ? E.ctr + 1 : nullptr;
-      PQ_TRY(qk_prep_launch(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, pd, c.nh, c.nkv,
-                            c.hd, layer_rot(E, D), 1, c.eps, E.st, true));
-      if (dev)
-        PQ_TRY(attn_ref_dev(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, pd, c.ctx, c.nh,
-                            c.nkv, c.hd, scale, layer_win(E, D), E.st));
-      else
-        PQ_TRY(pq_attn_ref(E.Wd, E.nin, D.kc, D.vc, E.Wd + E.qd + 2 * E.kvd, E.nin, E.A, E.qd, E.pos, c.nh, c.nkv,
-                           c.hd, 1, scale, layer_win(E, D), E.st));
+      const uint16_t *gate = E.Wd + E.qd + 2 * E.kvd;
+      if (attn_prep_fused()) {
+        PQ_TRY(attn_decode_ref_dev(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, gate, E.A, E.pos, pd,
+                                   c.ctx, c.nh, c.nkv, c.hd, layer_rot(E, D), c.eps, scale, layer_win(E, D), E.st));
+      } else {
+        PQ_TRY(qk_prep_launch(E.Wd, E.nin, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, E.pos, pd, c.nh,
+                              c.nkv, c.hd, layer_rot(E, D), 1, c.eps, E.st, true));
+        if (dev)
+          PQ_TRY(attn_ref_dev(E.Wd, E.nin, D.kc, D.vc, gate, E.nin, E.A, E.qd, pd, c.ctx, c.nh, c.nkv, c.hd, scale,
+                              layer_win(E, D), E.st));
+        else
+          PQ_TRY(pq_attn_ref(E.Wd, E.nin, D.kc, D.vc, gate, E.nin, E.A, E.qd, E.pos, c.nh, c.nkv, c.hd, 1, scale,
+                             layer_win(E, D), E.st));
+      }
       PQ_TRY(plain(D.out, E.A, E.Hb));
     } else if (D.out.split() && parts_fusable(D.out, PQ_PRO_CONV)) {
       p = pq_gemv_prologue{};

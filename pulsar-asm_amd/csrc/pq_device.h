@@ -326,6 +326,38 @@ __device__ __forceinline__ float head_sumsq(const float *x) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
 }
 
+// q/k head norm + RoPE from preloaded inputs: x[e] and wv[e] are element
+// lane + 64e of the head and of its norm weight, (c, sn) the cos/sin of the
+// lane's RoPE pair: pair lane & 31 for head_dim 64 (elements i and i + 32
+// sit in lanes i and i + 32), pair lane for head_dim 128 (elements lane and
+// lane + 64 in one lane). The arithmetic of qk_prep_kernel
+// (shared by the fused attention launches).
+template <int HD>
+__device__ __forceinline__ void norm_rope(const float *x, const float *wv, float c, float sn, int rot, float eps,
+                                          int lane, float *r) {
+  constexpr int E = HD / 64;
+  float v[E];
+  const float rs = 1.0f / sqrtf(head_sumsq<HD>(x) * (1.0f / (float)HD) + eps);
+#pragma unroll
+  for (int e = 0; e < E; e++) v[e] = bf2f(f2bf(wv[e] * bf2f(f2bf(x[e] * rs))));
+  const int half = rot / 2;
+  if constexpr (HD == 64) {
+    const float up = __shfl_down(v[0], 32, 64);
+    const float dn = __shfl_up(v[0], 32, 64);
+    r[0] = v[0];
+    if ((lane & 31) < half) r[0] = lane < 32 ? v[0] * c - up * sn : v[0] * c + dn * sn;
+  } else {
+    r[0] = v[0];
+    r[1] = v[1];
+    if (lane < half) {
+      r[0] = v[0] * c - v[1] * sn;
+      r[1] = v[1] * c + v[0] * sn;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; e++) r[e] = bf2f(f2bf(r[e]));
+}
+
 // Greedy argmax in the reference's order (k_argmax, lfm3_nanode.cu:942-964):
 // its 256 threads scan i = tid, tid + 256, ... keeping the first strict
 // maximum above -1e30 (kAmFloor), then two shfl_down trees (the 32 lanes of a

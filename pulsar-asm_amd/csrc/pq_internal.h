@@ -31,6 +31,13 @@ int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const 
                  const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, const int32_t *pos_dev,
                  int ctx, int nh, int nkv, int hd, float scale, int win, hipStream_t st);
 
+// pq_attn_decode_ref at the device position *pos_dev (null: at pos); LDS
+// sized for positions below ctx.
+int attn_decode_ref_dev(const uint16_t *qkv, const float *q_norm, const float *k_norm, const float *rope_cs,
+                        uint16_t *kcache, uint16_t *vcache, const uint16_t *gate, uint16_t *out, int pos,
+                        const int32_t *pos_dev, int ctx, int nh, int nkv, int hd, int rot, float eps, float scale,
+                        int win, hipStream_t st);
+
 // pq_attn_decode for one query at the device position *pos_dev (keys up to
 // it, window win), sized for positions below ctx.
 int attn_decode_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,

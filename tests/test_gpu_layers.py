@@ -180,6 +180,68 @@ def test_attention_ref_segment_order(orc, pq, dev):
     assert (_u16(out) == 0x3F81).all()
 
 
+# pq_attn_decode_ref (one decode token's q/k prep inside its attention launch)
+# against the oracle's head norm + RoPE + cache write, then orc_attn_ref and
+# the gate, bit for bit -- output and both cache rows, the projected row left
+# as it was -- and against the unfused pair pq_qk_prep_ref + pq_attn_ref.
+# The position's own key is the last of its score warp (32 warps) and of its
+# value segment (8): positions 0, 1, 31, 32, 63, 64, 256 and 289 put it in
+# the first or the last warp and segment, in a half-active wave (256: warp 0
+# has a round more than warp 1); GQA groups 1, 4 and 8, head_dim 64 and 128,
+# partial and full RoPE, windows 256, 100 and 1.
+@pytest.mark.parametrize("pos,nh,nkv,hd,rot,win", [
+    (0, 32, 8, 64, 32, 0), (1, 32, 8, 64, 32, 0), (31, 32, 8, 64, 32, 0), (32, 32, 8, 64, 32, 0),
+    (256, 32, 8, 64, 32, 0), (2047, 32, 8, 64, 32, 0),
+    (0, 16, 4, 128, 64, 0), (63, 16, 4, 128, 64, 0), (64, 16, 4, 128, 64, 0), (289, 16, 4, 128, 64, 0),
+    (1999, 16, 4, 128, 128, 256), (300, 16, 4, 128, 128, 256), (150, 8, 8, 64, 64, 100), (90, 16, 4, 128, 128, 1),
+    (700, 8, 1, 128, 64, 0)])
+def test_attention_decode_ref(orc, pq, dev, pos, nh, nkv, hd, rot, win):
+    ctx = pos + 3
+    kvd = nkv * hd
+    nin, rows, qn, kn, _ = _qkv_case(orc, nh, nkv, hd, 1, ctx, SEED + 31 * pos + hd)
+    cs = orc.rope_table(ctx, hd, rot, 1e6 if rot < hd else 1e4)
+    kc0 = np.zeros((ctx, kvd), np.uint16)
+    vc0 = np.zeros((ctx, kvd), np.uint16)
+    kc0[:pos] = orc.f2bf(orc.gen_normal(SEED + 5 * pos, pos * kvd).reshape(pos, kvd) * 2)
+    vc0[:pos] = orc.f2bf(orc.gen_normal(SEED + 5 * pos + 1, pos * kvd).reshape(pos, kvd) * 5)
+    r = rows[0]
+    qr = orc.rope(orc.headnorm(r[:nh * hd], qn, nh, hd), cs, pos, nh, hd, rot)
+    kc_r, vc_r = kc0.copy(), vc0.copy()
+    kc_r[pos] = orc.rope(orc.headnorm(r[nh * hd:nh * hd + kvd], kn, nkv, hd), cs, pos, nkv, hd, rot)
+    vc_r[pos] = r[nh * hd + kvd:nh * hd + 2 * kvd]
+    gate = r[nh * hd + 2 * kvd:]
+    scale = 1.0 / np.sqrt(hd)
+    want = orc.sigmoid_gate(gate, orc.attn_ref(qr, kc_r, vc_r, pos + 1, nh, nkv, hd, scale, win), nh, hd)
+    qkv = _t16(rows, dev)
+    qnd, knd, csd = (torch.from_numpy(a).to(dev) for a in (qn, kn, cs))
+    kc, vc = _t16(kc0, dev), _t16(vc0, dev)
+    out = torch.zeros(nh * hd, dtype=torch.int16, device=dev)
+    gd = qkv[0, nh * hd + 2 * kvd:]
+    pq.attn_decode_ref(qkv, qnd, knd, csd, kc, vc, pos, nh, nkv, hd, rot, scale, out, gate=gd, win=win)
+    got = _u16(out)
+    bad = np.argwhere(got != want)
+    assert bad.shape[0] == 0, f"{bad.shape[0]} differ, first {bad[:4].tolist()}"
+    assert np.array_equal(_u16(kc), kc_r) and np.array_equal(_u16(vc), vc_r)
+    assert np.array_equal(_u16(qkv), rows)
+    # the unfused pair on the same inputs
+    qkv2, kc2, vc2 = _t16(rows, dev), _t16(kc0, dev), _t16(vc0, dev)
+    out2 = torch.zeros(nh * hd, dtype=torch.int16, device=dev)
+    pq.qk_prep_ref(qkv2, nin, qnd, knd, csd, kc2, vc2, pos, nh, nkv, hd, rot, 1)
+    pq.attn_ref(qkv2, nin, kc2, vc2, pos, nh, nkv, hd, 1, scale, out2, nh * hd, gate=qkv2[:, nh * hd + 2 * kvd:],
+                gate_stride=nin, win=win)
+    assert np.array_equal(_u16(out2), got)
+    assert np.array_equal(_u16(kc2), kc_r) and np.array_equal(_u16(vc2), vc_r)
+
+
+def test_attention_decode_ref_rejects(pq, dev):
+    """Bad shapes fail on the host with an error, before any launch."""
+    z16 = torch.zeros(4096, dtype=torch.int16, device=dev)
+    zf = torch.zeros(4096, dtype=torch.float32, device=dev)
+    for pos, hd, rot in [(-1, 64, 32), (5, 96, 32), (5, 64, 33), (5, 64, 66)]:
+        with pytest.raises(RuntimeError):
+            pq.attn_decode_ref(z16, zf, zf, zf, z16, z16, pos, 4, 2, hd, rot, 0.125, z16)
+
+
 # T past one 32-position tile (33, 100, 256: the tile at 0 alone reads and then
 # rewrites the ring), T below the tap count (7, 3), a channel count that is not
 # a multiple of 64
