@@ -792,6 +792,9 @@ static bool parts_fusable(const Q8Dev &w, int kind) {
 // A split slot's GEMVs at T = 1 with the prologue pro, each part writing its
 // rows of y (bf16). Every launch runs the prologue; the vectors it writes once
 // (x_out, ring_out) get the same values from each, from unchanged inputs.
+// (A second part forked onto another stream inside the captured step, to run
+// beside the first, cost about 22 us per fork and join: 0.728 -> 0.909 ms per
+// token of the Q4 backbone, whose attention gate rows stay Q8.)
 static int parts_fused(Engine &E, const Q8Dev &w, const pq_gemv_prologue &pro, uint16_t *y) {
   for (const Part &p : w.parts) {
     if (p.bits == 8)
@@ -858,7 +861,7 @@ static int forward_decode_r2(Engine &E, bool dev) {
     LayerDev &D = E.L[l];
     if (l == 0 && (E.emb_bf16 || D.in.split())) {   // the row into xa, then its norm
       PQ_TRY(embed_r2(E, E.tok, xa, 1));
-      if (D.in.split()) {
+      if (D.in.split() && !parts_fusable(D.in, PQ_PRO_NORM)) {
         PQ_TRY(pq_rmsnorm(xa, nullptr, D.op_norm, nullptr, E.A, nullptr, nullptr, H, 1, c.eps, E.st));
         PQ_TRY(plain(D.in, E.A, E.Wd));
       } else {
@@ -867,7 +870,8 @@ static int forward_decode_r2(Engine &E, bool dev) {
         p.x_in = xa;
         p.w0 = D.op_norm;
         p.eps = c.eps;
-        PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
+        if (D.in.split()) PQ_TRY(parts_fused(E, D.in, p, E.Wd));
+        else PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
       }
     } else if (l == 0) {   // the token's embedding row (written once to xa), normalized
       p = pq_gemv_prologue{};
