@@ -839,6 +839,45 @@ def gemv_profile_workload(pq, torch, dev, which, copies=3):
     print(json.dumps({"gemv_profile": which, "algorithmic_bytes": out}), flush=True)
 
 
+def shard_workload(pq, torch, dev, G=8, resident_mb=128):
+    """The config-2 GEMVs at the shapes one of G GPUs runs when the layer is
+    sharded: q|k|v, gate+up and the LM head by rows (N/G rows, then an
+    all-gather of the outputs), o_proj and down by K in whole 256-wide chunks
+    (K/G columns, fp32 partials gathered and added in chunk order, which keeps
+    one GPU's bits). Each shape's launch period (pq_q8_gemv on x quantized
+    beforehand, G = 1 beside it) over a >= 300 MB rotated pool (weights from
+    HBM) and over a pool of about resident_mb (more than the L2s, less than the
+    256 MB Infinity Cache: weights from the memory-side cache, as a G-GPU shard
+    of the 24-layer backbone, about 225 MB at G = 8, would stay)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(20261201)
+    stream = pq.stream_ptr()
+    out = {}
+    for gg in (1, G):
+        shapes = [("qkv", 3072 // gg, 2048, "bf16"), ("o_proj", 2048, 2048 // gg, "f32" if gg > 1 else "bf16"),
+                  ("gate_up", 16384 // gg, 2048, "bf16"), ("down", 2048, 8192 // gg, "f32" if gg > 1 else "bf16"),
+                  ("lm_head", 65536 // gg, 2048, "f32")]
+        res = {}
+        for (name, N, K, o) in shapes:
+            qx, dx = pq.q8_quant(torch.randn(K, device=dev, generator=g))
+            y = torch.empty(N, dtype=torch.float32 if o == "f32" else torch.bfloat16, device=dev)
+            dt = pq.DT_F32 if o == "f32" else pq.DT_BF16
+            nb = N * K + N * (K // 32) * 2 + K + (K // 32) * 4 + N * (4 if o == "f32" else 2)
+            row = {"shape": f"{N}x{K}", "out": o, "bytes": nb}
+            for regime, mb in (("hbm", ROTATE_MB), ("infinity_cache", resident_mb)):
+                pool, _ = q8_pool(pq, torch, dev, g, N, K, min_mb=mb)
+                us = period_ms(torch, lambda i: pq.q8_gemv(pool[i % len(pool)], qx, dx, out_dtype=dt, out=y),
+                               3 * len(pool), stream) * 1e3
+                row[regime] = {"us": round(us, 2), "GB/s": round(nb / (us * 1e-6) / 1e9, 1), "copies": len(pool)}
+                del pool
+                torch.cuda.empty_cache()
+            res[name] = row
+        out[f"G{gg}"] = {"per_shape": res,
+                         "step_us": {r: round(sum(v[r]["us"] for v in res.values()), 2)
+                                     for r in ("hbm", "infinity_cache")}}
+    print(json.dumps({"shard_profile": G, **out}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -853,6 +892,9 @@ def main():
     ap.add_argument("--gemv-profile", choices=["ternary", "q4", "q5"],
                     help="only run eager launches of the ternary FFN GEMVs or the Q4 / Q5 layer GEMVs (3 weight "
                          "copies per shape) for counter runs; prints their algorithmic bytes")
+    ap.add_argument("--shard-profile", type=int, metavar="G",
+                    help="only time the config-2 GEMVs at the shapes one of G GPUs would run (rows or whole K "
+                         "chunks split G ways), from HBM and from the Infinity Cache; prints their periods")
     ap.add_argument("--decode-profile", choices=["synth", "real", "synth-ref", "real-ref", "synth-q4"],
                     help="only run one backbone's decode measurement (the synthetic or the real LFM3 shapes, "
                          "-ref: the reference's GEMV numerics, -q4: Q4 linears from a blob) for kernel traces; "
@@ -869,6 +911,13 @@ def main():
     dev = torch.device("cuda:0")
     if args.prefill_profile:
         prefill_profile_workload(pq, torch, dev)
+        return
+    if args.shard_profile:
+        if args.shard_profile not in (2, 4, 8):
+            print("--shard-profile G: G of 2, 4 or 8 (o_proj's K of 2048 splits in whole 256-wide chunks)",
+                  file=sys.stderr)
+            sys.exit(2)
+        shard_workload(pq, torch, dev, args.shard_profile)
         return
     if args.gemv_profile:
         if args.calib:   # the counter calibration of the traffic runs: 256 MiB read + 256 MiB written
