@@ -1,7 +1,9 @@
 // attn_ref.hip -- the attention of the reference-numerics engine (gfx950), in
 // the reference's own order: k_attn_head (lfm3_nanode.cu:503-602) over a bf16
 // KV cache [pos][nkv][hd] (written by pq_qk_prep_ref, as k_kv_write copies the
-// bf16 rows, 157-162), then k_sigmoid_gate's gate (852-858).
+// bf16 rows, 157-162), then k_sigmoid_gate's gate (852-858). For one decode
+// token the same kernel also forms the position's q, k and v rows itself
+// (pq_attn_decode_ref: the PREP form below), bit for bit the two launches.
 //
 // One workgroup per (q head, query position t), as the reference launches a
 // block of 256 per head (blockIdx.y the chunk position). Threads 0..255 are
