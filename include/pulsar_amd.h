@@ -306,6 +306,22 @@ int pq_attn_decode_ref(const uint16_t *qkv, const float *q_norm, const float *k_
                        uint16_t *out, int pos, int nh, int nkv, int hd, int rot, float eps, float scale,
                        int win, void *stream);
 
+/* pq_attn_decode_ref for a layer whose gate rows are a Q8 tensor of their own
+ * (a low-bit blob keeps gate_proj in Q8): the launch forms each head's gate
+ * itself, with the bits of the reference-numerics GEMV of those rows on
+ * rmsnorm(x, x_norm) (pq_q8r_gemv_fused with the NORM prologue: rmsnorm_body's
+ * order, then the 32 leaf chains of q8_partial<bf16, FMA=1> and k_combine's
+ * bf16), so that GEMV's launch is not needed. gate_codes [nh][2048] int8 and
+ * gate_scales [nh][64] fp32 row-major as the .lfm3q8 file stores them; x the
+ * bf16 residual [2048] (hidden 2048), x_norm its norm weight; eps serves both
+ * norms. Replaces, for one decode step, the gate rows' gemv (lfm3_nanode.cu
+ * 222-374, 383-440) with the kernels pq_attn_decode_ref replaces. */
+int pq_attn_decode_ref_q8gate(const uint16_t *qkv, const float *q_norm, const float *k_norm,
+                              const float *rope_cs, uint16_t *kcache, uint16_t *vcache,
+                              const int8_t *gate_codes, const float *gate_scales, const uint16_t *x,
+                              const float *x_norm, uint16_t *out, int pos, int nh, int nkv, int hd, int rot,
+                              float eps, float scale, int win, void *stream);
+
 /* Gated short conv over T positions: bcx rows [B | C | x] (3H), ring
  * [ntaps][H] bf16 (newest last, updated), out [T][H] bf16 = bf16(C * conv(B*x)).
  * ntaps 2, 3, 4 or 7. Replaces k_shift_in + k_conv7 / k_conv_chunk (892-941). */

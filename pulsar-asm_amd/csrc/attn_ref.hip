@@ -26,7 +26,9 @@
 #include "pq_device.h"
 #include "pq_host.h"
 #include "pq_internal.h"
+#include "pq_prologue.h"
 #include "q8_common.h"
+#include "q8r_common.h"
 
 
 namespace pq {
@@ -87,6 +89,24 @@ struct AttnPrep {
   float eps;
 };
 
+// GQ (with PREP): the head's gate is not read from the row but formed here,
+// for a layer whose gate rows are a Q8 part of their own (a low-bit blob keeps
+// gate_proj in Q8): rows [nh][kGateK] of codes and fp32 block scales, applied
+// to y = rmsnorm(x, w) of the residual x (bf16 [kGateK]) in rmsnorm_body's
+// order, with the arithmetic of the reference-numerics GEMV (its RESNORM
+// prologue's second norm, the 32 leaf chains, the leaf tree, bf16 of 0 +
+// the sum): the same bits as that GEMV's launch, which the layer then skips.
+// Waves 4-7 form y while waves 0-2 prepare q, k, v; wave 8 dots the gate row
+// while waves 0-3 form the softmax sums.
+constexpr int kGateK = 2048;
+struct AttnGate {
+  const int8_t *codes;     // [nh][kGateK] int8
+  const float *scales;     // [nh][kGateK / 32]
+  const uint16_t *x;       // the residual, bf16 [kGateK]
+  const float *w;          // the norm weight [kGateK]
+  float eps;
+};
+
 // PREP (one decode token, T = 1): q is the token's projected row [q | k | v]
 // (nh, nkv, nkv heads), and the workgroup first forms the position's q, k and
 // v rows as qk_prep_kernel does (head norm and RoPE for q and k, v as it is):
@@ -96,13 +116,14 @@ struct AttnPrep {
 // kvn instead, as the last key of its score warp and of its value segment, so
 // every sum keeps the order of the unfused pair (pq_qk_prep_ref, then the
 // attention of this kernel without PREP).
-template <int HD, bool PREP>
+template <int HD, bool PREP, bool GQ>
 __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__restrict__ q, int q_stride,
                                                         uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
                                                         const uint16_t *__restrict__ gate, int gate_stride,
                                                         uint16_t *__restrict__ out, int out_stride, int pos0,
                                                         const int32_t *__restrict__ pos_dev, int nh, int nkv,
-                                                        float scale, int win, AttnPrep pp) {
+                                                        float scale, int win, AttnPrep pp, AttnGate gq) {
+  static_assert(PREP || !GQ, "the gate is formed in the one-token form");
   constexpr int E = HD / 32;
   using KT = typename KVPiece<E>::T;
   extern __shared__ __align__(16) float sl[];   // the window's scores, then their e
@@ -110,6 +131,9 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
   __shared__ float seg[8][HD];
   __shared__ float qs[PREP ? HD : 1];                      // PREP: the position's q
   __shared__ __align__(16) uint16_t kvn[PREP ? 2 * HD : 2];   // PREP: its bf16 k, then v
+  __shared__ __align__(16) float gpart[GQ ? 8 : 1];                      // GQ: y's sum-of-squares partials
+  __shared__ __align__(16) float gxs[GQ ? (kGateK / kQ) * kRXStride : 4];   // GQ: y in the leaves' layout
+  __shared__ float gval;                                                  // GQ: the gate (bf16 value)
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 31, wid = tid >> 5;
   const int npos = (pos_dev != nullptr ? *pos_dev : pos0) + t + 1;
   const int lo = window_lo(npos, win), np = npos - lo;
@@ -138,6 +162,30 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
   KT wk[B], wv[B];
   if (nks > 0) ld(rk, wk, 0, W);   // the first round's keys load during the prep
   float qv[E];
+  float gy[8], gw[8];   // GQ, threads 256..511: 8 elements of the residual and of the norm weight
+  RBlocks gB;           // GQ, wave 8: the head's gate row (leaf L: blocks L and L + 32)
+  if constexpr (GQ) {
+    if (tid >= 256 && tid < 512) {
+      const int e0 = (tid - 256) * 8;
+      const uint4 u = *reinterpret_cast<const uint4 *>(gq.x + e0);
+      const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        gy[2 * i] = __uint_as_float(uw[i] << 16);
+        gy[2 * i + 1] = __uint_as_float(uw[i] & 0xffff0000u);
+      }
+      const float4 w0 = *reinterpret_cast<const float4 *>(gq.w + e0);
+      const float4 w1 = *reinterpret_cast<const float4 *>(gq.w + e0 + 4);
+      gw[0] = w0.x; gw[1] = w0.y; gw[2] = w0.z; gw[3] = w0.w;
+      gw[4] = w1.x; gw[5] = w1.y; gw[6] = w1.z; gw[7] = w1.w;
+    } else if (tid >= 512 && tid < 576) {
+      const __amdgpu_buffer_rsrc_t gc = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(gq.codes), (short)0,
+                                                                          nh * kGateK, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t gs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(gq.scales), (short)0,
+                                                                          nh * (kGateK / kQ) * 4, kRsrcWord3);
+      q8r_load<2>(gB, gc, gs, h, nh, kGateK, kGateK / kQ, kGateK / kQ, 0, lane);
+    }
+  }
   if constexpr (PREP) {
     if (tid < 192) {   // wave 0: q, wave 1: k, wave 2: v
       constexpr int EH = HD / 64;
@@ -179,7 +227,19 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
         }
       }
     }
+    if constexpr (GQ) {
+      if (tid >= 256 && tid < 512) ref_sumsq_part<8>(gy, gpart, tid - 256);
+    }
     __syncthreads();
+    if constexpr (GQ) {   // y = rmsnorm(x, w) as the GEMV prologue forms it, into the leaves' layout
+      if (tid >= 256 && tid < 512) {
+        norm_apply<8>(gy, gw, ordered_sum(gpart, 8), kGateK, gq.eps);
+        const int e0 = (tid - 256) * 8;
+        float *d = gxs + (e0 >> 5) * kRXStride + (e0 & 31);
+        *reinterpret_cast<float4 *>(d) = make_float4(gy[0], gy[1], gy[2], gy[3]);
+        *reinterpret_cast<float4 *>(d + 4) = make_float4(gy[4], gy[5], gy[6], gy[7]);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < E; j++) qv[j] = qs[lane * E + j];
   } else {
@@ -237,6 +297,12 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
 #pragma unroll
   for (int w = 1; w < kArThreads / 64; w++) m = fmaxf(m, red[w]);
   __syncthreads();
+  if constexpr (GQ) {   // the head's gate row on y (wave 8; y was written before two barriers)
+    if (tid >= 512 && tid < 576) {
+      const float a = leaf_tree32(q8r_leaf<2>(gB, gxs, kGateK / kQ, 0, lane));
+      if (tid == 512) gval = bf2f(f2bf(0.0f + a));
+    }
+  }
   if (tid < 256) {   // the reference's threads: e over keys tid, tid + 256, ..., then the warp trees
     float sum = 0.0f;
     for (int i = tid; i < np; i += 256) {
@@ -288,32 +354,36 @@ __global__ __launch_bounds__(kArThreads) void attn_ref_kernel(const uint16_t *__
     const float o = ((seg[0][tid] + seg[1][tid]) + (seg[2][tid] + seg[3][tid])) +
                     ((seg[4][tid] + seg[5][tid]) + (seg[6][tid] + seg[7][tid]));
     uint16_t ob = f2bf(o);
-    if (gate != nullptr) {   // k_sigmoid_gate: bf16(out * 1 / (1 + e^-g))
-      const float sg = 1.0f / (1.0f + expf_pq(-bf2f(gate[(size_t)t * gate_stride + h])));
+    if (GQ || gate != nullptr) {   // k_sigmoid_gate: bf16(out * 1 / (1 + e^-g))
+      const float g = GQ ? gval : bf2f(gate[(size_t)t * gate_stride + h]);
+      const float sg = 1.0f / (1.0f + expf_pq(-g));
       ob = f2bf(bf2f(ob) * sg);
     }
     out[(size_t)t * out_stride + (size_t)h * HD + tid] = ob;
   }
 }
 
-// pp non-null: the PREP kernel (T = 1)
+// pp non-null: the PREP kernel (T = 1); gq non-null (with pp): the GQ form
 static int attn_ref_launch(const uint16_t *q, int q_stride, const uint16_t *kcache, const uint16_t *vcache,
                            const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, int pos0,
                            const int32_t *pos_dev, int keys, int nh, int nkv, int hd, int T, float scale, int win,
-                           const AttnPrep *pp, hipStream_t st) {
+                           const AttnPrep *pp, const AttnGate *gq, hipStream_t st) {
   const dim3 grid((unsigned)nh, (unsigned)T), block(kArThreads);
   const size_t lds = (size_t)keys * sizeof(float);
   uint16_t *kc = const_cast<uint16_t *>(kcache), *vc = const_cast<uint16_t *>(vcache);
   const AttnPrep p = pp != nullptr ? *pp : AttnPrep{};
-#define PQ_AR(HH, PR)                                                                                              \
-  launch(attn_ref_kernel<HH, PR>, grid, block, lds, st, q, q_stride, kc, vc, gate, gate_stride, out, out_stride, \
-         pos0, pos_dev, nh, nkv, scale, win, p)
+  const AttnGate g = gq != nullptr ? *gq : AttnGate{};
+#define PQ_AR(HH, PR, GG)                                                                                  \
+  launch(attn_ref_kernel<HH, PR, GG>, grid, block, lds, st, q, q_stride, kc, vc, gate, gate_stride, out, \
+         out_stride, pos0, pos_dev, nh, nkv, scale, win, p, g)
   if (hd == 64) {
-    if (pp != nullptr) PQ_AR(64, true);
-    else PQ_AR(64, false);
+    if (pp != nullptr && gq != nullptr) PQ_AR(64, true, true);
+    else if (pp != nullptr) PQ_AR(64, true, false);
+    else PQ_AR(64, false, false);
   } else {
-    if (pp != nullptr) PQ_AR(128, true);
-    else PQ_AR(128, false);
+    if (pp != nullptr && gq != nullptr) PQ_AR(128, true, true);
+    else if (pp != nullptr) PQ_AR(128, true, false);
+    else PQ_AR(128, false, false);
   }
 #undef PQ_AR
   return check_launch(pp != nullptr ? "pq_attn_decode_ref" : "pq_attn_ref");
@@ -347,7 +417,7 @@ int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const 
   const int rc = attn_ref_check(q, kcache, vcache, out, nh, nkv, hd, 1, win, keys, "attn_ref_dev");
   if (rc) return rc;
   return attn_ref_launch(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, 0, pos_dev, keys, nh, nkv,
-                         hd, 1, scale, win, nullptr, st);
+                         hd, 1, scale, win, nullptr, nullptr, st);
 }
 
 // pq_attn_decode_ref at the device position *pos_dev (pos_dev null: pos):
@@ -355,7 +425,7 @@ int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const 
 int attn_decode_ref_dev(const uint16_t *qkv, const float *q_norm, const float *k_norm, const float *rope_cs,
                         uint16_t *kcache, uint16_t *vcache, const uint16_t *gate, uint16_t *out, int pos,
                         const int32_t *pos_dev, int ctx, int nh, int nkv, int hd, int rot, float eps, float scale,
-                        int win, hipStream_t st) {
+                        int win, hipStream_t st, const AttnGateQ8 *gq8) {
   const int keys = win > 0 && win < ctx ? win : ctx;
   PQ_REQUIRE(ctx > 0 && (pos_dev || (pos >= 0 && pos < ctx)), PQ_ERR_ARG, "pq_attn_decode_ref: pos=%d ctx=%d",
              pos, ctx);
@@ -364,8 +434,17 @@ int attn_decode_ref_dev(const uint16_t *qkv, const float *q_norm, const float *k
   rc = attn_prep_check(q_norm, k_norm, rope_cs, hd, rot, "pq_attn_decode_ref");
   if (rc) return rc;
   const AttnPrep pp{q_norm, k_norm, rope_cs, rot, eps};
+  if (gq8 != nullptr) {
+    PQ_REQUIRE(gq8->codes && gq8->scales && gq8->x && gq8->w && gq8->K == kGateK, PQ_ERR_ARG,
+               "pq_attn_decode_ref: the Q8 gate rows need codes, scales, x, w and K = %d (K = %d)", kGateK, gq8->K);
+    PQ_REQUIRE(aligned(gq8->codes, 16) && aligned(gq8->x, 16) && aligned(gq8->w, 16) && aligned(gq8->scales, 4),
+               PQ_ERR_ALIGN, "pq_attn_decode_ref: Q8 gate pointer alignment");
+    const AttnGate g{gq8->codes, gq8->scales, gq8->x, gq8->w, gq8->eps};
+    return attn_ref_launch(qkv, 0, kcache, vcache, nullptr, 0, out, 0, pos, pos_dev, keys, nh, nkv, hd, 1, scale,
+                           win, &pp, &g, st);
+  }
   return attn_ref_launch(qkv, 0, kcache, vcache, gate, 0, out, 0, pos, pos_dev, keys, nh, nkv, hd, 1, scale, win,
-                         &pp, st);
+                         &pp, nullptr, st);
 }
 
 }  // namespace pq
@@ -381,7 +460,17 @@ extern "C" int pq_attn_ref(const uint16_t *q, int q_stride, const uint16_t *kcac
   const int rc = attn_ref_check(q, kcache, vcache, out, nh, nkv, hd, T, win, keys, "pq_attn_ref");
   if (rc) return rc;
   return attn_ref_launch(q, q_stride, kcache, vcache, gate, gate_stride, out, out_stride, pos0, nullptr, keys, nh,
-                         nkv, hd, T, scale, win, nullptr, as_stream(stream));
+                         nkv, hd, T, scale, win, nullptr, nullptr, as_stream(stream));
+}
+
+extern "C" int pq_attn_decode_ref_q8gate(const uint16_t *qkv, const float *q_norm, const float *k_norm,
+                                         const float *rope_cs, uint16_t *kcache, uint16_t *vcache,
+                                         const int8_t *gate_codes, const float *gate_scales, const uint16_t *x,
+                                         const float *x_norm, uint16_t *out, int pos, int nh, int nkv, int hd, int rot,
+                                         float eps, float scale, int win, void *stream) {
+  const AttnGateQ8 g{gate_codes, gate_scales, x, x_norm, eps, kGateK};
+  return attn_decode_ref_dev(qkv, q_norm, k_norm, rope_cs, kcache, vcache, nullptr, out, pos, nullptr, pos + 1, nh, nkv,
+                             hd, rot, eps, scale, win, as_stream(stream), &g);
 }
 
 extern "C" int pq_attn_decode_ref(const uint16_t *qkv, const float *q_norm, const float *k_norm,
@@ -389,5 +478,5 @@ extern "C" int pq_attn_decode_ref(const uint16_t *qkv, const float *q_norm, cons
                                   uint16_t *out, int pos, int nh, int nkv, int hd, int rot, float eps, float scale,
                                   int win, void *stream) {
   return attn_decode_ref_dev(qkv, q_norm, k_norm, rope_cs, kcache, vcache, gate, out, pos, nullptr, pos + 1, nh, nkv,
-                             hd, rot, eps, scale, win, as_stream(stream));
+                             hd, rot, eps, scale, win, as_stream(stream), nullptr);
 }

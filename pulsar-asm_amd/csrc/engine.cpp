@@ -795,8 +795,10 @@ static bool parts_fusable(const Q8Dev &w, int kind) {
 // (A second part forked onto another stream inside the captured step, to run
 // beside the first, cost about 22 us per fork and join: 0.728 -> 0.909 ms per
 // token of the Q4 backbone, whose attention gate rows stay Q8.)
-static int parts_fused(Engine &E, const Q8Dev &w, const pq_gemv_prologue &pro, uint16_t *y) {
+static int parts_fused(Engine &E, const Q8Dev &w, const pq_gemv_prologue &pro, uint16_t *y,
+                       const Part *skip = nullptr) {
   for (const Part &p : w.parts) {
+    if (&p == skip) continue;
     if (p.bits == 8)
       PQ_TRY(pq_q8r_gemv_fused(w.pc + (size_t)p.r0 * w.K, w.sf + (size_t)p.r0 * (w.K / 32), &pro, y + p.r0,
                                PQ_DTYPE_BF16, p.n, w.K, nullptr, E.st));
@@ -826,6 +828,21 @@ static bool attn_prep_fused() {
     return e != nullptr && atoi(e) == 0;
   }();
   return !off;
+}
+
+// An attention layer's in-slot whose last part is the gate rows in Q8 (rows
+// qd + 2 kvd .., one per q head, K = 2048; a low-bit blob keeps gate_proj in
+// Q8): the decode attention forms the gates itself from those rows and the
+// residual (pq_attn_decode_ref's gate form), so the slot's launches leave
+// them out (PQ_ATTN_GATE=0: the part's own GEMV, as the unfused step runs it).
+static const Part *attn_gate_part(const Engine &E, const LayerDev &D) {
+  static const bool off = [] {
+    const char *e = getenv("PQ_ATTN_GATE");
+    return e != nullptr && atoi(e) == 0;
+  }();
+  if (off || !D.attn || !D.in.split() || D.in.parts.size() < 2 || D.in.K != 2048 || !attn_prep_fused()) return nullptr;
+  const Part &g = D.in.parts.back();
+  return g.bits == 8 && g.r0 == E.qd + 2 * E.kvd && g.n == E.c.nh ? &g : nullptr;
 }
 
 static int forward_decode_r2(Engine &E, bool dev) {
@@ -870,7 +887,7 @@ static int forward_decode_r2(Engine &E, bool dev) {
         p.x_in = xa;
         p.w0 = D.op_norm;
         p.eps = c.eps;
-        if (D.in.split()) PQ_TRY(parts_fused(E, D.in, p, E.Wd));
+        if (D.in.split()) PQ_TRY(parts_fused(E, D.in, p, E.Wd, attn_gate_part(E, D)));
         else PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
       }
     } else if (l == 0) {   // the token's embedding row (written once to xa), normalized
@@ -886,7 +903,7 @@ static int forward_decode_r2(Engine &E, bool dev) {
       PQ_TRY(gemv(D.in, E.Wd, PQ_DTYPE_BF16, nullptr));
     } else if (D.in.split() && parts_fusable(D.in, PQ_PRO_RESNORM)) {
       resnorm(E.L[l - 1].post_ffn_norm, D.op_norm);
-      PQ_TRY(parts_fused(E, D.in, p, E.Wd));
+      PQ_TRY(parts_fused(E, D.in, p, E.Wd, attn_gate_part(E, D)));
     } else if (D.in.split()) {
       PQ_TRY(resnorm_to(E.L[l - 1].post_ffn_norm, D.op_norm, E.A));
       PQ_TRY(plain(D.in, E.A, E.Wd));
@@ -897,7 +914,16 @@ static int forward_decode_r2(Engine &E, bool dev) {
     if (D.attn) {   // k_attn_head's order over the bf16 cache
       const int32_t *pd = dev ? E.ctr + 1 : nullptr;
       const uint16_t *gate = E.Wd + E.qd + 2 * E.kvd;
-      if (attn_prep_fused()) {
+      // the gates' rows left out of the in-slot above (the fused prologue forms: layer 0's NORM, RESNORM)
+      const bool fused_in = D.in.split() && (l == 0 ? parts_fusable(D.in, PQ_PRO_NORM) : parts_fusable(D.in, PQ_PRO_RESNORM));
+      const Part *gp = fused_in ? attn_gate_part(E, D) : nullptr;
+      if (gp != nullptr) {   // y = rmsnorm(xa, op_norm): xa is the layer input's residual (written by the in-slot)
+        const AttnGateQ8 g{D.in.pc + (size_t)gp->r0 * D.in.K, D.in.sf + (size_t)gp->r0 * (D.in.K / 32), xa,
+                           D.op_norm, c.eps, D.in.K};
+        PQ_TRY(attn_decode_ref_dev(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, nullptr, E.A, E.pos, pd,
+                                   c.ctx, c.nh, c.nkv, c.hd, layer_rot(E, D), c.eps, scale, layer_win(E, D), E.st,
+                                   &g));
+      } else if (attn_prep_fused()) {
         PQ_TRY(attn_decode_ref_dev(E.Wd, D.q_norm, D.k_norm, layer_rope(E, D), D.kc, D.vc, gate, E.A, E.pos, pd,
                                    c.ctx, c.nh, c.nkv, c.hd, layer_rot(E, D), c.eps, scale, layer_win(E, D), E.st));
       } else {

@@ -267,9 +267,11 @@ __device__ __forceinline__ float ordered_sum(const float *p, int n) {
 // (E = 4) or an 8-element piece of a lane, and the tree's offsets become lane
 // offsets or sums within the lane. part (16-byte aligned LDS) gets the
 // nparts = n/256 partials (1, 2, 4, .. 32; one barrier, LDS-only with LDSB);
-// every thread returns the total.
-template <int E, bool LDSB>
-__device__ __forceinline__ float ref_sumsq(const float *v, float *part, int nparts) {
+// every thread returns the total. ref_sumsq_part is the part before the
+// barrier for threads t = 0, 1, .. of a group that starts at a wave boundary
+// (t = threadIdx.x - a multiple of 64).
+template <int E>
+__device__ __forceinline__ void ref_sumsq_part(const float *v, float *part, int t_in_group) {
   static_assert(E == 4 || E == 8 || E == 16 || E == 32, "4 .. 32 elements per thread");
   constexpr int R = E >= 8 ? E / 8 : 1, LPR = E >= 8 ? 1 : 8 / E;
   float t[R];
@@ -290,7 +292,11 @@ __device__ __forceinline__ float ref_sumsq(const float *v, float *part, int npar
   ref_tree_step<E, 1>(t);
   constexpr int S = 32 * LPR / R;   // lanes per reference warp
   const int lane = threadIdx.x & 63;
-  if ((lane & (S - 1)) == 0) part[(threadIdx.x >> 6) * (64 / S) + lane / S] = t[0];
+  if ((lane & (S - 1)) == 0) part[(t_in_group >> 6) * (64 / S) + lane / S] = t[0];
+}
+template <int E, bool LDSB>
+__device__ __forceinline__ float ref_sumsq(const float *v, float *part, int nparts) {
+  ref_sumsq_part<E>(v, part, threadIdx.x);
   if constexpr (LDSB) lds_barrier();
   else __syncthreads();
   return ordered_sum(part, nparts);

@@ -31,12 +31,25 @@ int attn_ref_dev(const uint16_t *q, int q_stride, const uint16_t *kcache, const 
                  const uint16_t *gate, int gate_stride, uint16_t *out, int out_stride, const int32_t *pos_dev,
                  int ctx, int nh, int nkv, int hd, float scale, int win, hipStream_t st);
 
+// The gate rows of a layer as a Q8 part of their own, for the attention to
+// form: [nh][K] int8 codes, [nh][K/32] fp32 scales, applied to
+// rmsnorm(x, w) of the bf16 residual x (K = 2048).
+struct AttnGateQ8 {
+  const int8_t *codes;
+  const float *scales;
+  const uint16_t *x;
+  const float *w;
+  float eps;
+  int K;
+};
+
 // pq_attn_decode_ref at the device position *pos_dev (null: at pos); LDS
-// sized for positions below ctx.
+// sized for positions below ctx. gq8 non-null: the head gates formed in the
+// launch from those rows (gate is then not read).
 int attn_decode_ref_dev(const uint16_t *qkv, const float *q_norm, const float *k_norm, const float *rope_cs,
                         uint16_t *kcache, uint16_t *vcache, const uint16_t *gate, uint16_t *out, int pos,
                         const int32_t *pos_dev, int ctx, int nh, int nkv, int hd, int rot, float eps, float scale,
-                        int win, hipStream_t st);
+                        int win, hipStream_t st, const AttnGateQ8 *gq8 = nullptr);
 
 // pq_attn_decode for one query at the device position *pos_dev (keys up to
 // it, window win), sized for positions below ctx.

@@ -66,6 +66,7 @@ SIGNATURES = {
     "pq_qk_prep_ref": (I, [P, I, P, P, P, P, P, I, I, I, I, I, I, F, P]),
     "pq_attn_ref": (I, [P, I, P, P, P, I, P, I, I, I, I, I, I, F, I, P]),
     "pq_attn_decode_ref": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, F, F, I, P]),
+    "pq_attn_decode_ref_q8gate": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, F, F, I, P]),
     "pq_conv": (I, [P, P, P, P, I, I, I, P]),
     "pq_silu_mul": (I, [P, P, P, P, I, I, P]),
     "pq_silu_mul_interleaved": (I, [P, P, P, P, I, I, P]),

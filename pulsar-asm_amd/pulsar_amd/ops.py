@@ -8,7 +8,7 @@ import torch
 
 from . import check, lib
 
-__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "qlow_gemv_fused", "qlow_gemv_fused_swiglu", "qlow_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep", "qk_prep_ref", "attn_ref", "attn_decode_ref",
+__all__ = ["stream_ptr", "Q8Weight", "q8_quant", "q8_gemv", "q8_gemm", "q8r_gemv", "q8r_gemv_fused", "QlowWeight", "qlow_gemv", "qlow_gemv_fused", "qlow_gemv_fused_swiglu", "qlow_gemm", "DT_F32", "DT_BF16", "rmsnorm", "qk_prep", "qk_prep_ref", "attn_ref", "attn_decode_ref", "attn_decode_ref_q8gate",
            "attn_decode", "conv", "silu_mul", "argmax", "embed", "q8k_quant", "tq2_gemv", "tq2_gemv_batch", "gemv_fused",
            "gemv_fused_swiglu",
            "argmax_parts", "attn_layer_decode", "q8r_gemv_fused_swiglu", "PRO_Q8", "PRO_RESNORM", "PRO_NORM", "PRO_EMBED", "PRO_SILU",
@@ -265,6 +265,16 @@ def attn_decode_ref(qkv, q_norm, k_norm, rope_cs, kc, vc, pos, nh, nkv, hd, rot,
                                    _bits16(kc), _bits16(vc), _bits16(gate) if gate is not None else None,
                                    _bits16(out), pos, nh, nkv, hd, rot, eps, scale, win, stream_ptr()),
           "pq_attn_decode_ref")
+
+
+def attn_decode_ref_q8gate(qkv, q_norm, k_norm, rope_cs, kc, vc, gate_codes, gate_scales, x, x_norm, pos, nh, nkv, hd,
+                           rot, scale, out, eps=1e-5, win=0):
+    """attn_decode_ref with each head's gate formed in the launch from Q8 rows on rmsnorm(x, x_norm)
+    (pq_attn_decode_ref_q8gate)."""
+    check(lib().pq_attn_decode_ref_q8gate(_bits16(qkv), q_norm.data_ptr(), k_norm.data_ptr(), rope_cs.data_ptr(),
+                                          _bits16(kc), _bits16(vc), gate_codes.data_ptr(), gate_scales.data_ptr(),
+                                          _bits16(x), x_norm.data_ptr(), _bits16(out), pos, nh, nkv, hd, rot, eps,
+                                          scale, win, stream_ptr()), "pq_attn_decode_ref_q8gate")
 
 
 def attn_decode(q, q_stride, kc, vc, pos0, nh, nkv, hd, T, scale, gate=None, gate_stride=0, out=None,

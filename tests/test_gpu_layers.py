@@ -233,6 +233,50 @@ def test_attention_decode_ref(orc, pq, dev, pos, nh, nkv, hd, rot, win):
     assert np.array_equal(_u16(kc2), kc_r) and np.array_equal(_u16(vc2), vc_r)
 
 
+# pq_attn_decode_ref_q8gate: each head's gate formed in the attention launch
+# from Q8 rows on rmsnorm(x, w) equals the separate reference-numerics GEMV of
+# those rows (pq_q8r_gemv_fused, NORM prologue, bf16 out, itself pinned to
+# pq_rmsnorm + pq_q8r_gemv and the oracle) followed by pq_attn_decode_ref with
+# that gate, bit for bit, output and cache rows; head_dim 64 and 128, windows,
+# positions 0, 31 and 290.
+@pytest.mark.parametrize("pos,nh,nkv,hd,rot,win", [(0, 32, 8, 64, 32, 0), (290, 32, 8, 64, 32, 0),
+                                                   (31, 16, 4, 128, 64, 0), (300, 16, 4, 128, 128, 256)])
+def test_attention_decode_ref_q8gate(orc, pq, dev, pos, nh, nkv, hd, rot, win):
+    H = 2048
+    ctx = pos + 3
+    kvd = nkv * hd
+    nin, rows, qn, kn, _ = _qkv_case(orc, nh, nkv, hd, 1, ctx, SEED + 17 * pos + hd)
+    cs = orc.rope_table(ctx, hd, rot, 1e6 if rot < hd else 1e4)
+    kc0 = np.zeros((ctx, kvd), np.uint16)
+    vc0 = np.zeros((ctx, kvd), np.uint16)
+    kc0[:pos] = orc.f2bf(orc.gen_normal(SEED + 3 * pos, pos * kvd).reshape(pos, kvd) * 2)
+    vc0[:pos] = orc.f2bf(orc.gen_normal(SEED + 3 * pos + 1, pos * kvd).reshape(pos, kvd) * 5)
+    g = torch.Generator(device=dev)
+    g.manual_seed(pos + hd)
+    codes = torch.randint(-127, 128, (nh, H), dtype=torch.int8, device=dev, generator=g)
+    scales = torch.rand((nh, H // 32), device=dev, generator=g) * 0.002
+    x = (torch.randn(H, device=dev, generator=g) * 3).to(torch.bfloat16)
+    w = torch.rand(H, device=dev, generator=g) + 0.5
+    scale = 1.0 / np.sqrt(hd)
+    qnd, knd, csd = (torch.from_numpy(a).to(dev) for a in (qn, kn, cs))
+    # the separate gate GEMV, its bf16 gates, then the attention on them
+    gate = pq.q8r_gemv_fused(codes, scales, pq.PRO_NORM, out_dtype=pq.DT_BF16, x_in=x.view(torch.int16), w0=w)
+    kc_a, vc_a = _t16(kc0, dev), _t16(vc0, dev)
+    want = torch.zeros(nh * hd, dtype=torch.int16, device=dev)
+    pq.attn_decode_ref(_t16(rows, dev), qnd, knd, csd, kc_a, vc_a, pos, nh, nkv, hd, rot, scale, want,
+                       gate=gate.view(torch.int16), win=win)
+    # the one launch
+    kc_b, vc_b = _t16(kc0, dev), _t16(vc0, dev)
+    got = torch.zeros(nh * hd, dtype=torch.int16, device=dev)
+    pq.attn_decode_ref_q8gate(_t16(rows, dev), qnd, knd, csd, kc_b, vc_b, codes, scales, x.view(torch.int16), w,
+                              pos, nh, nkv, hd, rot, scale, got, win=win)
+    bad = np.argwhere(_u16(got) != _u16(want))
+    assert bad.shape[0] == 0, f"{bad.shape[0]} differ, first {bad[:4].tolist()}"
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+    # the gates matter: a zero gate row would leave the output at half
+    assert len(set(_u16(gate.view(torch.int16)).tolist())) > nh // 2
+
+
 def test_attention_decode_ref_rejects(pq, dev):
     """Bad shapes fail on the host with an error, before any launch."""
     z16 = torch.zeros(4096, dtype=torch.int16, device=dev)
